@@ -1,0 +1,169 @@
+/*
+ * rwkv7_hip.h -- C ABI of librwkv7_hip.so, the MI355X (gfx950) RWKV7 inference library.
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream handle
+ * (hipStream_t passed as void*; NULL is the legacy default stream). Nothing in
+ * the library allocates or frees device memory, creates streams or events, or
+ * synchronises the host: the caller owns every buffer, so the calls can be
+ * captured in a HIP graph. Each function returns 0 on success or one of the
+ * RWKV7_E* codes below (argument errors are detected on the host before any
+ * launch; launch failures return RWKV7_ELAUNCH).
+ *
+ * Element types: "f16" is IEEE binary16, "f32" binary32, "i64" int64. All
+ * arrays are dense row-major with the shapes stated. The RWKV7 head size N is
+ * 64. Citations name the yuyi2439/rwkv-tl interface each entry point stands
+ * in for (path:line in that repository).
+ */
+#ifndef RWKV7_HIP_H
+#define RWKV7_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RWKV7_ABI_VERSION 1
+#define RWKV7_HEAD_SIZE 64
+
+enum {
+  RWKV7_OK = 0,
+  RWKV7_EINVAL = 1,    /* null pointer, bad enum value */
+  RWKV7_ESHAPE = 2,    /* a dimension the kernels do not support */
+  RWKV7_EWORKSPACE = 3,/* workspace smaller than rwkv7_workspace_bytes() */
+  RWKV7_ELAUNCH = 4    /* a kernel launch returned a HIP error */
+};
+
+/* Model sizes. n_head * 64 == n_embd. Ranks are the LoRA widths of the w, a,
+ * v and g gates (src/rwkv_tl/weight.py:77-91; demo/_rwkv7_base.py:131-137). */
+typedef struct rwkv7_dims {
+  int32_t n_layer, n_embd, n_head, n_ffn, vocab;
+  int32_t rank_w, rank_a, rank_v, rank_g;
+} rwkv7_dims;
+
+/* Per-layer fp32 vectors, each [n_embd], stored consecutively in the layer's
+ * vector block in this order (src/rwkv_tl/weight.py:66-126). r_k is the
+ * [n_head, 64] tensor flattened. */
+enum {
+  RWKV7_V_LN1_W = 0, RWKV7_V_LN1_B, RWKV7_V_X_R, RWKV7_V_X_W, RWKV7_V_X_K,
+  RWKV7_V_X_V, RWKV7_V_X_A, RWKV7_V_X_G, RWKV7_V_W0, RWKV7_V_A0, RWKV7_V_V0,
+  RWKV7_V_K_K, RWKV7_V_K_A, RWKV7_V_R_K, RWKV7_V_LNX_W, RWKV7_V_LNX_B,
+  RWKV7_V_LN2_W, RWKV7_V_LN2_B, RWKV7_V_FFN_X_K, RWKV7_NVEC
+};
+
+/* Byte offsets inside one layer's weight arena. All f16 matrices are
+ * [out, in] (the checkpoint's own orientation):
+ *   w_rkv   [3C, C]   receptance, key, value rows stacked
+ *   w_lora1 [Rv+Rw+Ra+Rg, C]   v1^T, w1^T, a1^T, g1^T (the first LoRA steps)
+ *   w_lora2 [C, Rv+Rw+Ra+Rg]   row c = (v2[:,c], w2[:,c], a2[:,c], g2[:,c])
+ *   w_o     [C, C]
+ *   w_fk    [F, C]    ffn.key
+ *   w_fv    [C, F]    ffn.value
+ *   vec     [RWKV7_NVEC, C] f32
+ * w_lora1 immediately follows w_rkv, so the two form one [3C+sumR, C] matrix.
+ * Replaces the per-tensor attributes of RWKV7ATTWeight / RWKV7FFNWeight
+ * (src/rwkv_tl/weight.py:18-126) with one contiguous arena per layer. */
+typedef struct rwkv7_layer_layout {
+  int64_t w_rkv, w_lora1, w_lora2, w_o, w_fk, w_fv, vec;
+  int64_t bytes; /* arena size, a multiple of 256 */
+} rwkv7_layer_layout;
+
+/* Device-side model. Layer i's arena starts at layers + i * layout.bytes. */
+typedef struct rwkv7_model {
+  rwkv7_dims dims;
+  const void *layers; /* L consecutive layer arenas */
+  const void *emb;    /* f16 [V, C], LayerNorm ln0 already applied (weight.py:175) */
+  const void *head;   /* f16 [V, C] */
+  const void *ln_out; /* f32 [2, C]: weight, bias */
+} rwkv7_model;
+
+/* Recurrent state of `batch` independent sequences, layer-major arenas
+ * (src/rwkv_tl/state.py:35-44 plus a leading batch dimension):
+ *   tmix_x f16 [L, B, C]        time-mix token shift
+ *   rnn    f32 [L, B, H, 64, 64] wkv state S[h, value row, key column]
+ *   cmix_x f16 [L, B, C]        channel-mix token shift
+ * Updated in place by decode and prefill. */
+typedef struct rwkv7_state {
+  void *tmix_x;
+  void *rnn;
+  void *cmix_x;
+  int32_t batch;
+} rwkv7_state;
+
+/* ---- library ---------------------------------------------------------- */
+
+int rwkv7_abi_version(void);
+const char *rwkv7_strerror(int code);
+
+/* Fills *out for `dims`. Returns RWKV7_ESHAPE for unsupported sizes
+ * (n_embd != 64 * n_head, n_embd % 256, n_ffn % 256, ranks % 8, sum of ranks
+ * > 512). */
+int rwkv7_layer_layout_get(const rwkv7_dims *dims, rwkv7_layer_layout *out);
+
+/* Bytes of scratch that rwkv7_decode / rwkv7_prefill need for `batch`
+ * sequences of `seq_len` tokens (seq_len 1 for decode). */
+int64_t rwkv7_workspace_bytes(const rwkv7_dims *dims, int32_t batch, int32_t seq_len);
+
+/* ---- model steps ------------------------------------------------------ */
+
+/* One decode step for every sequence of `state`: tokens i64 [B] (device),
+ * logits f16 [B, V] (device). Equivalent of RWKV7Base.decode
+ * (demo/_rwkv7_base.py:74-87) / RWKV7Torch.decode (demo/rwkv7_torch.py:150-158),
+ * batched. Token ids outside [0, V) are clamped into range. */
+int rwkv7_decode(const rwkv7_model *model, const rwkv7_state *state,
+                 const int64_t *tokens, void *logits, void *workspace,
+                 int64_t workspace_bytes, void *stream);
+
+/* Prefill seq_len tokens per sequence: tokens i64 [B, T] (device). Updates
+ * state in place and produces no logits, like RWKV7Base.prefill
+ * (demo/_rwkv7_base.py:89-98) / RWKV7Torch.prefill (demo/rwkv7_torch.py:160-171). */
+int rwkv7_prefill(const rwkv7_model *model, const rwkv7_state *state,
+                  const int64_t *tokens, int32_t seq_len, void *workspace,
+                  int64_t workspace_bytes, void *stream);
+
+/* ---- operator level ---------------------------------------------------- */
+
+/* DPLR (wkv7) recurrence over B sequences of T tokens and H heads:
+ *   S[h] <- S[h] diag(w_t) + (S[h] a_t) b_t^T + v_t k_t^T ;  y_t = S[h] r_t
+ * S f32 [B, H, 64, 64] (in place); r, k, v, a, b f16 [B, T, H, 64];
+ * w f32 or f16 [B, T, H, 64] (w_is_f32 selects); y f16 [B, T, H, 64].
+ * Stands in for fused_dplr (T=1) and fused_dplr_T
+ * (src/rwkv_tl/kernels/dplr.py:256-285), where A = a, B = b. */
+int rwkv7_wkv7(float *S, const void *r, const void *w, int32_t w_is_f32,
+               const void *k, const void *v, const void *a, const void *b,
+               void *y, int32_t B, int32_t T, int32_t H, void *stream);
+
+/* LayerNorm over the last dimension (eps 1e-5): x f32 or f16 [M, C]
+ * (x_is_f32), weight/bias f32 [C], y f32 [M, C]. Stands in for LNWeight
+ * (src/rwkv_tl/weight.py:14-15). */
+int rwkv7_layernorm(const void *x, int32_t x_is_f32, const float *weight,
+                    const float *bias, float *y, int32_t M, int32_t C, void *stream);
+
+/* Token-shift lerps x + mu_i (prev - x), i < n_mix (1 or 6), all f16 [C]
+ * except mu f32 [n_mix, C]; out f16 [n_mix, C]. If x_copy != NULL it receives
+ * x after every read of prev (x_copy may alias prev). Stands in for
+ * fused_lerp6, fused_lerp6_copy and fused_lerp1_copy
+ * (src/rwkv_tl/kernels/lerp.py:140-198). */
+int rwkv7_lerp(const void *x, const void *prev, const float *mu, int32_t n_mix,
+               void *out, void *x_copy, int32_t C, void *stream);
+
+/* y = x W^T for one vector: x f32 [K], W f16 [N, K] (row stride ldw elements),
+ * y f32 [N]. K % 256 == 0. Stands in for the decode projections
+ * (demo/_rwkv7_base.py:87,206,290; kernels/gemm.py:215-262 at T=1). */
+int rwkv7_gemv_f16(const float *x, const void *W, int64_t ldw, float *y,
+                   int32_t N, int32_t K, void *stream);
+
+/* Y = epi(A W^T): A f16 [M, K] (row stride lda), W f16 [N, K] (ldw), fp32
+ * accumulation. epi: 0 store f32, 1 store f16, 2 relu^2 store f16,
+ * 3 add into f32 Y. Y row stride ldy. K % 8 == 0. Stands in for
+ * fused_rkv_gemm / ffn_h / ffn_v / out_mm (src/rwkv_tl/kernels/gemm.py:215-305). */
+int rwkv7_gemm_f16(const void *A, int64_t lda, const void *W, int64_t ldw,
+                   void *Y, int64_t ldy, int32_t M, int32_t N, int32_t K,
+                   int32_t epi, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RWKV7_HIP_H */

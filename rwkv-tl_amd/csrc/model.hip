@@ -1,0 +1,406 @@
+// C ABI of librwkv7_hip.so: layouts, workspace sizing, the decode and prefill
+// step sequencers and the operator-level entry points. Host code only; the
+// kernels live in gemv.hip, tmix.hip and gemm.hip.
+#include <string.h>
+
+#include "rwkv7_kernels.h"
+
+namespace rwkv7 {
+
+// ---- layouts -------------------------------------------------------------
+
+static int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+static int check_dims(const rwkv7_dims *d) {
+  if (!d) return RWKV7_EINVAL;
+  const int C = d->n_embd;
+  if (d->n_layer < 1 || C < 256 || C % 256 || C > 4096 || d->n_head * kN != C) return RWKV7_ESHAPE;
+  if (d->n_ffn < 256 || d->n_ffn % 256 || d->n_ffn > 8192 || d->vocab < 1) return RWKV7_ESHAPE;
+  const int r[4] = {d->rank_w, d->rank_a, d->rank_v, d->rank_g};
+  int sr = 0;
+  for (int i = 0; i < 4; ++i) {
+    if (r[i] < 8 || r[i] % 8) return RWKV7_ESHAPE;
+    sr += r[i];
+  }
+  if (sr > 512) return RWKV7_ESHAPE;
+  return RWKV7_OK;
+}
+
+static int sum_ranks(const rwkv7_dims &d) { return d.rank_w + d.rank_a + d.rank_v + d.rank_g; }
+
+static void layout_of(const rwkv7_dims &d, rwkv7_layer_layout *o) {
+  const int64_t C = d.n_embd, F = d.n_ffn, SR = sum_ranks(d);
+  int64_t off = 0;
+  o->w_rkv = off;
+  off += 3 * C * C * 2;
+  o->w_lora1 = off;  // contiguous with w_rkv (3*C*C*2 is a multiple of 256)
+  off = align256(off + SR * C * 2);
+  o->w_lora2 = off;
+  off = align256(off + C * SR * 2);
+  o->w_o = off;
+  off = align256(off + C * C * 2);
+  o->w_fk = off;
+  off = align256(off + F * C * 2);
+  o->w_fv = off;
+  off = align256(off + C * F * 2);
+  o->vec = off;
+  off = align256(off + int64_t(RWKV7_NVEC) * C * 4);
+  o->bytes = off;
+}
+
+// Workspace of the one-sequence decode path (GEMV kernels).
+struct DecodeWs {
+  float *x0, *xln, *proj, *vfirst, *yg, *xln2, *hid;
+};
+static int64_t decode_ws(const rwkv7_dims &d, char *base, DecodeWs *w) {
+  const int64_t C = d.n_embd, F = d.n_ffn, SR = sum_ranks(d);
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    char *p = base ? base + off : nullptr;
+    off = align256(off + bytes);
+    return reinterpret_cast<float *>(p);
+  };
+  DecodeWs t;
+  t.x0 = take(C * 4);
+  t.xln = take(C * 4);
+  t.proj = take((3 * C + SR) * 4);
+  t.vfirst = take(C * 4);
+  t.yg = take(C * 4);
+  t.xln2 = take(C * 4);
+  t.hid = take(F * 4);
+  if (w) *w = t;
+  return off;
+}
+
+// Workspace of the batched path (M = B * T rows).
+struct BatchWs {
+  float *x0, *rkv, *d, *vfirst, *wkab, *y;
+  uint16_t *xmix, *l1, *yg, *hid, *headin;
+};
+static int64_t batch_ws(const rwkv7_dims &d, int64_t B, int64_t T, char *base, BatchWs *w) {
+  const int64_t C = d.n_embd, F = d.n_ffn, SR = sum_ranks(d), M = B * T;
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    char *p = base ? base + off : nullptr;
+    off = align256(off + bytes);
+    return p;
+  };
+  BatchWs t;
+  t.x0 = reinterpret_cast<float *>(take(M * C * 4));
+  t.xmix = reinterpret_cast<uint16_t *>(take(6 * M * C * 2));
+  t.rkv = reinterpret_cast<float *>(take(3 * M * C * 4));
+  t.l1 = reinterpret_cast<uint16_t *>(take(M * SR * 2));
+  t.d = reinterpret_cast<float *>(take(4 * M * C * 4));
+  t.vfirst = reinterpret_cast<float *>(take(M * C * 4));
+  t.wkab = reinterpret_cast<float *>(take(5 * M * C * 4));
+  t.y = reinterpret_cast<float *>(take(M * C * 4));
+  t.yg = reinterpret_cast<uint16_t *>(take(M * C * 2));
+  t.hid = reinterpret_cast<uint16_t *>(take(M * F * 2));
+  t.headin = reinterpret_cast<uint16_t *>(take(B * C * 2));
+  if (w) *w = t;
+  return off;
+}
+
+#define RWKV7_TRY(expr)            \
+  do {                             \
+    int rc_ = (expr);              \
+    if (rc_ != RWKV7_OK) return rc_; \
+  } while (0)
+
+// One token for one sequence through the GEMV kernels.
+static int decode_one(const rwkv7_model &m, const rwkv7_state &s, const int64_t *tok, void *logits,
+                      char *ws, hipStream_t st) {
+  const rwkv7_dims &d = m.dims;
+  const int C = d.n_embd, F = d.n_ffn, H = d.n_head, SR = sum_ranks(d);
+  rwkv7_layer_layout lay;
+  layout_of(d, &lay);
+  DecodeWs w;
+  decode_ws(d, ws, &w);
+  RWKV7_TRY(launch_embed(tok, static_cast<const uint16_t *>(m.emb), w.x0, 1, C, d.vocab, st));
+  for (int l = 0; l < d.n_layer; ++l) {
+    const char *L = static_cast<const char *>(m.layers) + (int64_t)l * lay.bytes;
+    const float *vec = reinterpret_cast<const float *>(L + lay.vec);
+    uint16_t *tshift = static_cast<uint16_t *>(s.tmix_x) + (int64_t)l * C;
+    uint16_t *cshift = static_cast<uint16_t *>(s.cmix_x) + (int64_t)l * C;
+    float *rnn = static_cast<float *>(s.rnn) + (int64_t)l * H * kN * kN;
+
+    GemvArgs g = {};
+    g.W = reinterpret_cast<const uint16_t *>(L + lay.w_rkv);
+    g.ldw = C;
+    g.N = 3 * C + SR;
+    g.K = C;
+    g.x = w.x0;
+    g.ln_w = vec + RWKV7_V_LN1_W * C;
+    g.ln_b = vec + RWKV7_V_LN1_B * C;
+    g.prev = tshift;
+    g.mu = vec;
+    const int ends[7] = {C, 2 * C, 3 * C, 3 * C + d.rank_v, 3 * C + d.rank_v + d.rank_w,
+                         3 * C + d.rank_v + d.rank_w + d.rank_a, 3 * C + SR};
+    const int mus[7] = {RWKV7_V_X_R, RWKV7_V_X_K, RWKV7_V_X_V, RWKV7_V_X_V,
+                        RWKV7_V_X_W, RWKV7_V_X_A, RWKV7_V_X_G};
+    memcpy(g.seg_end, ends, sizeof ends);
+    memcpy(g.seg_mu, mus, sizeof mus);
+    g.xln_out = w.xln;
+    g.y = w.proj;
+    RWKV7_TRY((launch_gemv<PRO_TMIX, EPI_F32>(g, st)));
+
+    TmixDecodeArgs t;
+    t.proj = w.proj;
+    t.ldp = 3 * C + SR;
+    t.w_lora2 = reinterpret_cast<const uint16_t *>(L + lay.w_lora2);
+    t.vec = vec;
+    t.vfirst = w.vfirst;
+    t.rnn = rnn;
+    t.xln = w.xln;
+    t.shift = tshift;
+    t.yg = w.yg;
+    t.C = C;
+    t.H = H;
+    t.rv = d.rank_v;
+    t.rw = d.rank_w;
+    t.ra = d.rank_a;
+    t.rg = d.rank_g;
+    t.layer0 = l == 0;
+    RWKV7_TRY(launch_tmix_decode(t, 1, st));
+
+    GemvArgs o = {};
+    o.W = reinterpret_cast<const uint16_t *>(L + lay.w_o);
+    o.ldw = C;
+    o.N = C;
+    o.K = C;
+    o.x = w.yg;
+    o.y = w.x0;
+    RWKV7_TRY((launch_gemv<PRO_F32, EPI_RESID>(o, st)));
+
+    GemvArgs fk = {};
+    fk.W = reinterpret_cast<const uint16_t *>(L + lay.w_fk);
+    fk.ldw = C;
+    fk.N = F;
+    fk.K = C;
+    fk.x = w.x0;
+    fk.ln_w = vec + RWKV7_V_LN2_W * C;
+    fk.ln_b = vec + RWKV7_V_LN2_B * C;
+    fk.prev = cshift;
+    fk.mu = vec + RWKV7_V_FFN_X_K * C;
+    fk.xln_out = w.xln2;
+    fk.y = w.hid;
+    RWKV7_TRY((launch_gemv<PRO_CMIX, EPI_RELUSQ>(fk, st)));
+    RWKV7_TRY(launch_store_f16(w.xln2, cshift, C, st));
+
+    GemvArgs fv = {};
+    fv.W = reinterpret_cast<const uint16_t *>(L + lay.w_fv);
+    fv.ldw = F;
+    fv.N = C;
+    fv.K = F;
+    fv.x = w.hid;
+    fv.y = w.x0;
+    RWKV7_TRY((launch_gemv<PRO_F32, EPI_RESID>(fv, st)));
+  }
+  if (logits) {
+    const float *lo = static_cast<const float *>(m.ln_out);
+    GemvArgs hd = {};
+    hd.W = static_cast<const uint16_t *>(m.head);
+    hd.ldw = C;
+    hd.N = d.vocab;
+    hd.K = C;
+    hd.x = w.x0;
+    hd.ln_w = lo;
+    hd.ln_b = lo + C;
+    hd.y = logits;
+    RWKV7_TRY((launch_gemv<PRO_LN, EPI_F16>(hd, st)));
+  }
+  return RWKV7_OK;
+}
+
+// B sequences x T tokens through the MFMA GEMM path; logits (optional) of the
+// last token of each sequence.
+static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t *tok, int T,
+                       void *logits, char *ws, hipStream_t st) {
+  const rwkv7_dims &d = m.dims;
+  const int B = s.batch;
+  const int C = d.n_embd, F = d.n_ffn, H = d.n_head, SR = sum_ranks(d);
+  const int M = B * T;
+  const int64_t MC = (int64_t)M * C;
+  const int rv = d.rank_v, rw = d.rank_w, ra = d.rank_a, rg = d.rank_g;
+  rwkv7_layer_layout lay;
+  layout_of(d, &lay);
+  BatchWs w;
+  batch_ws(d, B, T, ws, &w);
+  RWKV7_TRY(launch_embed(tok, static_cast<const uint16_t *>(m.emb), w.x0, M, C, d.vocab, st));
+  for (int l = 0; l < d.n_layer; ++l) {
+    const char *L = static_cast<const char *>(m.layers) + (int64_t)l * lay.bytes;
+    const float *vec = reinterpret_cast<const float *>(L + lay.vec);
+    const uint16_t *wrkv = reinterpret_cast<const uint16_t *>(L + lay.w_rkv);
+    const uint16_t *wl1 = reinterpret_cast<const uint16_t *>(L + lay.w_lora1);
+    const uint16_t *wl2 = reinterpret_cast<const uint16_t *>(L + lay.w_lora2);
+    uint16_t *tshift = static_cast<uint16_t *>(s.tmix_x) + (int64_t)l * B * C;
+    uint16_t *cshift = static_cast<uint16_t *>(s.cmix_x) + (int64_t)l * B * C;
+    float *rnn = static_cast<float *>(s.rnn) + (int64_t)l * B * H * kN * kN;
+
+    LnShiftArgs ls = {w.x0, vec + RWKV7_V_LN1_W * C, vec + RWKV7_V_LN1_B * C, vec + RWKV7_V_X_R * C,
+                      6, w.xmix, tshift, C, T, M};
+    RWKV7_TRY(launch_ln_shift(ls, st));
+    const uint16_t *xr = w.xmix, *xw = w.xmix + MC, *xk = w.xmix + 2 * MC, *xv = w.xmix + 3 * MC,
+                   *xa = w.xmix + 4 * MC, *xg = w.xmix + 5 * MC;
+    GemmProb g1[7] = {
+        {xr, wrkv, w.rkv, C, C, C, C, C, GEPI_F32},
+        {xk, wrkv + (int64_t)C * C, w.rkv + MC, C, C, C, C, C, GEPI_F32},
+        {xv, wrkv + 2 * (int64_t)C * C, w.rkv + 2 * MC, C, C, C, C, C, GEPI_F32},
+        {xv, wl1, w.l1, C, C, SR, rv, C, GEPI_F16},
+        {xw, wl1 + (int64_t)rv * C, w.l1 + rv, C, C, SR, rw, C, GEPI_TANH_F16},
+        {xa, wl1 + (int64_t)(rv + rw) * C, w.l1 + rv + rw, C, C, SR, ra, C, GEPI_F16},
+        {xg, wl1 + (int64_t)(rv + rw + ra) * C, w.l1 + rv + rw + ra, C, C, SR, rg, C, GEPI_SIGM_F16},
+    };
+    RWKV7_TRY(launch_gemm_group(g1, 7, M, st));
+    GemmProb g2[4] = {
+        {w.l1, wl2, w.d, SR, SR, C, C, rv, GEPI_F32},
+        {w.l1 + rv, wl2 + rv, w.d + MC, SR, SR, C, C, rw, GEPI_F32},
+        {w.l1 + rv + rw, wl2 + rv + rw, w.d + 2 * MC, SR, SR, C, C, ra, GEPI_F32},
+        {w.l1 + rv + rw + ra, wl2 + rv + rw + ra, w.d + 3 * MC, SR, SR, C, C, rg, GEPI_F32},
+    };
+    RWKV7_TRY(launch_gemm_group(g2, 4, M, st));
+    GatesArgs ga = {w.rkv, w.d, vec, w.vfirst, w.wkab, C, M, l == 0};
+    RWKV7_TRY(launch_tmix_gates(ga, st));
+    ScanArgs<float, float, float> sc = {rnn,           w.rkv,         w.wkab + MC, w.wkab + 2 * MC,
+                                        w.wkab + 3 * MC, w.wkab + 4 * MC, w.wkab,      w.y,
+                                        B,             T,             H};
+    RWKV7_TRY(launch_wkv7_scan(sc, st));
+    GnGateArgs gn = {w.y, w.rkv, w.wkab + MC, w.wkab + 2 * MC, w.d + 3 * MC, vec, w.yg, C, M};
+    RWKV7_TRY(launch_gn_gate(gn, st));
+    GemmProb go = {w.yg, reinterpret_cast<const uint16_t *>(L + lay.w_o), w.x0, C, C, C, C, C, GEPI_ADD_F32};
+    RWKV7_TRY(launch_gemm_group(&go, 1, M, st));
+
+    LnShiftArgs lc = {w.x0, vec + RWKV7_V_LN2_W * C, vec + RWKV7_V_LN2_B * C, vec + RWKV7_V_FFN_X_K * C,
+                      1, w.xmix, cshift, C, T, M};
+    RWKV7_TRY(launch_ln_shift(lc, st));
+    GemmProb gk = {w.xmix, reinterpret_cast<const uint16_t *>(L + lay.w_fk), w.hid, C, C, F, F, C, GEPI_RELUSQ};
+    RWKV7_TRY(launch_gemm_group(&gk, 1, M, st));
+    GemmProb gv = {w.hid, reinterpret_cast<const uint16_t *>(L + lay.w_fv), w.x0, F, F, C, C, F, GEPI_ADD_F32};
+    RWKV7_TRY(launch_gemm_group(&gv, 1, M, st));
+  }
+  if (logits) {
+    const float *lo = static_cast<const float *>(m.ln_out);
+    RWKV7_TRY(launch_ln_rows(w.x0, 1, lo, lo + C, w.headin, 0, B, C, T, T - 1, st));
+    GemmProb gh = {w.headin, static_cast<const uint16_t *>(m.head), logits, C, C, d.vocab, d.vocab, C, GEPI_F16};
+    RWKV7_TRY(launch_gemm_group(&gh, 1, B, st));
+  }
+  return RWKV7_OK;
+}
+
+static int check_model_state(const rwkv7_model *m, const rwkv7_state *s) {
+  if (!m || !s) return RWKV7_EINVAL;
+  RWKV7_TRY(check_dims(&m->dims));
+  if (!m->layers || !m->emb || !m->head || !m->ln_out) return RWKV7_EINVAL;
+  if (!s->tmix_x || !s->rnn || !s->cmix_x || s->batch < 1) return RWKV7_EINVAL;
+  return RWKV7_OK;
+}
+
+}  // namespace rwkv7
+
+using namespace rwkv7;
+
+extern "C" {
+
+int rwkv7_abi_version(void) { return RWKV7_ABI_VERSION; }
+
+const char *rwkv7_strerror(int code) {
+  switch (code) {
+    case RWKV7_OK: return "ok";
+    case RWKV7_EINVAL: return "invalid argument (null pointer or bad enum value)";
+    case RWKV7_ESHAPE: return "unsupported shape";
+    case RWKV7_EWORKSPACE: return "workspace too small";
+    case RWKV7_ELAUNCH: return "kernel launch failed";
+    default: return "unknown error";
+  }
+}
+
+int rwkv7_layer_layout_get(const rwkv7_dims *dims, rwkv7_layer_layout *out) {
+  RWKV7_TRY(check_dims(dims));
+  if (!out) return RWKV7_EINVAL;
+  layout_of(*dims, out);
+  return RWKV7_OK;
+}
+
+int64_t rwkv7_workspace_bytes(const rwkv7_dims *dims, int32_t batch, int32_t seq_len) {
+  if (check_dims(dims) != RWKV7_OK || batch < 1 || seq_len < 1) return -1;
+  const int64_t a = decode_ws(*dims, nullptr, nullptr);
+  const int64_t b = batch_ws(*dims, batch, seq_len, nullptr, nullptr);
+  return a > b ? a : b;
+}
+
+int rwkv7_decode(const rwkv7_model *model, const rwkv7_state *state, const int64_t *tokens, void *logits,
+                 void *workspace, int64_t workspace_bytes, void *stream) {
+  RWKV7_TRY(check_model_state(model, state));
+  if (!tokens || !workspace) return RWKV7_EINVAL;
+  if (workspace_bytes < rwkv7_workspace_bytes(&model->dims, state->batch, 1)) return RWKV7_EWORKSPACE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (state->batch == 1) return decode_one(*model, *state, tokens, logits, static_cast<char *>(workspace), st);
+  return run_batched(*model, *state, tokens, 1, logits, static_cast<char *>(workspace), st);
+}
+
+int rwkv7_prefill(const rwkv7_model *model, const rwkv7_state *state, const int64_t *tokens, int32_t seq_len,
+                  void *workspace, int64_t workspace_bytes, void *stream) {
+  RWKV7_TRY(check_model_state(model, state));
+  if (!tokens || !workspace) return RWKV7_EINVAL;
+  if (seq_len < 1) return RWKV7_ESHAPE;
+  if (workspace_bytes < rwkv7_workspace_bytes(&model->dims, state->batch, seq_len)) return RWKV7_EWORKSPACE;
+  return run_batched(*model, *state, tokens, seq_len, nullptr, static_cast<char *>(workspace),
+                     static_cast<hipStream_t>(stream));
+}
+
+int rwkv7_wkv7(float *S, const void *r, const void *w, int32_t w_is_f32, const void *k, const void *v,
+               const void *a, const void *b, void *y, int32_t B, int32_t T, int32_t H, void *stream) {
+  if (!S || !r || !w || !k || !v || !a || !b || !y) return RWKV7_EINVAL;
+  if (B < 1 || T < 1 || H < 1) return RWKV7_ESHAPE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint16_t *r16 = static_cast<const uint16_t *>(r), *k16 = static_cast<const uint16_t *>(k),
+                 *v16 = static_cast<const uint16_t *>(v), *a16 = static_cast<const uint16_t *>(a),
+                 *b16 = static_cast<const uint16_t *>(b);
+  uint16_t *y16 = static_cast<uint16_t *>(y);
+  if (w_is_f32) {
+    ScanArgs<uint16_t, float, uint16_t> p = {S, r16, k16, v16, a16, b16, static_cast<const float *>(w), y16, B, T, H};
+    return launch_wkv7_scan(p, st);
+  }
+  ScanArgs<uint16_t, uint16_t, uint16_t> p = {S, r16, k16, v16, a16, b16, static_cast<const uint16_t *>(w), y16, B, T, H};
+  return launch_wkv7_scan(p, st);
+}
+
+int rwkv7_layernorm(const void *x, int32_t x_is_f32, const float *weight, const float *bias, float *y, int32_t M,
+                    int32_t C, void *stream) {
+  if (!x || !weight || !bias || !y) return RWKV7_EINVAL;
+  if (M < 1) return RWKV7_ESHAPE;
+  return launch_ln_rows(x, x_is_f32, weight, bias, y, 1, M, C, 1, 0, static_cast<hipStream_t>(stream));
+}
+
+int rwkv7_lerp(const void *x, const void *prev, const float *mu, int32_t n_mix, void *out, void *x_copy, int32_t C,
+               void *stream) {
+  if (!x || !prev || !mu || !out) return RWKV7_EINVAL;
+  if ((n_mix != 1 && n_mix != 6) || C < 1) return RWKV7_ESHAPE;
+  return launch_lerp(static_cast<const uint16_t *>(x), static_cast<const uint16_t *>(prev), mu, n_mix,
+                     static_cast<uint16_t *>(out), static_cast<uint16_t *>(x_copy), C,
+                     static_cast<hipStream_t>(stream));
+}
+
+int rwkv7_gemv_f16(const float *x, const void *W, int64_t ldw, float *y, int32_t N, int32_t K, void *stream) {
+  if (!x || !W || !y) return RWKV7_EINVAL;
+  if (N < 1 || K < 256 || K % 256 || K > 8192 || ldw < K || ldw % 8) return RWKV7_ESHAPE;
+  GemvArgs g = {};
+  g.W = static_cast<const uint16_t *>(W);
+  g.ldw = ldw;
+  g.N = N;
+  g.K = K;
+  g.x = x;
+  g.y = y;
+  return launch_gemv<PRO_F32, EPI_F32>(g, static_cast<hipStream_t>(stream));
+}
+
+int rwkv7_gemm_f16(const void *A, int64_t lda, const void *W, int64_t ldw, void *Y, int64_t ldy, int32_t M, int32_t N,
+                   int32_t K, int32_t epi, void *stream) {
+  if (!A || !W || !Y) return RWKV7_EINVAL;
+  if (epi < 0 || epi > 3) return RWKV7_EINVAL;
+  if (M < 1 || N < 1 || K < 8 || lda < K || ldw < K || ldy < N) return RWKV7_ESHAPE;
+  GemmProb p = {static_cast<const uint16_t *>(A), static_cast<const uint16_t *>(W), Y, lda, ldw, ldy, N, K, epi};
+  return launch_gemm_group(&p, 1, M, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

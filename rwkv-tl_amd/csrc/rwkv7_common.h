@@ -1,0 +1,98 @@
+// Device-side helpers shared by the RWKV7 gfx950 kernels.
+//
+// Wavefronts are 64 lanes. Reductions use DPP lane permutes inside a 16-lane
+// row and v_readlane across rows, so no reduction touches LDS.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/rwkv7_hip.h"
+
+#define RWKV7_DEV __device__ __forceinline__
+
+namespace rwkv7 {
+
+constexpr int kWave = 64;
+constexpr int kN = RWKV7_HEAD_SIZE;  // head size
+constexpr float kLnEps = 1e-5f;      // F.layer_norm default (src/rwkv_tl/weight.py:15)
+constexpr float kGnEps = 64e-5f;     // GroupNorm eps (demo/rwkv7_torch.py:114)
+// exp(-sigmoid(z) / sqrt(e)) decay (demo/rwkv7_torch.py:101-104); 1/sqrt(e) as float.
+constexpr float kInvSqrtE = 0.60653065971263342f;
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// ---- lane permutes ------------------------------------------------------
+
+template <int CTRL>
+RWKV7_DEV float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <- 7-i within each 8
+constexpr int kDppMirror = 0x140;     // lane i <- 15-i within each 16
+
+// Sum over groups of 4 consecutive lanes; every lane gets its group's sum.
+RWKV7_DEV float sum4(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  return v;
+}
+
+// Sum over each 16-lane row; every lane of the row gets the row sum.
+RWKV7_DEV float sum16(float v) {
+  v = sum4(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppMirror>(v);
+  return v;
+}
+
+// Sum over the whole wave; the result is wave-uniform.
+RWKV7_DEV float lane_value(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+RWKV7_DEV float wave_sum(float v) {
+  v = sum16(v);
+  return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+
+// ---- conversions ----------------------------------------------------------
+
+RWKV7_DEV void h8_to_f(const uint4 &u, float f[8]) {
+  half8 h = __builtin_bit_cast(half8, u);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f[i] = (float)h[i];
+}
+
+RWKV7_DEV uint4 f_to_h8(const float f[8]) {
+  half8 h;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) h[i] = (_Float16)f[i];
+  return __builtin_bit_cast(uint4, h);
+}
+
+RWKV7_DEV float h2f(uint16_t u) { return (float)__builtin_bit_cast(_Float16, u); }
+RWKV7_DEV uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+RWKV7_DEV float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
+
+// Weight streams are read exactly once per step: load them non-temporally so
+// they do not evict the small activation vectors every wave re-reads.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+RWKV7_DEV uint4 ld_stream(const uint4 *p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+}  // namespace rwkv7
+
+#define RWKV7_CHECK_LAUNCH()                                    \
+  do {                                                          \
+    if (hipGetLastError() != hipSuccess) return RWKV7_ELAUNCH;  \
+  } while (0)

@@ -1,0 +1,97 @@
+// Internal interface between the host sequencer (model.hip) and the kernel
+// translation units (gemv.hip, tmix.hip, gemm.hip). Not part of the C ABI.
+#pragma once
+
+#include "rwkv7_common.h"
+
+namespace rwkv7 {
+
+// Kernel argument blocks and launchers, shared by every translation unit.
+enum { PRO_F32 = 0, PRO_TMIX = 1, PRO_CMIX = 2, PRO_LN = 3, PRO_F16 = 4 };
+enum { EPI_F32 = 0, EPI_RESID = 1, EPI_RELUSQ = 2, EPI_F16 = 3 };
+struct GemvArgs {
+  const uint16_t *W;
+  int64_t ldw;
+  int N, K;
+  const void *x;
+  const float *ln_w;
+  const float *ln_b;
+  const uint16_t *prev;
+  const float *mu;
+  int seg_end[7];
+  int seg_mu[7];
+  float *xln_out;
+  void *y;
+};
+template <int PRO, int EPI> int launch_gemv(const GemvArgs &a, hipStream_t st);
+
+struct TmixDecodeArgs {
+  const float *proj;
+  int64_t ldp;
+  const uint16_t *w_lora2;
+  const float *vec;
+  float *vfirst;
+  float *rnn;
+  const float *xln;
+  uint16_t *shift;
+  float *yg;
+  int C, H, rv, rw, ra, rg, layer0;
+};
+int launch_tmix_decode(const TmixDecodeArgs &a, int B, hipStream_t st);
+
+template <typename TI, typename TW, typename TY>
+struct ScanArgs {
+  float *S;
+  const TI *r, *k, *v, *a, *b;
+  const TW *w;
+  TY *y;
+  int B, T, H;
+};
+template <typename TI, typename TW, typename TY>
+int launch_wkv7_scan(const ScanArgs<TI, TW, TY> &p, hipStream_t st);
+
+struct LnShiftArgs {
+  const float *x0;
+  const float *ln_w, *ln_b;
+  const float *mu;
+  int n_mix;
+  uint16_t *out;
+  uint16_t *shift;
+  int C, T, M;
+};
+int launch_ln_shift(const LnShiftArgs &a, hipStream_t st);
+
+struct GatesArgs {
+  const float *rkv;
+  const float *d;
+  const float *vec;
+  float *vfirst;
+  float *wkab;
+  int C, M, layer0;
+};
+int launch_tmix_gates(const GatesArgs &g, hipStream_t st);
+
+struct GnGateArgs {
+  const float *y, *r, *kn, *v, *g, *vec;
+  uint16_t *out;
+  int C, M;
+};
+int launch_gn_gate(const GnGateArgs &a, hipStream_t st);
+
+int launch_embed(const int64_t *tok, const uint16_t *emb, float *x0, int M, int C, int V, hipStream_t st);
+int launch_ln_rows(const void *x, int x_f32, const float *w, const float *b, void *out, int out_f32,
+                   int rows, int C, int stride, int offset, hipStream_t st);
+int launch_lerp(const uint16_t *x, const uint16_t *prev, const float *mu, int n_mix, uint16_t *out,
+                uint16_t *x_copy, int C, hipStream_t st);
+int launch_store_f16(const float *src, uint16_t *dst, int n, hipStream_t st);
+
+enum { GEPI_F32 = 0, GEPI_F16 = 1, GEPI_RELUSQ = 2, GEPI_ADD_F32 = 3, GEPI_TANH_F16 = 4, GEPI_SIGM_F16 = 5 };
+struct GemmProb {
+  const uint16_t *A, *W;
+  void *Y;
+  int64_t lda, ldw, ldy;
+  int N, K, epi;
+};
+int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st);
+
+}  // namespace rwkv7

@@ -1,0 +1,481 @@
+// Time-mix (TMIX) kernels: the wkv7 DPLR recurrence and everything fused
+// around it, plus the small elementwise stages of decode and prefill.
+//
+// wkv7 state: S[h] is 64x64 fp32, S[h][i][j] with i the value row and j the
+// key column (src/rwkv_tl/state.py:37-41). One step (demo/rwkv7_torch.py:49-64):
+//   sa_i  = sum_j S_ij a_j
+//   S'_ij = S_ij w_j + sa_i b_j + v_i k_j
+//   y_i   = sum_j S'_ij r_j
+// Rows are independent given the step's (w, a, b, k, r), so a head's rows can
+// be spread over lanes and workgroups freely; every reduction is along j.
+#include "rwkv7_kernels.h"
+
+namespace rwkv7 {
+
+// ---------------------------------------------------------------------------
+// Decode: one token per sequence, grid (H, B), 256 threads.
+// LoRA second step + gates + L2 norm + wkv7 + GroupNorm + r.k.r_k bonus +
+// output gate. Stands in for fused_gates / fused_l2norm_neg_kk_a / fused_dplr /
+// fused_gn_rkrk (src/rwkv_tl/kernels/gates.py:315-357, dplr.py:229-270) and
+// the gate multiply (demo/_rwkv7_base.py:206).
+// ---------------------------------------------------------------------------
+
+
+__global__ __launch_bounds__(256) void tmix_decode_kernel(TmixDecodeArgs a) {
+  __shared__ float s_lora[512];
+  __shared__ float s_d[4][kN];
+  __shared__ float s_r[kN], s_w[kN], s_k[kN], s_v[kN], s_a[kN], s_b[kN], s_g[kN], s_y[kN];
+  __shared__ float s_rk;
+
+  const int t = threadIdx.x;
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int C = a.C;
+  const int SR = a.rv + a.rw + a.ra + a.rg;
+  const float *prow = a.proj + (int64_t)b * a.ldp;
+  const float *vec = a.vec;
+
+  for (int i = t; i < SR; i += 256) {
+    float x = prow[3 * C + i];
+    if (i >= a.rv && i < a.rv + a.rw) x = tanhf(x);
+    else if (i >= a.rv + a.rw + a.ra) x = sigmoidf_(x);
+    s_lora[i] = x;
+  }
+  __syncthreads();
+
+  {  // LoRA second step: thread -> (gate q, channel c)
+    const int c = t & (kN - 1), q = t >> 6;
+    const int off = q == 0 ? 0 : q == 1 ? a.rv : q == 2 ? a.rv + a.rw : a.rv + a.rw + a.ra;
+    const int R = q == 0 ? a.rv : q == 1 ? a.rw : q == 2 ? a.ra : a.rg;
+    const uint4 *wr = reinterpret_cast<const uint4 *>(a.w_lora2 + (int64_t)(h * kN + c) * SR + off);
+    float acc = 0.f;
+    for (int r = 0; r < R; r += 8) {
+      float wf[8];
+      h8_to_f(wr[r >> 3], wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = fmaf(wf[e], s_lora[off + r + e], acc);
+    }
+    s_d[q][c] = acc;
+  }
+  __syncthreads();
+
+  if (t < kN) {  // gates, one lane per channel of this head
+    const int ch = h * kN + t;
+    const float r = prow[ch], k = prow[C + ch];
+    float v = prow[2 * C + ch];
+    float *vf = a.vfirst + (int64_t)b * C + ch;
+    if (a.layer0) {
+      *vf = v;
+    } else {
+      v = v + sigmoidf_(vec[RWKV7_V_V0 * C + ch] + s_d[0][t]) * (*vf - v);
+    }
+    const float w = expf(-sigmoidf_(vec[RWKV7_V_W0 * C + ch] + s_d[1][t]) / 1.6487212707001282f);
+    const float ag = sigmoidf_(vec[RWKV7_V_A0 * C + ch] + s_d[2][t]);
+    const float kk = k * vec[RWKV7_V_K_K * C + ch];
+    const float kn = k + vec[RWKV7_V_K_A * C + ch] * (k * ag - k);
+    const float nrm = sqrtf(wave_sum(kk * kk));
+    const float kh = kk / fmaxf(nrm, 1e-12f);
+    const float rk = wave_sum(r * kn * vec[RWKV7_V_R_K * C + ch]);
+    s_r[t] = r; s_w[t] = w; s_k[t] = kn; s_v[t] = v;
+    s_a[t] = kh; s_b[t] = -kh * ag; s_g[t] = s_d[3][t];
+    if (t == 0) s_rk = rk;
+    a.shift[(int64_t)b * C + ch] = f2h(a.xln[(int64_t)b * C + ch]);
+  }
+  __syncthreads();
+
+  {  // wkv7: thread -> row i, 16 key columns
+    const int i = t >> 2, j0 = (t & 3) * 16;
+    float4 *Sp = reinterpret_cast<float4 *>(a.rnn + (((int64_t)b * a.H + h) * kN + i) * kN + j0);
+    float S[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float4 u = Sp[q];
+      S[4 * q] = u.x; S[4 * q + 1] = u.y; S[4 * q + 2] = u.z; S[4 * q + 3] = u.w;
+    }
+    float sa = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sa = fmaf(S[e], s_a[j0 + e], sa);
+    sa = sum4(sa);
+    const float vi = s_v[i];
+    float y = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int j = j0 + e;
+      S[e] = S[e] * s_w[j] + sa * s_b[j] + vi * s_k[j];
+      y = fmaf(S[e], s_r[j], y);
+    }
+    y = sum4(y);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) Sp[q] = make_float4(S[4 * q], S[4 * q + 1], S[4 * q + 2], S[4 * q + 3]);
+    if ((t & 3) == 0) s_y[i] = y;
+  }
+  __syncthreads();
+
+  if (t < kN) {  // GroupNorm over the head + bonus + gate
+    const int ch = h * kN + t;
+    const float y = s_y[t];
+    const float mean = wave_sum(y) * (1.f / kN);
+    const float d = y - mean;
+    const float var = wave_sum(d * d) * (1.f / kN);
+    const float yn = d * rsqrtf(var + kGnEps) * vec[RWKV7_V_LNX_W * C + ch] + vec[RWKV7_V_LNX_B * C + ch];
+    a.yg[(int64_t)b * C + ch] = (yn + s_rk * s_v[t]) * s_g[t];
+  }
+}
+
+int launch_tmix_decode(const TmixDecodeArgs &a, int B, hipStream_t st) {
+  tmix_decode_kernel<<<dim3(a.H, B), 256, 0, st>>>(a);
+  RWKV7_CHECK_LAUNCH();
+  return RWKV7_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Serial wkv7 scan over T tokens. Grid (4 * H, B): each workgroup owns 16
+// value rows of one head; lane group of 16 per row, 4 key columns per lane,
+// so both reductions are 16-lane DPP sums. The step inputs of a chunk of
+// kCh tokens are staged in LDS (double-buffered: the next chunk's global loads
+// are issued before the current chunk's serial loop).
+// Stands in for fused_dplr_T (src/rwkv_tl/kernels/dplr.py:174-227,272-285).
+// ---------------------------------------------------------------------------
+
+constexpr int kCh = 16;
+
+
+template <typename T> RWKV7_DEV float to_f(T x);
+template <> RWKV7_DEV float to_f<float>(float x) { return x; }
+template <> RWKV7_DEV float to_f<uint16_t>(uint16_t x) { return h2f(x); }
+template <typename T> RWKV7_DEV T from_f(float x);
+template <> RWKV7_DEV float from_f<float>(float x) { return x; }
+template <> RWKV7_DEV uint16_t from_f<uint16_t>(float x) { return f2h(x); }
+
+template <typename TI, typename TW, typename TY>
+__global__ __launch_bounds__(256) void wkv7_scan_kernel(ScanArgs<TI, TW, TY> p) {
+  // s_in[buf][vec][token][64]: vec 0 w, 1 a, 2 b, 3 k, 4 r, 5 v
+  __shared__ float4 s_in[2][6][kCh][kN / 4];
+  __shared__ float s_y[kCh][16];
+
+  const int t = threadIdx.x;
+  const int h = blockIdx.x >> 2, quarter = blockIdx.x & 3, bi = blockIdx.y;
+  const int row = quarter * 16 + (t >> 4);
+  const int lc = (t & 15);  // owns key columns 4*lc .. 4*lc+3
+  const int H = p.H, T = p.T;
+  const int64_t ld = (int64_t)H * kN;  // elements between consecutive tokens
+  const int64_t base = ((int64_t)bi * T) * ld + (int64_t)h * kN;
+
+  // each thread stages 6 vectors x kCh tokens x 16 float4 / 256 threads = 6 float4
+  constexpr int kPer = 6 * kCh * (kN / 4) / 256;
+  float4 stage[kPer];
+  auto fetch = [&](int c0) {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int idx = t + 256 * u;
+      const int vecid = idx / (kCh * 16), rem = idx % (kCh * 16);
+      const int tok = rem >> 4, q = rem & 15;
+      const int tt = c0 + tok;
+      float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (tt < T) {
+        const int64_t off = base + (int64_t)tt * ld + q * 4;
+        if (vecid == 0) {
+          val = make_float4(to_f(p.w[off]), to_f(p.w[off + 1]), to_f(p.w[off + 2]), to_f(p.w[off + 3]));
+        } else {
+          const TI *src = vecid == 1 ? p.a : vecid == 2 ? p.b : vecid == 3 ? p.k : vecid == 4 ? p.r : p.v;
+          val = make_float4(to_f(src[off]), to_f(src[off + 1]), to_f(src[off + 2]), to_f(src[off + 3]));
+        }
+      }
+      stage[u] = val;
+    }
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int idx = t + 256 * u;
+      const int vecid = idx / (kCh * 16), rem = idx % (kCh * 16);
+      s_in[buf][vecid][rem >> 4][rem & 15] = stage[u];
+    }
+  };
+
+  float4 *Sp = reinterpret_cast<float4 *>(p.S + (((int64_t)bi * H + h) * kN + row) * kN) + lc;
+  float4 S = *Sp;
+
+  fetch(0);
+  commit(0);
+  __syncthreads();
+  const int nch = (T + kCh - 1) / kCh;
+  for (int c = 0; c < nch; ++c) {
+    const int buf = c & 1;
+    if (c + 1 < nch) fetch((c + 1) * kCh);
+    const int steps = min(kCh, T - c * kCh);
+    for (int s = 0; s < steps; ++s) {
+      const float4 w4 = s_in[buf][0][s][lc], a4 = s_in[buf][1][s][lc], b4 = s_in[buf][2][s][lc];
+      const float4 k4 = s_in[buf][3][s][lc], r4 = s_in[buf][4][s][lc];
+      const float vi = reinterpret_cast<const float *>(&s_in[buf][5][s][0])[row];
+      float sa = S.x * a4.x + S.y * a4.y + S.z * a4.z + S.w * a4.w;
+      sa = sum16(sa);
+      S.x = S.x * w4.x + sa * b4.x + vi * k4.x;
+      S.y = S.y * w4.y + sa * b4.y + vi * k4.y;
+      S.z = S.z * w4.z + sa * b4.z + vi * k4.z;
+      S.w = S.w * w4.w + sa * b4.w + vi * k4.w;
+      float y = S.x * r4.x + S.y * r4.y + S.z * r4.z + S.w * r4.w;
+      y = sum16(y);
+      if (lc == 0) s_y[s][t >> 4] = y;
+    }
+    __syncthreads();
+    if (t < steps * 16) {  // write this chunk's y rows: 16 values per token
+      const int s = t >> 4, rr = t & 15;
+      p.y[base + (int64_t)(c * kCh + s) * ld + quarter * 16 + rr] = from_f<TY>(s_y[s][rr]);
+    }
+    if (c + 1 < nch) commit(buf ^ 1);
+    __syncthreads();
+  }
+  *Sp = S;
+}
+
+template <typename TI, typename TW, typename TY>
+int launch_wkv7_scan(const ScanArgs<TI, TW, TY> &p, hipStream_t st) {
+  if (p.T <= 0 || p.B <= 0 || p.H <= 0) return RWKV7_OK;
+  wkv7_scan_kernel<TI, TW, TY><<<dim3(4 * p.H, p.B), 256, 0, st>>>(p);
+  RWKV7_CHECK_LAUNCH();
+  return RWKV7_OK;
+}
+
+template int launch_wkv7_scan<uint16_t, float, uint16_t>(const ScanArgs<uint16_t, float, uint16_t> &, hipStream_t);
+template int launch_wkv7_scan<uint16_t, uint16_t, uint16_t>(const ScanArgs<uint16_t, uint16_t, uint16_t> &, hipStream_t);
+template int launch_wkv7_scan<float, float, float>(const ScanArgs<float, float, float> &, hipStream_t);
+
+// ---------------------------------------------------------------------------
+// Prefill elementwise stages. Rows m = b * T + t of the [M, C] activations.
+// ---------------------------------------------------------------------------
+
+// Block-wide sum over 256 threads (4 waves); all threads get the result.
+RWKV7_DEV float block_sum256(float v, float *scratch4) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch4[w] = v;
+  __syncthreads();
+  return (scratch4[0] + scratch4[1]) + (scratch4[2] + scratch4[3]);
+}
+
+constexpr int kMaxCPer = 16;  // C <= 4096
+// Loop over the C/256 per-thread elements with a compile-time bound so the
+// per-thread arrays stay in registers.
+#define RWKV7_UNROLL_N(i) _Pragma("unroll") for (int i = 0; i < kMaxCPer; ++i) if (i < n)
+
+// LayerNorm of row `row` of x (f32, [*, C]) into out[] (C/256 values per
+// thread, element c = threadIdx.x + 256 * i).
+RWKV7_DEV void ln_row(const float *x, const float *w, const float *bvec, int C, float *out,
+                      float *scratch4) {
+  const int n = C >> 8;
+  float s = 0.f;
+  RWKV7_UNROLL_N(i) {
+    out[i] = x[threadIdx.x + 256 * i];
+    s += out[i];
+  }
+  const float mean = block_sum256(s, scratch4) / (float)C;
+  float q = 0.f;
+  RWKV7_UNROLL_N(i) {
+    const float d = out[i] - mean;
+    q += d * d;
+  }
+  const float rstd = rsqrtf(block_sum256(q, scratch4) / (float)C + kLnEps);
+  RWKV7_UNROLL_N(i) {
+    const int c = threadIdx.x + 256 * i;
+    out[i] = (out[i] - mean) * rstd * w[c] + bvec[c];
+  }
+}
+
+
+// Token shift of prefill (demo/rwkv7_torch.py:189-197, 251-254): prev[t] =
+// LN(x0[t-1]) and prev[0] = state; the state becomes LN(x0[T-1]). The
+// workgroup of t = 0 is the only one that touches the state: it reads it and
+// then writes the new value, so there is no cross-workgroup hazard.
+__global__ __launch_bounds__(256) void ln_shift_kernel(LnShiftArgs a) {
+  __shared__ float scratch4[4];
+  const int m = blockIdx.x;
+  const int t = m % a.T, b = m / a.T;
+  const int C = a.C, n = C >> 8;
+  float x[kMaxCPer], pv[kMaxCPer];
+  ln_row(a.x0 + (int64_t)m * C, a.ln_w, a.ln_b, C, x, scratch4);
+  if (t > 0) {
+    ln_row(a.x0 + (int64_t)(m - 1) * C, a.ln_w, a.ln_b, C, pv, scratch4);
+  } else {
+    RWKV7_UNROLL_N(i) pv[i] = h2f(a.shift[(int64_t)b * C + threadIdx.x + 256 * i]);
+  }
+  for (int j = 0; j < a.n_mix; ++j) {
+    uint16_t *o = a.out + ((int64_t)j * a.M + m) * C;
+    const float *mu = a.mu + (int64_t)j * C;
+    RWKV7_UNROLL_N(i) {
+      const int c = threadIdx.x + 256 * i;
+      o[c] = f2h(x[i] + mu[c] * (pv[i] - x[i]));
+    }
+  }
+  if (t == 0) {
+    float last[kMaxCPer];
+    if (a.T > 1) {
+      ln_row(a.x0 + (int64_t)(m + a.T - 1) * C, a.ln_w, a.ln_b, C, last, scratch4);
+    } else {
+      RWKV7_UNROLL_N(i) last[i] = x[i];
+    }
+    RWKV7_UNROLL_N(i) a.shift[(int64_t)b * C + threadIdx.x + 256 * i] = f2h(last[i]);
+  }
+}
+
+int launch_ln_shift(const LnShiftArgs &a, hipStream_t st) {
+  if (a.C % 256 || a.C > 256 * kMaxCPer) return RWKV7_ESHAPE;
+  ln_shift_kernel<<<a.M, 256, 0, st>>>(a);
+  RWKV7_CHECK_LAUNCH();
+  return RWKV7_OK;
+}
+
+
+// Gate math for prefill rows (demo/rwkv7_torch.py:203-224), one wave per
+// (row, head); lane = channel.
+__global__ __launch_bounds__(256) void tmix_gates_kernel(GatesArgs g) {
+  const int C = g.C;
+  const int gh = blockIdx.x * 4 + (threadIdx.x >> 6);  // global (row, head) index
+  const int H = C / kN;
+  const int m = gh / H, h = gh % H;
+  if (m >= g.M) return;
+  const int ch = h * kN + (threadIdx.x & 63);
+  const int64_t o = (int64_t)m * C + ch, MC = (int64_t)g.M * C;
+  const float *vec = g.vec;
+  const float k = g.rkv[MC + o];
+  float v = g.rkv[2 * MC + o];
+  if (g.layer0) {
+    g.vfirst[o] = v;
+  } else {
+    v = v + sigmoidf_(vec[RWKV7_V_V0 * C + ch] + g.d[o]) * (g.vfirst[o] - v);
+  }
+  const float w = expf(-sigmoidf_(vec[RWKV7_V_W0 * C + ch] + g.d[MC + o]) / 1.6487212707001282f);
+  const float ag = sigmoidf_(vec[RWKV7_V_A0 * C + ch] + g.d[2 * MC + o]);
+  const float kk = k * vec[RWKV7_V_K_K * C + ch];
+  const float kn = k + vec[RWKV7_V_K_A * C + ch] * (k * ag - k);
+  const float nrm = sqrtf(wave_sum(kk * kk));
+  const float kh = kk / fmaxf(nrm, 1e-12f);
+  g.wkab[o] = w;
+  g.wkab[MC + o] = kn;
+  g.wkab[2 * MC + o] = v;
+  g.wkab[3 * MC + o] = kh;
+  g.wkab[4 * MC + o] = -kh * ag;
+}
+
+int launch_tmix_gates(const GatesArgs &g, hipStream_t st) {
+  const int waves = g.M * (g.C / kN);
+  tmix_gates_kernel<<<(waves + 3) / 4, 256, 0, st>>>(g);
+  RWKV7_CHECK_LAUNCH();
+  return RWKV7_OK;
+}
+
+
+// GroupNorm + r.k.r_k bonus + gate (demo/rwkv7_torch.py:234-242).
+__global__ __launch_bounds__(256) void gn_gate_kernel(GnGateArgs a) {
+  const int C = a.C, H = C / kN;
+  const int gh = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int m = gh / H, h = gh % H;
+  if (m >= a.M) return;
+  const int ch = h * kN + (threadIdx.x & 63);
+  const int64_t o = (int64_t)m * C + ch;
+  const float y = a.y[o];
+  const float mean = wave_sum(y) * (1.f / kN);
+  const float d = y - mean;
+  const float var = wave_sum(d * d) * (1.f / kN);
+  const float yn = d * rsqrtf(var + kGnEps) * a.vec[RWKV7_V_LNX_W * C + ch] + a.vec[RWKV7_V_LNX_B * C + ch];
+  const float rk = wave_sum(a.r[o] * a.kn[o] * a.vec[RWKV7_V_R_K * C + ch]);
+  a.out[o] = f2h((yn + rk * a.v[o]) * a.g[o]);
+}
+
+int launch_gn_gate(const GnGateArgs &a, hipStream_t st) {
+  const int waves = a.M * (a.C / kN);
+  gn_gate_kernel<<<(waves + 3) / 4, 256, 0, st>>>(a);
+  RWKV7_CHECK_LAUNCH();
+  return RWKV7_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Small utility kernels.
+// ---------------------------------------------------------------------------
+
+// x0[m] = emb[tok[m]] as f32 (F.embedding, demo/rwkv7_torch.py:173-175).
+__global__ void embed_kernel(const int64_t *tok, const uint16_t *emb, float *x0, int C, int V) {
+  const int m = blockIdx.x;
+  int64_t id = tok[m];
+  id = id < 0 ? 0 : id >= V ? V - 1 : id;
+  const uint16_t *row = emb + id * C;
+  for (int c = threadIdx.x; c < C; c += blockDim.x) x0[(int64_t)m * C + c] = h2f(row[c]);
+}
+
+int launch_embed(const int64_t *tok, const uint16_t *emb, float *x0, int M, int C, int V, hipStream_t st) {
+  embed_kernel<<<M, 256, 0, st>>>(tok, emb, x0, C, V);
+  RWKV7_CHECK_LAUNCH();
+  return RWKV7_OK;
+}
+
+// out[i] = f16(LN(x[row_i])) with row_i = i * stride + offset (gathers the
+// last token of each sequence before the LM head).
+__global__ __launch_bounds__(256) void ln_rows_kernel(const void *x, int x_f32, const float *w,
+                                                      const float *bvec, void *out, int out_f32,
+                                                      int C, int stride, int offset) {
+  __shared__ float scratch4[4];
+  const int i = blockIdx.x;
+  const int64_t src = (int64_t)i * stride + offset;
+  const int n = C >> 8;
+  float v[kMaxCPer];
+  float s = 0.f;
+  RWKV7_UNROLL_N(q) {
+    const int c = threadIdx.x + 256 * q;
+    v[q] = x_f32 ? reinterpret_cast<const float *>(x)[src * C + c]
+                 : h2f(reinterpret_cast<const uint16_t *>(x)[src * C + c]);
+    s += v[q];
+  }
+  const float mean = block_sum256(s, scratch4) / (float)C;
+  float qv = 0.f;
+  RWKV7_UNROLL_N(q) {
+    const float d = v[q] - mean;
+    qv += d * d;
+  }
+  const float rstd = rsqrtf(block_sum256(qv, scratch4) / (float)C + kLnEps);
+  RWKV7_UNROLL_N(q) {
+    const int c = threadIdx.x + 256 * q;
+    const float y = (v[q] - mean) * rstd * w[c] + bvec[c];
+    if (out_f32) reinterpret_cast<float *>(out)[(int64_t)i * C + c] = y;
+    else reinterpret_cast<uint16_t *>(out)[(int64_t)i * C + c] = f2h(y);
+  }
+}
+
+int launch_ln_rows(const void *x, int x_f32, const float *w, const float *b, void *out, int out_f32,
+                   int rows, int C, int stride, int offset, hipStream_t st) {
+  if (C % 256 || C > 256 * kMaxCPer) return RWKV7_ESHAPE;
+  ln_rows_kernel<<<rows, 256, 0, st>>>(x, x_f32, w, b, out, out_f32, C, stride, offset);
+  RWKV7_CHECK_LAUNCH();
+  return RWKV7_OK;
+}
+
+// Token-shift lerps for one vector (src/rwkv_tl/kernels/lerp.py:140-198).
+__global__ void lerp_kernel(const uint16_t *x, const uint16_t *prev, const float *mu, int n_mix,
+                            uint16_t *out, uint16_t *x_copy, int C) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  const float xv = h2f(x[c]), pv = h2f(prev[c]);
+  for (int j = 0; j < n_mix; ++j) out[(int64_t)j * C + c] = f2h(xv + mu[(int64_t)j * C + c] * (pv - xv));
+  if (x_copy) x_copy[c] = x[c];  // after this thread's read of prev[c]
+}
+
+int launch_lerp(const uint16_t *x, const uint16_t *prev, const float *mu, int n_mix, uint16_t *out,
+                uint16_t *x_copy, int C, hipStream_t st) {
+  lerp_kernel<<<(C + 255) / 256, 256, 0, st>>>(x, prev, mu, n_mix, out, x_copy, C);
+  RWKV7_CHECK_LAUNCH();
+  return RWKV7_OK;
+}
+
+// Copies f32 -> f16 (decode: the channel-mix token-shift state update after
+// the FFN key GEMV has read the old state).
+__global__ void store_f16_kernel(const float *src, uint16_t *dst, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = f2h(src[i]);
+}
+
+int launch_store_f16(const float *src, uint16_t *dst, int n, hipStream_t st) {
+  store_f16_kernel<<<(n + 255) / 256, 256, 0, st>>>(src, dst, n);
+  RWKV7_CHECK_LAUNCH();
+  return RWKV7_OK;
+}
+
+}  // namespace rwkv7

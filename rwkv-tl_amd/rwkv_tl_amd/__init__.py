@@ -1,0 +1,71 @@
+"""rwkv_tl_amd: RWKV7 inference on AMD Instinct MI355X (gfx950) with hand-written HIP kernels.
+
+Drop-in for the GPU path of yuyi2439/rwkv-tl:
+
+* ``State``, ``RWKV7Weight``, ``LNWeight`` -- ``rwkv_tl.state`` / ``rwkv_tl.weight``
+* ``RWKV7Model`` -- ``demo._rwkv7_abc.RWKV7Model`` (decode / prefill / forward / generate)
+* ``RWKV7HIP`` -- the HIP model (stands in for ``demo.rwkv7_fp16.RWKV7FP16``)
+* ``HIPGraph`` / ``make_graph_cls`` -- ``demo.cuda_graph.CUDAGraph`` / ``make_graph_cls``
+* ``make_rwkv7`` -- ``demo.make_rwkv7``
+* ``kernels`` -- the operator-level API of ``rwkv_tl.kernels.fp16``
+* ``sample_logits`` -- ``demo.sampling.sample_logits``
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .checkpoint import SHAPES, ModelShape, make_random_state_dict
+from .hip_graph import HIPGraph, make_graph_cls, wrap_model
+from .model import RWKV7Model
+from .rwkv7_hip import RWKV7HIP
+from .sampling import sample_logits
+from .state import State
+from .weight import LNWeight, RWKV7Weight
+
+__all__ = [
+    "HIPGraph",
+    "LNWeight",
+    "ModelShape",
+    "RWKV7HIP",
+    "RWKV7Model",
+    "RWKV7Weight",
+    "SHAPES",
+    "State",
+    "make_graph_cls",
+    "make_random_state_dict",
+    "make_rwkv7",
+    "sample_logits",
+    "wrap_model",
+]
+
+# Backend names of demo/__init__.py:81-120. Every GPU-class name maps to the one
+# HIP model; the NVIDIA-specific variants (mx450, rtx3060) have no meaning on
+# MI355X and are accepted as aliases so existing scripts keep working.
+_HIP_BACKENDS = ("tuned", "auto", "fp16", "hip", "rtx3060", "mx450")
+
+
+def make_rwkv7(
+    device: torch.device | str,
+    *,
+    backend: str = "tuned",
+    use_graph: bool = True,
+    device_name: str | None = None,
+) -> type[RWKV7Model]:
+    """Pick the model class for ``device`` (``demo/__init__.py:43-78``).
+
+    Returns ``RWKV7HIP`` wrapped in ``HIPGraph`` when ``use_graph`` (the
+    default) and the device is a GPU. ``backend="bf16"`` and
+    ``backend="torch"`` raise: this library is fp16-only, and the pure-torch
+    reference model is a test oracle here, not a product backend.
+    """
+    device = torch.device(device)
+    if backend == "bf16":
+        raise ValueError("backend 'bf16' is not provided: the HIP kernels are float16 only")
+    if backend == "torch":
+        raise ValueError("backend 'torch' is not provided: the pure-torch model is only a test oracle here")
+    if backend not in _HIP_BACKENDS:
+        raise ValueError(f"unknown backend {backend!r} (expected one of {', '.join(_HIP_BACKENDS)})")
+    if device.type != "cuda":
+        raise ValueError(f"RWKV7HIP runs on a ROCm GPU; got device {device}")
+    return make_graph_cls(RWKV7HIP) if use_graph else RWKV7HIP

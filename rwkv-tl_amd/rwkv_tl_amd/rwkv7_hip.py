@@ -1,0 +1,178 @@
+"""``RWKV7HIP``: the RWKV7 model on hand-written gfx950 HIP kernels.
+
+Stands in for ``RWKV7FP16`` / ``RWKV7Base`` (``demo/rwkv7_fp16.py:16-25``,
+``demo/_rwkv7_base.py:33-310``). Every step is one call into
+``librwkv7_hip.so``:
+
+* ``decode`` -> ``rwkv7_decode``: one sequence runs fused fp16 GEMV kernels
+  (LayerNorm and token shift folded into the projection prologues, LoRA +
+  gates + wkv7 + GroupNorm + output gate in one per-head kernel); several
+  sequences run the MFMA GEMM path with M = batch.
+* ``prefill`` -> ``rwkv7_prefill``: MFMA GEMMs for every projection and a
+  serial, LDS-staged wkv7 scan per head.
+
+There is no CPU or torch fallback: without the library, construction raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+from torch import Tensor
+
+from . import _lib
+from .model import RWKV7Model
+from .state import State
+from .weight import RWKV7Weight, pack_device_weights
+
+
+class RWKV7HIP(RWKV7Model):
+    """RWKV7 decode / prefill on MI355X (fp16 weights, fp32 state and accumulation).
+
+    Args:
+        w: weights loaded as float16 on a ROCm device.
+        is_torch_compile: accepted for signature compatibility with the
+            reference classes and ignored (launch overhead is removed with HIP
+            graphs instead, see ``HIPGraph``).
+    """
+
+    def __init__(self, w: RWKV7Weight, *, is_torch_compile: bool = True) -> None:
+        super().__init__(w)
+        if w.dtype != torch.float16:
+            raise ValueError(f"kernel dtype torch.float16 does not match weight dtype {w.dtype}")
+        if w.device.type != "cuda":
+            raise ValueError(f"RWKV7HIP needs the weights on a ROCm GPU, got {w.device}")
+        self._is_torch_compile = is_torch_compile
+        self._lib = _lib.load()
+        self.dev = pack_device_weights(w)
+        self.V = int(self.dev.dims.vocab)
+        self._ws: Tensor | None = None
+        self._ws_bytes = 0
+        self._ws_retired: list[Tensor] = []  # kept alive: captured graphs may point at them
+
+    # ------------------------------------------------------------------ #
+    # buffers and descriptors
+    # ------------------------------------------------------------------ #
+
+    def workspace(self, batch: int, seq_len: int) -> Tensor:
+        """A scratch buffer big enough for ``batch x seq_len`` (grown, never shrunk)."""
+        need = int(self._lib.rwkv7_workspace_bytes(ctypes.byref(self.dev.dims), batch, seq_len))
+        if need < 0:
+            raise ValueError(f"unsupported batch={batch} seq_len={seq_len}")
+        if self._ws is None or self._ws_bytes < need:
+            if self._ws is not None:
+                self._ws_retired.append(self._ws)
+            self._ws = torch.empty(need, dtype=torch.uint8, device=self.w.device)
+            self._ws_bytes = need
+        return self._ws
+
+    def _check_state(self, S: State) -> None:
+        t0 = S[0][0]
+        if len(S[0]) != self.L or t0["x"].shape[-1] != self.C:
+            raise ValueError(f"state of {len(S[0])} layers x {t0['x'].shape[-1]} does not fit the model")
+        if t0["x"].dtype != torch.float16:
+            raise ValueError(f"state dtype {t0['x'].dtype} does not match the model dtype torch.float16")
+        if t0["x"].device != self.w.device:
+            raise ValueError(f"state on {t0['x'].device}, model on {self.w.device}")
+
+    @staticmethod
+    def _batch_of(S: State) -> int:
+        return 1 if S[0][0]["rnn"].dim() == 3 else S[0][0]["rnn"].shape[0]
+
+    def _arena_state(self, S: State) -> tuple[State, bool]:
+        """``S`` itself if its tensors are intact arena views, else a copy."""
+        if isinstance(S, State) and S.arena_intact():
+            return S, False
+        shadow = State(self.L, self.C, self.N, device=self.w.device, dtype=torch.float16,
+                       batch=None if S[0][0]["rnn"].dim() == 3 else self._batch_of(S))
+        shadow.copy_(S)
+        return shadow, True
+
+    @staticmethod
+    def _desc(S: State) -> _lib.StateDesc:
+        tx, rnn, cx = S.arenas
+        return _lib.StateDesc(tmix_x=tx.data_ptr(), rnn=rnn.data_ptr(), cmix_x=cx.data_ptr(), batch=S.batch_size)
+
+    def _tokens(self, tokens, shape: tuple[int, ...]) -> Tensor:
+        t = torch.as_tensor(tokens)
+        if t.numel() != int(torch.Size(shape).numel()):
+            raise ValueError(f"expected {shape} token ids, got shape {tuple(t.shape)}")
+        if t.dtype not in (torch.int64, torch.int32, torch.int16, torch.uint8):
+            raise ValueError(f"token ids must be integers, got {t.dtype}")
+        if t.device.type == "cpu" and t.numel() and (int(t.min()) < 0 or int(t.max()) >= self.V):
+            raise ValueError(f"token id out of range [0, {self.V})")
+        return t.to(device=self.w.device, dtype=torch.int64).reshape(shape).contiguous()
+
+    # ------------------------------------------------------------------ #
+    # raw steps (also what HIPGraph captures)
+    # ------------------------------------------------------------------ #
+
+    def decode_into(self, tok: Tensor, S: State, logits: Tensor | None) -> None:
+        """One decode step: ``tok`` int64 [B] on device, ``logits`` f16 [B, V] or None."""
+        B = S.batch_size
+        ws = self.workspace(B, 1)
+        sd = self._desc(S)
+        rc = self._lib.rwkv7_decode(
+            ctypes.byref(self.dev.desc), ctypes.byref(sd), tok.data_ptr(),
+            None if logits is None else logits.data_ptr(), ws.data_ptr(), ws.numel(),
+            _lib.stream_handle(),
+        )
+        _lib.check(rc, "rwkv7_decode")
+
+    def prefill_into(self, tok: Tensor, S: State) -> None:
+        """Prefill ``tok`` int64 [B, T] on device into ``S``."""
+        B, T = tok.shape
+        ws = self.workspace(B, T)
+        sd = self._desc(S)
+        rc = self._lib.rwkv7_prefill(
+            ctypes.byref(self.dev.desc), ctypes.byref(sd), tok.data_ptr(), T, ws.data_ptr(),
+            ws.numel(), _lib.stream_handle(),
+        )
+        _lib.check(rc, "rwkv7_prefill")
+
+    # ------------------------------------------------------------------ #
+    # RWKV7Model interface
+    # ------------------------------------------------------------------ #
+
+    def decode(self, token: Tensor, S: State) -> tuple[Tensor, State]:
+        """Advance one token per sequence; logits ``[V]`` (or ``[B, V]`` for a batched state)."""
+        self._check_state(S)
+        B = self._batch_of(S)
+        tok = self._tokens(token, (B,))
+        run, shadow = self._arena_state(S)
+        logits = torch.empty(B, self.V, dtype=torch.float16, device=self.w.device)
+        self.decode_into(tok, run, logits)
+        if shadow:
+            _copy_into(S, run)
+        return (logits[0] if S[0][0]["rnn"].dim() == 3 else logits), S
+
+    def prefill(self, tokens: Tensor, S: State) -> State:
+        """Consume ``tokens`` (``[T]``, or ``[B, T]`` for a batched state) in place."""
+        self._check_state(S)
+        tokens = torch.as_tensor(tokens)
+        if tokens.numel() == 0:
+            raise RuntimeError("prefill received an empty token sequence")
+        batched = S[0][0]["rnn"].dim() == 4
+        B = self._batch_of(S)
+        if batched:
+            if tokens.ndim != 2 or tokens.shape[0] != B:
+                raise ValueError(f"Expected [{B}, T] token ids for a batch-{B} state, got {tuple(tokens.shape)}")
+            shape = (B, tokens.shape[1])
+        else:
+            if tokens.ndim != 1:
+                raise ValueError(f"Expected 1D token sequence, got {tokens.shape}")
+            shape = (1, tokens.shape[0])
+        tok = self._tokens(tokens, shape)
+        run, shadow = self._arena_state(S)
+        self.prefill_into(tok, run)
+        if shadow:
+            _copy_into(S, run)
+        return S
+
+
+def _copy_into(dst, src: State) -> None:
+    """Copy ``src`` into any ``(tmix, cmix)`` state of the same shape."""
+    for ds, ss in zip(dst[0] + dst[1], src[0] + src[1]):
+        for k in ds:
+            ds[k].copy_(ss[k])

@@ -1,0 +1,208 @@
+"""RWKV7 weights (drop-in for ``rwkv_tl.weight``) and their HIP device arena.
+
+``RWKV7Weight(model_path, device=None, dtype=torch.float16)`` keeps the
+reference's loader contract and attribute layout (``src/rwkv_tl/weight.py``):
+tensors are cast to ``dtype`` at load (``:167-169``), matrices are kept
+transposed ``[in, out]`` with ``rkvWt`` stacked ``[3, C, C]`` (``:98-106``), the
+LoRA first steps in both orientations (``:77-91``) and the embedding
+layer-normalised once at load in ``dtype`` (``:175``). Checkpoints are read
+with ``torch.load(weights_only=True)``.
+
+``pack_device_weights`` builds what the HIP library reads: one contiguous arena
+per layer with every matrix in ``[out, in]`` (K-contiguous) order, the stacked
+``[3C + sumR, C]`` projection matrix for decode, per-head-contiguous LoRA
+second steps and the small vectors as fp32 (layout from
+``rwkv7_layer_layout_get`` in ``include/rwkv7_hip.h``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+from . import _lib
+
+
+class LNWeight:
+    """LayerNorm weight/bias; ``weight.py:6-15`` (``F.layer_norm``, eps 1e-5)."""
+
+    w: Tensor
+    b: Tensor
+
+    def __init__(self, W, prefix: str):
+        self.w = W[f"{prefix}.weight"]
+        self.b = W[f"{prefix}.bias"]
+
+    def __call__(self, x: Tensor) -> Tensor:
+        return F.layer_norm(x, (x.shape[-1],), self.w, self.b)
+
+
+class RWKV7ATTWeight:
+    """Time-mix weights; attribute layout of ``weight.py:18-106``."""
+
+    def __init__(self, W, prefix: str, ln_pre: LNWeight):
+        self.ln_pre = ln_pre
+        self.ln_x = LNWeight(W, f"{prefix}.ln_x")
+        for n in ("x_r", "x_w", "x_k", "x_v", "x_a", "x_g"):
+            setattr(self, n, W[f"{prefix}.{n}"].squeeze())
+        for g in ("w", "a", "v", "g"):
+            setattr(self, f"{g}1", W[f"{prefix}.{g}1"])
+            setattr(self, f"{g}1t", W[f"{prefix}.{g}1"].t().contiguous())
+            setattr(self, f"{g}2", W[f"{prefix}.{g}2"])
+        for n in ("w0", "a0", "v0", "r_k", "k_k", "k_a"):
+            setattr(self, n, W[f"{prefix}.{n}"])
+        self.rkvWt = torch.stack(
+            [W[f"{prefix}.{m}.weight"].T.contiguous() for m in ("receptance", "key", "value")]
+        )
+        self.oWt = W[f"{prefix}.output.weight"].T.contiguous()
+
+
+class RWKV7FFNWeight:
+    """Channel-mix weights; ``weight.py:109-126``."""
+
+    def __init__(self, W, prefix: str, ln_pre: LNWeight):
+        self.ln_pre = ln_pre
+        self.x_k = W[f"{prefix}.x_k"].squeeze()
+        self.kWt = W[f"{prefix}.key.weight"].T.contiguous()
+        self.vWt = W[f"{prefix}.value.weight"].T.contiguous()
+
+
+class RWKV7Block:
+    def __init__(self, W, prefix: str):
+        self.att = RWKV7ATTWeight(W, f"{prefix}.att", LNWeight(W, f"{prefix}.ln1"))
+        self.ffn = RWKV7FFNWeight(W, f"{prefix}.ffn", LNWeight(W, f"{prefix}.ln2"))
+
+
+class RWKV7Weight:
+    """Loaded RWKV7 weights; constructor contract of ``weight.py:155-184``."""
+
+    dtype: torch.dtype
+    device: torch.device
+    L: int
+    C: int
+
+    def __init__(
+        self,
+        model_path: str | None,
+        device: str | torch.device | None = None,
+        dtype: torch.dtype = torch.float16,
+        *,
+        state_dict: dict[str, Tensor] | None = None,
+    ):
+        if state_dict is None:
+            if model_path is None:
+                raise ValueError("either model_path or state_dict is required")
+            state_dict = torch.load(model_path, map_location=device, weights_only=True)
+        W = {
+            k: (v.to(device=device, dtype=dtype) if isinstance(v, Tensor) else v)
+            for k, v in state_dict.items()
+        }
+        self.head = W["head.weight"]
+        self.ln_in = LNWeight(W, "blocks.0.ln0")
+        self.ln_out = LNWeight(W, "ln_out")
+        self.emb = self.ln_in(W["emb.weight"])
+        self.dtype = dtype
+        self.device = self.emb.device
+        self.L = 1 + max(int(k.split(".")[1]) for k in W if k.startswith("blocks."))
+        self.C = self.emb.shape[1]
+        self.blocks = [RWKV7Block(W, f"blocks.{i}") for i in range(self.L)]
+
+    @classmethod
+    def from_state_dict(
+        cls,
+        state_dict: dict[str, Tensor],
+        device: str | torch.device | None = None,
+        dtype: torch.dtype = torch.float16,
+    ) -> "RWKV7Weight":
+        return cls(None, device=device, dtype=dtype, state_dict=state_dict)
+
+
+@dataclass
+class DeviceWeights:
+    """Device arenas of one model plus the ctypes descriptor pointing at them."""
+
+    dims: _lib.Dims
+    layout: _lib.LayerLayout
+    layers: Tensor   # uint8 [L, layout.bytes]
+    emb: Tensor      # f16 [V, C]
+    head: Tensor     # f16 [V, C]
+    ln_out: Tensor   # f32 [2, C]
+    desc: _lib.Model
+
+    @property
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.layers, self.emb, self.head, self.ln_out))
+
+
+def model_dims(w: RWKV7Weight) -> _lib.Dims:
+    att = w.blocks[0].att
+    return _lib.Dims(
+        n_layer=w.L,
+        n_embd=w.C,
+        n_head=w.C // 64,
+        n_ffn=w.blocks[0].ffn.kWt.shape[1],
+        vocab=w.head.shape[0],
+        rank_w=att.w1.shape[1],
+        rank_a=att.a1.shape[1],
+        rank_v=att.v1.shape[1],
+        rank_g=att.g1.shape[1],
+    )
+
+
+def layer_layout(dims: _lib.Dims) -> _lib.LayerLayout:
+    lib = _lib.load()
+    out = _lib.LayerLayout()
+    _lib.check(lib.rwkv7_layer_layout_get(ctypes.byref(dims), ctypes.byref(out)), "rwkv7_layer_layout_get")
+    return out
+
+
+def _f16_view(buf: Tensor, off: int, rows: int, cols: int) -> Tensor:
+    return buf[off : off + rows * cols * 2].view(torch.float16).view(rows, cols)
+
+
+def pack_device_weights(w: RWKV7Weight) -> DeviceWeights:
+    """Build the HIP arenas from reference-layout weights (fp16, on the GPU)."""
+    if w.dtype != torch.float16:
+        raise ValueError(f"the HIP kernels take float16 weights, got {w.dtype}")
+    dims = model_dims(w)
+    lay = layer_layout(dims)
+    C, F_ = dims.n_embd, dims.n_ffn
+    SR = dims.rank_w + dims.rank_a + dims.rank_v + dims.rank_g
+    dev = w.device
+    layers = torch.zeros(dims.n_layer, lay.bytes, dtype=torch.uint8, device=dev)
+    for i, blk in enumerate(w.blocks):
+        att, ffn, buf = blk.att, blk.ffn, layers[i]
+        rkv = _f16_view(buf, lay.w_rkv, 3 * C, C)
+        for j in range(3):
+            rkv[j * C : (j + 1) * C].copy_(att.rkvWt[j].T)
+        _f16_view(buf, lay.w_lora1, SR, C).copy_(torch.cat([att.v1t, att.w1t, att.a1t, att.g1t], 0))
+        _f16_view(buf, lay.w_lora2, C, SR).copy_(torch.cat([att.v2.T, att.w2.T, att.a2.T, att.g2.T], 1))
+        _f16_view(buf, lay.w_o, C, C).copy_(att.oWt.T)
+        _f16_view(buf, lay.w_fk, F_, C).copy_(ffn.kWt.T)
+        _f16_view(buf, lay.w_fv, C, F_).copy_(ffn.vWt.T)
+        vec = buf[lay.vec : lay.vec + _lib.NVEC * C * 4].view(torch.float32).view(_lib.NVEC, C)
+        src = {
+            "ln1_w": att.ln_pre.w, "ln1_b": att.ln_pre.b,
+            "x_r": att.x_r, "x_w": att.x_w, "x_k": att.x_k, "x_v": att.x_v,
+            "x_a": att.x_a, "x_g": att.x_g, "w0": att.w0, "a0": att.a0, "v0": att.v0,
+            "k_k": att.k_k, "k_a": att.k_a, "r_k": att.r_k,
+            "lnx_w": att.ln_x.w, "lnx_b": att.ln_x.b,
+            "ln2_w": ffn.ln_pre.w, "ln2_b": ffn.ln_pre.b, "ffn_x_k": ffn.x_k,
+        }
+        for j, name in enumerate(_lib.VEC_NAMES):
+            vec[j].copy_(src[name].reshape(-1).float())
+    emb = w.emb.contiguous()
+    head = w.head.contiguous()
+    ln_out = torch.stack([w.ln_out.w.float(), w.ln_out.b.float()]).contiguous()
+    desc = _lib.Model(
+        dims=dims,
+        layers=layers.data_ptr(),
+        emb=emb.data_ptr(),
+        head=head.data_ptr(),
+        ln_out=ln_out.data_ptr(),
+    )
+    return DeviceWeights(dims, lay, layers, emb, head, ln_out, desc)

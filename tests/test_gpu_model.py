@@ -1,0 +1,233 @@
+"""Model-level parity of the HIP path (GPU) against the CPU oracle.
+
+Two oracles, both the restated pure-torch model (``oracle/rwkv7_ref.py``) on
+the very same fp16 weights and embedding rows:
+
+* ``ref32``: fp32 math on the fp16 weights, fp16 token-shift state (the drop-in
+  ``State`` layout stores x in fp16). The HIP decode keeps every intermediate
+  in fp32, so this is the tight comparison: logits within 1e-2 abs + 1e-3 rel
+  (fp16 logits) and the fp32 wkv state within 1e-4 relative (Frobenius, per
+  layer) after many steps.
+* ``ref16``: the reference's own fp16 semantics (every torch op rounds to
+  fp16). Logits must still be within 1e-2 abs + 1e-3 rel. The state is only
+  compared loosely: the fp16 path's own state error vs exact fp32 math is
+  ~2e-3 relative, so 1e-4 against it is not attainable by any fp32 kernel.
+
+Prefill rounds the GEMM operands to fp16 (MFMA inputs), so its bars are the
+fp16-path ones; decode-after-prefill logits keep the 1e-2 / 1e-3 bar.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import rwkv7_ref as R
+from rwkv_tl_amd import RWKV7HIP, HIPGraph, State, make_rwkv7
+from rwkv_tl_amd.checkpoint import make_random_state_dict
+from rwkv_tl_amd.weight import RWKV7Weight
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_ATOL, LOGIT_RTOL = 1e-2, 1e-3
+STATE_REL = 1e-4
+
+
+def _rel(x, y):
+    return float((x.double() - y.double()).norm() / y.double().norm().clamp_min(1e-30))
+
+
+class Setup:
+    def __init__(self, shape: str, cuda):
+        self.sd = make_random_state_dict(shape, seed=0, dtype=torch.float16)
+        self.w = RWKV7Weight.from_state_dict(self.sd, device=cuda, dtype=torch.float16)
+        self.model = RWKV7HIP(self.w, is_torch_compile=False)
+        emb = self.w.emb.cpu()
+        self.ref32 = R.Weights.from_emb(self.sd, emb, torch.float32)
+        self.ref16 = R.Weights.from_emb(self.sd, emb, torch.float16)
+
+
+_CACHE: dict[str, Setup] = {}
+
+
+def setup_for(shape, cuda) -> Setup:
+    if shape not in _CACHE:
+        _CACHE.clear()
+        _CACHE[shape] = Setup(shape, cuda)
+    return _CACHE[shape]
+
+
+def _tokens(n, vocab, seed=1):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, vocab, (n,), generator=g)
+
+
+def _check_logits(got, ref, label):
+    got = got.float().cpu()
+    ref = ref.float().cpu()
+    bad = (got - ref).abs() > LOGIT_ATOL + LOGIT_RTOL * ref.abs()
+    assert not bool(bad.any()), f"{label}: {int(bad.sum())} logits off, max |d|={(got - ref).abs().max():.3e}"
+    assert int(got.argmax()) == int(ref.argmax()) or (got.max() - got[ref.argmax()]) < 2e-2, label
+
+
+def _check_state(S: State, ref_state, rel_bar, label):
+    for i in range(len(S.tmix)):
+        r = _rel(S.tmix[i]["rnn"].cpu(), ref_state[0][i]["rnn"])
+        assert r < rel_bar, f"{label}: layer {i} rnn rel err {r:.2e}"
+        xt = (S.tmix[i]["x"].cpu().float() - ref_state[0][i]["x"].float()).abs().max()
+        xc = (S.cmix[i]["x"].cpu().float() - ref_state[1][i]["x"].float()).abs().max()
+        assert xt <= 2e-2 and xc <= 2e-2, f"{label}: layer {i} shift state off ({xt:.2e}, {xc:.2e})"
+
+
+@pytest.mark.parametrize("shape,steps", [("tiny", 24), ("0.1b", 64)])
+def test_decode_matches_oracle(shape, steps, cuda):
+    print(f"decode parity {shape} steps={steps}", flush=True)
+    st = setup_for(shape, cuda)
+    toks = _tokens(steps, st.w.head.shape[0])
+    S = State(st.w.L, st.w.C, 64, device=cuda)
+    s32 = R.new_state(st.w.L, st.w.C, dtype=torch.float16)
+    s16 = R.new_state(st.w.L, st.w.C, dtype=torch.float16)
+    for i, t in enumerate(toks):
+        lg, S = st.model.decode(t.reshape(1).to(cuda), S)
+        l32, s32 = R.decode(st.ref32, t.reshape(1), s32)
+        if i % 8 == 0 or i == steps - 1:
+            l16, s16 = R.decode(st.ref16, t.reshape(1), s16)
+            _check_logits(lg, l16, f"{shape} step {i} vs ref16")
+        else:
+            _, s16 = R.decode(st.ref16, t.reshape(1), s16)
+        _check_logits(lg, l32, f"{shape} step {i} vs ref32")
+    _check_state(S, s32, STATE_REL, f"{shape} state vs ref32")
+    _check_state(S, s16, 2e-2, f"{shape} state vs ref16")
+
+
+@pytest.mark.slow
+def test_decode_0p4b_256_steps_state(cuda):
+    """Config C3 parity: 0.4B, 256 decode steps from zero state; fp32 state within
+    1e-4 relative of the fp32-math oracle, logits within 1e-2/1e-3 throughout."""
+    print("decode parity 0.4b 256 steps", flush=True)
+    st = setup_for("0.4b", cuda)
+    toks = _tokens(256, 65536, seed=3)
+    S = State(st.w.L, st.w.C, 64, device=cuda)
+    s32 = R.new_state(st.w.L, st.w.C, dtype=torch.float16)
+    for i, t in enumerate(toks):
+        lg, S = st.model.decode(t.reshape(1).to(cuda), S)
+        l32, s32 = R.decode(st.ref32, t.reshape(1), s32)
+        if i % 16 == 0 or i == 255:
+            _check_logits(lg, l32, f"0.4b step {i}")
+    _check_state(S, s32, STATE_REL, "0.4b state after 256 steps")
+
+
+@pytest.mark.parametrize("shape,T", [("tiny", 1), ("tiny", 15), ("tiny", 40), ("0.1b", 33)])
+def test_prefill_then_decode_matches_oracle(shape, T, cuda):
+    print(f"prefill parity {shape} T={T}", flush=True)
+    st = setup_for(shape, cuda)
+    toks = _tokens(T + 1, st.w.head.shape[0], seed=T)
+    S = State(st.w.L, st.w.C, 64, device=cuda)
+    st.model.prefill(toks[:-1].to(cuda), S)
+    lg, S = st.model.decode(toks[-1:].to(cuda), S)
+    s32 = R.new_state(st.w.L, st.w.C, dtype=torch.float16)
+    l32, s32 = R.forward(st.ref32, toks, s32)
+    s16 = R.new_state(st.w.L, st.w.C, dtype=torch.float16)
+    l16, s16 = R.forward(st.ref16, toks, s16)
+    _check_logits(lg, l32, f"{shape} T={T} vs ref32")
+    _check_logits(lg, l16, f"{shape} T={T} vs ref16")
+    _check_state(S, s32, 5e-3, f"{shape} T={T} state vs ref32")
+
+
+def test_prefill_rejects_empty_and_bad_shapes(cuda):
+    st = setup_for("tiny", cuda)
+    S = State(st.w.L, st.w.C, 64, device=cuda)
+    with pytest.raises(RuntimeError):
+        st.model.prefill(torch.tensor([], dtype=torch.long, device=cuda), S)
+    with pytest.raises(ValueError):
+        st.model.prefill(torch.zeros(2, 3, dtype=torch.long, device=cuda), S)
+    with pytest.raises(ValueError):
+        st.model.decode(torch.tensor([1, 2], device=cuda), S)
+    with pytest.raises(ValueError):
+        st.model.decode(torch.tensor([10**6]), S)
+
+
+@pytest.mark.parametrize("B", [2, 5])
+def test_batched_decode_rows_match_single_sequences(B, cuda):
+    print(f"batched decode B={B}", flush=True)
+    st = setup_for("tiny", cuda)
+    V = st.w.head.shape[0]
+    g = torch.Generator().manual_seed(B)
+    prompt = torch.randint(0, V, (B, 6), generator=g)
+    nxt = torch.randint(0, V, (4, B), generator=g)
+    S = State(st.w.L, st.w.C, 64, device=cuda, batch=B)
+    st.model.prefill(prompt.to(cuda), S)
+    ref = R.new_state(st.w.L, st.w.C, dtype=torch.float16, batch=B)
+    R.prefill(st.ref32, prompt, ref)
+    for step in range(4):
+        lg, S = st.model.decode(nxt[step].to(cuda), S)
+        l32, ref = R.decode(st.ref32, nxt[step], ref)
+        assert lg.shape == (B, V)
+        for b in range(B):
+            _check_logits(lg[b], l32[b], f"B={B} step {step} row {b}")
+    for i in range(st.w.L):
+        for b in range(B):
+            r = _rel(S.tmix[i]["rnn"][b].cpu(), ref[0][i]["rnn"][b])
+            assert r < 5e-3, f"layer {i} row {b}: {r:.2e}"
+
+
+def test_graph_replay_matches_eager(cuda):
+    """HIP-graph decode and prefill replay == eager calls, bit for bit, over
+    several replays with eager work and syncs in between."""
+    st = setup_for("tiny", cuda)
+    V = st.w.head.shape[0]
+    g = torch.Generator().manual_seed(11)
+    prompt = torch.randint(0, V, (12,), generator=g)
+    steps = torch.randint(0, V, (6,), generator=g)
+    graphed = HIPGraph(st.model)
+    Sa = State(st.w.L, st.w.C, 64, device=cuda)
+    Sb = State(st.w.L, st.w.C, 64, device=cuda)
+    graphed.prefill(prompt.to(cuda), Sa)
+    st.model.prefill(prompt.to(cuda), Sb)
+    for i in range(len(steps)):
+        la, Sa = graphed.decode(steps[i].to(cuda), Sa)
+        torch.cuda.synchronize()
+        lb, Sb = st.model.decode(steps[i].to(cuda), Sb)
+        torch.cuda.synchronize()
+        assert torch.equal(la, lb), f"replay {i}"
+        for x, y in zip(Sa.arenas, Sb.arenas):
+            assert torch.equal(x, y), f"replay {i} state"
+    assert len(graphed._graphs) == 2  # one prefill (T=12) and one decode graph
+
+
+def test_make_rwkv7_and_forward_generate(cuda):
+    st = setup_for("tiny", cuda)
+    cls = make_rwkv7(torch.device("cuda"))
+    model = cls(st.w)
+    V = st.w.head.shape[0]
+    toks = _tokens(9, V, seed=4)
+    S = model.new_state()
+    lg, S = model.forward(toks.to(cuda), S)
+    s32 = R.new_state(st.w.L, st.w.C, dtype=torch.float16)
+    l32, _ = R.forward(st.ref32, toks, s32)
+    _check_logits(lg, l32, "forward")
+    out, S = model.generate(toks.tolist(), model.new_state(), max_tokens=5)
+    assert len(out) == 5 and all(0 <= t < V for t in out)
+    # greedy generate == argmax chain of the oracle
+    s32 = R.new_state(st.w.L, st.w.C, dtype=torch.float16)
+    lg32, s32 = R.forward(st.ref32, toks, s32)
+    ids = []
+    for _ in range(5):
+        nxt = int(lg32.argmax())
+        ids.append(nxt)
+        lg32, s32 = R.decode(st.ref32, torch.tensor([nxt]), s32)
+    assert out == ids
+
+
+def test_rebound_state_runs_through_a_copy(cuda):
+    st = setup_for("tiny", cuda)
+    S = State(st.w.L, st.w.C, 64, device=cuda)
+    S2 = State(st.w.L, st.w.C, 64, device=cuda)
+    S.tmix[0]["x"] = S.tmix[0]["x"].clone()  # rebind, as a careless caller might
+    assert not S.arena_intact()
+    t = torch.tensor([7], device=cuda)
+    la, S = st.model.decode(t, S)
+    lb, S2 = st.model.decode(t, S2)
+    assert torch.equal(la, lb)
+    assert torch.equal(S.tmix[0]["x"], S2.tmix[0]["x"])
+    assert torch.equal(S.tmix[1]["rnn"], S2.tmix[1]["rnn"])

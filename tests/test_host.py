@@ -1,0 +1,193 @@
+"""Host-side tests (CPU only): the C ABI library, layouts, State, weights,
+sampling and the model factory. No kernel is launched here."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from oracle import rwkv7_ref as R
+from rwkv_tl_amd import _lib, make_rwkv7, sample_logits
+from rwkv_tl_amd.checkpoint import SHAPES, make_random_state_dict
+from rwkv_tl_amd.state import State
+from rwkv_tl_amd.weight import RWKV7Weight, layer_layout, model_dims
+
+REPO = Path(__file__).resolve().parent.parent
+HEADER = REPO / "include" / "rwkv7_hip.h"
+
+
+def _header_functions() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(rwkv7_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_header_symbol():
+    lib = _lib.load()
+    declared = _header_functions()
+    assert declared == sorted(_lib.SYMBOLS)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.rwkv7_abi_version() == _lib.ABI_VERSION
+    assert lib.rwkv7_strerror(2) == b"unsupported shape"
+
+
+def _dims(shape="0.4b") -> _lib.Dims:
+    s = SHAPES[shape]
+    return _lib.Dims(s.n_layer, s.n_embd, s.n_head, s.n_ffn, s.vocab, s.rank_w, s.rank_a, s.rank_v, s.rank_g)
+
+
+@pytest.mark.parametrize("shape", ["tiny", "0.1b", "0.4b", "1.5b"])
+def test_layer_layout(shape):
+    d = _dims(shape)
+    lay = layer_layout(d)
+    C, F = d.n_embd, d.n_ffn
+    SR = d.rank_w + d.rank_a + d.rank_v + d.rank_g
+    offs = [lay.w_rkv, lay.w_lora1, lay.w_lora2, lay.w_o, lay.w_fk, lay.w_fv, lay.vec, lay.bytes]
+    assert offs == sorted(offs)
+    assert lay.w_lora1 == lay.w_rkv + 3 * C * C * 2  # one [3C+SR, C] decode matrix
+    assert lay.w_lora2 >= lay.w_lora1 + SR * C * 2
+    assert lay.w_o >= lay.w_lora2 + C * SR * 2
+    assert lay.w_fk >= lay.w_o + C * C * 2
+    assert lay.w_fv >= lay.w_fk + F * C * 2
+    assert lay.vec >= lay.w_fv + C * F * 2
+    assert lay.bytes >= lay.vec + _lib.NVEC * C * 4
+    assert all(o % 256 == 0 for o in offs if o != lay.w_lora1)
+
+
+def test_layout_rejects_unsupported_dims():
+    lib = _lib.load()
+    out = _lib.LayerLayout()
+    bad = [
+        dict(n_embd=768 + 64),   # not a multiple of 256
+        dict(n_head=10),          # n_head * 64 != n_embd
+        dict(rank_w=60),          # rank not a multiple of 8
+        dict(n_ffn=1000),
+    ]
+    for change in bad:
+        d = _dims("0.4b")
+        for k, v in change.items():
+            setattr(d, k, v)
+        if "n_embd" in change:
+            d.n_head = d.n_embd // 64
+        assert lib.rwkv7_layer_layout_get(ctypes.byref(d), ctypes.byref(out)) == 2, change
+    assert lib.rwkv7_layer_layout_get(None, ctypes.byref(out)) == 1
+
+
+def test_workspace_and_entry_point_argument_errors():
+    lib = _lib.load()
+    d = _dims("0.4b")
+    assert lib.rwkv7_workspace_bytes(ctypes.byref(d), 1, 1) > 0
+    assert lib.rwkv7_workspace_bytes(ctypes.byref(d), 4, 128) > lib.rwkv7_workspace_bytes(ctypes.byref(d), 1, 1)
+    assert lib.rwkv7_workspace_bytes(ctypes.byref(d), 0, 1) == -1
+    # null descriptors are rejected on the host before any launch
+    assert lib.rwkv7_decode(None, None, None, None, None, 0, None) == 1
+    model = _lib.Model(dims=d)
+    st = _lib.StateDesc(batch=1)
+    assert lib.rwkv7_decode(ctypes.byref(model), ctypes.byref(st), None, None, None, 0, None) == 1
+    assert lib.rwkv7_wkv7(None, None, None, 0, None, None, None, None, None, 1, 1, 1, None) == 1
+    assert lib.rwkv7_gemm_f16(1, 8, 1, 8, 1, 8, 1, 8, 8, 9, None) == 1  # bad epilogue code
+    assert lib.rwkv7_gemv_f16(1, 1, 100, 1, 4, 100, None) == 2       # K % 256
+    assert lib.rwkv7_lerp(1, 1, 1, 3, 1, None, 8, None) == 2          # n_mix not 1 or 6
+
+
+def test_state_layout_and_arena():
+    S = State(3, 256, 64, dtype=torch.float16)
+    assert len(S.tmix) == 3 and len(S.cmix) == 3
+    assert S.tmix[0]["x"].shape == (256,) and S.tmix[0]["x"].dtype == torch.float16
+    assert S.tmix[0]["rnn"].shape == (4, 64, 64) and S.tmix[0]["rnn"].dtype == torch.float32
+    assert S.cmix[2]["x"].shape == (256,)
+    assert S.arena_intact()
+    S.tmix[1]["x"].fill_(1.0)
+    assert S.arenas[0][1].float().sum() == 256
+    S.reset()
+    assert S.arenas[0].abs().sum() == 0
+    S.tmix[1]["x"] = torch.zeros(256, dtype=torch.float16)  # a rebind
+    assert not S.arena_intact()
+    Sb = State(2, 256, 64, batch=5)
+    assert Sb.tmix[0]["rnn"].shape == (5, 4, 64, 64) and Sb.cmix[1]["x"].shape == (5, 256)
+    with pytest.raises(ValueError):
+        State(2, 100, 64)
+
+
+def test_weight_matches_oracle_restatement():
+    sd = make_random_state_dict("tiny", seed=0, dtype=torch.float32)
+    w = RWKV7Weight.from_state_dict(sd, device="cpu", dtype=torch.float16)
+    o = R.Weights(sd, torch.float16)
+    assert (w.L, w.C) == (o.L, o.C)
+    assert torch.equal(w.emb, o.emb) and torch.equal(w.head, o.head)
+    for a, b in zip(w.blocks, o.blocks):
+        assert torch.equal(a.att.rkvWt, b.att.rkvWt)
+        assert torch.equal(a.att.oWt, b.att.oWt)
+        assert torch.equal(a.att.g1t, b.att.g1t)
+        assert torch.equal(a.ffn.kWt, b.ffn.kWt) and torch.equal(a.ffn.vWt, b.ffn.vWt)
+    d = model_dims(w)
+    assert (d.n_layer, d.n_embd, d.n_ffn, d.vocab) == (3, 256, 1024, 512)
+    assert (d.rank_w, d.rank_a, d.rank_v, d.rank_g) == (32, 32, 16, 64)
+
+
+def test_weight_loads_checkpoint_file(tmp_path):
+    sd = make_random_state_dict("tiny", seed=1, dtype=torch.float32)
+    p = tmp_path / "ck.pth"
+    torch.save(sd, p)
+    w = RWKV7Weight(str(p), device="cpu", dtype=torch.float16)
+    assert w.L == 3 and w.dtype == torch.float16 and w.head.dtype == torch.float16
+
+
+# Known answers of the reference's test/test_sampling.py:11-59.
+def test_sampling_greedy_argmax():
+    logits = torch.tensor([1.0, 2.0, 0.5, 3.0])
+    assert sample_logits(logits).item() == 3
+    assert sample_logits(logits, temperature=0.0).item() == 3
+    assert sample_logits(logits, temperature=-1.0).item() == 3
+
+
+def test_sampling_top_k_one_is_greedy():
+    torch.manual_seed(0)
+    logits = torch.randn(100)
+    for _ in range(20):
+        assert sample_logits(logits, temperature=1.0, top_k=1).item() == int(logits.argmax())
+
+
+def test_sampling_repetition_penalty_flips_near_tie():
+    logits = torch.tensor([0.5, 0.4])
+    assert sample_logits(logits, temperature=1.0, top_k=1).item() == 0
+    got = sample_logits(logits, temperature=1.0, top_k=1, repetition_penalty=2.0, seen=torch.tensor([0]))
+    assert got.item() == 1
+
+
+def test_sampling_range_and_shape():
+    torch.manual_seed(0)
+    logits = torch.randn(100)
+    for _ in range(20):
+        assert 0 <= sample_logits(logits, temperature=1.0, top_k=50, top_p=0.9).item() < 100
+    for temperature in (None, 0.0, 1.0):
+        t = sample_logits(torch.randn(65536), temperature=temperature)
+        assert t.numel() == 1 and 0 <= int(t) < 65536
+    batch = sample_logits(torch.randn(3, 10), temperature=1.0, top_p=0.5)
+    assert batch.shape == (3,)
+
+
+def test_sampling_top_p_keeps_smallest_nucleus():
+    # probabilities 0.5, 0.3, 0.2: top_p 0.6 keeps the first two only
+    logits = torch.log(torch.tensor([0.5, 0.3, 0.2]))
+    torch.manual_seed(0)
+    draws = {int(sample_logits(logits, temperature=1.0, top_p=0.6)) for _ in range(200)}
+    assert draws == {0, 1}
+
+
+def test_make_rwkv7_backends():
+    with pytest.raises(ValueError):
+        make_rwkv7(torch.device("cuda"), backend="bf16")
+    with pytest.raises(ValueError):
+        make_rwkv7(torch.device("cuda"), backend="torch")
+    with pytest.raises(ValueError):
+        make_rwkv7(torch.device("cuda"), backend="nope")
+    with pytest.raises(ValueError):
+        make_rwkv7(torch.device("cpu"))
+    cls = make_rwkv7(torch.device("cuda"), backend="fp16")
+    assert cls.__name__ == "HIPGraphRWKV7HIP"
+    assert make_rwkv7(torch.device("cuda"), use_graph=False).__name__ == "RWKV7HIP"
