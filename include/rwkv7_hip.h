@@ -102,7 +102,11 @@ const char *rwkv7_strerror(int code);
 int rwkv7_layer_layout_get(const rwkv7_dims *dims, rwkv7_layer_layout *out);
 
 /* Bytes of scratch that rwkv7_decode / rwkv7_prefill need for `batch`
- * sequences of `seq_len` tokens (seq_len 1 for decode). */
+ * sequences of `seq_len` tokens (seq_len 1 for decode). The workspace must be
+ * zero-filled once after allocation: its first region holds the hand-off words
+ * of the persistent decode kernel (32-bit word 8, bytes 32..35, counts waits
+ * that timed out) and is kept consistent by every later call. One workspace
+ * must not be used by two calls that can run concurrently. */
 int64_t rwkv7_workspace_bytes(const rwkv7_dims *dims, int32_t batch, int32_t seq_len);
 
 /* ---- model steps ------------------------------------------------------ */

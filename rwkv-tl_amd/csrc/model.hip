@@ -1,6 +1,7 @@
 // C ABI of librwkv7_hip.so: layouts, workspace sizing, the decode and prefill
 // step sequencers and the operator-level entry points. Host code only; the
 // kernels live in gemv.hip, tmix.hip and gemm.hip.
+#include <stdlib.h>
 #include <string.h>
 
 #include "rwkv7_kernels.h"
@@ -52,9 +53,16 @@ static void layout_of(const rwkv7_dims &d, rwkv7_layer_layout *o) {
 struct DecodeWs {
   float *x0, *xln, *proj, *vfirst, *yg, *xln2, *hid;
 };
+// The workspace starts with the persistent decode kernel's exchange region
+// (synchronisation words and tagged hand-off vectors); it must be zero when the
+// workspace is first used and is only ever touched by that kernel.
+static int64_t exchange_bytes(const rwkv7_dims &d) {
+  return align256(mk_exchange_bytes(d.n_embd, d.n_ffn, sum_ranks(d)));
+}
+
 static int64_t decode_ws(const rwkv7_dims &d, char *base, DecodeWs *w) {
   const int64_t C = d.n_embd, F = d.n_ffn, SR = sum_ranks(d);
-  int64_t off = 0;
+  int64_t off = exchange_bytes(d);
   auto take = [&](int64_t bytes) {
     char *p = base ? base + off : nullptr;
     off = align256(off + bytes);
@@ -79,7 +87,7 @@ struct BatchWs {
 };
 static int64_t batch_ws(const rwkv7_dims &d, int64_t B, int64_t T, char *base, BatchWs *w) {
   const int64_t C = d.n_embd, F = d.n_ffn, SR = sum_ranks(d), M = B * T;
-  int64_t off = 0;
+  int64_t off = exchange_bytes(d);
   auto take = [&](int64_t bytes) {
     char *p = base ? base + off : nullptr;
     off = align256(off + bytes);
@@ -334,7 +342,17 @@ int rwkv7_decode(const rwkv7_model *model, const rwkv7_state *state, const int64
   if (!tokens || !workspace) return RWKV7_EINVAL;
   if (workspace_bytes < rwkv7_workspace_bytes(&model->dims, state->batch, 1)) return RWKV7_EWORKSPACE;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (state->batch == 1) return decode_one(*model, *state, tokens, logits, static_cast<char *>(workspace), st);
+  if (state->batch == 1) {
+    const rwkv7_dims &d = model->dims;
+    const char *path = getenv("RWKV7_DECODE_PATH");
+    const bool kernels = path && strcmp(path, "kernels") == 0;
+    if (!kernels && logits && mk_supported(d, mk_cus())) {
+      rwkv7_layer_layout lay;
+      layout_of(d, &lay);
+      return launch_decode_mk(*model, lay, *state, tokens, logits, static_cast<char *>(workspace), st);
+    }
+    return decode_one(*model, *state, tokens, logits, static_cast<char *>(workspace), st);
+  }
   return run_batched(*model, *state, tokens, 1, logits, static_cast<char *>(workspace), st);
 }
 

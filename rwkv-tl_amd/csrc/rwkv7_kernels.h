@@ -94,4 +94,11 @@ struct GemmProb {
 };
 int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st);
 
+// One-token, one-sequence decode as a single persistent kernel (decode_mk.hip).
+int mk_cus();
+bool mk_supported(const rwkv7_dims &d, int G);
+int64_t mk_exchange_bytes(int C, int F, int SR);
+int launch_decode_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const rwkv7_state &s,
+                     const int64_t *tok, void *logits, char *xreg, hipStream_t st);
+
 }  // namespace rwkv7

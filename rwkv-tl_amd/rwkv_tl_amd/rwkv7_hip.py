@@ -63,7 +63,8 @@ class RWKV7HIP(RWKV7Model):
         if self._ws is None or self._ws_bytes < need:
             if self._ws is not None:
                 self._ws_retired.append(self._ws)
-            self._ws = torch.empty(need, dtype=torch.uint8, device=self.w.device)
+            # zeroed: the decode kernel's hand-off words at its start must not match any tag
+            self._ws = torch.zeros(need, dtype=torch.uint8, device=self.w.device)
             self._ws_bytes = need
         return self._ws
 

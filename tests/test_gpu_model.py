@@ -219,6 +219,34 @@ def test_make_rwkv7_and_forward_generate(cuda):
     assert out == ids
 
 
+@pytest.mark.parametrize("shape", ["tiny", "0.1b", "0.4b"])
+def test_persistent_decode_matches_kernel_path(shape, cuda, monkeypatch):
+    """The one-launch decode kernel and the multi-kernel GEMV path agree with
+    each other and with the fp32-math oracle; no hand-off wait timed out."""
+    print(f"persistent decode vs kernel path {shape}", flush=True)
+    st = setup_for(shape, cuda)
+    V = st.w.head.shape[0]
+    toks = _tokens(12, V, seed=21)
+    Sa = State(st.w.L, st.w.C, 64, device=cuda)
+    Sb = State(st.w.L, st.w.C, 64, device=cuda)
+    s32 = R.new_state(st.w.L, st.w.C, dtype=torch.float16)
+    for i, t in enumerate(toks):
+        la, Sa = st.model.decode(t.reshape(1).to(cuda), Sa)
+        monkeypatch.setenv("RWKV7_DECODE_PATH", "kernels")
+        lb, Sb = st.model.decode(t.reshape(1).to(cuda), Sb)
+        monkeypatch.delenv("RWKV7_DECODE_PATH")
+        l32, s32 = R.decode(st.ref32, t.reshape(1), s32)
+        _check_logits(la, l32, f"{shape} persistent step {i}")
+        _check_logits(lb, l32, f"{shape} kernels step {i}")
+        torch.testing.assert_close(la.float(), lb.float(), rtol=2e-3, atol=2e-3)
+    _check_state(Sa, s32, STATE_REL, f"{shape} persistent state")
+    for x, y in zip(Sa.arenas[1:2], Sb.arenas[1:2]):
+        assert _rel(x.cpu(), y.cpu()) < 1e-5
+    torch.cuda.synchronize()
+    errors = int(st.model.workspace(1, 1)[32:36].view(torch.int32).item())
+    assert errors == 0, f"{errors} hand-off waits timed out"
+
+
 def test_rebound_state_runs_through_a_copy(cuda):
     st = setup_for("tiny", cuda)
     S = State(st.w.L, st.w.C, 64, device=cuda)
