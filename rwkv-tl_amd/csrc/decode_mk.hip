@@ -35,7 +35,7 @@ namespace rwkv7 {
 
 constexpr int kT = 512;        // threads per workgroup
 constexpr int kW = kT / 64;    // waves per workgroup
-constexpr int kRMax = 4;       // max rows per wave in P1 / P4
+constexpr int kRMax = 4;       // max rows per wave in P1 / P4 (the RM template bound)
 constexpr int kSpinLimit = 1 << 21;
 
 // sync words (the first 256 bytes of the exchange region)
@@ -170,14 +170,14 @@ struct MkArgs {
 };
 
 // Loads this wave's rows of W (row stride ld halfs) for a wave-per-row stage:
-// wave w owns rows r0 + w + kW * i (i < kRMax) below r1; lane l holds the
+// wave w owns rows r0 + w + kW * i (i < RM) below r1; lane l holds the
 // 16-byte chunks l + 64 * c of each row.
-template <int CPL>
-RWKV7_DEV void load_rows(const uint16_t *W, int64_t ld, int r0, int r1, int K, uint4 (&wreg)[kRMax][CPL]) {
+template <int RM, int CPL>
+RWKV7_DEV void load_rows(const uint16_t *W, int64_t ld, int r0, int r1, int K, uint4 (&wreg)[RM][CPL]) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int nch = K >> 3;
 #pragma unroll
-  for (int i = 0; i < kRMax; ++i) {
+  for (int i = 0; i < RM; ++i) {
     const int r = r0 + wv + kW * i;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
@@ -232,9 +232,81 @@ RWKV7_DEV float dot_split(const uint4 (&wreg)[NC], const float *x, int nrow, int
   return out;
 }
 
-// CPL: 16-byte chunks per lane of a C-long row; NC5: chunks per lane of the
-// K-split rows of P3/P5; NPTH: hidden-vector words polled per thread.
-template <int CPL, int NC5, int NPTH>
+// Loads vec[c] for this thread's elements c = threadIdx.x + kT * i (i < CPL).
+template <int CPL>
+RWKV7_DEV void ld_own(float (&dst)[CPL], const float *src, int C) {
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = threadIdx.x + kT * i;
+    dst[i] = c < C ? src[c] : 0.f;
+  }
+}
+template <int CPL>
+RWKV7_DEV void ld_own16(float (&dst)[CPL], const uint16_t *src, int C) {
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = threadIdx.x + kT * i;
+    dst[i] = c < C ? h2f(src[c]) : 0.f;
+  }
+}
+
+// Polls this thread's own elements c = threadIdx.x + kT * i of a tagged vector
+// into registers (no barrier).
+template <int CPL>
+RWKV7_DEV void poll_own(const MkCtx &cx, const uint64_t *src, int n, unsigned tag, float (&dst)[CPL]) {
+  unsigned pending = 0;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i)
+    if ((int)threadIdx.x + kT * i < n) pending |= 1u << i;
+    else dst[i] = 0.f;
+  int spins = 0;
+  while (pending) {
+    uint64_t w[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i)
+      if (pending & (1u << i)) w[i] = ld_u64(src + threadIdx.x + kT * i);
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      if ((pending & (1u << i)) && (unsigned)(w[i] >> 32) == tag) {
+        dst[i] = __builtin_bit_cast(float, (unsigned)w[i]);
+        pending &= ~(1u << i);
+      }
+    }
+    if (pending) {
+      ++spins;
+      if ((spins & 63) == 0 && cx.aborted()) break;
+      if (spins > kSpinLimit) {
+        cx.abort();
+        break;
+      }
+    }
+  }
+}
+
+// LayerNorm of a vector held as this thread's own elements (block reductions).
+template <int CPL>
+RWKV7_DEV void ln_own(float (&x)[CPL], const float (&w)[CPL], const float (&b)[CPL], int C, float *red) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) s += x[i];
+  const float mean = block_sum(s, red) / (float)C;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i)
+    if ((int)threadIdx.x + kT * i < C) {
+      const float d = x[i] - mean;
+      q += d * d;
+    }
+  const float rstd = rsqrtf(block_sum(q, red) / (float)C + kLnEps);
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) x[i] = (x[i] - mean) * rstd * w[i] + b[i];
+}
+
+// RM: rows per wave in P1/P4; CPL: 16-byte chunks per lane of a C-long row
+// (also this thread's share of a C-long vector); NC5: chunks per lane of the
+// K-split rows of P3/P5; NPTH: hidden-vector words polled per thread; NL2:
+// LoRA second-step chunks per thread.
+template <int RM, int CPL, int NC5, int NPTH, int NL2>
 __global__ __launch_bounds__(kT) void decode_mk_kernel(MkArgs a) {
   extern __shared__ __align__(16) float smem[];
   const int C = a.C, F = a.F, H = a.H, L = a.L;
@@ -242,19 +314,19 @@ __global__ __launch_bounds__(kT) void decode_mk_kernel(MkArgs a) {
   const int G = gridDim.x, g = blockIdx.x;
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
 
-  float *s_x = smem;             // [C]  input vector of P1/P4/head
+  float *s_x = smem;             // [C]  mixed input of P4 / normalised input of the head
   float *s_ln1 = s_x + C;        // [C]  LN1 output (kept to P3 for the shift state)
   float *s_ln2 = s_ln1 + C;      // [C]  LN2 output (kept to P5)
-  float *s_prev = s_ln2 + C;     // [C]  token-shift state of the current mix, f32
+  float *s_spare = s_ln2 + C;    // [C]
   const int nin = mk_nin(C, F, SR);
-  float *s_in = s_prev + C;      // [nin] polled stage inputs / P1 segment mixes
+  float *s_in = s_spare + C;     // [nin] polled stage inputs / P1 segment mixes
   float *s_red = s_in + nin;     // [64]
   float *s_own = s_red + 64;     // [16] this workgroup's rows of the residual
   float *s_vf = s_own + 16;      // [64] v_first of the head this workgroup owns
   float *s_core = s_vf + 64;     // [8][64] r w k v a b g y
   float *s_lora = s_core + 8 * 64;  // [512]
   float *s_d = s_lora + 512;        // [4][64] LoRA second-step results
-  uint16_t *s_l2 = reinterpret_cast<uint16_t *>(s_d + 256);  // [SR][64] LoRA second step (transposed)
+  (void)s_spare;
 
   MkCtx cx;
   cx.sync = a.sync;
@@ -284,6 +356,39 @@ __global__ __launch_bounds__(kT) void decode_mk_kernel(MkArgs a) {
   };
   const int seg0 = seg_of(p1a), nseg = seg_of(p1b - 1) - seg0 + 1;
 
+  // P2 thread roles: 8 threads per channel c2 of the head; thread sub2 takes the
+  // 16-byte chunks sub2, sub2+8, ... of the channel's [v|w|a|g] LoRA row
+  const int c2 = t >> 3, sub2 = t & 7;
+  const int nch2 = SR >> 3;
+  const int b1 = a.rv >> 3, b2 = (a.rv + a.rw) >> 3, b3 = (a.rv + a.rw + a.ra) >> 3;  // gate bounds in chunks
+
+  // ---- prefetched operands (each issued one stage ahead of its use) -----------
+  uint4 w1[RM][CPL];               // P1 rows
+  float ln1w[CPL], ln1b[CPL], prv1[CPL], mu1[4][CPL];
+  uint4 w2[NL2];                   // P2 LoRA second-step chunks
+  float4 S0 = make_float4(0.f, 0.f, 0.f, 0.f), S1 = S0;  // P2 state rows
+  float gv[8];                     // P2 per-channel vectors
+  uint4 w3[NC5];                   // P3 rows
+  uint4 w4[RM][CPL];               // P4 rows
+  float ln2w[CPL], ln2b[CPL], prv2[CPL], mu4[CPL];
+  uint4 w5[NC5];                   // P5 rows
+
+  auto prefetch_p1 = [&](int l) {
+    const char *Lp = a.layers + (int64_t)l * a.lbytes;
+    const float *vec = reinterpret_cast<const float *>(Lp + a.o_vec);
+    load_rows<RM, CPL>(reinterpret_cast<const uint16_t *>(Lp + a.o_rkv), C, p1a, p1b, C, w1);
+    ld_own<CPL>(ln1w, vec + RWKV7_V_LN1_W * C, C);
+    ld_own<CPL>(ln1b, vec + RWKV7_V_LN1_B * C, C);
+    ld_own16<CPL>(prv1, a.tmix_x + (int64_t)l * C, C);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (q < nseg) ld_own<CPL>(mu1[q], vec + (int64_t)seg_mu(seg0 + q) * C, C);
+  };
+
+  prefetch_p1(0);
+  float xo[CPL];
+  ld_own16<CPL>(xo, erow, C);
+
   for (int l = 0; l < L; ++l) {
     const char *Lp = a.layers + (int64_t)l * a.lbytes;
     const float *vec = reinterpret_cast<const float *>(Lp + a.o_vec);
@@ -291,28 +396,40 @@ __global__ __launch_bounds__(kT) void decode_mk_kernel(MkArgs a) {
 
     // ---------------- P1: LN1 + shift + [r;k;v;LoRA1] ------------------------
     {
-      uint4 wreg[kRMax][CPL];
-      load_rows<CPL>(reinterpret_cast<const uint16_t *>(Lp + a.o_rkv), C, p1a, p1b, C, wreg);
-      const uint16_t *tx = a.tmix_x + (int64_t)l * C;
-      for (int c = t; c < C; c += kT) s_prev[c] = h2f(tx[c]);
-      if (l == 0) {
-        for (int c = t; c < C; c += kT) s_x[c] = h2f(erow[c]);
-        __syncthreads();
-      } else {
-        poll_vec<4>(cx, a.x_ex, C, cx.tag(ph - 1), s_x, Ident());
+      if (l > 0) poll_own<CPL>(cx, a.x_ex, C, cx.tag(ph - 1), xo);
+      // stage-ahead prefetch: P2 (head workgroups) and P3
+      if (g < H) {
+        const uint4 *row = reinterpret_cast<const uint4 *>(
+            reinterpret_cast<const uint16_t *>(Lp + a.o_l2) + (int64_t)(g * kN + c2) * SR);
+#pragma unroll
+        for (int i = 0; i < NL2; ++i) w2[i] = sub2 + 8 * i < nch2 ? row[sub2 + 8 * i] : make_uint4(0, 0, 0, 0);
+        const float4 *Sp = reinterpret_cast<const float4 *>(
+            a.rnn + (((int64_t)l * H + g) * kN + (t >> 3)) * kN + (t & 7) * 8);
+        S0 = Sp[0];
+        S1 = Sp[1];
+        if (t < 64) {
+          const int ch = g * kN + t;
+          const int idx[8] = {RWKV7_V_V0, RWKV7_V_W0, RWKV7_V_A0, RWKV7_V_K_K,
+                              RWKV7_V_K_A, RWKV7_V_R_K, RWKV7_V_LNX_W, RWKV7_V_LNX_B};
+#pragma unroll
+          for (int j = 0; j < 8; ++j) gv[j] = vec[idx[j] * C + ch];
+        }
       }
-      ln_lds(s_x, s_ln1, vec + RWKV7_V_LN1_W * C, vec + RWKV7_V_LN1_B * C, C, s_red);
-      // mixed inputs x + mu_s (prev - x) of the (at most kMaxSeg) row segments this
-      // workgroup's rows fall in, built once in LDS (s_in is free until P2)
-      for (int q = 0; q < nseg; ++q) {
-        const float *mu = vec + (int64_t)seg_mu(seg0 + q) * C;
-        float *dst = s_in + q * C;
-        for (int c = t; c < C; c += kT) dst[c] = s_ln1[c] + mu[c] * (s_prev[c] - s_ln1[c]);
+      ln_own<CPL>(xo, ln1w, ln1b, C, s_red);
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int c = t + kT * i;
+        if (c < C) {
+          s_ln1[c] = xo[i];
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (q < nseg) s_in[q * C + c] = xo[i] + mu1[q][i] * (prv1[i] - xo[i]);
+        }
       }
       __syncthreads();
       const unsigned tg = cx.tag(ph);
 #pragma unroll
-      for (int i = 0; i < kRMax; ++i) {
+      for (int i = 0; i < RM; ++i) {
         const int r = p1a + wv + kW * i;
         if (r >= p1b) break;
         const float *xs = s_in + (seg_of(r) - seg0) * C;
@@ -320,11 +437,13 @@ __global__ __launch_bounds__(kT) void decode_mk_kernel(MkArgs a) {
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
           const int j = lane + 64 * c;
-          if (j < (C >> 3)) acc = dot8(wreg[i][c], xs + 8 * j, acc);
+          if (j < (C >> 3)) acc = dot8(w1[i][c], xs + 8 * j, acc);
         }
         acc = wave_sum(acc);
         if (lane == 0) publish(a.proj_ex + r, tg, acc);
       }
+      // stage-ahead prefetch: P3 (small; issued here to keep it out of P1's registers)
+      load_split<NC5>(reinterpret_cast<const uint16_t *>(Lp + a.o_o), C, owa, nown, ks, C, w3);
       // P2 / P3 poll into s_in, which still holds the segment mixes other waves read
       __syncthreads();
     }
@@ -332,24 +451,6 @@ __global__ __launch_bounds__(kT) void decode_mk_kernel(MkArgs a) {
     // ---------------- P2: per-head core (workgroups 0..H-1) -------------------
     if (g < H) {
       const int h = g;
-      // prefetch: LoRA second-step rows of this head (transposed into LDS) and the state
-      const uint4 *l2g = reinterpret_cast<const uint4 *>(
-          reinterpret_cast<const uint16_t *>(Lp + a.o_l2) + (int64_t)h * kN * SR);
-      const int nl2 = kN * SR / 8;
-      for (int i = t; i < nl2; i += kT) {
-        const uint4 u = l2g[i];
-        const int c = (i * 8) / SR, r0 = (i * 8) % SR;
-        // halves split with integer shifts (a vector bit-cast to 16-bit lanes was
-        // mis-lowered here to one 4-byte load stored eight times)
-        const unsigned pk[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) s_l2[(r0 + e) * kN + c] = (uint16_t)(pk[e >> 1] >> (16 * (e & 1)));
-      }
-      const int row = t >> 3, j0 = (t & 7) * 8;
-      float4 *Sp = reinterpret_cast<float4 *>(a.rnn + (((int64_t)l * H + h) * kN + row) * kN + j0);
-      float4 S0 = Sp[0], S1 = Sp[1];
-
-      // inputs: r, k, v of this head (192) and the LoRA first step (SR)
       poll_vec<2>(cx, a.proj_ex, 192 + SR, cx.tag(ph), s_in, [&](int i) {
         return i < 192 ? (i >> 6) * C + h * kN + (i & 63) : 3 * C + (i - 192);
       });
@@ -362,37 +463,51 @@ __global__ __launch_bounds__(kT) void decode_mk_kernel(MkArgs a) {
       __syncthreads();
       float *s_r = s_core, *s_w = s_core + 64, *s_k = s_core + 128, *s_v = s_core + 192;
       float *s_a = s_core + 256, *s_b = s_core + 320, *s_g = s_core + 384, *s_y = s_core + 448;
-      if (t < 256) {
-        const int c = t & 63, q = t >> 6;
-        const int off = q == 0 ? 0 : q == 1 ? a.rv : q == 2 ? a.rv + a.rw : a.rv + a.rw + a.ra;
-        const int R = q == 0 ? a.rv : q == 1 ? a.rw : q == 2 ? a.ra : a.rg;
-        float acc = 0.f;
-        for (int r = 0; r < R; ++r) acc = fmaf(h2f(s_l2[(off + r) * kN + c]), s_lora[off + r], acc);
-        s_d[q * 64 + c] = acc;
+      {  // LoRA second step from the prefetched chunks; per-gate partial sums joined
+         // across the channel's 8 lanes
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < NL2; ++i) {
+          const int cj = sub2 + 8 * i;
+          if (cj < nch2) {
+            const float p = dot8(w2[i], s_lora + 8 * cj, 0.f);
+            const int q = (cj >= b1) + (cj >= b2) + (cj >= b3);
+            acc[0] += q == 0 ? p : 0.f;
+            acc[1] += q == 1 ? p : 0.f;
+            acc[2] += q == 2 ? p : 0.f;
+            acc[3] += q == 3 ? p : 0.f;
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float v = sum4(acc[q]);
+          v += dpp<kDppHalfMirror>(v);
+          if (sub2 == 0) s_d[q * 64 + c2] = v;
+        }
       }
       __syncthreads();
       if (t < 64) {
-        const int ch = h * kN + t;
         const float r = s_in[t], k = s_in[64 + t];
         float v = s_in[128 + t];
         if (l == 0) {
           s_vf[t] = v;
         } else {
-          v = v + sigmoidf_(vec[RWKV7_V_V0 * C + ch] + s_d[t]) * (s_vf[t] - v);
+          v = v + sigmoidf_(gv[0] + s_d[t]) * (s_vf[t] - v);
         }
-        const float w = expf(-sigmoidf_(vec[RWKV7_V_W0 * C + ch] + s_d[64 + t]) / 1.6487212707001282f);
-        const float ag = sigmoidf_(vec[RWKV7_V_A0 * C + ch] + s_d[128 + t]);
-        const float kk = k * vec[RWKV7_V_K_K * C + ch];
-        const float kn = k + vec[RWKV7_V_K_A * C + ch] * (k * ag - k);
+        const float w = expf(-sigmoidf_(gv[1] + s_d[64 + t]) / 1.6487212707001282f);
+        const float ag = sigmoidf_(gv[2] + s_d[128 + t]);
+        const float kk = k * gv[3];
+        const float kn = k + gv[4] * (k * ag - k);
         const float nrm = sqrtf(wave_sum(kk * kk));
         const float kh = kk / fmaxf(nrm, 1e-12f);
-        const float rk = wave_sum(r * kn * vec[RWKV7_V_R_K * C + ch]);
+        const float rk = wave_sum(r * kn * gv[5]);
         s_r[t] = r; s_w[t] = w; s_k[t] = kn; s_v[t] = v;
         s_a[t] = kh; s_b[t] = -kh * ag; s_g[t] = s_d[192 + t];
         if (t == 0) s_red[32] = rk;
       }
       __syncthreads();
       {
+        const int row = t >> 3, j0 = (t & 7) * 8;
         float Sv[8] = {S0.x, S0.y, S0.z, S0.w, S1.x, S1.y, S1.z, S1.w};
         float sa = 0.f;
 #pragma unroll
@@ -409,6 +524,7 @@ __global__ __launch_bounds__(kT) void decode_mk_kernel(MkArgs a) {
         }
         y = sum4(y);
         y += dpp<kDppHalfMirror>(y);
+        float4 *Sp = reinterpret_cast<float4 *>(a.rnn + (((int64_t)l * H + h) * kN + row) * kN + j0);
         Sp[0] = make_float4(Sv[0], Sv[1], Sv[2], Sv[3]);
         Sp[1] = make_float4(Sv[4], Sv[5], Sv[6], Sv[7]);
         if ((t & 7) == 0) s_y[row] = y;
@@ -420,17 +536,21 @@ __global__ __launch_bounds__(kT) void decode_mk_kernel(MkArgs a) {
         const float mean = wave_sum(y) * (1.f / kN);
         const float d = y - mean;
         const float var = wave_sum(d * d) * (1.f / kN);
-        const float yn = d * rsqrtf(var + kGnEps) * vec[RWKV7_V_LNX_W * C + ch] + vec[RWKV7_V_LNX_B * C + ch];
+        const float yn = d * rsqrtf(var + kGnEps) * gv[6] + gv[7];
         publish(a.core_ex + ch, cx.tag(ph + 1), (yn + s_red[32] * s_v[t]) * s_g[t]);
       }
     }
 
     // ---------------- P3: o-projection + residual -----------------------------
     {
-      uint4 wreg[NC5];
-      load_split<NC5>(reinterpret_cast<const uint16_t *>(Lp + a.o_o), C, owa, nown, ks, C, wreg);
       poll_vec<4>(cx, a.core_ex, C, cx.tag(ph + 1), s_in, Ident());
-      const float d = dot_split<NC5>(wreg, s_in, nown, ks, C, s_red);
+      // stage-ahead prefetch: P4
+      load_rows<RM, CPL>(reinterpret_cast<const uint16_t *>(Lp + a.o_fk), C, p4a, p4b, C, w4);
+      ld_own<CPL>(ln2w, vec + RWKV7_V_LN2_W * C, C);
+      ld_own<CPL>(ln2b, vec + RWKV7_V_LN2_B * C, C);
+      ld_own<CPL>(mu4, vec + RWKV7_V_FFN_X_K * C, C);
+      ld_own16<CPL>(prv2, a.cmix_x + (int64_t)l * C, C);
+      const float d = dot_split<NC5>(w3, s_in, nown, ks, C, s_red);
       const unsigned tg = cx.tag(ph + 2);
       if (t < nown) {
         s_own[t] += d;
@@ -442,27 +562,29 @@ __global__ __launch_bounds__(kT) void decode_mk_kernel(MkArgs a) {
 
     // ---------------- P4: LN2 + shift + FFN key + relu^2 ----------------------
     {
-      uint4 wreg[kRMax][CPL];
-      load_rows<CPL>(reinterpret_cast<const uint16_t *>(Lp + a.o_fk), C, p4a, p4b, C, wreg);
-      const uint16_t *cxs = a.cmix_x + (int64_t)l * C;
-      for (int c = t; c < C; c += kT) s_prev[c] = h2f(cxs[c]);
-      poll_vec<4>(cx, a.x_ex, C, cx.tag(ph + 2), s_x, Ident());
-      ln_lds(s_x, s_ln2, vec + RWKV7_V_LN2_W * C, vec + RWKV7_V_LN2_B * C, C, s_red);
-      const float *mu = vec + RWKV7_V_FFN_X_K * C;
-      for (int c = t; c < C; c += kT) s_x[c] = s_ln2[c] + mu[c] * (s_prev[c] - s_ln2[c]);
+      poll_own<CPL>(cx, a.x_ex, C, cx.tag(ph + 2), xo);
+      // stage-ahead prefetch: P5
+      load_split<NC5>(reinterpret_cast<const uint16_t *>(Lp + a.o_fv), F, owa, nown, ks, F, w5);
+      ln_own<CPL>(xo, ln2w, ln2b, C, s_red);
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int c = t + kT * i;
+        if (c < C) {
+          s_ln2[c] = xo[i];
+          s_x[c] = xo[i] + mu4[i] * (prv2[i] - xo[i]);
+        }
+      }
       __syncthreads();
       const unsigned tg = cx.tag(ph + 3);
 #pragma unroll
-      for (int i = 0; i < kRMax; ++i) {
+      for (int i = 0; i < RM; ++i) {
         const int r = p4a + wv + kW * i;
         if (r >= p4b) break;
         float acc = 0.f;
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
           const int j = lane + 64 * c;
-          if (j < (C >> 3)) {
-            acc = dot8(wreg[i][c], s_x + 8 * j, acc);
-          }
+          if (j < (C >> 3)) acc = dot8(w4[i][c], s_x + 8 * j, acc);
         }
         acc = wave_sum(acc);
         const float q = fmaxf(acc, 0.f);
@@ -472,10 +594,9 @@ __global__ __launch_bounds__(kT) void decode_mk_kernel(MkArgs a) {
 
     // ---------------- P5: FFN value + residual --------------------------------
     {
-      uint4 wreg[NC5];
-      load_split<NC5>(reinterpret_cast<const uint16_t *>(Lp + a.o_fv), F, owa, nown, ks, F, wreg);
       poll_vec<NPTH>(cx, a.hid_ex, F, cx.tag(ph + 3), s_in, Ident());
-      const float d = dot_split<NC5>(wreg, s_in, nown, ks, F, s_red);
+      if (l + 1 < L) prefetch_p1(l + 1);  // stage-ahead prefetch: next layer's P1
+      const float d = dot_split<NC5>(w5, s_in, nown, ks, F, s_red);
       const unsigned tg = cx.tag(ph + 4);
       if (t < nown) {
         s_own[t] += d;
@@ -487,33 +608,44 @@ __global__ __launch_bounds__(kT) void decode_mk_kernel(MkArgs a) {
 
   // ---------------- head: ln_out + logits ---------------------------------------
   {
-    poll_vec<4>(cx, a.x_ex, C, cx.tag(5 * L - 1), s_x, Ident());
-    ln_lds(s_x, s_x, a.ln_out, a.ln_out + C, C, s_red);
     const int ha = (int)((int64_t)a.V * g / G), hb = (int)((int64_t)a.V * (g + 1) / G);
-    for (int r0 = ha + wv * 4; r0 < hb; r0 += kW * 4) {
-      uint4 wreg[4][CPL];
+    float low[CPL], lob[CPL];
+    ld_own<CPL>(low, a.ln_out, C);
+    ld_own<CPL>(lob, a.ln_out + C, C);
+    uint4 wh[4][CPL];
+    auto load_head = [&](int r0) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
           const int j = lane + 64 * c;
-          wreg[i][c] = (r0 + i < hb && j < (C >> 3))
-                           ? ld_stream(reinterpret_cast<const uint4 *>(a.head + (int64_t)(r0 + i) * C) + j)
-                           : make_uint4(0, 0, 0, 0);
+          wh[i][c] = (r0 + i < hb && j < (C >> 3))
+                         ? ld_stream(reinterpret_cast<const uint4 *>(a.head + (int64_t)(r0 + i) * C) + j)
+                         : make_uint4(0, 0, 0, 0);
         }
+    };
+    load_head(ha + wv * 4);
+    poll_own<CPL>(cx, a.x_ex, C, cx.tag(5 * L - 1), xo);
+    ln_own<CPL>(xo, low, lob, C, s_red);
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = t + kT * i;
+      if (c < C) s_x[c] = xo[i];
+    }
+    __syncthreads();
+    for (int r0 = ha + wv * 4; r0 < hb; r0 += kW * 4) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float acc = 0.f;
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
           const int j = lane + 64 * c;
-          if (j < (C >> 3)) {
-            acc = dot8(wreg[i][c], s_x + 8 * j, acc);
-          }
+          if (j < (C >> 3)) acc = dot8(wh[i][c], s_x + 8 * j, acc);
         }
         acc = wave_sum(acc);
         if (lane == i && r0 + i < hb) a.logits[r0 + i] = f2h(acc);
       }
+      if (r0 + kW * 4 < hb) load_head(r0 + kW * 4);
     }
   }
   // all workgroups have read the epoch and passed their last wait on it
@@ -532,12 +664,17 @@ static int mk_nc5(const rwkv7_dims &d, int G) {
   return (per + 63) / 64;
 }
 
-// Template instance for these sizes: 0 = <2,4,8>, 1 = <4,8,16>, 2 = <4,16,16>; -1 if none fits.
+// Template instance for these sizes: 0 = <2,2,4,8,5>; -1 if none fits.
 static int mk_variant(const rwkv7_dims &d, int G) {
   const int cpl = ((d.n_embd >> 3) + 63) / 64, nc5 = mk_nc5(d, G), npth = (d.n_ffn + kT - 1) / kT;
-  if (cpl <= 2 && nc5 <= 4 && npth <= 8) return 0;
-  if (cpl <= 4 && nc5 <= 8 && npth <= 16) return 1;
-  if (cpl <= 4 && nc5 <= 16 && npth <= 16) return 2;
+  const int nl2 = ((d.rank_w + d.rank_a + d.rank_v + d.rank_g) / 8 + 7) / 8;  // P2 chunks per thread
+  const int n1 = 3 * d.n_embd + d.rank_w + d.rank_a + d.rank_v + d.rank_g;
+  const int rm = ((n1 + G - 1) / G + kW - 1) / kW > ((d.n_ffn + G - 1) / G + kW - 1) / kW
+                     ? ((n1 + G - 1) / G + kW - 1) / kW
+                     : ((d.n_ffn + G - 1) / G + kW - 1) / kW;
+  if (rm <= 2 && cpl <= 2 && nc5 <= 4 && npth <= 8 && nl2 <= 5) return 0;
+  // The wider instances (n_embd 2048) exceed the register file and spill to
+  // scratch; those models decode one sequence through the GEMV kernels instead.
   return -1;
 }
 
@@ -556,7 +693,7 @@ int mk_cus() {
 
 int64_t mk_lds_bytes(int C, int F, int SR) {
   const int nin = mk_nin(C, F, SR);
-  return (int64_t)(4 * C + nin + 64 + 16 + 64 + 8 * 64 + 512 + 256) * 4 + (int64_t)SR * kN * 2;
+  return (int64_t)(4 * C + nin + 64 + 16 + 64 + 8 * 64 + 512 + 256) * 4;
 }
 
 // Exchange region: sync words, then x (C), proj (3C+SR), core (C), hid (F) as u64.
@@ -575,6 +712,7 @@ bool mk_supported(const rwkv7_dims &d, int G) {
   if ((C + G - 1) / G > 16) return false;
   if (mk_variant(d, G) < 0) return false;
   if (F > 8192 || 192 + SR > 8192) return false;
+
   // P1 keeps the mixed input of every row segment a workgroup touches (<= 4)
   const int e[6] = {C, 2 * C, 3 * C, 3 * C + d.rank_v, 3 * C + d.rank_v + d.rank_w,
                     3 * C + d.rank_v + d.rank_w + d.rank_a};
@@ -630,19 +768,15 @@ int launch_decode_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const 
   a.hid_ex = a.core_ex + C;
   const int64_t lds = mk_lds_bytes(C, F, SR);
   const int variant = mk_variant(d, G);
-  const void *fn = variant == 0   ? (const void *)decode_mk_kernel<2, 4, 8>
-                   : variant == 1 ? (const void *)decode_mk_kernel<4, 8, 16>
-                                  : (const void *)decode_mk_kernel<4, 16, 16>;
+  const void *fn = (const void *)decode_mk_kernel<2, 2, 4, 8, 5>;
   if (variant < 0) return RWKV7_ESHAPE;
-  static int64_t lds_set[3] = {0, 0, 0};  // largest dynamic LDS size already allowed per variant
-  if (lds > lds_set[variant]) {
+  static int64_t lds_set = 0;  // largest dynamic LDS size already allowed
+  if (lds > lds_set) {
     if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
       return RWKV7_ELAUNCH;
-    lds_set[variant] = lds;
+    lds_set = lds;
   }
-  if (variant == 0) decode_mk_kernel<2, 4, 8><<<G, kT, lds, st>>>(a);
-  else if (variant == 1) decode_mk_kernel<4, 8, 16><<<G, kT, lds, st>>>(a);
-  else decode_mk_kernel<4, 16, 16><<<G, kT, lds, st>>>(a);
+  decode_mk_kernel<2, 2, 4, 8, 5><<<G, kT, lds, st>>>(a);
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;
 }
