@@ -8,11 +8,29 @@
   generator and resident on the device before timing starts. ``value`` is
   ms/token over exactly K timed steps (HIP events on the replay stream,
   bracketed by device synchronisation).
-* Extra lines of the same JSON object: decode at batch 16 (ms/step and
-  tokens/s), prefill T=128 and T=8 (ms), the roofline of the dominant kernel
-  and of the whole step, and the CPU baseline: the oracle's pure-torch fp32
+* ``roofline`` is that of the dominant kernel, the persistent decode kernel
+  (``decode_mk_kernel``, the whole batch-1 step in one launch): algorithmic
+  bytes per launch (fp16 weights and head read once, fp32 wkv state and f16
+  shift states read and written, token embedding row and logits) divided by
+  its average launch duration, measured with HIP events recorded around each
+  launch on the stream it is launched on. ``traffic`` is the HBM bytes per
+  launch that ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` counted, each
+  scaled by what the same counter reads for a copy kernel of known size; it is
+  read from the committed summary ``profiles/decode_mk_kernel_traffic.txt``
+  (null if absent), which ``--pmc-summary`` writes from the two counter runs.
+* Extra keys of the same JSON object: decode at batch 16 (ms/step and
+  tokens/s), prefill T=128 and T=8 (ms), the roofline of the whole step as
+  the caller sees it, and the CPU baseline: the oracle's pure-torch fp32
   model (a port of the reference's ``demo/rwkv7_torch.py``) timed on this
   host's cores on a bounded sample of the same decode workload.
+
+Profiling recipe (the counter runs behind ``traffic``)::
+
+    rocprofv3 --pmc FETCH_SIZE --kernel-trace -f csv -d OUT/fetch -o run -- \
+        python bench.py --steps 16 --warmup 4 --no-cpu --no-extra --calib-copy
+    rocprofv3 --pmc WRITE_SIZE --kernel-trace -f csv -d OUT/write -o run -- \
+        python bench.py --steps 16 --warmup 4 --no-cpu --no-extra --calib-copy
+    python bench.py --pmc-summary OUT/fetch OUT/write > profiles/decode_mk_kernel_traffic.txt
 """
 
 from __future__ import annotations
@@ -32,6 +50,9 @@ for _p in (REPO / "rwkv-tl_amd", REPO):
 METRIC = "RWKV7-0.4B ms/token decode B=1 & prefill T=128 ms; % HBM/MFMA roofline"
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
+DOMINANT_KERNEL = "decode_mk_kernel"
+TRAFFIC_FILE = REPO / "profiles" / "decode_mk_kernel_traffic.txt"
+CALIB_BYTES = 1 << 30  # the calibration copy reads and writes this many bytes
 
 
 def algorithmic_bytes(shape, batch: int, tokens_per_seq: int, head: bool) -> float:
@@ -61,6 +82,78 @@ def time_cuda(fn, iters: int) -> float:
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / iters
+
+
+def calib_copy() -> None:
+    """A plain copy kernel of known size (CALIB_BYTES read, CALIB_BYTES
+    written), run so that counter runs can scale FETCH_SIZE / WRITE_SIZE."""
+    import torch
+
+    src = torch.ones(CALIB_BYTES // 2, dtype=torch.float16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def _counter_rows(folder: Path) -> list[dict]:
+    import csv
+
+    files = sorted(Path(folder).rglob("*counter_collection.csv"))
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {folder}")
+    rows = []
+    for f in files:
+        with open(f, newline="") as fh:
+            rows.extend(csv.DictReader(fh))
+    return rows
+
+
+def _per_dispatch(rows: list[dict], counter: str, name_part: str) -> list[float]:
+    """Counter value (KiB) per dispatch of kernels whose name contains name_part."""
+    acc: dict[str, float] = {}
+    for r in rows:
+        if r.get("Counter_Name") == counter and name_part in r.get("Kernel_Name", ""):
+            key = r.get("Dispatch_Id") or r.get("Correlation_Id")
+            acc[key] = acc.get(key, 0.0) + float(r["Counter_Value"])
+    return list(acc.values())
+
+
+def pmc_summary(fetch_dir: str, write_dir: str) -> str:
+    """Text summary of the FETCH_SIZE and WRITE_SIZE runs: per-launch bytes of
+    the dominant kernel, each scaled by the calibration copy's reading."""
+    import statistics
+
+    f_rows, w_rows = _counter_rows(Path(fetch_dir)), _counter_rows(Path(write_dir))
+    out = []
+    vals = {}
+    for counter, rows in (("FETCH_SIZE", f_rows), ("WRITE_SIZE", w_rows)):
+        mk = _per_dispatch(rows, counter, DOMINANT_KERNEL)
+        cp = _per_dispatch(rows, counter, "neg_kernel") or _per_dispatch(rows, counter, "elementwise")
+        if not mk or not cp:
+            raise SystemExit(f"{counter}: no dispatches of {DOMINANT_KERNEL} or of the calibration copy")
+        mk_kib, cp_kib = statistics.median(mk), statistics.median(cp)
+        factor = (CALIB_BYTES / 1024.0) / cp_kib
+        vals[counter] = mk_kib * 1024.0 * factor
+        out.append(
+            f"{counter}: {DOMINANT_KERNEL} median {mk_kib:.1f} KiB/dispatch over {len(mk)} dispatches; "
+            f"calibration copy reads {cp_kib:.1f} KiB for {CALIB_BYTES // 1024} KiB moved -> factor {factor:.4f}; "
+            f"scaled {vals[counter]:.0f} B"
+        )
+    total = vals["FETCH_SIZE"] + vals["WRITE_SIZE"]
+    out.append(f"traffic_bytes_per_launch: {total:.0f}")
+    return "\n".join(out)
+
+
+def traffic_from_profile() -> float | None:
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(shape_name: str, steps: int, warmup: int) -> dict:
@@ -111,7 +204,13 @@ def main() -> None:
     ap.add_argument("--cpu-steps", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the headline decode line")
+    ap.add_argument("--calib-copy", action="store_true", help="also run a 1 GiB copy kernel (counter calibration)")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="summarise two rocprofv3 --pmc csv runs and exit (no GPU)")
     args = ap.parse_args()
+    if args.pmc_summary:
+        print(pmc_summary(*args.pmc_summary))
+        return
     if args.gpus != 1:
         print(
             f"bench.py measures one GPU only (--gpus {args.gpus} requested): the decode path has no "
@@ -155,6 +254,23 @@ def main() -> None:
     step_bytes = algorithmic_bytes(shape, 1, 1, head=True)
     step_gbs = step_bytes / (ms_tok * 1e-3) / 1e9
 
+    # ---- dominant kernel: one persistent launch per step, timed per launch --
+    if model.decode_launches(1) != 1:
+        raise SystemExit("the 0.4B batch-1 decode did not take the one-launch persistent path")
+    logits1 = torch.empty(1, V, dtype=torch.float16, device=dev)
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    torch.cuda.synchronize()
+    for i in range(K):
+        evs[i][0].record(stream)
+        model.decode_into(toks[Wm + i], S, logits1)
+        evs[i][1].record(stream)
+    torch.cuda.synchronize()
+    kern_us = 1000.0 * sum(a.elapsed_time(b) for a, b in evs) / K
+    kern_gbs = step_bytes / (kern_us * 1e-6) / 1e9
+    traffic = traffic_from_profile()
+    log(f"{DOMINANT_KERNEL}: {kern_us:.2f} us/launch")
+
     out: dict = {
         "metric": METRIC,
         "value": round(ms_tok, 5),
@@ -169,7 +285,7 @@ def main() -> None:
         "dtype": "f16",
         "data": "synthetic: seeded random-init weights (N(0,0.02)) and uniform random token ids",
         "config": {
-            "workload": "RWKV7-0.4B decode B=1, HIP-graph replay (config 3)",
+            "workload": "RWKV7-0.4B decode B=1 through HIPGraph (config 3; one persistent kernel per token)",
             "layers": shape.n_layer,
             "n_embd": shape.n_embd,
             "vocab": V,
@@ -186,7 +302,17 @@ def main() -> None:
             "alg_bytes_per_step": step_bytes,
         },
     }
-    out["roofline"] = dict(out["roofline_step"], kernel="whole decode step (graph replay)")
+    out["roofline"] = {
+        "bound": "hbm",
+        "achieved": round(kern_gbs, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
+        "traffic": traffic,
+        "kernel": DOMINANT_KERNEL,
+        "avg_launch_us": round(kern_us, 2),
+        "alg_bytes_per_launch": step_bytes,
+    }
 
     if not args.no_extra:
         # ---- decode B=16 ----
@@ -225,6 +351,8 @@ def main() -> None:
         out["prefill"] = pre
         out["prefill_T128_ms"] = pre["T128"]["ms"]
 
+    if args.calib_copy:
+        calib_copy()
     if not args.no_cpu:
         log(f"CPU baseline: {args.cpu_steps} decode steps of the fp32 oracle")
         out["cpu_baseline"] = cpu_baseline("0.4b", args.cpu_steps, 1)

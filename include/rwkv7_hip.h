@@ -119,6 +119,14 @@ int rwkv7_decode(const rwkv7_model *model, const rwkv7_state *state,
                  const int64_t *tokens, void *logits, void *workspace,
                  int64_t workspace_bytes, void *stream);
 
+/* Number of kernel launches one rwkv7_decode call makes for `batch`
+ * sequences (with_logits: whether logits are requested), or -1 for
+ * unsupported dims. 1 means the step is one persistent kernel, so a graph
+ * replay gains nothing over a direct call. The reference has no counterpart:
+ * its CUDAGraph wrapper (demo/cuda_graph.py:61-235) always captures; this
+ * lets the HIP-graph wrapper skip capture where it cannot help. */
+int rwkv7_decode_launches(const rwkv7_dims *dims, int32_t batch, int32_t with_logits);
+
 /* Prefill seq_len tokens per sequence: tokens i64 [B, T] (device). Updates
  * state in place and produces no logits, like RWKV7Base.prefill
  * (demo/_rwkv7_base.py:89-98) / RWKV7Torch.prefill (demo/rwkv7_torch.py:160-171). */

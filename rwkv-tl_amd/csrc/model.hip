@@ -303,6 +303,16 @@ static int check_model_state(const rwkv7_model *m, const rwkv7_state *s) {
   return RWKV7_OK;
 }
 
+// The one-launch persistent kernel serves batch-1 steps that produce logits,
+// for the sizes it was compiled for; RWKV7_DECODE_PATH=kernels forces the
+// multi-launch path (used by the tests that compare the two).
+static bool use_persistent_decode(const rwkv7_dims &d, int batch, bool logits) {
+  if (batch != 1 || !logits) return false;
+  const char *path = getenv("RWKV7_DECODE_PATH");
+  if (path && strcmp(path, "kernels") == 0) return false;
+  return mk_supported(d, mk_cus());
+}
+
 }  // namespace rwkv7
 
 using namespace rwkv7;
@@ -336,6 +346,15 @@ int64_t rwkv7_workspace_bytes(const rwkv7_dims *dims, int32_t batch, int32_t seq
   return a > b ? a : b;
 }
 
+int rwkv7_decode_launches(const rwkv7_dims *dims, int32_t batch, int32_t with_logits) {
+  if (check_dims(dims) != RWKV7_OK || batch < 1) return -1;
+  if (use_persistent_decode(*dims, batch, with_logits != 0)) return 1;
+  // decode_one: embed, 6 per layer, head GEMV; run_batched: embed, 10 per
+  // layer, final LayerNorm and head GEMM
+  if (batch == 1) return 1 + 6 * dims->n_layer + (with_logits ? 1 : 0);
+  return 1 + 10 * dims->n_layer + (with_logits ? 2 : 0);
+}
+
 int rwkv7_decode(const rwkv7_model *model, const rwkv7_state *state, const int64_t *tokens, void *logits,
                  void *workspace, int64_t workspace_bytes, void *stream) {
   RWKV7_TRY(check_model_state(model, state));
@@ -343,12 +362,9 @@ int rwkv7_decode(const rwkv7_model *model, const rwkv7_state *state, const int64
   if (workspace_bytes < rwkv7_workspace_bytes(&model->dims, state->batch, 1)) return RWKV7_EWORKSPACE;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (state->batch == 1) {
-    const rwkv7_dims &d = model->dims;
-    const char *path = getenv("RWKV7_DECODE_PATH");
-    const bool kernels = path && strcmp(path, "kernels") == 0;
-    if (!kernels && logits && mk_supported(d, mk_cus())) {
+    if (use_persistent_decode(model->dims, 1, logits != nullptr)) {
       rwkv7_layer_layout lay;
-      layout_of(d, &lay);
+      layout_of(model->dims, &lay);
       return launch_decode_mk(*model, lay, *state, tokens, logits, static_cast<char *>(workspace), st);
     }
     return decode_one(*model, *state, tokens, logits, static_cast<char *>(workspace), st);

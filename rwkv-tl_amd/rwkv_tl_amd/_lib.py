@@ -32,6 +32,7 @@ SYMBOLS = (
     "rwkv7_strerror",
     "rwkv7_layer_layout_get",
     "rwkv7_workspace_bytes",
+    "rwkv7_decode_launches",
     "rwkv7_decode",
     "rwkv7_prefill",
     "rwkv7_wkv7",
@@ -103,6 +104,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "rwkv7_strerror": (ctypes.c_char_p, [ctypes.c_int]),
         "rwkv7_layer_layout_get": (ctypes.c_int, [ctypes.POINTER(Dims), ctypes.POINTER(LayerLayout)]),
         "rwkv7_workspace_bytes": (i64, [ctypes.POINTER(Dims), i32, i32]),
+        "rwkv7_decode_launches": (ctypes.c_int, [ctypes.POINTER(Dims), i32, i32]),
         "rwkv7_decode": (ctypes.c_int, [ctypes.POINTER(Model), ctypes.POINTER(StateDesc), vp, vp, vp, i64, vp]),
         "rwkv7_prefill": (ctypes.c_int, [ctypes.POINTER(Model), ctypes.POINTER(StateDesc), vp, i32, vp, i64, vp]),
         "rwkv7_wkv7": (ctypes.c_int, [vp, vp, vp, i32, vp, vp, vp, vp, vp, i32, i32, i32, vp]),

@@ -8,7 +8,9 @@ every replay (6L small copies per token plus a ``token.item()`` host sync,
 arenas' addresses and replays in place. Per replay the only other work is a
 device copy of the token ids into the graph's input buffer and a clone of the
 logits. A state whose tensors were rebound (not arena views any more) runs
-eagerly.
+eagerly, and so does a decode step that the library runs as one persistent
+kernel (``RWKV7HIP.decode_launches(B) == 1``), where a replay cannot save
+launches and would only add the token copy.
 
 Capture is lazy and per exact shape: decode per (state, batch), prefill per
 (state, T) for 2 <= T <= ``prefill_graph_max_t``; larger T runs eagerly.
@@ -109,6 +111,9 @@ class HIPGraph(RWKV7Model):
             return m.decode(token, S)
         m._check_state(S)
         B = S.batch_size
+        if m.decode_launches(B) == 1:
+            # one persistent kernel: a replay would only add the token copy
+            return m.decode(token, S)
         key = self._key("decode", S, B)
         entry = self._graphs.get(key)
         if entry is None:

@@ -109,6 +109,10 @@ class RWKV7HIP(RWKV7Model):
     # raw steps (also what HIPGraph captures)
     # ------------------------------------------------------------------ #
 
+    def decode_launches(self, batch: int) -> int:
+        """Kernel launches of one decode step with logits (1: a single persistent kernel)."""
+        return int(self._lib.rwkv7_decode_launches(ctypes.byref(self.dev.dims), batch, 1))
+
     def decode_into(self, tok: Tensor, S: State, logits: Tensor | None) -> None:
         """One decode step: ``tok`` int64 [B] on device, ``logits`` f16 [B, V] or None."""
         B = S.batch_size

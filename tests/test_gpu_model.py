@@ -171,10 +171,17 @@ def test_batched_decode_rows_match_single_sequences(B, cuda):
             assert r < 5e-3, f"layer {i} row {b}: {r:.2e}"
 
 
-def test_graph_replay_matches_eager(cuda):
+@pytest.mark.parametrize("path", ["persistent", "kernels"])
+def test_graph_replay_matches_eager(cuda, path, monkeypatch):
     """HIP-graph decode and prefill replay == eager calls, bit for bit, over
-    several replays with eager work and syncs in between."""
+    several replays with eager work and syncs in between. On the persistent
+    path decode is one launch and runs eagerly; the multi-launch path is
+    captured."""
+    if path == "kernels":
+        monkeypatch.setenv("RWKV7_DECODE_PATH", "kernels")
     st = setup_for("tiny", cuda)
+    single = st.model.decode_launches(1) == 1
+    assert single == (path == "persistent")
     V = st.w.head.shape[0]
     g = torch.Generator().manual_seed(11)
     prompt = torch.randint(0, V, (12,), generator=g)
@@ -192,7 +199,8 @@ def test_graph_replay_matches_eager(cuda):
         assert torch.equal(la, lb), f"replay {i}"
         for x, y in zip(Sa.arenas, Sb.arenas):
             assert torch.equal(x, y), f"replay {i} state"
-    assert len(graphed._graphs) == 2  # one prefill (T=12) and one decode graph
+    # one prefill graph (T=12), plus a decode graph on the multi-launch path
+    assert len(graphed._graphs) == (1 if single else 2)
 
 
 def test_make_rwkv7_and_forward_generate(cuda):
