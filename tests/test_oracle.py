@@ -122,16 +122,58 @@ def test_wkv7_step_matches_brute_force():
     torch.testing.assert_close(Sf.double(), torch.tensor(Sb, dtype=torch.float64), rtol=1e-5, atol=1e-5)
 
 
+def _steps(step, S, vecs):
+    r, w, k, v, a, b = vecs
+    ys = []
+    for t in range(r.shape[0]):
+        y, S = step(S, r[t], w[t], k[t], v[t], a[t], b[t])
+        ys.append(y)
+    return torch.stack(ys), S
+
+
 def test_wkv7_brute_plants_detected():
-    """A dropped term or transposed operand in the step changes the result."""
-    S, (r, w, k, v, a, b) = _rand_step(T=1, dtype=torch.float32)
-    y, Sn = R.wkv7_step(S, r[0], w[0], k[0], v[0], a[0], b[0])
-    # transposed state (S^T instead of S) gives a different update
-    y2, _ = R.wkv7_step(S.transpose(1, 2), r[0], w[0], k[0], v[0], a[0], b[0])
-    assert not torch.allclose(y, y2)
-    # dropping the rank-1 term gives a different update
-    y3, _ = R.wkv7_step(S, r[0], w[0], k[0], v[0], torch.zeros_like(a[0]), b[0])
-    assert not torch.allclose(y, y3)
+    """Planted mistakes in a copy of the oracle's step (CPU only) must fail the
+    brute-force check that the real step passes: the check can tell a wrong
+    index, a dropped term, a wrong sign and a stale operand apart."""
+    S, vecs = _rand_step(T=3, dtype=torch.float32)
+    yb, Sb = R.wkv7_brute(S.tolist(), *[x.tolist() for x in vecs])
+    yb, Sb = torch.tensor(yb, dtype=torch.float64), torch.tensor(Sb, dtype=torch.float64)
+
+    def agrees(step):
+        y, Sn = _steps(step, S.clone(), vecs)
+        return torch.allclose(y.double(), yb, rtol=1e-5, atol=1e-6) and torch.allclose(
+            Sn.double(), Sb, rtol=1e-5, atol=1e-6
+        )
+
+    assert agrees(R.wkv7_step)
+
+    def decay_rows(S, r, w, k, v, a, b):  # w applied along the value axis
+        Sn = S * w.unsqueeze(2) + torch.einsum("hva,ha,hb->hvb", S, a, b) + torch.einsum("hv,hk->hvk", v, k)
+        return torch.einsum("hvk,hk->hv", Sn, r), Sn
+
+    def no_rank1(S, r, w, k, v, a, b):  # dropped (S a) b^T
+        Sn = S * w.unsqueeze(1) + torch.einsum("hv,hk->hvk", v, k)
+        return torch.einsum("hvk,hk->hv", Sn, r), Sn
+
+    def flipped(S, r, w, k, v, a, b):  # wrong sign on the rank-1 term
+        Sn = S * w.unsqueeze(1) - torch.einsum("hva,ha,hb->hvb", S, a, b) + torch.einsum("hv,hk->hvk", v, k)
+        return torch.einsum("hvk,hk->hv", Sn, r), Sn
+
+    def stale_sa(S, r, w, k, v, a, b):  # S a taken after the decay instead of before
+        Sd = S * w.unsqueeze(1)
+        Sn = Sd + torch.einsum("hva,ha,hb->hvb", Sd, a, b) + torch.einsum("hv,hk->hvk", v, k)
+        return torch.einsum("hvk,hk->hv", Sn, r), Sn
+
+    def kv_swapped(S, r, w, k, v, a, b):  # k v^T instead of v k^T
+        Sn = S * w.unsqueeze(1) + torch.einsum("hva,ha,hb->hvb", S, a, b) + torch.einsum("hk,hv->hvk", v, k)
+        return torch.einsum("hvk,hk->hv", Sn, r), Sn
+
+    def y_before(S, r, w, k, v, a, b):  # y read from the old state
+        Sn = S * w.unsqueeze(1) + torch.einsum("hva,ha,hb->hvb", S, a, b) + torch.einsum("hv,hk->hvk", v, k)
+        return torch.einsum("hvk,hk->hv", S, r), Sn
+
+    for bad in (decay_rows, no_rank1, flipped, stale_sa, kv_swapped, y_before):
+        assert not agrees(bad), bad.__name__
 
 
 def test_wkv7_closed_forms():
