@@ -8,38 +8,68 @@
 //   P4  LN2 + token shift + FFN key + relu^2                       (F rows)
 //   P5  FFN value + residual                                       (C rows, K=F)
 // so decode is a chain of 5L+1 stages, each moving a few MiB of weights. Here
-// the whole token runs in one launch with one workgroup per CU. Every stage's
-// rows are split evenly over the workgroups; a workgroup issues the loads of
-// its weight slice BEFORE waiting for the stage's input vector, so weight
-// streaming overlaps the hand-off latency. Inputs are exchanged through global
-// memory as 64-bit words {tag:32, value:32} written and read with device-scope
-// (sc1) accesses: the consumer polls the data words themselves, so a hand-off
-// costs one memory round trip and needs no atomics or cache maintenance. The
-// tag is unique per (launch, stage), so words left over from older stages or
-// launches never match.
+// the whole token runs in one launch with one workgroup per CU; every stage's
+// rows are split evenly over the workgroups and exchanged through global memory
+// as 64-bit words {tag:32, value:32}, written and read with device-scope (sc1)
+// accesses. The consumer polls the data words themselves, so a hand-off costs
+// one memory round trip and needs no atomics or cache maintenance; the tag is
+// unique per (launch, stage), so words left over from older stages or launches
+// never match.
 //
-// Every wait is bounded: past ~1 s a waiter raises a per-launch abort word and
-// gives up, and every other waiter then gives up within a few polls, so a
-// launch always terminates (its output is then garbage and an error counter is
-// set). The grid must be resident all at once: one 512-thread workgroup per
-// CU, grid = CU count.
+// Wave roles. Vector-memory loads of one wave complete in issue order, so a
+// wave that polls hand-off words while weight loads are in flight waits for
+// those loads on every poll. The workgroup therefore splits the two jobs:
+//   * wave 7 (the comm wave) polls each stage's input vector into LDS and
+//     never issues a weight load (one wave gathers a 1024-word vector in about
+//     half the time two waves that must agree on completion take);
+//   * waves 0..6 (math waves) stream weights into registers two stages ahead
+//     of their use and compute. A math wave waits for its loads only at the
+//     end of a stage (s_waitcnt vmcnt(0) right before it issues the next
+//     stage's loads), when everything outstanding is at least one stage old.
+// The two roles run separate code and meet at the same sequence of workgroup
+// barriers (listed in comm_main). Every output row belongs to one math wave,
+// and LayerNorm statistics are recomputed per wave, so apart from the per-head
+// core (P2) no stage needs a cross-wave reduction.
+//
+// Every wait is bounded: past ~1 s a comm wave raises a per-launch abort
+// word and gives up, every other comm wave then gives up within a few polls,
+// and barriers never wait on memory, so a launch always terminates (its output
+// is then garbage and an error counter is set). The grid must be resident all
+// at once: one 512-thread workgroup per CU, grid = CU count.
 //
 // Reference counterparts: RWKV7Base.decode / make_TMIX / make_CMIX
 // (demo/_rwkv7_base.py:74-87,153-206,285-290) and the captured decode graph
 // (demo/cuda_graph.py:111-128).
+#include <type_traits>
+
 #include "rwkv7_kernels.h"
 
 #define RWKV7_DEV_HOST_INLINE __host__ __device__ inline
 
 namespace rwkv7 {
 
-constexpr int kT = 512;        // threads per workgroup
-constexpr int kW = kT / 64;    // waves per workgroup
-constexpr int kRMax = 4;       // max rows per wave in P1 / P4 (the RM template bound)
+constexpr int kT = 512;          // threads per workgroup
+constexpr int kW = kT / 64;      // waves per workgroup
+constexpr int kNComm = 1;        // comm waves (the last ones)
+constexpr int kMW = kW - kNComm; // math waves 0..kMW-1
+constexpr int kMT = kMW * 64;    // math threads
+constexpr int kHB = 4;           // head rows per batch
+constexpr int kHRing = 3;        // head batches in flight
 constexpr int kSpinLimit = 1 << 21;
+constexpr int kRep = 8;          // replicas of each broadcast hand-off vector
+static_assert(kRep < 64, "lanes 0..kRep of a wave publish a value and its state");
 
-// sync words (the first 256 bytes of the exchange region)
-enum { SY_EPOCH = 0, SY_ABORT = 16, SY_ERRORS = 32 };
+// 32-bit sync words at the start of the exchange region (byte offsets 0, 16
+// and 32): launch epoch, abort word, count of waits that timed out
+enum { SY_EPOCH = 0, SY_ABORT = 4, SY_ERRORS = 8 };
+
+// s_waitcnt vmcnt(0), leaving the export and LDS counters alone
+RWKV7_DEV void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Keeps the instruction scheduler from moving anything across this point:
+// placed after a prefetch so its loads are issued there, not sunk next to
+// their first use.
+RWKV7_DEV void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
 RWKV7_DEV unsigned ld_u32(const unsigned *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -55,13 +85,16 @@ RWKV7_DEV void publish(uint64_t *p, unsigned tag, float v) {
                      __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Tags are 32-bit and wrap: tag = epoch * nph + 1 + phase (mod 2^32). A slot
+// is rewritten by every launch, so a stale word is at most one launch old
+// (or a few, after aborted launches), and two tags of one slot collide only
+// k launches apart with k * nph = 0 (mod 2^32), i.e. never in practice. The
+// first launch on a zeroed workspace uses tags 1..nph, never 0.
 struct MkCtx {
   unsigned *sync;
   unsigned epoch;
-  unsigned nph;
-  RWKV7_DEV unsigned tag(int phase) const {
-    return (unsigned)(((uint64_t)epoch * nph + (uint64_t)phase) % 0xFFFFFFFFull) + 1u;
-  }
+  unsigned tag0;  // epoch * nph + 1
+  RWKV7_DEV unsigned tag(int phase) const { return tag0 + (unsigned)phase; }
   RWKV7_DEV bool aborted() const { return ld_u32(sync + SY_ABORT) == epoch + 1u; }
   RWKV7_DEV void abort() const {
     st_u32(sync + SY_ABORT, epoch + 1u);
@@ -69,39 +102,81 @@ struct MkCtx {
   }
 };
 
-// Waits until every word src[idx(i)] (i < n, i.e. the entries this thread
-// handles: i = threadIdx.x + kT * j) carries `tag`, storing the values into
-// dst[i]. Ends with a workgroup barrier.
-template <int NPT, typename Idx>
-RWKV7_DEV void poll_vec(const MkCtx &cx, const uint64_t *src, int n, unsigned tag, float *dst, Idx idx) {
-  unsigned pending = 0;
-#pragma unroll
-  for (int j = 0; j < NPT; ++j)
-    if ((int)threadIdx.x + kT * j < n) pending |= 1u << j;
-  int spins = 0;
-  while (pending) {
-    uint64_t w[NPT];
-#pragma unroll
-    for (int j = 0; j < NPT; ++j)
-      if (pending & (1u << j)) w[j] = ld_u64(src + idx(threadIdx.x + kT * j));
-#pragma unroll
-    for (int j = 0; j < NPT; ++j) {
-      if ((pending & (1u << j)) && (unsigned)(w[j] >> 32) == tag) {
-        dst[threadIdx.x + kT * j] = __builtin_bit_cast(float, (unsigned)w[j]);
-        pending &= ~(1u << j);
-      }
-    }
-    if (pending) {
-      ++spins;
-      if ((spins & 63) == 0 && cx.aborted()) break;
-      if (spins > kSpinLimit) {
-        cx.abort();
-        break;
-      }
-    }
+struct MkArgs {
+  const char *layers;
+  int64_t lbytes, o_rkv, o_l2, o_o, o_fk, o_fv, o_vec;
+  const uint16_t *emb, *head;
+  const float *ln_out;
+  int L, C, H, F, V, rv, rw, ra, rg;
+  uint16_t *tmix_x;
+  float *rnn;
+  uint16_t *cmix_x;
+  const int64_t *tok;
+  uint16_t *logits;
+  // hand-off words; x, core and hid have kRep replicas of C, C and F words
+  uint64_t *x_ex, *proj_ex, *core_ex, *hid_ex;
+  unsigned *sync;
+};
+
+// Row ranges and roles, computed identically by every wave of a workgroup.
+struct MkGeom {
+  int C, F, H, L, SR, G, g;
+  int p1a, p1b;      // rows of the stacked [r;k;v;LoRA1] matrix (P1)
+  int p4a, p4b;      // rows of the FFN key matrix (P4)
+  int owa, nown;     // channels whose residual this workgroup owns (P3, P5)
+  int seg0, nseg;    // P1 row segments touched (see seg_of)
+  int ha, hb;        // head rows
+  bool head;         // this workgroup runs the per-head core of head g (P2)
+  int e[6];          // P1 segment starts: k, v, LoRA v, w, a, g
+  RWKV7_DEV int seg_of(int r) const {
+    return (r >= e[0]) + (r >= e[1]) + (r >= e[2]) + (r >= e[3]) + (r >= e[4]) + (r >= e[5]);
   }
-  __syncthreads();
+};
+
+RWKV7_DEV int seg_mu(int sgm) {  // vector-block index of each P1 segment's mix
+  return sgm == 0 ? RWKV7_V_X_R : sgm == 1 ? RWKV7_V_X_K : sgm <= 3 ? RWKV7_V_X_V
+       : sgm == 4 ? RWKV7_V_X_W : sgm == 5 ? RWKV7_V_X_A : RWKV7_V_X_G;
 }
+
+// LDS layout (floats). Each stage input has its own buffer, so the comm wave
+// fills the next stage's input while the math waves read the current one.
+struct MkLds {
+  float *x1;      // [C]  P1 input x (and the head's input)
+  float *ln1;     // [C]  LN1(x): the time-mix shift state written in P3
+  float *mix;     // [4][C] P1 segment mixes; the head's normalised input
+  float *p2;      // [192 + SR] P2 input: r, k, v of the head, activated LoRA1
+  float *gsum;    // [5][64] LoRA second-step dots: v, w, a, g (two halves)
+  float *core;    // [7][64] r w k a b y v of the head (P2)
+  float *core_in; // [C]  P3 input
+  float *x4;      // [C]  P4 input x'
+  float *ln2;     // [C]  LN2(x'): the channel-mix shift state written in P5
+  float *mix4;    // [C]  P4 mix
+  float *hid;     // [F]  P5 input
+  unsigned *pubs; // count of math-wave publish steps (the comm waves' start signal)
+};
+
+RWKV7_DEV_HOST_INLINE int64_t mk_lds_floats(int C, int F, int SR) {
+  return (int64_t)10 * C + (192 + SR) + 5 * 64 + 7 * 64 + F + 4;
+}
+
+RWKV7_DEV MkLds mk_lds(float *smem, int C, int F, int SR) {
+  MkLds s;
+  s.x1 = smem;
+  s.ln1 = s.x1 + C;
+  s.mix = s.ln1 + C;
+  s.core_in = s.mix + 4 * C;
+  s.x4 = s.core_in + C;
+  s.ln2 = s.x4 + C;
+  s.mix4 = s.ln2 + C;
+  s.hid = s.mix4 + C;
+  s.p2 = s.hid + F;
+  s.gsum = s.p2 + 192 + SR;
+  s.core = s.gsum + 5 * 64;
+  s.pubs = reinterpret_cast<unsigned *>(s.core + 7 * 64);
+  return s;
+}
+
+// ---- math-wave helpers --------------------------------------------------------
 
 // acc + sum_e w[e] * x[e] for 8 f16 weights and 8 f32 inputs in LDS.
 RWKV7_DEV float dot8(const uint4 &w, const float *x, float acc) {
@@ -115,568 +190,728 @@ RWKV7_DEV float dot8(const uint4 &w, const float *x, float acc) {
   return acc;
 }
 
+// Same with the 8 inputs in registers.
+RWKV7_DEV float dot8r(const uint4 &w, const float (&x)[8], float acc) {
+  float wf[8];
+  h8_to_f(w, wf);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc = fmaf(wf[e], x[e], acc);
+  return acc;
+}
+
+// Dot of one row held by the wave (lane l has chunks l + 64c) with x in LDS;
+// the wave-uniform result.
+template <int NC>
+RWKV7_DEV float row_dot(const uint4 (&w)[NC], const float *x, int nch) {
+  const int lane = threadIdx.x & 63;
+  float acc = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int j = lane + 64 * c;
+    if (j < nch) acc = dot8(w[c], x + 8 * j, acc);
+  }
+  return wave_sum(acc);
+}
+
+// Loads row r of W (row stride ld halfs, nch 16-byte chunks) as lane chunks.
+template <int NC>
+RWKV7_DEV void load_row(const uint16_t *W, int64_t ld, int r, bool valid, int nch, uint4 (&w)[NC]) {
+  const int lane = threadIdx.x & 63;
+  const uint4 *row = reinterpret_cast<const uint4 *>(W + (int64_t)r * ld);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int j = lane + 64 * c;
+    w[c] = (valid && j < nch) ? ld_stream(row + j) : make_uint4(0, 0, 0, 0);
+  }
+}
+
+// Mean and 1/std of a C-vector in LDS (C <= 256 * NV), computed by one wave:
+// one batched read into registers, then two passes over them.
+template <int NV>
+RWKV7_DEV float2 wave_ln_stats(const float *x, int C) {
+  const int lane = threadIdx.x & 63;
+  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+  const int C4 = C >> 2;
+  float4 v[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int i = lane + 64 * k;
+    v[k] = i < C4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
+  const float mean = wave_sum(s) / (float)C;
+  float q = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    if (lane + 64 * k < C4) {
+      const float a = v[k].x - mean, b = v[k].y - mean, c = v[k].z - mean, d = v[k].w - mean;
+      q += (a * a + b * b) + (c * c + d * d);
+    }
+  }
+  return make_float2(mean, rsqrtf(wave_sum(q) / (float)C + kLnEps));
+}
+
+// ---- comm wave ------------------------------------------------------------------
+
+// ---- comm waves -----------------------------------------------------------------
+
+// 16-byte device-scope (sc1) loads through a buffer resource: two tagged words
+// per load, and reads past the end of the resource return zero.
+RWKV7_DEV __amdgpu_buffer_rsrc_t words_rsrc(const uint64_t *p, int64_t nwords) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t *>(p), 0, (int)(nwords * 8), 0x00020000);
+}
+RWKV7_DEV uint4 ld_pair(__amdgpu_buffer_rsrc_t r, int word) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, word * 8, 0, /*sc1*/ 16);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// Waits until every word idx(i), i < n, of the buffer `r` carries `tag`,
+// handing each value to put(i, v). idx must map each even i and i + 1 to
+// consecutive, 16-byte aligned words. Comm wave cw, lane l handles the pairs
+// p = 64 cw + l + 64 kNComm j (j < NJ), i = 2p.
+//
+// A poll round is one 16-byte load per pair, and under weight streaming its
+// round trip is ~1.5 us, so a round issued just before the last word lands
+// would cost another full round trip. The loop therefore keeps D rounds in
+// flight (re-issued unconditionally, so the compiler's load counting stays
+// exact) and checks them oldest first: new data is seen within about
+// RTT / D of arriving. At most 16 loads per lane are in flight (more slows a
+// wave down sharply). `probe` > 0 first polls one pair in every `probe` words
+// until those carry the tag, to spare traffic while producers still compute.
+template <int NJ, int D, typename Idx, typename Put>
+RWKV7_DEV void comm_poll(const MkCtx &cx, int cw, __amdgpu_buffer_rsrc_t r, int n, int probe, unsigned tag,
+                         Idx idx, Put put) {
+  static_assert(NJ * D <= 16 && NJ <= 16, "at most 16 loads per lane in flight");
+  int p0 = 64 * cw + (threadIdx.x & 63);
+  asm volatile("" : "+v"(p0));  // per-call addresses: keep them out of the layer loop
+  constexpr int kStep = 64 * kNComm;
+  const int np = n >> 1;
+  int spins = 0;
+  auto keep_waiting = [&]() {  // bounded: false once the launch is aborted
+    ++spins;
+    if ((spins & 1023) == 0 && cx.aborted()) return false;
+    if (spins > kSpinLimit) {
+      cx.abort();
+      return false;
+    }
+    return true;
+  };
+  if (probe > 0) {
+    const int nq = (n + probe - 1) / probe;
+    bool waiting = p0 < nq;
+    while (waiting) {
+      asm volatile("" ::: "memory");  // re-read every round
+      const uint4 v = ld_pair(r, idx(probe * p0));
+      if (v.y == tag) waiting = false;
+      else if (!keep_waiting()) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  unsigned pending = 0;
+  int addr[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int p = p0 + kStep * j;
+    if (p < np) pending |= 1u << j;
+    addr[j] = idx(p < np ? 2 * p : 0);
+  }
+  uint4 buf[D][NJ];
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) buf[d][j] = ld_pair(r, addr[j]);
+  // Straight-line body: every buffer is checked and re-issued each pass, so at
+  // each check exactly (D - 1) * NJ younger loads are in flight.
+  while (true) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        if (((pending >> j) & 1) && buf[d][j].y == tag && buf[d][j].w == tag) {
+          const int i = 2 * (p0 + kStep * j);
+          put(i, __builtin_bit_cast(float, buf[d][j].x));
+          put(i + 1, __builtin_bit_cast(float, buf[d][j].z));
+          pending &= ~(1u << j);
+        }
+      }
+      asm volatile("" ::: "memory");  // re-read every round
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) buf[d][j] = ld_pair(r, addr[j]);
+    }
+    if (__builtin_amdgcn_ballot_w64(pending != 0) == 0 || !keep_waiting()) break;
+  }
+}
+
 struct Ident {
   RWKV7_DEV int operator()(int i) const { return i; }
 };
 
-// Sum over the 512 threads; every thread gets the result.
-RWKV7_DEV float block_sum(float v, float *red) {
-  v = wave_sum(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < kW; ++i) s += red[i];
-  return s;
-}
-
-// out[c] = LN(x)[c] for c < C (x, out in LDS; out may alias x).
-RWKV7_DEV void ln_lds(const float *x, float *out, const float *w, const float *b, int C, float *red) {
-  float s = 0.f;
-  for (int c = threadIdx.x; c < C; c += kT) s += x[c];
-  const float mean = block_sum(s, red) / (float)C;
-  float q = 0.f;
-  for (int c = threadIdx.x; c < C; c += kT) {
-    const float d = x[c] - mean;
-    q += d * d;
-  }
-  const float rstd = rsqrtf(block_sum(q, red) / (float)C + kLnEps);
-  __syncthreads();
-  for (int c = threadIdx.x; c < C; c += kT) out[c] = (x[c] - mean) * rstd * w[c] + b[c];
-  __syncthreads();
-}
-
-// Floats of the stage-input region: the polled FFN hidden vector, P2's inputs,
-// or up to 4 per-segment mixed vectors of P1.
-RWKV7_DEV_HOST_INLINE int mk_nin(int C, int F, int SR) {
-  int n = F > 192 + SR ? F : 192 + SR;
-  return n > 4 * C ? n : 4 * C;
-}
-
-struct MkArgs {
-  const char *layers;
-  int64_t lbytes, o_rkv, o_l2, o_o, o_fk, o_fv, o_vec;
-  const uint16_t *emb, *head;
-  const float *ln_out;
-  int L, C, H, F, V, rv, rw, ra, rg;
-  uint16_t *tmix_x;
-  float *rnn;
-  uint16_t *cmix_x;
-  const int64_t *tok;
-  uint16_t *logits;
-  uint64_t *x_ex, *proj_ex, *core_ex, *hid_ex;
-  unsigned *sync;
-};
-
-// Loads this wave's rows of W (row stride ld halfs) for a wave-per-row stage:
-// wave w owns rows r0 + w + kW * i (i < RM) below r1; lane l holds the
-// 16-byte chunks l + 64 * c of each row.
-template <int RM, int CPL>
-RWKV7_DEV void load_rows(const uint16_t *W, int64_t ld, int r0, int r1, int K, uint4 (&wreg)[RM][CPL]) {
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int nch = K >> 3;
-#pragma unroll
-  for (int i = 0; i < RM; ++i) {
-    const int r = r0 + wv + kW * i;
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      const int j = lane + 64 * c;
-      wreg[i][c] = (r < r1 && j < nch) ? ld_stream(reinterpret_cast<const uint4 *>(W + (int64_t)r * ld) + j)
-                                       : make_uint4(0, 0, 0, 0);
-    }
-  }
-}
-
-// Rows split along K over several waves (P3, P5): wave w works on row
-// r0 + w / ks, K-part w % ks; lane chunks j = part*per + lane + 64*c.
-template <int NC>
-RWKV7_DEV void load_split(const uint16_t *W, int64_t ld, int r0, int nrow, int ks, int K, uint4 (&wreg)[NC]) {
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int nch = K >> 3, per = (nch + ks - 1) / ks;
-  const int row = wv / ks, part = wv % ks;
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int jj = lane + 64 * c;
-    const int j = part * per + jj;
-    wreg[c] = (row < nrow && jj < per && j < nch)
-                  ? ld_stream(reinterpret_cast<const uint4 *>(W + (int64_t)(r0 + row) * ld) + j)
-                  : make_uint4(0, 0, 0, 0);
-  }
-}
-
-// Partial dot of the split rows with x (LDS f32, K values); partial sums are
-// combined through red[] and row results returned to threads t < nrow.
-template <int NC>
-RWKV7_DEV float dot_split(const uint4 (&wreg)[NC], const float *x, int nrow, int ks, int K, float *red) {
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int nch = K >> 3, per = (nch + ks - 1) / ks;
-  const int part = wv % ks;
-  float acc = 0.f;
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int jj = lane + 64 * c;
-    const int j = part * per + jj;
-    if (jj < per && j < nch) {
-      acc = dot8(wreg[c], x + 8 * j, acc);
-    }
-  }
-  acc = wave_sum(acc);
-  if (lane == 0) red[wv] = acc;
-  __syncthreads();
-  float out = 0.f;
-  if ((int)threadIdx.x < nrow) {
-    for (int p = 0; p < ks; ++p) out += red[threadIdx.x * ks + p];
-  }
-  __syncthreads();
-  return out;
-}
-
-// Loads vec[c] for this thread's elements c = threadIdx.x + kT * i (i < CPL).
-template <int CPL>
-RWKV7_DEV void ld_own(float (&dst)[CPL], const float *src, int C) {
-#pragma unroll
-  for (int i = 0; i < CPL; ++i) {
-    const int c = threadIdx.x + kT * i;
-    dst[i] = c < C ? src[c] : 0.f;
-  }
-}
-template <int CPL>
-RWKV7_DEV void ld_own16(float (&dst)[CPL], const uint16_t *src, int C) {
-#pragma unroll
-  for (int i = 0; i < CPL; ++i) {
-    const int c = threadIdx.x + kT * i;
-    dst[i] = c < C ? h2f(src[c]) : 0.f;
-  }
-}
-
-// Polls this thread's own elements c = threadIdx.x + kT * i of a tagged vector
-// into registers (no barrier).
-template <int CPL>
-RWKV7_DEV void poll_own(const MkCtx &cx, const uint64_t *src, int n, unsigned tag, float (&dst)[CPL]) {
-  unsigned pending = 0;
-#pragma unroll
-  for (int i = 0; i < CPL; ++i)
-    if ((int)threadIdx.x + kT * i < n) pending |= 1u << i;
-    else dst[i] = 0.f;
+// Waits (LDS spin, bounded by the launch's abort word) until the math waves
+// of this workgroup have completed `target` publish steps.
+RWKV7_DEV void wait_local(const MkCtx &cx, const unsigned *pubs, unsigned target) {
   int spins = 0;
-  while (pending) {
-    uint64_t w[CPL];
-#pragma unroll
-    for (int i = 0; i < CPL; ++i)
-      if (pending & (1u << i)) w[i] = ld_u64(src + threadIdx.x + kT * i);
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      if ((pending & (1u << i)) && (unsigned)(w[i] >> 32) == tag) {
-        dst[i] = __builtin_bit_cast(float, (unsigned)w[i]);
-        pending &= ~(1u << i);
-      }
-    }
-    if (pending) {
-      ++spins;
-      if ((spins & 63) == 0 && cx.aborted()) break;
-      if (spins > kSpinLimit) {
-        cx.abort();
-        break;
-      }
+  while (__hip_atomic_load(pubs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+    __builtin_amdgcn_s_sleep(1);
+    if ((++spins & 1023) == 0 && cx.aborted()) break;
+    if (spins > kSpinLimit) {
+      cx.abort();
+      break;
     }
   }
 }
 
-// LayerNorm of a vector held as this thread's own elements (block reductions).
-template <int CPL>
-RWKV7_DEV void ln_own(float (&x)[CPL], const float (&w)[CPL], const float (&b)[CPL], int C, float *red) {
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < CPL; ++i) s += x[i];
-  const float mean = block_sum(s, red) / (float)C;
-  float q = 0.f;
-#pragma unroll
-  for (int i = 0; i < CPL; ++i)
-    if ((int)threadIdx.x + kT * i < C) {
-      const float d = x[i] - mean;
-      q += d * d;
-    }
-  const float rstd = rsqrtf(block_sum(q, red) / (float)C + kLnEps);
-#pragma unroll
-  for (int i = 0; i < CPL; ++i) x[i] = (x[i] - mean) * rstd * w[i] + b[i];
+// Workgroup roles. Workgroups 0..H-1 (head workgroups) run only the
+// per-head core P2 of head g; the others (workers) run P1, P3, P4, P5 and the
+// logits, each stage's rows split evenly over the workers. A head workgroup
+// thus streams only its own head's operands (LoRA second-step rows, wkv state)
+// and nothing delays its hand-offs, which sit on the critical path.
+//
+// Barrier schedules (one line per workgroup barrier; the comm and math waves
+// of a workgroup execute the same sequence):
+//   head, per layer:    HA  P2 input in p2
+//                       B2a LoRA second-step dots in gsum
+//                       B2b gates in core
+//                       B2c wkv outputs in core
+//   worker, per layer:  A1  P1 input in x1
+//                       B1  P1 mixes in mix
+//                       A3  P3 input in core_in
+//                       A4  P4 input in x4
+//                       B4  P4 mix in mix4
+//                       A5  P5 input in hid
+//   worker, after:      AH  head input in x1
+//                       BH  normalised head input in mix
+// Worker math waves count their publish steps in s.pubs (kMW per P1, P3, P4,
+// P5); the comm wave starts reading a vector the workers produce only after
+// its own workgroup's share is out.
+
+// NJX: pairs per comm lane of a C-vector; NJF: of half an F-vector (the FFN
+// hidden vector is read in two halves).
+template <int NJX, int NJF>
+RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, const MkCtx &cx, int cw) {
+  constexpr int DX = 16 / NJX, DF = 16 / NJF;
+  const int lane = threadIdx.x & 63;
+  const int C = m.C, F = m.F, L = m.L;
+  int64_t token = a.tok[0];
+  token = token < 0 ? 0 : token >= a.V ? a.V - 1 : token;
+  const uint16_t *erow = a.emb + token * C;
+  for (int c = 64 * cw + lane; c < C; c += 64 * kNComm) s.x1[c] = h2f(erow[c]);
+  auto to = [](float *d) { return [d](int i, float v) { d[i] = v; }; };
+  const int rp = m.g % kRep;  // the replica this workgroup reads
+  const __amdgpu_buffer_rsrc_t r_x = words_rsrc(a.x_ex + (int64_t)rp * C, C);
+  const __amdgpu_buffer_rsrc_t r_core = words_rsrc(a.core_ex + (int64_t)rp * C, C);
+  const __amdgpu_buffer_rsrc_t r_hid = words_rsrc(a.hid_ex + (int64_t)rp * F, F / 2);
+  const __amdgpu_buffer_rsrc_t r_hid2 = words_rsrc(a.hid_ex + (int64_t)rp * F + F / 2, F / 2);
+  unsigned pubs = 0;  // publish steps of the math waves seen so far
+  for (int l = 0; l < L; ++l) {
+    const int ph = 5 * l;
+    __syncthreads();  // A1
+    __syncthreads();  // B1
+    pubs += kMW;
+    // the head workgroups' outputs: one probe pair per head first
+    comm_poll<NJX, DX>(cx, cw, r_core, C, kN, cx.tag(ph + 1), Ident(), to(s.core_in));
+    __syncthreads();  // A3
+    pubs += kMW;
+    wait_local(cx, s.pubs, pubs);
+    comm_poll<NJX, DX>(cx, cw, r_x, C, 0, cx.tag(ph + 2), Ident(), to(s.x4));
+    __syncthreads();  // A4
+    __syncthreads();  // B4
+    pubs += kMW;
+    wait_local(cx, s.pubs, pubs);
+    comm_poll<NJF, DF>(cx, cw, r_hid, F / 2, 0, cx.tag(ph + 3), Ident(), to(s.hid));
+    comm_poll<NJF, DF>(cx, cw, r_hid2, F / 2, 0, cx.tag(ph + 3), Ident(), to(s.hid + F / 2));
+    __syncthreads();  // A5
+    pubs += kMW;
+    wait_local(cx, s.pubs, pubs);
+    comm_poll<NJX, DX>(cx, cw, r_x, C, 0, cx.tag(ph + 4), Ident(), to(s.x1));
+  }
+  __syncthreads();  // AH
+  __syncthreads();  // BH
 }
 
-// RM: rows per wave in P1/P4; CPL: 16-byte chunks per lane of a C-long row
-// (also this thread's share of a C-long vector); NC5: chunks per lane of the
-// K-split rows of P3/P5; NPTH: hidden-vector words polled per thread; NL2:
-// LoRA second-step chunks per thread.
-template <int RM, int CPL, int NC5, int NPTH, int NL2>
-__global__ __launch_bounds__(kT) void decode_mk_kernel(MkArgs a) {
-  extern __shared__ __align__(16) float smem[];
-  const int C = a.C, F = a.F, H = a.H, L = a.L;
-  const int SR = a.rv + a.rw + a.ra + a.rg;
-  const int G = gridDim.x, g = blockIdx.x;
-  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+// NJP: pairs per comm lane of the P2 input vector.
+template <int NJP>
+RWKV7_DEV void comm_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const MkCtx &cx, int cw) {
+  constexpr int DP = 16 / NJP;
+  const int C = m.C, SR = m.SR, L = m.L;
+  const int h = m.g, rv = a.rv, rwa = a.rv + a.rw, rwaa = a.rv + a.rw + a.ra;
+  const __amdgpu_buffer_rsrc_t r_proj = words_rsrc(a.proj_ex, 3 * C + SR);
+  for (int l = 0; l < L; ++l) {
+    // r, k, v of this head and the whole LoRA first step, activated on arrival
+    // (tanh for w, sigmoid for g)
+    comm_poll<NJP, DP>(cx, cw, r_proj, 192 + SR, 0, cx.tag(5 * l),
+                       [&](int i) { return i < 192 ? (i >> 6) * C + h * kN + (i & 63) : 3 * C + (i - 192); },
+                       [&](int i, float v) {
+                         const int j = i - 192;
+                         if (j >= rv && j < rwa) v = tanhf(v);
+                         else if (j >= rwaa) v = sigmoidf_(v);
+                         s.p2[i] = v;
+                       });
+    __syncthreads();  // HA
+    __syncthreads();  // B2a
+    __syncthreads();  // B2b
+    __syncthreads();  // B2c
+  }
+}
 
-  float *s_x = smem;             // [C]  mixed input of P4 / normalised input of the head
-  float *s_ln1 = s_x + C;        // [C]  LN1 output (kept to P3 for the shift state)
-  float *s_ln2 = s_ln1 + C;      // [C]  LN2 output (kept to P5)
-  float *s_spare = s_ln2 + C;    // [C]
-  const int nin = mk_nin(C, F, SR);
-  float *s_in = s_spare + C;     // [nin] polled stage inputs / P1 segment mixes
-  float *s_red = s_in + nin;     // [64]
-  float *s_own = s_red + 64;     // [16] this workgroup's rows of the residual
-  float *s_vf = s_own + 16;      // [64] v_first of the head this workgroup owns
-  float *s_core = s_vf + 64;     // [8][64] r w k v a b g y
-  float *s_lora = s_core + 8 * 64;  // [512]
-  float *s_d = s_lora + 512;        // [4][64] LoRA second-step results
-  (void)s_spare;
+// ---- math waves -----------------------------------------------------------------
+
+// Per-head core of head g for every layer: LoRA second step, gates, L2 norm,
+// wkv7, GroupNorm, output gate (demo/rwkv7_torch.py:92-120). NL2: LoRA
+// second-step chunks per thread.
+template <int NL2>
+RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const MkCtx &cx, int wv) {
+  int mt = threadIdx.x, lane = mt & 63;
+  auto refresh = [&]() {
+    asm volatile("" : "+v"(mt));
+    lane = mt & 63;
+  };
+  const int C = m.C, H = m.H, SR = m.SR, L = m.L, g = m.g;
+  const int nch2 = SR >> 3;
+  // LoRA second step: wave q < 5 computes part q (v, w, a, first and second
+  // half of g) for channel lane; part q covers chunks [p2s(q), p2s(q + 1)) of
+  // the channel's [v|w|a|g] row
+  const int b1 = a.rv >> 3, b2 = (a.rv + a.rw) >> 3, b3 = (a.rv + a.rw + a.ra) >> 3;
+  const int b4 = b3 + (nch2 - b3 + 1) / 2;
+  auto p2s = [&](int q) { return q == 0 ? 0 : q == 1 ? b1 : q == 2 ? b2 : q == 3 ? b3 : q == 4 ? b4 : nch2; };
+  uint4 w2[NL2];
+  float4 S4[4];
+  float gv[8];
+  auto pre_p2 = [&](int l) {
+    const char *Lp = a.layers + (int64_t)l * a.lbytes;
+    if (wv < 5) {
+      const uint4 *row = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(Lp + a.o_l2) +
+                                                         (int64_t)(g * kN + lane) * SR);
+      const int js = p2s(wv), je = p2s(wv + 1);
+      if (je > js) {
+#pragma unroll
+        for (int i = 0; i < NL2; ++i) w2[i] = ld_stream(row + (js + i < je ? js + i : je - 1));
+      }
+    }
+    if (mt < 4 * kN) {
+      const float4 *Sp = reinterpret_cast<const float4 *>(a.rnn + (((int64_t)l * H + g) * kN + (mt >> 2)) * kN) +
+                         (mt & 3) * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) S4[e] = Sp[e];
+    }
+    if (wv == 0) {
+      const float *vec = reinterpret_cast<const float *>(Lp + a.o_vec);
+      const int idx[8] = {RWKV7_V_V0, RWKV7_V_W0, RWKV7_V_A0, RWKV7_V_K_K,
+                          RWKV7_V_K_A, RWKV7_V_R_K, RWKV7_V_LNX_W, RWKV7_V_LNX_B};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) gv[j] = vec[idx[j] * C + g * kN + lane];
+    }
+    sched_fence();
+  };
+  float vfirst = 0.f;  // v of layer 0 for channel g*64 + lane (wave 0)
+  float *s_r = s.core, *s_w = s.core + 64, *s_k = s.core + 128, *s_a = s.core + 192, *s_b = s.core + 256,
+        *s_y = s.core + 320;
+  pre_p2(0);
+  for (int l = 0; l < L; ++l) {
+    __syncthreads();  // HA
+    wait_vm0();       // this layer's operands (issued a layer ago)
+    refresh();
+    if (wv < 5) {  // LoRA second step, part wv of channel lane
+      const int js = p2s(wv), je = p2s(wv + 1);
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < NL2; ++i)
+        if (js + i < je) acc = dot8(w2[i], s.p2 + 192 + 8 * (js + i), acc);
+      s.gsum[wv * kN + lane] = acc;
+    }
+    __syncthreads();  // B2a
+    float v = 0.f, gate = 0.f, rk = 0.f;
+    if (wv == 0) {  // lane t = channel g*64 + t
+      const int t = lane;
+      const float dv = s.gsum[t], dw = s.gsum[kN + t], da = s.gsum[2 * kN + t];
+      const float dg = s.gsum[3 * kN + t] + s.gsum[4 * kN + t];
+      const float r = s.p2[t], k = s.p2[64 + t];
+      v = s.p2[128 + t];
+      if (l == 0) vfirst = v;
+      else v = v + sigmoidf_(gv[0] + dv) * (vfirst - v);
+      const float w = expf(-sigmoidf_(gv[1] + dw) / 1.6487212707001282f);
+      const float ag = sigmoidf_(gv[2] + da);
+      const float kk = k * gv[3];
+      const float kn = k + gv[4] * (k * ag - k);
+      const float nrm = sqrtf(wave_sum(kk * kk));
+      const float kh = kk / fmaxf(nrm, 1e-12f);
+      rk = wave_sum(r * kn * gv[5]);
+      gate = dg;
+      s_r[t] = r; s_w[t] = w; s_k[t] = kn; s_a[t] = kh; s_b[t] = -kh * ag;
+      s.core[384 + t] = v;
+    }
+    __syncthreads();  // B2b
+    if (mt < 4 * kN) {  // wkv7: 4 threads per state row, 16 columns each
+      const int row = mt >> 2, j0 = (mt & 3) * 16;
+      float Sv[16];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        Sv[4 * e] = S4[e].x; Sv[4 * e + 1] = S4[e].y; Sv[4 * e + 2] = S4[e].z; Sv[4 * e + 3] = S4[e].w;
+      }
+      float av[16], wv16[16], bv[16], kv[16], rv16[16];
+      auto ld16 = [&](float (&d)[16], const float *src) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float4 q = reinterpret_cast<const float4 *>(src + j0)[e];
+          d[4 * e] = q.x; d[4 * e + 1] = q.y; d[4 * e + 2] = q.z; d[4 * e + 3] = q.w;
+        }
+      };
+      ld16(av, s_a);
+      ld16(wv16, s_w);
+      ld16(bv, s_b);
+      ld16(kv, s_k);
+      ld16(rv16, s_r);
+      const float vi = s.core[384 + row];
+      float sa = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sa = fmaf(Sv[e], av[e], sa);
+      sa = sum4(sa);
+      float y = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        Sv[e] = Sv[e] * wv16[e] + sa * bv[e] + vi * kv[e];
+        y = fmaf(Sv[e], rv16[e], y);
+      }
+      y = sum4(y);
+      float4 *Sp = reinterpret_cast<float4 *>(a.rnn + (((int64_t)l * H + g) * kN + row) * kN + j0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Sp[e] = make_float4(Sv[4 * e], Sv[4 * e + 1], Sv[4 * e + 2], Sv[4 * e + 3]);
+      if ((mt & 3) == 0) s_y[row] = y;
+    }
+    __syncthreads();  // B2c
+    if (wv == 0) {
+      const float y = s_y[lane];
+      const float mean = wave_sum(y) * (1.f / kN);
+      const float d = y - mean;
+      const float var = wave_sum(d * d) * (1.f / kN);
+      const float yn = d * rsqrtf(var + kGnEps) * gv[6] + gv[7];
+      const float out = (yn + rk * v) * gate;
+#pragma unroll
+      for (int rp = 0; rp < kRep; ++rp) publish(a.core_ex + (int64_t)rp * C + g * kN + lane, cx.tag(5 * l + 1), out);
+    }
+    // next layer's operands: a whole layer to arrive
+    refresh();
+    if (l + 1 < L) pre_p2(l + 1);
+  }
+}
+
+// P1, P3, P4, P5 and the logits on the worker workgroups. CPL: 16-byte chunks
+// per lane of a C-long row; RM: P1/P4 rows per math wave; NC5: chunks per lane
+// of an F-long row; VPL: elements per math thread of a C-vector; NHB: head
+// batches.
+//
+// Weight schedule: right after publishing P1, a worker issues every load of
+// the rest of the layer (P3, P4, P5 rows and vectors, next layer's P1 rows and
+// vectors). They stream while the head workgroups run P2 (the layer's longest
+// wait), and a single vmcnt(0) at the start of P3 covers them all, so the
+// later hand-offs of the layer run with no weight traffic in flight.
+template <int CPL, int RM, int NC5, int VPL, int NHB>
+RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, const MkCtx &cx, int wv) {
+  // Math threads are 0..kMT-1. refresh() passes the thread index through an
+  // empty asm at each stage, so per-thread addresses are recomputed there
+  // instead of being hoisted out of the layer loop into ~100 live registers.
+  int mt = threadIdx.x, lane = mt & 63;
+  auto refresh = [&]() {
+    asm volatile("" : "+v"(mt));
+    lane = mt & 63;
+  };
+  const int C = m.C, F = m.F, L = m.L;
+  const int nchC = C >> 3, nchF = F >> 3;
+
+  uint4 w1[RM][CPL];
+  float v1w[VPL], v1b[VPL], mu1[4][VPL];
+  uint16_t pv1[VPL];
+  uint4 w3[CPL];
+  uint4 w4[RM][CPL];
+  float v4w[VPL], v4b[VPL], mu4[VPL];
+  uint16_t pv4[VPL];
+  uint4 w5[NC5];
+  uint4 wh[kHRing][kHB][CPL];
+  float hlw[VPL], hlb[VPL];
+
+  auto layer_ptr = [&](int l) { return a.layers + (int64_t)l * a.lbytes; };
+  auto vec_ptr = [&](int l) { return reinterpret_cast<const float *>(layer_ptr(l) + a.o_vec); };
+  auto ld_vec = [&](float (&d)[VPL], const float *src) {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int c = mt + kMT * i;
+      d[i] = c < C ? src[c] : 0.f;
+    }
+  };
+  auto ld_vec16 = [&](uint16_t (&d)[VPL], const uint16_t *src) {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int c = mt + kMT * i;
+      d[i] = c < C ? src[c] : (uint16_t)0;
+    }
+  };
+  auto pre_p1 = [&](int l) {
+    const uint16_t *W = reinterpret_cast<const uint16_t *>(layer_ptr(l) + a.o_rkv);
+#pragma unroll
+    for (int i = 0; i < RM; ++i) {
+      const int r = m.p1a + wv + kMW * i;
+      load_row<CPL>(W, C, r, r < m.p1b, nchC, w1[i]);
+    }
+    const float *vec = vec_ptr(l);
+    ld_vec(v1w, vec + RWKV7_V_LN1_W * C);
+    ld_vec(v1b, vec + RWKV7_V_LN1_B * C);
+    ld_vec16(pv1, a.tmix_x + (int64_t)l * C);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (q < m.nseg) ld_vec(mu1[q], vec + (int64_t)seg_mu(m.seg0 + q) * C);
+    sched_fence();
+  };
+  auto pre_p3 = [&](int l) {
+    const uint16_t *W = reinterpret_cast<const uint16_t *>(layer_ptr(l) + a.o_o);
+    load_row<CPL>(W, C, m.owa + wv, wv < m.nown, nchC, w3);
+    sched_fence();
+  };
+  auto pre_p4 = [&](int l) {
+    const uint16_t *W = reinterpret_cast<const uint16_t *>(layer_ptr(l) + a.o_fk);
+#pragma unroll
+    for (int i = 0; i < RM; ++i) {
+      const int r = m.p4a + wv + kMW * i;
+      load_row<CPL>(W, C, r, r < m.p4b, nchC, w4[i]);
+    }
+    const float *vec = vec_ptr(l);
+    ld_vec(v4w, vec + RWKV7_V_LN2_W * C);
+    ld_vec(v4b, vec + RWKV7_V_LN2_B * C);
+    ld_vec(mu4, vec + RWKV7_V_FFN_X_K * C);
+    ld_vec16(pv4, a.cmix_x + (int64_t)l * C);
+    sched_fence();
+  };
+  auto pre_p5 = [&](int l) {
+    const uint16_t *W = reinterpret_cast<const uint16_t *>(layer_ptr(l) + a.o_fv);
+    load_row<NC5>(W, F, m.owa + wv, wv < m.nown, nchF, w5);
+    sched_fence();
+  };
+  // head rows of this wave: a contiguous range, kHB rows per batch
+  const int hr0 = m.ha + (int)((int64_t)(m.hb - m.ha) * wv / kMW);
+  const int hr1 = m.ha + (int)((int64_t)(m.hb - m.ha) * (wv + 1) / kMW);
+  // Head loads are unconditional (rows and chunks clamped into range, unused
+  // lanes later multiply by a zero input) so that the unrolled head loop issues
+  // a fixed number of loads and the compiler's load counting stays exact.
+  auto pre_head = [&](int b, uint4 (&dst)[kHB][CPL]) {
+#pragma unroll
+    for (int k = 0; k < kHB; ++k) {
+      int r = hr0 + kHB * b + k;
+      r = r < m.hb ? r : m.hb - 1;
+      const uint4 *row = reinterpret_cast<const uint4 *>(a.head + (int64_t)r * C);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const int j = lane + 64 * c;
+        dst[k][c] = ld_stream(row + (j < nchC ? j : nchC - 1));
+      }
+    }
+    sched_fence();
+  };
+  auto count_publish = [&]() {  // this wave's publishes of the stage are issued
+    if (lane == 0) __hip_atomic_fetch_add(s.pubs, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  };
+
+  float xown = 0.f;  // residual of channel owa + wv (waves wv < nown)
+  pre_p1(0);
+  wait_vm0();
+  for (int l = 0; l < L; ++l) {
+    const int ph = 5 * l;
+    // ---------------- P1: LN1 + shift + [r;k;v;LoRA1] ------------------------
+    __syncthreads();  // A1
+    refresh();
+    {
+      const float2 st = wave_ln_stats<2 * CPL>(s.x1, C);
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        const int c = mt + kMT * i;
+        if (c < C) {
+          const float ln = (s.x1[c] - st.x) * st.y * v1w[i] + v1b[i];
+          const float prv = h2f(pv1[i]);
+          s.ln1[c] = ln;
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (q < m.nseg) s.mix[q * C + c] = ln + mu1[q][i] * (prv - ln);
+        }
+      }
+      if (l == 0 && wv < m.nown) xown = s.x1[m.owa + wv];
+    }
+    __syncthreads();  // B1
+    {
+      const unsigned tg = cx.tag(ph);
+#pragma unroll
+      for (int i = 0; i < RM; ++i) {
+        const int r = m.p1a + wv + kMW * i;
+        if (r < m.p1b) {
+          const float d = row_dot<CPL>(w1[i], s.mix + (m.seg_of(r) - m.seg0) * C, nchC);
+          if (lane == 0) publish(a.proj_ex + r, tg, d);
+        }
+      }
+    }
+    count_publish();
+    // every load of the rest of the layer, issued while the head workgroups work
+    refresh();
+    pre_p3(l);
+    pre_p4(l);
+    pre_p5(l);
+    if (l + 1 < L) pre_p1(l + 1);
+    __syncthreads();  // A3
+    wait_vm0();
+    // ---------------- P3: o-projection + residual -----------------------------
+    refresh();
+    if (wv < m.nown) {
+      const float d = row_dot<CPL>(w3, s.core_in, nchC);
+      xown += d;
+      const int c = m.owa + wv;
+      if (lane < kRep) publish(a.x_ex + (int64_t)lane * C + c, cx.tag(ph + 2), xown);
+      // every reader of this layer's time-mix shift state is done (all of P2's inputs arrived)
+      if (lane == kRep) a.tmix_x[(int64_t)l * C + c] = f2h(s.ln1[c]);
+    }
+    count_publish();
+    __syncthreads();  // A4
+    // ---------------- P4: LN2 + shift + FFN key + relu^2 ----------------------
+    refresh();
+    {
+      const float2 st = wave_ln_stats<2 * CPL>(s.x4, C);
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        const int c = mt + kMT * i;
+        if (c < C) {
+          const float ln = (s.x4[c] - st.x) * st.y * v4w[i] + v4b[i];
+          s.ln2[c] = ln;
+          s.mix4[c] = ln + mu4[i] * (h2f(pv4[i]) - ln);
+        }
+      }
+    }
+    __syncthreads();  // B4
+    {
+      const unsigned tg = cx.tag(ph + 3);
+#pragma unroll
+      for (int i = 0; i < RM; ++i) {
+        const int r = m.p4a + wv + kMW * i;
+        if (r < m.p4b) {
+          const float q = fmaxf(row_dot<CPL>(w4[i], s.mix4, nchC), 0.f);
+          if (lane < kRep) publish(a.hid_ex + (int64_t)lane * F + r, tg, q * q);
+        }
+      }
+    }
+    count_publish();
+    __syncthreads();  // A5
+    // ---------------- P5: FFN value + residual --------------------------------
+    refresh();
+    if (wv < m.nown) {
+      const float d = row_dot<NC5>(w5, s.hid, nchF);
+      xown += d;
+      const int c = m.owa + wv;
+      if (lane < kRep) publish(a.x_ex + (int64_t)lane * C + c, cx.tag(ph + 4), xown);
+      if (lane == kRep) a.cmix_x[(int64_t)l * C + c] = f2h(s.ln2[c]);
+    }
+    count_publish();
+  }
+
+  // ---------------- head: ln_out + logits ---------------------------------------
+  refresh();
+#pragma unroll
+  for (int b = 0; b < kHRing; ++b) pre_head(b, wh[b]);
+  ld_vec(hlw, a.ln_out);
+  ld_vec(hlb, a.ln_out + C);
+  __syncthreads();  // AH
+  {
+    const float2 st = wave_ln_stats<2 * CPL>(s.x1, C);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int c = mt + kMT * i;
+      if (c < C) s.mix[c] = (s.x1[c] - st.x) * st.y * hlw[i] + hlb[i];
+    }
+  }
+  __syncthreads();  // BH
+  float xr[CPL][8];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int j = lane + 64 * c;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xr[c][e] = j < nchC ? s.mix[8 * j + e] : 0.f;
+  }
+  float out = 0.f;  // lane k: logit of row hr0 + k
+#pragma unroll
+  for (int b = 0; b < NHB; ++b) {
+    uint4 (&cur)[kHB][CPL] = wh[b % kHRing];
+#pragma unroll
+    for (int k = 0; k < kHB; ++k) {
+      float acc = 0.f;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) acc = dot8r(cur[k][c], xr[c], acc);
+      acc = wave_sum(acc);
+      if (lane == kHB * b + k) out = acc;
+    }
+    if (b + kHRing < NHB) pre_head(b + kHRing, cur);
+  }
+  if (hr0 + lane < hr1) a.logits[hr0 + lane] = f2h(out);
+}
+
+// One workgroup per CU by construction (2 waves per SIMD): telling the
+// compiler so keeps its scheduler from trading prefetch distance for an
+// occupancy this kernel never runs at.
+template <int CPL, int RM, int NC5, int VPL, int NL2, int NJ, int NHB>
+__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_mk_kernel(MkArgs a) {
+  extern __shared__ __align__(16) float smem[];
+  MkGeom m;
+  m.C = a.C;
+  m.F = a.F;
+  m.H = a.H;
+  m.L = a.L;
+  m.SR = a.rv + a.rw + a.ra + a.rg;
+  m.G = gridDim.x;
+  m.g = blockIdx.x;
+  m.head = m.g < m.H;
+  // worker rows: split over the G - H workers
+  const int Gw = m.G - m.H, gw = m.head ? 0 : m.g - m.H;
+  const int N1 = 3 * m.C + m.SR;
+  auto part = [&](int n, int i) { return (int)((int64_t)n * i / Gw); };
+  m.p1a = part(N1, gw);
+  m.p1b = m.head ? m.p1a : part(N1, gw + 1);
+  m.p4a = part(m.F, gw);
+  m.p4b = m.head ? m.p4a : part(m.F, gw + 1);
+  m.owa = part(m.C, gw);
+  m.nown = m.head ? 0 : part(m.C, gw + 1) - m.owa;
+  m.ha = part(a.V, gw);
+  m.hb = m.head ? m.ha : part(a.V, gw + 1);
+  m.e[0] = m.C;
+  m.e[1] = 2 * m.C;
+  m.e[2] = 3 * m.C;
+  m.e[3] = m.e[2] + a.rv;
+  m.e[4] = m.e[3] + a.rw;
+  m.e[5] = m.e[4] + a.ra;
+  m.seg0 = m.seg_of(m.p1a);
+  m.nseg = m.p1b > m.p1a ? m.seg_of(m.p1b - 1) - m.seg0 + 1 : 0;
+  const MkLds s = mk_lds(smem, m.C, m.F, m.SR);
 
   MkCtx cx;
   cx.sync = a.sync;
   cx.epoch = ld_u32(a.sync + SY_EPOCH);
-  cx.nph = 5u * L + 1u;
+  cx.tag0 = cx.epoch * (5u * m.L + 1u) + 1u;
 
-  const int N1 = 3 * C + SR;
-  const int p1a = (int)((int64_t)N1 * g / G), p1b = (int)((int64_t)N1 * (g + 1) / G);
-  const int p4a = (int)((int64_t)F * g / G), p4b = (int)((int64_t)F * (g + 1) / G);
-  const int owa = (int)((int64_t)C * g / G), owb = (int)((int64_t)C * (g + 1) / G);
-  const int nown = owb - owa;
-  const int ks = nown > 0 ? (kW / nown > 0 ? kW / nown : 1) : 1;
-
-  int64_t token = a.tok[0];
-  token = token < 0 ? 0 : token >= a.V ? a.V - 1 : token;
-  const uint16_t *erow = a.emb + token * C;
-  if (t < nown) s_own[t] = h2f(erow[owa + t]);
-
-  // rows of the stacked P1 matrix fall in 7 segments: r, k, v, LoRA v, w, a, g
-  const int e0 = C, e1 = 2 * C, e2 = 3 * C, e3 = e2 + a.rv, e4 = e3 + a.rw, e5 = e4 + a.ra;
-  auto seg_of = [=](int r) {
-    return (r >= e0) + (r >= e1) + (r >= e2) + (r >= e3) + (r >= e4) + (r >= e5);
-  };
-  auto seg_mu = [](int sgm) {  // vector-block index of each segment's mix
-    return sgm == 0 ? RWKV7_V_X_R : sgm == 1 ? RWKV7_V_X_K : sgm <= 3 ? RWKV7_V_X_V
-         : sgm == 4 ? RWKV7_V_X_W : sgm == 5 ? RWKV7_V_X_A : RWKV7_V_X_G;
-  };
-  const int seg0 = seg_of(p1a), nseg = seg_of(p1b - 1) - seg0 + 1;
-
-  // P2 thread roles: 8 threads per channel c2 of the head; thread sub2 takes the
-  // 16-byte chunks sub2, sub2+8, ... of the channel's [v|w|a|g] LoRA row
-  const int c2 = t >> 3, sub2 = t & 7;
-  const int nch2 = SR >> 3;
-  const int b1 = a.rv >> 3, b2 = (a.rv + a.rw) >> 3, b3 = (a.rv + a.rw + a.ra) >> 3;  // gate bounds in chunks
-
-  // ---- prefetched operands (each issued one stage ahead of its use) -----------
-  uint4 w1[RM][CPL];               // P1 rows
-  float ln1w[CPL], ln1b[CPL], prv1[CPL], mu1[4][CPL];
-  uint4 w2[NL2];                   // P2 LoRA second-step chunks
-  float4 S0 = make_float4(0.f, 0.f, 0.f, 0.f), S1 = S0;  // P2 state rows
-  float gv[8];                     // P2 per-channel vectors
-  uint4 w3[NC5];                   // P3 rows
-  uint4 w4[RM][CPL];               // P4 rows
-  float ln2w[CPL], ln2b[CPL], prv2[CPL], mu4[CPL];
-  uint4 w5[NC5];                   // P5 rows
-
-  auto prefetch_p1 = [&](int l) {
-    const char *Lp = a.layers + (int64_t)l * a.lbytes;
-    const float *vec = reinterpret_cast<const float *>(Lp + a.o_vec);
-    load_rows<RM, CPL>(reinterpret_cast<const uint16_t *>(Lp + a.o_rkv), C, p1a, p1b, C, w1);
-    ld_own<CPL>(ln1w, vec + RWKV7_V_LN1_W * C, C);
-    ld_own<CPL>(ln1b, vec + RWKV7_V_LN1_B * C, C);
-    ld_own16<CPL>(prv1, a.tmix_x + (int64_t)l * C, C);
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (q < nseg) ld_own<CPL>(mu1[q], vec + (int64_t)seg_mu(seg0 + q) * C, C);
-  };
-
-  prefetch_p1(0);
-  float xo[CPL];
-  ld_own16<CPL>(xo, erow, C);
-
-  for (int l = 0; l < L; ++l) {
-    const char *Lp = a.layers + (int64_t)l * a.lbytes;
-    const float *vec = reinterpret_cast<const float *>(Lp + a.o_vec);
-    const int ph = 5 * l;
-
-    // ---------------- P1: LN1 + shift + [r;k;v;LoRA1] ------------------------
-    {
-      if (l > 0) poll_own<CPL>(cx, a.x_ex, C, cx.tag(ph - 1), xo);
-      // stage-ahead prefetch: P2 (head workgroups) and P3
-      if (g < H) {
-        const uint4 *row = reinterpret_cast<const uint4 *>(
-            reinterpret_cast<const uint16_t *>(Lp + a.o_l2) + (int64_t)(g * kN + c2) * SR);
-#pragma unroll
-        for (int i = 0; i < NL2; ++i) w2[i] = sub2 + 8 * i < nch2 ? row[sub2 + 8 * i] : make_uint4(0, 0, 0, 0);
-        const float4 *Sp = reinterpret_cast<const float4 *>(
-            a.rnn + (((int64_t)l * H + g) * kN + (t >> 3)) * kN + (t & 7) * 8);
-        S0 = Sp[0];
-        S1 = Sp[1];
-        if (t < 64) {
-          const int ch = g * kN + t;
-          const int idx[8] = {RWKV7_V_V0, RWKV7_V_W0, RWKV7_V_A0, RWKV7_V_K_K,
-                              RWKV7_V_K_A, RWKV7_V_R_K, RWKV7_V_LNX_W, RWKV7_V_LNX_B};
-#pragma unroll
-          for (int j = 0; j < 8; ++j) gv[j] = vec[idx[j] * C + ch];
-        }
-      }
-      ln_own<CPL>(xo, ln1w, ln1b, C, s_red);
-#pragma unroll
-      for (int i = 0; i < CPL; ++i) {
-        const int c = t + kT * i;
-        if (c < C) {
-          s_ln1[c] = xo[i];
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (q < nseg) s_in[q * C + c] = xo[i] + mu1[q][i] * (prv1[i] - xo[i]);
-        }
-      }
-      __syncthreads();
-      const unsigned tg = cx.tag(ph);
-#pragma unroll
-      for (int i = 0; i < RM; ++i) {
-        const int r = p1a + wv + kW * i;
-        if (r >= p1b) break;
-        const float *xs = s_in + (seg_of(r) - seg0) * C;
-        float acc = 0.f;
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-          const int j = lane + 64 * c;
-          if (j < (C >> 3)) acc = dot8(w1[i][c], xs + 8 * j, acc);
-        }
-        acc = wave_sum(acc);
-        if (lane == 0) publish(a.proj_ex + r, tg, acc);
-      }
-      // stage-ahead prefetch: P3 (small; issued here to keep it out of P1's registers)
-      load_split<NC5>(reinterpret_cast<const uint16_t *>(Lp + a.o_o), C, owa, nown, ks, C, w3);
-      // P2 / P3 poll into s_in, which still holds the segment mixes other waves read
-      __syncthreads();
-    }
-
-    // ---------------- P2: per-head core (workgroups 0..H-1) -------------------
-    if (g < H) {
-      const int h = g;
-      poll_vec<2>(cx, a.proj_ex, 192 + SR, cx.tag(ph), s_in, [&](int i) {
-        return i < 192 ? (i >> 6) * C + h * kN + (i & 63) : 3 * C + (i - 192);
-      });
-      for (int i = t; i < SR; i += kT) {
-        float x = s_in[192 + i];
-        if (i >= a.rv && i < a.rv + a.rw) x = tanhf(x);
-        else if (i >= a.rv + a.rw + a.ra) x = sigmoidf_(x);
-        s_lora[i] = x;
-      }
-      __syncthreads();
-      float *s_r = s_core, *s_w = s_core + 64, *s_k = s_core + 128, *s_v = s_core + 192;
-      float *s_a = s_core + 256, *s_b = s_core + 320, *s_g = s_core + 384, *s_y = s_core + 448;
-      {  // LoRA second step from the prefetched chunks; per-gate partial sums joined
-         // across the channel's 8 lanes
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int i = 0; i < NL2; ++i) {
-          const int cj = sub2 + 8 * i;
-          if (cj < nch2) {
-            const float p = dot8(w2[i], s_lora + 8 * cj, 0.f);
-            const int q = (cj >= b1) + (cj >= b2) + (cj >= b3);
-            acc[0] += q == 0 ? p : 0.f;
-            acc[1] += q == 1 ? p : 0.f;
-            acc[2] += q == 2 ? p : 0.f;
-            acc[3] += q == 3 ? p : 0.f;
-          }
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          float v = sum4(acc[q]);
-          v += dpp<kDppHalfMirror>(v);
-          if (sub2 == 0) s_d[q * 64 + c2] = v;
-        }
-      }
-      __syncthreads();
-      if (t < 64) {
-        const float r = s_in[t], k = s_in[64 + t];
-        float v = s_in[128 + t];
-        if (l == 0) {
-          s_vf[t] = v;
-        } else {
-          v = v + sigmoidf_(gv[0] + s_d[t]) * (s_vf[t] - v);
-        }
-        const float w = expf(-sigmoidf_(gv[1] + s_d[64 + t]) / 1.6487212707001282f);
-        const float ag = sigmoidf_(gv[2] + s_d[128 + t]);
-        const float kk = k * gv[3];
-        const float kn = k + gv[4] * (k * ag - k);
-        const float nrm = sqrtf(wave_sum(kk * kk));
-        const float kh = kk / fmaxf(nrm, 1e-12f);
-        const float rk = wave_sum(r * kn * gv[5]);
-        s_r[t] = r; s_w[t] = w; s_k[t] = kn; s_v[t] = v;
-        s_a[t] = kh; s_b[t] = -kh * ag; s_g[t] = s_d[192 + t];
-        if (t == 0) s_red[32] = rk;
-      }
-      __syncthreads();
-      {
-        const int row = t >> 3, j0 = (t & 7) * 8;
-        float Sv[8] = {S0.x, S0.y, S0.z, S0.w, S1.x, S1.y, S1.z, S1.w};
-        float sa = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sa = fmaf(Sv[e], s_a[j0 + e], sa);
-        sa = sum4(sa);
-        sa += dpp<kDppHalfMirror>(sa);
-        const float vi = s_v[row];
-        float y = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int j = j0 + e;
-          Sv[e] = Sv[e] * s_w[j] + sa * s_b[j] + vi * s_k[j];
-          y = fmaf(Sv[e], s_r[j], y);
-        }
-        y = sum4(y);
-        y += dpp<kDppHalfMirror>(y);
-        float4 *Sp = reinterpret_cast<float4 *>(a.rnn + (((int64_t)l * H + h) * kN + row) * kN + j0);
-        Sp[0] = make_float4(Sv[0], Sv[1], Sv[2], Sv[3]);
-        Sp[1] = make_float4(Sv[4], Sv[5], Sv[6], Sv[7]);
-        if ((t & 7) == 0) s_y[row] = y;
-      }
-      __syncthreads();
-      if (t < 64) {
-        const int ch = h * kN + t;
-        const float y = s_y[t];
-        const float mean = wave_sum(y) * (1.f / kN);
-        const float d = y - mean;
-        const float var = wave_sum(d * d) * (1.f / kN);
-        const float yn = d * rsqrtf(var + kGnEps) * gv[6] + gv[7];
-        publish(a.core_ex + ch, cx.tag(ph + 1), (yn + s_red[32] * s_v[t]) * s_g[t]);
-      }
-    }
-
-    // ---------------- P3: o-projection + residual -----------------------------
-    {
-      poll_vec<4>(cx, a.core_ex, C, cx.tag(ph + 1), s_in, Ident());
-      // stage-ahead prefetch: P4
-      load_rows<RM, CPL>(reinterpret_cast<const uint16_t *>(Lp + a.o_fk), C, p4a, p4b, C, w4);
-      ld_own<CPL>(ln2w, vec + RWKV7_V_LN2_W * C, C);
-      ld_own<CPL>(ln2b, vec + RWKV7_V_LN2_B * C, C);
-      ld_own<CPL>(mu4, vec + RWKV7_V_FFN_X_K * C, C);
-      ld_own16<CPL>(prv2, a.cmix_x + (int64_t)l * C, C);
-      const float d = dot_split<NC5>(w3, s_in, nown, ks, C, s_red);
-      const unsigned tg = cx.tag(ph + 2);
-      if (t < nown) {
-        s_own[t] += d;
-        publish(a.x_ex + owa + t, tg, s_own[t]);
-        // every reader of this layer's time-mix shift state is done (all of P2's inputs arrived)
-        a.tmix_x[(int64_t)l * C + owa + t] = f2h(s_ln1[owa + t]);
-      }
-    }
-
-    // ---------------- P4: LN2 + shift + FFN key + relu^2 ----------------------
-    {
-      poll_own<CPL>(cx, a.x_ex, C, cx.tag(ph + 2), xo);
-      // stage-ahead prefetch: P5
-      load_split<NC5>(reinterpret_cast<const uint16_t *>(Lp + a.o_fv), F, owa, nown, ks, F, w5);
-      ln_own<CPL>(xo, ln2w, ln2b, C, s_red);
-#pragma unroll
-      for (int i = 0; i < CPL; ++i) {
-        const int c = t + kT * i;
-        if (c < C) {
-          s_ln2[c] = xo[i];
-          s_x[c] = xo[i] + mu4[i] * (prv2[i] - xo[i]);
-        }
-      }
-      __syncthreads();
-      const unsigned tg = cx.tag(ph + 3);
-#pragma unroll
-      for (int i = 0; i < RM; ++i) {
-        const int r = p4a + wv + kW * i;
-        if (r >= p4b) break;
-        float acc = 0.f;
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-          const int j = lane + 64 * c;
-          if (j < (C >> 3)) acc = dot8(w4[i][c], s_x + 8 * j, acc);
-        }
-        acc = wave_sum(acc);
-        const float q = fmaxf(acc, 0.f);
-        if (lane == 0) publish(a.hid_ex + r, tg, q * q);
-      }
-    }
-
-    // ---------------- P5: FFN value + residual --------------------------------
-    {
-      poll_vec<NPTH>(cx, a.hid_ex, F, cx.tag(ph + 3), s_in, Ident());
-      if (l + 1 < L) prefetch_p1(l + 1);  // stage-ahead prefetch: next layer's P1
-      const float d = dot_split<NC5>(w5, s_in, nown, ks, F, s_red);
-      const unsigned tg = cx.tag(ph + 4);
-      if (t < nown) {
-        s_own[t] += d;
-        publish(a.x_ex + owa + t, tg, s_own[t]);
-        a.cmix_x[(int64_t)l * C + owa + t] = f2h(s_ln2[owa + t]);
-      }
-    }
+  if (threadIdx.x == 0) *s.pubs = 0u;  // ordered before any increment by the first barrier
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (m.head) {
+    if (wv >= kMW) comm_head<NJ>(a, m, s, cx, wv - kMW);
+    else math_head<NL2>(a, m, s, cx, wv);
+  } else {
+    if (wv >= kMW) comm_worker<4 * CPL / kNComm, 2 * NC5 / kNComm>(a, m, s, cx, wv - kMW);
+    else math_worker<CPL, RM, NC5, VPL, NHB>(a, m, s, cx, wv);
   }
-
-  // ---------------- head: ln_out + logits ---------------------------------------
-  {
-    const int ha = (int)((int64_t)a.V * g / G), hb = (int)((int64_t)a.V * (g + 1) / G);
-    float low[CPL], lob[CPL];
-    ld_own<CPL>(low, a.ln_out, C);
-    ld_own<CPL>(lob, a.ln_out + C, C);
-    uint4 wh[4][CPL];
-    auto load_head = [&](int r0) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-          const int j = lane + 64 * c;
-          wh[i][c] = (r0 + i < hb && j < (C >> 3))
-                         ? ld_stream(reinterpret_cast<const uint4 *>(a.head + (int64_t)(r0 + i) * C) + j)
-                         : make_uint4(0, 0, 0, 0);
-        }
-    };
-    load_head(ha + wv * 4);
-    poll_own<CPL>(cx, a.x_ex, C, cx.tag(5 * L - 1), xo);
-    ln_own<CPL>(xo, low, lob, C, s_red);
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const int c = t + kT * i;
-      if (c < C) s_x[c] = xo[i];
-    }
-    __syncthreads();
-    for (int r0 = ha + wv * 4; r0 < hb; r0 += kW * 4) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float acc = 0.f;
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-          const int j = lane + 64 * c;
-          if (j < (C >> 3)) acc = dot8(wh[i][c], s_x + 8 * j, acc);
-        }
-        acc = wave_sum(acc);
-        if (lane == i && r0 + i < hb) a.logits[r0 + i] = f2h(acc);
-      }
-      if (r0 + kW * 4 < hb) load_head(r0 + kW * 4);
-    }
-  }
-  // all workgroups have read the epoch and passed their last wait on it
-  if (g == 0 && t == 0) st_u32(a.sync + SY_EPOCH, cx.epoch + 1u);
+  // A worker ends only after every workgroup has published (its logits need
+  // the last layer's x, which needs every worker's P5 and every head's core),
+  // and every workgroup read the epoch before its first publish.
+  if (m.g == m.H && threadIdx.x == 0) st_u32(a.sync + SY_EPOCH, cx.epoch + 1u);
 }
 
 // ---- host side --------------------------------------------------------------
 
-// Chunks per lane of the K-split P3/P5 rows for workgroup count G.
-static int mk_nc5(const rwkv7_dims &d, int G) {
-  const int C = d.n_embd, F = d.n_ffn;
-  int nown = (C + G - 1) / G;
-  if (nown < 1) nown = 1;
-  const int ks = kW / nown > 0 ? kW / nown : 1;
-  const int per = ((F >> 3) + ks - 1) / ks;
-  return (per + 63) / 64;
-}
+// The one compiled instance: CPL 2, RM 3, NC5 8, VPL 3, NL2 8, NJ 4, NHB 10
+// (NJ: pairs per comm lane of the P2 input vector).
+constexpr int kCPL = 2, kRM = 3, kNC5 = 8, kVPL = 3, kNL2 = 8, kNJ = 4, kNHB = 10;
+#define RWKV7_MK_INSTANCE decode_mk_kernel<kCPL, kRM, kNC5, kVPL, kNL2, kNJ, kNHB>
 
-// Template instance for these sizes: 0 = <2,2,4,8,5>; -1 if none fits.
-static int mk_variant(const rwkv7_dims &d, int G) {
-  const int cpl = ((d.n_embd >> 3) + 63) / 64, nc5 = mk_nc5(d, G), npth = (d.n_ffn + kT - 1) / kT;
-  const int nl2 = ((d.rank_w + d.rank_a + d.rank_v + d.rank_g) / 8 + 7) / 8;  // P2 chunks per thread
-  const int n1 = 3 * d.n_embd + d.rank_w + d.rank_a + d.rank_v + d.rank_g;
-  const int rm = ((n1 + G - 1) / G + kW - 1) / kW > ((d.n_ffn + G - 1) / G + kW - 1) / kW
-                     ? ((n1 + G - 1) / G + kW - 1) / kW
-                     : ((d.n_ffn + G - 1) / G + kW - 1) / kW;
-  if (rm <= 2 && cpl <= 2 && nc5 <= 4 && npth <= 8 && nl2 <= 5) return 0;
-  // The wider instances (n_embd 2048) exceed the register file and spill to
-  // scratch; those models decode one sequence through the GEMV kernels instead.
-  return -1;
-}
+static int cdiv(int a, int b) { return (a + b - 1) / b; }
 
 static int g_cus = 0;
 
@@ -691,29 +926,40 @@ int mk_cus() {
   return g_cus;
 }
 
-int64_t mk_lds_bytes(int C, int F, int SR) {
-  const int nin = mk_nin(C, F, SR);
-  return (int64_t)(4 * C + nin + 64 + 16 + 64 + 8 * 64 + 512 + 256) * 4;
-}
+static int64_t mk_lds_bytes(int C, int F, int SR) { return mk_lds_floats(C, F, SR) * 4; }
 
-// Exchange region: sync words, then x (C), proj (3C+SR), core (C), hid (F) as u64.
+// Exchange region: sync words, then x (kRep x C), proj (3C+SR), core
+// (kRep x C), hid (kRep x F) as u64.
 int64_t mk_exchange_bytes(int C, int F, int SR) {
-  return 256 + (int64_t)(C + 3 * C + SR + C + F) * 8;
+  return 256 + (int64_t)(kRep * C + 3 * C + SR + kRep * C + kRep * F) * 8;
 }
-
 
 bool mk_supported(const rwkv7_dims &d, int G) {
-  const int C = d.n_embd, F = d.n_ffn, SR = d.rank_w + d.rank_a + d.rank_v + d.rank_g;
-  if (G < 1) return false;
+  const int C = d.n_embd, F = d.n_ffn, H = d.n_head, V = d.vocab;
+  const int SR = d.rank_w + d.rank_a + d.rank_v + d.rank_g;
+  const int Gw = G - H;  // worker workgroups
+  if (C != H * kN || Gw < 1) return false;
   const int N1 = 3 * C + SR;
-  const int c8 = C >> 3;
-  if (C > 2048 || (c8 + 63) / 64 > 4) return false;
-  if ((N1 + G - 1) / G > kRMax * kW || (F + G - 1) / G > kRMax * kW) return false;
-  if ((C + G - 1) / G > 16) return false;
-  if (mk_variant(d, G) < 0) return false;
-  if (F > 8192 || 192 + SR > 8192) return false;
-
-  // P1 keeps the mixed input of every row segment a workgroup touches (<= 4)
+  // every worker owns at least one residual channel and one P1 row, so each
+  // worker's end implies every workgroup has published
+  if (C < Gw || N1 < Gw || F < Gw || V < Gw) return false;
+  if (cdiv(C >> 3, 64) > kCPL || cdiv(F >> 3, 64) > kNC5) return false;
+  if (cdiv(cdiv(N1, Gw), kMW) > kRM || cdiv(cdiv(F, Gw), kMW) > kRM) return false;
+  if (cdiv(C, Gw) > kMW) return false;  // one residual channel per math wave
+  if (cdiv(C, kMT) > kVPL) return false;
+  // P2 parts (v, w, a, two halves of g), at most kNL2 chunks each, one wave each
+  {
+    const int cv = d.rank_v >> 3, cw = d.rank_w >> 3, ca = d.rank_a >> 3, cg = d.rank_g >> 3;
+    if (cv > kNL2 || cw > kNL2 || ca > kNL2 || (cg + 1) / 2 > kNL2 || kMW < 5) return false;
+  }
+  const int cj = 2 * 64 * kNComm;  // words per round: one pair per lane and slot
+  if (cdiv(C, cj) > 4 * kCPL / kNComm || cdiv(F / 2, cj) > 2 * kNC5 / kNComm || cdiv(192 + SR, cj) > kNJ)
+    return false;
+  if (F % 512) return false;  // halves of the hidden vector in whole 16-byte pairs per lane round
+  if (H > 64 * kNComm) return false;  // one probe lane per head
+  const int hrows = cdiv(cdiv(V, Gw), kMW);
+  if (hrows > kHB * kNHB || hrows > 64) return false;
+  // P1 keeps the mixed input of every row segment a worker touches (<= 4)
   const int e[6] = {C, 2 * C, 3 * C, 3 * C + d.rank_v, 3 * C + d.rank_v + d.rank_w,
                     3 * C + d.rank_v + d.rank_w + d.rank_a};
   auto seg = [&](int r) {
@@ -721,9 +967,9 @@ bool mk_supported(const rwkv7_dims &d, int G) {
     for (int i = 0; i < 6; ++i) s += r >= e[i];
     return s;
   };
-  for (int g = 0; g < G; ++g) {
-    const int r0 = (int)((int64_t)N1 * g / G), r1 = (int)((int64_t)N1 * (g + 1) / G);
-    if (r1 <= r0 || seg(r1 - 1) - seg(r0) + 1 > 4) return false;
+  for (int g = 0; g < Gw; ++g) {
+    const int r0 = (int)((int64_t)N1 * g / Gw), r1 = (int)((int64_t)N1 * (g + 1) / Gw);
+    if (seg(r1 - 1) - seg(r0) + 1 > 4) return false;
   }
   return mk_lds_bytes(C, F, SR) <= 160 * 1024;
 }
@@ -734,6 +980,7 @@ int launch_decode_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const 
   const int SR = d.rank_w + d.rank_a + d.rank_v + d.rank_g;
   const int G = mk_cus();
   const int C = d.n_embd, F = d.n_ffn;
+  if (!mk_supported(d, G)) return RWKV7_ESHAPE;
   MkArgs a;
   a.layers = static_cast<const char *>(m.layers);
   a.lbytes = lay.bytes;
@@ -763,20 +1010,18 @@ int launch_decode_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const 
   a.sync = reinterpret_cast<unsigned *>(xreg);
   uint64_t *ex = reinterpret_cast<uint64_t *>(xreg + 256);
   a.x_ex = ex;
-  a.proj_ex = a.x_ex + C;
+  a.proj_ex = a.x_ex + (int64_t)kRep * C;
   a.core_ex = a.proj_ex + 3 * C + SR;
-  a.hid_ex = a.core_ex + C;
+  a.hid_ex = a.core_ex + (int64_t)kRep * C;
   const int64_t lds = mk_lds_bytes(C, F, SR);
-  const int variant = mk_variant(d, G);
-  const void *fn = (const void *)decode_mk_kernel<2, 2, 4, 8, 5>;
-  if (variant < 0) return RWKV7_ESHAPE;
+  const void *fn = (const void *)RWKV7_MK_INSTANCE;
   static int64_t lds_set = 0;  // largest dynamic LDS size already allowed
   if (lds > lds_set) {
     if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
       return RWKV7_ELAUNCH;
     lds_set = lds;
   }
-  decode_mk_kernel<2, 2, 4, 8, 5><<<G, kT, lds, st>>>(a);
+  RWKV7_MK_INSTANCE<<<G, kT, lds, st>>>(a);
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;
 }
