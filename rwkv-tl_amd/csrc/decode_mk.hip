@@ -632,18 +632,22 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
 
   auto layer_ptr = [&](int l) { return a.layers + (int64_t)l * a.lbytes; };
   auto vec_ptr = [&](int l) { return reinterpret_cast<const float *>(layer_ptr(l) + a.o_vec); };
+  // Vector loads are unconditional (index clamped; elements past C are never
+  // used): a load under a branch makes the compiler wait for it inside the
+  // branch (converting it there, or at the join), which stalls the prefetch
+  // behind every load issued before it.
   auto ld_vec = [&](float (&d)[VPL], const float *src) {
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int c = mt + kMT * i;
-      d[i] = c < C ? src[c] : 0.f;
+      d[i] = src[c < C ? c : C - 1];
     }
   };
   auto ld_vec16 = [&](uint16_t (&d)[VPL], const uint16_t *src) {
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int c = mt + kMT * i;
-      d[i] = c < C ? src[c] : (uint16_t)0;
+      d[i] = src[c < C ? c : C - 1];
     }
   };
   auto pre_p1 = [&](int l) {
@@ -809,10 +813,10 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
 
   // ---------------- head: ln_out + logits ---------------------------------------
   refresh();
-#pragma unroll
-  for (int b = 0; b < kHRing; ++b) pre_head(b, wh[b]);
   ld_vec(hlw, a.ln_out);
   ld_vec(hlb, a.ln_out + C);
+#pragma unroll
+  for (int b = 0; b < kHRing; ++b) pre_head(b, wh[b]);
   __syncthreads();  // AH
   {
     const float2 st = wave_ln_stats<2 * CPL>(s.x1, C);

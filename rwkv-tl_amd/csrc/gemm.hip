@@ -5,14 +5,24 @@
 // K-contiguous, which is what v_mfma_f32_16x16x32_f16 wants in every lane
 // (8 consecutive k of one row). Accumulation is fp32.
 //
-// Workgroup tile BM x 64, 4 waves; wave w owns output columns [16w, 16w+16)
-// and all BM rows (BM/16 accumulators). The A tile (BM x 32 per k-step) is
-// staged in LDS and shared by the 4 waves; each wave reads its W fragment
-// straight from global memory (each weight byte is used by exactly one wave).
-// Both are double-buffered in registers one k-step ahead.
+// At the sizes of prefill and batched decode (M = B*T up to a few hundred) the
+// product is bound by streaming W from HBM, so the kernel is built around
+// keeping many weight loads in flight on every CU:
+//   * workgroup tile: BM rows x 64 columns; wave w owns columns [16w, 16w+16)
+//     and all BM rows (BM/16 accumulators);
+//   * each wave streams its 16-row strip of W straight into registers, a chunk
+//     (4 k-steps of 32) ahead of its use, double-buffered in registers;
+//   * the A tile is staged through LDS in chunks of 128 k, double-buffered, and
+//     shared by the 4 waves;
+//   * split-K: when the tiles alone cannot fill the GPU (N = 1024 at small M
+//     gives 16 tiles), the K range of each tile is split over S workgroups
+//     (S a power of two). Each writes its fp32 partial tile to the workspace;
+//     the last of the S to finish (a per-tile arrival counter, reset by that
+//     workgroup) sums the S partials in split order, so the result does not
+//     depend on which workgroup came last, and applies the epilogue.
 //
-// One launch runs a group of up to 8 problems that share M (the r/k/v
-// projections and the four LoRA first steps of one layer, for instance).
+// One launch runs a group of up to 8 problems that share M and A's rows (the
+// r/k/v projections and the four LoRA first steps of one layer, for instance).
 // Reference counterparts: fused_rkv_gemm, ffn_h, ffn_v, out_mm
 // (src/rwkv_tl/kernels/gemm.py:215-305) and the torch LoRA matmuls of prefill
 // (demo/_rwkv7_base.py:243-269).
@@ -20,142 +30,299 @@
 
 namespace rwkv7 {
 
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int kMaxProb = 8;
+constexpr int kBN = 64;       // columns per workgroup tile
+constexpr int kKC = 128;      // k per staged A chunk (4 k-steps)
+constexpr int kLdsPadH = 8;   // halves of padding per A row in LDS
+constexpr int kMaxSplit = 16;
 
 struct GemmGroup {
   GemmProb p[kMaxProb];
-  int tile_begin[kMaxProb + 1];
+  int wg_begin[kMaxProb + 1];  // first workgroup of each problem
+  int splits[kMaxProb];        // S of each problem
+  int kslice[kMaxProb];        // k per split (multiple of kKC)
+  int64_t part_off[kMaxProb];  // floats into part
+  int ctr_off[kMaxProb];       // counters into ctr
   int nprob, M, m_tiles;
+  float *part;
+  unsigned *ctr;
 };
 
-constexpr int kBN = 64, kBK = 32, kLdsPad = 8;
+RWKV7_DEV void store_epi(const GemmProb &P, int row, int col, float v) {
+  const int64_t o = (int64_t)row * P.ldy + col;
+  switch (P.epi) {
+    case GEPI_F32: reinterpret_cast<float *>(P.Y)[o] = v; break;
+    case GEPI_F16: reinterpret_cast<uint16_t *>(P.Y)[o] = f2h(v); break;
+    case GEPI_RELUSQ: {
+      const float q = fmaxf(v, 0.f);
+      reinterpret_cast<uint16_t *>(P.Y)[o] = f2h(q * q);
+      break;
+    }
+    case GEPI_ADD_F32: reinterpret_cast<float *>(P.Y)[o] += v; break;
+    case GEPI_TANH_F16: reinterpret_cast<uint16_t *>(P.Y)[o] = f2h(tanhf(v)); break;
+    default: reinterpret_cast<uint16_t *>(P.Y)[o] = f2h(sigmoidf_(v)); break;
+  }
+}
 
 template <int BM>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
-  __shared__ uint4 s_a[2][BM][(kBK + kLdsPad) / 8];
+  constexpr int MB = BM / 16;                // 16-row blocks
+  constexpr int kRowH = kKC + kLdsPadH;      // halves per LDS row
+  constexpr int kAPer = BM * (kKC / 8) / 256;  // 16-byte A pieces per thread per chunk
+  __shared__ __align__(16) uint16_t s_a[2][BM][kRowH];
+  __shared__ int s_last;
 
-  int bx = blockIdx.x, pi = 0;
+  const int bx = blockIdx.x;
+  int pi = 0;
 #pragma unroll
-  for (int i = 1; i < kMaxProb; ++i) pi += (i < g.nprob && bx >= g.tile_begin[i]);
+  for (int i = 1; i < kMaxProb; ++i) pi += (i < g.nprob && bx >= g.wg_begin[i]);
   const GemmProb &P = g.p[pi];
-  const int local = bx - g.tile_begin[pi];
-  const int mt = local % g.m_tiles, nt = local / g.m_tiles;
+  const int S = g.splits[pi];
+  const int local = bx - g.wg_begin[pi];
+  const int split = local & (S - 1), tile = local / S;
+  const int mt = tile % g.m_tiles, nt = tile / g.m_tiles;
   const int m0 = mt * BM, n0 = nt * kBN;
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const int M = g.M, N = P.N, K = P.K;
+  const int kb = split * g.kslice[pi];
+  const int ke = min(K, kb + g.kslice[pi]);
+  // chunks of this split, padded to even (the chunk loop is unrolled by two so
+  // the register double buffers have fixed names); padding chunks are skipped
+  const int nch = (ke - kb + kKC - 1) / kKC;
+  const int nch2 = (nch + 1) & ~1;
 
-  // A tile loader: BM rows x 4 chunks of 8 halfs.
-  constexpr int kAChunks = BM * 4;
-  constexpr int kAPer = (kAChunks + 255) / 256;
+  // A staging: piece idx -> row idx >> 4, 16-byte column idx & 15. Loads are
+  // unconditional (row and k clamped into range) and masked after arrival, so
+  // the compiler can count outstanding loads exactly.
   uint4 a_reg[kAPer];
-  auto load_a = [&](int k0) {
+  auto load_a = [&](int c) {
+    const int k0 = kb + c * kKC;
 #pragma unroll
     for (int u = 0; u < kAPer; ++u) {
       const int idx = t + 256 * u;
-      const int r = idx >> 2, kc = (idx & 3) * 8;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (idx < kAChunks && m0 + r < M && k0 + kc < K)
-        v = *reinterpret_cast<const uint4 *>(P.A + (int64_t)(m0 + r) * P.lda + k0 + kc);
-      a_reg[u] = v;
+      const int r = m0 + (idx >> 4), k = k0 + 8 * (idx & 15);
+      const int rc = r < M ? r : M - 1, kc = k < K - 8 ? k : K - 8;
+      a_reg[u] = *reinterpret_cast<const uint4 *>(P.A + (int64_t)rc * P.lda + kc);
     }
   };
-  auto store_a = [&](int buf) {
+  auto store_a = [&](int c, int buf) {
+    const int k0 = kb + c * kKC;
 #pragma unroll
     for (int u = 0; u < kAPer; ++u) {
       const int idx = t + 256 * u;
-      if (idx < kAChunks) s_a[buf][idx >> 2][idx & 3] = a_reg[u];
+      const int r = m0 + (idx >> 4), k = k0 + 8 * (idx & 15);
+      const uint4 v = (r < M && k < ke) ? a_reg[u] : make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4 *>(&s_a[buf][idx >> 4][8 * (idx & 15)]) = v;
     }
   };
-  // W fragment: lane -> row n0 + 16 wv + (lane & 15), k-chunk (lane >> 4).
+  // W fragment of k-step j of chunk c: lane -> row n0 + 16 wv + (lane & 15),
+  // 8 k at 32 j + 8 (lane >> 4) (clamped into range; out-of-range k meets a
+  // zero A and out-of-range rows are never stored).
   const int wn = n0 + wv * 16 + (lane & 15);
-  const uint16_t *wrow = P.W + (int64_t)(wn < N ? wn : 0) * P.ldw + (lane >> 4) * 8;
-  auto load_w = [&](int k0) -> uint4 {
-    if (wn < N && k0 + (lane >> 4) * 8 < K) return ld_stream(reinterpret_cast<const uint4 *>(wrow + k0));
-    return make_uint4(0, 0, 0, 0);
+  const uint16_t *wrow = P.W + (int64_t)(wn < N ? wn : N - 1) * P.ldw;
+  auto load_w = [&](int c, uint4 (&dst)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = kb + c * kKC + 32 * j + 8 * (lane >> 4);
+      dst[j] = ld_stream(reinterpret_cast<const uint4 *>(wrow + (k < K - 8 ? k : K - 8)));
+    }
   };
 
-  floatx4 acc[BM / 16];
+  floatx4 acc[MB];
 #pragma unroll
-  for (int i = 0; i < BM / 16; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < MB; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  load_a(0);
-  uint4 w_cur = load_w(0);
-  store_a(0);
-  __syncthreads();
-  const int nk = (K + kBK - 1) / kBK;
-  for (int ks = 0; ks < nk; ++ks) {
-    const int buf = ks & 1;
-    uint4 w_next = make_uint4(0, 0, 0, 0);
-    if (ks + 1 < nk) {
-      load_a((ks + 1) * kBK);
-      w_next = load_w((ks + 1) * kBK);
-    }
-    const half8 bfrag = __builtin_bit_cast(half8, w_cur);
+  auto compute = [&](int buf, const uint4 (&w)[4]) {
 #pragma unroll
-    for (int mb = 0; mb < BM / 16; ++mb) {
-      const half8 afrag = __builtin_bit_cast(half8, s_a[buf][mb * 16 + (lane & 15)][lane >> 4]);
-      acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag, bfrag, acc[mb], 0, 0, 0);
+    for (int j = 0; j < 4; ++j) {
+      const half8 bfrag = __builtin_bit_cast(half8, w[j]);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const half8 afrag = __builtin_bit_cast(
+            half8, *reinterpret_cast<const uint4 *>(&s_a[buf][mb * 16 + (lane & 15)][32 * j + 8 * (lane >> 4)]));
+        acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag, bfrag, acc[mb], 0, 0, 0);
+      }
     }
-    if (ks + 1 < nk) store_a(buf ^ 1);
-    w_cur = w_next;
+  };
+
+  uint4 w0[4], w1[4];
+  load_a(0);
+  load_w(0, w0);
+  load_w(1, w1);
+  store_a(0, 0);
+  __syncthreads();
+  for (int c = 0; c < nch2; c += 2) {
+    // chunk c (A in buffer 0, W in w0)
+    load_a(c + 1);
+    if (c < nch) compute(0, w0);
+    load_w(c + 2, w0);
+    store_a(c + 1, 1);
+    __syncthreads();
+    // chunk c + 1 (A in buffer 1, W in w1)
+    load_a(c + 2);
+    if (c + 1 < nch) compute(1, w1);
+    load_w(c + 3, w1);
+    store_a(c + 2, 0);
     __syncthreads();
   }
 
   // Epilogue: lane holds rows 4 * (lane >> 4) + {0..3} of column (lane & 15).
   const int col = n0 + wv * 16 + (lane & 15);
+  if (S > 1) {
+    // Partials go out with device-scope (sc1) stores, which complete only once
+    // visible to every CU; each wave waits for its own (an asm with a memory
+    // clobber, so the compiler keeps every store before it), then one thread
+    // counts the workgroup in. The last workgroup reads them with device-scope
+    // loads. No cache write-back or invalidation is involved.
+    float *pbase = g.part + g.part_off[pi] + (int64_t)tile * S * 4 * MB * 256;
+    const int nbytes = S * 4 * MB * 256 * 4;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(pbase, 0, nbytes, 0x00020000);
+    const int my = ((split * 4 + wv) * MB * 64 + lane) * 16;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[mb]), rs, my + mb * 64 * 16, 0, 16);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t == 0) {
+      unsigned *ctr = g.ctr + g.ctr_off[pi] + tile;
+      const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = old == (unsigned)(S - 1);
+      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    // NB splits per batch of loads (16 float4 per lane in flight), summed in
+    // split order; indices past S are clamped and their values dropped
+    constexpr int NB = MB >= 16 ? 1 : 16 / MB;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < S; s0 += NB) {
+      floatx4 q[NB][MB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int sp = s0 + b < S ? s0 + b : S - 1;
+        const int at = ((sp * 4 + wv) * MB * 64 + lane) * 16;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          q[b][mb] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, at + mb * 64 * 16, 0, 16));
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const bool use = s0 + b < S;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[mb] += use ? q[b][mb] : floatx4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  }
   if (col >= N) return;
 #pragma unroll
-  for (int mb = 0; mb < BM / 16; ++mb) {
+  for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = m0 + mb * 16 + (lane >> 4) * 4 + r;
-      if (row >= M) continue;
-      const float v = acc[mb][r];
-      const int64_t o = (int64_t)row * P.ldy + col;
-      switch (P.epi) {
-        case GEPI_F32: reinterpret_cast<float *>(P.Y)[o] = v; break;
-        case GEPI_F16: reinterpret_cast<uint16_t *>(P.Y)[o] = f2h(v); break;
-        case GEPI_RELUSQ: {
-          const float q = fmaxf(v, 0.f);
-          reinterpret_cast<uint16_t *>(P.Y)[o] = f2h(q * q);
-          break;
-        }
-        case GEPI_ADD_F32: reinterpret_cast<float *>(P.Y)[o] += v; break;
-        case GEPI_TANH_F16: reinterpret_cast<uint16_t *>(P.Y)[o] = f2h(tanhf(v)); break;
-        default: reinterpret_cast<uint16_t *>(P.Y)[o] = f2h(sigmoidf_(v)); break;
-      }
+      if (row < M) store_epi(P, row, col, acc[mb][r]);
     }
   }
 }
 
-// Checks shapes and launches one group. Every problem needs K % 8 == 0 and
-// 16-byte aligned rows (lda, ldw multiples of 8).
-int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st) {
+static int bm_for(int M) { return M <= 16 ? 16 : M <= 32 ? 32 : M <= 64 ? 64 : 128; }
+
+static int pow2_floor(int x) {
+  int p = 1;
+  while (p * 2 <= x) p *= 2;
+  return p;
+}
+
+// Splits of every problem of a group: none when the tiles already cover the
+// GPU, else enough to reach about two workgroups per CU, each split keeping at
+// least one 128-wide chunk of K and the partial tiles of a problem (written
+// and read once) no larger than its weights.
+static void plan_splits(const GemmProb *probs, int nprob, int M, int cus, bool can_split, int *S, int *kslice) {
+  const int BM = bm_for(M);
+  const int m_tiles = (M + BM - 1) / BM;
+  int tiles = 0;
+  for (int i = 0; i < nprob; ++i) tiles += m_tiles * ((probs[i].N + kBN - 1) / kBN);
+  int want = 1;
+  if (can_split && tiles < cus) {
+    want = 1;
+    while (want < kMaxSplit && tiles * want < 2 * cus) want *= 2;
+  }
+  for (int i = 0; i < nprob; ++i) {
+    const int K = probs[i].K;
+    const int64_t ti = (int64_t)m_tiles * ((probs[i].N + kBN - 1) / kBN);
+    const int64_t wbytes = (int64_t)probs[i].N * K * 2, pbytes = ti * BM * kBN * 4;
+    int maxs = pow2_floor(K >= kKC ? K / kKC : 1);
+    const int maxt = pow2_floor((int)(wbytes / pbytes > 1 ? (wbytes / pbytes > kMaxSplit ? kMaxSplit : wbytes / pbytes) : 1));
+    maxs = maxs < maxt ? maxs : maxt;
+    const int s = want < maxs ? want : maxs;
+    S[i] = s;
+    kslice[i] = ((K + s - 1) / s + kKC - 1) / kKC * kKC;
+  }
+}
+
+int64_t gemm_ws_bytes(int M, int cus) {
+  // at most 2 * cus * 2 workgroups carry a partial tile (tiles < cus, splits
+  // chosen to reach < 4 * cus), BM x 64 floats each
+  const int64_t part = (int64_t)4 * cus * bm_for(M) * kBN * 4;
+  return part;
+}
+
+// Checks shapes and launches one group. Every problem needs K % 8 == 0, K >= 8
+// and 16-byte aligned rows (lda, ldw multiples of 8). part/ctr: split-K
+// workspace (gemm_ws_bytes(M) bytes and kGemmCounters zeroed counters); with
+// part == nullptr no problem is split.
+int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, float *part, unsigned *ctr) {
   if (nprob < 1 || nprob > kMaxProb || M <= 0) return RWKV7_ESHAPE;
+  const int cus = mk_cus();
+  if (cus <= 0) return RWKV7_ELAUNCH;
   GemmGroup g;
-  const int BM = M <= 16 ? 16 : M <= 32 ? 32 : M <= 64 ? 64 : 128;
+  const int BM = bm_for(M);
   g.M = M;
   g.m_tiles = (M + BM - 1) / BM;
   g.nprob = nprob;
-  int tiles = 0;
+  g.part = part;
+  g.ctr = ctr;
+  int S[kMaxProb], ks[kMaxProb];
+  for (int i = 0; i < nprob; ++i) {
+    const GemmProb &p = probs[i];
+    if (p.K < 8 || p.N <= 0 || p.K % 8 || p.lda % 8 || p.ldw % 8) return RWKV7_ESHAPE;
+    if (!p.A || !p.W || !p.Y) return RWKV7_EINVAL;
+  }
+  plan_splits(probs, nprob, M, cus, part != nullptr && ctr != nullptr, S, ks);
+  int wgs = 0, ctrs = 0;
+  int64_t pfl = 0;
   for (int i = 0; i < kMaxProb; ++i) {
-    g.tile_begin[i] = tiles;
+    g.wg_begin[i] = wgs;
     if (i < nprob) {
-      const GemmProb &p = probs[i];
-      if (p.K <= 0 || p.N <= 0 || p.K % 8 || p.lda % 8 || p.ldw % 8) return RWKV7_ESHAPE;
-      if (!p.A || !p.W || !p.Y) return RWKV7_EINVAL;
-      g.p[i] = p;
-      tiles += g.m_tiles * ((p.N + kBN - 1) / kBN);
+      const int tiles = g.m_tiles * ((probs[i].N + kBN - 1) / kBN);
+      g.p[i] = probs[i];
+      g.splits[i] = S[i];
+      g.kslice[i] = ks[i];
+      g.part_off[i] = pfl;
+      g.ctr_off[i] = ctrs;
+      wgs += tiles * S[i];
+      if (S[i] > 1) {
+        pfl += (int64_t)tiles * S[i] * BM * kBN;
+        ctrs += tiles;
+      }
     } else {
       g.p[i] = probs[0];
+      g.splits[i] = 1;
+      g.kslice[i] = kKC;
+      g.part_off[i] = 0;
+      g.ctr_off[i] = 0;
     }
   }
-  g.tile_begin[kMaxProb] = tiles;
+  g.wg_begin[kMaxProb] = wgs;
+  if (pfl * 4 > gemm_ws_bytes(M, cus) || ctrs > kGemmCounters) return RWKV7_EWORKSPACE;
   switch (BM) {
-    case 16: gemm_kernel<16><<<tiles, 256, 0, st>>>(g); break;
-    case 32: gemm_kernel<32><<<tiles, 256, 0, st>>>(g); break;
-    case 64: gemm_kernel<64><<<tiles, 256, 0, st>>>(g); break;
-    default: gemm_kernel<128><<<tiles, 256, 0, st>>>(g); break;
+    case 16: gemm_kernel<16><<<wgs, 256, 0, st>>>(g); break;
+    case 32: gemm_kernel<32><<<wgs, 256, 0, st>>>(g); break;
+    case 64: gemm_kernel<64><<<wgs, 256, 0, st>>>(g); break;
+    default: gemm_kernel<128><<<wgs, 256, 0, st>>>(g); break;
   }
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;

@@ -59,10 +59,18 @@ struct DecodeWs {
 static int64_t exchange_bytes(const rwkv7_dims &d) {
   return align256(mk_exchange_bytes(d.n_embd, d.n_ffn, sum_ranks(d)));
 }
+// Then the GEMM split-K arrival counters (zero between launches), then the
+// path's own buffers.
+static unsigned *gemm_counters(const rwkv7_dims &d, char *base) {
+  return reinterpret_cast<unsigned *>(base + exchange_bytes(d));
+}
+static int64_t fixed_bytes(const rwkv7_dims &d) {
+  return exchange_bytes(d) + align256((int64_t)kGemmCounters * 4);
+}
 
 static int64_t decode_ws(const rwkv7_dims &d, char *base, DecodeWs *w) {
   const int64_t C = d.n_embd, F = d.n_ffn, SR = sum_ranks(d);
-  int64_t off = exchange_bytes(d);
+  int64_t off = fixed_bytes(d);
   auto take = [&](int64_t bytes) {
     char *p = base ? base + off : nullptr;
     off = align256(off + bytes);
@@ -82,12 +90,12 @@ static int64_t decode_ws(const rwkv7_dims &d, char *base, DecodeWs *w) {
 
 // Workspace of the batched path (M = B * T rows).
 struct BatchWs {
-  float *x0, *rkv, *d, *vfirst, *wkab, *y;
+  float *x0, *rkv, *d, *vfirst, *wkab, *y, *part;
   uint16_t *xmix, *l1, *yg, *hid, *headin;
 };
 static int64_t batch_ws(const rwkv7_dims &d, int64_t B, int64_t T, char *base, BatchWs *w) {
   const int64_t C = d.n_embd, F = d.n_ffn, SR = sum_ranks(d), M = B * T;
-  int64_t off = exchange_bytes(d);
+  int64_t off = fixed_bytes(d);
   auto take = [&](int64_t bytes) {
     char *p = base ? base + off : nullptr;
     off = align256(off + bytes);
@@ -105,6 +113,8 @@ static int64_t batch_ws(const rwkv7_dims &d, int64_t B, int64_t T, char *base, B
   t.yg = reinterpret_cast<uint16_t *>(take(M * C * 2));
   t.hid = reinterpret_cast<uint16_t *>(take(M * F * 2));
   t.headin = reinterpret_cast<uint16_t *>(take(B * C * 2));
+  const int cus = mk_cus();
+  t.part = reinterpret_cast<float *>(take(gemm_ws_bytes((int)(M > B ? M : B), cus > 0 ? cus : 256)));
   if (w) *w = t;
   return off;
 }
@@ -234,6 +244,7 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
   layout_of(d, &lay);
   BatchWs w;
   batch_ws(d, B, T, ws, &w);
+  unsigned *ctr = gemm_counters(d, ws);
   RWKV7_TRY(launch_embed(tok, static_cast<const uint16_t *>(m.emb), w.x0, M, C, d.vocab, st));
   for (int l = 0; l < d.n_layer; ++l) {
     const char *L = static_cast<const char *>(m.layers) + (int64_t)l * lay.bytes;
@@ -259,14 +270,14 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
         {xa, wl1 + (int64_t)(rv + rw) * C, w.l1 + rv + rw, C, C, SR, ra, C, GEPI_F16},
         {xg, wl1 + (int64_t)(rv + rw + ra) * C, w.l1 + rv + rw + ra, C, C, SR, rg, C, GEPI_SIGM_F16},
     };
-    RWKV7_TRY(launch_gemm_group(g1, 7, M, st));
+    RWKV7_TRY(launch_gemm_group(g1, 7, M, st, w.part, ctr));
     GemmProb g2[4] = {
         {w.l1, wl2, w.d, SR, SR, C, C, rv, GEPI_F32},
         {w.l1 + rv, wl2 + rv, w.d + MC, SR, SR, C, C, rw, GEPI_F32},
         {w.l1 + rv + rw, wl2 + rv + rw, w.d + 2 * MC, SR, SR, C, C, ra, GEPI_F32},
         {w.l1 + rv + rw + ra, wl2 + rv + rw + ra, w.d + 3 * MC, SR, SR, C, C, rg, GEPI_F32},
     };
-    RWKV7_TRY(launch_gemm_group(g2, 4, M, st));
+    RWKV7_TRY(launch_gemm_group(g2, 4, M, st, w.part, ctr));
     GatesArgs ga = {w.rkv, w.d, vec, w.vfirst, w.wkab, C, M, l == 0};
     RWKV7_TRY(launch_tmix_gates(ga, st));
     ScanArgs<float, float, float> sc = {rnn,           w.rkv,         w.wkab + MC, w.wkab + 2 * MC,
@@ -276,21 +287,21 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
     GnGateArgs gn = {w.y, w.rkv, w.wkab + MC, w.wkab + 2 * MC, w.d + 3 * MC, vec, w.yg, C, M};
     RWKV7_TRY(launch_gn_gate(gn, st));
     GemmProb go = {w.yg, reinterpret_cast<const uint16_t *>(L + lay.w_o), w.x0, C, C, C, C, C, GEPI_ADD_F32};
-    RWKV7_TRY(launch_gemm_group(&go, 1, M, st));
+    RWKV7_TRY(launch_gemm_group(&go, 1, M, st, w.part, ctr));
 
     LnShiftArgs lc = {w.x0, vec + RWKV7_V_LN2_W * C, vec + RWKV7_V_LN2_B * C, vec + RWKV7_V_FFN_X_K * C,
                       1, w.xmix, cshift, C, T, M};
     RWKV7_TRY(launch_ln_shift(lc, st));
     GemmProb gk = {w.xmix, reinterpret_cast<const uint16_t *>(L + lay.w_fk), w.hid, C, C, F, F, C, GEPI_RELUSQ};
-    RWKV7_TRY(launch_gemm_group(&gk, 1, M, st));
+    RWKV7_TRY(launch_gemm_group(&gk, 1, M, st, w.part, ctr));
     GemmProb gv = {w.hid, reinterpret_cast<const uint16_t *>(L + lay.w_fv), w.x0, F, F, C, C, F, GEPI_ADD_F32};
-    RWKV7_TRY(launch_gemm_group(&gv, 1, M, st));
+    RWKV7_TRY(launch_gemm_group(&gv, 1, M, st, w.part, ctr));
   }
   if (logits) {
     const float *lo = static_cast<const float *>(m.ln_out);
     RWKV7_TRY(launch_ln_rows(w.x0, 1, lo, lo + C, w.headin, 0, B, C, T, T - 1, st));
     GemmProb gh = {w.headin, static_cast<const uint16_t *>(m.head), logits, C, C, d.vocab, d.vocab, C, GEPI_F16};
-    RWKV7_TRY(launch_gemm_group(&gh, 1, B, st));
+    RWKV7_TRY(launch_gemm_group(&gh, 1, B, st, w.part, ctr));
   }
   return RWKV7_OK;
 }
@@ -434,7 +445,7 @@ int rwkv7_gemm_f16(const void *A, int64_t lda, const void *W, int64_t ldw, void 
   if (epi < 0 || epi > 3) return RWKV7_EINVAL;
   if (M < 1 || N < 1 || K < 8 || lda < K || ldw < K || ldy < N) return RWKV7_ESHAPE;
   GemmProb p = {static_cast<const uint16_t *>(A), static_cast<const uint16_t *>(W), Y, lda, ldw, ldy, N, K, epi};
-  return launch_gemm_group(&p, 1, M, static_cast<hipStream_t>(stream));
+  return launch_gemm_group(&p, 1, M, static_cast<hipStream_t>(stream), nullptr, nullptr);
 }
 
 }  // extern "C"

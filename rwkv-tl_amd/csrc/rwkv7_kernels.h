@@ -92,7 +92,12 @@ struct GemmProb {
   int64_t lda, ldw, ldy;
   int N, K, epi;
 };
-int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st);
+// Split-K workspace: gemm_ws_bytes(M, cus) bytes of partial tiles and
+// kGemmCounters arrival counters that start at zero (every launch leaves them
+// at zero). With part == nullptr no problem is split.
+constexpr int kGemmCounters = 1024;
+int64_t gemm_ws_bytes(int M, int cus);
+int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, float *part, unsigned *ctr);
 
 // One-token, one-sequence decode as a single persistent kernel (decode_mk.hip).
 int mk_cus();

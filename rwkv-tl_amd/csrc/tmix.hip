@@ -259,68 +259,106 @@ constexpr int kMaxCPer = 16;  // C <= 4096
 // per-thread arrays stay in registers.
 #define RWKV7_UNROLL_N(i) _Pragma("unroll") for (int i = 0; i < kMaxCPer; ++i) if (i < n)
 
-// LayerNorm of row `row` of x (f32, [*, C]) into out[] (C/256 values per
-// thread, element c = threadIdx.x + 256 * i).
-RWKV7_DEV void ln_row(const float *x, const float *w, const float *bvec, int C, float *out,
-                      float *scratch4) {
-  const int n = C >> 8;
-  float s = 0.f;
-  RWKV7_UNROLL_N(i) {
-    out[i] = x[threadIdx.x + 256 * i];
-    s += out[i];
-  }
-  const float mean = block_sum256(s, scratch4) / (float)C;
-  float q = 0.f;
-  RWKV7_UNROLL_N(i) {
-    const float d = out[i] - mean;
-    q += d * d;
-  }
-  const float rstd = rsqrtf(block_sum256(q, scratch4) / (float)C + kLnEps);
-  RWKV7_UNROLL_N(i) {
-    const int c = threadIdx.x + 256 * i;
-    out[i] = (out[i] - mean) * rstd * w[c] + bvec[c];
-  }
-}
-
-
 // Token shift of prefill (demo/rwkv7_torch.py:189-197, 251-254): prev[t] =
 // LN(x0[t-1]) and prev[0] = state; the state becomes LN(x0[T-1]). The
 // workgroup of t = 0 is the only one that touches the state: it reads it and
 // then writes the new value, so there is no cross-workgroup hazard.
+//
+// The kernel is latency-bound (one row per workgroup), so every load (this
+// row, the previous one, the last one for t = 0, the LayerNorm vectors and
+// the mix vectors) is issued up front, and the statistics of all three rows
+// share two block reductions (two-pass mean / variance, as ln_row).
+RWKV7_DEV void block_sum3(float &a, float &b, float &c, float (*red)[4]) {
+  a = wave_sum(a);
+  b = wave_sum(b);
+  c = wave_sum(c);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    red[0][w] = a;
+    red[1][w] = b;
+    red[2][w] = c;
+  }
+  __syncthreads();
+  a = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+  b = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+  c = (red[2][0] + red[2][1]) + (red[2][2] + red[2][3]);
+}
+
+template <int NP>
 __global__ __launch_bounds__(256) void ln_shift_kernel(LnShiftArgs a) {
-  __shared__ float scratch4[4];
+  __shared__ float red[2][3][4];
   const int m = blockIdx.x;
   const int t = m % a.T, b = m / a.T;
-  const int C = a.C, n = C >> 8;
-  float x[kMaxCPer], pv[kMaxCPer];
-  ln_row(a.x0 + (int64_t)m * C, a.ln_w, a.ln_b, C, x, scratch4);
-  if (t > 0) {
-    ln_row(a.x0 + (int64_t)(m - 1) * C, a.ln_w, a.ln_b, C, pv, scratch4);
-  } else {
-    RWKV7_UNROLL_N(i) pv[i] = h2f(a.shift[(int64_t)b * C + threadIdx.x + 256 * i]);
+  const int C = a.C, tid = threadIdx.x;
+  const bool has_prev = t > 0, has_last = t == 0 && a.T > 1;
+  const float *rc = a.x0 + (int64_t)m * C;
+  const float *rp = a.x0 + (int64_t)(has_prev ? m - 1 : m) * C;
+  const float *rl = a.x0 + (int64_t)(has_last ? m + a.T - 1 : m) * C;
+  uint16_t *sh = a.shift + (int64_t)b * C;
+  float xc[NP], xp[NP], xl[NP], lw[NP], lb[NP], mu[6][NP];
+  uint16_t st[NP];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int c = tid + 256 * i;
+    xc[i] = rc[c];
+    xp[i] = rp[c];
+    xl[i] = rl[c];
+    lw[i] = a.ln_w[c];
+    lb[i] = a.ln_b[c];
+    st[i] = sh[c];
+  }
+#pragma unroll
+  for (int j = 0; j < 6; ++j)
+#pragma unroll
+    for (int i = 0; i < NP; ++i) mu[j][i] = a.mu[(int64_t)(j < a.n_mix ? j : 0) * C + tid + 256 * i];
+
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    s0 += xc[i];
+    s1 += xp[i];
+    s2 += xl[i];
+  }
+  block_sum3(s0, s1, s2, red[0]);
+  const float invC = 1.f / (float)C;
+  const float m0 = s0 * invC, m1 = s1 * invC, m2 = s2 * invC;
+  float q0 = 0.f, q1 = 0.f, q2 = 0.f;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    q0 += (xc[i] - m0) * (xc[i] - m0);
+    q1 += (xp[i] - m1) * (xp[i] - m1);
+    q2 += (xl[i] - m2) * (xl[i] - m2);
+  }
+  block_sum3(q0, q1, q2, red[1]);
+  const float r0 = rsqrtf(q0 * invC + kLnEps), r1 = rsqrtf(q1 * invC + kLnEps), r2 = rsqrtf(q2 * invC + kLnEps);
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    xc[i] = (xc[i] - m0) * r0 * lw[i] + lb[i];
+    xp[i] = has_prev ? (xp[i] - m1) * r1 * lw[i] + lb[i] : h2f(st[i]);
   }
   for (int j = 0; j < a.n_mix; ++j) {
     uint16_t *o = a.out + ((int64_t)j * a.M + m) * C;
-    const float *mu = a.mu + (int64_t)j * C;
-    RWKV7_UNROLL_N(i) {
-      const int c = threadIdx.x + 256 * i;
-      o[c] = f2h(x[i] + mu[c] * (pv[i] - x[i]));
-    }
+#pragma unroll
+    for (int i = 0; i < NP; ++i) o[tid + 256 * i] = f2h(xc[i] + mu[j][i] * (xp[i] - xc[i]));
   }
   if (t == 0) {
-    float last[kMaxCPer];
-    if (a.T > 1) {
-      ln_row(a.x0 + (int64_t)(m + a.T - 1) * C, a.ln_w, a.ln_b, C, last, scratch4);
-    } else {
-      RWKV7_UNROLL_N(i) last[i] = x[i];
-    }
-    RWKV7_UNROLL_N(i) a.shift[(int64_t)b * C + threadIdx.x + 256 * i] = f2h(last[i]);
+#pragma unroll
+    for (int i = 0; i < NP; ++i) sh[tid + 256 * i] = f2h(has_last ? (xl[i] - m2) * r2 * lw[i] + lb[i] : xc[i]);
   }
 }
 
 int launch_ln_shift(const LnShiftArgs &a, hipStream_t st) {
-  if (a.C % 256 || a.C > 256 * kMaxCPer) return RWKV7_ESHAPE;
-  ln_shift_kernel<<<a.M, 256, 0, st>>>(a);
+  if (a.C % 256 || a.C > 256 * kMaxCPer || a.n_mix < 1 || a.n_mix > 6) return RWKV7_ESHAPE;
+  switch (a.C / 256) {
+#define RWKV7_LNS_CASE(n) \
+  case n: ln_shift_kernel<n><<<a.M, 256, 0, st>>>(a); break;
+    RWKV7_LNS_CASE(1) RWKV7_LNS_CASE(2) RWKV7_LNS_CASE(3) RWKV7_LNS_CASE(4)
+    RWKV7_LNS_CASE(5) RWKV7_LNS_CASE(6) RWKV7_LNS_CASE(7) RWKV7_LNS_CASE(8)
+    RWKV7_LNS_CASE(9) RWKV7_LNS_CASE(10) RWKV7_LNS_CASE(11) RWKV7_LNS_CASE(12)
+    RWKV7_LNS_CASE(13) RWKV7_LNS_CASE(14) RWKV7_LNS_CASE(15) RWKV7_LNS_CASE(16)
+#undef RWKV7_LNS_CASE
+    default: return RWKV7_ESHAPE;
+  }
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;
 }
