@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define RWKV7_ABI_VERSION 1
+#define RWKV7_ABI_VERSION 2
 #define RWKV7_HEAD_SIZE 64
 
 enum {
@@ -64,18 +64,40 @@ enum {
  * w_lora1 immediately follows w_rkv, so the two form one [3C+sumR, C] matrix.
  * Replaces the per-tensor attributes of RWKV7ATTWeight / RWKV7FFNWeight
  * (src/rwkv_tl/weight.py:18-126) with one contiguous arena per layer. */
+/* Fragment order, an optional second copy of the matrices that prefill and
+ * batched decode multiply (MFMA GEMMs). A matrix W [N, K] is padded with zeros
+ * to N' = 16*ceil(N/16) rows and K' = 32*ceil(K/32) columns and cut into
+ * blocks of 16 rows x 32 columns; block (s, j), s < N'/16, j < K'/32, is the
+ * 1024 bytes at byte offset ((s * K'/32) + j) * 1024, and inside it the 16
+ * bytes at 16*l (l = 0..63) hold W[16 s + l % 16][32 j + 8 (l / 16) .. +8):
+ * exactly the B operand of one 64-lane v_mfma_f32_16x16x32_f16, so one wave
+ * load of a block reads one contiguous KiB. Offsets inside a layer's
+ * fragment arena (gates in the order v, w, a, g, as w_lora1):
+ *   f_rkv    [3C, C]       receptance, key, value rows stacked
+ *   f_l1[g]  [R_g, C]      first LoRA steps
+ *   f_l2[g]  [C, R_g]      second LoRA steps (K = R_g)
+ *   f_o [C, C], f_fk [F, C], f_fv [C, F]
+ * frag_bytes is the fragment arena size, a multiple of 256. */
 typedef struct rwkv7_layer_layout {
   int64_t w_rkv, w_lora1, w_lora2, w_o, w_fk, w_fv, vec;
   int64_t bytes; /* arena size, a multiple of 256 */
+  int64_t f_rkv, f_l1[4], f_l2[4], f_o, f_fk, f_fv;
+  int64_t frag_bytes;
 } rwkv7_layer_layout;
 
-/* Device-side model. Layer i's arena starts at layers + i * layout.bytes. */
+/* Device-side model. Layer i's arena starts at layers + i * layout.bytes.
+ * layers_frag and head_frag are optional (NULL: the GEMMs read the row-major
+ * arenas); when set, layer i's fragment arena starts at
+ * layers_frag + i * layout.frag_bytes and head_frag holds the head [V, C] in
+ * fragment order. The two copies must hold the same weights. */
 typedef struct rwkv7_model {
   rwkv7_dims dims;
   const void *layers; /* L consecutive layer arenas */
   const void *emb;    /* f16 [V, C], LayerNorm ln0 already applied (weight.py:175) */
   const void *head;   /* f16 [V, C] */
   const void *ln_out; /* f32 [2, C]: weight, bias */
+  const void *layers_frag; /* optional: L fragment arenas */
+  const void *head_frag;   /* optional: head in fragment order */
 } rwkv7_model;
 
 /* Recurrent state of `batch` independent sequences, layer-major arenas

@@ -66,6 +66,63 @@ RWKV7_DEV void store_epi(const GemmProb &P, int row, int col, float v) {
   }
 }
 
+// Split-K hand-off shared by both kernels. Each of the workgroup's `nhold`
+// holder waves (index `hold`, or -1 for a wave holding nothing) owns MB float4
+// per lane. Returns false for every workgroup but the last of the S; the last
+// gets the split-ordered sum in acc. Partials go out with device-scope (sc1)
+// stores, which complete only once visible to every CU; each wave waits for
+// its own (an asm with a memory clobber keeps every store before it), then one
+// thread counts the workgroup in, and the last workgroup reads the partials
+// with device-scope loads. No cache write-back or invalidation is involved.
+template <int MB>
+RWKV7_DEV bool splitk_arrive(floatx4 (&acc)[MB], float *pbase, int S, int split, int nhold, int hold,
+                             unsigned *ctr, int *s_last) {
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  const int lane = threadIdx.x & 63;
+  const int nbytes = S * nhold * MB * 64 * 16;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(pbase, 0, nbytes, 0x00020000);
+  if (hold >= 0) {
+    const int my = ((split * nhold + hold) * MB * 64 + lane) * 16;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, acc[mb]), rs, my + mb * 64 * 16, 0, 16);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = old == (unsigned)(S - 1);
+    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_last = last;
+  }
+  __syncthreads();
+  if (!*s_last) return false;
+  if (hold < 0) return true;
+  // NB splits per batch of loads (16 float4 per lane in flight), summed in
+  // split order; indices past S are clamped and their values dropped
+  constexpr int NB = MB >= 16 ? 1 : 16 / MB;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < S; s0 += NB) {
+    floatx4 q[NB][MB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int sp = s0 + b < S ? s0 + b : S - 1;
+      const int at = ((sp * nhold + hold) * MB * 64 + lane) * 16;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        q[b][mb] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, at + mb * 64 * 16, 0, 16));
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const bool use = s0 + b < S;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) acc[mb] += use ? q[b][mb] : floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  return true;
+}
+
 template <int BM>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
   constexpr int MB = BM / 16;                // 16-row blocks
@@ -120,13 +177,20 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
   // W fragment of k-step j of chunk c: lane -> row n0 + 16 wv + (lane & 15),
   // 8 k at 32 j + 8 (lane >> 4) (clamped into range; out-of-range k meets a
   // zero A and out-of-range rows are never stored).
+  // In fragment order the wave's strip (clamped to the padded rows) is read
+  // one contiguous KiB per k-step; k-steps past the padded K are clamped.
+  const bool frag = P.Wf != nullptr;
   const int wn = n0 + wv * 16 + (lane & 15);
-  const uint16_t *wrow = P.W + (int64_t)(wn < N ? wn : N - 1) * P.ldw;
+  const int nstrip = (N + 15) / 16, strip = min(n0 / 16 + wv, nstrip - 1);
+  const uint16_t *wbase = frag ? P.Wf + ((int64_t)strip * P.nksf * 64 + lane) * 8
+                               : P.W + (int64_t)(wn < N ? wn : N - 1) * P.ldw;
   auto load_w = [&](int c, uint4 (&dst)[4]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int k = kb + c * kKC + 32 * j + 8 * (lane >> 4);
-      dst[j] = ld_stream(reinterpret_cast<const uint4 *>(wrow + (k < K - 8 ? k : K - 8)));
+      const int ks = min((kb + c * kKC) / 32 + j, P.nksf - 1);
+      const int64_t off = frag ? (int64_t)ks * 512 : (int64_t)(k < K - 8 ? k : K - 8);
+      dst[j] = ld_stream(reinterpret_cast<const uint4 *>(wbase + off));
     }
   };
 
@@ -171,51 +235,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
   // Epilogue: lane holds rows 4 * (lane >> 4) + {0..3} of column (lane & 15).
   const int col = n0 + wv * 16 + (lane & 15);
   if (S > 1) {
-    // Partials go out with device-scope (sc1) stores, which complete only once
-    // visible to every CU; each wave waits for its own (an asm with a memory
-    // clobber, so the compiler keeps every store before it), then one thread
-    // counts the workgroup in. The last workgroup reads them with device-scope
-    // loads. No cache write-back or invalidation is involved.
     float *pbase = g.part + g.part_off[pi] + (int64_t)tile * S * 4 * MB * 256;
-    const int nbytes = S * 4 * MB * 256 * 4;
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(pbase, 0, nbytes, 0x00020000);
-    const int my = ((split * 4 + wv) * MB * 64 + lane) * 16;
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[mb]), rs, my + mb * 64 * 16, 0, 16);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (t == 0) {
-      unsigned *ctr = g.ctr + g.ctr_off[pi] + tile;
-      const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int last = old == (unsigned)(S - 1);
-      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_last = last;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    // NB splits per batch of loads (16 float4 per lane in flight), summed in
-    // split order; indices past S are clamped and their values dropped
-    constexpr int NB = MB >= 16 ? 1 : 16 / MB;
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) acc[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < S; s0 += NB) {
-      floatx4 q[NB][MB];
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        const int sp = s0 + b < S ? s0 + b : S - 1;
-        const int at = ((sp * 4 + wv) * MB * 64 + lane) * 16;
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-          q[b][mb] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, at + mb * 64 * 16, 0, 16));
-      }
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        const bool use = s0 + b < S;
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) acc[mb] += use ? q[b][mb] : floatx4{0.f, 0.f, 0.f, 0.f};
-      }
-    }
+    if (!splitk_arrive<MB>(acc, pbase, S, split, 4, wv, g.ctr + g.ctr_off[pi] + tile, &s_last)) return;
   }
   if (col >= N) return;
 #pragma unroll
@@ -226,6 +247,189 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
       if (row < M) store_epi(P, row, col, acc[mb][r]);
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Skinny path, M <= 32 (batched decode, short prefill). One workgroup of 4
+// waves per 16-column strip of W (and per split of K, see below); the waves
+// split the strip's k-steps, each loading its W fragments and the A fragments
+// of the live rows straight from memory (A is small and stays in L2) in
+// batches of KB k-steps, all in flight before the first product. Loads are
+// exact: no k-step is loaded twice and rows past M are not loaded (their MFMA
+// rows compute zeros that are never stored). The 4 per-wave accumulators are
+// summed through LDS in wave order.
+//
+// A CU streams about 30 GB/s of loads, so a strip whose W and A run past
+// ~64 KB (K = 4096) is also split over S workgroups; the last to arrive sums
+// the S partials in split order (the protocol of the tiled kernel below).
+// ---------------------------------------------------------------------------
+constexpr int kSkW = 4;           // waves per workgroup
+constexpr int kSkinnyMaxM = 32;   // M up to this runs the skinny path
+
+struct SkinnyGroup {
+  GemmProb p[kMaxProb];
+  int wg_begin[kMaxProb + 1];  // first workgroup of each problem
+  int splits[kMaxProb];        // S of each problem (power of two)
+  int64_t part_off[kMaxProb];  // floats into part
+  int ctr_off[kMaxProb];
+  int nprob, M;
+  float *part;
+  unsigned *ctr;
+};
+
+template <int MB>
+__global__ __launch_bounds__(256) void gemm_skinny_kernel(SkinnyGroup g) {
+  constexpr int KB = MB == 1 ? 8 : 5;
+  __shared__ __align__(16) float4 red[kSkW][MB][64];
+  __shared__ int s_last;
+  const int bx = blockIdx.x;
+  int pi = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxProb; ++i) pi += (i < g.nprob && bx >= g.wg_begin[i]);
+  const GemmProb &P = g.p[pi];
+  const int S = g.splits[pi];
+  const int local = bx - g.wg_begin[pi];
+  const int split = local & (S - 1), strip = local / S;
+  const int n0 = strip * 16;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int M = g.M, N = P.N, K = P.K;
+  // k-steps of this split, then of this wave
+  const int nks = (K + 31) / 32;
+  const int sps = (nks + S - 1) / S;
+  const int s0 = split * sps, s1 = min(nks, s0 + sps);
+  const int per = (s1 - s0 + kSkW - 1) / kSkW;
+  const int ks0 = s0 + wv * per, ks1 = min(s1, ks0 + per);
+  // W fragment of k-step ks: fragment order reads block (strip, ks), one
+  // contiguous KiB per wave; row-major reads 8 k of row n0 + lane % 16
+  const bool frag = P.Wf != nullptr;
+  const int wn = n0 + (lane & 15);
+  const uint16_t *wbase = frag ? P.Wf + ((int64_t)strip * P.nksf * 64 + lane) * 8
+                               : P.W + (int64_t)(wn < N ? wn : N - 1) * P.ldw;
+  auto woff = [&](int ks) -> int64_t {
+    const int k = 32 * ks + 8 * (lane >> 4);
+    return frag ? (int64_t)ks * 512 : (int64_t)(k < K - 8 ? k : K - 8);
+  };
+  const uint16_t *arow[MB];
+  bool alive[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int r = mb * 16 + (lane & 15);
+    alive[mb] = r < M;
+    arow[mb] = P.A + (int64_t)(r < M ? r : M - 1) * P.lda;
+  }
+  floatx4 acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int kb = ks0; kb < ks1; kb += KB) {
+    const int cnt = min(KB, ks1 - kb);  // wave-uniform
+    uint4 wf[KB], af[KB][MB];
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      wf[j] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) af[j][mb] = make_uint4(0, 0, 0, 0);
+      if (j < cnt) {
+        const int k = 32 * (kb + j) + 8 * (lane >> 4);
+        const int kc = k < K - 8 ? k : K - 8;
+        wf[j] = ld_stream(reinterpret_cast<const uint4 *>(wbase + woff(kb + j)));
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          if (alive[mb] && k < K) af[j][mb] = *reinterpret_cast<const uint4 *>(arow[mb] + kc);
+      }
+    }
+    // every load of the batch is issued before the first product waits
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      if (j < cnt) {
+        const half8 bfrag = __builtin_bit_cast(half8, wf[j]);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, af[j][mb]), bfrag, acc[mb], 0,
+                                                           0, 0);
+      }
+    }
+  }
+  // cross-wave sum in wave order; wave 0 holds the strip's result
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) red[wv][mb][lane] = make_float4(acc[mb][0], acc[mb][1], acc[mb][2], acc[mb][3]);
+  __syncthreads();
+  if (wv == 0) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      floatx4 o = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < kSkW; ++w) {
+        const float4 q = red[w][mb][lane];
+        o += floatx4{q.x, q.y, q.z, q.w};
+      }
+      acc[mb] = o;
+    }
+  }
+  if (S > 1) {
+    float *pbase = g.part + g.part_off[pi] + (int64_t)strip * S * MB * 256;
+    if (!splitk_arrive<MB>(acc, pbase, S, split, 1, wv == 0 ? 0 : -1, g.ctr + g.ctr_off[pi] + strip, &s_last))
+      return;
+  }
+  const int col = n0 + (lane & 15);
+  if (wv != 0 || col >= N) return;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = mb * 16 + (lane >> 4) * 4 + r;
+      if (row < M) store_epi(P, row, col, acc[mb][r]);
+    }
+  }
+}
+
+// Splits of a skinny strip: enough that one workgroup moves at most ~64 KB
+// of W and A.
+static int skinny_splits(int M, int K, bool can_split) {
+  if (!can_split) return 1;
+  const int64_t per_k = 16 * 2 + (int64_t)(M < 16 ? M : 16) * 2 * ((M + 15) / 16);  // bytes per unit of k
+  int S = 1;
+  while (S < kMaxSplit && (int64_t)K / S * per_k > 64 * 1024 && K / (2 * S) >= 256) S *= 2;
+  return S;
+}
+
+static int launch_skinny(const GemmProb *probs, int nprob, int M, hipStream_t st, float *part, unsigned *ctr,
+                         int64_t part_cap) {
+  SkinnyGroup g;
+  g.nprob = nprob;
+  g.M = M;
+  g.part = part;
+  g.ctr = ctr;
+  const int MB = (M + 15) / 16;
+  int wgs = 0, ctrs = 0;
+  int64_t pfl = 0;
+  for (int i = 0; i < kMaxProb; ++i) {
+    g.wg_begin[i] = wgs;
+    if (i < nprob) {
+      const int strips = (probs[i].N + 15) / 16;
+      const int S = skinny_splits(M, probs[i].K, part != nullptr && ctr != nullptr);
+      g.p[i] = probs[i];
+      g.splits[i] = S;
+      g.part_off[i] = pfl;
+      g.ctr_off[i] = ctrs;
+      wgs += strips * S;
+      if (S > 1) {
+        pfl += (int64_t)strips * S * MB * 256;
+        ctrs += strips;
+      }
+    } else {
+      g.p[i] = probs[0];
+      g.splits[i] = 1;
+      g.part_off[i] = 0;
+      g.ctr_off[i] = 0;
+    }
+  }
+  g.wg_begin[kMaxProb] = wgs;
+  if (pfl * 4 > part_cap || ctrs > kGemmCounters) return RWKV7_EWORKSPACE;
+  if (MB == 1) gemm_skinny_kernel<1><<<wgs, 256, 0, st>>>(g);
+  else gemm_skinny_kernel<2><<<wgs, 256, 0, st>>>(g);
+  RWKV7_CHECK_LAUNCH();
+  return RWKV7_OK;
 }
 
 static int bm_for(int M) { return M <= 16 ? 16 : M <= 32 ? 32 : M <= 64 ? 64 : 128; }
@@ -291,6 +495,7 @@ int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, f
     if (p.K < 8 || p.N <= 0 || p.K % 8 || p.lda % 8 || p.ldw % 8) return RWKV7_ESHAPE;
     if (!p.A || !p.W || !p.Y) return RWKV7_EINVAL;
   }
+  if (M <= kSkinnyMaxM) return launch_skinny(probs, nprob, M, st, part, ctr, gemm_ws_bytes(M, cus));
   plan_splits(probs, nprob, M, cus, part != nullptr && ctr != nullptr, S, ks);
   int wgs = 0, ctrs = 0;
   int64_t pfl = 0;

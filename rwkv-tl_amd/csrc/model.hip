@@ -29,6 +29,9 @@ static int check_dims(const rwkv7_dims *d) {
 
 static int sum_ranks(const rwkv7_dims &d) { return d.rank_w + d.rank_a + d.rank_v + d.rank_g; }
 
+// bytes of an [N, K] matrix in fragment order (N, K padded to 16, 32)
+static int64_t frag_bytes(int64_t N, int64_t K) { return ((N + 15) / 16 * 16) * ((K + 31) / 32 * 32) * 2; }
+
 static void layout_of(const rwkv7_dims &d, rwkv7_layer_layout *o) {
   const int64_t C = d.n_embd, F = d.n_ffn, SR = sum_ranks(d);
   int64_t off = 0;
@@ -47,6 +50,26 @@ static void layout_of(const rwkv7_dims &d, rwkv7_layer_layout *o) {
   o->vec = off;
   off = align256(off + int64_t(RWKV7_NVEC) * C * 4);
   o->bytes = off;
+  // fragment arena
+  const int64_t R[4] = {d.rank_v, d.rank_w, d.rank_a, d.rank_g};
+  off = 0;
+  o->f_rkv = off;
+  off = align256(off + frag_bytes(3 * C, C));
+  for (int g = 0; g < 4; ++g) {
+    o->f_l1[g] = off;
+    off = align256(off + frag_bytes(R[g], C));
+  }
+  for (int g = 0; g < 4; ++g) {
+    o->f_l2[g] = off;
+    off = align256(off + frag_bytes(C, R[g]));
+  }
+  o->f_o = off;
+  off = align256(off + frag_bytes(C, C));
+  o->f_fk = off;
+  off = align256(off + frag_bytes(F, C));
+  o->f_fv = off;
+  off = align256(off + frag_bytes(C, F));
+  o->frag_bytes = off;
 }
 
 // Workspace of the one-sequence decode path (GEMV kernels).
@@ -270,6 +293,17 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
         {xa, wl1 + (int64_t)(rv + rw) * C, w.l1 + rv + rw, C, C, SR, ra, C, GEPI_F16},
         {xg, wl1 + (int64_t)(rv + rw + ra) * C, w.l1 + rv + rw + ra, C, C, SR, rg, C, GEPI_SIGM_F16},
     };
+    // fragment-order copies (16 x 32 blocks) when the model has them
+    const char *Fl = m.layers_frag ? static_cast<const char *>(m.layers_frag) + (int64_t)l * lay.frag_bytes : nullptr;
+    auto frag = [&](GemmProb &p, int64_t off, int64_t strip0) {
+      if (!Fl) return;
+      p.nksf = (p.K + 31) / 32;
+      p.Wf = reinterpret_cast<const uint16_t *>(Fl + off) + strip0 * p.nksf * 512;
+    };
+    frag(g1[0], lay.f_rkv, 0);
+    frag(g1[1], lay.f_rkv, C / 16);
+    frag(g1[2], lay.f_rkv, 2 * C / 16);
+    for (int g = 0; g < 4; ++g) frag(g1[3 + g], lay.f_l1[g], 0);
     RWKV7_TRY(launch_gemm_group(g1, 7, M, st, w.part, ctr));
     GemmProb g2[4] = {
         {w.l1, wl2, w.d, SR, SR, C, C, rv, GEPI_F32},
@@ -277,6 +311,7 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
         {w.l1 + rv + rw, wl2 + rv + rw, w.d + 2 * MC, SR, SR, C, C, ra, GEPI_F32},
         {w.l1 + rv + rw + ra, wl2 + rv + rw + ra, w.d + 3 * MC, SR, SR, C, C, rg, GEPI_F32},
     };
+    for (int g = 0; g < 4; ++g) frag(g2[g], lay.f_l2[g], 0);
     RWKV7_TRY(launch_gemm_group(g2, 4, M, st, w.part, ctr));
     GatesArgs ga = {w.rkv, w.d, vec, w.vfirst, w.wkab, C, M, l == 0};
     RWKV7_TRY(launch_tmix_gates(ga, st));
@@ -287,20 +322,27 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
     GnGateArgs gn = {w.y, w.rkv, w.wkab + MC, w.wkab + 2 * MC, w.d + 3 * MC, vec, w.yg, C, M};
     RWKV7_TRY(launch_gn_gate(gn, st));
     GemmProb go = {w.yg, reinterpret_cast<const uint16_t *>(L + lay.w_o), w.x0, C, C, C, C, C, GEPI_ADD_F32};
+    frag(go, lay.f_o, 0);
     RWKV7_TRY(launch_gemm_group(&go, 1, M, st, w.part, ctr));
 
     LnShiftArgs lc = {w.x0, vec + RWKV7_V_LN2_W * C, vec + RWKV7_V_LN2_B * C, vec + RWKV7_V_FFN_X_K * C,
                       1, w.xmix, cshift, C, T, M};
     RWKV7_TRY(launch_ln_shift(lc, st));
     GemmProb gk = {w.xmix, reinterpret_cast<const uint16_t *>(L + lay.w_fk), w.hid, C, C, F, F, C, GEPI_RELUSQ};
+    frag(gk, lay.f_fk, 0);
     RWKV7_TRY(launch_gemm_group(&gk, 1, M, st, w.part, ctr));
     GemmProb gv = {w.hid, reinterpret_cast<const uint16_t *>(L + lay.w_fv), w.x0, F, F, C, C, F, GEPI_ADD_F32};
+    frag(gv, lay.f_fv, 0);
     RWKV7_TRY(launch_gemm_group(&gv, 1, M, st, w.part, ctr));
   }
   if (logits) {
     const float *lo = static_cast<const float *>(m.ln_out);
     RWKV7_TRY(launch_ln_rows(w.x0, 1, lo, lo + C, w.headin, 0, B, C, T, T - 1, st));
     GemmProb gh = {w.headin, static_cast<const uint16_t *>(m.head), logits, C, C, d.vocab, d.vocab, C, GEPI_F16};
+    if (m.head_frag) {
+      gh.Wf = static_cast<const uint16_t *>(m.head_frag);
+      gh.nksf = (C + 31) / 32;
+    }
     RWKV7_TRY(launch_gemm_group(&gh, 1, B, st, w.part, ctr));
   }
   return RWKV7_OK;

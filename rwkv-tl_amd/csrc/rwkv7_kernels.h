@@ -91,6 +91,10 @@ struct GemmProb {
   void *Y;
   int64_t lda, ldw, ldy;
   int N, K, epi;
+  // optional: W in fragment order (16 x 32 blocks, include/rwkv7_hip.h), with
+  // nksf blocks per 16-row strip; nullptr reads the row-major W
+  const uint16_t *Wf;
+  int nksf;
 };
 // Split-K workspace: gemm_ws_bytes(M, cus) bytes of partial tiles and
 // kGemmCounters arrival counters that start at zero (every launch leaves them

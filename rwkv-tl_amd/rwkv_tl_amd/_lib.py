@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the HIP library)
 
 LIB_NAME = "librwkv7_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # enum indices of the per-layer fp32 vector block (RWKV7_V_*)
 VEC_NAMES = (
@@ -60,7 +60,9 @@ class Dims(ctypes.Structure):
 class LayerLayout(ctypes.Structure):
     _fields_ = [
         (n, ctypes.c_int64)
-        for n in ("w_rkv", "w_lora1", "w_lora2", "w_o", "w_fk", "w_fv", "vec", "bytes")
+        for n in ("w_rkv", "w_lora1", "w_lora2", "w_o", "w_fk", "w_fv", "vec", "bytes", "f_rkv")
+    ] + [("f_l1", ctypes.c_int64 * 4), ("f_l2", ctypes.c_int64 * 4)] + [
+        (n, ctypes.c_int64) for n in ("f_o", "f_fk", "f_fv", "frag_bytes")
     ]
 
 
@@ -71,6 +73,8 @@ class Model(ctypes.Structure):
         ("emb", ctypes.c_void_p),
         ("head", ctypes.c_void_p),
         ("ln_out", ctypes.c_void_p),
+        ("layers_frag", ctypes.c_void_p),
+        ("head_frag", ctypes.c_void_p),
     ]
 
 

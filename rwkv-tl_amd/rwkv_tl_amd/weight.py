@@ -132,10 +132,25 @@ class DeviceWeights:
     head: Tensor     # f16 [V, C]
     ln_out: Tensor   # f32 [2, C]
     desc: _lib.Model
+    layers_frag: Tensor | None = None  # uint8 [L, layout.frag_bytes]
+    head_frag: Tensor | None = None    # f16, the head in fragment order
 
     @property
     def nbytes(self) -> int:
-        return sum(t.numel() * t.element_size() for t in (self.layers, self.emb, self.head, self.ln_out))
+        ts = (self.layers, self.emb, self.head, self.ln_out, self.layers_frag, self.head_frag)
+        return sum(t.numel() * t.element_size() for t in ts if t is not None)
+
+
+def to_fragments(W: Tensor) -> Tensor:
+    """``W [N, K]`` in fragment order (``include/rwkv7_hip.h``): zero-padded to
+    16-row x 32-column blocks, block (s, j) at ``(s * K'/32 + j) * 512``
+    halves, lane ``l`` of a block holding ``W[16 s + l % 16, 32 j + 8 (l // 16) :+8]``."""
+    N, K = W.shape
+    Np, Kp = -(-N // 16) * 16, -(-K // 32) * 32
+    P = torch.zeros(Np, Kp, dtype=W.dtype, device=W.device)
+    P[:N, :K] = W
+    # [s, r, j, c, e] -> [s, j, c, r, e]: lane = c * 16 + r
+    return P.view(Np // 16, 16, Kp // 32, 4, 8).permute(0, 2, 3, 1, 4).reshape(-1)
 
 
 def model_dims(w: RWKV7Weight) -> _lib.Dims:
@@ -164,8 +179,12 @@ def _f16_view(buf: Tensor, off: int, rows: int, cols: int) -> Tensor:
     return buf[off : off + rows * cols * 2].view(torch.float16).view(rows, cols)
 
 
-def pack_device_weights(w: RWKV7Weight) -> DeviceWeights:
-    """Build the HIP arenas from reference-layout weights (fp16, on the GPU)."""
+def pack_device_weights(w: RWKV7Weight, fragments: bool = True) -> DeviceWeights:
+    """Build the HIP arenas from reference-layout weights (fp16, on the GPU).
+
+    ``fragments`` also builds the fragment-order copy the prefill / batched
+    decode GEMMs stream (one contiguous KiB per wave load); it roughly doubles
+    the weight memory."""
     if w.dtype != torch.float16:
         raise ValueError(f"the HIP kernels take float16 weights, got {w.dtype}")
     dims = model_dims(w)
@@ -198,11 +217,36 @@ def pack_device_weights(w: RWKV7Weight) -> DeviceWeights:
     emb = w.emb.contiguous()
     head = w.head.contiguous()
     ln_out = torch.stack([w.ln_out.w.float(), w.ln_out.b.float()]).contiguous()
+    layers_frag = head_frag = None
+    if fragments:
+        layers_frag = torch.zeros(dims.n_layer, lay.frag_bytes, dtype=torch.uint8, device=dev)
+        R = (dims.rank_v, dims.rank_w, dims.rank_a, dims.rank_g)
+        for i in range(dims.n_layer):
+            buf, src = layers_frag[i], layers[i]
+
+            def put(off: int, Wm: Tensor) -> None:
+                f = to_fragments(Wm)
+                buf[off : off + f.numel() * 2].view(torch.float16).copy_(f)
+
+            put(lay.f_rkv, _f16_view(src, lay.w_rkv, 3 * C, C))
+            l1 = _f16_view(src, lay.w_lora1, SR, C)
+            l2 = _f16_view(src, lay.w_lora2, C, SR)
+            r0 = 0
+            for g in range(4):
+                put(lay.f_l1[g], l1[r0 : r0 + R[g]])
+                put(lay.f_l2[g], l2[:, r0 : r0 + R[g]])
+                r0 += R[g]
+            put(lay.f_o, _f16_view(src, lay.w_o, C, C))
+            put(lay.f_fk, _f16_view(src, lay.w_fk, F_, C))
+            put(lay.f_fv, _f16_view(src, lay.w_fv, C, F_))
+        head_frag = to_fragments(head).contiguous()
     desc = _lib.Model(
         dims=dims,
         layers=layers.data_ptr(),
         emb=emb.data_ptr(),
         head=head.data_ptr(),
         ln_out=ln_out.data_ptr(),
+        layers_frag=layers_frag.data_ptr() if layers_frag is not None else None,
+        head_frag=head_frag.data_ptr() if head_frag is not None else None,
     )
-    return DeviceWeights(dims, lay, layers, emb, head, ln_out, desc)
+    return DeviceWeights(dims, lay, layers, emb, head, ln_out, desc, layers_frag, head_frag)

@@ -14,7 +14,7 @@ from oracle import rwkv7_ref as R
 from rwkv_tl_amd import _lib, make_rwkv7, sample_logits
 from rwkv_tl_amd.checkpoint import SHAPES, make_random_state_dict
 from rwkv_tl_amd.state import State
-from rwkv_tl_amd.weight import RWKV7Weight, layer_layout, model_dims
+from rwkv_tl_amd.weight import RWKV7Weight, layer_layout, model_dims, to_fragments
 
 REPO = Path(__file__).resolve().parent.parent
 HEADER = REPO / "include" / "rwkv7_hip.h"
@@ -56,6 +56,37 @@ def test_layer_layout(shape):
     assert lay.vec >= lay.w_fv + C * F * 2
     assert lay.bytes >= lay.vec + _lib.NVEC * C * 4
     assert all(o % 256 == 0 for o in offs if o != lay.w_lora1)
+    # fragment arena: every matrix padded to 16 x 32 blocks, in order, no overlap
+    def fb(n, k):
+        return (-(-n // 16) * 16) * (-(-k // 32) * 32) * 2
+
+    R = (d.rank_v, d.rank_w, d.rank_a, d.rank_g)
+    regions = [(lay.f_rkv, fb(3 * C, C))] + [(lay.f_l1[g], fb(R[g], C)) for g in range(4)]
+    regions += [(lay.f_l2[g], fb(C, R[g])) for g in range(4)]
+    regions += [(lay.f_o, fb(C, C)), (lay.f_fk, fb(F, C)), (lay.f_fv, fb(C, F))]
+    for (o0, n0), (o1, _) in zip(regions, regions[1:]):
+        assert o0 % 256 == 0 and o1 >= o0 + n0
+    assert lay.frag_bytes >= regions[-1][0] + regions[-1][1] and lay.frag_bytes % 256 == 0
+
+
+def test_fragment_order_matches_header_definition():
+    """Block (s, j) of W [N, K] is 1024 bytes at (s * K'/32 + j) * 1024 and its
+    lane l holds W[16 s + l % 16, 32 j + 8 (l // 16) : +8], zero-padded."""
+    N, K = 37, 70  # both ragged: padded to 48 x 96
+    W = torch.arange(N * K, dtype=torch.float32).view(N, K) + 1
+    f = to_fragments(W)
+    Np, Kp = 48, 96
+    assert f.numel() == Np * Kp
+    blocks = f.view(Np // 16, Kp // 32, 64, 8)
+    for s in range(Np // 16):
+        for j in range(Kp // 32):
+            for lane in range(64):
+                r, k0 = 16 * s + lane % 16, 32 * j + 8 * (lane // 16)
+                want = torch.zeros(8)
+                if r < N:
+                    ks = [k for k in range(k0, k0 + 8) if k < K]
+                    want[: len(ks)] = W[r, ks[0] : ks[-1] + 1] if ks else want[:0]
+                assert torch.equal(blocks[s, j, lane], want), (s, j, lane)
 
 
 def test_layout_rejects_unsupported_dims():
