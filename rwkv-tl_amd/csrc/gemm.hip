@@ -138,17 +138,22 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
   const GemmProb &P = g.p[pi];
   const int S = g.splits[pi];
   const int local = bx - g.wg_begin[pi];
-  const int split = local & (S - 1), tile = local / S;
-  const int mt = tile % g.m_tiles, nt = tile / g.m_tiles;
+  // Workgroup order: a unit u = (n-tile, split) reads one W slice; its m-tiles
+  // get indices 8 apart, so they run on the same XCD (workgroups are dealt
+  // round-robin over the 8 XCDs) and all but the first find W in that L2.
+  const int mtl = g.m_tiles;
+  const int u = local / (8 * mtl) * 8 + (local & 7);
+  const int mt = local % (8 * mtl) / 8;
+  const int nunits = (P.N + kBN - 1) / kBN * S;
+  if (u >= nunits) return;  // padding of the last group of 8 units
+  const int split = u & (S - 1), nt = u / S;
+  const int tile = nt * mtl + mt;
   const int m0 = mt * BM, n0 = nt * kBN;
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const int M = g.M, N = P.N, K = P.K;
   const int kb = split * g.kslice[pi];
   const int ke = min(K, kb + g.kslice[pi]);
-  // chunks of this split, padded to even (the chunk loop is unrolled by two so
-  // the register double buffers have fixed names); padding chunks are skipped
-  const int nch = (ke - kb + kKC - 1) / kKC;
-  const int nch2 = (nch + 1) & ~1;
+  const int nch = (ke - kb + kKC - 1) / kKC;  // chunks of this split
 
   // A staging: piece idx -> row idx >> 4, 16-byte column idx & 15. Loads are
   // unconditional (row and k clamped into range) and masked after arrival, so
@@ -184,13 +189,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
   const int nstrip = (N + 15) / 16, strip = min(n0 / 16 + wv, nstrip - 1);
   const uint16_t *wbase = frag ? P.Wf + ((int64_t)strip * P.nksf * 64 + lane) * 8
                                : P.W + (int64_t)(wn < N ? wn : N - 1) * P.ldw;
+  const int nksf1 = P.nksf - 1, kb32 = kb / 32, wmul = frag ? 512 : 0, kmul = frag ? 0 : 1;
   auto load_w = [&](int c, uint4 (&dst)[4]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int k = kb + c * kKC + 32 * j + 8 * (lane >> 4);
-      const int ks = min((kb + c * kKC) / 32 + j, P.nksf - 1);
-      const int64_t off = frag ? (int64_t)ks * 512 : (int64_t)(k < K - 8 ? k : K - 8);
-      dst[j] = ld_stream(reinterpret_cast<const uint4 *>(wbase + off));
+      const int ks = min(kb32 + 4 * c + j, nksf1);
+      const int64_t off = (int64_t)ks * wmul + (k < K - 8 ? k : K - 8) * kmul;
+      dst[j] = *reinterpret_cast<const uint4 *>(wbase + off);
     }
   };
 
@@ -211,23 +217,34 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
     }
   };
 
+  // Chunk loop, unrolled by two so the register double buffers of W have
+  // fixed names. Every load is unconditional (addresses clamped) so the
+  // compiler counts outstanding loads exactly; an odd chunk count gets one
+  // padding chunk whose products are skipped.
+  const int nch2 = (nch + 1) & ~1;
   uint4 w0[4], w1[4];
   load_a(0);
   load_w(0, w0);
   load_w(1, w1);
   store_a(0, 0);
   __syncthreads();
+  // (scheduling barriers keep each chunk's A loads ahead of the W loads issued
+  // after its products, so storing A to LDS waits for A alone)
   for (int c = 0; c < nch2; c += 2) {
     // chunk c (A in buffer 0, W in w0)
     load_a(c + 1);
-    if (c < nch) compute(0, w0);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(0, w0);
     load_w(c + 2, w0);
+    __builtin_amdgcn_sched_barrier(0);
     store_a(c + 1, 1);
     __syncthreads();
     // chunk c + 1 (A in buffer 1, W in w1)
     load_a(c + 2);
+    __builtin_amdgcn_sched_barrier(0);
     if (c + 1 < nch) compute(1, w1);
     load_w(c + 3, w1);
+    __builtin_amdgcn_sched_barrier(0);
     store_a(c + 2, 0);
     __syncthreads();
   }
@@ -432,46 +449,38 @@ static int launch_skinny(const GemmProb *probs, int nprob, int M, hipStream_t st
   return RWKV7_OK;
 }
 
-static int bm_for(int M) { return M <= 16 ? 16 : M <= 32 ? 32 : M <= 64 ? 64 : 128; }
+// Row tile of the tiled path: 32 rows up to M = 256 (the tiles alone then
+// cover the GPU and W, re-read per row tile, comes from L2), 128 beyond.
+static int bm_for(int M) { return M <= 256 ? 32 : 128; }
 
-static int pow2_floor(int x) {
-  int p = 1;
-  while (p * 2 <= x) p *= 2;
-  return p;
-}
-
-// Splits of every problem of a group: none when the tiles already cover the
-// GPU, else enough to reach about two workgroups per CU, each split keeping at
-// least one 128-wide chunk of K and the partial tiles of a problem (written
-// and read once) no larger than its weights.
+// Splits of a tiled problem: K is split (power of two, each split keeping at
+// least two 128-wide chunks) until the group has a workgroup per CU and no
+// workgroup streams more than ~128 KB of W and A.
 static void plan_splits(const GemmProb *probs, int nprob, int M, int cus, bool can_split, int *S, int *kslice) {
   const int BM = bm_for(M);
   const int m_tiles = (M + BM - 1) / BM;
   int tiles = 0;
   for (int i = 0; i < nprob; ++i) tiles += m_tiles * ((probs[i].N + kBN - 1) / kBN);
-  int want = 1;
-  if (can_split && tiles < cus) {
-    want = 1;
-    while (want < kMaxSplit && tiles * want < 2 * cus) want *= 2;
-  }
   for (int i = 0; i < nprob; ++i) {
     const int K = probs[i].K;
-    const int64_t ti = (int64_t)m_tiles * ((probs[i].N + kBN - 1) / kBN);
-    const int64_t wbytes = (int64_t)probs[i].N * K * 2, pbytes = ti * BM * kBN * 4;
-    int maxs = pow2_floor(K >= kKC ? K / kKC : 1);
-    const int maxt = pow2_floor((int)(wbytes / pbytes > 1 ? (wbytes / pbytes > kMaxSplit ? kMaxSplit : wbytes / pbytes) : 1));
-    maxs = maxs < maxt ? maxs : maxt;
-    const int s = want < maxs ? want : maxs;
+    int s = 1;
+    if (can_split) {
+      auto bytes = [&](int sp) { return (int64_t)(kBN + BM) * 2 * ((K + sp - 1) / sp); };
+      while (s < kMaxSplit && K / (2 * s) >= 2 * kKC && (tiles * s < cus || bytes(s) > 128 * 1024) &&
+             (int64_t)tiles * 2 * s <= 4 * cus)
+        s *= 2;
+    }
     S[i] = s;
     kslice[i] = ((K + s - 1) / s + kKC - 1) / kKC * kKC;
   }
 }
 
 int64_t gemm_ws_bytes(int M, int cus) {
-  // at most 2 * cus * 2 workgroups carry a partial tile (tiles < cus, splits
-  // chosen to reach < 4 * cus), BM x 64 floats each
-  const int64_t part = (int64_t)4 * cus * bm_for(M) * kBN * 4;
-  return part;
+  // partial tiles of BM x 64 floats; the tiled plan keeps tiles x S <= 4 cus,
+  // the skinny one at most 16 splits of 16-column strips of 32 rows
+  const int64_t tiled = (int64_t)4 * cus * bm_for(M) * kBN * 4;
+  const int64_t skinny = (int64_t)4 * cus * 32 * 16 * 4;
+  return tiled > skinny ? tiled : skinny;
 }
 
 // Checks shapes and launches one group. Every problem needs K % 8 == 0, K >= 8
@@ -503,12 +512,13 @@ int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, f
     g.wg_begin[i] = wgs;
     if (i < nprob) {
       const int tiles = g.m_tiles * ((probs[i].N + kBN - 1) / kBN);
+      const int units = (probs[i].N + kBN - 1) / kBN * S[i];
       g.p[i] = probs[i];
       g.splits[i] = S[i];
       g.kslice[i] = ks[i];
       g.part_off[i] = pfl;
       g.ctr_off[i] = ctrs;
-      wgs += tiles * S[i];
+      wgs += (units + 7) / 8 * 8 * g.m_tiles;
       if (S[i] > 1) {
         pfl += (int64_t)tiles * S[i] * BM * kBN;
         ctrs += tiles;
