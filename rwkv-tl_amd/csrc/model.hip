@@ -113,7 +113,7 @@ static int64_t decode_ws(const rwkv7_dims &d, char *base, DecodeWs *w) {
 
 // Workspace of the batched path (M = B * T rows).
 struct BatchWs {
-  float *x0, *rkv, *d, *vfirst, *wkab, *y, *part;
+  float *x0, *rkv, *d, *vfirst, *kv, *y, *part;  // kv: gated k, mixed v [2][M][C]
   uint16_t *xmix, *l1, *yg, *hid, *headin;
 };
 static int64_t batch_ws(const rwkv7_dims &d, int64_t B, int64_t T, char *base, BatchWs *w) {
@@ -131,7 +131,7 @@ static int64_t batch_ws(const rwkv7_dims &d, int64_t B, int64_t T, char *base, B
   t.l1 = reinterpret_cast<uint16_t *>(take(M * SR * 2));
   t.d = reinterpret_cast<float *>(take(4 * M * C * 4));
   t.vfirst = reinterpret_cast<float *>(take(M * C * 4));
-  t.wkab = reinterpret_cast<float *>(take(5 * M * C * 4));
+  t.kv = reinterpret_cast<float *>(take(2 * M * C * 4));
   t.y = reinterpret_cast<float *>(take(M * C * 4));
   t.yg = reinterpret_cast<uint16_t *>(take(M * C * 2));
   t.hid = reinterpret_cast<uint16_t *>(take(M * F * 2));
@@ -313,13 +313,9 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
     };
     for (int g = 0; g < 4; ++g) frag(g2[g], lay.f_l2[g], 0);
     RWKV7_TRY(launch_gemm_group(g2, 4, M, st, w.part, ctr));
-    GatesArgs ga = {w.rkv, w.d, vec, w.vfirst, w.wkab, C, M, l == 0};
-    RWKV7_TRY(launch_tmix_gates(ga, st));
-    ScanArgs<float, float, float> sc = {rnn,           w.rkv,         w.wkab + MC, w.wkab + 2 * MC,
-                                        w.wkab + 3 * MC, w.wkab + 4 * MC, w.wkab,      w.y,
-                                        B,             T,             H};
-    RWKV7_TRY(launch_wkv7_scan(sc, st));
-    GnGateArgs gn = {w.y, w.rkv, w.wkab + MC, w.wkab + 2 * MC, w.d + 3 * MC, vec, w.yg, C, M};
+    PrefillScanArgs sc = {rnn, w.rkv, w.d, vec, w.vfirst, w.y, w.kv, w.kv + MC, B, T, H, C, M, l == 0};
+    RWKV7_TRY(launch_wkv7_prefill(sc, st));
+    GnGateArgs gn = {w.y, w.rkv, w.kv, w.kv + MC, w.d + 3 * MC, vec, w.yg, C, M};
     RWKV7_TRY(launch_gn_gate(gn, st));
     GemmProb go = {w.yg, reinterpret_cast<const uint16_t *>(L + lay.w_o), w.x0, C, C, C, C, C, GEPI_ADD_F32};
     frag(go, lay.f_o, 0);

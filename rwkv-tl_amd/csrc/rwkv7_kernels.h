@@ -61,15 +61,17 @@ struct LnShiftArgs {
 };
 int launch_ln_shift(const LnShiftArgs &a, hipStream_t st);
 
-struct GatesArgs {
-  const float *rkv;
-  const float *d;
-  const float *vec;
-  float *vfirst;
-  float *wkab;
-  int C, M, layer0;
+// Prefill time-mix core: gates of every token fused into the wkv7 scan.
+// rkv f32 [3][M][C] (r, k, v), d f32 [4][M][C] (LoRA second steps v, w, a, g),
+// vfirst f32 [M][C] (written on layer 0, read after), outputs y, kn_out (the
+// gated k) and v_out (the mixed v), f32 [M][C]; M = B * T, rows b * T + t.
+struct PrefillScanArgs {
+  float *S;
+  const float *rkv, *d, *vec;
+  float *vfirst, *y, *kn_out, *v_out;
+  int B, T, H, C, M, layer0;
 };
-int launch_tmix_gates(const GatesArgs &g, hipStream_t st);
+int launch_wkv7_prefill(const PrefillScanArgs &p, hipStream_t st);
 
 struct GnGateArgs {
   const float *y, *r, *kn, *v, *g, *vec;

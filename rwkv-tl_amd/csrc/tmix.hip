@@ -241,6 +241,174 @@ template int launch_wkv7_scan<uint16_t, uint16_t, uint16_t>(const ScanArgs<uint1
 template int launch_wkv7_scan<float, float, float>(const ScanArgs<float, float, float> &, hipStream_t);
 
 // ---------------------------------------------------------------------------
+// Prefill time-mix core: the gate math of each token (demo/rwkv7_torch.py:
+// 203-224) fused into the wkv7 scan (dplr.py:174-227). Grid (4 * H, B): each
+// workgroup owns 16 value rows of one head, computes the gates of all 64
+// channels of its head (the L2 norm of kk needs them all) while staging a chunk
+// of 16 tokens, and writes the gated k and the mixed v of its 16 channels (and
+// v itself on layer 0) for the GroupNorm stage.
+//
+// Step loop: 16 lanes per row, 4 key columns per lane, so sa = S a is a 16-lane
+// DPP sum; S w + v k is formed while that sum runs, so the new state is one FMA
+// past sa; the next step's inputs are read from LDS while the current step
+// computes; y is left as per-lane partials in LDS and summed once per chunk.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p) {
+  // s_in[buf][vec][token][16 float4]: vec 0 w, 1 a, 2 b, 3 k, 4 r, 5 v
+  __shared__ float4 s_in[2][6][kCh][kN / 4];
+  __shared__ float s_yp[kCh][16][17];  // per-lane partial y: [step][row][lane], padded
+
+  const int t = threadIdx.x;
+  const int h = blockIdx.x >> 2, quarter = blockIdx.x & 3, bi = blockIdx.y;
+  const int row = quarter * 16 + (t >> 4);
+  const int lc = t & 15;  // owns key columns 4*lc .. 4*lc+3
+  const int H = p.H, T = p.T, C = p.C;
+  const int64_t MC = (int64_t)p.M * C;
+  const int64_t base = (int64_t)bi * T * C + (int64_t)h * kN;  // token 0, channel 0 of the head
+  const float *vec = p.vec;
+
+  // staging: thread -> token t >> 4 of the chunk, channels 4q .. 4q+3
+  const int st_tok = t >> 4, q = t & 15;
+  const int ch0 = h * kN + 4 * q;
+  auto ld4 = [&](const float *src) { return *reinterpret_cast<const float4 *>(src); };
+  const float4 v0v = ld4(vec + RWKV7_V_V0 * C + ch0), w0v = ld4(vec + RWKV7_V_W0 * C + ch0);
+  const float4 a0v = ld4(vec + RWKV7_V_A0 * C + ch0), kkv = ld4(vec + RWKV7_V_K_K * C + ch0);
+  const float4 kav = ld4(vec + RWKV7_V_K_A * C + ch0);
+  float4 g_r, g_k, g_v, g_dv, g_dw, g_da, g_vf;
+  auto fetch = [&](int c0) {
+    const int tt = c0 + st_tok;
+    const int ts = tt < T ? tt : T - 1;  // clamped (its step is never run)
+    const int64_t o = base + (int64_t)ts * C + 4 * q;
+    g_r = ld4(p.rkv + o);
+    g_k = ld4(p.rkv + MC + o);
+    g_v = ld4(p.rkv + 2 * MC + o);
+    g_dv = ld4(p.d + o);
+    g_dw = ld4(p.d + MC + o);
+    g_da = ld4(p.d + 2 * MC + o);
+    g_vf = p.layer0 ? g_v : ld4(p.vfirst + o);
+  };
+  auto commit = [&](int c0, int buf) {
+    const int tt = c0 + st_tok;
+    const float k4[4] = {g_k.x, g_k.y, g_k.z, g_k.w};
+    const float vr[4] = {g_v.x, g_v.y, g_v.z, g_v.w}, dv[4] = {g_dv.x, g_dv.y, g_dv.z, g_dv.w};
+    const float dw[4] = {g_dw.x, g_dw.y, g_dw.z, g_dw.w}, da[4] = {g_da.x, g_da.y, g_da.z, g_da.w};
+    const float vf[4] = {g_vf.x, g_vf.y, g_vf.z, g_vf.w};
+    const float pv0[4] = {v0v.x, v0v.y, v0v.z, v0v.w}, pw0[4] = {w0v.x, w0v.y, w0v.z, w0v.w};
+    const float pa0[4] = {a0v.x, a0v.y, a0v.z, a0v.w}, pkk[4] = {kkv.x, kkv.y, kkv.z, kkv.w};
+    const float pka[4] = {kav.x, kav.y, kav.z, kav.w};
+    float w[4], kn[4], v[4], kk[4], ag[4];
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = p.layer0 ? vr[e] : vr[e] + sigmoidf_(pv0[e] + dv[e]) * (vf[e] - vr[e]);
+      w[e] = expf(-sigmoidf_(pw0[e] + dw[e]) / 1.6487212707001282f);
+      ag[e] = sigmoidf_(pa0[e] + da[e]);
+      kk[e] = k4[e] * pkk[e];
+      kn[e] = k4[e] + pka[e] * (k4[e] * ag[e] - k4[e]);
+      ss += kk[e] * kk[e];
+    }
+    const float inv = 1.f / fmaxf(sqrtf(sum16(ss)), 1e-12f);
+    float a[4], b[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a[e] = kk[e] * inv;
+      b[e] = -a[e] * ag[e];
+    }
+    s_in[buf][0][st_tok][q] = make_float4(w[0], w[1], w[2], w[3]);
+    s_in[buf][1][st_tok][q] = make_float4(a[0], a[1], a[2], a[3]);
+    s_in[buf][2][st_tok][q] = make_float4(b[0], b[1], b[2], b[3]);
+    s_in[buf][3][st_tok][q] = make_float4(kn[0], kn[1], kn[2], kn[3]);
+    s_in[buf][4][st_tok][q] = g_r;
+    s_in[buf][5][st_tok][q] = make_float4(v[0], v[1], v[2], v[3]);
+    // this workgroup's 16 channels of the values GroupNorm needs
+    if (tt < T && (q >> 2) == quarter) {
+      const int64_t o = base + (int64_t)tt * C + 4 * q;
+      *reinterpret_cast<float4 *>(p.kn_out + o) = make_float4(kn[0], kn[1], kn[2], kn[3]);
+      *reinterpret_cast<float4 *>(p.v_out + o) = make_float4(v[0], v[1], v[2], v[3]);
+      if (p.layer0) *reinterpret_cast<float4 *>(p.vfirst + o) = g_v;
+    }
+  };
+
+  float4 *Sp = reinterpret_cast<float4 *>(p.S + (((int64_t)bi * H + h) * kN + row) * kN) + lc;
+  float4 S = *Sp;
+
+  fetch(0);
+  commit(0, 0);
+  __syncthreads();
+  const int nch = (T + kCh - 1) / kCh;
+  for (int c = 0; c < nch; ++c) {
+    const int buf = c & 1;
+    if (c + 1 < nch) fetch((c + 1) * kCh);
+    const int steps = min(kCh, T - c * kCh);
+    const float *vrow = reinterpret_cast<const float *>(&s_in[buf][5][0][0]) + row;
+    struct In {
+      float4 w, a, b, k, r;
+      float v;
+    };
+    auto load_in = [&](In &x, int st) {
+      x.w = s_in[buf][0][st][lc];
+      x.a = s_in[buf][1][st][lc];
+      x.b = s_in[buf][2][st][lc];
+      x.k = s_in[buf][3][st][lc];
+      x.r = s_in[buf][4][st][lc];
+      x.v = vrow[st * kN];
+    };
+    auto step = [&](const In &x, int st) {
+      float p0 = S.x * x.a.x, p1 = S.z * x.a.z;
+      p0 = fmaf(S.y, x.a.y, p0);
+      p1 = fmaf(S.w, x.a.w, p1);
+      float4 pre;
+      pre.x = fmaf(S.x, x.w.x, x.v * x.k.x);
+      pre.y = fmaf(S.y, x.w.y, x.v * x.k.y);
+      pre.z = fmaf(S.z, x.w.z, x.v * x.k.z);
+      pre.w = fmaf(S.w, x.w.w, x.v * x.k.w);
+      const float sa = sum16(p0 + p1);
+      S.x = fmaf(sa, x.b.x, pre.x);
+      S.y = fmaf(sa, x.b.y, pre.y);
+      S.z = fmaf(sa, x.b.z, pre.z);
+      S.w = fmaf(sa, x.b.w, pre.w);
+      float y0 = S.x * x.r.x, y1 = S.z * x.r.z;
+      y0 = fmaf(S.y, x.r.y, y0);
+      y1 = fmaf(S.w, x.r.w, y1);
+      s_yp[st][t >> 4][lc] = y0 + y1;
+    };
+    // two input register sets in turn: the next step's inputs are read from
+    // LDS while the current step computes
+    In x0, x1;
+    load_in(x0, 0);
+    int st = 0;
+    for (; st + 1 < steps; st += 2) {
+      load_in(x1, st + 1);
+      step(x0, st);
+      load_in(x0, st + 2 < steps ? st + 2 : st + 1);
+      step(x1, st + 1);
+    }
+    if (st < steps) step(x0, st);
+    __syncthreads();
+    {  // y of (step t >> 4, row t & 15): sum of the 16 lane partials
+      const int ss = t >> 4, rr = t & 15;
+      if (ss < steps) {
+        float y = 0.f;
+#pragma unroll
+        for (int l = 0; l < 16; ++l) y += s_yp[ss][rr][l];
+        p.y[base + (int64_t)(c * kCh + ss) * C + quarter * 16 + rr] = y;
+      }
+    }
+    if (c + 1 < nch) commit((c + 1) * kCh, buf ^ 1);
+    __syncthreads();
+  }
+  *Sp = S;
+}
+
+int launch_wkv7_prefill(const PrefillScanArgs &p, hipStream_t st) {
+  if (p.T <= 0 || p.B <= 0 || p.H <= 0) return RWKV7_OK;
+  if (p.C != p.H * kN) return RWKV7_ESHAPE;
+  wkv7_prefill_kernel<<<dim3(4 * p.H, p.B), 256, 0, st>>>(p);
+  RWKV7_CHECK_LAUNCH();
+  return RWKV7_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Prefill elementwise stages. Rows m = b * T + t of the [M, C] activations.
 // ---------------------------------------------------------------------------
 
@@ -359,45 +527,6 @@ int launch_ln_shift(const LnShiftArgs &a, hipStream_t st) {
 #undef RWKV7_LNS_CASE
     default: return RWKV7_ESHAPE;
   }
-  RWKV7_CHECK_LAUNCH();
-  return RWKV7_OK;
-}
-
-
-// Gate math for prefill rows (demo/rwkv7_torch.py:203-224), one wave per
-// (row, head); lane = channel.
-__global__ __launch_bounds__(256) void tmix_gates_kernel(GatesArgs g) {
-  const int C = g.C;
-  const int gh = blockIdx.x * 4 + (threadIdx.x >> 6);  // global (row, head) index
-  const int H = C / kN;
-  const int m = gh / H, h = gh % H;
-  if (m >= g.M) return;
-  const int ch = h * kN + (threadIdx.x & 63);
-  const int64_t o = (int64_t)m * C + ch, MC = (int64_t)g.M * C;
-  const float *vec = g.vec;
-  const float k = g.rkv[MC + o];
-  float v = g.rkv[2 * MC + o];
-  if (g.layer0) {
-    g.vfirst[o] = v;
-  } else {
-    v = v + sigmoidf_(vec[RWKV7_V_V0 * C + ch] + g.d[o]) * (g.vfirst[o] - v);
-  }
-  const float w = expf(-sigmoidf_(vec[RWKV7_V_W0 * C + ch] + g.d[MC + o]) / 1.6487212707001282f);
-  const float ag = sigmoidf_(vec[RWKV7_V_A0 * C + ch] + g.d[2 * MC + o]);
-  const float kk = k * vec[RWKV7_V_K_K * C + ch];
-  const float kn = k + vec[RWKV7_V_K_A * C + ch] * (k * ag - k);
-  const float nrm = sqrtf(wave_sum(kk * kk));
-  const float kh = kk / fmaxf(nrm, 1e-12f);
-  g.wkab[o] = w;
-  g.wkab[MC + o] = kn;
-  g.wkab[2 * MC + o] = v;
-  g.wkab[3 * MC + o] = kh;
-  g.wkab[4 * MC + o] = -kh * ag;
-}
-
-int launch_tmix_gates(const GatesArgs &g, hipStream_t st) {
-  const int waves = g.M * (g.C / kN);
-  tmix_gates_kernel<<<(waves + 3) / 4, 256, 0, st>>>(g);
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;
 }
