@@ -196,6 +196,58 @@ int rwkv7_gemm_f16(const void *A, int64_t lda, const void *W, int64_t ldw,
                    void *Y, int64_t ldy, int32_t M, int32_t N, int32_t K,
                    int32_t epi, void *stream);
 
+/* ---- time-mix stage operators (f16 in and out, fp32 arithmetic) --------- */
+
+/* out[i] = exp(-sigmoid(w0[i] + x[i]) / sqrt(e)), i < C.
+ * Replaces fused_w_gate (src/rwkv_tl/kernels/gates.py:287-291). */
+int rwkv7_w_gate(const void *x, const void *w0, void *out, int32_t C, void *stream);
+
+/* out = v + sigmoid(v0 + v12) * (v_first - v), [C].
+ * Replaces fused_v_gate (gates.py:293-297). */
+int rwkv7_v_gate(const void *v, const void *v_first, const void *v0, const void *v12, void *out,
+                 int32_t C, void *stream);
+
+/* a = sigmoid(a0 + a_x), kk = k * k_k, k' = k + k_a * (k * a - k), [C].
+ * Replaces fused_a_kk_k (gates.py:299-313). */
+int rwkv7_a_kk_k(const void *a0, const void *a_x, const void *k, const void *k_k, const void *k_a,
+                 void *a_out, void *kk_out, void *k_out, int32_t C, void *stream);
+
+/* Operands of rwkv7_gates, all f16: rank inputs vr [Rv], wr [Rw], ar [Ra],
+ * gr [Rg] (first-step results, before activation); second-step matrices
+ * v2t [C, Rv], w2t [C, Rw], a2t [C, Ra], g2t [C, Rg]; vectors [C]. */
+typedef struct rwkv7_gates_io {
+  const void *vr, *wr, *ar, *gr;
+  const void *v2t, *w2t, *a2t, *g2t;
+  const void *v, *v_first, *k, *v0, *w0, *a0, *k_k, *k_a;
+  void *v_out, *w_out, *a_out, *kk_out, *k_out, *g_out;
+} rwkv7_gates_io;
+
+/* LoRA second steps with their activations (tanh for w, sigmoid for g) and
+ * the gate math: v' = v + sigmoid(v0 + v2t vr) (v_first - v),
+ * w = exp(-sigmoid(w0 + w2t tanh(wr)) / sqrt(e)), a = sigmoid(a0 + a2t ar),
+ * kk = k k_k, k' = k + k_a (k a - k), g = g2t sigmoid(gr).
+ * Replaces fused_gates (gates.py:125-213,315-357). */
+int rwkv7_gates(const rwkv7_gates_io *io, int32_t rank_v, int32_t rank_w, int32_t rank_a, int32_t rank_g,
+                int32_t C, void *stream);
+
+/* Packed LoRA first steps: out = [v1t; w1t; a1t; g1t] @ (xv | xw | xa | xg),
+ * W [Rv+Rw+Ra+Rg, C], inputs [C], out [Rv+Rw+Ra+Rg]; C % 8 == 0.
+ * Replaces fused_rank_gemv (gates.py:215-285). */
+int rwkv7_rank_gemv(const void *xv, const void *xw, const void *xa, const void *xg, const void *W, void *out,
+                    int32_t rank_v, int32_t rank_w, int32_t rank_a, int32_t rank_g, int32_t C, void *stream);
+
+/* Per head h < H over its 64 channels: kk_norm = kk / max(||kk||, 1e-12),
+ * b = -kk_norm * a; all [H, 64].
+ * Replaces fused_l2norm_neg_kk_a (src/rwkv_tl/kernels/dplr.py:45-71,229-235). */
+int rwkv7_l2norm_neg_kk_a(const void *kk, const void *a, void *kk_norm, void *b, int32_t H, void *stream);
+
+/* Per head: GroupNorm of y (biased variance, eps 64e-5) * ln_w + ln_b, plus
+ * (sum over the head of r * k * r_k) * v; y, r, k, v, r_k [H, 64], ln_w,
+ * ln_b and out [H * 64].
+ * Replaces fused_gn_rkrk (dplr.py:73-124,237-254). */
+int rwkv7_gn_rkrk(const void *y, const void *r, const void *k, const void *v, const void *r_k,
+                  const void *ln_w, const void *ln_b, void *out, int32_t H, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,6 +19,13 @@ What it restates (reference citations are ``path:line`` in yuyi2439/rwkv-tl):
 * ``tmix_seq`` / ``cmix_seq`` / ``prefill`` -- ``demo/rwkv7_torch.py:160-171,
   180-257`` (serial DPLR over t, ``:227-232``).
 * ``forward``        -- ``demo/_rwkv7_abc.py:74-89``.
+* operator level (the CPU branches of the reference's kernel wrappers, in
+  fp32): ``w_gate`` / ``v_gate`` / ``a_kk_k`` -- ``src/rwkv_tl/kernels/
+  gates.py:287-313``; ``gates`` -- ``gates.py:315-357``; ``rank_gemv`` --
+  ``gates.py:254-285``; ``l2norm_neg_kk_a`` -- ``src/rwkv_tl/kernels/
+  dplr.py:229-235``; ``gn_rkrk`` -- ``dplr.py:237-254``. They are pinned by
+  composing them into one token of ``time_mix`` (golden-pinned) and by the
+  closed forms of each formula (tests/test_oracle.py).
 
 The op order and dtypes of every torch call follow the reference line by line,
 so that with fp16 weights it reproduces the reference's fp16 rounding points
@@ -403,3 +410,75 @@ def forward(W: Weights, tokens: Tensor, state):
         return decode(W, tokens.reshape(-1), state)
     prefill(W, tokens[:-1], state)
     return decode(W, tokens[-1:], state)
+
+
+# --------------------------------------------------------------------------
+# Operator level: the time-mix stages one by one (fp32 arithmetic)
+# --------------------------------------------------------------------------
+
+
+def _f(*ts: Tensor) -> list[Tensor]:
+    return [t.float() for t in ts]
+
+
+def w_gate(x: Tensor, w0: Tensor) -> Tensor:
+    # src/rwkv_tl/kernels/gates.py:287-291
+    x, w0 = _f(x, w0)
+    return torch.exp(-torch.sigmoid(w0 + x) / SQRT_E)
+
+
+def v_gate(v: Tensor, v_first: Tensor, v0: Tensor, v12: Tensor) -> Tensor:
+    # gates.py:293-297
+    v, v_first, v0, v12 = _f(v, v_first, v0, v12)
+    return v + torch.sigmoid(v0 + v12) * (v_first - v)
+
+
+def a_kk_k(a0: Tensor, a_x: Tensor, k: Tensor, k_k: Tensor, k_a: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    # gates.py:299-313
+    a0, a_x, k, k_k, k_a = _f(a0, a_x, k, k_k, k_a)
+    a = torch.sigmoid(a0 + a_x)
+    return a, k * k_k, k + k_a * (k * a - k)
+
+
+def gates(vr, wr, ar, gr, v, v_first, k, v2t, w2t, a2t, g2t, v0, w0, a0, k_k, k_a):
+    """gates.py:315-357: returns ``(v, w, a, kk, k, g)``."""
+    vr, wr, ar, gr, v, v_first, k, v2t, w2t, a2t, g2t, v0, w0, a0, k_k, k_a = _f(
+        vr, wr, ar, gr, v, v_first, k, v2t, w2t, a2t, g2t, v0, w0, a0, k_k, k_a
+    )
+    v12 = v2t @ vr
+    w12 = w2t @ torch.tanh(wr)
+    a12 = a2t @ ar
+    g12 = g2t @ torch.sigmoid(gr)
+    v_out = v + torch.sigmoid(v0 + v12) * (v_first - v)
+    w_out = torch.exp(-torch.sigmoid(w0 + w12) / SQRT_E)
+    a = torch.sigmoid(a0 + a12)
+    return v_out, w_out, a, k * k_k, k + k_a * (k * a - k), g12
+
+
+def rank_gemv(xv, xw, xa, xg, packed, rv: int, rw: int, ra: int, rg: int) -> Tensor:
+    # gates.py:254-285 (rows of the packed [v1t; w1t; a1t; g1t] by segment)
+    xv, xw, xa, xg, packed = _f(xv, xw, xa, xg, packed)
+    return torch.cat(
+        [
+            packed[:rv] @ xv,
+            packed[rv : rv + rw] @ xw,
+            packed[rv + rw : rv + rw + ra] @ xa,
+            packed[rv + rw + ra : rv + rw + ra + rg] @ xg,
+        ]
+    )
+
+
+def l2norm_neg_kk_a(kk: Tensor, a: Tensor) -> tuple[Tensor, Tensor]:
+    # src/rwkv_tl/kernels/dplr.py:229-235, per head over dim 1
+    kk, a = _f(kk, a)
+    den = torch.sqrt(torch.sum(kk * kk, dim=1, keepdim=True))
+    kn = kk / torch.clamp(den, min=1e-12)
+    return kn, -kn * a
+
+
+def gn_rkrk(y, r, k, v, r_k, ln_w, ln_b) -> Tensor:
+    # dplr.py:237-254: GroupNorm over heads (eps 64e-5) + (sum r k r_k) v
+    y, r, k, v, r_k, ln_w, ln_b = _f(y, r, k, v, r_k, ln_w, ln_b)
+    h, n = y.shape
+    yf = F.group_norm(y.reshape(1, h * n), h, ln_w, ln_b, GN_EPS).reshape(-1)
+    return yf + (torch.sum(r * k * r_k, dim=1, keepdim=True) * v).reshape(-1)

@@ -486,4 +486,64 @@ int rwkv7_gemm_f16(const void *A, int64_t lda, const void *W, int64_t ldw, void 
   return launch_gemm_group(&p, 1, M, static_cast<hipStream_t>(stream), nullptr, nullptr);
 }
 
+static const uint16_t *h16(const void *p) { return static_cast<const uint16_t *>(p); }
+static uint16_t *h16(void *p) { return static_cast<uint16_t *>(p); }
+static hipStream_t hs(void *s) { return static_cast<hipStream_t>(s); }
+
+int rwkv7_w_gate(const void *x, const void *w0, void *out, int32_t C, void *stream) {
+  if (!x || !w0 || !out) return RWKV7_EINVAL;
+  if (C < 1) return RWKV7_ESHAPE;
+  return launch_w_gate(h16(x), h16(w0), h16(out), C, hs(stream));
+}
+
+int rwkv7_v_gate(const void *v, const void *v_first, const void *v0, const void *v12, void *out, int32_t C,
+                 void *stream) {
+  if (!v || !v_first || !v0 || !v12 || !out) return RWKV7_EINVAL;
+  if (C < 1) return RWKV7_ESHAPE;
+  return launch_v_gate(h16(v), h16(v_first), h16(v0), h16(v12), h16(out), C, hs(stream));
+}
+
+int rwkv7_a_kk_k(const void *a0, const void *a_x, const void *k, const void *k_k, const void *k_a, void *a_out,
+                 void *kk_out, void *k_out, int32_t C, void *stream) {
+  if (!a0 || !a_x || !k || !k_k || !k_a || !a_out || !kk_out || !k_out) return RWKV7_EINVAL;
+  if (C < 1) return RWKV7_ESHAPE;
+  return launch_a_kk_k(h16(a0), h16(a_x), h16(k), h16(k_k), h16(k_a), h16(a_out), h16(kk_out), h16(k_out), C,
+                       hs(stream));
+}
+
+int rwkv7_gates(const rwkv7_gates_io *io, int32_t rank_v, int32_t rank_w, int32_t rank_a, int32_t rank_g, int32_t C,
+                void *stream) {
+  if (!io) return RWKV7_EINVAL;
+  const void *ins[16] = {io->vr, io->wr, io->ar, io->gr, io->v2t, io->w2t, io->a2t, io->g2t,
+                         io->v,  io->v_first, io->k, io->v0, io->w0, io->a0, io->k_k, io->k_a};
+  const void *outs[6] = {io->v_out, io->w_out, io->a_out, io->kk_out, io->k_out, io->g_out};
+  for (const void *p : ins)
+    if (!p) return RWKV7_EINVAL;
+  for (const void *p : outs)
+    if (!p) return RWKV7_EINVAL;
+  if (C < 1 || rank_v < 1 || rank_w < 1 || rank_a < 1 || rank_g < 1) return RWKV7_ESHAPE;
+  return launch_gates(*io, rank_v, rank_w, rank_a, rank_g, C, hs(stream));
+}
+
+int rwkv7_rank_gemv(const void *xv, const void *xw, const void *xa, const void *xg, const void *W, void *out,
+                    int32_t rank_v, int32_t rank_w, int32_t rank_a, int32_t rank_g, int32_t C, void *stream) {
+  if (!xv || !xw || !xa || !xg || !W || !out) return RWKV7_EINVAL;
+  if (C < 8 || C % 8 || rank_v < 1 || rank_w < 1 || rank_a < 1 || rank_g < 1) return RWKV7_ESHAPE;
+  return launch_rank_gemv(h16(xv), h16(xw), h16(xa), h16(xg), h16(W), h16(out), rank_v, rank_w, rank_a, rank_g, C,
+                          hs(stream));
+}
+
+int rwkv7_l2norm_neg_kk_a(const void *kk, const void *a, void *kk_norm, void *b, int32_t H, void *stream) {
+  if (!kk || !a || !kk_norm || !b) return RWKV7_EINVAL;
+  if (H < 1) return RWKV7_ESHAPE;
+  return launch_l2norm(h16(kk), h16(a), h16(kk_norm), h16(b), H, hs(stream));
+}
+
+int rwkv7_gn_rkrk(const void *y, const void *r, const void *k, const void *v, const void *r_k, const void *ln_w,
+                  const void *ln_b, void *out, int32_t H, void *stream) {
+  if (!y || !r || !k || !v || !r_k || !ln_w || !ln_b || !out) return RWKV7_EINVAL;
+  if (H < 1) return RWKV7_ESHAPE;
+  return launch_gn_rkrk(h16(y), h16(r), h16(k), h16(v), h16(r_k), h16(ln_w), h16(ln_b), h16(out), H, hs(stream));
+}
+
 }  // extern "C"

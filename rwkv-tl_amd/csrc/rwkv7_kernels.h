@@ -105,6 +105,19 @@ constexpr int kGemmCounters = 1024;
 int64_t gemm_ws_bytes(int M, int cus);
 int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, float *part, unsigned *ctr);
 
+// Operator-level time-mix stages (ops.hip).
+int launch_w_gate(const uint16_t *x, const uint16_t *w0, uint16_t *out, int C, hipStream_t st);
+int launch_v_gate(const uint16_t *v, const uint16_t *vf, const uint16_t *v0, const uint16_t *v12, uint16_t *out,
+                  int C, hipStream_t st);
+int launch_a_kk_k(const uint16_t *a0, const uint16_t *ax, const uint16_t *k, const uint16_t *k_k,
+                  const uint16_t *k_a, uint16_t *a_out, uint16_t *kk_out, uint16_t *k_out, int C, hipStream_t st);
+int launch_gates(const rwkv7_gates_io &io, int rv, int rw, int ra, int rg, int C, hipStream_t st);
+int launch_rank_gemv(const uint16_t *xv, const uint16_t *xw, const uint16_t *xa, const uint16_t *xg,
+                     const uint16_t *W, uint16_t *out, int rv, int rw, int ra, int rg, int C, hipStream_t st);
+int launch_l2norm(const uint16_t *kk, const uint16_t *a, uint16_t *kn, uint16_t *b, int H, hipStream_t st);
+int launch_gn_rkrk(const uint16_t *y, const uint16_t *r, const uint16_t *k, const uint16_t *v, const uint16_t *r_k,
+                   const uint16_t *lw, const uint16_t *lb, uint16_t *out, int H, hipStream_t st);
+
 // One-token, one-sequence decode as a single persistent kernel (decode_mk.hip).
 int mk_cus();
 bool mk_supported(const rwkv7_dims &d, int G);

@@ -40,6 +40,13 @@ SYMBOLS = (
     "rwkv7_lerp",
     "rwkv7_gemv_f16",
     "rwkv7_gemm_f16",
+    "rwkv7_w_gate",
+    "rwkv7_v_gate",
+    "rwkv7_a_kk_k",
+    "rwkv7_gates",
+    "rwkv7_rank_gemv",
+    "rwkv7_l2norm_neg_kk_a",
+    "rwkv7_gn_rkrk",
 )
 
 
@@ -87,6 +94,19 @@ class StateDesc(ctypes.Structure):
     ]
 
 
+class GatesIO(ctypes.Structure):
+    """``rwkv7_gates_io``: operands of ``rwkv7_gates`` (all f16 device pointers)."""
+
+    _fields_ = [
+        (n, ctypes.c_void_p)
+        for n in (
+            "vr", "wr", "ar", "gr", "v2t", "w2t", "a2t", "g2t",
+            "v", "v_first", "k", "v0", "w0", "a0", "k_k", "k_a",
+            "v_out", "w_out", "a_out", "kk_out", "k_out", "g_out",
+        )
+    ]
+
+
 class HipError(RuntimeError):
     """A nonzero return code from the HIP library."""
 
@@ -116,6 +136,13 @@ def _declare(lib: ctypes.CDLL) -> None:
         "rwkv7_lerp": (ctypes.c_int, [vp, vp, vp, i32, vp, vp, i32, vp]),
         "rwkv7_gemv_f16": (ctypes.c_int, [vp, vp, i64, vp, i32, i32, vp]),
         "rwkv7_gemm_f16": (ctypes.c_int, [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp]),
+        "rwkv7_w_gate": (ctypes.c_int, [vp, vp, vp, i32, vp]),
+        "rwkv7_v_gate": (ctypes.c_int, [vp, vp, vp, vp, vp, i32, vp]),
+        "rwkv7_a_kk_k": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, i32, vp]),
+        "rwkv7_gates": (ctypes.c_int, [ctypes.POINTER(GatesIO), i32, i32, i32, i32, i32, vp]),
+        "rwkv7_rank_gemv": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]),
+        "rwkv7_l2norm_neg_kk_a": (ctypes.c_int, [vp, vp, vp, vp, i32, vp]),
+        "rwkv7_gn_rkrk": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, i32, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

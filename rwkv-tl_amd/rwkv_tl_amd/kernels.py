@@ -12,9 +12,16 @@ dtype). There is no CPU branch: the reference's in-function torch fallbacks
   (``lerp.py:140-198``).
 * ``layer_norm`` (``weight.py:14-15``), ``gemv`` and ``gemm`` (the projection
   GEMMs of ``gemm.py:215-305``), ``fused_rkv_gemm`` (``gemm.py:215-262``).
+* The time-mix stage operators, f16 in and out: ``fused_w_gate``,
+  ``fused_v_gate``, ``fused_a_kk_k`` (``gates.py:287-313``), ``fused_gates``
+  (``gates.py:315-357``), ``fused_rank_gemv`` (``gates.py:254-285``),
+  ``fused_l2norm_neg_kk_a`` (``dplr.py:229-235``), ``fused_gn_rkrk``
+  (``dplr.py:237-254``).
 """
 
 from __future__ import annotations
+
+import ctypes
 
 import torch
 from torch import Tensor
@@ -173,3 +180,111 @@ def fused_rkv_gemm(xr: Tensor, xk: Tensor, xv: Tensor, Wb: Tensor) -> Tensor:
     orientation (``gemm.py:215-262``); returns f16 [3, T, C]."""
     outs = [gemm(x.contiguous(), Wb[i].T.contiguous(), "f16") for i, x in enumerate((xr, xk, xv))]
     return torch.stack(outs)
+
+
+# ---------------------------------------------------------------------------
+# time-mix stage operators (f16 tensors, fp32 arithmetic inside)
+# ---------------------------------------------------------------------------
+
+
+def _f16(*ts: Tensor) -> None:
+    _dev(*ts)
+    for t in ts:
+        _need(t.dtype == torch.float16, f"expected float16, got {t.dtype}")
+
+
+def _vecs(C: int, *ts: Tensor) -> None:
+    _f16(*ts)
+    for t in ts:
+        _need(t.numel() == C, f"expected {C} elements, got shape {tuple(t.shape)}")
+
+
+def fused_w_gate(x: Tensor, w0: Tensor) -> Tensor:
+    """``exp(-sigmoid(w0 + x) / sqrt(e))`` over [C] (``gates.py:287-291``)."""
+    C = x.numel()
+    _vecs(C, x, w0)
+    out = torch.empty_like(x)
+    _lib.check(_lib.load().rwkv7_w_gate(x.data_ptr(), w0.data_ptr(), out.data_ptr(), C, _lib.stream_handle()),
+               "rwkv7_w_gate")
+    return out
+
+
+def fused_v_gate(v: Tensor, v_first: Tensor, v0: Tensor, v12: Tensor) -> Tensor:
+    """``v + sigmoid(v0 + v12) * (v_first - v)`` over [C] (``gates.py:293-297``)."""
+    C = v.numel()
+    _vecs(C, v, v_first, v0, v12)
+    out = torch.empty_like(v)
+    _lib.check(_lib.load().rwkv7_v_gate(v.data_ptr(), v_first.data_ptr(), v0.data_ptr(), v12.data_ptr(),
+                                        out.data_ptr(), C, _lib.stream_handle()), "rwkv7_v_gate")
+    return out
+
+
+def fused_a_kk_k(a0: Tensor, a_x: Tensor, k: Tensor, k_k: Tensor, k_a: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """``(sigmoid(a0 + a_x), k * k_k, k + k_a * (k * a - k))`` over [C] (``gates.py:299-313``)."""
+    C = k.numel()
+    _vecs(C, a0, a_x, k, k_k, k_a)
+    a, kk, kn = (torch.empty_like(k) for _ in range(3))
+    _lib.check(_lib.load().rwkv7_a_kk_k(a0.data_ptr(), a_x.data_ptr(), k.data_ptr(), k_k.data_ptr(), k_a.data_ptr(),
+                                        a.data_ptr(), kk.data_ptr(), kn.data_ptr(), C, _lib.stream_handle()),
+               "rwkv7_a_kk_k")
+    return a, kk, kn
+
+
+def fused_gates(vr: Tensor, wr: Tensor, ar: Tensor, gr: Tensor, v: Tensor, v_first: Tensor, k: Tensor,
+                v2t: Tensor, w2t: Tensor, a2t: Tensor, g2t: Tensor, v0: Tensor, w0: Tensor, a0: Tensor,
+                k_k: Tensor, k_a: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """LoRA second steps + gate math; returns ``(v, w, a, kk, k, g)``, each [C] (``gates.py:315-357``).
+
+    ``vr/wr/ar/gr`` are the first-step results [R] before activation,
+    ``v2t/w2t/a2t/g2t`` the second-step matrices [C, R]."""
+    C = v.numel()
+    _vecs(C, v, v_first, k, v0, w0, a0, k_k, k_a)
+    _f16(vr, wr, ar, gr, v2t, w2t, a2t, g2t)
+    ranks = []
+    for r_, m_ in ((vr, v2t), (wr, w2t), (ar, a2t), (gr, g2t)):
+        _need(m_.dim() == 2 and m_.shape == (C, r_.numel()), f"rank matrix {tuple(m_.shape)} vs [{C}, {r_.numel()}]")
+        ranks.append(r_.numel())
+    outs = [torch.empty_like(v) for _ in range(6)]
+    io = _lib.GatesIO(*(t.data_ptr() for t in (vr, wr, ar, gr, v2t, w2t, a2t, g2t, v, v_first, k, v0, w0, a0,
+                                               k_k, k_a, *outs)))
+    _lib.check(_lib.load().rwkv7_gates(ctypes.byref(io), *ranks, C, _lib.stream_handle()), "rwkv7_gates")
+    return tuple(outs)
+
+
+def fused_rank_gemv(xv: Tensor, xw: Tensor, xa: Tensor, xg: Tensor, packed: Tensor,
+                    rv: int, rw: int, ra: int, rg: int) -> Tensor:
+    """``[v1t; w1t; a1t; g1t] @ [xv; xw; xa; xg]`` by row segment; returns [rv+rw+ra+rg] (``gates.py:254-285``)."""
+    C = xv.numel()
+    _vecs(C, xv, xw, xa, xg)
+    _f16(packed)
+    _need(packed.shape == (rv + rw + ra + rg, C), f"packed {tuple(packed.shape)} vs [{rv + rw + ra + rg}, {C}]")
+    out = torch.empty(rv + rw + ra + rg, dtype=torch.float16, device=xv.device)
+    _lib.check(_lib.load().rwkv7_rank_gemv(xv.data_ptr(), xw.data_ptr(), xa.data_ptr(), xg.data_ptr(),
+                                           packed.data_ptr(), out.data_ptr(), rv, rw, ra, rg, C,
+                                           _lib.stream_handle()), "rwkv7_rank_gemv")
+    return out
+
+
+def fused_l2norm_neg_kk_a(kk: Tensor, a: Tensor) -> tuple[Tensor, Tensor]:
+    """Per head ``kk / max(||kk||, 1e-12)`` and ``-(that) * a``, [H, 64] (``dplr.py:229-235``)."""
+    _f16(kk, a)
+    _need(kk.dim() == 2 and kk.shape[1] == N and a.shape == kk.shape, "kk and a must be [H, 64]")
+    kn, b = torch.empty_like(kk), torch.empty_like(kk)
+    _lib.check(_lib.load().rwkv7_l2norm_neg_kk_a(kk.data_ptr(), a.data_ptr(), kn.data_ptr(), b.data_ptr(),
+                                                 kk.shape[0], _lib.stream_handle()), "rwkv7_l2norm_neg_kk_a")
+    return kn, b
+
+
+def fused_gn_rkrk(y: Tensor, r: Tensor, k: Tensor, v: Tensor, r_k: Tensor, ln_xW: Tensor, ln_xB: Tensor) -> Tensor:
+    """GroupNorm per head (eps 64e-5) + ``(sum r k r_k) * v``; [H, 64] in, [H*64] out (``dplr.py:237-254``)."""
+    _f16(y, r, k, v, r_k, ln_xW, ln_xB)
+    _need(y.dim() == 2 and y.shape[1] == N, "y must be [H, 64]")
+    for t in (r, k, v, r_k):
+        _need(t.shape == y.shape, "r, k, v, r_k must match y")
+    H = y.shape[0]
+    _need(ln_xW.numel() == H * N and ln_xB.numel() == H * N, "ln_x weight and bias must have H*64 elements")
+    out = torch.empty(H * N, dtype=torch.float16, device=y.device)
+    _lib.check(_lib.load().rwkv7_gn_rkrk(y.data_ptr(), r.data_ptr(), k.data_ptr(), v.data_ptr(), r_k.data_ptr(),
+                                         ln_xW.data_ptr(), ln_xB.data_ptr(), out.data_ptr(), H,
+                                         _lib.stream_handle()), "rwkv7_gn_rkrk")
+    return out

@@ -11,6 +11,10 @@ same seeded inputs:
 * LayerNorm vs ``F.layer_norm``; token-shift lerps vs the closed form with the
   reference's test tolerance (test/test_kernels.py:17-43: fp16, C=768, seeds
   42..49, 0.01).
+* The time-mix stage operators (single gates, fused gates, packed LoRA first
+  step, L2 norm, GroupNorm + bonus) vs the oracle's operator restatements on
+  the same fp16 inputs: f16 outputs within rtol 4e-3, atol 4e-3 (one or two
+  fp16 ulps at these magnitudes; both sides compute in fp32).
 """
 
 from __future__ import annotations
@@ -167,3 +171,76 @@ def test_lerp_copy_variants_update_state_after_read(cuda):
     buf = torch.zeros_like(x)
     outs = K.fused_lerp6_copy(x, prev0, *([mu] * 6), buf)
     assert len(outs) == 6 and torch.equal(buf, x)
+
+
+# --------------------------------------------------------------------------
+# time-mix stage operators
+# --------------------------------------------------------------------------
+
+OP_TOL = dict(rtol=4e-3, atol=4e-3)
+
+
+def _h(g, *shape, scale=1.0, shift=0.0):
+    return (torch.randn(*shape, generator=g) * scale + shift).half()
+
+
+@pytest.mark.parametrize("C", [1, 768, 1024, 4099])
+def test_single_gates_match_oracle(C, cuda):
+    g = torch.Generator().manual_seed(C)
+    x, w0, v, vf, v0, v12, a0, ax, k, kk, ka = (_h(g, C) for _ in range(11))
+    dev = lambda *ts: [t.to(cuda) for t in ts]  # noqa: E731
+    torch.testing.assert_close(K.fused_w_gate(*dev(x, w0)).cpu().float(), R.w_gate(x, w0), **OP_TOL)
+    torch.testing.assert_close(K.fused_v_gate(*dev(v, vf, v0, v12)).cpu().float(), R.v_gate(v, vf, v0, v12), **OP_TOL)
+    got = K.fused_a_kk_k(*dev(a0, ax, k, kk, ka))
+    for gg, ww in zip(got, R.a_kk_k(a0, ax, k, kk, ka)):
+        torch.testing.assert_close(gg.cpu().float(), ww, **OP_TOL)
+
+
+@pytest.mark.parametrize("C,ranks", [(1024, (32, 64, 64, 128)), (768, (16, 32, 32, 64)), (256, (8, 24, 40, 72))])
+def test_fused_gates_match_oracle(C, ranks, cuda):
+    g = torch.Generator().manual_seed(C + sum(ranks))
+    rv, rw, ra, rg = ranks
+    vr, wr, ar, gr = (_h(g, r) for r in ranks)
+    mats = [_h(g, C, r, scale=0.1) for r in ranks]
+    vecs = [_h(g, C) for _ in range(8)]  # v, v_first, k, v0, w0, a0, k_k, k_a
+    args = (vr, wr, ar, gr, *vecs[:3], *mats, *vecs[3:])
+    got = K.fused_gates(*(t.to(cuda) for t in args))
+    want = R.gates(*args)
+    for name, gg, ww in zip(("v", "w", "a", "kk", "k", "g"), got, want):
+        torch.testing.assert_close(gg.cpu().float(), ww, **OP_TOL, msg=name)
+
+
+@pytest.mark.parametrize("C,ranks", [(1024, (32, 64, 64, 128)), (2048, (64, 64, 96, 256)), (256, (8, 24, 40, 72))])
+def test_fused_rank_gemv_matches_oracle(C, ranks, cuda):
+    g = torch.Generator().manual_seed(C)
+    xs = [_h(g, C) for _ in range(4)]
+    packed = _h(g, sum(ranks), C, scale=0.05)
+    got = K.fused_rank_gemv(*(t.to(cuda) for t in xs), packed.to(cuda), *ranks)
+    torch.testing.assert_close(got.cpu().float(), R.rank_gemv(*xs, packed, *ranks), **OP_TOL)
+
+
+@pytest.mark.parametrize("H", [1, 12, 16, 33])
+def test_l2norm_and_gn_rkrk_match_oracle(H, cuda):
+    g = torch.Generator().manual_seed(H)
+    kk, a = _h(g, H, 64), torch.rand(H, 64, generator=g).half()
+    kk[0] = 0  # the zero head: clamped denominator, outputs stay zero
+    kn, b = K.fused_l2norm_neg_kk_a(kk.to(cuda), a.to(cuda))
+    wkn, wb = R.l2norm_neg_kk_a(kk, a)
+    torch.testing.assert_close(kn.cpu().float(), wkn, **OP_TOL)
+    torch.testing.assert_close(b.cpu().float(), wb, **OP_TOL)
+    y, r, k, v, rk = (_h(g, H, 64) for _ in range(5))
+    lw, lb = _h(g, H * 64, scale=0.2, shift=1.0), _h(g, H * 64, scale=0.2)
+    got = K.fused_gn_rkrk(*(t.to(cuda) for t in (y, r, k, v, rk, lw, lb)))
+    torch.testing.assert_close(got.cpu().float(), R.gn_rkrk(y, r, k, v, rk, lw, lb), rtol=1e-2, atol=1e-2)
+
+
+def test_stage_operators_reject_bad_shapes(cuda):
+    h = lambda *s: torch.zeros(*s, dtype=torch.float16, device=cuda)  # noqa: E731
+    with pytest.raises(ValueError):
+        K.fused_w_gate(h(8), h(9))
+    with pytest.raises(ValueError):
+        K.fused_l2norm_neg_kk_a(h(2, 32), h(2, 32))
+    with pytest.raises(ValueError):
+        K.fused_rank_gemv(h(64), h(64), h(64), h(64), h(10, 64), 2, 2, 2, 2)
+    with pytest.raises(ValueError):
+        K.fused_w_gate(h(8).float(), h(8))

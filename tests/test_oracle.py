@@ -216,3 +216,100 @@ def test_layernorm_closed_forms():
     const = torch.full((C,), 3.0, dtype=torch.float64)
     ln2 = R._LN({"p.weight": torch.ones(C, dtype=torch.float64), "p.bias": torch.full((C,), 0.5, dtype=torch.float64)}, "p")
     torch.testing.assert_close(ln2(const), torch.full((C,), 0.5, dtype=torch.float64))
+
+
+# --------------------------------------------------------------------------
+# Operator-level oracle (the time-mix stages one by one)
+# --------------------------------------------------------------------------
+
+
+def test_operator_oracle_composes_to_time_mix():
+    """One token of ``time_mix`` (pinned by the reference's golden vectors)
+    rebuilt from the operator restatements: rank_gemv -> gates -> l2norm_neg_kk_a
+    -> wkv7_step -> gn_rkrk -> gate and o-projection. A dropped term, a wrong
+    operand or a swapped activation in any operator breaks the match."""
+    sd = make_random_state_dict("tiny", seed=3, dtype=torch.float32)
+    W = R.Weights(sd, dtype=torch.float32)
+    H, C, N = W.H, W.C, 64
+    att = W.blocks[1].att
+    g = torch.Generator().manual_seed(11)
+    x0, prev, v_first = (torch.randn(C, generator=g) for _ in range(3))
+    S0 = torch.randn(H, N, N, generator=g) * 0.1
+    st = {"x": prev.clone(), "rnn": S0.clone()}
+    out_ref, _ = R.time_mix(att, x0, v_first.clone(), st, H, N)
+
+    x = att.ln_pre(x0)
+    xr, xw, xk, xv, xa, xg = (x + getattr(att, n) * (prev - x) for n in ("x_r", "x_w", "x_k", "x_v", "x_a", "x_g"))
+    r, k, v = xr @ att.rkvWt[0], xk @ att.rkvWt[1], xv @ att.rkvWt[2]
+    ranks = [att.v1.shape[1], att.w1.shape[1], att.a1.shape[1], att.g1.shape[1]]
+    packed = torch.cat([att.v1.t(), att.w1.t(), att.a1.t(), att.g1.t()])
+    vr, wr, ar, gr = R.rank_gemv(xv, xw, xa, xg, packed, *ranks).split(ranks)
+    vec = lambda t: t.reshape(-1)  # noqa: E731
+    v2, w2, a, kk, k2, gg = R.gates(vr, wr, ar, gr, v, v_first, k, att.v2.t(), att.w2.t(), att.a2.t(), att.g2.t(),
+                                    vec(att.v0), vec(att.w0), vec(att.a0), vec(att.k_k), vec(att.k_a))
+    kn, b = R.l2norm_neg_kk_a(kk.reshape(H, N), a.reshape(H, N))
+    hn = lambda t: t.reshape(H, N)  # noqa: E731
+    y, S1 = R.wkv7_step(S0, hn(r), hn(w2), hn(k2), hn(v2), kn, b)
+    yo = R.gn_rkrk(y, hn(r), hn(k2), hn(v2), att.r_k, att.ln_x.w, att.ln_x.b)
+    out = x0 + (yo * gg) @ att.oWt
+    torch.testing.assert_close(out, out_ref, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(S1, st["rnn"], rtol=1e-5, atol=1e-6)
+
+
+def test_operator_oracle_closed_forms():
+    """Limits and special points that fix each formula."""
+    e = math.exp
+    C = 8
+    z, one = torch.zeros(C), torch.ones(C)
+    big = torch.full((C,), 80.0)
+    sq = math.sqrt(math.e)
+    torch.testing.assert_close(R.w_gate(z, z), torch.full((C,), e(-0.5 / sq)))
+    torch.testing.assert_close(R.w_gate(big, z), torch.full((C,), e(-1 / sq)))
+    torch.testing.assert_close(R.w_gate(-big, z), one)
+    v, vf = torch.arange(C, dtype=torch.float32), -torch.arange(C, dtype=torch.float32) - 1
+    torch.testing.assert_close(R.v_gate(v, vf, -big, z), v)
+    torch.testing.assert_close(R.v_gate(v, vf, big, z), vf)
+    torch.testing.assert_close(R.v_gate(v, vf, z, z), (v + vf) / 2)
+    k, kk_ = torch.linspace(-2, 2, C), torch.linspace(0.5, 1.5, C)
+    a, kk, k0 = R.a_kk_k(z, z, k, kk_, z)
+    torch.testing.assert_close(a, one / 2)
+    torch.testing.assert_close(kk, k * kk_)
+    torch.testing.assert_close(k0, k)  # k_a = 0 keeps k
+    _, _, k1 = R.a_kk_k(z, z, k, kk_, one)
+    torch.testing.assert_close(k1, k * 0.5)  # k_a = 1 gives k * a
+    # L2 norm: unit rows, the zero row stays zero (clamp at 1e-12), b = -kn * a
+    H = 3
+    kkh = torch.randn(H, 64, generator=torch.Generator().manual_seed(2))
+    kkh[1] = 0
+    ah = torch.rand(H, 64, generator=torch.Generator().manual_seed(3))
+    kn, b = R.l2norm_neg_kk_a(kkh, ah)
+    torch.testing.assert_close(kn.norm(dim=1), torch.tensor([1.0, 0.0, 1.0]))
+    torch.testing.assert_close(b, -kn * ah)
+    # GroupNorm: a constant head normalises to 0 (out = ln_b + rk * v); a head
+    # 0..63 has mean 31.5 and biased variance (64^2 - 1) / 12
+    y = torch.stack([torch.full((64,), 5.0), torch.arange(64, dtype=torch.float32)])
+    r_, k_, v_, rk_ = (torch.rand(2, 64, generator=torch.Generator().manual_seed(s)) for s in (4, 5, 6, 7))
+    lw, lb = torch.rand(128, generator=torch.Generator().manual_seed(8)), torch.rand(128, generator=torch.Generator().manual_seed(9))
+    out = R.gn_rkrk(y, r_, k_, v_, rk_, lw, lb).reshape(2, 64)
+    bonus = (r_ * k_ * rk_).sum(1, keepdim=True) * v_
+    torch.testing.assert_close(out[0], lb[:64] + bonus[0])
+    yn = (torch.arange(64.0) - 31.5) / math.sqrt((64 * 64 - 1) / 12 + 64e-5)
+    torch.testing.assert_close(out[1], yn * lw[64:] + lb[64:] + bonus[1])
+    # rank_gemv: a one-hot row j selects element j of its segment's input
+    rv, rw, ra, rg, Cx = 2, 3, 1, 2, 8
+    xs = [torch.randn(Cx, generator=torch.Generator().manual_seed(20 + i)) for i in range(4)]
+    packed = torch.zeros(rv + rw + ra + rg, Cx)
+    for j in range(rv + rw + ra + rg):
+        packed[j, j] = 1.0
+    seg = [0] * rv + [1] * rw + [2] * ra + [3] * rg
+    torch.testing.assert_close(R.rank_gemv(*xs, packed, rv, rw, ra, rg), torch.stack([xs[seg[j]][j] for j in range(8)]))
+    # gates with zero second-step matrices: v12 = w12 = a12 = g12 = 0
+    Rk = 4
+    zr, zm = torch.zeros(Rk), torch.zeros(C, Rk)
+    v0_, w0_, a0_ = torch.linspace(-1, 1, C), torch.linspace(-2, 2, C), torch.linspace(-3, 3, C)
+    vo, wo, ao, kko, ko, go = R.gates(zr, zr, zr, zr, v, vf, k, zm, zm, zm, zm, v0_, w0_, a0_, kk_, one)
+    torch.testing.assert_close(vo, v + torch.sigmoid(v0_) * (vf - v))
+    torch.testing.assert_close(wo, torch.exp(-torch.sigmoid(w0_) / sq))
+    torch.testing.assert_close(ao, torch.sigmoid(a0_))
+    torch.testing.assert_close(ko, k * torch.sigmoid(a0_))
+    torch.testing.assert_close(go, z)
