@@ -113,7 +113,8 @@ struct MkArgs {
   uint16_t *cmix_x;
   const int64_t *tok;
   uint16_t *logits;
-  // hand-off words; x, core and hid have kRep replicas of C, C and F words
+  // hand-off words; x, proj, core and hid have kRep replicas of C, 3C+SR, C
+  // and F words
   uint64_t *x_ex, *proj_ex, *core_ex, *hid_ex;
   unsigned *sync;
 };
@@ -436,11 +437,12 @@ RWKV7_DEV void comm_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
   constexpr int DP = 16 / NJP;
   const int C = m.C, SR = m.SR, L = m.L;
   const int h = m.g, rv = a.rv, rwa = a.rv + a.rw, rwaa = a.rv + a.rw + a.ra;
-  const __amdgpu_buffer_rsrc_t r_proj = words_rsrc(a.proj_ex, 3 * C + SR);
+  const __amdgpu_buffer_rsrc_t r_proj = words_rsrc(a.proj_ex + (int64_t)(h % kRep) * (3 * C + SR), 3 * C + SR);
   for (int l = 0; l < L; ++l) {
     // r, k, v of this head and the whole LoRA first step, activated on arrival
     // (tanh for w, sigmoid for g)
-    comm_poll<NJP, DP>(cx, cw, r_proj, 192 + SR, 0, cx.tag(5 * l),
+    // (a sparse probe first: this poll starts a whole layer before its data)
+    comm_poll<NJP, DP>(cx, cw, r_proj, 192 + SR, 32, cx.tag(5 * l),
                        [&](int i) { return i < 192 ? (i >> 6) * C + h * kN + (i & 63) : 3 * C + (i - 192); },
                        [&](int i, float v) {
                          const int j = i - 192;
@@ -542,9 +544,11 @@ RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
       s.core[384 + t] = v;
     }
     __syncthreads();  // B2b
-    if (mt < 4 * kN) {  // wkv7: 4 threads per state row, 16 columns each
-      const int row = mt >> 2, j0 = (mt & 3) * 16;
-      float Sv[16];
+    // wkv7: 4 threads per state row, 16 columns each; the new state is written
+    // back only after the core output is published (wave 0 publishes first)
+    const int row = mt >> 2, j0 = (mt & 3) * 16;
+    float Sv[16];
+    if (mt < 4 * kN) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         Sv[4 * e] = S4[e].x; Sv[4 * e + 1] = S4[e].y; Sv[4 * e + 2] = S4[e].z; Sv[4 * e + 3] = S4[e].w;
@@ -574,9 +578,6 @@ RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
         y = fmaf(Sv[e], rv16[e], y);
       }
       y = sum4(y);
-      float4 *Sp = reinterpret_cast<float4 *>(a.rnn + (((int64_t)l * H + g) * kN + row) * kN + j0);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) Sp[e] = make_float4(Sv[4 * e], Sv[4 * e + 1], Sv[4 * e + 2], Sv[4 * e + 3]);
       if ((mt & 3) == 0) s_y[row] = y;
     }
     __syncthreads();  // B2c
@@ -589,6 +590,11 @@ RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
       const float out = (yn + rk * v) * gate;
 #pragma unroll
       for (int rp = 0; rp < kRep; ++rp) publish(a.core_ex + (int64_t)rp * C + g * kN + lane, cx.tag(5 * l + 1), out);
+    }
+    if (mt < 4 * kN) {
+      float4 *Sp = reinterpret_cast<float4 *>(a.rnn + (((int64_t)l * H + g) * kN + row) * kN + j0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Sp[e] = make_float4(Sv[4 * e], Sv[4 * e + 1], Sv[4 * e + 2], Sv[4 * e + 3]);
     }
     // next layer's operands: a whole layer to arrive
     refresh();
@@ -746,12 +752,13 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
         const int r = m.p1a + wv + kMW * i;
         if (r < m.p1b) {
           const float d = row_dot<CPL>(w1[i], s.mix + (m.seg_of(r) - m.seg0) * C, nchC);
-          if (lane == 0) publish(a.proj_ex + r, tg, d);
+          if (lane < kRep) publish(a.proj_ex + (int64_t)lane * (3 * C + m.SR) + r, tg, d);
         }
       }
     }
     count_publish();
-    // every load of the rest of the layer, issued while the head workgroups work
+    // every load of the rest of the layer, issued while the head workgroups wait
+    // for their input (that hand-off is slow anyway) and compute
     refresh();
     pre_p3(l);
     pre_p4(l);
@@ -935,7 +942,7 @@ static int64_t mk_lds_bytes(int C, int F, int SR) { return mk_lds_floats(C, F, S
 // Exchange region: sync words, then x (kRep x C), proj (3C+SR), core
 // (kRep x C), hid (kRep x F) as u64.
 int64_t mk_exchange_bytes(int C, int F, int SR) {
-  return 256 + (int64_t)(kRep * C + 3 * C + SR + kRep * C + kRep * F) * 8;
+  return 256 + (int64_t)(kRep * C + kRep * (3 * C + SR) + kRep * C + kRep * F) * 8;
 }
 
 bool mk_supported(const rwkv7_dims &d, int G) {
@@ -1015,7 +1022,7 @@ int launch_decode_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const 
   uint64_t *ex = reinterpret_cast<uint64_t *>(xreg + 256);
   a.x_ex = ex;
   a.proj_ex = a.x_ex + (int64_t)kRep * C;
-  a.core_ex = a.proj_ex + 3 * C + SR;
+  a.core_ex = a.proj_ex + (int64_t)kRep * (3 * C + SR);
   a.hid_ex = a.core_ex + (int64_t)kRep * C;
   const int64_t lds = mk_lds_bytes(C, F, SR);
   const void *fn = (const void *)RWKV7_MK_INSTANCE;
