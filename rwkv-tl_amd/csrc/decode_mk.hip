@@ -415,7 +415,7 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     __syncthreads();  // A3
     pubs += kMW;
     wait_local(cx, s.pubs, pubs);
-    comm_poll<NJX, DX>(cx, cw, r_x, C, 0, cx.tag(ph + 2), Ident(), to(s.x4));
+    comm_poll<NJX, DX>(cx, cw, r_x, C, 64, cx.tag(ph + 2), Ident(), to(s.x4));
     __syncthreads();  // A4
     __syncthreads();  // B4
     pubs += kMW;
@@ -427,7 +427,7 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     __syncthreads();  // A5
     pubs += kMW;
     wait_local(cx, s.pubs, pubs);
-    comm_poll<NJX, DX>(cx, cw, r_x, C, 0, cx.tag(ph + 4), Ident(), to(s.x1));
+    comm_poll<NJX, DX>(cx, cw, r_x, C, 64, cx.tag(ph + 4), Ident(), to(s.x1));
   }
   __syncthreads();  // AH
   __syncthreads();  // BH
