@@ -423,7 +423,8 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     // sparse probe first: a full read of the hidden vector by every worker
     // per round would flood the fabric the data has to arrive through
     comm_poll<NJF, DF>(cx, cw, r_hid, F / 2, 64, cx.tag(ph + 3), Ident(), to(s.hid));
-    comm_poll<NJF, DF>(cx, cw, r_hid2, F / 2, 64, cx.tag(ph + 3), Ident(), to(s.hid + F / 2));
+    // (no probe: once the first half is in, the second nearly always is)
+    comm_poll<NJF, DF>(cx, cw, r_hid2, F / 2, 0, cx.tag(ph + 3), Ident(), to(s.hid + F / 2));
     __syncthreads();  // A5
     pubs += kMW;
     wait_local(cx, s.pubs, pubs);
