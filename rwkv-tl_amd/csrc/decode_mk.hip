@@ -420,10 +420,9 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     __syncthreads();  // B4
     pubs += kMW;
     wait_local(cx, s.pubs, pubs);
-    // sparse probe first: a full read of the hidden vector by every worker
-    // per round would flood the fabric the data has to arrive through
-    comm_poll<NJF, DF>(cx, cw, r_hid, F / 2, 64, cx.tag(ph + 3), Ident(), to(s.hid));
-    // (no probe: once the first half is in, the second nearly always is)
+    // no probe: every worker publishes its P4 rows within a fraction of a
+    // microsecond of the others, so the first full read finds nearly all
+    comm_poll<NJF, DF>(cx, cw, r_hid, F / 2, 0, cx.tag(ph + 3), Ident(), to(s.hid));
     comm_poll<NJF, DF>(cx, cw, r_hid2, F / 2, 0, cx.tag(ph + 3), Ident(), to(s.hid + F / 2));
     __syncthreads();  // A5
     pubs += kMW;
