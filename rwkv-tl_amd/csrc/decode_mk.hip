@@ -154,10 +154,11 @@ struct MkLds {
   float *mix4;    // [C]  P4 mix
   float *hid;     // [F]  P5 input
   unsigned *pubs; // count of math-wave publish steps (the comm waves' start signal)
+  float *lns;     // [4] LayerNorm mean, rstd of x (P1 input) and of x' (P4 input)
 };
 
 RWKV7_DEV_HOST_INLINE int64_t mk_lds_floats(int C, int F, int SR) {
-  return (int64_t)10 * C + (192 + SR) + 5 * 64 + 7 * 64 + F + 4;
+  return (int64_t)10 * C + (192 + SR) + 5 * 64 + 7 * 64 + F + 8;
 }
 
 RWKV7_DEV MkLds mk_lds(float *smem, int C, int F, int SR) {
@@ -174,6 +175,7 @@ RWKV7_DEV MkLds mk_lds(float *smem, int C, int F, int SR) {
   s.gsum = s.p2 + 192 + SR;
   s.core = s.gsum + 5 * 64;
   s.pubs = reinterpret_cast<unsigned *>(s.core + 7 * 64);
+  s.lns = s.core + 7 * 64 + 4;
   return s;
 }
 
@@ -398,6 +400,17 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
   token = token < 0 ? 0 : token >= a.V ? a.V - 1 : token;
   const uint16_t *erow = a.emb + token * C;
   for (int c = 64 * cw + lane; c < C; c += 64 * kNComm) s.x1[c] = h2f(erow[c]);
+  // LayerNorm statistics of each received x / x', computed once here for the
+  // whole workgroup (math waves only apply them)
+  static_assert(kNComm == 1, "one comm wave holds the whole vector");
+  auto stats = [&](const float *x, float *out) {
+    const float2 st = wave_ln_stats<NJX / 2>(x, C);
+    if (lane == 0) {
+      out[0] = st.x;
+      out[1] = st.y;
+    }
+  };
+  stats(s.x1, s.lns);
   auto to = [](float *d) { return [d](int i, float v) { d[i] = v; }; };
   const int rp = m.g % kRep;  // the replica this workgroup reads
   const __amdgpu_buffer_rsrc_t r_x = words_rsrc(a.x_ex + (int64_t)rp * C, C);
@@ -416,6 +429,7 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     pubs += kMW;
     wait_local(cx, s.pubs, pubs);
     comm_poll<NJX, DX>(cx, cw, r_x, C, 64, cx.tag(ph + 2), Ident(), to(s.x4));
+    stats(s.x4, s.lns + 2);
     __syncthreads();  // A4
     __syncthreads();  // B4
     pubs += kMW;
@@ -428,6 +442,7 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     pubs += kMW;
     wait_local(cx, s.pubs, pubs);
     comm_poll<NJX, DX>(cx, cw, r_x, C, 64, cx.tag(ph + 4), Ident(), to(s.x1));
+    stats(s.x1, s.lns);
   }
   __syncthreads();  // AH
   __syncthreads();  // BH
@@ -731,7 +746,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     __syncthreads();  // A1
     refresh();
     {
-      const float2 st = wave_ln_stats<2 * CPL>(s.x1, C);
+      const float2 st = make_float2(s.lns[0], s.lns[1]);
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
         const int c = mt + kMT * i;
@@ -783,7 +798,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     // ---------------- P4: LN2 + shift + FFN key + relu^2 ----------------------
     refresh();
     {
-      const float2 st = wave_ln_stats<2 * CPL>(s.x4, C);
+      const float2 st = make_float2(s.lns[2], s.lns[3]);
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
         const int c = mt + kMT * i;
@@ -828,7 +843,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
   for (int b = 0; b < kHRing; ++b) pre_head(b, wh[b]);
   __syncthreads();  // AH
   {
-    const float2 st = wave_ln_stats<2 * CPL>(s.x1, C);
+    const float2 st = make_float2(s.lns[0], s.lns[1]);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int c = mt + kMT * i;
