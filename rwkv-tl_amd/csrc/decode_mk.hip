@@ -203,17 +203,37 @@ RWKV7_DEV float dot8r(const uint4 &w, const float (&x)[8], float acc) {
 }
 
 // Dot of one row held by the wave (lane l has chunks l + 64c) with x in LDS;
-// the wave-uniform result.
+// the wave-uniform result. Every LDS read of the row is issued before the
+// first FMA (a sched_barrier keeps the compiler from interleaving them, which
+// would cost one LDS round trip per chunk); a chunk past the row (zero
+// weights, see load_row) reads a valid x chunk instead. Two accumulators
+// halve the dependent FMA chain.
 template <int NC>
 RWKV7_DEV float row_dot(const uint4 (&w)[NC], const float *x, int nch) {
   const int lane = threadIdx.x & 63;
-  float acc = 0.f;
+  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+  float4 xa[NC], xb[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    const int j = lane + 64 * c;
-    if (j < nch) acc = dot8(w[c], x + 8 * j, acc);
+    int j = lane + 64 * c;
+    j = j < nch ? j : nch - 1;
+    xa[c] = x4[2 * j];
+    xb[c] = x4[2 * j + 1];
   }
-  return wave_sum(acc);
+  sched_fence();
+  float acc[2] = {0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    float wf[8];
+    h8_to_f(w[c], wf);
+    float a = acc[c & 1];
+    a = fmaf(wf[0], xa[c].x, a); a = fmaf(wf[1], xa[c].y, a);
+    a = fmaf(wf[2], xa[c].z, a); a = fmaf(wf[3], xa[c].w, a);
+    a = fmaf(wf[4], xb[c].x, a); a = fmaf(wf[5], xb[c].y, a);
+    a = fmaf(wf[6], xb[c].z, a); a = fmaf(wf[7], xb[c].w, a);
+    acc[c & 1] = a;
+  }
+  return wave_sum(acc[0] + acc[1]);
 }
 
 // Loads row r of W (row stride ld halfs, nch 16-byte chunks) as lane chunks.
@@ -533,11 +553,16 @@ RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
     refresh();
     if (wv < 5) {  // LoRA second step, part wv of channel lane
       const int js = p2s(wv), je = p2s(wv + 1);
-      float acc = 0.f;
+      // branch-free (a chunk past the part gets zero weights), so every LDS
+      // read is issued up front
+      float acc[2] = {0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < NL2; ++i)
-        if (js + i < je) acc = dot8(w2[i], s.p2 + 192 + 8 * (js + i), acc);
-      s.gsum[wv * kN + lane] = acc;
+      for (int i = 0; i < NL2; ++i) {
+        const bool in = js + i < je;
+        const uint4 wq = in ? w2[i] : make_uint4(0, 0, 0, 0);
+        acc[i & 1] = dot8(wq, s.p2 + 192 + 8 * (in ? js + i : js), acc[i & 1]);
+      }
+      s.gsum[wv * kN + lane] = acc[0] + acc[1];
     }
     __syncthreads();  // B2a
     float v = 0.f, gate = 0.f, rk = 0.f;
