@@ -257,10 +257,13 @@ RWKV7_DEV float2 wave_ln_stats(const float *x, int C) {
   const int C4 = C >> 2;
   float4 v[NV];
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
+  for (int k = 0; k < NV; ++k) {  // unconditional reads (index clamped), zeroed after
     const int i = lane + 64 * k;
-    v[k] = i < C4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    v[k] = x4[i < C4 ? i : C4 - 1];
   }
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+    if (lane + 64 * k >= C4) v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
   float s = 0.f;
 #pragma unroll
   for (int k = 0; k < NV; ++k) s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
@@ -514,6 +517,8 @@ RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
   const int b1 = a.rv >> 3, b2 = (a.rv + a.rw) >> 3, b3 = (a.rv + a.rw + a.ra) >> 3;
   const int b4 = b3 + (nch2 - b3 + 1) / 2;
   auto p2s = [&](int q) { return q == 0 ? 0 : q == 1 ? b1 : q == 2 ? b2 : q == 3 ? b3 : q == 4 ? b4 : nch2; };
+  // this wave's LoRA second-step part (waves 0..4), fixed for the launch
+  const int js = wv < 5 ? p2s(wv) : 0, je = wv < 5 ? p2s(wv + 1) : 0;
   uint4 w2[NL2];
   float4 S4[4];
   float gv[8];
@@ -522,7 +527,6 @@ RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
     if (wv < 5) {
       const uint4 *row = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(Lp + a.o_l2) +
                                                          (int64_t)(g * kN + lane) * SR);
-      const int js = p2s(wv), je = p2s(wv + 1);
       if (je > js) {
 #pragma unroll
         for (int i = 0; i < NL2; ++i) w2[i] = ld_stream(row + (js + i < je ? js + i : je - 1));
@@ -552,15 +556,28 @@ RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
     wait_vm0();       // this layer's operands (issued a layer ago)
     refresh();
     if (wv < 5) {  // LoRA second step, part wv of channel lane
-      const int js = p2s(wv), je = p2s(wv + 1);
-      // branch-free (a chunk past the part gets zero weights), so every LDS
-      // read is issued up front
+      // every LDS read issued before the first FMA; a chunk past the part
+      // gets zero weights and reads the part's first chunk
+      const float4 *x4 = reinterpret_cast<const float4 *>(s.p2 + 192);
+      float4 xa[NL2], xb[NL2];
+#pragma unroll
+      for (int i = 0; i < NL2; ++i) {
+        const int c = js + i < je ? js + i : js;
+        xa[i] = x4[2 * c];
+        xb[i] = x4[2 * c + 1];
+      }
+      sched_fence();
       float acc[2] = {0.f, 0.f};
 #pragma unroll
       for (int i = 0; i < NL2; ++i) {
-        const bool in = js + i < je;
-        const uint4 wq = in ? w2[i] : make_uint4(0, 0, 0, 0);
-        acc[i & 1] = dot8(wq, s.p2 + 192 + 8 * (in ? js + i : js), acc[i & 1]);
+        float wf[8];
+        h8_to_f(js + i < je ? w2[i] : make_uint4(0, 0, 0, 0), wf);
+        float t = acc[i & 1];
+        t = fmaf(wf[0], xa[i].x, t); t = fmaf(wf[1], xa[i].y, t);
+        t = fmaf(wf[2], xa[i].z, t); t = fmaf(wf[3], xa[i].w, t);
+        t = fmaf(wf[4], xb[i].x, t); t = fmaf(wf[5], xb[i].y, t);
+        t = fmaf(wf[6], xb[i].z, t); t = fmaf(wf[7], xb[i].w, t);
+        acc[i & 1] = t;
       }
       s.gsum[wv * kN + lane] = acc[0] + acc[1];
     }
@@ -772,11 +789,17 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     refresh();
     {
       const float2 st = make_float2(s.lns[0], s.lns[1]);
+      float xv[VPL];  // read up front (index clamped), not one LDS round trip per element
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        const int c = mt + kMT * i;
+        xv[i] = s.x1[c < C ? c : C - 1];
+      }
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
         const int c = mt + kMT * i;
         if (c < C) {
-          const float ln = (s.x1[c] - st.x) * st.y * v1w[i] + v1b[i];
+          const float ln = (xv[i] - st.x) * st.y * v1w[i] + v1b[i];
           const float prv = h2f(pv1[i]);
           s.ln1[c] = ln;
 #pragma unroll
@@ -824,11 +847,17 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     refresh();
     {
       const float2 st = make_float2(s.lns[2], s.lns[3]);
+      float xv[VPL];
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        const int c = mt + kMT * i;
+        xv[i] = s.x4[c < C ? c : C - 1];
+      }
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
         const int c = mt + kMT * i;
         if (c < C) {
-          const float ln = (s.x4[c] - st.x) * st.y * v4w[i] + v4b[i];
+          const float ln = (xv[i] - st.x) * st.y * v4w[i] + v4b[i];
           s.ln2[c] = ln;
           s.mix4[c] = ln + mu4[i] * (h2f(pv4[i]) - ln);
         }
