@@ -416,7 +416,7 @@ RWKV7_DEV void wait_local(const MkCtx &cx, const unsigned *pubs, unsigned target
 // hidden vector is read in two halves).
 template <int NJX, int NJF>
 RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, const MkCtx &cx, int cw) {
-  constexpr int DX = 16 / NJX, DF = 16 / NJF;
+  constexpr int DX = 1, DF = 16 / NJF;
   const int lane = threadIdx.x & 63;
   const int C = m.C, F = m.F, L = m.L;
   int64_t token = a.tok[0];
@@ -447,11 +447,11 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     __syncthreads();  // B1
     pubs += kMW;
     // the head workgroups' outputs: one probe pair per head first
-    comm_poll<NJX, DX>(cx, cw, r_core, C, kN, cx.tag(ph + 1), Ident(), to(s.core_in));
+    comm_poll<NJX, DX>(cx, cw, r_core, C, 2 * kN, cx.tag(ph + 1), Ident(), to(s.core_in));
     __syncthreads();  // A3
     pubs += kMW;
     wait_local(cx, s.pubs, pubs);
-    comm_poll<NJX, DX>(cx, cw, r_x, C, 64, cx.tag(ph + 2), Ident(), to(s.x4));
+    comm_poll<NJX, DX>(cx, cw, r_x, C, 256, cx.tag(ph + 2), Ident(), to(s.x4));
     stats(s.x4, s.lns + 2);
     __syncthreads();  // A4
     __syncthreads();  // B4
@@ -464,7 +464,7 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     __syncthreads();  // A5
     pubs += kMW;
     wait_local(cx, s.pubs, pubs);
-    comm_poll<NJX, DX>(cx, cw, r_x, C, 64, cx.tag(ph + 4), Ident(), to(s.x1));
+    comm_poll<NJX, DX>(cx, cw, r_x, C, 256, cx.tag(ph + 4), Ident(), to(s.x1));
     stats(s.x1, s.lns);
   }
   __syncthreads();  // AH
@@ -474,7 +474,7 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
 // NJP: pairs per comm lane of the P2 input vector.
 template <int NJP>
 RWKV7_DEV void comm_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const MkCtx &cx, int cw) {
-  constexpr int DP = 16 / NJP;
+  constexpr int DP = 1;
   const int C = m.C, SR = m.SR, L = m.L;
   const int h = m.g, rv = a.rv, rwa = a.rv + a.rw, rwaa = a.rv + a.rw + a.ra;
   const __amdgpu_buffer_rsrc_t r_proj = words_rsrc(a.proj_ex + (int64_t)(h % kRep) * (3 * C + SR), 3 * C + SR);
@@ -482,7 +482,7 @@ RWKV7_DEV void comm_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
     // r, k, v of this head and the whole LoRA first step, activated on arrival
     // (tanh for w, sigmoid for g)
     // (a sparse probe first: this poll starts a whole layer before its data)
-    comm_poll<NJP, DP>(cx, cw, r_proj, 192 + SR, 32, cx.tag(5 * l),
+    comm_poll<NJP, DP>(cx, cw, r_proj, 192 + SR, 128, cx.tag(5 * l),
                        [&](int i) { return i < 192 ? (i >> 6) * C + h * kN + (i & 63) : 3 * C + (i - 192); },
                        [&](int i, float v) {
                          const int j = i - 192;
