@@ -447,11 +447,11 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     __syncthreads();  // B1
     pubs += kMW;
     // the head workgroups' outputs: one probe pair per head first
-    comm_poll<NJX, DX>(cx, cw, r_core, C, 2 * kN, cx.tag(ph + 1), Ident(), to(s.core_in));
+    comm_poll<NJX, DX>(cx, cw, r_core, C, 4 * kN, cx.tag(ph + 1), Ident(), to(s.core_in));
     __syncthreads();  // A3
     pubs += kMW;
     wait_local(cx, s.pubs, pubs);
-    comm_poll<NJX, DX>(cx, cw, r_x, C, 256, cx.tag(ph + 2), Ident(), to(s.x4));
+    comm_poll<NJX, DX>(cx, cw, r_x, C, 512, cx.tag(ph + 2), Ident(), to(s.x4));
     stats(s.x4, s.lns + 2);
     __syncthreads();  // A4
     __syncthreads();  // B4
@@ -459,12 +459,12 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     wait_local(cx, s.pubs, pubs);
     // no probe: every worker publishes its P4 rows within a fraction of a
     // microsecond of the others, so the first full read finds nearly all
-    comm_poll<NJF, DF>(cx, cw, r_hid, F / 2, 0, cx.tag(ph + 3), Ident(), to(s.hid));
+    comm_poll<NJF, DF>(cx, cw, r_hid, F / 2, 256, cx.tag(ph + 3), Ident(), to(s.hid));
     comm_poll<NJF, DF>(cx, cw, r_hid2, F / 2, 0, cx.tag(ph + 3), Ident(), to(s.hid + F / 2));
     __syncthreads();  // A5
     pubs += kMW;
     wait_local(cx, s.pubs, pubs);
-    comm_poll<NJX, DX>(cx, cw, r_x, C, 256, cx.tag(ph + 4), Ident(), to(s.x1));
+    comm_poll<NJX, DX>(cx, cw, r_x, C, 512, cx.tag(ph + 4), Ident(), to(s.x1));
     stats(s.x1, s.lns);
   }
   __syncthreads();  // AH
@@ -482,7 +482,7 @@ RWKV7_DEV void comm_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
     // r, k, v of this head and the whole LoRA first step, activated on arrival
     // (tanh for w, sigmoid for g)
     // (a sparse probe first: this poll starts a whole layer before its data)
-    comm_poll<NJP, DP>(cx, cw, r_proj, 192 + SR, 128, cx.tag(5 * l),
+    comm_poll<NJP, DP>(cx, cw, r_proj, 192 + SR, 256, cx.tag(5 * l),
                        [&](int i) { return i < 192 ? (i >> 6) * C + h * kN + (i & 63) : 3 * C + (i - 192); },
                        [&](int i, float v) {
                          const int j = i - 192;
