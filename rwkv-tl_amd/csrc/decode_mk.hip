@@ -94,6 +94,7 @@ struct MkCtx {
   unsigned *sync;
   unsigned epoch;
   unsigned tag0;  // epoch * nph + 1
+  int pskew;      // probe offset of this workgroup (even)
   RWKV7_DEV unsigned tag(int phase) const { return tag0 + (unsigned)phase; }
   RWKV7_DEV bool aborted() const { return ld_u32(sync + SY_ABORT) == epoch + 1u; }
   RWKV7_DEV void abort() const {
@@ -326,10 +327,14 @@ RWKV7_DEV void comm_poll(const MkCtx &cx, int cw, __amdgpu_buffer_rsrc_t r, int 
   };
   if (probe > 0) {
     const int nq = (n + probe - 1) / probe;
+    // the probed word of each stride, shifted per workgroup so that the
+    // readers of one replica do not all poll the same few lines
+    int pq = probe * p0 + cx.pskew % probe;
+    pq = pq < n ? pq : probe * p0;
     bool waiting = p0 < nq;
     while (waiting) {
       asm volatile("" ::: "memory");  // re-read every round
-      const uint4 v = ld_pair(r, idx(probe * p0));
+      const uint4 v = ld_pair(r, idx(pq));
       if (v.y == tag) waiting = false;
       else if (!keep_waiting()) break;
       __builtin_amdgcn_s_sleep(1);
@@ -970,6 +975,7 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   cx.sync = a.sync;
   cx.epoch = ld_u32(a.sync + SY_EPOCH);
   cx.tag0 = cx.epoch * (5u * m.L + 1u) + 1u;
+  cx.pskew = (m.g / kRep) * 34;
 
   if (threadIdx.x == 0) *s.pubs = 0u;  // ordered before any increment by the first barrier
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
