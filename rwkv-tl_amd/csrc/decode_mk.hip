@@ -57,6 +57,7 @@ constexpr int kHB = 4;           // head rows per batch
 constexpr int kHRing = 3;        // head batches in flight
 constexpr int kSpinLimit = 1 << 21;
 constexpr int kRep = 8;          // replicas of each broadcast hand-off vector
+constexpr int kHidProbe = 512;   // probe stride of each FFN hidden-vector slice
 static_assert(kRep < 64, "lanes 0..kRep of a wave publish a value and its state");
 
 // 32-bit sync words at the start of the exchange region (byte offsets 0, 16
@@ -417,11 +418,11 @@ RWKV7_DEV void wait_local(const MkCtx &cx, const unsigned *pubs, unsigned target
 // P5); the comm wave starts reading a vector the workers produce only after
 // its own workgroup's share is out.
 
-// NJX: pairs per comm lane of a C-vector; NJF: of half an F-vector (the FFN
-// hidden vector is read in two halves).
+// NJX: pairs per comm lane of a C-vector; NJF: of one of the kW slices of
+// the FFN hidden vector (every wave of the workgroup reads one slice).
 template <int NJX, int NJF>
 RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, const MkCtx &cx, int cw) {
-  constexpr int DX = 1, DF = 16 / NJF;
+  constexpr int DX = 1;
   const int lane = threadIdx.x & 63;
   const int C = m.C, F = m.F, L = m.L;
   int64_t token = a.tok[0];
@@ -443,8 +444,8 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
   const int rp = m.g % kRep;  // the replica this workgroup reads
   const __amdgpu_buffer_rsrc_t r_x = words_rsrc(a.x_ex + (int64_t)rp * C, C);
   const __amdgpu_buffer_rsrc_t r_core = words_rsrc(a.core_ex + (int64_t)rp * C, C);
-  const __amdgpu_buffer_rsrc_t r_hid = words_rsrc(a.hid_ex + (int64_t)rp * F, F / 2);
-  const __amdgpu_buffer_rsrc_t r_hid2 = words_rsrc(a.hid_ex + (int64_t)rp * F + F / 2, F / 2);
+  const int FS = F / kW;  // words of one hidden-vector slice
+  const __amdgpu_buffer_rsrc_t r_hid = words_rsrc(a.hid_ex + (int64_t)rp * F + (int64_t)kMW * FS, FS);
   unsigned pubs = 0;  // publish steps of the math waves seen so far
   for (int l = 0; l < L; ++l) {
     const int ph = 5 * l;
@@ -462,10 +463,8 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     __syncthreads();  // B4
     pubs += kMW;
     wait_local(cx, s.pubs, pubs);
-    // no probe: every worker publishes its P4 rows within a fraction of a
-    // microsecond of the others, so the first full read finds nearly all
-    comm_poll<NJF, DF>(cx, cw, r_hid, F / 2, 256, cx.tag(ph + 3), Ident(), to(s.hid));
-    comm_poll<NJF, DF>(cx, cw, r_hid2, F / 2, 0, cx.tag(ph + 3), Ident(), to(s.hid + F / 2));
+    // the last slice of the hidden vector (the math waves read the others)
+    comm_poll<NJF, 1>(cx, 0, r_hid, FS, kHidProbe, cx.tag(ph + 3), Ident(), to(s.hid + kMW * FS));
     __syncthreads();  // A5
     pubs += kMW;
     wait_local(cx, s.pubs, pubs);
@@ -881,6 +880,14 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
       }
     }
     count_publish();
+    {
+      // every wave reads one slice of the hidden vector (the math waves are
+      // idle until it is complete, and 8 readers cut its round trips)
+      const int FS = F / kW;
+      const __amdgpu_buffer_rsrc_t r = words_rsrc(a.hid_ex + (int64_t)(m.g % kRep) * F + (int64_t)wv * FS, FS);
+      comm_poll<NC5 / 2, 1>(cx, 0, r, FS, kHidProbe, cx.tag(ph + 3), Ident(),
+                            [&](int i, float v) { s.hid[wv * FS + i] = v; });
+    }
     __syncthreads();  // A5
     // ---------------- P5: FFN value + residual --------------------------------
     refresh();
@@ -983,7 +990,7 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     if (wv >= kMW) comm_head<NJ>(a, m, s, cx, wv - kMW);
     else math_head<NL2>(a, m, s, cx, wv);
   } else {
-    if (wv >= kMW) comm_worker<4 * CPL / kNComm, 2 * NC5 / kNComm>(a, m, s, cx, wv - kMW);
+    if (wv >= kMW) comm_worker<4 * CPL / kNComm, NC5 / 2>(a, m, s, cx, wv - kMW);
     else math_worker<CPL, RM, NC5, VPL, NHB>(a, m, s, cx, wv);
   }
   // A worker ends only after every workgroup has published (its logits need
@@ -1041,9 +1048,8 @@ bool mk_supported(const rwkv7_dims &d, int G) {
     if (cv > kNL2 || cw > kNL2 || ca > kNL2 || (cg + 1) / 2 > kNL2 || kMW < 5) return false;
   }
   const int cj = 2 * 64 * kNComm;  // words per round: one pair per lane and slot
-  if (cdiv(C, cj) > 4 * kCPL / kNComm || cdiv(F / 2, cj) > 2 * kNC5 / kNComm || cdiv(192 + SR, cj) > kNJ)
-    return false;
-  if (F % 512) return false;  // halves of the hidden vector in whole 16-byte pairs per lane round
+  if (cdiv(C, cj) > 4 * kCPL / kNComm || cdiv(F / kW, cj) > kNC5 / 2 || cdiv(192 + SR, cj) > kNJ) return false;
+  if (F % (2 * kW)) return false;  // hidden-vector slices of whole 16-byte pairs
   if (H > 64 * kNComm) return false;  // one probe lane per head
   const int hrows = cdiv(cdiv(V, Gw), kMW);
   if (hrows > kHB * kNHB || hrows > 64) return false;
