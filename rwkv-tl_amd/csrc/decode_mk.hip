@@ -58,6 +58,7 @@ constexpr int kHRing = 3;        // head batches in flight
 constexpr int kSpinLimit = 1 << 21;
 constexpr int kRep = 8;          // replicas of each broadcast hand-off vector
 constexpr int kHidProbe = 512;   // probe stride of each FFN hidden-vector slice
+constexpr int kXProbe = 512;     // probe stride of the x vectors
 static_assert(kRep < 64, "lanes 0..kRep of a wave publish a value and its state");
 
 // 32-bit sync words at the start of the exchange region (byte offsets 0, 16
@@ -156,11 +157,12 @@ struct MkLds {
   float *mix4;    // [C]  P4 mix
   float *hid;     // [F]  P5 input
   unsigned *pubs; // count of math-wave publish steps (the comm waves' start signal)
-  float *lns;     // [4] LayerNorm mean, rstd of x (P1 input) and of x' (P4 input)
+  unsigned *xflag; // tag of the x vector the comm wave's probe saw arriving (a start hint)
+  float *xst;     // [2][kW][2] (mean, M2) of each wave's slice of x (P1 input), x' (P4 input)
 };
 
 RWKV7_DEV_HOST_INLINE int64_t mk_lds_floats(int C, int F, int SR) {
-  return (int64_t)10 * C + (192 + SR) + 5 * 64 + 7 * 64 + F + 8;
+  return (int64_t)10 * C + (192 + SR) + 5 * 64 + 7 * 64 + F + 4 + 4 * kW;
 }
 
 RWKV7_DEV MkLds mk_lds(float *smem, int C, int F, int SR) {
@@ -177,7 +179,8 @@ RWKV7_DEV MkLds mk_lds(float *smem, int C, int F, int SR) {
   s.gsum = s.p2 + 192 + SR;
   s.core = s.gsum + 5 * 64;
   s.pubs = reinterpret_cast<unsigned *>(s.core + 7 * 64);
-  s.lns = s.core + 7 * 64 + 4;
+  s.xflag = s.pubs + 1;
+  s.xst = s.core + 7 * 64 + 4;
   return s;
 }
 
@@ -281,6 +284,41 @@ RWKV7_DEV float2 wave_ln_stats(const float *x, int C) {
   return make_float2(mean, rsqrtf(wave_sum(q) / (float)C + kLnEps));
 }
 
+// ---- x hand-offs: every wave reads one slice ------------------------------------
+
+// Mean and M2 (sum of squared deviations) of this wave's slice
+// x[w*XS, (w+1)*XS) (XS <= 128: at most two values per lane), into st[0..1].
+RWKV7_DEV void slice_stats(const float *x, int w, int XS, float *st) {
+  const int lane = threadIdx.x & 63;
+  const int i0 = lane, i1 = lane + 64;
+  const float a = x[w * XS + (i0 < XS ? i0 : 0)], b = x[w * XS + (i1 < XS ? i1 : 0)];
+  const float na = i0 < XS ? 1.f : 0.f, nb = i1 < XS ? 1.f : 0.f;
+  const float mean = wave_sum(na * a + nb * b) / (float)XS;
+  const float da = a - mean, db = b - mean;
+  const float m2 = wave_sum(na * da * da + nb * db * db);
+  if (lane == 0) {
+    st[0] = mean;
+    st[1] = m2;
+  }
+}
+
+// LayerNorm mean and 1/std of a C-vector from its kW equal slices' (mean, M2)
+// (pairwise-combination formula: M2 = sum M2_w + XS * sum (mean_w - mean)^2).
+RWKV7_DEV float2 combine_stats(const float *st, int C) {
+  const float XS = (float)(C / kW);
+  float mean = 0.f;
+#pragma unroll
+  for (int w = 0; w < kW; ++w) mean += st[2 * w];
+  mean *= 1.f / kW;
+  float m2 = 0.f;
+#pragma unroll
+  for (int w = 0; w < kW; ++w) {
+    const float d = st[2 * w] - mean;
+    m2 += st[2 * w + 1] + XS * d * d;
+  }
+  return make_float2(mean, rsqrtf(m2 / (float)C + kLnEps));
+}
+
 // ---- comm wave ------------------------------------------------------------------
 
 // ---- comm waves -----------------------------------------------------------------
@@ -295,29 +333,12 @@ RWKV7_DEV uint4 ld_pair(__amdgpu_buffer_rsrc_t r, int word) {
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
-// Waits until every word idx(i), i < n, of the buffer `r` carries `tag`,
-// handing each value to put(i, v). idx must map each even i and i + 1 to
-// consecutive, 16-byte aligned words. Comm wave cw, lane l handles the pairs
-// p = 64 cw + l + 64 kNComm j (j < NJ), i = 2p.
-//
-// A poll round is one 16-byte load per pair, and under weight streaming its
-// round trip is ~1.5 us, so a round issued just before the last word lands
-// would cost another full round trip. The loop therefore keeps D rounds in
-// flight (re-issued unconditionally, so the compiler's load counting stays
-// exact) and checks them oldest first: new data is seen within about
-// RTT / D of arriving. At most 16 loads per lane are in flight (more slows a
-// wave down sharply). `probe` > 0 first polls one pair in every `probe` words
-// until those carry the tag, to spare traffic while producers still compute.
-template <int NJ, int D, typename Idx, typename Put>
-RWKV7_DEV void comm_poll(const MkCtx &cx, int cw, __amdgpu_buffer_rsrc_t r, int n, int probe, unsigned tag,
-                         Idx idx, Put put) {
-  static_assert(NJ * D <= 16 && NJ <= 16, "at most 16 loads per lane in flight");
-  int p0 = 64 * cw + (threadIdx.x & 63);
-  asm volatile("" : "+v"(p0));  // per-call addresses: keep them out of the layer loop
-  constexpr int kStep = 64 * kNComm;
-  const int np = n >> 1;
+// Spins until the launch is aborted or the spin limit is hit (then aborts it).
+struct SpinBound {
+  const MkCtx &cx;
   int spins = 0;
-  auto keep_waiting = [&]() {  // bounded: false once the launch is aborted
+  RWKV7_DEV explicit SpinBound(const MkCtx &c) : cx(c) {}
+  RWKV7_DEV bool keep_waiting() {  // bounded: false once the launch is aborted
     ++spins;
     if ((spins & 1023) == 0 && cx.aborted()) return false;
     if (spins > kSpinLimit) {
@@ -325,22 +346,40 @@ RWKV7_DEV void comm_poll(const MkCtx &cx, int cw, __amdgpu_buffer_rsrc_t r, int 
       return false;
     }
     return true;
-  };
-  if (probe > 0) {
-    const int nq = (n + probe - 1) / probe;
-    // the probed word of each stride, shifted per workgroup so that the
-    // readers of one replica do not all poll the same few lines
-    int pq = probe * p0 + cx.pskew % probe;
-    pq = pq < n ? pq : probe * p0;
-    bool waiting = p0 < nq;
-    while (waiting) {
-      asm volatile("" ::: "memory");  // re-read every round
-      const uint4 v = ld_pair(r, idx(pq));
-      if (v.y == tag) waiting = false;
-      else if (!keep_waiting()) break;
-      __builtin_amdgcn_s_sleep(1);
-    }
   }
+};
+
+// Probe phase: polls one pair in every `probe` words (lane l of wave cw takes
+// stride 64 cw + l) until those carry the tag.
+template <typename Idx>
+RWKV7_DEV void probe_wait(const MkCtx &cx, int cw, __amdgpu_buffer_rsrc_t r, int n, int probe, unsigned tag,
+                          Idx idx) {
+  SpinBound sb(cx);
+  const int p0 = 64 * cw + (threadIdx.x & 63);
+  const int nq = (n + probe - 1) / probe;
+  // the probed word of each stride, shifted per workgroup so that the
+  // readers of one replica do not all poll the same few lines
+  int pq = probe * p0 + cx.pskew % probe;
+  pq = pq < n ? pq : probe * p0;
+  bool waiting = p0 < nq;
+  while (waiting) {
+    asm volatile("" ::: "memory");  // re-read every round
+    const uint4 v = ld_pair(r, idx(pq));
+    if (v.y == tag) waiting = false;
+    else if (!sb.keep_waiting()) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// Full phase: reads every pair until all carry the tag (see comm_poll).
+template <int NJ, int D, typename Idx, typename Put>
+RWKV7_DEV void read_all(const MkCtx &cx, int cw, __amdgpu_buffer_rsrc_t r, int n, unsigned tag, Idx idx, Put put) {
+  static_assert(NJ * D <= 16 && NJ <= 16, "at most 16 loads per lane in flight");
+  SpinBound sb(cx);
+  int p0 = 64 * cw + (threadIdx.x & 63);
+  asm volatile("" : "+v"(p0));  // per-call addresses: keep them out of the layer loop
+  constexpr int kStep = 64 * kNComm;
+  const int np = n >> 1;
   unsigned pending = 0;
   int addr[NJ];
 #pragma unroll
@@ -372,7 +411,35 @@ RWKV7_DEV void comm_poll(const MkCtx &cx, int cw, __amdgpu_buffer_rsrc_t r, int 
 #pragma unroll
       for (int j = 0; j < NJ; ++j) buf[d][j] = ld_pair(r, addr[j]);
     }
-    if (__builtin_amdgcn_ballot_w64(pending != 0) == 0 || !keep_waiting()) break;
+    if (__builtin_amdgcn_ballot_w64(pending != 0) == 0 || !sb.keep_waiting()) break;
+  }
+}
+
+// Waits until every word idx(i), i < n, of the buffer `r` carries `tag`,
+// handing each value to put(i, v). idx must map each even i and i + 1 to
+// consecutive, 16-byte aligned words. Comm wave cw, lane l handles the pairs
+// p = 64 cw + l + 64 kNComm j (j < NJ), i = 2p.
+//
+// A poll round is one 16-byte load per pair. The full phase keeps D rounds in
+// flight (re-issued unconditionally, so the compiler's load counting stays
+// exact) and checks them oldest first. At most 16 loads per lane are in
+// flight. `probe` > 0 first polls one pair in every `probe` words until those
+// carry the tag, to spare traffic while producers still compute: poll traffic
+// slows every hand-off on the chip, so probes are sparse and D is 1.
+template <int NJ, int D, typename Idx, typename Put>
+RWKV7_DEV void comm_poll(const MkCtx &cx, int cw, __amdgpu_buffer_rsrc_t r, int n, int probe, unsigned tag,
+                         Idx idx, Put put) {
+  if (probe > 0) probe_wait(cx, cw, r, n, probe, tag, idx);
+  read_all<NJ, D>(cx, cw, r, n, tag, idx, put);
+}
+
+// Waits (LDS spin, bounded) until *flag == tag. Only a start hint: the reads
+// that follow check every word's tag themselves.
+RWKV7_DEV void wait_flag(const MkCtx &cx, const unsigned *flag, unsigned tag) {
+  SpinBound sb(cx);
+  while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != tag) {
+    __builtin_amdgcn_s_sleep(1);
+    if (!sb.keep_waiting()) break;
   }
 }
 
@@ -428,21 +495,24 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
   int64_t token = a.tok[0];
   token = token < 0 ? 0 : token >= a.V ? a.V - 1 : token;
   const uint16_t *erow = a.emb + token * C;
-  for (int c = 64 * cw + lane; c < C; c += 64 * kNComm) s.x1[c] = h2f(erow[c]);
-  // LayerNorm statistics of each received x / x', computed once here for the
-  // whole workgroup (math waves only apply them)
-  static_assert(kNComm == 1, "one comm wave holds the whole vector");
-  auto stats = [&](const float *x, float *out) {
-    const float2 st = wave_ln_stats<NJX / 2>(x, C);
-    if (lane == 0) {
-      out[0] = st.x;
-      out[1] = st.y;
-    }
-  };
-  stats(s.x1, s.lns);
+  // this wave's slice of x (the math waves load and read the others); its
+  // LayerNorm partial statistics go to xst
+  static_assert(kNComm == 1, "the comm wave holds slice kMW");
+  const int XS = C / kW;
+  for (int i = lane; i < XS; i += 64) s.x1[kMW * XS + i] = h2f(erow[kMW * XS + i]);
+  slice_stats(s.x1, kMW, XS, s.xst + 2 * kMW);
   auto to = [](float *d) { return [d](int i, float v) { d[i] = v; }; };
   const int rp = m.g % kRep;  // the replica this workgroup reads
-  const __amdgpu_buffer_rsrc_t r_x = words_rsrc(a.x_ex + (int64_t)rp * C, C);
+  const __amdgpu_buffer_rsrc_t r_xall = words_rsrc(a.x_ex + (int64_t)rp * C, C);
+  const __amdgpu_buffer_rsrc_t r_x = words_rsrc(a.x_ex + (int64_t)rp * C + kMW * XS, XS);
+  // x hand-offs: this wave probes the whole vector, tells the math waves (each
+  // reads one slice) through xflag, then reads slice kMW
+  auto poll_x = [&](unsigned tag, float *x, float *st) {
+    probe_wait(cx, 0, r_xall, C, kXProbe, tag, Ident());
+    if (lane == 0) __hip_atomic_store(s.xflag, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    read_all<1, 1>(cx, 0, r_x, XS, tag, Ident(), to(x + kMW * XS));
+    slice_stats(x, kMW, XS, st + 2 * kMW);
+  };
   const __amdgpu_buffer_rsrc_t r_core = words_rsrc(a.core_ex + (int64_t)rp * C, C);
   const int FS = F / kW;  // words of one hidden-vector slice
   const __amdgpu_buffer_rsrc_t r_hid = words_rsrc(a.hid_ex + (int64_t)rp * F + (int64_t)kMW * FS, FS);
@@ -457,8 +527,7 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     __syncthreads();  // A3
     pubs += kMW;
     wait_local(cx, s.pubs, pubs);
-    comm_poll<NJX, DX>(cx, cw, r_x, C, 512, cx.tag(ph + 2), Ident(), to(s.x4));
-    stats(s.x4, s.lns + 2);
+    poll_x(cx.tag(ph + 2), s.x4, s.xst + 2 * kW);
     __syncthreads();  // A4
     __syncthreads();  // B4
     pubs += kMW;
@@ -468,8 +537,7 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     __syncthreads();  // A5
     pubs += kMW;
     wait_local(cx, s.pubs, pubs);
-    comm_poll<NJX, DX>(cx, cw, r_x, C, 512, cx.tag(ph + 4), Ident(), to(s.x1));
-    stats(s.x1, s.lns);
+    poll_x(cx.tag(ph + 4), s.x1, s.xst);
   }
   __syncthreads();  // AH
   __syncthreads();  // BH
@@ -784,6 +852,22 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
   };
 
   float xown = 0.f;  // residual of channel owa + wv (waves wv < nown)
+  // x hand-offs: this wave reads slice wv of x (the comm wave slice kMW) and
+  // leaves the slice's LayerNorm partial statistics in xst
+  const int XS = C / kW;
+  const __amdgpu_buffer_rsrc_t r_xs = words_rsrc(a.x_ex + (int64_t)(m.g % kRep) * C + wv * XS, XS);
+  auto poll_x = [&](unsigned tag, float *x, float *st) {
+    wait_flag(cx, s.xflag, tag);  // the comm wave's probe saw the vector arriving
+    read_all<1, 1>(cx, 0, r_xs, XS, tag, Ident(), [&](int i, float v) { x[wv * XS + i] = v; });
+    slice_stats(x, wv, XS, st + 2 * wv);
+  };
+  {
+    int64_t token = a.tok[0];
+    token = token < 0 ? 0 : token >= a.V ? a.V - 1 : token;
+    const uint16_t *erow = a.emb + token * C;
+    for (int i = lane; i < XS; i += 64) s.x1[wv * XS + i] = h2f(erow[wv * XS + i]);
+    slice_stats(s.x1, wv, XS, s.xst + 2 * wv);
+  }
   pre_p1(0);
   wait_vm0();
   for (int l = 0; l < L; ++l) {
@@ -792,7 +876,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     __syncthreads();  // A1
     refresh();
     {
-      const float2 st = make_float2(s.lns[0], s.lns[1]);
+      const float2 st = combine_stats(s.xst, C);
       float xv[VPL];  // read up front (index clamped), not one LDS round trip per element
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
@@ -846,11 +930,12 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
       if (lane == kRep) a.tmix_x[(int64_t)l * C + c] = f2h(s.ln1[c]);
     }
     count_publish();
+    poll_x(cx.tag(ph + 2), s.x4, s.xst + 2 * kW);
     __syncthreads();  // A4
     // ---------------- P4: LN2 + shift + FFN key + relu^2 ----------------------
     refresh();
     {
-      const float2 st = make_float2(s.lns[2], s.lns[3]);
+      const float2 st = combine_stats(s.xst + 2 * kW, C);
       float xv[VPL];
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
@@ -899,6 +984,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
       if (lane == kRep) a.cmix_x[(int64_t)l * C + c] = f2h(s.ln2[c]);
     }
     count_publish();
+    poll_x(cx.tag(ph + 4), s.x1, s.xst);
   }
 
   // ---------------- head: ln_out + logits ---------------------------------------
@@ -909,7 +995,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
   for (int b = 0; b < kHRing; ++b) pre_head(b, wh[b]);
   __syncthreads();  // AH
   {
-    const float2 st = make_float2(s.lns[0], s.lns[1]);
+    const float2 st = combine_stats(s.xst, C);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int c = mt + kMT * i;
@@ -984,7 +1070,10 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   cx.tag0 = cx.epoch * (5u * m.L + 1u) + 1u;
   cx.pskew = (m.g / kRep) * 34;
 
-  if (threadIdx.x == 0) *s.pubs = 0u;  // ordered before any increment by the first barrier
+  if (threadIdx.x == 0) {  // ordered before any use by the first barrier
+    *s.pubs = 0u;
+    *s.xflag = 0u;
+  }
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (m.head) {
     if (wv >= kMW) comm_head<NJ>(a, m, s, cx, wv - kMW);
@@ -1050,6 +1139,7 @@ bool mk_supported(const rwkv7_dims &d, int G) {
   const int cj = 2 * 64 * kNComm;  // words per round: one pair per lane and slot
   if (cdiv(C, cj) > 4 * kCPL / kNComm || cdiv(F / kW, cj) > kNC5 / 2 || cdiv(192 + SR, cj) > kNJ) return false;
   if (F % (2 * kW)) return false;  // hidden-vector slices of whole 16-byte pairs
+  if (C % (2 * kW) || C / kW > 128) return false;  // x slices: whole pairs, <= 2 values per lane
   if (H > 64 * kNComm) return false;  // one probe lane per head
   const int hrows = cdiv(cdiv(V, Gw), kMW);
   if (hrows > kHB * kNHB || hrows > 64) return false;
