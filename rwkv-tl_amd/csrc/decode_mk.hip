@@ -57,7 +57,7 @@ constexpr int kHB = 4;           // head rows per batch
 constexpr int kHRing = 3;        // head batches in flight
 constexpr int kSpinLimit = 1 << 21;
 constexpr int kRep = 8;          // replicas of each broadcast hand-off vector
-constexpr int kHidProbe = 512;   // probe stride of each FFN hidden-vector slice
+constexpr int kHidProbe = 2048;  // probe stride of the FFN hidden vector
 constexpr int kXProbe = 512;     // probe stride of the x vectors
 static_assert(kRep < 64, "lanes 0..kRep of a wave publish a value and its state");
 
@@ -514,8 +514,10 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     slice_stats(x, kMW, XS, st + 2 * kMW);
   };
   const __amdgpu_buffer_rsrc_t r_core = words_rsrc(a.core_ex + (int64_t)rp * C, C);
+  const __amdgpu_buffer_rsrc_t r_cs = words_rsrc(a.core_ex + (int64_t)rp * C + kMW * (C / kW), C / kW);
   const int FS = F / kW;  // words of one hidden-vector slice
   const __amdgpu_buffer_rsrc_t r_hid = words_rsrc(a.hid_ex + (int64_t)rp * F + (int64_t)kMW * FS, FS);
+  const __amdgpu_buffer_rsrc_t r_hidall = words_rsrc(a.hid_ex + (int64_t)rp * F, F);
   unsigned pubs = 0;  // publish steps of the math waves seen so far
   for (int l = 0; l < L; ++l) {
     const int ph = 5 * l;
@@ -523,7 +525,9 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     __syncthreads();  // B1
     pubs += kMW;
     // the head workgroups' outputs: one probe pair per head first
-    comm_poll<NJX, DX>(cx, cw, r_core, C, 4 * kN, cx.tag(ph + 1), Ident(), to(s.core_in));
+    probe_wait(cx, 0, r_core, C, 4 * kN, cx.tag(ph + 1), Ident());
+    if (lane == 0) __hip_atomic_store(s.xflag, cx.tag(ph + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    read_all<1, 1>(cx, 0, r_cs, XS, cx.tag(ph + 1), Ident(), to(s.core_in + kMW * XS));
     __syncthreads();  // A3
     pubs += kMW;
     wait_local(cx, s.pubs, pubs);
@@ -533,7 +537,9 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     pubs += kMW;
     wait_local(cx, s.pubs, pubs);
     // the last slice of the hidden vector (the math waves read the others)
-    comm_poll<NJF, 1>(cx, 0, r_hid, FS, kHidProbe, cx.tag(ph + 3), Ident(), to(s.hid + kMW * FS));
+    probe_wait(cx, 0, r_hidall, F, kHidProbe, cx.tag(ph + 3), Ident());
+    if (lane == 0) __hip_atomic_store(s.xflag, cx.tag(ph + 3), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    read_all<NJF, 1>(cx, 0, r_hid, FS, cx.tag(ph + 3), Ident(), to(s.hid + kMW * FS));
     __syncthreads();  // A5
     pubs += kMW;
     wait_local(cx, s.pubs, pubs);
@@ -856,6 +862,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
   // leaves the slice's LayerNorm partial statistics in xst
   const int XS = C / kW;
   const __amdgpu_buffer_rsrc_t r_xs = words_rsrc(a.x_ex + (int64_t)(m.g % kRep) * C + wv * XS, XS);
+  const __amdgpu_buffer_rsrc_t r_cso = words_rsrc(a.core_ex + (int64_t)(m.g % kRep) * C + wv * XS, XS);
   auto poll_x = [&](unsigned tag, float *x, float *st) {
     wait_flag(cx, s.xflag, tag);  // the comm wave's probe saw the vector arriving
     read_all<1, 1>(cx, 0, r_xs, XS, tag, Ident(), [&](int i, float v) { x[wv * XS + i] = v; });
@@ -917,6 +924,8 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     pre_p4(l);
     pre_p5(l);
     if (l + 1 < L) pre_p1(l + 1);
+    wait_flag(cx, s.xflag, cx.tag(ph + 1));
+    read_all<1, 1>(cx, 0, r_cso, XS, cx.tag(ph + 1), Ident(), [&](int i, float v) { s.core_in[wv * XS + i] = v; });
     __syncthreads();  // A3
     wait_vm0();
     // ---------------- P3: o-projection + residual -----------------------------
@@ -970,7 +979,8 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
       // idle until it is complete, and 8 readers cut its round trips)
       const int FS = F / kW;
       const __amdgpu_buffer_rsrc_t r = words_rsrc(a.hid_ex + (int64_t)(m.g % kRep) * F + (int64_t)wv * FS, FS);
-      comm_poll<NC5 / 2, 1>(cx, 0, r, FS, kHidProbe, cx.tag(ph + 3), Ident(),
+      wait_flag(cx, s.xflag, cx.tag(ph + 3));  // the comm wave's probe saw it arriving
+      read_all<NC5 / 2, 1>(cx, 0, r, FS, cx.tag(ph + 3), Ident(),
                             [&](int i, float v) { s.hid[wv * FS + i] = v; });
     }
     __syncthreads();  // A5
