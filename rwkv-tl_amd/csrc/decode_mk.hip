@@ -57,8 +57,8 @@ constexpr int kHB = 4;           // head rows per batch
 constexpr int kHRing = 3;        // head batches in flight
 constexpr int kSpinLimit = 1 << 21;
 constexpr int kRep = 8;          // replicas of each broadcast hand-off vector
-constexpr int kHidProbe = 2048;  // probe stride of the FFN hidden vector
-constexpr int kXProbe = 512;     // probe stride of the x vectors
+constexpr int kHidProbe = 4096;  // probe stride of the FFN hidden vector
+constexpr int kXProbe = 1024;    // probe stride of the x vectors
 static_assert(kRep < 64, "lanes 0..kRep of a wave publish a value and its state");
 
 // 32-bit sync words at the start of the exchange region (byte offsets 0, 16
@@ -525,7 +525,7 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     __syncthreads();  // B1
     pubs += kMW;
     // the head workgroups' outputs: one probe pair per head first
-    probe_wait(cx, 0, r_core, C, 4 * kN, cx.tag(ph + 1), Ident());
+    probe_wait(cx, 0, r_core, C, 16 * kN, cx.tag(ph + 1), Ident());
     if (lane == 0) __hip_atomic_store(s.xflag, cx.tag(ph + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     read_all<1, 1>(cx, 0, r_cs, XS, cx.tag(ph + 1), Ident(), to(s.core_in + kMW * XS));
     __syncthreads();  // A3
@@ -549,6 +549,33 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
   __syncthreads();  // BH
 }
 
+// Word of P2 input element i of head h in a proj replica: r, k, v of the head
+// (i < 192), then the whole LoRA first step.
+struct HeadWord {
+  int C, h;
+  RWKV7_DEV int operator()(int i) const { return i < 192 ? (i >> 6) * C + h * kN + (i & 63) : 3 * C + (i - 192); }
+};
+RWKV7_DEV HeadWord head_word(int C, int h) { return HeadWord{C, h}; }
+
+// Wave w's slice of the P2 input (every wave of a head workgroup reads one),
+// activated on arrival: tanh for the w LoRA, sigmoid for the g LoRA.
+RWKV7_DEV void head_read(const MkCtx &cx, const MkArgs &a, const MkLds &s, int h, int w, unsigned tag) {
+  const int C = a.C, n = 192 + a.rv + a.rw + a.ra + a.rg;
+  const int rv = a.rv, rwa = a.rv + a.rw, rwaa = a.rv + a.rw + a.ra;
+  const int S = ((n + kW - 1) / kW + 1) & ~1;  // even slice length
+  const int i0 = w * S, m = n - i0 < S ? n - i0 : S;
+  if (m <= 0) return;
+  const __amdgpu_buffer_rsrc_t r = words_rsrc(a.proj_ex + (int64_t)(h % kRep) * (3 * C + n - 192), 3 * C + n - 192);
+  const HeadWord hw = head_word(C, h);
+  read_all<1, 1>(cx, 0, r, m, tag, [&](int li) { return hw(i0 + li); },
+                 [&](int li, float v) {
+                   const int j = i0 + li - 192;
+                   if (j >= rv && j < rwa) v = tanhf(v);
+                   else if (j >= rwaa) v = sigmoidf_(v);
+                   s.p2[i0 + li] = v;
+                 });
+}
+
 // NJP: pairs per comm lane of the P2 input vector.
 template <int NJP>
 RWKV7_DEV void comm_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const MkCtx &cx, int cw) {
@@ -557,17 +584,13 @@ RWKV7_DEV void comm_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
   const int h = m.g, rv = a.rv, rwa = a.rv + a.rw, rwaa = a.rv + a.rw + a.ra;
   const __amdgpu_buffer_rsrc_t r_proj = words_rsrc(a.proj_ex + (int64_t)(h % kRep) * (3 * C + SR), 3 * C + SR);
   for (int l = 0; l < L; ++l) {
-    // r, k, v of this head and the whole LoRA first step, activated on arrival
-    // (tanh for w, sigmoid for g)
-    // (a sparse probe first: this poll starts a whole layer before its data)
-    comm_poll<NJP, DP>(cx, cw, r_proj, 192 + SR, 256, cx.tag(5 * l),
-                       [&](int i) { return i < 192 ? (i >> 6) * C + h * kN + (i & 63) : 3 * C + (i - 192); },
-                       [&](int i, float v) {
-                         const int j = i - 192;
-                         if (j >= rv && j < rwa) v = tanhf(v);
-                         else if (j >= rwaa) v = sigmoidf_(v);
-                         s.p2[i] = v;
-                       });
+    // r, k, v of this head and the whole LoRA first step: a sparse probe
+    // (this poll starts a whole layer before its data), then every wave reads
+    // one slice (see head_read)
+    probe_wait(cx, 0, r_proj, 192 + SR, 512, cx.tag(5 * l), head_word(C, h));
+    if ((threadIdx.x & 63) == 0)
+      __hip_atomic_store(s.xflag, cx.tag(5 * l), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    head_read(cx, a, s, h, kMW, cx.tag(5 * l));
     __syncthreads();  // HA
     __syncthreads();  // B2a
     __syncthreads();  // B2b
@@ -630,6 +653,8 @@ RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
         *s_y = s.core + 320;
   pre_p2(0);
   for (int l = 0; l < L; ++l) {
+    wait_flag(cx, s.xflag, cx.tag(5 * l));  // the comm wave's probe saw the P2 input arriving
+    head_read(cx, a, s, g, wv, cx.tag(5 * l));
     __syncthreads();  // HA
     wait_vm0();       // this layer's operands (issued a layer ago)
     refresh();
