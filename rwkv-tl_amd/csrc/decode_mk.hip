@@ -470,8 +470,7 @@ RWKV7_DEV void wait_local(const MkCtx &cx, const unsigned *pubs, unsigned target
 // Barrier schedules (one line per workgroup barrier; the comm and math waves
 // of a workgroup execute the same sequence):
 //   head, per layer:    HA  P2 input in p2
-//                       B2a LoRA second-step dots in gsum
-//                       B2b gates in core
+//                       B2b gates in core (each LoRA part's wave finishes its gate)
 //                       B2c wkv outputs in core
 //   worker, per layer:  A1  P1 input in x1
 //                       B1  P1 mixes in mix
@@ -592,7 +591,6 @@ RWKV7_DEV void comm_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
       __hip_atomic_store(s.xflag, cx.tag(5 * l), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     head_read(cx, a, s, h, kMW, cx.tag(5 * l));
     __syncthreads();  // HA
-    __syncthreads();  // B2a
     __syncthreads();  // B2b
     __syncthreads();  // B2c
   }
@@ -639,7 +637,7 @@ RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
 #pragma unroll
       for (int e = 0; e < 4; ++e) S4[e] = Sp[e];
     }
-    if (wv == 0) {
+    if (wv < 3) {  // the gate vectors (waves 0..2 finish the v, w and a parts)
       const float *vec = reinterpret_cast<const float *>(Lp + a.o_vec);
       const int idx[8] = {RWKV7_V_V0, RWKV7_V_W0, RWKV7_V_A0, RWKV7_V_K_K,
                           RWKV7_V_K_A, RWKV7_V_R_K, RWKV7_V_LNX_W, RWKV7_V_LNX_B};
@@ -682,28 +680,30 @@ RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
         t = fmaf(wf[6], xb[i].z, t); t = fmaf(wf[7], xb[i].w, t);
         acc[i & 1] = t;
       }
-      s.gsum[wv * kN + lane] = acc[0] + acc[1];
-    }
-    __syncthreads();  // B2a
-    float v = 0.f, gate = 0.f, rk = 0.f;
-    if (wv == 0) {  // lane t = channel g*64 + t
+      const float d = acc[0] + acc[1];
+      // each part's wave finishes its own gates for channel t = lane
       const int t = lane;
-      const float dv = s.gsum[t], dw = s.gsum[kN + t], da = s.gsum[2 * kN + t];
-      const float dg = s.gsum[3 * kN + t] + s.gsum[4 * kN + t];
-      const float r = s.p2[t], k = s.p2[64 + t];
-      v = s.p2[128 + t];
-      if (l == 0) vfirst = v;
-      else v = v + sigmoidf_(gv[0] + dv) * (vfirst - v);
-      const float w = expf(-sigmoidf_(gv[1] + dw) / 1.6487212707001282f);
-      const float ag = sigmoidf_(gv[2] + da);
-      const float kk = k * gv[3];
-      const float kn = k + gv[4] * (k * ag - k);
-      const float nrm = sqrtf(wave_sum(kk * kk));
-      const float kh = kk / fmaxf(nrm, 1e-12f);
-      rk = wave_sum(r * kn * gv[5]);
-      gate = dg;
-      s_r[t] = r; s_w[t] = w; s_k[t] = kn; s_a[t] = kh; s_b[t] = -kh * ag;
-      s.core[384 + t] = v;
+      if (wv == 0) {  // v, mixed with layer 0's v
+        float v = s.p2[128 + t];
+        if (l == 0) vfirst = v;
+        else v = v + sigmoidf_(gv[0] + d) * (vfirst - v);
+        s.core[384 + t] = v;
+        s_r[t] = s.p2[t];
+      } else if (wv == 1) {  // decay
+        s_w[t] = expf(-sigmoidf_(gv[1] + d) / 1.6487212707001282f);
+      } else if (wv == 2) {  // a, the normalised key kk and the key with its a-mix
+        const float r = s.p2[t], k = s.p2[64 + t];
+        const float ag = sigmoidf_(gv[2] + d);
+        const float kk = k * gv[3];
+        const float kn = k + gv[4] * (k * ag - k);
+        const float nrm = sqrtf(wave_sum(kk * kk));
+        const float kh = kk / fmaxf(nrm, 1e-12f);
+        const float rk = wave_sum(r * kn * gv[5]);
+        s_k[t] = kn; s_a[t] = kh; s_b[t] = -kh * ag;
+        if (t == 0) s.gsum[0] = rk;
+      } else {  // the two halves of the output gate's dot
+        s.gsum[wv * kN + t] = d;
+      }
     }
     __syncthreads();  // B2b
     // wkv7: 4 threads per state row, 16 columns each; the new state is written
@@ -741,14 +741,32 @@ RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
       }
       y = sum4(y);
       if ((mt & 3) == 0) s_y[row] = y;
+      // GroupNorm partials of this wave's 16 rows (each row's y is in 4 lanes)
+      const float m16 = wave_sum(y) * (1.f / (4 * 16));
+      const float dy = y - m16;
+      const float m2 = wave_sum(dy * dy) * 0.25f;
+      if (lane == 0) {
+        s.gsum[8 + 2 * wv] = m16;
+        s.gsum[9 + 2 * wv] = m2;
+      }
     }
     __syncthreads();  // B2c
     if (wv == 0) {
+      // GroupNorm of the head from the 4 waves' (mean, M2) over 16 rows each
+      float mean = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) mean += s.gsum[8 + 2 * w];
+      mean *= 0.25f;
+      float m2 = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float dm = s.gsum[8 + 2 * w] - mean;
+        m2 += s.gsum[9 + 2 * w] + 16.f * dm * dm;
+      }
       const float y = s_y[lane];
-      const float mean = wave_sum(y) * (1.f / kN);
-      const float d = y - mean;
-      const float var = wave_sum(d * d) * (1.f / kN);
-      const float yn = d * rsqrtf(var + kGnEps) * gv[6] + gv[7];
+      const float v = s.core[384 + lane], rk = s.gsum[0];
+      const float gate = s.gsum[3 * kN + lane] + s.gsum[4 * kN + lane];
+      const float yn = (y - mean) * rsqrtf(m2 * (1.f / kN) + kGnEps) * gv[6] + gv[7];
       const float out = (yn + rk * v) * gate;
 #pragma unroll
       for (int rp = 0; rp < kRep; ++rp) publish(a.core_ex + (int64_t)rp * C + g * kN + lane, cx.tag(5 * l + 1), out);
