@@ -696,9 +696,10 @@ RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
         const float ag = sigmoidf_(gv[2] + d);
         const float kk = k * gv[3];
         const float kn = k + gv[4] * (k * ag - k);
-        const float nrm = sqrtf(wave_sum(kk * kk));
-        const float kh = kk / fmaxf(nrm, 1e-12f);
-        const float rk = wave_sum(r * kn * gv[5]);
+        // kk / max(|kk|, 1e-12) = kk * rsqrt(max(|kk|^2, 1e-24)); both sums in lockstep
+        const float2 sums = wave_sum2(kk * kk, r * kn * gv[5]);
+        const float kh = kk * rsqrtf(fmaxf(sums.x, 1e-24f));
+        const float rk = sums.y;
         s_k[t] = kn; s_a[t] = kh; s_b[t] = -kh * ag;
         if (t == 0) s.gsum[0] = rk;
       } else {  // the two halves of the output gate's dot

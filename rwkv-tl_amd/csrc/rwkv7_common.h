@@ -62,6 +62,20 @@ RWKV7_DEV float wave_sum(float v) {
   return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
 }
 
+// Two independent wave sums, reduced in lockstep (one latency chain for both).
+RWKV7_DEV float2 wave_sum2(float a, float b) {
+  a += dpp<kDppXor1>(a);
+  b += dpp<kDppXor1>(b);
+  a += dpp<kDppXor2>(a);
+  b += dpp<kDppXor2>(b);
+  a += dpp<kDppHalfMirror>(a);
+  b += dpp<kDppHalfMirror>(b);
+  a += dpp<kDppMirror>(a);
+  b += dpp<kDppMirror>(b);
+  return make_float2((lane_value(a, 0) + lane_value(a, 16)) + (lane_value(a, 32) + lane_value(a, 48)),
+                     (lane_value(b, 0) + lane_value(b, 16)) + (lane_value(b, 32) + lane_value(b, 48)));
+}
+
 // ---- conversions ----------------------------------------------------------
 
 RWKV7_DEV void h8_to_f(const uint4 &u, float f[8]) {
