@@ -266,6 +266,123 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
   }
 }
 
+// Prefetch-all variant of gemm_kernel for splits of at most NC chunks (every
+// prefill GEMM at M <= 256 after plan_splits): all A chunks and all W chunks of
+// the split are issued before the first product, so a workgroup waits for one
+// memory round trip instead of one per chunk pair (the tiles are latency-bound
+// at these sizes, not bandwidth-bound). Same tiling, unit order, split-K
+// hand-off and epilogue as gemm_kernel.
+template <int BM, int NC>
+__global__ __launch_bounds__(256) void gemm_pf_kernel(GemmGroup g) {
+  constexpr int MB = BM / 16;
+  constexpr int kRowH = kKC + kLdsPadH;
+  constexpr int kAPer = BM * (kKC / 8) / 256;
+  __shared__ __align__(16) uint16_t s_a[NC][BM][kRowH];
+  __shared__ int s_last;
+
+  const int bx = blockIdx.x;
+  int pi = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxProb; ++i) pi += (i < g.nprob && bx >= g.wg_begin[i]);
+  const GemmProb &P = g.p[pi];
+  const int S = g.splits[pi];
+  const int local = bx - g.wg_begin[pi];
+  const int mtl = g.m_tiles;
+  const int u = local / (8 * mtl) * 8 + (local & 7);
+  const int mt = local % (8 * mtl) / 8;
+  const int nunits = (P.N + kBN - 1) / kBN * S;
+  if (u >= nunits) return;
+  const int split = u & (S - 1), nt = u / S;
+  const int tile = nt * mtl + mt;
+  const int m0 = mt * BM, n0 = nt * kBN;
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int M = g.M, N = P.N, K = P.K;
+  const int kb = split * g.kslice[pi];
+  const int ke = min(K, kb + g.kslice[pi]);
+  const int nch = (ke - kb + kKC - 1) / kKC;  // chunks of this split (<= NC)
+
+  // A pieces (row idx >> 4, 16-byte column idx & 15), loads clamped into range
+  // and masked when stored; a chunk past the split re-reads the split's last
+  // chunk (an L2 hit) and is never multiplied.
+  uint4 a_reg[NC][kAPer];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int k0 = kb + (c < nch ? c : nch - 1) * kKC;
+#pragma unroll
+    for (int q = 0; q < kAPer; ++q) {
+      const int idx = t + 256 * q;
+      const int r = m0 + (idx >> 4), k = k0 + 8 * (idx & 15);
+      const int rc = r < M ? r : M - 1, kc = k < K - 8 ? k : K - 8;
+      a_reg[c][q] = *reinterpret_cast<const uint4 *>(P.A + (int64_t)rc * P.lda + kc);
+    }
+  }
+  const bool frag = P.Wf != nullptr;
+  const int wn = n0 + wv * 16 + (lane & 15);
+  const int nstrip = (N + 15) / 16, strip = min(n0 / 16 + wv, nstrip - 1);
+  const uint16_t *wbase = frag ? P.Wf + ((int64_t)strip * P.nksf * 64 + lane) * 8
+                               : P.W + (int64_t)(wn < N ? wn : N - 1) * P.ldw;
+  const int nksf1 = P.nksf - 1, kb32 = kb / 32, wmul = frag ? 512 : 0, kmul = frag ? 0 : 1;
+  uint4 wr[NC][4];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int cc = c < nch ? c : nch - 1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = kb + cc * kKC + 32 * j + 8 * (lane >> 4);
+      const int ks = min(kb32 + 4 * cc + j, nksf1);
+      const int64_t off = (int64_t)ks * wmul + (k < K - 8 ? k : K - 8) * kmul;
+      wr[c][j] = *reinterpret_cast<const uint4 *>(wbase + off);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int k0 = kb + c * kKC;
+#pragma unroll
+    for (int q = 0; q < kAPer; ++q) {
+      const int idx = t + 256 * q;
+      const int r = m0 + (idx >> 4), k = k0 + 8 * (idx & 15);
+      const uint4 v = (r < M && k < ke) ? a_reg[c][q] : make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4 *>(&s_a[c][idx >> 4][8 * (idx & 15)]) = v;
+    }
+  }
+  __syncthreads();
+
+  floatx4 acc[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    if (c < nch) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const half8 bfrag = __builtin_bit_cast(half8, wr[c][j]);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const half8 afrag = __builtin_bit_cast(
+              half8, *reinterpret_cast<const uint4 *>(&s_a[c][mb * 16 + (lane & 15)][32 * j + 8 * (lane >> 4)]));
+          acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag, bfrag, acc[mb], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  const int col = n0 + wv * 16 + (lane & 15);
+  if (S > 1) {
+    float *pbase = g.part + g.part_off[pi] + (int64_t)tile * S * 4 * MB * 256;
+    if (!splitk_arrive<MB>(acc, pbase, S, split, 4, wv, g.ctr + g.ctr_off[pi] + tile, &s_last)) return;
+  }
+  if (col >= N) return;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = m0 + mb * 16 + (lane >> 4) * 4 + r;
+      if (row < M) store_epi(P, row, col, acc[mb][r]);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Skinny path, M <= 32 (batched decode, short prefill). One workgroup of 4
 // waves per 16-column strip of W (and per split of K, see below); the waves
@@ -533,6 +650,16 @@ int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, f
   }
   g.wg_begin[kMaxProb] = wgs;
   if (pfl * 4 > gemm_ws_bytes(M, cus) || ctrs > kGemmCounters) return RWKV7_EWORKSPACE;
+  // every split of at most 4 chunks: the prefetch-all kernel (BM <= 64)
+  int ncmax = 1;
+  for (int i = 0; i < nprob; ++i) ncmax = max(ncmax, ks[i] / kKC);
+  if (BM == 32 && ncmax <= 4) {
+    if (ncmax == 1) gemm_pf_kernel<32, 1><<<wgs, 256, 0, st>>>(g);
+    else if (ncmax == 2) gemm_pf_kernel<32, 2><<<wgs, 256, 0, st>>>(g);
+    else gemm_pf_kernel<32, 4><<<wgs, 256, 0, st>>>(g);
+    RWKV7_CHECK_LAUNCH();
+    return RWKV7_OK;
+  }
   switch (BM) {
     case 16: gemm_kernel<16><<<wgs, 256, 0, st>>>(g); break;
     case 32: gemm_kernel<32><<<wgs, 256, 0, st>>>(g); break;
