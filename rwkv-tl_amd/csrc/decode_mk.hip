@@ -304,19 +304,23 @@ RWKV7_DEV void slice_stats(const float *x, int w, int XS, float *st) {
 
 // LayerNorm mean and 1/std of a C-vector from its kW equal slices' (mean, M2)
 // (pairwise-combination formula: M2 = sum M2_w + XS * sum (mean_w - mean)^2).
-RWKV7_DEV float2 combine_stats(const float *st, int C) {
+// st is 16-byte aligned: the kW pairs are read as kW / 2 float4 in one batch.
+RWKV7_DEV float2 combine_stats(const float *st, int C, float inv_c) {
   const float XS = (float)(C / kW);
+  float4 q[kW / 2];
+#pragma unroll
+  for (int i = 0; i < kW / 2; ++i) q[i] = reinterpret_cast<const float4 *>(st)[i];
   float mean = 0.f;
 #pragma unroll
-  for (int w = 0; w < kW; ++w) mean += st[2 * w];
+  for (int i = 0; i < kW / 2; ++i) mean += q[i].x + q[i].z;
   mean *= 1.f / kW;
   float m2 = 0.f;
 #pragma unroll
-  for (int w = 0; w < kW; ++w) {
-    const float d = st[2 * w] - mean;
-    m2 += st[2 * w + 1] + XS * d * d;
+  for (int i = 0; i < kW / 2; ++i) {
+    const float d0 = q[i].x - mean, d1 = q[i].z - mean;
+    m2 += (q[i].y + XS * d0 * d0) + (q[i].w + XS * d1 * d1);
   }
-  return make_float2(mean, rsqrtf(m2 / (float)C + kLnEps));
+  return make_float2(mean, rsqrtf(m2 * inv_c + kLnEps));
 }
 
 // ---- comm wave ------------------------------------------------------------------
@@ -902,6 +906,13 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
   };
 
   float xown = 0.f;  // residual of channel owa + wv (waves wv < nown)
+  const float inv_c = 1.f / (float)C;
+  // materialises values loaded above (one wait for the whole batch) so the
+  // compiler does not sink the loads into the conditional code that uses them
+  auto keep_v = [](float (&v)[VPL]) {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) asm volatile("" ::"v"(v[i]));
+  };
   // x hand-offs: this wave reads slice wv of x (the comm wave slice kMW) and
   // leaves the slice's LayerNorm partial statistics in xst
   const int XS = C / kW;
@@ -927,13 +938,14 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     __syncthreads();  // A1
     refresh();
     {
-      const float2 st = combine_stats(s.xst, C);
+      const float2 st = combine_stats(s.xst, C, inv_c);
       float xv[VPL];  // read up front (index clamped), not one LDS round trip per element
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
         const int c = mt + kMT * i;
         xv[i] = s.x1[c < C ? c : C - 1];
       }
+      keep_v(xv);
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
         const int c = mt + kMT * i;
@@ -988,13 +1000,14 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     // ---------------- P4: LN2 + shift + FFN key + relu^2 ----------------------
     refresh();
     {
-      const float2 st = combine_stats(s.xst + 2 * kW, C);
+      const float2 st = combine_stats(s.xst + 2 * kW, C, inv_c);
       float xv[VPL];
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
         const int c = mt + kMT * i;
         xv[i] = s.x4[c < C ? c : C - 1];
       }
+      keep_v(xv);
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
         const int c = mt + kMT * i;
@@ -1049,7 +1062,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
   for (int b = 0; b < kHRing; ++b) pre_head(b, wh[b]);
   __syncthreads();  // AH
   {
-    const float2 st = combine_stats(s.xst, C);
+    const float2 st = combine_stats(s.xst, C, inv_c);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int c = mt + kMT * i;
