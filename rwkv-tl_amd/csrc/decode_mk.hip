@@ -19,20 +19,23 @@
 // Wave roles. Vector-memory loads of one wave complete in issue order, so a
 // wave that polls hand-off words while weight loads are in flight waits for
 // those loads on every poll. The workgroup therefore splits the two jobs:
-//   * wave 7 (the comm wave) polls each stage's input vector into LDS and
-//     never issues a weight load (one wave gathers a 1024-word vector in about
-//     half the time two waves that must agree on completion take);
-//   * waves 0..6 (math waves) stream weights into registers two stages ahead
-//     of their use and compute. A math wave waits for its loads only at the
-//     end of a stage (s_waitcnt vmcnt(0) right before it issues the next
-//     stage's loads), when everything outstanding is at least one stage old.
-// The two roles run separate code and meet at the same sequence of workgroup
-// barriers (listed in comm_main). Every output row belongs to one math wave,
-// and LayerNorm statistics are recomputed per wave, so apart from the per-head
-// core (P2) no stage needs a cross-wave reduction.
+//   * wave 7 (the comm wave) never issues a weight load; it probes each
+//     stage's input vector (one word, offset per workgroup) and, once the
+//     probe sees the vector arriving, tells the other waves through an LDS
+//     flag;
+//   * waves 0..6 (math waves) stream weights into registers a stage or more
+//     ahead of their use and compute; a worker issues all of a layer's
+//     remaining weight loads right after its P1 publish, so they are old by
+//     the time its next poll waits behind them.
+// After the probe every wave reads one slice of the vector (8 readers, one
+// read round), and leaves the LayerNorm partials (mean, M2) of its slice in
+// LDS; the stage's threads combine the 8 pairs. The roles meet at the same
+// sequence of workgroup barriers (listed above comm_worker). Every output row
+// belongs to one math wave, so apart from the per-head core (P2) and the
+// LayerNorm partials no stage needs a cross-wave reduction.
 //
-// Every wait is bounded: past ~1 s a comm wave raises a per-launch abort
-// word and gives up, every other comm wave then gives up within a few polls,
+// Every wait is bounded: past ~1 s a waiting wave raises a per-launch abort
+// word and gives up, every other waiting wave then gives up within a few polls,
 // and barriers never wait on memory, so a launch always terminates (its output
 // is then garbage and an error counter is set). The grid must be resident all
 // at once: one 512-thread workgroup per CU, grid = CU count.
@@ -253,37 +256,6 @@ RWKV7_DEV void load_row(const uint16_t *W, int64_t ld, int r, bool valid, int nc
   }
 }
 
-// Mean and 1/std of a C-vector in LDS (C <= 256 * NV), computed by one wave:
-// one batched read into registers, then two passes over them.
-template <int NV>
-RWKV7_DEV float2 wave_ln_stats(const float *x, int C) {
-  const int lane = threadIdx.x & 63;
-  const float4 *x4 = reinterpret_cast<const float4 *>(x);
-  const int C4 = C >> 2;
-  float4 v[NV];
-#pragma unroll
-  for (int k = 0; k < NV; ++k) {  // unconditional reads (index clamped), zeroed after
-    const int i = lane + 64 * k;
-    v[k] = x4[i < C4 ? i : C4 - 1];
-  }
-#pragma unroll
-  for (int k = 0; k < NV; ++k)
-    if (lane + 64 * k >= C4) v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-  float s = 0.f;
-#pragma unroll
-  for (int k = 0; k < NV; ++k) s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
-  const float mean = wave_sum(s) / (float)C;
-  float q = 0.f;
-#pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    if (lane + 64 * k < C4) {
-      const float a = v[k].x - mean, b = v[k].y - mean, c = v[k].z - mean, d = v[k].w - mean;
-      q += (a * a + b * b) + (c * c + d * d);
-    }
-  }
-  return make_float2(mean, rsqrtf(wave_sum(q) / (float)C + kLnEps));
-}
-
 // ---- x hand-offs: every wave reads one slice ------------------------------------
 
 // Mean and M2 (sum of squared deviations) of this wave's slice
@@ -375,7 +347,15 @@ RWKV7_DEV void probe_wait(const MkCtx &cx, int cw, __amdgpu_buffer_rsrc_t r, int
   }
 }
 
-// Full phase: reads every pair until all carry the tag (see comm_poll).
+// Reads until every word idx(i), i < n, of the buffer `r` carries `tag`,
+// handing each value to put(i, v). idx must map each even i and i + 1 to
+// consecutive, 16-byte aligned words; lane l of wave cw handles the pairs
+// p = 64 cw + l + 64 kNComm j (j < NJ), i = 2p. A round is one 16-byte load per
+// pair; D rounds stay in flight (re-issued unconditionally, so the compiler's
+// load counting stays exact), checked oldest first, at most 16 loads per lane.
+// Poll traffic slows every hand-off on the chip, so callers start this only
+// after a sparse probe (probe_wait, here or in the workgroup's comm wave, which
+// then raises an LDS flag) and use D = 1.
 template <int NJ, int D, typename Idx, typename Put>
 RWKV7_DEV void read_all(const MkCtx &cx, int cw, __amdgpu_buffer_rsrc_t r, int n, unsigned tag, Idx idx, Put put) {
   static_assert(NJ * D <= 16 && NJ <= 16, "at most 16 loads per lane in flight");
@@ -417,24 +397,6 @@ RWKV7_DEV void read_all(const MkCtx &cx, int cw, __amdgpu_buffer_rsrc_t r, int n
     }
     if (__builtin_amdgcn_ballot_w64(pending != 0) == 0 || !sb.keep_waiting()) break;
   }
-}
-
-// Waits until every word idx(i), i < n, of the buffer `r` carries `tag`,
-// handing each value to put(i, v). idx must map each even i and i + 1 to
-// consecutive, 16-byte aligned words. Comm wave cw, lane l handles the pairs
-// p = 64 cw + l + 64 kNComm j (j < NJ), i = 2p.
-//
-// A poll round is one 16-byte load per pair. The full phase keeps D rounds in
-// flight (re-issued unconditionally, so the compiler's load counting stays
-// exact) and checks them oldest first. At most 16 loads per lane are in
-// flight. `probe` > 0 first polls one pair in every `probe` words until those
-// carry the tag, to spare traffic while producers still compute: poll traffic
-// slows every hand-off on the chip, so probes are sparse and D is 1.
-template <int NJ, int D, typename Idx, typename Put>
-RWKV7_DEV void comm_poll(const MkCtx &cx, int cw, __amdgpu_buffer_rsrc_t r, int n, int probe, unsigned tag,
-                         Idx idx, Put put) {
-  if (probe > 0) probe_wait(cx, cw, r, n, probe, tag, idx);
-  read_all<NJ, D>(cx, cw, r, n, tag, idx, put);
 }
 
 // Waits (LDS spin, bounded) until *flag == tag. Only a start hint: the reads
@@ -488,11 +450,10 @@ RWKV7_DEV void wait_local(const MkCtx &cx, const unsigned *pubs, unsigned target
 // P5); the comm wave starts reading a vector the workers produce only after
 // its own workgroup's share is out.
 
-// NJX: pairs per comm lane of a C-vector; NJF: of one of the kW slices of
-// the FFN hidden vector (every wave of the workgroup reads one slice).
-template <int NJX, int NJF>
-RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, const MkCtx &cx, int cw) {
-  constexpr int DX = 1;
+// NJF: pairs per lane of one of the kW slices of the FFN hidden vector (every
+// wave of the workgroup reads one slice).
+template <int NJF>
+RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, const MkCtx &cx) {
   const int lane = threadIdx.x & 63;
   const int C = m.C, F = m.F, L = m.L;
   int64_t token = a.tok[0];
@@ -579,12 +540,9 @@ RWKV7_DEV void head_read(const MkCtx &cx, const MkArgs &a, const MkLds &s, int h
                  });
 }
 
-// NJP: pairs per comm lane of the P2 input vector.
-template <int NJP>
-RWKV7_DEV void comm_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const MkCtx &cx, int cw) {
-  constexpr int DP = 1;
+RWKV7_DEV void comm_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const MkCtx &cx) {
   const int C = m.C, SR = m.SR, L = m.L;
-  const int h = m.g, rv = a.rv, rwa = a.rv + a.rw, rwaa = a.rv + a.rw + a.ra;
+  const int h = m.g;
   const __amdgpu_buffer_rsrc_t r_proj = words_rsrc(a.proj_ex + (int64_t)(h % kRep) * (3 * C + SR), 3 * C + SR);
   for (int l = 0; l < L; ++l) {
     // r, k, v of this head and the whole LoRA first step: a sparse probe
@@ -1097,7 +1055,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
 // One workgroup per CU by construction (2 waves per SIMD): telling the
 // compiler so keeps its scheduler from trading prefetch distance for an
 // occupancy this kernel never runs at.
-template <int CPL, int RM, int NC5, int VPL, int NL2, int NJ, int NHB>
+template <int CPL, int RM, int NC5, int VPL, int NL2, int NHB>
 __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_mk_kernel(MkArgs a) {
   extern __shared__ __align__(16) float smem[];
   MkGeom m;
@@ -1143,10 +1101,10 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   }
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (m.head) {
-    if (wv >= kMW) comm_head<NJ>(a, m, s, cx, wv - kMW);
+    if (wv >= kMW) comm_head(a, m, s, cx);
     else math_head<NL2>(a, m, s, cx, wv);
   } else {
-    if (wv >= kMW) comm_worker<4 * CPL / kNComm, NC5 / 2>(a, m, s, cx, wv - kMW);
+    if (wv >= kMW) comm_worker<NC5 / 2>(a, m, s, cx);
     else math_worker<CPL, RM, NC5, VPL, NHB>(a, m, s, cx, wv);
   }
   // A worker ends only after every workgroup has published (its logits need
@@ -1157,10 +1115,9 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 
 // ---- host side --------------------------------------------------------------
 
-// The one compiled instance: CPL 2, RM 3, NC5 8, VPL 3, NL2 8, NJ 4, NHB 10
-// (NJ: pairs per comm lane of the P2 input vector).
-constexpr int kCPL = 2, kRM = 3, kNC5 = 8, kVPL = 3, kNL2 = 8, kNJ = 4, kNHB = 10;
-#define RWKV7_MK_INSTANCE decode_mk_kernel<kCPL, kRM, kNC5, kVPL, kNL2, kNJ, kNHB>
+// The one compiled instance: CPL 2, RM 3, NC5 8, VPL 3, NL2 8, NHB 10.
+constexpr int kCPL = 2, kRM = 3, kNC5 = 8, kVPL = 3, kNL2 = 8, kNHB = 10;
+#define RWKV7_MK_INSTANCE decode_mk_kernel<kCPL, kRM, kNC5, kVPL, kNL2, kNHB>
 
 static int cdiv(int a, int b) { return (a + b - 1) / b; }
 
@@ -1204,7 +1161,10 @@ bool mk_supported(const rwkv7_dims &d, int G) {
     if (cv > kNL2 || cw > kNL2 || ca > kNL2 || (cg + 1) / 2 > kNL2 || kMW < 5) return false;
   }
   const int cj = 2 * 64 * kNComm;  // words per round: one pair per lane and slot
-  if (cdiv(C, cj) > 4 * kCPL / kNComm || cdiv(F / kW, cj) > kNC5 / 2 || cdiv(192 + SR, cj) > kNJ) return false;
+  // x, core and hidden-vector slices: one read round of at most one (x, core)
+  // or NC5 / 2 (hidden) pairs per lane; the P2 input in kW even slices of at
+  // most 128 words
+  if (C / kW > cj || cdiv(F / kW, cj) > kNC5 / 2 || ((192 + SR + kW - 1) / kW + 1) / 2 > 64) return false;
   if (F % (2 * kW)) return false;  // hidden-vector slices of whole 16-byte pairs
   if (C % (2 * kW) || C / kW > 128) return false;  // x slices: whole pairs, <= 2 values per lane
   if (H > 64 * kNComm) return false;  // one probe lane per head
