@@ -123,6 +123,90 @@ RWKV7_DEV bool splitk_arrive(floatx4 (&acc)[MB], float *pbase, int S, int split,
   return true;
 }
 
+// The work unit of one tiled-GEMM workgroup (gemm_kernel, gemm_pf_kernel).
+// Workgroup order: a unit u = (n-tile, split) reads one W slice; its m-tiles
+// get indices 8 apart, so they run on the same XCD (workgroups are dealt
+// round-robin over the 8 XCDs) and all but the first find W in that L2.
+struct TileUnit {
+  int pi, S, split, tile, m0, n0, kb, ke, nch;
+  bool live;  // false for the padding of the last group of 8 units
+};
+template <int BM>
+RWKV7_DEV TileUnit tile_unit(const GemmGroup &g) {
+  TileUnit w;
+  const int bx = blockIdx.x;
+  w.pi = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxProb; ++i) w.pi += (i < g.nprob && bx >= g.wg_begin[i]);
+  const GemmProb &P = g.p[w.pi];
+  w.S = g.splits[w.pi];
+  const int local = bx - g.wg_begin[w.pi];
+  const int mtl = g.m_tiles;
+  const int u = local / (8 * mtl) * 8 + (local & 7);
+  const int mt = local % (8 * mtl) / 8;
+  w.live = u < (P.N + kBN - 1) / kBN * w.S;
+  w.split = u & (w.S - 1);
+  const int nt = u / w.S;
+  w.tile = nt * mtl + mt;
+  w.m0 = mt * BM;
+  w.n0 = nt * kBN;
+  w.kb = w.split * g.kslice[w.pi];
+  w.ke = min(P.K, w.kb + g.kslice[w.pi]);
+  w.nch = (w.ke - w.kb + kKC - 1) / kKC;  // chunks of this split
+  return w;
+}
+
+// W of k-step ks (a 32-wide k block) for the wave's 16-column strip: lane ->
+// row n0 + 16 wv + (lane & 15), 8 k at 32 ks + 8 (lane >> 4). In fragment
+// order the strip (clamped to the padded rows) is one contiguous KiB per
+// k-step; k-steps past the padded K are clamped (out-of-range k meets a zero A,
+// out-of-range rows are never stored).
+struct WStrip {
+  const uint16_t *base;
+  int K, nksf1, wmul, kmul, lane;
+  RWKV7_DEV uint4 load(int kstep) const {
+    const int k = 32 * kstep + 8 * (lane >> 4);
+    const int ks = min(kstep, nksf1);
+    const int64_t off = (int64_t)ks * wmul + (k < K - 8 ? k : K - 8) * kmul;
+    return *reinterpret_cast<const uint4 *>(base + off);
+  }
+};
+RWKV7_DEV WStrip w_strip(const GemmProb &P, int n0, int wv, int lane) {
+  WStrip s;
+  const bool frag = P.Wf != nullptr;
+  const int wn = n0 + wv * 16 + (lane & 15);
+  const int nstrip = (P.N + 15) / 16, strip = min(n0 / 16 + wv, nstrip - 1);
+  s.base = frag ? P.Wf + ((int64_t)strip * P.nksf * 64 + lane) * 8 : P.W + (int64_t)(wn < P.N ? wn : P.N - 1) * P.ldw;
+  s.K = P.K;
+  s.nksf1 = P.nksf - 1;
+  s.wmul = frag ? 512 : 0;
+  s.kmul = frag ? 0 : 1;
+  s.lane = lane;
+  return s;
+}
+
+// Split-K hand-off (when S > 1) and epilogue of a workgroup's tile: lane holds
+// rows 4 (lane >> 4) + {0..3} of column (lane & 15) of each 16-row block.
+template <int MB>
+RWKV7_DEV void tile_store(const GemmGroup &g, const TileUnit &w, floatx4 (&acc)[MB], int *s_last) {
+  const GemmProb &P = g.p[w.pi];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int col = w.n0 + wv * 16 + (lane & 15);
+  if (w.S > 1) {
+    float *pbase = g.part + g.part_off[w.pi] + (int64_t)w.tile * w.S * 4 * MB * 256;
+    if (!splitk_arrive<MB>(acc, pbase, w.S, w.split, 4, wv, g.ctr + g.ctr_off[w.pi] + w.tile, s_last)) return;
+  }
+  if (col >= P.N) return;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = w.m0 + mb * 16 + (lane >> 4) * 4 + r;
+      if (row < g.M) store_epi(P, row, col, acc[mb][r]);
+    }
+  }
+}
+
 template <int BM>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
   constexpr int MB = BM / 16;                // 16-row blocks
@@ -131,29 +215,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
   __shared__ __align__(16) uint16_t s_a[2][BM][kRowH];
   __shared__ int s_last;
 
-  const int bx = blockIdx.x;
-  int pi = 0;
-#pragma unroll
-  for (int i = 1; i < kMaxProb; ++i) pi += (i < g.nprob && bx >= g.wg_begin[i]);
-  const GemmProb &P = g.p[pi];
-  const int S = g.splits[pi];
-  const int local = bx - g.wg_begin[pi];
-  // Workgroup order: a unit u = (n-tile, split) reads one W slice; its m-tiles
-  // get indices 8 apart, so they run on the same XCD (workgroups are dealt
-  // round-robin over the 8 XCDs) and all but the first find W in that L2.
-  const int mtl = g.m_tiles;
-  const int u = local / (8 * mtl) * 8 + (local & 7);
-  const int mt = local % (8 * mtl) / 8;
-  const int nunits = (P.N + kBN - 1) / kBN * S;
-  if (u >= nunits) return;  // padding of the last group of 8 units
-  const int split = u & (S - 1), nt = u / S;
-  const int tile = nt * mtl + mt;
-  const int m0 = mt * BM, n0 = nt * kBN;
+  const TileUnit U = tile_unit<BM>(g);
+  if (!U.live) return;
+  const GemmProb &P = g.p[U.pi];
+  const int m0 = U.m0, kb = U.kb, ke = U.ke, nch = U.nch;
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-  const int M = g.M, N = P.N, K = P.K;
-  const int kb = split * g.kslice[pi];
-  const int ke = min(K, kb + g.kslice[pi]);
-  const int nch = (ke - kb + kKC - 1) / kKC;  // chunks of this split
+  const int M = g.M, K = P.K;
 
   // A staging: piece idx -> row idx >> 4, 16-byte column idx & 15. Loads are
   // unconditional (row and k clamped into range) and masked after arrival, so
@@ -179,25 +246,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
       *reinterpret_cast<uint4 *>(&s_a[buf][idx >> 4][8 * (idx & 15)]) = v;
     }
   };
-  // W fragment of k-step j of chunk c: lane -> row n0 + 16 wv + (lane & 15),
-  // 8 k at 32 j + 8 (lane >> 4) (clamped into range; out-of-range k meets a
-  // zero A and out-of-range rows are never stored).
-  // In fragment order the wave's strip (clamped to the padded rows) is read
-  // one contiguous KiB per k-step; k-steps past the padded K are clamped.
-  const bool frag = P.Wf != nullptr;
-  const int wn = n0 + wv * 16 + (lane & 15);
-  const int nstrip = (N + 15) / 16, strip = min(n0 / 16 + wv, nstrip - 1);
-  const uint16_t *wbase = frag ? P.Wf + ((int64_t)strip * P.nksf * 64 + lane) * 8
-                               : P.W + (int64_t)(wn < N ? wn : N - 1) * P.ldw;
-  const int nksf1 = P.nksf - 1, kb32 = kb / 32, wmul = frag ? 512 : 0, kmul = frag ? 0 : 1;
+  // W fragments of chunk c: k-steps kb/32 + 4c + j (see WStrip)
+  const WStrip ws = w_strip(P, U.n0, wv, lane);
+  const int kb32 = kb / 32;
   auto load_w = [&](int c, uint4 (&dst)[4]) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int k = kb + c * kKC + 32 * j + 8 * (lane >> 4);
-      const int ks = min(kb32 + 4 * c + j, nksf1);
-      const int64_t off = (int64_t)ks * wmul + (k < K - 8 ? k : K - 8) * kmul;
-      dst[j] = *reinterpret_cast<const uint4 *>(wbase + off);
-    }
+    for (int j = 0; j < 4; ++j) dst[j] = ws.load(kb32 + 4 * c + j);
   };
 
   floatx4 acc[MB];
@@ -249,21 +303,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
     __syncthreads();
   }
 
-  // Epilogue: lane holds rows 4 * (lane >> 4) + {0..3} of column (lane & 15).
-  const int col = n0 + wv * 16 + (lane & 15);
-  if (S > 1) {
-    float *pbase = g.part + g.part_off[pi] + (int64_t)tile * S * 4 * MB * 256;
-    if (!splitk_arrive<MB>(acc, pbase, S, split, 4, wv, g.ctr + g.ctr_off[pi] + tile, &s_last)) return;
-  }
-  if (col >= N) return;
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = m0 + mb * 16 + (lane >> 4) * 4 + r;
-      if (row < M) store_epi(P, row, col, acc[mb][r]);
-    }
-  }
+  tile_store<MB>(g, U, acc, &s_last);
 }
 
 // Prefetch-all variant of gemm_kernel for splits of at most NC chunks (every
@@ -280,26 +320,12 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmGroup g) {
   __shared__ __align__(16) uint16_t s_a[NC][BM][kRowH];
   __shared__ int s_last;
 
-  const int bx = blockIdx.x;
-  int pi = 0;
-#pragma unroll
-  for (int i = 1; i < kMaxProb; ++i) pi += (i < g.nprob && bx >= g.wg_begin[i]);
-  const GemmProb &P = g.p[pi];
-  const int S = g.splits[pi];
-  const int local = bx - g.wg_begin[pi];
-  const int mtl = g.m_tiles;
-  const int u = local / (8 * mtl) * 8 + (local & 7);
-  const int mt = local % (8 * mtl) / 8;
-  const int nunits = (P.N + kBN - 1) / kBN * S;
-  if (u >= nunits) return;
-  const int split = u & (S - 1), nt = u / S;
-  const int tile = nt * mtl + mt;
-  const int m0 = mt * BM, n0 = nt * kBN;
+  const TileUnit U = tile_unit<BM>(g);
+  if (!U.live) return;
+  const GemmProb &P = g.p[U.pi];
+  const int m0 = U.m0, kb = U.kb, ke = U.ke, nch = U.nch;  // nch <= NC
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-  const int M = g.M, N = P.N, K = P.K;
-  const int kb = split * g.kslice[pi];
-  const int ke = min(K, kb + g.kslice[pi]);
-  const int nch = (ke - kb + kKC - 1) / kKC;  // chunks of this split (<= NC)
+  const int M = g.M, K = P.K;
 
   // A pieces (row idx >> 4, 16-byte column idx & 15), loads clamped into range
   // and masked when stored; a chunk past the split re-reads the split's last
@@ -316,23 +342,14 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmGroup g) {
       a_reg[c][q] = *reinterpret_cast<const uint4 *>(P.A + (int64_t)rc * P.lda + kc);
     }
   }
-  const bool frag = P.Wf != nullptr;
-  const int wn = n0 + wv * 16 + (lane & 15);
-  const int nstrip = (N + 15) / 16, strip = min(n0 / 16 + wv, nstrip - 1);
-  const uint16_t *wbase = frag ? P.Wf + ((int64_t)strip * P.nksf * 64 + lane) * 8
-                               : P.W + (int64_t)(wn < N ? wn : N - 1) * P.ldw;
-  const int nksf1 = P.nksf - 1, kb32 = kb / 32, wmul = frag ? 512 : 0, kmul = frag ? 0 : 1;
+  const WStrip ws = w_strip(P, U.n0, wv, lane);
+  const int kb32 = kb / 32;
   uint4 wr[NC][4];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int cc = c < nch ? c : nch - 1;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int k = kb + cc * kKC + 32 * j + 8 * (lane >> 4);
-      const int ks = min(kb32 + 4 * cc + j, nksf1);
-      const int64_t off = (int64_t)ks * wmul + (k < K - 8 ? k : K - 8) * kmul;
-      wr[c][j] = *reinterpret_cast<const uint4 *>(wbase + off);
-    }
+    for (int j = 0; j < 4; ++j) wr[c][j] = ws.load(kb32 + 4 * cc + j);
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -367,20 +384,7 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmGroup g) {
     }
   }
 
-  const int col = n0 + wv * 16 + (lane & 15);
-  if (S > 1) {
-    float *pbase = g.part + g.part_off[pi] + (int64_t)tile * S * 4 * MB * 256;
-    if (!splitk_arrive<MB>(acc, pbase, S, split, 4, wv, g.ctr + g.ctr_off[pi] + tile, &s_last)) return;
-  }
-  if (col >= N) return;
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = m0 + mb * 16 + (lane >> 4) * 4 + r;
-      if (row < M) store_epi(P, row, col, acc[mb][r]);
-    }
-  }
+  tile_store<MB>(g, U, acc, &s_last);
 }
 
 // ---------------------------------------------------------------------------
