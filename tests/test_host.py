@@ -168,6 +168,24 @@ def test_weight_loads_checkpoint_file(tmp_path):
     assert w.L == 3 and w.dtype == torch.float16 and w.head.dtype == torch.float16
 
 
+def test_weight_loads_bf16_checkpoint_as_fp16(tmp_path):
+    """Real checkpoints are bf16 (src/rwkv_tl/weight.py:161-169): the loader
+    converts every tensor to the target dtype once, so a bf16 file loads to
+    exactly the fp16 rounding of its values, and LN0 is applied to emb in
+    fp16 (the same path as an fp16 file of those values)."""
+    sd32 = make_random_state_dict("tiny", seed=2, dtype=torch.float32)
+    sd_bf16 = {k: v.to(torch.bfloat16) for k, v in sd32.items()}
+    p = tmp_path / "ck_bf16.pth"
+    torch.save(sd_bf16, p)
+    w = RWKV7Weight(str(p), device="cpu", dtype=torch.float16)
+    ref = RWKV7Weight.from_state_dict({k: v.to(torch.float16) for k, v in sd_bf16.items()}, device="cpu")
+    assert w.head.dtype == torch.float16
+    assert torch.equal(w.head, sd_bf16["head.weight"].to(torch.float16))
+    assert torch.equal(w.emb, ref.emb)
+    for a, b in zip(w.blocks, ref.blocks):
+        assert torch.equal(a.att.rkvWt[1], b.att.rkvWt[1]) and torch.equal(a.ffn.vWt, b.ffn.vWt)
+
+
 # Known answers of the reference's test/test_sampling.py:11-59.
 def test_sampling_greedy_argmax():
     logits = torch.tensor([1.0, 2.0, 0.5, 3.0])
