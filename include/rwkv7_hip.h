@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define RWKV7_ABI_VERSION 2
+#define RWKV7_ABI_VERSION 3
 #define RWKV7_HEAD_SIZE 64
 
 enum {
@@ -247,6 +247,36 @@ int rwkv7_l2norm_neg_kk_a(const void *kk, const void *a, void *kk_norm, void *b,
  * Replaces fused_gn_rkrk (dplr.py:73-124,237-254). */
 int rwkv7_gn_rkrk(const void *y, const void *r, const void *k, const void *v, const void *r_k,
                   const void *ln_w, const void *ln_b, void *out, int32_t H, void *stream);
+
+/* ---- sampling ---------------------------------------------------------- */
+
+/* Parameters of one sampling call (demo/sampling.py:13-70). */
+typedef struct rwkv7_sampling {
+  float temperature;        /* <= 0: greedy argmax, first index among ties */
+  int32_t top_k;            /* <= 0 or >= V: no top-k filter */
+  float top_p;              /* >= 1: no nucleus filter */
+  float repetition_penalty; /* 1: none; else seen tokens' logits x -> x > 0 ? x / p : x * p */
+  uint64_t seed;            /* Philox4x32-10 key */
+  uint64_t offset;          /* counter of this draw (one per call; the row is the second counter word) */
+} rwkv7_sampling;
+
+/* Sample one token per row of logits [B, V], f16 or f32 (logits_is_f32;
+ * row stride ld elements, V <= 65536), into out i64 [B]. In order: repetition penalty on the tokens
+ * whose bit is set in seen u32 [B, seen_ld] (bit t % 32 of word t / 32;
+ * NULL: none), greedy argmax if temperature <= 0, else division by the
+ * temperature, top-k (keep x >= the k-th largest), top-p (keep the tokens
+ * whose descending-order cumulative probability, excluding their own, is
+ * <= top_p) and one draw from the kept distribution, computed in 64-bit fixed
+ * point and drawn by inverse CDF in vocabulary order with Philox4x32-10
+ * (key = seed, counter = (offset, row, 0)). update_seen sets the sampled
+ * token's bit in seen. probs f32 [B, probs_ld] (optional) receives the kept
+ * distribution (one-hot when greedy). One workgroup per row, no host sync.
+ * Stands in for sample_logits (demo/sampling.py:13-70) as called by
+ * RWKV7Model.generate (demo/_rwkv7_abc.py:41-72), with the draw of
+ * torch.multinomial replaced by the counter-based one above. */
+int rwkv7_sample(const void *logits, int32_t logits_is_f32, int64_t ld, int32_t B, int32_t V, const rwkv7_sampling *params,
+                 uint32_t *seen, int64_t seen_ld, int32_t update_seen, int64_t *out, float *probs,
+                 int64_t probs_ld, void *stream);
 
 #ifdef __cplusplus
 }

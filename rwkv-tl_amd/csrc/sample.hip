@@ -1,0 +1,414 @@
+// Token sampling on the device: repetition penalty, greedy argmax,
+// temperature, top-k, top-p and the random draw for each row of logits, in
+// one launch (semantics of demo/sampling.py:13-70).
+//
+// One 1024-thread workgroup per row; thread t holds logits [64 t, 64 t + 64)
+// (f16 or f32 in memory, f32 in registers; V <= 65536), so the row is read
+// from HBM once.
+//
+// * Thresholds. top-k keeps x >= the k-th largest value (ties kept, as
+//   torch.topk's cutoff with `>=`); top-p keeps x >= the largest value y whose
+//   inclusive mass sum_{x_j >= y} p_j exceeds top_p (the token at which the
+//   descending cumulative mass first passes top_p is the last one kept, as in
+//   sampling.py:62-68). Both are "largest value y with weight(x >= y) > W"
+//   and are found exactly, without sorting: one pass of 256 equal-width bins
+//   over [min, max] (the bin index is a monotone function of x), then radix
+//   passes of up to 8 bits over the order-preserving integer key of x inside
+//   the chosen bin, until one value remains.
+// * Mass. exp(x - max) is summed in 64-bit fixed point (scale 2^40), so every
+//   sum is exact and the result does not depend on summation order.
+// * Draw. One Philox4x32-10 block (Salmon et al., "Parallel random numbers:
+//   as easy as 1, 2, 3", SC'11) per row: key = seed, counter = (offset, row,
+//   0). Its first 64 bits r pick target = floor(Z r / 2^64) in [0, Z), and the
+//   token is the first index (vocabulary order) whose inclusive prefix of kept
+//   mass exceeds target: inverse-CDF sampling of the kept distribution.
+#include "rwkv7_common.h"
+
+namespace rwkv7 {
+namespace {
+
+typedef unsigned long long u64;
+
+constexpr int kSmpThreads = 1024;
+constexpr int kSmpWaves = kSmpThreads / kWave;
+constexpr int kSmpE = 64;                      // logits per thread
+constexpr int kSmpMaxV = kSmpThreads * kSmpE;  // 65536
+constexpr float kFix = 1099511627776.0f;       // 2^40
+constexpr float kInf = __builtin_inff();
+
+struct SampleArgs {
+  const void *logits;
+  int64_t ld;
+  int V;
+  float temp, top_p, pen;
+  int top_k;
+  uint32_t seed_lo, seed_hi, off_lo, off_hi;
+  uint32_t *seen;
+  int64_t seen_ld;
+  int update_seen;
+  int64_t *out;
+  float *probs;
+  int64_t probs_ld;
+};
+
+struct SampleLds {
+  u64 hist[256];
+  u64 wu[kSmpWaves];
+  float wa[kSmpWaves], wb[kSmpWaves];
+  int wi[kSmpWaves];
+  u64 cross_above;
+  int cross_bin;
+};
+
+RWKV7_DEV uint32_t okey(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+RWKV7_DEV float okey_inv(uint32_t k) { return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k); }
+
+RWKV7_DEV u64 shfl_xor64(u64 v, int m) {
+  const int lo = __shfl_xor((int)(uint32_t)v, m), hi = __shfl_xor((int)(uint32_t)(v >> 32), m);
+  return (u64)(uint32_t)lo | ((u64)(uint32_t)hi << 32);
+}
+RWKV7_DEV u64 shfl_up64(u64 v, int d) {
+  const int lo = __shfl_up((int)(uint32_t)v, d), hi = __shfl_up((int)(uint32_t)(v >> 32), d);
+  return (u64)(uint32_t)lo | ((u64)(uint32_t)hi << 32);
+}
+RWKV7_DEV u64 shfl_down64(u64 v, int d) {
+  const int lo = __shfl_down((int)(uint32_t)v, d), hi = __shfl_down((int)(uint32_t)(v >> 32), d);
+  return (u64)(uint32_t)lo | ((u64)(uint32_t)hi << 32);
+}
+
+// The compiler would otherwise keep per-element values (64 u64 weights, 64
+// keys) live from one pass to the next instead of recomputing them from the 64
+// logits, which overflows the 128 VGPRs of a 1024-thread workgroup: each pass
+// reads its constants through this opaque copy.
+RWKV7_DEV float opaque(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+RWKV7_DEV u64 mass(float x, float m) { return (u64)(expf(x - m) * kFix); }
+
+RWKV7_DEV bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+// Block (max value, lowest index among ties); every thread gets the result.
+RWKV7_DEV void block_argmax(float &v, int &i, SampleLds &s) {
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) {
+    const float ov = __shfl_xor(v, m);
+    const int oi = __shfl_xor(i, m);
+    if (better(ov, oi, v, i)) v = ov, i = oi;
+  }
+  const int w = threadIdx.x / kWave;
+  if (threadIdx.x % kWave == 0) s.wa[w] = v, s.wi[w] = i;
+  __syncthreads();
+  v = s.wa[0], i = s.wi[0];
+  for (int j = 1; j < kSmpWaves; ++j)
+    if (better(s.wa[j], s.wi[j], v, i)) v = s.wa[j], i = s.wi[j];
+  __syncthreads();
+}
+
+RWKV7_DEV void block_minmax(float &lo, float &hi, SampleLds &s) {
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) {
+    lo = fminf(lo, __shfl_xor(lo, m));
+    hi = fmaxf(hi, __shfl_xor(hi, m));
+  }
+  const int w = threadIdx.x / kWave;
+  if (threadIdx.x % kWave == 0) s.wa[w] = lo, s.wb[w] = hi;
+  __syncthreads();
+  lo = s.wa[0], hi = s.wb[0];
+  for (int j = 1; j < kSmpWaves; ++j) lo = fminf(lo, s.wa[j]), hi = fmaxf(hi, s.wb[j]);
+  __syncthreads();
+}
+
+// Exclusive prefix of x over the block in thread order, and the block total.
+RWKV7_DEV u64 block_excl_scan(u64 x, u64 &total, SampleLds &s) {
+  const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+  u64 inc = x;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const u64 o = shfl_up64(inc, d);
+    if (lane >= d) inc += o;
+  }
+  if (lane == kWave - 1) s.wu[w] = inc;
+  __syncthreads();
+  u64 base = 0, tot = 0;
+  for (int j = 0; j < kSmpWaves; ++j) {
+    const u64 o = s.wu[j];
+    base += j < w ? o : 0ull;
+    tot += o;
+  }
+  __syncthreads();
+  total = tot;
+  return base + inc - x;
+}
+
+// Over s.hist, the largest bin b with above + sum_{b' >= b} hist[b'] > W.
+// Sets s.cross_bin = b (-1 if none) and s.cross_above = above + sum_{b' > b}.
+RWKV7_DEV void find_cross(SampleLds &s, u64 above, u64 W) {
+  if (threadIdx.x < kWave) {
+    const int L = threadIdx.x;
+    const u64 h[4] = {s.hist[4 * L], s.hist[4 * L + 1], s.hist[4 * L + 2], s.hist[4 * L + 3]};
+    const u64 own = (h[0] + h[1]) + (h[2] + h[3]);
+    u64 suf = own;  // sum over bins >= 4 L
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const u64 o = shfl_down64(suf, d);
+      if (L + d < kWave) suf += o;
+    }
+    // suf does not increase with L, so the lanes that pass form a prefix
+    const u64 mask = __ballot(above + suf > W);
+    if (mask == 0) {
+      if (L == 0) s.cross_bin = -1;
+    } else if (L == 63 - __clzll(mask)) {
+      u64 acc = above + suf - own;  // <= W: the lane above failed
+      int b = 4 * L;
+      for (int j = 3; j >= 0; --j) {
+        if (acc + h[j] > W) {
+          b = 4 * L + j;
+          break;
+        }
+        acc += h[j];
+      }
+      s.cross_bin = b;
+      s.cross_above = acc;
+    }
+  }
+  __syncthreads();
+}
+
+// Largest kept value y (kept: x > -inf) with sum over kept x >= y of wt(x)
+// > W, where wt(x) = 1 (MASS false) or floor(exp(x - m) 2^40). If the total
+// is <= W, the smallest kept value (so every kept element stays kept).
+template <bool MASS>
+RWKV7_DEV float select_gt(const float (&l)[kSmpE], float m, u64 W, SampleLds &s) {
+  auto wt = [](float x, float mm) -> u64 { return MASS ? mass(x, mm) : 1ull; };
+  float lo = kInf, hi = -kInf;
+#pragma unroll
+  for (int e = 0; e < kSmpE; ++e)
+    if (l[e] > -kInf) lo = fminf(lo, l[e]), hi = fmaxf(hi, l[e]);
+  block_minmax(lo, hi, s);
+  if (!(lo < hi)) return lo;
+  // pass 0: equal-width bins over [lo, hi]
+  const float scale = fminf(256.f / (hi - lo), 3.0e38f);  // finite, so (lo - lo) * scale == 0
+  auto lbin = [](float x, float o, float sc) { return (int)fminf(255.f, (x - o) * sc); };
+  for (int i = threadIdx.x; i < 256; i += kSmpThreads) s.hist[i] = 0;
+  __syncthreads();
+  {
+    const float mo = opaque(m);
+#pragma unroll
+    for (int e = 0; e < kSmpE; ++e)
+      if (l[e] > -kInf) atomicAdd(&s.hist[lbin(l[e], lo, scale)], wt(l[e], mo));
+  }
+  __syncthreads();
+  find_cross(s, 0, W);
+  const int b0 = s.cross_bin;
+  if (b0 < 0) return lo;
+  u64 above = s.cross_above;
+  float nlo = kInf, nhi = -kInf;
+  {
+    const float lo2 = opaque(lo), sc2 = opaque(scale);
+#pragma unroll
+    for (int e = 0; e < kSmpE; ++e)
+      if (l[e] > -kInf && lbin(l[e], lo2, sc2) == b0) nlo = fminf(nlo, l[e]), nhi = fmaxf(nhi, l[e]);
+  }
+  block_minmax(nlo, nhi, s);  // its barriers also order the cross_bin reads before the next write
+  // radix passes over the keys in [kl, kh]: the elements of bin b0
+  uint32_t kl = okey(nlo), kh = okey(nhi);
+  while (kl != kh) {
+    const int top = 31 - __clz(kl ^ kh);  // highest differing bit
+    const int sh = max(0, top - 7);
+    const uint32_t dmask = (1u << (top - sh + 1)) - 1u;
+    for (int i = threadIdx.x; i < 256; i += kSmpThreads) s.hist[i] = 0;
+    __syncthreads();
+    const float zero = opaque(0.f), mo = opaque(m);
+#pragma unroll
+    for (int e = 0; e < kSmpE; ++e) {
+      const uint32_t k = okey(l[e] + zero);  // + 0 keeps the value (no -0 is left)
+      if (l[e] > -kInf && k >= kl && k <= kh) atomicAdd(&s.hist[(k >> sh) & dmask], wt(l[e], mo));
+    }
+    __syncthreads();
+    find_cross(s, above, W);
+    const int b = s.cross_bin;
+    above = s.cross_above;
+    __syncthreads();
+    if (b < 0) break;  // unreachable: above <= W < above + weight([kl, kh]) holds here
+    const uint32_t keep_hi = top == 31 ? 0u : (0xffffffffu << (top + 1));
+    const uint32_t nl = (kl & keep_hi) | ((uint32_t)b << sh);
+    const uint32_t nh = nl | ((1u << sh) - 1u);
+    kl = max(kl, nl);
+    kh = min(kh, nh);
+  }
+  return okey_inv(kl);
+}
+
+RWKV7_DEV void philox4x32_10(uint32_t c[4], uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const u64 p0 = (u64)0xD2511F53u * c[0], p1 = (u64)0xCD9E8D57u * c[2];
+    const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c[1] ^ k0, n2 = (uint32_t)(p0 >> 32) ^ c[3] ^ k1;
+    c[0] = n0, c[1] = (uint32_t)p1, c[2] = n2, c[3] = (uint32_t)p0;
+    k0 += 0x9E3779B9u, k1 += 0xBB67AE85u;
+  }
+}
+
+// Logits 8..8c+7 of this thread's 64, as f32 (-inf past V). VEC: rows
+// 16-byte aligned and V % 8 == 0, so each 8-logit chunk is whole 16-byte
+// loads or wholly past V.
+template <bool VEC, bool F32>
+RWKV7_DEV void load8(const void *row_ptr, int i0, int V, float *f) {
+  if (VEC) {
+    if (F32) {
+      const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(row_ptr) + i0);
+      const float4 u = i0 < V ? p[0] : make_float4(-kInf, -kInf, -kInf, -kInf);
+      const float4 v = i0 < V ? p[1] : make_float4(-kInf, -kInf, -kInf, -kInf);
+      f[0] = u.x, f[1] = u.y, f[2] = u.z, f[3] = u.w, f[4] = v.x, f[5] = v.y, f[6] = v.z, f[7] = v.w;
+    } else {
+      const uint32_t ninf2 = 0xfc00fc00u;  // two f16 -inf
+      const uint4 u = i0 < V ? *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(row_ptr) + i0)
+                             : make_uint4(ninf2, ninf2, ninf2, ninf2);
+      h8_to_f(u, f);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = i0 + j;
+      f[j] = i >= V ? -kInf : F32 ? static_cast<const float *>(row_ptr)[i] : h2f(static_cast<const uint16_t *>(row_ptr)[i]);
+    }
+  }
+}
+
+template <bool VEC, bool F32>
+__global__ __launch_bounds__(kSmpThreads) void sample_kernel(SampleArgs a) {
+  __shared__ SampleLds s;
+  const int row = blockIdx.x, base = threadIdx.x * kSmpE, V = a.V;
+  const void *src = static_cast<const char *>(a.logits) + (int64_t)row * a.ld * (F32 ? 4 : 2);
+  float l[kSmpE];
+#pragma unroll
+  for (int c = 0; c < kSmpE / 8; ++c) load8<VEC, F32>(src, base + 8 * c, V, &l[8 * c]);
+  // repetition penalty (sampling.py:44-47), applied once per seen token
+  if (a.seen && a.pen != 1.f) {
+    const uint32_t *sr = a.seen + (int64_t)row * a.seen_ld;
+    const int nw = (V + 31) / 32;
+    const uint32_t m0 = 2 * threadIdx.x < nw ? sr[2 * threadIdx.x] : 0u;
+    const uint32_t m1 = 2 * threadIdx.x + 1 < nw ? sr[2 * threadIdx.x + 1] : 0u;
+#pragma unroll
+    for (int e = 0; e < kSmpE; ++e) {
+      if (((e < 32 ? m0 : m1) >> (e & 31)) & 1u) l[e] = l[e] > 0.f ? l[e] / a.pen : l[e] * a.pen;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < kSmpE; ++e) l[e] = l[e] + 0.f;  // -0 -> +0: one key per value
+
+  int token;
+  if (!(a.temp > 0.f)) {
+    // greedy: argmax, first index among ties (sampling.py:49-50)
+    float v = -kInf;
+    int vi = 0x7fffffff;
+#pragma unroll
+    for (int e = 0; e < kSmpE; ++e)
+      if (better(l[e], base + e, v, vi)) v = l[e], vi = base + e;
+    block_argmax(v, vi, s);
+    token = vi < V ? vi : 0;  // only a row of NaNs leaves vi past V
+    if (a.probs) {
+      float *pr = a.probs + (int64_t)row * a.probs_ld;
+#pragma unroll
+      for (int e = 0; e < kSmpE; ++e)
+        if (base + e < V) pr[base + e] = base + e == token ? 1.f : 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < kSmpE; ++e) l[e] = l[e] / a.temp;
+    float lo = kInf, m = -kInf;
+#pragma unroll
+    for (int e = 0; e < kSmpE; ++e)
+      if (l[e] > -kInf) lo = fminf(lo, l[e]), m = fmaxf(m, l[e]);
+    block_minmax(lo, m, s);
+    if (a.top_k > 0 && a.top_k < V) {  // sampling.py:56-60
+      const float tk = select_gt<false>(l, m, (u64)(a.top_k - 1), s);
+#pragma unroll
+      for (int e = 0; e < kSmpE; ++e)
+        if (l[e] < tk) l[e] = -kInf;
+    }
+    if (a.top_p < 1.f) {  // sampling.py:62-68
+      u64 own = 0, z = 0;
+      const float mo = opaque(m);
+#pragma unroll
+      for (int e = 0; e < kSmpE; ++e)
+        if (l[e] > -kInf) own += mass(l[e], mo);
+      block_excl_scan(own, z, s);
+      const float tp = select_gt<true>(l, m, (u64)((double)a.top_p * (double)z), s);
+#pragma unroll
+      for (int e = 0; e < kSmpE; ++e)
+        if (l[e] < tp) l[e] = -kInf;
+    }
+    u64 own = 0, z = 0;
+    const float m1 = opaque(m);
+#pragma unroll
+    for (int e = 0; e < kSmpE; ++e)
+      if (l[e] > -kInf) own += mass(l[e], m1);
+    const u64 excl = block_excl_scan(own, z, s);
+    uint32_t c[4] = {a.off_lo, a.off_hi, (uint32_t)row, 0u};
+    philox4x32_10(c, a.seed_lo, a.seed_hi);
+    const u64 target = __umul64hi(z, (u64)c[0] | ((u64)c[1] << 32));  // in [0, z)
+    token = -1;  // exactly one thread finds it: z >= 2^40, since the maximum is always kept
+    if (excl <= target && target < excl + own) {
+      u64 acc = excl;
+      const float m2 = opaque(m);
+#pragma unroll
+      for (int e = 0; e < kSmpE; ++e) {
+        if (l[e] > -kInf) acc += mass(l[e], m2);
+        if (token < 0 && acc > target) token = base + e;
+      }
+    }
+    if (a.probs) {
+      float *pr = a.probs + (int64_t)row * a.probs_ld;
+      const float inv = 1.f / (float)z, m3 = opaque(m);
+#pragma unroll
+      for (int e = 0; e < kSmpE; ++e)
+        if (base + e < V) pr[base + e] = l[e] > -kInf ? (float)mass(l[e], m3) * inv : 0.f;
+    }
+  }
+  if (token >= 0 && (a.temp > 0.f || threadIdx.x == 0)) {
+    a.out[row] = token;
+    if (a.update_seen) atomicOr(a.seen + (int64_t)row * a.seen_ld + token / 32, 1u << (token % 32));
+  }
+}
+
+}  // namespace
+}  // namespace rwkv7
+
+extern "C" int rwkv7_sample(const void *logits, int32_t logits_is_f32, int64_t ld, int32_t B, int32_t V, const rwkv7_sampling *p,
+                            uint32_t *seen, int64_t seen_ld, int32_t update_seen, int64_t *out, float *probs,
+                            int64_t probs_ld, void *stream) {
+  using namespace rwkv7;
+  if (!logits || !p || !out || B < 1 || (update_seen && !seen)) return RWKV7_EINVAL;
+  if (V < 1 || V > kSmpMaxV || ld < V || (seen && seen_ld < (V + 31) / 32) || (probs && probs_ld < V))
+    return RWKV7_ESHAPE;
+  SampleArgs a;
+  a.logits = logits;
+  a.ld = ld;
+  a.V = V;
+  a.temp = p->temperature;
+  a.top_p = p->top_p;
+  a.pen = p->repetition_penalty;
+  a.top_k = p->top_k;
+  a.seed_lo = (uint32_t)p->seed, a.seed_hi = (uint32_t)(p->seed >> 32);
+  a.off_lo = (uint32_t)p->offset, a.off_hi = (uint32_t)(p->offset >> 32);
+  a.seen = seen;
+  a.seen_ld = seen_ld;
+  a.update_seen = update_seen;
+  a.out = out;
+  a.probs = probs;
+  a.probs_ld = probs_ld;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool vec = reinterpret_cast<uintptr_t>(logits) % 16 == 0 && ld % 8 == 0 && V % 8 == 0;
+  if (logits_is_f32)
+    vec ? sample_kernel<true, true><<<B, kSmpThreads, 0, st>>>(a) : sample_kernel<false, true><<<B, kSmpThreads, 0, st>>>(a);
+  else
+    vec ? sample_kernel<true, false><<<B, kSmpThreads, 0, st>>>(a) : sample_kernel<false, false><<<B, kSmpThreads, 0, st>>>(a);
+  RWKV7_CHECK_LAUNCH();
+  return RWKV7_OK;
+}

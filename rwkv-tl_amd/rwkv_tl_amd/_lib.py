@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the HIP library)
 
 LIB_NAME = "librwkv7_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # enum indices of the per-layer fp32 vector block (RWKV7_V_*)
 VEC_NAMES = (
@@ -47,6 +47,7 @@ SYMBOLS = (
     "rwkv7_rank_gemv",
     "rwkv7_l2norm_neg_kk_a",
     "rwkv7_gn_rkrk",
+    "rwkv7_sample",
 )
 
 
@@ -107,6 +108,19 @@ class GatesIO(ctypes.Structure):
     ]
 
 
+class Sampling(ctypes.Structure):
+    """``rwkv7_sampling``: parameters of one ``rwkv7_sample`` call."""
+
+    _fields_ = [
+        ("temperature", ctypes.c_float),
+        ("top_k", ctypes.c_int32),
+        ("top_p", ctypes.c_float),
+        ("repetition_penalty", ctypes.c_float),
+        ("seed", ctypes.c_uint64),
+        ("offset", ctypes.c_uint64),
+    ]
+
+
 class HipError(RuntimeError):
     """A nonzero return code from the HIP library."""
 
@@ -143,6 +157,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "rwkv7_rank_gemv": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]),
         "rwkv7_l2norm_neg_kk_a": (ctypes.c_int, [vp, vp, vp, vp, i32, vp]),
         "rwkv7_gn_rkrk": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, i32, vp]),
+        "rwkv7_sample": (ctypes.c_int, [vp, i32, i64, i32, i32, ctypes.POINTER(Sampling), vp, i64, i32, vp, vp, i64, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

@@ -12,7 +12,7 @@ from abc import ABC, abstractmethod
 import torch
 from torch import Tensor
 
-from .sampling import sample_logits
+from .sampling import Sampler
 from .state import State
 from .weight import RWKV7Weight
 
@@ -50,25 +50,27 @@ class RWKV7Model(ABC):
         top_p: float = 1.0,
         repetition_penalty: float = 1.0,
     ) -> tuple[list[int], State]:
-        """Prompt with ``tokens`` and sample ``max_tokens`` more (``_rwkv7_abc.py:41-72``)."""
+        """Prompt with ``tokens`` and sample ``max_tokens`` more (``_rwkv7_abc.py:41-72``).
+
+        Each step is decode plus one sampling launch that writes the token into
+        a device buffer the next decode reads: no host sync until the final
+        ``tolist()``. Repetition penalty applies to the generated tokens only,
+        as in the reference (``seen=out``)."""
         if isinstance(tokens, Tensor) and tokens.ndim != 1:
             raise ValueError(f"Expected 1D token sequence, got {tokens.shape}")
         if isinstance(tokens, list):
             tokens = torch.as_tensor(tokens, device=self.w.device)
-        out = torch.tensor([], dtype=torch.long, device=self.w.device)
         S = self.prefill(tokens[:-1], S)  # raises on a one-token prompt, as the reference does
+        out = torch.empty(max_tokens, dtype=torch.long, device=self.w.device)
+        sampler = Sampler(
+            self.w.head.shape[0], self.w.device, temperature=temperature, top_k=top_k, top_p=top_p,
+            repetition_penalty=repetition_penalty,
+        )
         token = tokens[-1]
-        for _ in range(max_tokens):
+        for i in range(max_tokens):
             logits, S = self.decode(token, S)
-            token = sample_logits(
-                logits,
-                temperature=temperature,
-                top_k=top_k,
-                top_p=top_p,
-                repetition_penalty=repetition_penalty,
-                seen=out,
-            )
-            out = torch.cat([out, token.reshape(1).to(out.device)])
+            sampler(logits, out[i : i + 1])
+            token = out[i]
         return out.tolist(), S
 
     def forward(self, tokens: Tensor, S: State) -> tuple[Tensor, State]:

@@ -11,6 +11,7 @@ import pytest
 import torch
 
 from oracle import rwkv7_ref as R
+from oracle import sampling_ref as S
 from rwkv_tl_amd import _lib, make_rwkv7, sample_logits
 from rwkv_tl_amd.checkpoint import SHAPES, make_random_state_dict
 from rwkv_tl_amd.state import State
@@ -186,46 +187,79 @@ def test_weight_loads_bf16_checkpoint_as_fp16(tmp_path):
         assert torch.equal(a.att.rkvWt[1], b.att.rkvWt[1]) and torch.equal(a.ffn.vWt, b.ffn.vWt)
 
 
-# Known answers of the reference's test/test_sampling.py:11-59.
-def test_sampling_greedy_argmax():
+# Oracle sampling pinned by the known answers of the reference's
+# test/test_sampling.py:11-59 and by the filters' definitions.
+def test_sampling_ref_greedy_argmax():
     logits = torch.tensor([1.0, 2.0, 0.5, 3.0])
-    assert sample_logits(logits).item() == 3
-    assert sample_logits(logits, temperature=0.0).item() == 3
-    assert sample_logits(logits, temperature=-1.0).item() == 3
+    assert S.sample_logits_ref(logits).item() == 3
+    assert S.sample_logits_ref(logits, temperature=0.0).item() == 3
+    assert S.sample_logits_ref(logits, temperature=-1.0).item() == 3
 
 
-def test_sampling_top_k_one_is_greedy():
+def test_sampling_ref_top_k_one_is_greedy():
     torch.manual_seed(0)
     logits = torch.randn(100)
     for _ in range(20):
-        assert sample_logits(logits, temperature=1.0, top_k=1).item() == int(logits.argmax())
+        assert S.sample_logits_ref(logits, temperature=1.0, top_k=1).item() == int(logits.argmax())
 
 
-def test_sampling_repetition_penalty_flips_near_tie():
+def test_sampling_ref_repetition_penalty_flips_near_tie():
     logits = torch.tensor([0.5, 0.4])
-    assert sample_logits(logits, temperature=1.0, top_k=1).item() == 0
-    got = sample_logits(logits, temperature=1.0, top_k=1, repetition_penalty=2.0, seen=torch.tensor([0]))
+    assert S.sample_logits_ref(logits, temperature=1.0, top_k=1).item() == 0
+    got = S.sample_logits_ref(logits, temperature=1.0, top_k=1, repetition_penalty=2.0, seen=torch.tensor([0]))
     assert got.item() == 1
 
 
-def test_sampling_range_and_shape():
+def test_sampling_ref_range_and_shape():
     torch.manual_seed(0)
     logits = torch.randn(100)
     for _ in range(20):
-        assert 0 <= sample_logits(logits, temperature=1.0, top_k=50, top_p=0.9).item() < 100
+        assert 0 <= S.sample_logits_ref(logits, temperature=1.0, top_k=50, top_p=0.9).item() < 100
     for temperature in (None, 0.0, 1.0):
-        t = sample_logits(torch.randn(65536), temperature=temperature)
+        t = S.sample_logits_ref(torch.randn(65536), temperature=temperature)
         assert t.numel() == 1 and 0 <= int(t) < 65536
-    batch = sample_logits(torch.randn(3, 10), temperature=1.0, top_p=0.5)
-    assert batch.shape == (3,)
+    assert S.sample_logits_ref(torch.randn(3, 10), temperature=1.0, top_p=0.5).shape == (3,)
 
 
-def test_sampling_top_p_keeps_smallest_nucleus():
+def test_sampling_ref_top_p_keeps_smallest_nucleus():
     # probabilities 0.5, 0.3, 0.2: top_p 0.6 keeps the first two only
     logits = torch.log(torch.tensor([0.5, 0.3, 0.2]))
     torch.manual_seed(0)
-    draws = {int(sample_logits(logits, temperature=1.0, top_p=0.6)) for _ in range(200)}
+    draws = {int(S.sample_logits_ref(logits, temperature=1.0, top_p=0.6)) for _ in range(200)}
     assert draws == {0, 1}
+
+
+@pytest.mark.parametrize("top_k,top_p", [(5, 1.0), (0, 0.5), (0, 0.9), (7, 0.8), (1, 0.3), (40, 0.05)])
+def test_sampling_ref_filters_match_definitions(top_k, top_p):
+    g = torch.Generator().manual_seed(top_k * 100 + int(top_p * 10))
+    for temperature in (0.7, 1.3):
+        logits = torch.randn(40, generator=g) * 2
+        l = S.filtered_logits_ref(logits, temperature=temperature, top_k=top_k, top_p=top_p)
+        got = [bool(v) for v in torch.isfinite(l)]
+        want = S.kept_mask_brute((logits.float() / temperature).tolist(), top_k, top_p)
+        assert got == want
+
+
+def test_philox_known_answers():
+    """Random123 known-answer vectors of philox4x32 with 10 rounds."""
+    assert S.philox4x32_10((0, 0, 0, 0), (0, 0)) == (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)
+    f = 0xFFFFFFFF
+    assert S.philox4x32_10((f, f, f, f), (f, f)) == (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)
+    assert S.philox4x32_10((0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344), (0xA4093822, 0x299F31D0)) == (
+        0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1,
+    )
+
+
+def test_draw_ref_is_inverse_cdf():
+    probs = __import__("numpy").array([0.1, 0.0, 0.6, 0.3])
+    for off in range(50):
+        tok, t, cdf = S.draw_ref(probs, seed=12345, offset=off)
+        assert probs[tok] > 0 and (tok == 0 or cdf[tok - 1] <= t) and t < cdf[tok]
+
+
+def test_sample_logits_rejects_cpu_tensors():
+    with pytest.raises(ValueError):
+        sample_logits(torch.randn(10))
 
 
 def test_make_rwkv7_backends():
