@@ -88,7 +88,7 @@ RWKV7_DEV float opaque(float x) {
   return x;
 }
 
-RWKV7_DEV u64 mass(float x, float m) { return (u64)(expf(x - m) * kFix); }
+RWKV7_DEV u64 mass(float x, float m) { return (u64)(__expf(x - m) * kFix); }
 
 RWKV7_DEV bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
 

@@ -8,13 +8,16 @@ Drop-in for the GPU path of yuyi2439/rwkv-tl:
 * ``HIPGraph`` / ``make_graph_cls`` -- ``demo.cuda_graph.CUDAGraph`` / ``make_graph_cls``
 * ``make_rwkv7`` -- ``demo.make_rwkv7``
 * ``kernels`` -- the operator-level API of ``rwkv_tl.kernels.fp16``
-* ``sample_logits`` -- ``demo.sampling.sample_logits``
+* ``sample_logits`` -- ``demo.sampling.sample_logits`` (one HIP kernel launch)
+* ``operators`` -- ``torch.ops.rwkv_tl.*`` (``rwkv_tl.operators``), registered on import
+* ``tokenizer.Tokenizer`` -- ``rwkv_tl.tokenizer.Tokenizer``
 """
 
 from __future__ import annotations
 
 import torch
 
+from . import operators  # noqa: F401  (registers torch.ops.rwkv_tl.*, as src/rwkv_tl/__init__.py:10 does)
 from .checkpoint import SHAPES, ModelShape, make_random_state_dict
 from .hip_graph import HIPGraph, make_graph_cls, wrap_model
 from .model import RWKV7Model

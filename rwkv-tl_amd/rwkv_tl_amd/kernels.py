@@ -9,7 +9,7 @@ dtype). There is no CPU branch: the reference's in-function torch fallbacks
 * ``fused_dplr(S, R, W, K, V, A, B)`` / ``fused_dplr_T(...)``: the wkv7 DPLR
   step / sequence (``dplr.py:256-285``); ``wkv7`` is the batched form.
 * ``fused_lerp6`` / ``fused_lerp6_copy`` / ``fused_lerp1_copy``
-  (``lerp.py:140-198``).
+  (``lerp.py:140-198``), ``fused_lerp6_rkv_copy`` (``lerp.py:200-219``).
 * ``layer_norm`` (``weight.py:14-15``), ``gemv`` and ``gemm`` (the projection
   GEMMs of ``gemm.py:215-305``), ``fused_rkv_gemm`` (``gemm.py:215-262``).
 * The time-mix stage operators, f16 in and out: ``fused_w_gate``,
@@ -180,6 +180,15 @@ def fused_rkv_gemm(xr: Tensor, xk: Tensor, xv: Tensor, Wb: Tensor) -> Tensor:
     orientation (``gemm.py:215-262``); returns f16 [3, T, C]."""
     outs = [gemm(x.contiguous(), Wb[i].T.contiguous(), "f16") for i, x in enumerate((xr, xk, xv))]
     return torch.stack(outs)
+
+
+def fused_lerp6_rkv_copy(x, prev, x_r, x_w, x_k, x_v, x_a, x_g, x_copy, rWt_stack):
+    """``fused_lerp6_copy`` then the r/k/v projections of ``xr, xk, xv`` by
+    ``rWt_stack`` [3, C, C] (``[in, out]``); returns ``(r, k, v, xv, xw, xa, xg)``
+    (``lerp.py:200-219``)."""
+    xr, xw, xk, xv, xa, xg = fused_lerp6_copy(x, prev, x_r, x_w, x_k, x_v, x_a, x_g, x_copy)
+    rkv = fused_rkv_gemm(xr.unsqueeze(0), xk.unsqueeze(0), xv.unsqueeze(0), rWt_stack)
+    return rkv[0, 0], rkv[1, 0], rkv[2, 0], xv, xw, xa, xg
 
 
 # ---------------------------------------------------------------------------
