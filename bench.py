@@ -24,6 +24,14 @@
   model (a port of the reference's ``demo/rwkv7_torch.py``) timed on this
   host's cores on a bounded sample of the same decode workload.
 
+``python bench.py --generate`` prints a different single JSON line instead:
+``generate`` of 128 tokens after a 16-token prompt on the same model and
+weights, greedy and with temperature 1 / top-k 50 / top-p 0.9, each step one
+decode replay plus one launch of the sampling kernel (``rwkv7_sample``), and
+the same loop with the reference's sampling composition in torch operators
+(``demo/sampling.py:13-70``) for comparison; plus the sampling kernel's
+average launch time (HIP events) at B=1 and B=16.
+
 Profiling recipe (the counter runs behind ``traffic``)::
 
     rocprofv3 --pmc FETCH_SIZE --kernel-trace -f csv -d OUT/fetch -o run -- \
@@ -196,6 +204,83 @@ def cpu_baseline(shape_name: str, steps: int, warmup: int) -> dict:
     }
 
 
+def _torch_ops_sample(l, temperature, top_k, top_p):
+    """The reference's sampling composition (demo/sampling.py:52-70) in torch
+    operators on the device: the per-token cost the sampling kernel replaces."""
+    import torch
+
+    l = l.float() / temperature
+    cutoff = torch.topk(l, top_k, dim=-1).values[..., -1:]
+    l = torch.where(l >= cutoff, l, torch.full_like(l, float("-inf")))
+    probs = torch.softmax(l, dim=-1)
+    sp, si = torch.sort(probs, descending=True, dim=-1)
+    drop = torch.cumsum(sp, dim=-1) - sp > top_p
+    kept = torch.gather(l, -1, si)
+    l = l.scatter(-1, si, torch.where(drop, torch.full_like(kept, float("-inf")), kept))
+    return torch.multinomial(torch.softmax(l, dim=-1), 1).squeeze(-1)
+
+
+def bench_generate() -> dict:
+    import torch
+
+    from rwkv_tl_amd import make_rwkv7
+    from rwkv_tl_amd.checkpoint import make_random_state_dict
+    from rwkv_tl_amd.sampling import Sampler
+    from rwkv_tl_amd.weight import RWKV7Weight
+
+    dev = torch.device("cuda:0")
+    sd = make_random_state_dict("0.4b", seed=0, dtype=torch.float16)
+    w = RWKV7Weight.from_state_dict(sd, device=dev, dtype=torch.float16)
+    del sd
+    model = make_rwkv7(dev)(w, is_torch_compile=False)
+    V, n_new = w.head.shape[0], 128
+    prompt = torch.randint(0, V, (16,), generator=torch.Generator().manual_seed(1)).tolist()
+    cfgs = {"greedy": dict(), "t1_topk50_topp0.9": dict(temperature=1.0, top_k=50, top_p=0.9)}
+    out: dict = {"mode": "generate", "workload": "RWKV7-0.4B generate 128 tokens after a 16-token prompt, B=1",
+                 "data": "synthetic: seeded random-init weights and prompt", "unit": "ms/token"}
+    for name, kw in cfgs.items():
+        model.generate(prompt, model.new_state(), 8, **kw)  # warm-up (graph capture)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        model.generate(prompt, model.new_state(), n_new, **kw)
+        out[name] = {"ms_per_token": round((time.perf_counter() - t0) * 1000.0 / n_new, 4)}
+        log(f"generate {name}: {out[name]['ms_per_token']} ms/token")
+    # the same loop with the torch-operator sampler (first pass: warm-up)
+    kw = cfgs["t1_topk50_topp0.9"]
+    for n in (8, n_new):
+        S = model.new_state()
+        S = model.prefill(torch.tensor(prompt[:-1], device=dev), S)
+        tok = torch.tensor(prompt[-1], device=dev)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        toks = []
+        for _ in range(n):
+            logits, S = model.decode(tok, S)
+            tok = _torch_ops_sample(logits, **kw)
+            toks.append(tok)
+        torch.stack(toks).tolist()
+    out["t1_topk50_topp0.9_torch_ops"] = {"ms_per_token": round((time.perf_counter() - t0) * 1000.0 / n_new, 4)}
+    # the sampling kernel alone, per launch
+    for B in (1, 16):
+        logits = (torch.randn(B, V, generator=torch.Generator().manual_seed(B)) * 2).half().to(dev)
+        res = torch.empty(B, dtype=torch.int64, device=dev)
+        for name, kw in cfgs.items():
+            smp = Sampler(V, dev, batch=B, **kw)
+            for _ in range(10):
+                smp(logits, res)
+            stream = torch.cuda.current_stream()
+            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(100)]
+            for a, b in evs:
+                a.record(stream)
+                smp(logits, res)
+                b.record(stream)
+            torch.cuda.synchronize()
+            us = 1000.0 * sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+            out[name][f"sample_kernel_us_B{B}"] = round(us, 2)
+            log(f"sample kernel {name} B={B}: {us:.2f} us")
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -205,6 +290,8 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the headline decode line")
     ap.add_argument("--calib-copy", action="store_true", help="also run a 1 GiB copy kernel (counter calibration)")
+    ap.add_argument("--generate", action="store_true",
+                    help="time generate() with the on-device sampler instead (one different JSON line)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two rocprofv3 --pmc csv runs and exit (no GPU)")
     args = ap.parse_args()
@@ -218,6 +305,9 @@ def main() -> None:
             file=sys.stderr,
         )
         sys.exit(2)
+    if args.generate:
+        print(json.dumps(bench_generate()), flush=True)
+        return
 
     import torch
 
