@@ -35,6 +35,7 @@ constexpr int kSmpE = 64;                      // logits per thread
 constexpr int kSmpMaxV = kSmpThreads * kSmpE;  // 65536
 constexpr float kFix = 1099511627776.0f;       // 2^40
 constexpr float kInf = __builtin_inff();
+constexpr int kCandCap = 4096;                 // LDS candidates of a threshold's bin
 
 struct SampleArgs {
   const void *logits;
@@ -58,6 +59,8 @@ struct SampleLds {
   int wi[kSmpWaves];
   u64 cross_above;
   int cross_bin;
+  int ncand;
+  float cand[kCandCap];
 };
 
 RWKV7_DEV uint32_t okey(float f) {
@@ -180,21 +183,23 @@ RWKV7_DEV void find_cross(SampleLds &s, u64 above, u64 W) {
 }
 
 // Largest kept value y (kept: x > -inf) with sum over kept x >= y of wt(x)
-// > W, where wt(x) = 1 (MASS false) or floor(exp(x - m) 2^40). If the total
-// is <= W, the smallest kept value (so every kept element stays kept).
+// > W, where wt(x) = 1 (MASS false) or mass(x, m); [lo, hi] is the range of
+// the kept values. If the total is <= W, lo (every kept element stays kept).
+//
+// One pass of 256 equal-width bins over [lo, hi] picks the bin that holds y;
+// its elements are copied to LDS (when there are at most kCandCap of them),
+// and radix passes of up to 8 bits over their order-preserving keys narrow the
+// key range to one value. A larger bin is narrowed the same way straight from
+// the registers.
 template <bool MASS>
-RWKV7_DEV float select_gt(const float (&l)[kSmpE], float m, u64 W, SampleLds &s) {
+RWKV7_DEV float select_gt(const float (&l)[kSmpE], float lo, float hi, float m, u64 W, SampleLds &s) {
   auto wt = [](float x, float mm) -> u64 { return MASS ? mass(x, mm) : 1ull; };
-  float lo = kInf, hi = -kInf;
-#pragma unroll
-  for (int e = 0; e < kSmpE; ++e)
-    if (l[e] > -kInf) lo = fminf(lo, l[e]), hi = fmaxf(hi, l[e]);
-  block_minmax(lo, hi, s);
   if (!(lo < hi)) return lo;
   // pass 0: equal-width bins over [lo, hi]
   const float scale = fminf(256.f / (hi - lo), 3.0e38f);  // finite, so (lo - lo) * scale == 0
   auto lbin = [](float x, float o, float sc) { return (int)fminf(255.f, (x - o) * sc); };
   for (int i = threadIdx.x; i < 256; i += kSmpThreads) s.hist[i] = 0;
+  if (threadIdx.x == 0) s.ncand = 0;
   __syncthreads();
   {
     const float mo = opaque(m);
@@ -207,14 +212,22 @@ RWKV7_DEV float select_gt(const float (&l)[kSmpE], float m, u64 W, SampleLds &s)
   const int b0 = s.cross_bin;
   if (b0 < 0) return lo;
   u64 above = s.cross_above;
+  // the elements of bin b0: their range, and a copy in LDS
   float nlo = kInf, nhi = -kInf;
   {
     const float lo2 = opaque(lo), sc2 = opaque(scale);
 #pragma unroll
-    for (int e = 0; e < kSmpE; ++e)
-      if (l[e] > -kInf && lbin(l[e], lo2, sc2) == b0) nlo = fminf(nlo, l[e]), nhi = fmaxf(nhi, l[e]);
+    for (int e = 0; e < kSmpE; ++e) {
+      if (l[e] > -kInf && lbin(l[e], lo2, sc2) == b0) {
+        nlo = fminf(nlo, l[e]), nhi = fmaxf(nhi, l[e]);
+        const int slot = atomicAdd(&s.ncand, 1);
+        if (slot < kCandCap) s.cand[slot] = l[e];
+      }
+    }
   }
-  block_minmax(nlo, nhi, s);  // its barriers also order the cross_bin reads before the next write
+  block_minmax(nlo, nhi, s);  // its barriers order the copy and the cross_bin reads before what follows
+  const int ncand = s.ncand;
+  const bool from_lds = ncand <= kCandCap;  // block-uniform
   // radix passes over the keys in [kl, kh]: the elements of bin b0
   uint32_t kl = okey(nlo), kh = okey(nhi);
   while (kl != kh) {
@@ -224,10 +237,18 @@ RWKV7_DEV float select_gt(const float (&l)[kSmpE], float m, u64 W, SampleLds &s)
     for (int i = threadIdx.x; i < 256; i += kSmpThreads) s.hist[i] = 0;
     __syncthreads();
     const float zero = opaque(0.f), mo = opaque(m);
+    if (from_lds) {
+      for (int i = threadIdx.x; i < ncand; i += kSmpThreads) {
+        const float x = s.cand[i];
+        const uint32_t k = okey(x);
+        if (k >= kl && k <= kh) atomicAdd(&s.hist[(k >> sh) & dmask], wt(x, mo));
+      }
+    } else {
 #pragma unroll
-    for (int e = 0; e < kSmpE; ++e) {
-      const uint32_t k = okey(l[e] + zero);  // + 0 keeps the value (no -0 is left)
-      if (l[e] > -kInf && k >= kl && k <= kh) atomicAdd(&s.hist[(k >> sh) & dmask], wt(l[e], mo));
+      for (int e = 0; e < kSmpE; ++e) {
+        const uint32_t k = okey(l[e] + zero);  // + 0 keeps the value (no -0 is left)
+        if (l[e] > -kInf && k >= kl && k <= kh) atomicAdd(&s.hist[(k >> sh) & dmask], wt(l[e], mo));
+      }
     }
     __syncthreads();
     find_cross(s, above, W);
@@ -326,29 +347,31 @@ __global__ __launch_bounds__(kSmpThreads) void sample_kernel(SampleArgs a) {
     for (int e = 0; e < kSmpE; ++e)
       if (l[e] > -kInf) lo = fminf(lo, l[e]), m = fmaxf(m, l[e]);
     block_minmax(lo, m, s);
+    float thr = -kInf;  // tokens with x >= thr stay
     if (a.top_k > 0 && a.top_k < V) {  // sampling.py:56-60
-      const float tk = select_gt<false>(l, m, (u64)(a.top_k - 1), s);
-#pragma unroll
-      for (int e = 0; e < kSmpE; ++e)
-        if (l[e] < tk) l[e] = -kInf;
+      thr = select_gt<false>(l, lo, m, m, (u64)(a.top_k - 1), s);
+      lo = thr;  // the smallest value top-k keeps
     }
     if (a.top_p < 1.f) {  // sampling.py:62-68
       u64 own = 0, z = 0;
       const float mo = opaque(m);
 #pragma unroll
-      for (int e = 0; e < kSmpE; ++e)
+      for (int e = 0; e < kSmpE; ++e) {
+        if (l[e] < thr) l[e] = -kInf;
         if (l[e] > -kInf) own += mass(l[e], mo);
+      }
       block_excl_scan(own, z, s);
-      const float tp = select_gt<true>(l, m, (u64)((double)a.top_p * (double)z), s);
-#pragma unroll
-      for (int e = 0; e < kSmpE; ++e)
-        if (l[e] < tp) l[e] = -kInf;
+      thr = select_gt<true>(l, lo, m, m, (u64)((double)a.top_p * (double)z), s);
     }
     u64 own = 0, z = 0;
-    const float m1 = opaque(m);
+    {
+      const float m1 = opaque(m);
 #pragma unroll
-    for (int e = 0; e < kSmpE; ++e)
-      if (l[e] > -kInf) own += mass(l[e], m1);
+      for (int e = 0; e < kSmpE; ++e) {
+        if (l[e] < thr) l[e] = -kInf;
+        if (l[e] > -kInf) own += mass(l[e], m1);
+      }
+    }
     const u64 excl = block_excl_scan(own, z, s);
     uint32_t c[4] = {a.off_lo, a.off_hi, (uint32_t)row, 0u};
     philox4x32_10(c, a.seed_lo, a.seed_hi);

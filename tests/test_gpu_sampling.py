@@ -179,6 +179,39 @@ def test_filters_with_ties_keep_whole_tie_groups():
             assert np.all(ok), diff[~ok][:8]
 
 
+def test_threshold_bin_larger_than_the_lds_copy():
+    """Two far outliers stretch the first pass's 256 equal-width bins so that
+    one bin holds ~20k logits: more than the 4096 the kernel copies to LDS,
+    so the thresholds are narrowed from the registers instead. (The high
+    outlier stays within exp(-20) of the cluster, so no kept token's weight
+    rounds to zero and "kept" can be read off the probabilities.)"""
+    g = torch.Generator().manual_seed(11)
+    x = torch.rand(65536, generator=g) * 0.5
+    x[100], x[200] = 20.0, -60.0
+    logits = x.half()
+    xf = logits.float().numpy()
+    for kw in (dict(temperature=1.0, top_k=1000), dict(temperature=1.0, top_p=0.5),
+               dict(temperature=1.0, top_k=20000, top_p=0.9)):
+        # without the high outlier (which would take all the mass) for top-p
+        lg = logits.clone()
+        if "top_p" in kw:
+            lg[100] = 0.25
+        xv = lg.float().numpy()
+        ref_l = S.filtered_logits_ref(lg, **kw)
+        want = torch.isfinite(ref_l).numpy()
+        _, p = _run(lg, **kw)
+        kept = p[0] > 0
+        cut = xv[kept].min()
+        assert np.all(kept[xv > cut]) and not np.any(kept[xv < cut])
+        diff = np.nonzero(kept != want)[0]
+        if diff.size:
+            assert kw.get("top_p", 1.0) < 1.0
+            before = _before_mass(S.filtered_logits_ref(lg, **{**kw, "top_p": 1.0}))
+            ok = (xv[diff] == cut) | (np.abs(before[diff] - kw["top_p"]) < 1e-5)
+            assert np.all(ok), diff[~ok][:8]
+    assert xf[100] == 20.0
+
+
 def test_draw_distribution_chi_square():
     V, B = 24, 8192
     logits = torch.linspace(-2, 2, V)
