@@ -32,6 +32,15 @@ the same loop with the reference's sampling composition in torch operators
 (``demo/sampling.py:13-70``) for comparison; plus the sampling kernel's
 average launch time (HIP events) at B=1 and B=16.
 
+``python bench.py --configs`` prints one more JSON line with the survey's
+other measurement configurations, each timed with HIP events after warm-up:
+C2 (standalone wkv7 scan, B=8, H=16, T=128, fp32 w and state, f16 r/k/v/a/b),
+C4 (0.4B prefill at B x T in 1x8, 1x32, 1x64, 1x128, 1x512, 8x8, 16x16 from a
+zero state, then 64 decode steps of the same batch) and C5 (1.5B-shaped
+model, ranks 96/96/64/256: prefill 4 x 1024, then decode B=64 for 128
+steps), with the algorithmic bytes and FLOPs of each and the fractions of the
+HBM and MFMA peaks they reach.
+
 Profiling recipe (the counter runs behind ``traffic``)::
 
     rocprofv3 --pmc FETCH_SIZE --kernel-trace -f csv -d OUT/fetch -o run -- \
@@ -220,6 +229,99 @@ def _torch_ops_sample(l, temperature, top_k, top_p):
     return torch.multinomial(torch.softmax(l, dim=-1), 1).squeeze(-1)
 
 
+def _flops(shape, tokens: int, head: bool) -> float:
+    C, F, L, V = shape.n_embd, shape.n_ffn, shape.n_layer, shape.vocab
+    SR = shape.rank_w + shape.rank_a + shape.rank_v + shape.rank_g
+    return 2.0 * tokens * (L * (4 * C * C + 2 * C * F + 2 * C * SR) + (V * C if head else 0))
+
+
+def _fracs(alg_bytes: float, flops: float, ms: float) -> dict:
+    return {
+        "alg_bytes": alg_bytes,
+        "alg_flops": flops,
+        "hbm_frac": round(alg_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+    }
+
+
+def bench_configs() -> dict:
+    import torch
+
+    from rwkv_tl_amd import SHAPES, HIPGraph, RWKV7HIP, State
+    from rwkv_tl_amd import kernels as K
+    from rwkv_tl_amd.checkpoint import make_random_state_dict
+    from rwkv_tl_amd.weight import RWKV7Weight
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(1)
+    out: dict = {"mode": "configs", "data": "synthetic: seeded random-init weights and uniform random token ids",
+                 "unit": "ms"}
+
+    # C2: the wkv7 scan alone
+    B, T, H, N = 8, 128, 16, 64
+    r, k, v = (torch.randn(B, T, H, N, generator=g).half().to(dev) for _ in range(3))
+    w = torch.exp(-torch.exp(torch.randn(B, T, H, N, generator=g) * 0.5 - 0.5)).to(dev)
+    kh = torch.nn.functional.normalize(torch.randn(B, T, H, N, generator=g), dim=-1)
+    alpha = torch.sigmoid(torch.randn(B, T, H, N, generator=g))
+    a, b = (-kh).half().to(dev), (kh * alpha).half().to(dev)
+    S0 = (torch.randn(B, H, N, N, generator=g) * 0.1).to(dev)
+    S = S0.clone()
+    ms = time_cuda(lambda: K.wkv7(S, r, w, k, v, a, b), 20)
+    c2_bytes = B * T * H * N * (5 * 2 + 4 + 2) + 2 * 4 * B * H * N * N
+    out["C2_wkv7_B8_H16_T128"] = {"ms": round(ms, 4), **_fracs(c2_bytes, 9.0 * N * N * B * T * H, ms),
+                                  "note": "FLOPs are VALU work (9 N^2 per head per token), not MFMA"}
+    log(f"C2 wkv7: {ms:.4f} ms")
+
+    def model_for(name: str):
+        sd = make_random_state_dict(name, seed=0, dtype=torch.float16)
+        wt = RWKV7Weight.from_state_dict(sd, device=dev, dtype=torch.float16)
+        del sd
+        m = RWKV7HIP(wt, is_torch_compile=False)
+        return wt, m, HIPGraph(m)
+
+    def run_case(shape, wt, m, gm, Bq: int, Tq: int, n_dec: int, tag: str, dec_b: int | None = None) -> None:
+        """Prefill Bq x Tq from a zero state, then n_dec decode steps of dec_b
+        sequences (default Bq, continuing the prefilled state; otherwise from a
+        zero state of dec_b sequences)."""
+        V = shape.vocab
+        dec_b = dec_b or Bq
+        toks = torch.randint(0, V, (Bq, Tq), generator=g).to(dev)
+        dec = torch.randint(0, V, (n_dec + 4, dec_b), generator=g).to(dev)
+        Sq = State(wt.L, wt.C, 64, device=dev, batch=Bq)
+        for _ in range(2):
+            m.prefill(toks, Sq)
+        torch.cuda.synchronize()
+        Sq = State(wt.L, wt.C, 64, device=dev, batch=Bq)
+        ms_p = time_cuda(lambda: m.prefill(toks, Sq), 10 if Bq * Tq <= 512 else 3)
+        if dec_b != Bq:
+            Sq = State(wt.L, wt.C, 64, device=dev, batch=dec_b)
+        for i in range(4):
+            gm.decode(dec[i], Sq)
+        it = iter(range(4, n_dec + 4))
+        ms_d = time_cuda(lambda: gm.decode(dec[next(it)], Sq), n_dec)
+        out[tag] = {
+            "prefill_ms": round(ms_p, 4),
+            "prefill_tokens_per_s": round(Bq * Tq * 1000.0 / ms_p, 1),
+            "prefill": _fracs(algorithmic_bytes(shape, Bq, Tq, head=False), _flops(shape, Bq * Tq, False), ms_p),
+            "decode_batch": dec_b,
+            "decode_ms_per_step": round(ms_d, 4),
+            "decode_tokens_per_s": round(dec_b * 1000.0 / ms_d, 1),
+            "decode": _fracs(algorithmic_bytes(shape, dec_b, 1, head=True), _flops(shape, dec_b, True), ms_d),
+        }
+        log(f"{tag}: prefill {ms_p:.3f} ms, decode {ms_d:.4f} ms/step")
+
+    shape = SHAPES["0.4b"]
+    wt, m, gm = model_for("0.4b")
+    for Bq, Tq in ((1, 8), (1, 32), (1, 64), (1, 128), (1, 512), (8, 8), (16, 16)):
+        run_case(shape, wt, m, gm, Bq, Tq, 64, f"C4_0.4b_prefill_{Bq}x{Tq}_then_64_decode")
+    del wt, m, gm
+    torch.cuda.empty_cache()
+    shape = SHAPES["1.5b"]
+    wt, m, gm = model_for("1.5b")
+    run_case(shape, wt, m, gm, 4, 1024, 128, "C5_1.5b_prefill_4x1024_then_decode_B64", dec_b=64)
+    return out
+
+
 def bench_generate() -> dict:
     import torch
 
@@ -290,6 +392,8 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the headline decode line")
     ap.add_argument("--calib-copy", action="store_true", help="also run a 1 GiB copy kernel (counter calibration)")
+    ap.add_argument("--configs", action="store_true",
+                    help="time the survey's C2, C4 and C5 configurations instead (one different JSON line)")
     ap.add_argument("--generate", action="store_true",
                     help="time generate() with the on-device sampler instead (one different JSON line)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -307,6 +411,9 @@ def main() -> None:
         sys.exit(2)
     if args.generate:
         print(json.dumps(bench_generate()), flush=True)
+        return
+    if args.configs:
+        print(json.dumps(bench_configs()), flush=True)
         return
 
     import torch

@@ -539,13 +539,31 @@ static int launch_skinny(const GemmProb *probs, int nprob, int M, hipStream_t st
   g.part = part;
   g.ctr = ctr;
   const int MB = (M + 15) / 16;
+  // splits per problem, then halved (largest strips x splits first) until the
+  // partial tiles and arrival counters fit the workspace
+  int split[kMaxProb] = {};
+  for (int i = 0; i < nprob; ++i) split[i] = skinny_splits(M, probs[i].K, part != nullptr && ctr != nullptr);
+  for (;;) {
+    int64_t need_fl = 0;
+    int need_ctr = 0, worst = -1;
+    int64_t worst_units = 0;
+    for (int i = 0; i < nprob; ++i) {
+      const int strips = (probs[i].N + 15) / 16;
+      if (split[i] == 1) continue;
+      need_fl += (int64_t)strips * split[i] * MB * 256;
+      need_ctr += strips;
+      if ((int64_t)strips * split[i] > worst_units) worst_units = (int64_t)strips * split[i], worst = i;
+    }
+    if ((need_fl * 4 <= part_cap && need_ctr <= kGemmCounters) || worst < 0) break;
+    split[worst] /= 2;
+  }
   int wgs = 0, ctrs = 0;
   int64_t pfl = 0;
   for (int i = 0; i < kMaxProb; ++i) {
     g.wg_begin[i] = wgs;
     if (i < nprob) {
       const int strips = (probs[i].N + 15) / 16;
-      const int S = skinny_splits(M, probs[i].K, part != nullptr && ctr != nullptr);
+      const int S = split[i];
       g.p[i] = probs[i];
       g.splits[i] = S;
       g.part_off[i] = pfl;

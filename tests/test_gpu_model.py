@@ -171,6 +171,74 @@ def test_batched_decode_rows_match_single_sequences(B, cuda):
             assert r < 5e-3, f"layer {i} row {b}: {r:.2e}"
 
 
+@pytest.mark.slow
+def test_1p5b_shape_batched_prefill_and_decode_match_oracle(cuda):
+    """The 1.5B shape of config C5 (C=2048, H=32, F=8192, ranks 96/96/64/256,
+    the largest LoRA width the library takes): batch 2, prefill 3 tokens then
+    2 decode steps, and a batch-1 decode, against the fp32-math oracle."""
+    print("1.5b batched prefill + decode", flush=True)
+    _CACHE.clear()
+    sd = make_random_state_dict("1.5b", seed=0, dtype=torch.float16)
+    w = RWKV7Weight.from_state_dict(sd, device=cuda, dtype=torch.float16)
+    model = RWKV7HIP(w, is_torch_compile=False)
+    ref32 = R.Weights.from_emb(sd, w.emb.cpu(), torch.float32)
+    del sd
+    B, V = 2, w.head.shape[0]
+    g = torch.Generator().manual_seed(15)
+    prompt = torch.randint(0, V, (B, 3), generator=g)
+    nxt = torch.randint(0, V, (2, B), generator=g)
+    S = State(w.L, w.C, 64, device=cuda, batch=B)
+    model.prefill(prompt.to(cuda), S)
+    ref = R.new_state(w.L, w.C, dtype=torch.float16, batch=B)
+    R.prefill(ref32, prompt, ref)
+    for step in range(2):
+        lg, S = model.decode(nxt[step].to(cuda), S)
+        l32, ref = R.decode(ref32, nxt[step], ref)
+        for b in range(B):
+            _check_logits(lg[b], l32[b], f"1.5b B=2 step {step} row {b}")
+    for i in range(w.L):
+        for b in range(B):
+            r = _rel(S.tmix[i]["rnn"][b].cpu(), ref[0][i]["rnn"][b])
+            assert r < 5e-3, f"1.5b layer {i} row {b}: {r:.2e}"
+    S1 = State(w.L, w.C, 64, device=cuda)
+    lg1, S1 = model.decode(nxt[0, :1].to(cuda), S1)
+    l1, _ = R.decode(ref32, nxt[0, :1], R.new_state(w.L, w.C, dtype=torch.float16))
+    _check_logits(lg1, l1, "1.5b B=1 decode")
+
+
+@pytest.mark.slow
+def test_1p5b_shape_long_prefill_and_batch64_properties(cuda):
+    """Config C5's sizes on the 1.5B shape, where the CPU oracle is too slow:
+    prefill of 4 x 1024 tokens in one call equals two calls of 512 (fp32
+    state within 5e-3, the prefill bar), and rows of a batch-64 decode equal
+    the same sequences decoded one at a time (logits within 1e-2 / 1e-3)."""
+    print("1.5b 4x1024 prefill and B=64 decode properties", flush=True)
+    _CACHE.clear()
+    sd = make_random_state_dict("1.5b", seed=0, dtype=torch.float16)
+    w = RWKV7Weight.from_state_dict(sd, device=cuda, dtype=torch.float16)
+    del sd
+    model = RWKV7HIP(w, is_torch_compile=False)
+    V = w.head.shape[0]
+    g = torch.Generator().manual_seed(21)
+    toks = torch.randint(0, V, (4, 1024), generator=g).to(cuda)
+    S1 = State(w.L, w.C, 64, device=cuda, batch=4)
+    model.prefill(toks, S1)
+    S2 = State(w.L, w.C, 64, device=cuda, batch=4)
+    model.prefill(toks[:, :512].contiguous(), S2)
+    model.prefill(toks[:, 512:].contiguous(), S2)
+    for i in range(w.L):
+        r = _rel(S1.tmix[i]["rnn"].cpu(), S2.tmix[i]["rnn"].cpu())
+        assert r < 5e-3, f"layer {i}: one 1024-token prefill vs two of 512: {r:.2e}"
+    B = 64
+    nxt = torch.randint(0, V, (B,), generator=g).to(cuda)
+    SB = State(w.L, w.C, 64, device=cuda, batch=B)
+    lgB, SB = model.decode(nxt, SB)
+    for b in (0, 17, 63):
+        Sb = State(w.L, w.C, 64, device=cuda)
+        lgb, Sb = model.decode(nxt[b : b + 1], Sb)
+        _check_logits(lgB[b], lgb, f"1.5b B=64 row {b} vs B=1")
+
+
 @pytest.mark.parametrize("path", ["persistent", "kernels"])
 def test_graph_replay_matches_eager(cuda, path, monkeypatch):
     """HIP-graph decode and prefill replay == eager calls, bit for bit, over
