@@ -115,6 +115,7 @@ static int64_t decode_ws(const rwkv7_dims &d, char *base, DecodeWs *w) {
 struct BatchWs {
   float *x0, *rkv, *d, *vfirst, *kv, *y, *part;  // kv: gated k, mixed v [2][M][C]
   uint16_t *xmix, *l1, *yg, *hid, *headin;
+  float *U, *Send, *Pend;  // segmented scan of long sequences (null with one segment)
 };
 static int64_t batch_ws(const rwkv7_dims &d, int64_t B, int64_t T, char *base, BatchWs *w) {
   const int64_t C = d.n_embd, F = d.n_ffn, SR = sum_ranks(d), M = B * T;
@@ -138,6 +139,15 @@ static int64_t batch_ws(const rwkv7_dims &d, int64_t B, int64_t T, char *base, B
   t.headin = reinterpret_cast<uint16_t *>(take(B * C * 2));
   const int cus = mk_cus();
   t.part = reinterpret_cast<float *>(take(gemm_ws_bytes((int)(M > B ? M : B), cus > 0 ? cus : 256)));
+  int seg_len;
+  const int64_t nseg = prefill_segments((int)T, &seg_len);
+  t.U = t.Send = t.Pend = nullptr;
+  if (nseg > 1) {
+    const int64_t slab = nseg * B * d.n_head * (int64_t)RWKV7_HEAD_SIZE * RWKV7_HEAD_SIZE * 4;
+    t.U = reinterpret_cast<float *>(take(M * C * 4));
+    t.Send = reinterpret_cast<float *>(take(slab));
+    t.Pend = reinterpret_cast<float *>(take(slab));
+  }
   if (w) *w = t;
   return off;
 }
@@ -313,7 +323,8 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
     };
     for (int g = 0; g < 4; ++g) frag(g2[g], lay.f_l2[g], 0);
     RWKV7_TRY(launch_gemm_group(g2, 4, M, st, w.part, ctr));
-    PrefillScanArgs sc = {rnn, w.rkv, w.d, vec, w.vfirst, w.y, w.kv, w.kv + MC, B, T, H, C, M, l == 0};
+    PrefillScanArgs sc = {rnn, w.rkv, w.d, vec, w.vfirst, w.y, w.kv, w.kv + MC, B, T, H, C, M, l == 0,
+                          w.U, w.Send, w.Pend};
     RWKV7_TRY(launch_wkv7_prefill(sc, st));
     GnGateArgs gn = {w.y, w.rkv, w.kv, w.kv + MC, w.d + 3 * MC, vec, w.yg, C, M};
     RWKV7_TRY(launch_gn_gate(gn, st));

@@ -52,6 +52,19 @@ RWKV7_DEV float sum16(float v) {
   return v;
 }
 
+// Two independent 16-lane row sums, reduced in lockstep.
+RWKV7_DEV float2 sum16x2(float a, float b) {
+  a += dpp<kDppXor1>(a);
+  b += dpp<kDppXor1>(b);
+  a += dpp<kDppXor2>(a);
+  b += dpp<kDppXor2>(b);
+  a += dpp<kDppHalfMirror>(a);
+  b += dpp<kDppHalfMirror>(b);
+  a += dpp<kDppMirror>(a);
+  b += dpp<kDppMirror>(b);
+  return make_float2(a, b);
+}
+
 // Sum over the whole wave; the result is wave-uniform.
 RWKV7_DEV float lane_value(float v, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));

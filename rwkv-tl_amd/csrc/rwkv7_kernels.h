@@ -65,12 +65,19 @@ int launch_ln_shift(const LnShiftArgs &a, hipStream_t st);
 // rkv f32 [3][M][C] (r, k, v), d f32 [4][M][C] (LoRA second steps v, w, a, g),
 // vfirst f32 [M][C] (written on layer 0, read after), outputs y, kn_out (the
 // gated k) and v_out (the mixed v), f32 [M][C]; M = B * T, rows b * T + t.
+// Long sequences are scanned in nseg segments of seg_len tokens at once
+// (prefill_segments); segments after the first start from a zero state and
+// also carry their transition product, and a second kernel chains the
+// segments. U [M, C], Send and Pend [nseg, B, H, 64, 64] (f32) are workspace
+// for that; unused (may be null) when nseg == 1.
 struct PrefillScanArgs {
   float *S;
   const float *rkv, *d, *vec;
   float *vfirst, *y, *kn_out, *v_out;
   int B, T, H, C, M, layer0;
+  float *U, *Send, *Pend;
 };
+int prefill_segments(int T, int *seg_len);
 int launch_wkv7_prefill(const PrefillScanArgs &p, hipStream_t st);
 
 struct GnGateArgs {

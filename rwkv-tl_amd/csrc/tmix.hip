@@ -252,14 +252,28 @@ template int launch_wkv7_scan<float, float, float>(const ScanArgs<float, float, 
 // DPP sum; S w + v k is formed while that sum runs, so the new state is one FMA
 // past sa; the next step's inputs are read from LDS while the current step
 // computes; y is left as per-lane partials in LDS and summed once per chunk.
+//
+// Segments (grid z): a long sequence is cut into nseg pieces of seg_len tokens
+// scanned at once. Segment 0 starts from the real state; segment j > 0 starts
+// from zero and also carries the rows of its transition product
+// P_t = M_1 ... M_t (M = diag(w) + a b^T, from the identity, no v k term), so
+// that with S_in the state entering it, S_t = S_in P_t + S_loc_t and
+// y_t = y_loc_t + S_in u_t with u_t = P_t r. It writes y_loc and u, and its
+// end state and product to Send / Pend; wkv7_prefill_combine_kernel then
+// chains the segments and adds S_in u_t.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p) {
+template <bool SEG>  // SEG: launched with more than one segment
+__global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p, int seg_len, int nseg) {
   // s_in[buf][vec][token][16 float4]: vec 0 w, 1 a, 2 b, 3 k, 4 r, 5 v
   __shared__ float4 s_in[2][6][kCh][kN / 4];
   __shared__ float s_yp[kCh][16][17];  // per-lane partial y: [step][row][lane], padded
+  __shared__ float s_up[SEG ? kCh : 1][16][17];  // the same for u (segments after the first)
 
   const int t = threadIdx.x;
   const int h = blockIdx.x >> 2, quarter = blockIdx.x & 3, bi = blockIdx.y;
+  const int seg = blockIdx.z;
+  const bool tail = SEG && seg > 0;  // block-uniform
+  const int t0 = seg * seg_len, t1 = min(p.T, t0 + seg_len), Tl = t1 - t0;
   const int row = quarter * 16 + (t >> 4);
   const int lc = t & 15;  // owns key columns 4*lc .. 4*lc+3
   const int H = p.H, T = p.T, C = p.C;
@@ -276,8 +290,8 @@ __global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p) {
   const float4 kav = ld4(vec + RWKV7_V_K_A * C + ch0);
   float4 g_r, g_k, g_v, g_dv, g_dw, g_da, g_vf;
   auto fetch = [&](int c0) {
-    const int tt = c0 + st_tok;
-    const int ts = tt < T ? tt : T - 1;  // clamped (its step is never run)
+    const int tt = t0 + c0 + st_tok;
+    const int ts = tt < t1 ? tt : t1 - 1;  // clamped (its step is never run)
     const int64_t o = base + (int64_t)ts * C + 4 * q;
     g_r = ld4(p.rkv + o);
     g_k = ld4(p.rkv + MC + o);
@@ -288,7 +302,7 @@ __global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p) {
     g_vf = p.layer0 ? g_v : ld4(p.vfirst + o);
   };
   auto commit = [&](int c0, int buf) {
-    const int tt = c0 + st_tok;
+    const int tt = t0 + c0 + st_tok;
     const float k4[4] = {g_k.x, g_k.y, g_k.z, g_k.w};
     const float vr[4] = {g_v.x, g_v.y, g_v.z, g_v.w}, dv[4] = {g_dv.x, g_dv.y, g_dv.z, g_dv.w};
     const float dw[4] = {g_dw.x, g_dw.y, g_dw.z, g_dw.w}, da[4] = {g_da.x, g_da.y, g_da.z, g_da.w};
@@ -321,7 +335,7 @@ __global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p) {
     s_in[buf][4][st_tok][q] = g_r;
     s_in[buf][5][st_tok][q] = make_float4(v[0], v[1], v[2], v[3]);
     // this workgroup's 16 channels of the values GroupNorm needs
-    if (tt < T && (q >> 2) == quarter) {
+    if (tt < t1 && (q >> 2) == quarter) {
       const int64_t o = base + (int64_t)tt * C + 4 * q;
       *reinterpret_cast<float4 *>(p.kn_out + o) = make_float4(kn[0], kn[1], kn[2], kn[3]);
       *reinterpret_cast<float4 *>(p.v_out + o) = make_float4(v[0], v[1], v[2], v[3]);
@@ -330,16 +344,22 @@ __global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p) {
   };
 
   float4 *Sp = reinterpret_cast<float4 *>(p.S + (((int64_t)bi * H + h) * kN + row) * kN) + lc;
-  float4 S = *Sp;
+  float4 S = tail ? make_float4(0.f, 0.f, 0.f, 0.f) : *Sp;
+  // rows of the transition product, from the identity (tail segments only)
+  float4 P = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (lc == (row >> 2)) {
+    const int e = row & 3;
+    P = make_float4(e == 0, e == 1, e == 2, e == 3);
+  }
 
   fetch(0);
   commit(0, 0);
   __syncthreads();
-  const int nch = (T + kCh - 1) / kCh;
+  const int nch = (Tl + kCh - 1) / kCh;
   for (int c = 0; c < nch; ++c) {
     const int buf = c & 1;
     if (c + 1 < nch) fetch((c + 1) * kCh);
-    const int steps = min(kCh, T - c * kCh);
+    const int steps = min(kCh, Tl - c * kCh);
     const float *vrow = reinterpret_cast<const float *>(&s_in[buf][5][0][0]) + row;
     struct In {
       float4 w, a, b, k, r;
@@ -372,39 +392,212 @@ __global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p) {
       y1 = fmaf(S.w, x.r.w, y1);
       s_yp[st][t >> 4][lc] = y0 + y1;
     };
+    // the same step plus the transition product's rows: P <- P (diag(w) + a b^T)
+    auto step_tail = [&](const In &x, int st) {
+      float p0 = S.x * x.a.x, p1 = S.z * x.a.z;
+      float q0 = P.x * x.a.x, q1 = P.z * x.a.z;
+      p0 = fmaf(S.y, x.a.y, p0);
+      p1 = fmaf(S.w, x.a.w, p1);
+      q0 = fmaf(P.y, x.a.y, q0);
+      q1 = fmaf(P.w, x.a.w, q1);
+      float4 pre;
+      pre.x = fmaf(S.x, x.w.x, x.v * x.k.x);
+      pre.y = fmaf(S.y, x.w.y, x.v * x.k.y);
+      pre.z = fmaf(S.z, x.w.z, x.v * x.k.z);
+      pre.w = fmaf(S.w, x.w.w, x.v * x.k.w);
+      const float2 sums = sum16x2(p0 + p1, q0 + q1);
+      S.x = fmaf(sums.x, x.b.x, pre.x);
+      S.y = fmaf(sums.x, x.b.y, pre.y);
+      S.z = fmaf(sums.x, x.b.z, pre.z);
+      S.w = fmaf(sums.x, x.b.w, pre.w);
+      P.x = fmaf(sums.y, x.b.x, P.x * x.w.x);
+      P.y = fmaf(sums.y, x.b.y, P.y * x.w.y);
+      P.z = fmaf(sums.y, x.b.z, P.z * x.w.z);
+      P.w = fmaf(sums.y, x.b.w, P.w * x.w.w);
+      float y0 = S.x * x.r.x, y1 = S.z * x.r.z;
+      float u0 = P.x * x.r.x, u1 = P.z * x.r.z;
+      y0 = fmaf(S.y, x.r.y, y0);
+      y1 = fmaf(S.w, x.r.w, y1);
+      u0 = fmaf(P.y, x.r.y, u0);
+      u1 = fmaf(P.w, x.r.w, u1);
+      s_yp[st][t >> 4][lc] = y0 + y1;
+      if (SEG) s_up[st][t >> 4][lc] = u0 + u1;
+    };
     // two input register sets in turn: the next step's inputs are read from
     // LDS while the current step computes
     In x0, x1;
     load_in(x0, 0);
     int st = 0;
-    for (; st + 1 < steps; st += 2) {
-      load_in(x1, st + 1);
-      step(x0, st);
-      load_in(x0, st + 2 < steps ? st + 2 : st + 1);
-      step(x1, st + 1);
+    if (!tail) {
+      for (; st + 1 < steps; st += 2) {
+        load_in(x1, st + 1);
+        step(x0, st);
+        load_in(x0, st + 2 < steps ? st + 2 : st + 1);
+        step(x1, st + 1);
+      }
+      if (st < steps) step(x0, st);
+    } else if (SEG) {
+      for (; st + 1 < steps; st += 2) {
+        load_in(x1, st + 1);
+        step_tail(x0, st);
+        load_in(x0, st + 2 < steps ? st + 2 : st + 1);
+        step_tail(x1, st + 1);
+      }
+      if (st < steps) step_tail(x0, st);
     }
-    if (st < steps) step(x0, st);
     __syncthreads();
-    {  // y of (step t >> 4, row t & 15): sum of the 16 lane partials
+    {  // y (and u) of (step t >> 4, row t & 15): sums of the 16 lane partials
       const int ss = t >> 4, rr = t & 15;
       if (ss < steps) {
         float y = 0.f;
 #pragma unroll
         for (int l = 0; l < 16; ++l) y += s_yp[ss][rr][l];
-        p.y[base + (int64_t)(c * kCh + ss) * C + quarter * 16 + rr] = y;
+        const int64_t o = base + (int64_t)(t0 + c * kCh + ss) * C + quarter * 16 + rr;
+        p.y[o] = y;
+        if (SEG && tail) {
+          float u = 0.f;
+#pragma unroll
+          for (int l = 0; l < 16; ++l) u += s_up[SEG ? ss : 0][rr][l];
+          p.U[o] = u;
+        }
       }
     }
     if (c + 1 < nch) commit((c + 1) * kCh, buf ^ 1);
     __syncthreads();
   }
-  *Sp = S;
+  if (!SEG) {
+    *Sp = S;
+  } else {
+    const int64_t slab = (int64_t)p.B * H * kN * kN;
+    const int64_t o = (((int64_t)bi * H + h) * kN + row) * kN + 4 * lc;
+    *reinterpret_cast<float4 *>(p.Send + seg * slab + o) = S;
+    if (tail) *reinterpret_cast<float4 *>(p.Pend + seg * slab + o) = P;
+  }
+}
+
+// Chains the segments of wkv7_prefill_kernel. Grid (4 H, B, (nseg - 1) *
+// nblk): the workgroup of segment j >= 1 and 16-token block k of it forms the
+// state entering j, S_in(1) = Send(0), S_in(i + 1) = S_in(i) Pend(i) + Send(i),
+// adds S_in(j) u_t to y_t of its tokens, and (block 0 of the last segment)
+// writes the final state. 16 rows of one head per workgroup, 4 columns per
+// lane. The products are staged in LDS kPmBuf at a time with all their loads
+// in flight, since they were written by other XCDs and each load is a trip to
+// memory.
+constexpr int kPmBuf = 3;
+__global__ __launch_bounds__(256) void wkv7_prefill_combine_kernel(PrefillScanArgs p, int seg_len, int nseg) {
+  __shared__ float s_row[16][kN + 4];
+  __shared__ float4 s_pm[kPmBuf][kN][kN / 4];
+  __shared__ float4 s_sd[kPmBuf][256];  // this thread's Send rows
+  const int t = threadIdx.x;
+  const int nblk = (seg_len + kCh - 1) / kCh;
+  const int h = blockIdx.x >> 2, quarter = blockIdx.x & 3, bi = blockIdx.y;
+  const int j = blockIdx.z / nblk + 1, blk = blockIdx.z % nblk;
+  const int r16 = t >> 4, row = quarter * 16 + r16, lc = t & 15;
+  const int H = p.H, C = p.C;
+  const int64_t slab = (int64_t)p.B * H * kN * kN;
+  const int64_t hoff = ((int64_t)bi * H + h) * kN * kN;
+  auto at = [&](const float *m, int i) {
+    return *reinterpret_cast<const float4 *>(m + i * slab + hoff + (int64_t)row * kN + 4 * lc);
+  };
+  const bool final_state = j == nseg - 1 && blk == 0;
+  const int last = final_state ? j : j - 1;  // products to apply
+  // this block's u loads go out first: they do not depend on the chain
+  const int64_t base = (int64_t)bi * p.T * C + (int64_t)h * kN;
+  const int tb = j * seg_len + blk * kCh;
+  const int n = min(kCh, min(p.T, (j + 1) * seg_len) - tb);
+  float4 u[kCh];
+#pragma unroll
+  for (int q = 0; q < kCh; ++q) {
+    u[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (q < n) u[q] = *reinterpret_cast<const float4 *>(p.U + base + (int64_t)(tb + q) * C + 4 * lc);
+  }
+  float4 sin = at(p.Send, 0), sin_j = sin;
+  for (int g0 = 1; g0 <= last; g0 += kPmBuf) {
+    const int gn = min(kPmBuf, last - g0 + 1);
+    __syncthreads();  // the previous group's readers are done
+#pragma unroll
+    for (int b = 0; b < kPmBuf; ++b) {
+      if (b < gn) {  // global to LDS: no load waits for a store
+        const float4 *src = reinterpret_cast<const float4 *>(p.Pend + (g0 + b) * slab + hoff);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) (&s_pm[b][0][0])[t + 256 * e] = src[t + 256 * e];
+        s_sd[b][t] = at(p.Send, g0 + b);
+      }
+    }
+    for (int b = 0; b < gn; ++b) {
+      {
+        if (g0 + b == j) sin_j = sin;
+        __syncthreads();
+        *reinterpret_cast<float4 *>(&s_row[r16][4 * lc]) = sin;
+        __syncthreads();
+        float4 acc = s_sd[b][t];
+#pragma unroll 16
+        for (int k = 0; k < kN; ++k) {
+          const float sk = s_row[r16][k];
+          const float4 pr = s_pm[b][k][lc];
+          acc.x = fmaf(sk, pr.x, acc.x);
+          acc.y = fmaf(sk, pr.y, acc.y);
+          acc.z = fmaf(sk, pr.z, acc.z);
+          acc.w = fmaf(sk, pr.w, acc.w);
+        }
+        sin = acc;
+      }
+    }
+  }
+  if (final_state) {
+    *(reinterpret_cast<float4 *>(p.S + hoff + (int64_t)row * kN) + lc) = sin;
+    sin = sin_j;  // the state entering segment j, for the outputs below
+  }
+  // y_t += S_in(j) u_t for the (up to) 16 tokens of this block: the 16 lanes'
+  // partial dots summed through LDS, lane k finishing token k
+  float part[kCh];
+#pragma unroll
+  for (int q = 0; q < kCh; ++q)
+    part[q] = fmaf(sin.x, u[q].x, fmaf(sin.y, u[q].y, fmaf(sin.z, u[q].z, sin.w * u[q].w)));
+  __syncthreads();  // s_pm readers are done: its first 16 KB take the partials
+  float *red = reinterpret_cast<float *>(&s_pm[0][0][0]);  // [16 rows][16 tokens][17]
+#pragma unroll
+  for (int q = 0; q < kCh; ++q) red[(r16 * kCh + q) * 17 + lc] = part[q];
+  __syncthreads();
+  if (lc < n) {
+    float tot = 0.f;
+#pragma unroll
+    for (int l = 0; l < 16; ++l) tot += red[(r16 * kCh + lc) * 17 + l];
+    p.y[base + (int64_t)(tb + lc) * C + row] += tot;
+  }
+}
+
+// Segments of the prefill scan for T tokens: up to 16 of >= 32 tokens (a
+// multiple of the 16-token staging chunk); one segment below 64 tokens.
+int prefill_segments(int T, int *seg_len) {
+  int P = T / 32;
+  if (P > 16) P = 16;
+  if (P < 2) {
+    *seg_len = T;
+    return 1;
+  }
+  int L = (T + P - 1) / P;
+  L = (L + kCh - 1) / kCh * kCh;
+  *seg_len = L;
+  return (T + L - 1) / L;
 }
 
 int launch_wkv7_prefill(const PrefillScanArgs &p, hipStream_t st) {
   if (p.T <= 0 || p.B <= 0 || p.H <= 0) return RWKV7_OK;
   if (p.C != p.H * kN) return RWKV7_ESHAPE;
-  wkv7_prefill_kernel<<<dim3(4 * p.H, p.B), 256, 0, st>>>(p);
+  int seg_len;
+  const int nseg = prefill_segments(p.T, &seg_len);
+  if (nseg > 1 && (!p.U || !p.Send || !p.Pend)) return RWKV7_EWORKSPACE;
+  if (nseg == 1)
+    wkv7_prefill_kernel<false><<<dim3(4 * p.H, p.B, 1), 256, 0, st>>>(p, seg_len, nseg);
+  else
+    wkv7_prefill_kernel<true><<<dim3(4 * p.H, p.B, nseg), 256, 0, st>>>(p, seg_len, nseg);
   RWKV7_CHECK_LAUNCH();
+  if (nseg > 1) {
+    const int nblk = (seg_len + kCh - 1) / kCh;
+    wkv7_prefill_combine_kernel<<<dim3(4 * p.H, p.B, (nseg - 1) * nblk), 256, 0, st>>>(p, seg_len, nseg);
+    RWKV7_CHECK_LAUNCH();
+  }
   return RWKV7_OK;
 }
 

@@ -117,7 +117,11 @@ def test_decode_0p4b_256_steps_state(cuda):
     _check_state(S, s32, STATE_REL, "0.4b state after 256 steps")
 
 
-@pytest.mark.parametrize("shape,T", [("tiny", 1), ("tiny", 15), ("tiny", 40), ("0.1b", 33)])
+# T >= 64 runs the segmented scan (segments of >= 32 tokens chained by a
+# second kernel): 64 -> 2 x 32, 100 -> 48 + 48 + 4, 130 -> 4 x 48 (last 16),
+# 300 -> 7 x 48 (last 12).
+@pytest.mark.parametrize("shape,T", [("tiny", 1), ("tiny", 15), ("tiny", 40), ("0.1b", 33),
+                                     ("tiny", 64), ("tiny", 100), ("tiny", 300), ("0.1b", 130)])
 def test_prefill_then_decode_matches_oracle(shape, T, cuda):
     print(f"prefill parity {shape} T={T}", flush=True)
     st = setup_for(shape, cuda)
@@ -145,6 +149,29 @@ def test_prefill_rejects_empty_and_bad_shapes(cuda):
         st.model.decode(torch.tensor([1, 2], device=cuda), S)
     with pytest.raises(ValueError):
         st.model.decode(torch.tensor([10**6]), S)
+
+
+def test_batched_segmented_prefill_matches_oracle(cuda):
+    """B=3 sequences of 80 tokens (three segments each) prefilled in one call:
+    every row's state and next logits match the oracle's."""
+    print("batched segmented prefill B=3 T=80", flush=True)
+    st = setup_for("tiny", cuda)
+    V, B = st.w.head.shape[0], 3
+    g = torch.Generator().manual_seed(80)
+    prompt = torch.randint(0, V, (B, 80), generator=g)
+    nxt = torch.randint(0, V, (B,), generator=g)
+    S = State(st.w.L, st.w.C, 64, device=cuda, batch=B)
+    st.model.prefill(prompt.to(cuda), S)
+    lg, S = st.model.decode(nxt.to(cuda), S)
+    ref = R.new_state(st.w.L, st.w.C, dtype=torch.float16, batch=B)
+    R.prefill(st.ref32, prompt, ref)
+    l32, ref = R.decode(st.ref32, nxt, ref)
+    for b in range(B):
+        _check_logits(lg[b], l32[b], f"segmented prefill row {b}")
+    for i in range(st.w.L):
+        for b in range(B):
+            r = _rel(S.tmix[i]["rnn"][b].cpu(), ref[0][i]["rnn"][b])
+            assert r < 5e-3, f"layer {i} row {b}: {r:.2e}"
 
 
 @pytest.mark.parametrize("B", [2, 5])
