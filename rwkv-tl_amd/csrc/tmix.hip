@@ -567,11 +567,12 @@ __global__ __launch_bounds__(256) void wkv7_prefill_combine_kernel(PrefillScanAr
   }
 }
 
-// Segments of the prefill scan for T tokens: up to 16 of >= 32 tokens (a
-// multiple of the 16-token staging chunk); one segment below 64 tokens.
+// Segments of the prefill scan for T tokens (lengths a multiple of the
+// 16-token staging chunk): one below 64 tokens, up to 4 of >= 32 tokens below
+// 256, up to 8 of >= 64 tokens beyond (measured on 0.4B: more, shorter
+// segments lose more to the chain of products than they gain in the scan).
 int prefill_segments(int T, int *seg_len) {
-  int P = T / 32;
-  if (P > 16) P = 16;
+  int P = T < 64 ? 1 : T < 256 ? min(4, T / 32) : min(8, T / 64);
   if (P < 2) {
     *seg_len = T;
     return 1;
