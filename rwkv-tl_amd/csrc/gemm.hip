@@ -589,8 +589,10 @@ static int launch_skinny(const GemmProb *probs, int nprob, int M, hipStream_t st
 }
 
 // Row tile of the tiled path: 32 rows up to M = 256 (the tiles alone then
-// cover the GPU and W, re-read per row tile, comes from L2), 128 beyond.
-static int bm_for(int M) { return M <= 256 ? 32 : 128; }
+// cover the GPU and W, re-read per row tile, comes from L2), 64 beyond
+// (measured at M = 512 to 4096: 128-row tiles leave too few workgroups per CU
+// to hide the chunk loads; 32-row tiles re-read W too often).
+static int bm_for(int M) { return M <= 256 ? 32 : 64; }
 
 // Splits of a tiled problem: K is split (power of two, each split keeping at
 // least two 128-wide chunks) until the group has a workgroup per CU and no

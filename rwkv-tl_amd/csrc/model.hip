@@ -140,7 +140,7 @@ static int64_t batch_ws(const rwkv7_dims &d, int64_t B, int64_t T, char *base, B
   const int cus = mk_cus();
   t.part = reinterpret_cast<float *>(take(gemm_ws_bytes((int)(M > B ? M : B), cus > 0 ? cus : 256)));
   int seg_len;
-  const int64_t nseg = prefill_segments((int)T, &seg_len);
+  const int64_t nseg = prefill_segments((int)T, (int)B, d.n_head, &seg_len);
   t.U = t.Send = t.Pend = nullptr;
   if (nseg > 1) {
     const int64_t slab = nseg * B * d.n_head * (int64_t)RWKV7_HEAD_SIZE * RWKV7_HEAD_SIZE * 4;

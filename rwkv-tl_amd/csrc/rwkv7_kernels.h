@@ -77,7 +77,7 @@ struct PrefillScanArgs {
   int B, T, H, C, M, layer0;
   float *U, *Send, *Pend;
 };
-int prefill_segments(int T, int *seg_len);
+int prefill_segments(int T, int B, int H, int *seg_len);
 int launch_wkv7_prefill(const PrefillScanArgs &p, hipStream_t st);
 
 struct GnGateArgs {

@@ -567,12 +567,15 @@ __global__ __launch_bounds__(256) void wkv7_prefill_combine_kernel(PrefillScanAr
   }
 }
 
-// Segments of the prefill scan for T tokens (lengths a multiple of the
-// 16-token staging chunk): one below 64 tokens, up to 4 of >= 32 tokens below
-// 256, up to 8 of >= 64 tokens beyond (measured on 0.4B: more, shorter
-// segments lose more to the chain of products than they gain in the scan).
-int prefill_segments(int T, int *seg_len) {
+// Segments of the prefill scan for T tokens of B sequences of H heads
+// (lengths a multiple of the 16-token staging chunk): one below 64 tokens, up
+// to 4 of >= 32 tokens below 256, up to 8 of >= 64 tokens beyond (measured on
+// 0.4B: more, shorter segments lose more to the chain of products than they
+// gain in the scan), and no more than fit the 4 H B workgroups of one segment
+// on the GPU's 256 CUs at once (a segmented workgroup takes a CU's LDS).
+int prefill_segments(int T, int B, int H, int *seg_len) {
   int P = T < 64 ? 1 : T < 256 ? min(4, T / 32) : min(8, T / 64);
+  P = min(P, 256 / max(1, 4 * H * B));
   if (P < 2) {
     *seg_len = T;
     return 1;
@@ -587,7 +590,7 @@ int launch_wkv7_prefill(const PrefillScanArgs &p, hipStream_t st) {
   if (p.T <= 0 || p.B <= 0 || p.H <= 0) return RWKV7_OK;
   if (p.C != p.H * kN) return RWKV7_ESHAPE;
   int seg_len;
-  const int nseg = prefill_segments(p.T, &seg_len);
+  const int nseg = prefill_segments(p.T, p.B, p.H, &seg_len);
   if (nseg > 1 && (!p.U || !p.Send || !p.Pend)) return RWKV7_EWORKSPACE;
   if (nseg == 1)
     wkv7_prefill_kernel<false><<<dim3(4 * p.H, p.B, 1), 256, 0, st>>>(p, seg_len, nseg);
