@@ -596,7 +596,8 @@ static int bm_for(int M) { return M <= 256 ? 32 : 64; }
 
 // Splits of a tiled problem: K is split (power of two, each split keeping at
 // least two 128-wide chunks) until the group has a workgroup per CU and no
-// workgroup streams more than ~128 KB of W and A.
+// workgroup streams more than ~256 KB of W and A (measured: a 128 KB cap,
+// i.e. twice the splits, made prefill at T = 128 to 512 2-8% slower).
 static void plan_splits(const GemmProb *probs, int nprob, int M, int cus, bool can_split, int *S, int *kslice) {
   const int BM = bm_for(M);
   const int m_tiles = (M + BM - 1) / BM;
@@ -607,7 +608,7 @@ static void plan_splits(const GemmProb *probs, int nprob, int M, int cus, bool c
     int s = 1;
     if (can_split) {
       auto bytes = [&](int sp) { return (int64_t)(kBN + BM) * 2 * ((K + sp - 1) / sp); };
-      while (s < kMaxSplit && K / (2 * s) >= 2 * kKC && (tiles * s < cus || bytes(s) > 128 * 1024) &&
+      while (s < kMaxSplit && K / (2 * s) >= 2 * kKC && (tiles * s < cus || bytes(s) > 256 * 1024) &&
              (int64_t)tiles * 2 * s <= 4 * cus)
         s *= 2;
     }
@@ -674,13 +675,14 @@ int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, f
   }
   g.wg_begin[kMaxProb] = wgs;
   if (pfl * 4 > gemm_ws_bytes(M, cus) || ctrs > kGemmCounters) return RWKV7_EWORKSPACE;
-  // every split of at most 4 chunks: the prefetch-all kernel (BM <= 64)
+  // every split of at most 8 chunks: the prefetch-all kernel
   int ncmax = 1;
   for (int i = 0; i < nprob; ++i) ncmax = max(ncmax, ks[i] / kKC);
-  if (BM == 32 && ncmax <= 4) {
+  if (BM == 32 && ncmax <= 8) {
     if (ncmax == 1) gemm_pf_kernel<32, 1><<<wgs, 256, 0, st>>>(g);
     else if (ncmax == 2) gemm_pf_kernel<32, 2><<<wgs, 256, 0, st>>>(g);
-    else gemm_pf_kernel<32, 4><<<wgs, 256, 0, st>>>(g);
+    else if (ncmax <= 4) gemm_pf_kernel<32, 4><<<wgs, 256, 0, st>>>(g);
+    else gemm_pf_kernel<32, 8><<<wgs, 256, 0, st>>>(g);
     RWKV7_CHECK_LAUNCH();
     return RWKV7_OK;
   }
