@@ -522,12 +522,14 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(SkinnyGroup g) {
 }
 
 // Splits of a skinny strip: enough that one workgroup moves at most ~64 KB
-// of W and A.
+// of W and A, ~128 KB above 16 rows (measured: with 17..32 rows the larger
+// cap is 4-5% faster, with up to 16 rows 2% slower).
 static int skinny_splits(int M, int K, bool can_split) {
   if (!can_split) return 1;
   const int64_t per_k = 16 * 2 + (int64_t)(M < 16 ? M : 16) * 2 * ((M + 15) / 16);  // bytes per unit of k
+  const int64_t cap = M > 16 ? 128 * 1024 : 64 * 1024;
   int S = 1;
-  while (S < kMaxSplit && (int64_t)K / S * per_k > 64 * 1024 && K / (2 * S) >= 256) S *= 2;
+  while (S < kMaxSplit && (int64_t)K / S * per_k > cap && K / (2 * S) >= 256) S *= 2;
   return S;
 }
 
