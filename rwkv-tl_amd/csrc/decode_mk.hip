@@ -343,7 +343,7 @@ RWKV7_DEV void probe_wait(const MkCtx &cx, int cw, __amdgpu_buffer_rsrc_t r, int
     const uint4 v = ld_pair(r, idx(pq));
     if (v.y == tag) waiting = false;
     else if (!sb.keep_waiting()) break;
-    __builtin_amdgcn_s_sleep(1);
+    else __builtin_amdgcn_s_sleep(1);  // only while some lane still waits
   }
 }
 
