@@ -182,17 +182,17 @@ RWKV7_DEV void find_cross(SampleLds &s, u64 above, u64 W) {
   __syncthreads();
 }
 
-// Largest kept value y (kept: x > -inf) with sum over kept x >= y of wt(x)
-// > W, where wt(x) = 1 (MASS false) or mass(x, m); [lo, hi] is the range of
-// the kept values. If the total is <= W, lo (every kept element stays kept).
+// Largest value y among the elements x >= lo (lo > -inf; hi their maximum) with
+// sum over x >= y of wt(x) > W, where wt(x) = 1 (MASS false) or mass(x, m).
+// If the total is <= W, lo. Each thread holds E elements (-inf: none).
 //
 // One pass of 256 equal-width bins over [lo, hi] picks the bin that holds y;
 // its elements are copied to LDS (when there are at most kCandCap of them),
 // and radix passes of up to 8 bits over their order-preserving keys narrow the
 // key range to one value. A larger bin is narrowed the same way straight from
 // the registers.
-template <bool MASS>
-RWKV7_DEV float select_gt(const float (&l)[kSmpE], float lo, float hi, float m, u64 W, SampleLds &s) {
+template <bool MASS, int E>
+RWKV7_DEV float select_gt(const float (&l)[E], float lo, float hi, float m, u64 W, SampleLds &s) {
   auto wt = [](float x, float mm) -> u64 { return MASS ? mass(x, mm) : 1ull; };
   if (!(lo < hi)) return lo;
   // pass 0: equal-width bins over [lo, hi]
@@ -204,8 +204,8 @@ RWKV7_DEV float select_gt(const float (&l)[kSmpE], float lo, float hi, float m, 
   {
     const float mo = opaque(m);
 #pragma unroll
-    for (int e = 0; e < kSmpE; ++e)
-      if (l[e] > -kInf) atomicAdd(&s.hist[lbin(l[e], lo, scale)], wt(l[e], mo));
+    for (int e = 0; e < E; ++e)
+      if (l[e] > -kInf && l[e] >= lo) atomicAdd(&s.hist[lbin(l[e], lo, scale)], wt(l[e], mo));
   }
   __syncthreads();
   find_cross(s, 0, W);
@@ -217,8 +217,8 @@ RWKV7_DEV float select_gt(const float (&l)[kSmpE], float lo, float hi, float m, 
   {
     const float lo2 = opaque(lo), sc2 = opaque(scale);
 #pragma unroll
-    for (int e = 0; e < kSmpE; ++e) {
-      if (l[e] > -kInf && lbin(l[e], lo2, sc2) == b0) {
+    for (int e = 0; e < E; ++e) {
+      if (l[e] > -kInf && l[e] >= lo2 && lbin(l[e], lo2, sc2) == b0) {
         nlo = fminf(nlo, l[e]), nhi = fmaxf(nhi, l[e]);
         const int slot = atomicAdd(&s.ncand, 1);
         if (slot < kCandCap) s.cand[slot] = l[e];
@@ -245,7 +245,7 @@ RWKV7_DEV float select_gt(const float (&l)[kSmpE], float lo, float hi, float m, 
       }
     } else {
 #pragma unroll
-      for (int e = 0; e < kSmpE; ++e) {
+      for (int e = 0; e < E; ++e) {
         const uint32_t k = okey(l[e] + zero);  // + 0 keeps the value (no -0 is left)
         if (l[e] > -kInf && k >= kl && k <= kh) atomicAdd(&s.hist[(k >> sh) & dmask], wt(l[e], mo));
       }
@@ -342,14 +342,24 @@ __global__ __launch_bounds__(kSmpThreads) void sample_kernel(SampleArgs a) {
   } else {
 #pragma unroll
     for (int e = 0; e < kSmpE; ++e) l[e] = l[e] / a.temp;
-    float lo = kInf, m = -kInf;
+    float lo = kInf, m = -kInf, tmax = -kInf;
 #pragma unroll
     for (int e = 0; e < kSmpE; ++e)
-      if (l[e] > -kInf) lo = fminf(lo, l[e]), m = fmaxf(m, l[e]);
+      if (l[e] > -kInf) lo = fminf(lo, l[e]), tmax = fmaxf(tmax, l[e]);
+    m = tmax;
     block_minmax(lo, m, s);
     float thr = -kInf;  // tokens with x >= thr stay
     if (a.top_k > 0 && a.top_k < V) {  // sampling.py:56-60
-      thr = select_gt<false>(l, lo, m, m, (u64)(a.top_k - 1), s);
+      // The k-th largest value is at least the k-th largest of the threads'
+      // maxima when k threads hold values: only values from there up take part.
+      float floor_k = lo;
+      if (__syncthreads_count(tmax > -kInf) >= a.top_k) {
+        float tl = tmax > -kInf ? tmax : kInf, th = tmax;
+        block_minmax(tl, th, s);
+        const float tv[1] = {tmax};
+        floor_k = select_gt<false, 1>(tv, tl, th, m, (u64)(a.top_k - 1), s);
+      }
+      thr = select_gt<false, kSmpE>(l, floor_k, m, m, (u64)(a.top_k - 1), s);
       lo = thr;  // the smallest value top-k keeps
     }
     if (a.top_p < 1.f) {  // sampling.py:62-68
@@ -361,7 +371,7 @@ __global__ __launch_bounds__(kSmpThreads) void sample_kernel(SampleArgs a) {
         if (l[e] > -kInf) own += mass(l[e], mo);
       }
       block_excl_scan(own, z, s);
-      thr = select_gt<true>(l, lo, m, m, (u64)((double)a.top_p * (double)z), s);
+      thr = select_gt<true, kSmpE>(l, lo, m, m, (u64)((double)a.top_p * (double)z), s);
     }
     u64 own = 0, z = 0;
     {
