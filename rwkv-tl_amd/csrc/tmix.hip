@@ -262,12 +262,14 @@ template int launch_wkv7_scan<float, float, float>(const ScanArgs<float, float, 
 // end state and product to Send / Pend; wkv7_prefill_combine_kernel then
 // chains the segments and adds S_in u_t.
 // ---------------------------------------------------------------------------
-template <bool SEG>  // SEG: launched with more than one segment
+// SEG: launched with more than one segment. CH: tokens staged per chunk (16;
+// 1 for single-token steps, whose small LDS lets four workgroups share a CU).
+template <bool SEG, int CH>
 __global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p, int seg_len, int nseg) {
   // s_in[buf][vec][token][16 float4]: vec 0 w, 1 a, 2 b, 3 k, 4 r, 5 v
-  __shared__ float4 s_in[2][6][kCh][kN / 4];
-  __shared__ float s_yp[kCh][16][17];  // per-lane partial y: [step][row][lane], padded
-  __shared__ float s_up[SEG ? kCh : 1][16][17];  // the same for u (segments after the first)
+  __shared__ float4 s_in[2][6][CH][kN / 4];
+  __shared__ float s_yp[CH][16][17];  // per-lane partial y: [step][row][lane], padded
+  __shared__ float s_up[SEG ? CH : 1][16][17];  // the same for u (segments after the first)
 
   const int t = threadIdx.x;
   const int h = blockIdx.x >> 2, quarter = blockIdx.x & 3, bi = blockIdx.y;
@@ -281,8 +283,11 @@ __global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p, in
   const int64_t base = (int64_t)bi * T * C + (int64_t)h * kN;  // token 0, channel 0 of the head
   const float *vec = p.vec;
 
-  // staging: thread -> token t >> 4 of the chunk, channels 4q .. 4q+3
+  // staging: thread -> token t >> 4 of the chunk, channels 4q .. 4q+3 (the
+  // threads of tokens past CH compute a copy of the chunk's last token and
+  // store nothing)
   const int st_tok = t >> 4, q = t & 15;
+  const bool stager = st_tok < CH;
   const int ch0 = h * kN + 4 * q;
   auto ld4 = [&](const float *src) { return *reinterpret_cast<const float4 *>(src); };
   const float4 v0v = ld4(vec + RWKV7_V_V0 * C + ch0), w0v = ld4(vec + RWKV7_V_W0 * C + ch0);
@@ -328,6 +333,7 @@ __global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p, in
       a[e] = kk[e] * inv;
       b[e] = -a[e] * ag[e];
     }
+    if (!stager) return;
     s_in[buf][0][st_tok][q] = make_float4(w[0], w[1], w[2], w[3]);
     s_in[buf][1][st_tok][q] = make_float4(a[0], a[1], a[2], a[3]);
     s_in[buf][2][st_tok][q] = make_float4(b[0], b[1], b[2], b[3]);
@@ -355,11 +361,11 @@ __global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p, in
   fetch(0);
   commit(0, 0);
   __syncthreads();
-  const int nch = (Tl + kCh - 1) / kCh;
+  const int nch = (Tl + CH - 1) / CH;
   for (int c = 0; c < nch; ++c) {
     const int buf = c & 1;
-    if (c + 1 < nch) fetch((c + 1) * kCh);
-    const int steps = min(kCh, Tl - c * kCh);
+    if (c + 1 < nch) fetch((c + 1) * CH);
+    const int steps = min(CH, Tl - c * CH);
     const float *vrow = reinterpret_cast<const float *>(&s_in[buf][5][0][0]) + row;
     struct In {
       float4 w, a, b, k, r;
@@ -452,7 +458,7 @@ __global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p, in
         float y = 0.f;
 #pragma unroll
         for (int l = 0; l < 16; ++l) y += s_yp[ss][rr][l];
-        const int64_t o = base + (int64_t)(t0 + c * kCh + ss) * C + quarter * 16 + rr;
+        const int64_t o = base + (int64_t)(t0 + c * CH + ss) * C + quarter * 16 + rr;
         p.y[o] = y;
         if (SEG && tail) {
           float u = 0.f;
@@ -462,7 +468,7 @@ __global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p, in
         }
       }
     }
-    if (c + 1 < nch) commit((c + 1) * kCh, buf ^ 1);
+    if (c + 1 < nch) commit((c + 1) * CH, buf ^ 1);
     __syncthreads();
   }
   if (!SEG) {
@@ -592,10 +598,12 @@ int launch_wkv7_prefill(const PrefillScanArgs &p, hipStream_t st) {
   int seg_len;
   const int nseg = prefill_segments(p.T, p.B, p.H, &seg_len);
   if (nseg > 1 && (!p.U || !p.Send || !p.Pend)) return RWKV7_EWORKSPACE;
-  if (nseg == 1)
-    wkv7_prefill_kernel<false><<<dim3(4 * p.H, p.B, 1), 256, 0, st>>>(p, seg_len, nseg);
+  if (p.T == 1)
+    wkv7_prefill_kernel<false, 1><<<dim3(4 * p.H, p.B, 1), 256, 0, st>>>(p, seg_len, nseg);
+  else if (nseg == 1)
+    wkv7_prefill_kernel<false, kCh><<<dim3(4 * p.H, p.B, 1), 256, 0, st>>>(p, seg_len, nseg);
   else
-    wkv7_prefill_kernel<true><<<dim3(4 * p.H, p.B, nseg), 256, 0, st>>>(p, seg_len, nseg);
+    wkv7_prefill_kernel<true, kCh><<<dim3(4 * p.H, p.B, nseg), 256, 0, st>>>(p, seg_len, nseg);
   RWKV7_CHECK_LAUNCH();
   if (nseg > 1) {
     const int nblk = (seg_len + kCh - 1) / kCh;
