@@ -19,8 +19,10 @@
   read from the committed summary ``profiles/decode_mk_kernel_traffic.txt``
   (null if absent), which ``--pmc-summary`` writes from the two counter runs.
 * Extra keys of the same JSON object: decode at batch 16 (ms/step and
-  tokens/s), prefill T=128 and T=8 (ms), the roofline of the whole step as
-  the caller sees it, and the CPU baseline: the oracle's pure-torch fp32
+  tokens/s), prefill T=128 and T=8 (ms), the int8 weight-only GEMV
+  (``rwkv7_gemv_i8``) against the f16 GEMV on the head matrix (65536 x 1024;
+  average launch time over 100 launches and fraction of HBM peak for each),
+  the roofline of the whole step as the caller sees it, and the CPU baseline: the oracle's pure-torch fp32
   model (a port of the reference's ``demo/rwkv7_torch.py``) timed on this
   host's cores on a bounded sample of the same decode workload.
 
@@ -526,6 +528,33 @@ def main() -> None:
             "hbm_frac": round(b16 / (ms16 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         }
         log(f"decode B=16: {ms16:.4f} ms/step")
+        # ---- int8 weight-only GEMV vs the f16 GEMV on the head shape ----
+        # (direct C-ABI calls into a preallocated output, so the host wrapper's
+        # checks and allocation stay out of the timed launches)
+        from rwkv_tl_amd import _lib as LB
+        from rwkv_tl_amd import kernels as KO
+
+        Wh = w.head.contiguous()
+        Nh = Wh.shape[0]
+        qh, sh = KO.quantize_i8(Wh)
+        xh = torch.randn(w.C, generator=g).to(dev)
+        yh = torch.empty(Nh, dtype=torch.float32, device=dev)
+        lib, sth = LB.load(), LB.stream_handle()
+        g8 = lambda: lib.rwkv7_gemv_i8(xh.data_ptr(), qh.data_ptr(), w.C, sh.data_ptr(), yh.data_ptr(), Nh, w.C, sth)
+        g16 = lambda: lib.rwkv7_gemv_f16(xh.data_ptr(), Wh.data_ptr(), w.C, yh.data_ptr(), Nh, w.C, sth)
+        LB.check(g8(), "rwkv7_gemv_i8")
+        LB.check(g16(), "rwkv7_gemv_f16")
+        us8 = time_cuda(g8, 100) * 1e3
+        us16 = time_cuda(g16, 100) * 1e3
+        b8, b16h = Nh * w.C + 8 * Nh + 4 * w.C, 2 * Nh * w.C + 4 * Nh + 4 * w.C
+        out["gemv_i8_head"] = {
+            "shape": [Nh, w.C],
+            "i8_us": round(us8, 2),
+            "i8_hbm_frac": round(b8 / (us8 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "f16_us": round(us16, 2),
+            "f16_hbm_frac": round(b16h / (us16 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        }
+        log(f"gemv head {Nh}x{w.C}: int8 {us8:.2f} us, f16 {us16:.2f} us")
         # ---- prefill ----
         pre = {}
         for T in (8, 128):

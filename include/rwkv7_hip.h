@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define RWKV7_ABI_VERSION 3
+#define RWKV7_ABI_VERSION 4
 #define RWKV7_HEAD_SIZE 64
 
 enum {
@@ -187,6 +187,14 @@ int rwkv7_lerp(const void *x, const void *prev, const float *mu, int32_t n_mix,
  * (demo/_rwkv7_base.py:87,206,290; kernels/gemm.py:215-262 at T=1). */
 int rwkv7_gemv_f16(const float *x, const void *W, int64_t ldw, float *y,
                    int32_t N, int32_t K, void *stream);
+
+/* y[n] = scale[n] * sum_k x[k] Q[n, k]: Q int8 [N, K] (row stride ldq bytes,
+ * ldq % 16 == 0, Q and x 16-byte aligned), scale f32 [N], x and y f32.
+ * 16 <= K <= 8192, K % 16 == 0. Weight-only int8 GEMV with the dequant fused
+ * into the kernel: the quantisation step the reference plans for its
+ * hand-written GEMV (TODO.md:58-63), which has no kernel there yet. */
+int rwkv7_gemv_i8(const float *x, const void *Q, int64_t ldq, const float *scale,
+                  float *y, int32_t N, int32_t K, void *stream);
 
 /* Y = epi(A W^T): A f16 [M, K] (row stride lda), W f16 [N, K] (ldw), fp32
  * accumulation. epi: 0 store f32, 1 store f16, 2 relu^2 store f16,

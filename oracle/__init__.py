@@ -10,4 +10,6 @@ CPU baseline). The HIP library and its Python host code never import it.
 follows and the tests that pin it. ``oracle.sampling_ref`` restates the
 reference's token sampling (``demo/sampling.py``) and the sampling kernel's
 counter-based draw (Philox4x32-10), as the checker of ``rwkv7_sample``.
+``oracle.quant_ref`` is the float64 checker of the int8 weight-only GEMV
+(``rwkv7_gemv_i8``) and of the per-row int8 quantisation it reads.
 """

@@ -151,6 +151,34 @@ def gemv(x: Tensor, W: Tensor) -> Tensor:
     return y
 
 
+def quantize_i8(W: Tensor) -> tuple[Tensor, Tensor]:
+    """Symmetric per-row int8 weights for ``gemv_i8``: ``scale = max|W[n]| / 127``
+    (fp32; 0 for an all-zero row), ``q = round_half_even(W / scale)`` in
+    [-127, 127], so ``|W - scale * q| <= scale / 2``. A weight-format step
+    (torch on W's device), like the checkpoint dtype conversion."""
+    _need(W.dim() == 2 and W.is_floating_point(), "W must be a floating [N, K] matrix")
+    w = W.float()
+    scale = w.abs().amax(dim=1) / 127.0
+    q = torch.round(w / torch.where(scale > 0, scale, torch.ones_like(scale))[:, None]).clamp_(-127, 127)
+    return q.to(torch.int8).contiguous(), scale.contiguous()
+
+
+def gemv_i8(x: Tensor, q: Tensor, scale: Tensor) -> Tensor:
+    """``y[n] = scale[n] * sum_k x[k] q[n, k]`` for int8 q [N, K], f32 scale [N]
+    and f32 x [K] (K % 16 == 0, K <= 8192); returns f32 [N]."""
+    _dev(x, q, scale)
+    _need(q.dtype == torch.int8 and q.dim() == 2 and q.is_contiguous(), "q must be contiguous int8 [N, K]")
+    N, Kd = q.shape
+    _need(scale.dtype == torch.float32 and scale.shape == (N,) and scale.is_contiguous(), "scale must be f32 [N]")
+    _need(x.dtype == torch.float32 and x.shape == (Kd,) and x.is_contiguous(), "x must be contiguous f32 [K]")
+    y = torch.empty(N, dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    rc = lib.rwkv7_gemv_i8(x.data_ptr(), q.data_ptr(), Kd, scale.data_ptr(), y.data_ptr(), N, Kd,
+                           _lib.stream_handle())
+    _lib.check(rc, "rwkv7_gemv_i8")
+    return y
+
+
 def gemm(A: Tensor, W: Tensor, epi: str = "f32", out: Tensor | None = None) -> Tensor:
     """``epi(A W^T)`` for f16 A [M, K], W [N, K]; ``epi`` in f32/f16/relu2/add.
 
