@@ -313,3 +313,29 @@ def test_operator_oracle_closed_forms():
     torch.testing.assert_close(ao, torch.sigmoid(a0_))
     torch.testing.assert_close(ko, k * torch.sigmoid(a0_))
     torch.testing.assert_close(go, z)
+
+
+@pytest.mark.slow
+def test_c4_ref16_fixture_matches_oracle(golden_dir):
+    """The committed C4 fp16-oracle fixture (tests/golden/make_c4_ref16.py) is
+    the oracle's own output: recompute the 1x8 case here and compare the stored
+    entries exactly; the stored indices include the 64 largest logits."""
+    from safetensors.torch import load_file
+
+    from rwkv_tl_amd.weight import RWKV7Weight
+
+    fx = load_file(str(golden_dir / "c4_ref16.safetensors"))
+    sd = make_random_state_dict("0.4b", seed=0, dtype=torch.float16)
+    w = RWKV7Weight.from_state_dict(sd, device="cpu", dtype=torch.float16)
+    W16 = R.Weights.from_emb(sd, w.emb, torch.float16)
+    V = w.head.shape[0]
+    g = torch.Generator().manual_seed(1000 * 1 + 8)
+    prompt = torch.randint(0, V, (1, 8), generator=g)
+    toks = torch.randint(0, V, (64, 1), generator=g)
+    assert fx["1x8_row0_prompt_ends"].tolist() == [int(prompt[0, 0]), int(prompt[0, -1])]
+    st = R.new_state(w.L, w.C, dtype=torch.float16)
+    R.prefill(W16, prompt[0], st)
+    lg, _ = R.decode(W16, toks[0, :1], st)
+    idx = fx["1x8_row0_idx"]
+    assert torch.equal(lg.float()[idx], fx["1x8_row0_val"])
+    assert set(torch.topk(lg.float(), 64).indices.tolist()) == set(idx[:64].tolist())
