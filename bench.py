@@ -1,13 +1,15 @@
-"""Benchmark: RWKV7-0.4B fp16 decode (B=1, HIP-graph replay) on one MI355X.
+"""Benchmark: RWKV7-0.4B fp16 decode (B=1) and prefill on one MI355X.
 
 ``python bench.py [--gpus 1] [--steps K] [--warmup W]`` prints ONE JSON line.
 
 * A step is one decode token of the 0.4B model (24 layers, C=1024, H=16,
   F=4096, V=65536, LoRA ranks 64/64/32/128), fp16 weights from seed 0, batch
-  1, through ``HIPGraph`` replay, token ids drawn uniformly from a seeded
-  generator and resident on the device before timing starts. ``value`` is
-  ms/token over exactly K timed steps (HIP events on the replay stream,
-  bracketed by device synchronisation).
+  1, called through the ``HIPGraph`` wrapper (which launches a batch-1 step
+  directly: it is one persistent kernel, so a graph replay would save
+  nothing), token ids drawn uniformly from a seeded generator and resident on
+  the device before timing starts. ``value`` is ms/token over exactly K timed
+  steps (HIP events on the launch stream, bracketed by device
+  synchronisation).
 * ``roofline`` is that of the dominant kernel, the persistent decode kernel
   (``decode_mk_kernel``, the whole batch-1 step in one launch): algorithmic
   bytes per launch (fp16 weights and head read once, fp32 wkv state and f16
@@ -19,7 +21,9 @@
   read from the committed summary ``profiles/decode_mk_kernel_traffic.txt``
   (null if absent), which ``--pmc-summary`` writes from the two counter runs.
 * Extra keys of the same JSON object: decode at batch 16 (ms/step and
-  tokens/s), prefill T=128 and T=8 (ms), the int8 weight-only GEMV
+  tokens/s), prefill T=128 and T=8 as flat keys ``prefill_T128_ms``,
+  ``prefill_T128_hbm_frac``, ``prefill_T128_mfma_frac`` (and the same for
+  T8; prefill through HIP-graph replay for T <= 64), the int8 weight-only GEMV
   (``rwkv7_gemv_i8``) against the f16 GEMV on the head matrix (65536 x 1024;
   average launch time over 100 launches and fraction of HBM peak for each),
   the roofline of the whole step as the caller sees it, and the CPU baseline: the oracle's pure-torch fp32
@@ -484,7 +488,7 @@ def main() -> None:
         "dtype": "f16",
         "data": "synthetic: seeded random-init weights (N(0,0.02)) and uniform random token ids",
         "config": {
-            "workload": "RWKV7-0.4B decode B=1 through HIPGraph (config 3; one persistent kernel per token)",
+            "workload": "RWKV7-0.4B decode B=1 (config 3): one persistent kernel launch per token",
             "layers": shape.n_layer,
             "n_embd": shape.n_embd,
             "vocab": V,
@@ -574,8 +578,11 @@ def main() -> None:
                 "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 5),
             }
             log(f"prefill T={T}: {ms:.4f} ms")
-        out["prefill"] = pre
-        out["prefill_T128_ms"] = pre["T128"]["ms"]
+        for k, v in pre.items():
+            out[f"prefill_{k}_ms"] = v["ms"]
+            out[f"prefill_{k}_hbm_frac"] = v["hbm_frac"]
+            out[f"prefill_{k}_mfma_frac"] = v["mfma_frac"]
+            out[f"prefill_{k}_tokens_per_s"] = v["tokens_per_s"]
 
     if args.calib_copy:
         calib_copy()

@@ -4,8 +4,8 @@
  * Every entry point takes plain device pointers, sizes and a HIP stream handle
  * (hipStream_t passed as void*; NULL is the legacy default stream). Nothing in
  * the library allocates or frees device memory, creates streams or events, or
- * synchronises the host: the caller owns every buffer, so the calls can be
- * captured in a HIP graph. Each function returns 0 on success or one of the
+ * synchronises the host (except rwkv7_workspace_errors, a status query): the
+ * caller owns every buffer, so the calls can be captured in a HIP graph. Each function returns 0 on success or one of the
  * RWKV7_E* codes below (argument errors are detected on the host before any
  * launch; launch failures return RWKV7_ELAUNCH).
  *
@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define RWKV7_ABI_VERSION 4
+#define RWKV7_ABI_VERSION 5
 #define RWKV7_HEAD_SIZE 64
 
 enum {
@@ -98,7 +98,12 @@ typedef struct rwkv7_model {
   const void *ln_out; /* f32 [2, C]: weight, bias */
   const void *layers_frag; /* optional: L fragment arenas */
   const void *head_frag;   /* optional: head in fragment order */
+  uint32_t flags;          /* RWKV7_MODEL_* path choices, 0 for the defaults */
 } rwkv7_model;
+
+/* rwkv7_model.flags: run batch-1 decode as one launch per stage (the
+ * multi-launch GEMV path) instead of the single persistent kernel. */
+#define RWKV7_MODEL_MULTI_LAUNCH_DECODE 1u
 
 /* Recurrent state of `batch` independent sequences, layer-major arenas
  * (src/rwkv_tl/state.py:35-44 plus a leading batch dimension):
@@ -126,10 +131,20 @@ int rwkv7_layer_layout_get(const rwkv7_dims *dims, rwkv7_layer_layout *out);
 /* Bytes of scratch that rwkv7_decode / rwkv7_prefill need for `batch`
  * sequences of `seq_len` tokens (seq_len 1 for decode). The workspace must be
  * zero-filled once after allocation: its first region holds the hand-off words
- * of the persistent decode kernel (32-bit word 8, bytes 32..35, counts waits
- * that timed out) and is kept consistent by every later call. One workspace
- * must not be used by two calls that can run concurrently. */
+ * of the persistent decode kernel and is kept consistent by every later call.
+ * One workspace must not be used by two calls that can run concurrently. */
 int64_t rwkv7_workspace_bytes(const rwkv7_dims *dims, int32_t batch, int32_t seq_len);
+
+/* Number of persistent-decode launches on `workspace` that were aborted
+ * (32-bit word at byte 32 of the workspace, cumulative; the caller may zero
+ * it). Synchronises `stream` first. A launch aborts when one of its grid-wide
+ * hand-offs waits longer than about a second (its workgroups were not all
+ * resident, e.g. beside another process's kernels) or when its abort word was
+ * set before it started; it then writes NaN into the logits of every row whose
+ * inputs did not arrive and stops writing state, so the State holds the layers
+ * completed before the failure. No counterpart in the reference (its CUDA
+ * graphs have no grid-wide waits). */
+int rwkv7_workspace_errors(const void *workspace, int64_t workspace_bytes, uint32_t *count, void *stream);
 
 /* ---- model steps ------------------------------------------------------ */
 
@@ -142,12 +157,12 @@ int rwkv7_decode(const rwkv7_model *model, const rwkv7_state *state,
                  int64_t workspace_bytes, void *stream);
 
 /* Number of kernel launches one rwkv7_decode call makes for `batch`
- * sequences (with_logits: whether logits are requested), or -1 for
+ * sequences of `model` (with_logits: whether logits are requested), or -1 for
  * unsupported dims. 1 means the step is one persistent kernel, so a graph
  * replay gains nothing over a direct call. The reference has no counterpart:
  * its CUDAGraph wrapper (demo/cuda_graph.py:61-235) always captures; this
  * lets the HIP-graph wrapper skip capture where it cannot help. */
-int rwkv7_decode_launches(const rwkv7_dims *dims, int32_t batch, int32_t with_logits);
+int rwkv7_decode_launches(const rwkv7_model *model, int32_t batch, int32_t with_logits);
 
 /* Prefill seq_len tokens per sequence: tokens i64 [B, T] (device). Updates
  * state in place and produces no logits, like RWKV7Base.prefill

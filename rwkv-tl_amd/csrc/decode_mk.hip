@@ -36,13 +36,19 @@
 //
 // Every wait is bounded: past ~1 s a waiting wave raises a per-launch abort
 // word and gives up, every other waiting wave then gives up within a few polls,
-// and barriers never wait on memory, so a launch always terminates (its output
-// is then garbage and an error counter is set). The grid must be resident all
-// at once: one 512-thread workgroup per CU, grid = CU count.
+// and barriers never wait on memory, so a launch always terminates. A
+// workgroup that gave up (or found the launch aborted) publishes nothing
+// more, writes no more state, and writes NaN logits; the launch's first worker
+// counts the aborted launch in an error word that the host reads
+// (rwkv7_workspace_errors). State layers updated before the failure stay
+// updated. The grid must be resident all at once: one 512-thread workgroup
+// per CU, grid = CU count; the host checks the occupancy for this kernel
+// before choosing it.
 //
 // Reference counterparts: RWKV7Base.decode / make_TMIX / make_CMIX
 // (demo/_rwkv7_base.py:74-87,153-206,285-290) and the captured decode graph
 // (demo/cuda_graph.py:111-128).
+#include <atomic>
 #include <type_traits>
 
 #include "rwkv7_kernels.h"
@@ -65,8 +71,12 @@ constexpr int kXProbe = 1024;    // probe stride of the x vectors
 static_assert(kRep < 64, "lanes 0..kRep of a wave publish a value and its state");
 
 // 32-bit sync words at the start of the exchange region (byte offsets 0, 16
-// and 32): launch epoch, abort word, count of waits that timed out
+// and 32): launch epoch, abort word (epoch + 1 while the launch with that
+// epoch is aborted), count of aborted launches. Then kMaxG start words (one per
+// workgroup: epoch + 1 once it started), then the hand-off vectors.
 enum { SY_EPOCH = 0, SY_ABORT = 4, SY_ERRORS = 8 };
+constexpr int kSyncBytes = 256;
+constexpr int kMaxG = 1024;
 
 // s_waitcnt vmcnt(0), leaving the export and LDS counters alone
 RWKV7_DEV void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
@@ -97,14 +107,19 @@ RWKV7_DEV void publish(uint64_t *p, unsigned tag, float v) {
 // first launch on a zeroed workspace uses tags 1..nph, never 0.
 struct MkCtx {
   unsigned *sync;
+  unsigned *fail;  // LDS word: nonzero once a wave of this workgroup gave up a wait
   unsigned epoch;
   unsigned tag0;  // epoch * nph + 1
   int pskew;      // probe offset of this workgroup (even)
   RWKV7_DEV unsigned tag(int phase) const { return tag0 + (unsigned)phase; }
   RWKV7_DEV bool aborted() const { return ld_u32(sync + SY_ABORT) == epoch + 1u; }
+  RWKV7_DEV bool failed() const {
+    return __hip_atomic_load(fail, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u;
+  }
+  RWKV7_DEV void give_up() const { __hip_atomic_store(fail, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
   RWKV7_DEV void abort() const {
     st_u32(sync + SY_ABORT, epoch + 1u);
-    __hip_atomic_fetch_add(sync + SY_ERRORS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    give_up();
   }
 };
 
@@ -123,6 +138,7 @@ struct MkArgs {
   // and F words
   uint64_t *x_ex, *proj_ex, *core_ex, *hid_ex;
   unsigned *sync;
+  unsigned *started;  // [kMaxG] start words
 };
 
 // Row ranges and roles, computed identically by every wave of a workgroup.
@@ -161,11 +177,13 @@ struct MkLds {
   float *hid;     // [F]  P5 input
   unsigned *pubs; // count of math-wave publish steps (the comm waves' start signal)
   unsigned *xflag; // tag of the x vector the comm wave's probe saw arriving (a start hint)
+  unsigned *fail;  // a wave of this workgroup gave up a wait (see MkCtx)
+  unsigned *ep;    // the launch epoch, read once by thread 0
   float *xst;     // [2][kW][2] (mean, M2) of each wave's slice of x (P1 input), x' (P4 input)
 };
 
 RWKV7_DEV_HOST_INLINE int64_t mk_lds_floats(int C, int F, int SR) {
-  return (int64_t)10 * C + (192 + SR) + 5 * 64 + 7 * 64 + F + 4 + 4 * kW;
+  return (int64_t)10 * C + (192 + SR) + 5 * 64 + 7 * 64 + F + 8 + 4 * kW;
 }
 
 RWKV7_DEV MkLds mk_lds(float *smem, int C, int F, int SR) {
@@ -183,7 +201,9 @@ RWKV7_DEV MkLds mk_lds(float *smem, int C, int F, int SR) {
   s.core = s.gsum + 5 * 64;
   s.pubs = reinterpret_cast<unsigned *>(s.core + 7 * 64);
   s.xflag = s.pubs + 1;
-  s.xst = s.core + 7 * 64 + 4;
+  s.fail = s.pubs + 2;
+  s.ep = s.pubs + 3;
+  s.xst = s.core + 7 * 64 + 8;
   return s;
 }
 
@@ -314,9 +334,14 @@ struct SpinBound {
   const MkCtx &cx;
   int spins = 0;
   RWKV7_DEV explicit SpinBound(const MkCtx &c) : cx(c) {}
-  RWKV7_DEV bool keep_waiting() {  // bounded: false once the launch is aborted
+  // bounded: false once this workgroup gave up or the launch is aborted
+  RWKV7_DEV bool keep_waiting() {
     ++spins;
-    if ((spins & 1023) == 0 && cx.aborted()) return false;
+    if (cx.failed()) return false;
+    if ((spins & 1023) == 0 && cx.aborted()) {
+      cx.give_up();
+      return false;
+    }
     if (spins > kSpinLimit) {
       cx.abort();
       return false;
@@ -416,14 +441,10 @@ struct Ident {
 // Waits (LDS spin, bounded by the launch's abort word) until the math waves
 // of this workgroup have completed `target` publish steps.
 RWKV7_DEV void wait_local(const MkCtx &cx, const unsigned *pubs, unsigned target) {
-  int spins = 0;
+  SpinBound sb(cx);
   while (__hip_atomic_load(pubs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
     __builtin_amdgcn_s_sleep(1);
-    if ((++spins & 1023) == 0 && cx.aborted()) break;
-    if (spins > kSpinLimit) {
-      cx.abort();
-      break;
-    }
+    if (!sb.keep_waiting()) break;
   }
 }
 
@@ -714,7 +735,9 @@ RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
       }
     }
     __syncthreads();  // B2c
-    if (wv == 0) {
+    // inputs of this layer arrived (a wave that gave up set fail before HA)
+    const bool ok = !cx.failed();
+    if (wv == 0 && ok) {
       // GroupNorm of the head from the 4 waves' (mean, M2) over 16 rows each
       float mean = 0.f;
 #pragma unroll
@@ -734,7 +757,7 @@ RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
 #pragma unroll
       for (int rp = 0; rp < kRep; ++rp) publish(a.core_ex + (int64_t)rp * C + g * kN + lane, cx.tag(5 * l + 1), out);
     }
-    if (mt < 4 * kN) {
+    if (mt < 4 * kN && ok) {
       float4 *Sp = reinterpret_cast<float4 *>(a.rnn + (((int64_t)l * H + g) * kN + row) * kN + j0);
 #pragma unroll
       for (int e = 0; e < 4; ++e) Sp[e] = make_float4(Sv[4 * e], Sv[4 * e + 1], Sv[4 * e + 2], Sv[4 * e + 3]);
@@ -920,13 +943,14 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     }
     __syncthreads();  // B1
     {
+      const bool ok = !cx.failed();
       const unsigned tg = cx.tag(ph);
 #pragma unroll
       for (int i = 0; i < RM; ++i) {
         const int r = m.p1a + wv + kMW * i;
         if (r < m.p1b) {
           const float d = row_dot<CPL>(w1[i], s.mix + (m.seg_of(r) - m.seg0) * C, nchC);
-          if (lane < kRep) publish(a.proj_ex + (int64_t)lane * (3 * C + m.SR) + r, tg, d);
+          if (lane < kRep && ok) publish(a.proj_ex + (int64_t)lane * (3 * C + m.SR) + r, tg, d);
         }
       }
     }
@@ -944,7 +968,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     wait_vm0();
     // ---------------- P3: o-projection + residual -----------------------------
     refresh();
-    if (wv < m.nown) {
+    if (wv < m.nown && !cx.failed()) {
       const float d = row_dot<CPL>(w3, s.core_in, nchC);
       xown += d;
       const int c = m.owa + wv;
@@ -978,13 +1002,14 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     }
     __syncthreads();  // B4
     {
+      const bool ok = !cx.failed();
       const unsigned tg = cx.tag(ph + 3);
 #pragma unroll
       for (int i = 0; i < RM; ++i) {
         const int r = m.p4a + wv + kMW * i;
         if (r < m.p4b) {
           const float q = fmaxf(row_dot<CPL>(w4[i], s.mix4, nchC), 0.f);
-          if (lane < kRep) publish(a.hid_ex + (int64_t)lane * F + r, tg, q * q);
+          if (lane < kRep && ok) publish(a.hid_ex + (int64_t)lane * F + r, tg, q * q);
         }
       }
     }
@@ -1001,7 +1026,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     __syncthreads();  // A5
     // ---------------- P5: FFN value + residual --------------------------------
     refresh();
-    if (wv < m.nown) {
+    if (wv < m.nown && !cx.failed()) {
       const float d = row_dot<NC5>(w5, s.hid, nchF);
       xown += d;
       const int c = m.owa + wv;
@@ -1014,6 +1039,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
 
   // ---------------- head: ln_out + logits ---------------------------------------
   refresh();
+  const bool glob_abort = cx.aborted();  // issued before the head rows, used after them
   ld_vec(hlw, a.ln_out);
   ld_vec(hlb, a.ln_out + C);
 #pragma unroll
@@ -1028,6 +1054,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     }
   }
   __syncthreads();  // BH
+  const bool bad = cx.failed() || glob_abort;
   float xr[CPL][8];
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
@@ -1049,7 +1076,8 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     }
     if (b + kHRing < NHB) pre_head(b + kHRing, cur);
   }
-  if (hr0 + lane < hr1) a.logits[hr0 + lane] = f2h(out);
+  // NaN logits if this workgroup's input did not arrive or the launch was aborted
+  if (hr0 + lane < hr1) a.logits[hr0 + lane] = bad ? (uint16_t)0x7E00u : f2h(out);
 }
 
 // One workgroup per CU by construction (2 waves per SIMD): telling the
@@ -1089,16 +1117,26 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   m.nseg = m.p1b > m.p1a ? m.seg_of(m.p1b - 1) - m.seg0 + 1 : 0;
   const MkLds s = mk_lds(smem, m.C, m.F, m.SR);
 
+  // One thread reads the epoch and the abort word, so every wave of the
+  // workgroup takes the same view of the launch; a launch whose abort word is
+  // already set for its epoch does no work (every wait gives up at once).
+  if (threadIdx.x == 0) {
+    const unsigned e = ld_u32(a.sync + SY_EPOCH);
+    const unsigned ab = ld_u32(a.sync + SY_ABORT);
+    *s.pubs = 0u;
+    *s.xflag = 0u;
+    *s.ep = e;
+    *s.fail = ab == e + 1u ? 1u : 0u;
+    st_u32(a.started + m.g, e + 1u);
+  }
+  __syncthreads();
   MkCtx cx;
   cx.sync = a.sync;
-  cx.epoch = ld_u32(a.sync + SY_EPOCH);
+  cx.fail = s.fail;
+  cx.epoch = __builtin_amdgcn_readfirstlane(*s.ep);
   cx.tag0 = cx.epoch * (5u * m.L + 1u) + 1u;
   cx.pskew = (m.g / kRep) * 34;
 
-  if (threadIdx.x == 0) {  // ordered before any use by the first barrier
-    *s.pubs = 0u;
-    *s.xflag = 0u;
-  }
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (m.head) {
     if (wv >= kMW) comm_head(a, m, s, cx);
@@ -1107,10 +1145,20 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     if (wv >= kMW) comm_worker<NC5 / 2>(a, m, s, cx);
     else math_worker<CPL, RM, NC5, VPL, NHB>(a, m, s, cx, wv);
   }
-  // A worker ends only after every workgroup has published (its logits need
-  // the last layer's x, which needs every worker's P5 and every head's core),
-  // and every workgroup read the epoch before its first publish.
-  if (m.g == m.H && threadIdx.x == 0) st_u32(a.sync + SY_EPOCH, cx.epoch + 1u);
+  // The next launch's epoch. In a launch that completed, this worker ends only
+  // after every workgroup has published (its logits need the last layer's x,
+  // which needs every worker's P5 and every head's core), so every workgroup
+  // read the epoch already. An aborted launch is counted, and the epoch is
+  // advanced only once every workgroup recorded its start (bounded wait).
+  if (m.g == m.H && threadIdx.x == 0) {
+    if (cx.aborted()) {
+      __hip_atomic_fetch_add(a.sync + SY_ERRORS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      int spins = 0;
+      for (int g = 0; g < m.G; ++g)
+        while (ld_u32(a.started + g) != cx.epoch + 1u && ++spins < kSpinLimit) __builtin_amdgcn_s_sleep(1);
+    }
+    st_u32(a.sync + SY_EPOCH, cx.epoch + 1u);
+  }
 }
 
 // ---- host side --------------------------------------------------------------
@@ -1121,25 +1169,62 @@ constexpr int kCPL = 2, kRM = 3, kNC5 = 8, kVPL = 3, kNL2 = 8, kNHB = 10;
 
 static int cdiv(int a, int b) { return (a + b - 1) / b; }
 
-static int g_cus = 0;
+// Per-device facts, filled on first use with that device current: the CU
+// count, the largest dynamic LDS size already allowed for the kernel, and
+// whether a grid of one workgroup per CU with a given LDS size fits at once.
+constexpr int kMaxDevices = 64;
+struct MkDevice {
+  std::atomic<int> cus{0};
+  std::atomic<int64_t> lds_allowed{0};
+  std::atomic<int64_t> resident_lds{0};  // largest LDS size found co-resident
+};
+static MkDevice g_mk_dev[kMaxDevices];
+
+static MkDevice *mk_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  return &g_mk_dev[dev];
+}
 
 int mk_cus() {
-  if (g_cus == 0) {
+  MkDevice *d = mk_device();
+  if (!d) return 0;
+  int n = d->cus.load(std::memory_order_relaxed);
+  if (n == 0) {
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 0;
     hipDeviceProp_t p;
-    if (hipGetDeviceProperties(&p, dev) != hipSuccess) return 0;
-    g_cus = p.multiProcessorCount;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&p, dev) != hipSuccess) return 0;
+    n = p.multiProcessorCount;
+    d->cus.store(n, std::memory_order_relaxed);
   }
-  return g_cus;
+  return n;
 }
 
 static int64_t mk_lds_bytes(int C, int F, int SR) { return mk_lds_floats(C, F, SR) * 4; }
 
-// Exchange region: sync words, then x (kRep x C), proj (3C+SR), core
-// (kRep x C), hid (kRep x F) as u64.
+// Exchange region: sync words, start words, then x (kRep x C), proj (3C+SR),
+// core (kRep x C), hid (kRep x F) as u64.
 int64_t mk_exchange_bytes(int C, int F, int SR) {
-  return 256 + (int64_t)(kRep * C + kRep * (3 * C + SR) + kRep * C + kRep * F) * 8;
+  return kSyncBytes + 4 * kMaxG + (int64_t)(kRep * C + kRep * (3 * C + SR) + kRep * C + kRep * F) * 8;
+}
+
+// Allows the kernel its dynamic LDS on the current device and checks that a
+// grid of one workgroup per CU can be resident at once (the occupancy of this
+// kernel instance with that LDS is at least one workgroup per CU).
+static bool mk_prepare(int64_t lds) {
+  MkDevice *d = mk_device();
+  if (!d) return false;
+  const void *fn = (const void *)RWKV7_MK_INSTANCE;
+  if (lds > d->lds_allowed.load(std::memory_order_relaxed)) {
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) return false;
+    d->lds_allowed.store(lds, std::memory_order_relaxed);
+  }
+  if (lds <= d->resident_lds.load(std::memory_order_relaxed)) return true;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kT, (size_t)lds) != hipSuccess || per_cu < 1)
+    return false;
+  d->resident_lds.store(lds, std::memory_order_relaxed);
+  return true;
 }
 
 bool mk_supported(const rwkv7_dims &d, int G) {
@@ -1171,6 +1256,7 @@ bool mk_supported(const rwkv7_dims &d, int G) {
   const int hrows = cdiv(cdiv(V, Gw), kMW);
   if (hrows > kHB * kNHB || hrows > 64) return false;
   // P1 keeps the mixed input of every row segment a worker touches (<= 4)
+  if (G > kMaxG) return false;
   const int e[6] = {C, 2 * C, 3 * C, 3 * C + d.rank_v, 3 * C + d.rank_v + d.rank_w,
                     3 * C + d.rank_v + d.rank_w + d.rank_a};
   auto seg = [&](int r) {
@@ -1185,13 +1271,20 @@ bool mk_supported(const rwkv7_dims &d, int G) {
   return mk_lds_bytes(C, F, SR) <= 160 * 1024;
 }
 
+bool mk_usable(const rwkv7_dims &d) {
+  const int G = mk_cus();
+  if (G < 1 || !mk_supported(d, G)) return false;
+  const int SR = d.rank_w + d.rank_a + d.rank_v + d.rank_g;
+  return mk_prepare(mk_lds_bytes(d.n_embd, d.n_ffn, SR));
+}
+
 int launch_decode_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const rwkv7_state &s,
                      const int64_t *tok, void *logits, char *xreg, hipStream_t st) {
   const rwkv7_dims &d = m.dims;
   const int SR = d.rank_w + d.rank_a + d.rank_v + d.rank_g;
   const int G = mk_cus();
   const int C = d.n_embd, F = d.n_ffn;
-  if (!mk_supported(d, G)) return RWKV7_ESHAPE;
+  if (!mk_usable(d)) return RWKV7_ESHAPE;
   MkArgs a;
   a.layers = static_cast<const char *>(m.layers);
   a.lbytes = lay.bytes;
@@ -1219,19 +1312,13 @@ int launch_decode_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const 
   a.tok = tok;
   a.logits = static_cast<uint16_t *>(logits);
   a.sync = reinterpret_cast<unsigned *>(xreg);
-  uint64_t *ex = reinterpret_cast<uint64_t *>(xreg + 256);
+  a.started = reinterpret_cast<unsigned *>(xreg + kSyncBytes);
+  uint64_t *ex = reinterpret_cast<uint64_t *>(xreg + kSyncBytes + 4 * kMaxG);
   a.x_ex = ex;
   a.proj_ex = a.x_ex + (int64_t)kRep * C;
   a.core_ex = a.proj_ex + (int64_t)kRep * (3 * C + SR);
   a.hid_ex = a.core_ex + (int64_t)kRep * C;
   const int64_t lds = mk_lds_bytes(C, F, SR);
-  const void *fn = (const void *)RWKV7_MK_INSTANCE;
-  static int64_t lds_set = 0;  // largest dynamic LDS size already allowed
-  if (lds > lds_set) {
-    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-      return RWKV7_ELAUNCH;
-    lds_set = lds;
-  }
   RWKV7_MK_INSTANCE<<<G, kT, lds, st>>>(a);
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;

@@ -137,10 +137,10 @@ static int64_t batch_ws(const rwkv7_dims &d, int64_t B, int64_t T, char *base, B
   t.yg = reinterpret_cast<uint16_t *>(take(M * C * 2));
   t.hid = reinterpret_cast<uint16_t *>(take(M * F * 2));
   t.headin = reinterpret_cast<uint16_t *>(take(B * C * 2));
-  const int cus = mk_cus();
-  t.part = reinterpret_cast<float *>(take(gemm_ws_bytes((int)(M > B ? M : B), cus > 0 ? cus : 256)));
+  const int cus = mk_cus() > 0 ? mk_cus() : 256;
+  t.part = reinterpret_cast<float *>(take(gemm_ws_bytes((int)(M > B ? M : B), cus)));
   int seg_len;
-  const int64_t nseg = prefill_segments((int)T, (int)B, d.n_head, &seg_len);
+  const int64_t nseg = prefill_segments((int)T, (int)B, d.n_head, cus, &seg_len);
   t.U = t.Send = t.Pend = nullptr;
   if (nseg > 1) {
     const int64_t slab = nseg * B * d.n_head * (int64_t)RWKV7_HEAD_SIZE * RWKV7_HEAD_SIZE * 4;
@@ -364,13 +364,12 @@ static int check_model_state(const rwkv7_model *m, const rwkv7_state *s) {
 }
 
 // The one-launch persistent kernel serves batch-1 steps that produce logits,
-// for the sizes it was compiled for; RWKV7_DECODE_PATH=kernels forces the
-// multi-launch path (used by the tests that compare the two).
-static bool use_persistent_decode(const rwkv7_dims &d, int batch, bool logits) {
-  if (batch != 1 || !logits) return false;
-  const char *path = getenv("RWKV7_DECODE_PATH");
-  if (path && strcmp(path, "kernels") == 0) return false;
-  return mk_supported(d, mk_cus());
+// for the sizes it was compiled for and when its grid fits on the device at
+// once; the model flag RWKV7_MODEL_MULTI_LAUNCH_DECODE selects the
+// multi-launch path instead.
+static bool use_persistent_decode(const rwkv7_dims &d, uint32_t flags, int batch, bool logits) {
+  if (batch != 1 || !logits || (flags & RWKV7_MODEL_MULTI_LAUNCH_DECODE)) return false;
+  return mk_usable(d);
 }
 
 }  // namespace rwkv7
@@ -406,9 +405,10 @@ int64_t rwkv7_workspace_bytes(const rwkv7_dims *dims, int32_t batch, int32_t seq
   return a > b ? a : b;
 }
 
-int rwkv7_decode_launches(const rwkv7_dims *dims, int32_t batch, int32_t with_logits) {
-  if (check_dims(dims) != RWKV7_OK || batch < 1) return -1;
-  if (use_persistent_decode(*dims, batch, with_logits != 0)) return 1;
+int rwkv7_decode_launches(const rwkv7_model *model, int32_t batch, int32_t with_logits) {
+  if (!model || check_dims(&model->dims) != RWKV7_OK || batch < 1) return -1;
+  const rwkv7_dims *dims = &model->dims;
+  if (use_persistent_decode(*dims, model->flags, batch, with_logits != 0)) return 1;
   // decode_one: embed, 6 per layer, head GEMV; run_batched: embed, 10 per
   // layer, final LayerNorm and head GEMM
   if (batch == 1) return 1 + 6 * dims->n_layer + (with_logits ? 1 : 0);
@@ -422,7 +422,7 @@ int rwkv7_decode(const rwkv7_model *model, const rwkv7_state *state, const int64
   if (workspace_bytes < rwkv7_workspace_bytes(&model->dims, state->batch, 1)) return RWKV7_EWORKSPACE;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (state->batch == 1) {
-    if (use_persistent_decode(model->dims, 1, logits != nullptr)) {
+    if (use_persistent_decode(model->dims, model->flags, 1, logits != nullptr)) {
       rwkv7_layer_layout lay;
       layout_of(model->dims, &lay);
       return launch_decode_mk(*model, lay, *state, tokens, logits, static_cast<char *>(workspace), st);
@@ -430,6 +430,18 @@ int rwkv7_decode(const rwkv7_model *model, const rwkv7_state *state, const int64
     return decode_one(*model, *state, tokens, logits, static_cast<char *>(workspace), st);
   }
   return run_batched(*model, *state, tokens, 1, logits, static_cast<char *>(workspace), st);
+}
+
+int rwkv7_workspace_errors(const void *workspace, int64_t workspace_bytes, uint32_t *count, void *stream) {
+  if (!workspace || !count) return RWKV7_EINVAL;
+  if (workspace_bytes < 64) return RWKV7_EWORKSPACE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (hipStreamSynchronize(st) != hipSuccess) return RWKV7_ELAUNCH;
+  uint32_t v = 0;
+  if (hipMemcpy(&v, static_cast<const char *>(workspace) + 32, 4, hipMemcpyDeviceToHost) != hipSuccess)
+    return RWKV7_ELAUNCH;
+  *count = v;
+  return RWKV7_OK;
 }
 
 int rwkv7_prefill(const rwkv7_model *model, const rwkv7_state *state, const int64_t *tokens, int32_t seq_len,

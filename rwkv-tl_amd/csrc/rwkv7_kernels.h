@@ -77,7 +77,7 @@ struct PrefillScanArgs {
   int B, T, H, C, M, layer0;
   float *U, *Send, *Pend;
 };
-int prefill_segments(int T, int B, int H, int *seg_len);
+int prefill_segments(int T, int B, int H, int cus, int *seg_len);
 int launch_wkv7_prefill(const PrefillScanArgs &p, hipStream_t st);
 
 struct GnGateArgs {
@@ -128,6 +128,9 @@ int launch_gn_rkrk(const uint16_t *y, const uint16_t *r, const uint16_t *k, cons
 // One-token, one-sequence decode as a single persistent kernel (decode_mk.hip).
 int mk_cus();
 bool mk_supported(const rwkv7_dims &d, int G);
+// mk_supported on the current device's CU count, and the kernel's grid fits
+// there all at once (checked once per device)
+bool mk_usable(const rwkv7_dims &d);
 int64_t mk_exchange_bytes(int C, int F, int SR);
 int launch_decode_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const rwkv7_state &s,
                      const int64_t *tok, void *logits, char *xreg, hipStream_t st);

@@ -127,17 +127,7 @@ int launch_tmix_decode(const TmixDecodeArgs &a, int B, hipStream_t st) {
   return RWKV7_OK;
 }
 
-// ---------------------------------------------------------------------------
-// Serial wkv7 scan over T tokens. Grid (4 * H, B): each workgroup owns 16
-// value rows of one head; lane group of 16 per row, 4 key columns per lane,
-// so both reductions are 16-lane DPP sums. The step inputs of a chunk of
-// kCh tokens are staged in LDS (double-buffered: the next chunk's global loads
-// are issued before the current chunk's serial loop).
-// Stands in for fused_dplr_T (src/rwkv_tl/kernels/dplr.py:174-227,272-285).
-// ---------------------------------------------------------------------------
-
 constexpr int kCh = 16;
-
 
 template <typename T> RWKV7_DEV float to_f(T x);
 template <> RWKV7_DEV float to_f<float>(float x) { return x; }
@@ -146,168 +136,90 @@ template <typename T> RWKV7_DEV T from_f(float x);
 template <> RWKV7_DEV float from_f<float>(float x) { return x; }
 template <> RWKV7_DEV uint16_t from_f<uint16_t>(float x) { return f2h(x); }
 
-template <typename TI, typename TW, typename TY>
-__global__ __launch_bounds__(256) void wkv7_scan_kernel(ScanArgs<TI, TW, TY> p) {
-  // s_in[buf][vec][token][64]: vec 0 w, 1 a, 2 b, 3 k, 4 r, 5 v
-  __shared__ float4 s_in[2][6][kCh][kN / 4];
-  __shared__ float s_y[kCh][16];
-
-  const int t = threadIdx.x;
-  const int h = blockIdx.x >> 2, quarter = blockIdx.x & 3, bi = blockIdx.y;
-  const int row = quarter * 16 + (t >> 4);
-  const int lc = (t & 15);  // owns key columns 4*lc .. 4*lc+3
-  const int H = p.H, T = p.T;
-  const int64_t ld = (int64_t)H * kN;  // elements between consecutive tokens
-  const int64_t base = ((int64_t)bi * T) * ld + (int64_t)h * kN;
-
-  // each thread stages 6 vectors x kCh tokens x 16 float4 / 256 threads = 6 float4
-  constexpr int kPer = 6 * kCh * (kN / 4) / 256;
-  float4 stage[kPer];
-  auto fetch = [&](int c0) {
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      const int idx = t + 256 * u;
-      const int vecid = idx / (kCh * 16), rem = idx % (kCh * 16);
-      const int tok = rem >> 4, q = rem & 15;
-      const int tt = c0 + tok;
-      float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (tt < T) {
-        const int64_t off = base + (int64_t)tt * ld + q * 4;
-        if (vecid == 0) {
-          val = make_float4(to_f(p.w[off]), to_f(p.w[off + 1]), to_f(p.w[off + 2]), to_f(p.w[off + 3]));
-        } else {
-          const TI *src = vecid == 1 ? p.a : vecid == 2 ? p.b : vecid == 3 ? p.k : vecid == 4 ? p.r : p.v;
-          val = make_float4(to_f(src[off]), to_f(src[off + 1]), to_f(src[off + 2]), to_f(src[off + 3]));
-        }
-      }
-      stage[u] = val;
-    }
-  };
-  auto commit = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      const int idx = t + 256 * u;
-      const int vecid = idx / (kCh * 16), rem = idx % (kCh * 16);
-      s_in[buf][vecid][rem >> 4][rem & 15] = stage[u];
-    }
-  };
-
-  float4 *Sp = reinterpret_cast<float4 *>(p.S + (((int64_t)bi * H + h) * kN + row) * kN) + lc;
-  float4 S = *Sp;
-
-  fetch(0);
-  commit(0);
-  __syncthreads();
-  const int nch = (T + kCh - 1) / kCh;
-  for (int c = 0; c < nch; ++c) {
-    const int buf = c & 1;
-    if (c + 1 < nch) fetch((c + 1) * kCh);
-    const int steps = min(kCh, T - c * kCh);
-    for (int s = 0; s < steps; ++s) {
-      const float4 w4 = s_in[buf][0][s][lc], a4 = s_in[buf][1][s][lc], b4 = s_in[buf][2][s][lc];
-      const float4 k4 = s_in[buf][3][s][lc], r4 = s_in[buf][4][s][lc];
-      const float vi = reinterpret_cast<const float *>(&s_in[buf][5][s][0])[row];
-      float sa = S.x * a4.x + S.y * a4.y + S.z * a4.z + S.w * a4.w;
-      sa = sum16(sa);
-      S.x = S.x * w4.x + sa * b4.x + vi * k4.x;
-      S.y = S.y * w4.y + sa * b4.y + vi * k4.y;
-      S.z = S.z * w4.z + sa * b4.z + vi * k4.z;
-      S.w = S.w * w4.w + sa * b4.w + vi * k4.w;
-      float y = S.x * r4.x + S.y * r4.y + S.z * r4.z + S.w * r4.w;
-      y = sum16(y);
-      if (lc == 0) s_y[s][t >> 4] = y;
-    }
-    __syncthreads();
-    if (t < steps * 16) {  // write this chunk's y rows: 16 values per token
-      const int s = t >> 4, rr = t & 15;
-      p.y[base + (int64_t)(c * kCh + s) * ld + quarter * 16 + rr] = from_f<TY>(s_y[s][rr]);
-    }
-    if (c + 1 < nch) commit(buf ^ 1);
-    __syncthreads();
-  }
-  *Sp = S;
+// Four consecutive elements as float4: one 16-byte load for f32, one 8-byte
+// load for f16.
+RWKV7_DEV float4 ld4_as_f(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+RWKV7_DEV float4 ld4_as_f(const uint16_t *p) {
+  const half4 h = __builtin_bit_cast(half4, *reinterpret_cast<const uint2 *>(p));
+  return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
 }
-
-template <typename TI, typename TW, typename TY>
-int launch_wkv7_scan(const ScanArgs<TI, TW, TY> &p, hipStream_t st) {
-  if (p.T <= 0 || p.B <= 0 || p.H <= 0) return RWKV7_OK;
-  wkv7_scan_kernel<TI, TW, TY><<<dim3(4 * p.H, p.B), 256, 0, st>>>(p);
-  RWKV7_CHECK_LAUNCH();
-  return RWKV7_OK;
-}
-
-template int launch_wkv7_scan<uint16_t, float, uint16_t>(const ScanArgs<uint16_t, float, uint16_t> &, hipStream_t);
-template int launch_wkv7_scan<uint16_t, uint16_t, uint16_t>(const ScanArgs<uint16_t, uint16_t, uint16_t> &, hipStream_t);
-template int launch_wkv7_scan<float, float, float>(const ScanArgs<float, float, float> &, hipStream_t);
 
 // ---------------------------------------------------------------------------
-// Prefill time-mix core: the gate math of each token (demo/rwkv7_torch.py:
-// 203-224) fused into the wkv7 scan (dplr.py:174-227). Grid (4 * H, B): each
-// workgroup owns 16 value rows of one head, computes the gates of all 64
-// channels of its head (the L2 norm of kk needs them all) while staging a chunk
-// of 16 tokens, and writes the gated k and the mixed v of its 16 channels (and
-// v itself on layer 0) for the GroupNorm stage.
+// Chunked wkv7 scan (demo/rwkv7_torch.py:227-232; dplr.py:174-227). Grid
+// (4 * H, B[, segments]): each workgroup owns 16 value rows of one head's fp32
+// state, kept in registers: 16 lanes per row, 4 key columns per lane. The step
+// inputs (w, a, b, k, r, v) of CH tokens at a time are staged through
+// double-buffered LDS by a staging policy:
+//   * GateStager (the model's prefill and batched decode): the gate math of
+//     each token (demo/rwkv7_torch.py:203-224) from the projections -- every
+//     workgroup computes all 64 channels of its head (the L2 norm of kk needs
+//     them all) and writes the gated k and the mixed v of its 16 channels (and
+//     v itself on layer 0) for the GroupNorm stage;
+//   * RawStager (the operator-level rwkv7_wkv7): the inputs as given.
 //
-// Step loop: 16 lanes per row, 4 key columns per lane, so sa = S a is a 16-lane
-// DPP sum; S w + v k is formed while that sum runs, so the new state is one FMA
-// past sa; the next step's inputs are read from LDS while the current step
-// computes; y is left as per-lane partials in LDS and summed once per chunk.
+// Step loop: sa = S a is a 16-lane DPP sum; S w + v k is formed while it runs,
+// so the new state is one FMA past sa; the next step's inputs are read from
+// LDS while the current step computes; y is left as per-lane partials in LDS
+// and summed once per chunk.
 //
-// Segments (grid z): a long sequence is cut into nseg pieces of seg_len tokens
-// scanned at once. Segment 0 starts from the real state; segment j > 0 starts
-// from zero and also carries the rows of its transition product
-// P_t = M_1 ... M_t (M = diag(w) + a b^T, from the identity, no v k term), so
-// that with S_in the state entering it, S_t = S_in P_t + S_loc_t and
+// Segments (grid z, model path): a long sequence is cut into nseg pieces of
+// seg_len tokens scanned at once. Segment 0 starts from the real state;
+// segment j > 0 starts from zero and also carries the rows of its transition
+// product P_t = M_1 ... M_t (M = diag(w) + a b^T, from the identity, no v k
+// term), so that with S_in the state entering it, S_t = S_in P_t + S_loc_t and
 // y_t = y_loc_t + S_in u_t with u_t = P_t r. It writes y_loc and u, and its
 // end state and product to Send / Pend; wkv7_prefill_combine_kernel then
 // chains the segments and adds S_in u_t.
 // ---------------------------------------------------------------------------
-// SEG: launched with more than one segment. CH: tokens staged per chunk (16;
-// 1 for single-token steps, whose small LDS lets four workgroups share a CU).
-template <bool SEG, int CH>
-__global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p, int seg_len, int nseg) {
-  // s_in[buf][vec][token][16 float4]: vec 0 w, 1 a, 2 b, 3 k, 4 r, 5 v
-  __shared__ float4 s_in[2][6][CH][kN / 4];
-  __shared__ float s_yp[CH][16][17];  // per-lane partial y: [step][row][lane], padded
-  __shared__ float s_up[SEG ? CH : 1][16][17];  // the same for u (segments after the first)
 
-  const int t = threadIdx.x;
-  const int h = blockIdx.x >> 2, quarter = blockIdx.x & 3, bi = blockIdx.y;
-  const int seg = blockIdx.z;
-  const bool tail = SEG && seg > 0;  // block-uniform
-  const int t0 = seg * seg_len, t1 = min(p.T, t0 + seg_len), Tl = t1 - t0;
-  const int row = quarter * 16 + (t >> 4);
-  const int lc = t & 15;  // owns key columns 4*lc .. 4*lc+3
-  const int H = p.H, T = p.T, C = p.C;
-  const int64_t MC = (int64_t)p.M * C;
-  const int64_t base = (int64_t)bi * T * C + (int64_t)h * kN;  // token 0, channel 0 of the head
-  const float *vec = p.vec;
+// s_in[buf][vec][token][16 float4]: vec 0 w, 1 a, 2 b, 3 k, 4 r, 5 v
+template <int CH>
+using StageBuf = float4[6][CH][kN / 4];
 
-  // staging: thread -> token t >> 4 of the chunk, channels 4q .. 4q+3 (the
-  // threads of tokens past CH compute a copy of the chunk's last token and
-  // store nothing)
-  const int st_tok = t >> 4, q = t & 15;
-  const bool stager = st_tok < CH;
-  const int ch0 = h * kN + 4 * q;
-  auto ld4 = [&](const float *src) { return *reinterpret_cast<const float4 *>(src); };
-  const float4 v0v = ld4(vec + RWKV7_V_V0 * C + ch0), w0v = ld4(vec + RWKV7_V_W0 * C + ch0);
-  const float4 a0v = ld4(vec + RWKV7_V_A0 * C + ch0), kkv = ld4(vec + RWKV7_V_K_K * C + ch0);
-  const float4 kav = ld4(vec + RWKV7_V_K_A * C + ch0);
+// Model path: gates of each token from r, k, v and the LoRA second steps.
+// Thread -> token t >> 4 of the chunk, channels 4q .. 4q+3 of the head (the
+// threads of tokens past CH compute a copy of the chunk's last token and store
+// nothing; every thread takes part in the 16-lane L2-norm sum).
+template <int CH>
+struct GateStager {
+  using Args = PrefillScanArgs;
+  const PrefillScanArgs &p;
+  int64_t base, MC;
+  int t1, quarter, st_tok, q, C;
+  bool stager;
+  float4 v0v, w0v, a0v, kkv, kav;
   float4 g_r, g_k, g_v, g_dv, g_dw, g_da, g_vf;
-  auto fetch = [&](int c0) {
-    const int tt = t0 + c0 + st_tok;
+
+  RWKV7_DEV GateStager(const PrefillScanArgs &p_, int h, int quarter_, int64_t base_, int t1_)
+      : p(p_), base(base_), t1(t1_), quarter(quarter_) {
+    const int t = threadIdx.x;
+    C = p.C;
+    MC = (int64_t)p.M * C;
+    st_tok = t >> 4;
+    q = t & 15;
+    stager = st_tok < CH;
+    const int ch0 = h * kN + 4 * q;
+    const float *vec = p.vec;
+    v0v = ld4_as_f(vec + RWKV7_V_V0 * C + ch0);
+    w0v = ld4_as_f(vec + RWKV7_V_W0 * C + ch0);
+    a0v = ld4_as_f(vec + RWKV7_V_A0 * C + ch0);
+    kkv = ld4_as_f(vec + RWKV7_V_K_K * C + ch0);
+    kav = ld4_as_f(vec + RWKV7_V_K_A * C + ch0);
+  }
+  RWKV7_DEV void fetch(int c0) {  // c0: first token of the chunk
+    const int tt = c0 + st_tok;
     const int ts = tt < t1 ? tt : t1 - 1;  // clamped (its step is never run)
     const int64_t o = base + (int64_t)ts * C + 4 * q;
-    g_r = ld4(p.rkv + o);
-    g_k = ld4(p.rkv + MC + o);
-    g_v = ld4(p.rkv + 2 * MC + o);
-    g_dv = ld4(p.d + o);
-    g_dw = ld4(p.d + MC + o);
-    g_da = ld4(p.d + 2 * MC + o);
-    g_vf = p.layer0 ? g_v : ld4(p.vfirst + o);
-  };
-  auto commit = [&](int c0, int buf) {
-    const int tt = t0 + c0 + st_tok;
+    g_r = ld4_as_f(p.rkv + o);
+    g_k = ld4_as_f(p.rkv + MC + o);
+    g_v = ld4_as_f(p.rkv + 2 * MC + o);
+    g_dv = ld4_as_f(p.d + o);
+    g_dw = ld4_as_f(p.d + MC + o);
+    g_da = ld4_as_f(p.d + 2 * MC + o);
+    g_vf = p.layer0 ? g_v : ld4_as_f(p.vfirst + o);
+  }
+  RWKV7_DEV void commit(int c0, StageBuf<CH> &dst) {
+    const int tt = c0 + st_tok;
     const float k4[4] = {g_k.x, g_k.y, g_k.z, g_k.w};
     const float vr[4] = {g_v.x, g_v.y, g_v.z, g_v.w}, dv[4] = {g_dv.x, g_dv.y, g_dv.z, g_dv.w};
     const float dw[4] = {g_dw.x, g_dw.y, g_dw.z, g_dw.w}, da[4] = {g_da.x, g_da.y, g_da.z, g_da.w};
@@ -334,12 +246,12 @@ __global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p, in
       b[e] = -a[e] * ag[e];
     }
     if (!stager) return;
-    s_in[buf][0][st_tok][q] = make_float4(w[0], w[1], w[2], w[3]);
-    s_in[buf][1][st_tok][q] = make_float4(a[0], a[1], a[2], a[3]);
-    s_in[buf][2][st_tok][q] = make_float4(b[0], b[1], b[2], b[3]);
-    s_in[buf][3][st_tok][q] = make_float4(kn[0], kn[1], kn[2], kn[3]);
-    s_in[buf][4][st_tok][q] = g_r;
-    s_in[buf][5][st_tok][q] = make_float4(v[0], v[1], v[2], v[3]);
+    dst[0][st_tok][q] = make_float4(w[0], w[1], w[2], w[3]);
+    dst[1][st_tok][q] = make_float4(a[0], a[1], a[2], a[3]);
+    dst[2][st_tok][q] = make_float4(b[0], b[1], b[2], b[3]);
+    dst[3][st_tok][q] = make_float4(kn[0], kn[1], kn[2], kn[3]);
+    dst[4][st_tok][q] = g_r;
+    dst[5][st_tok][q] = make_float4(v[0], v[1], v[2], v[3]);
     // this workgroup's 16 channels of the values GroupNorm needs
     if (tt < t1 && (q >> 2) == quarter) {
       const int64_t o = base + (int64_t)tt * C + 4 * q;
@@ -347,7 +259,65 @@ __global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p, in
       *reinterpret_cast<float4 *>(p.v_out + o) = make_float4(v[0], v[1], v[2], v[3]);
       if (p.layer0) *reinterpret_cast<float4 *>(p.vfirst + o) = g_v;
     }
-  };
+  }
+  RWKV7_DEV void put_y(int64_t o, float y) { p.y[o] = y; }
+};
+
+// Operator level: w, a, b, k, r, v as given ([B, T, H, 64]; w f32 or f16).
+// Thread -> token t >> 4, float4 q = t & 15 of the head's 64 channels.
+template <int CH, typename TI, typename TW, typename TY>
+struct RawStager {
+  using Args = ScanArgs<TI, TW, TY>;
+  const Args &p;
+  int64_t base;
+  int t1, st_tok, q, C;
+  bool stager;
+  float4 g[6];
+
+  RWKV7_DEV RawStager(const Args &p_, int, int, int64_t base_, int t1_) : p(p_), base(base_), t1(t1_) {
+    C = p.H * kN;
+    st_tok = threadIdx.x >> 4;
+    q = threadIdx.x & 15;
+    stager = st_tok < CH;
+  }
+  RWKV7_DEV void fetch(int c0) {
+    const int tt = c0 + st_tok;
+    const int ts = tt < t1 ? tt : t1 - 1;
+    const int64_t o = base + (int64_t)ts * C + 4 * q;
+    g[0] = ld4_as_f(p.w + o);
+    g[1] = ld4_as_f(p.a + o);
+    g[2] = ld4_as_f(p.b + o);
+    g[3] = ld4_as_f(p.k + o);
+    g[4] = ld4_as_f(p.r + o);
+    g[5] = ld4_as_f(p.v + o);
+  }
+  RWKV7_DEV void commit(int, StageBuf<CH> &dst) {
+    if (!stager) return;
+#pragma unroll
+    for (int i = 0; i < 6; ++i) dst[i][st_tok][q] = g[i];
+  }
+  RWKV7_DEV void put_y(int64_t o, float y) { p.y[o] = from_f<TY>(y); }
+};
+
+// SEG: launched with more than one segment (GateStager only). CH: tokens
+// staged per chunk (16; 1 for single-token steps, whose small LDS lets four
+// workgroups share a CU).
+template <bool SEG, int CH, class St>
+__global__ __launch_bounds__(256) void dplr_scan_kernel(typename St::Args p, int seg_len, int nseg) {
+  __shared__ StageBuf<CH> s_in[2];
+  __shared__ float s_yp[CH][16][17];  // per-lane partial y: [step][row][lane], padded
+  __shared__ float s_up[SEG ? CH : 1][16][17];  // the same for u (segments after the first)
+
+  const int t = threadIdx.x;
+  const int h = blockIdx.x >> 2, quarter = blockIdx.x & 3, bi = blockIdx.y;
+  const int seg = blockIdx.z;
+  const bool tail = SEG && seg > 0;  // block-uniform
+  const int H = p.H, T = p.T, C = H * kN;
+  const int t0 = seg * seg_len, t1 = min(T, t0 + seg_len), Tl = t1 - t0;
+  const int row = quarter * 16 + (t >> 4);
+  const int lc = t & 15;  // owns key columns 4*lc .. 4*lc+3
+  const int64_t base = (int64_t)bi * T * C + (int64_t)h * kN;  // token 0, channel 0 of the head
+  St st(p, h, quarter, base, t1);
 
   float4 *Sp = reinterpret_cast<float4 *>(p.S + (((int64_t)bi * H + h) * kN + row) * kN) + lc;
   float4 S = tail ? make_float4(0.f, 0.f, 0.f, 0.f) : *Sp;
@@ -358,28 +328,28 @@ __global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p, in
     P = make_float4(e == 0, e == 1, e == 2, e == 3);
   }
 
-  fetch(0);
-  commit(0, 0);
+  st.fetch(t0);
+  st.commit(t0, s_in[0]);
   __syncthreads();
   const int nch = (Tl + CH - 1) / CH;
   for (int c = 0; c < nch; ++c) {
     const int buf = c & 1;
-    if (c + 1 < nch) fetch((c + 1) * CH);
+    if (c + 1 < nch) st.fetch(t0 + (c + 1) * CH);
     const int steps = min(CH, Tl - c * CH);
     const float *vrow = reinterpret_cast<const float *>(&s_in[buf][5][0][0]) + row;
     struct In {
       float4 w, a, b, k, r;
       float v;
     };
-    auto load_in = [&](In &x, int st) {
-      x.w = s_in[buf][0][st][lc];
-      x.a = s_in[buf][1][st][lc];
-      x.b = s_in[buf][2][st][lc];
-      x.k = s_in[buf][3][st][lc];
-      x.r = s_in[buf][4][st][lc];
-      x.v = vrow[st * kN];
+    auto load_in = [&](In &x, int sp) {
+      x.w = s_in[buf][0][sp][lc];
+      x.a = s_in[buf][1][sp][lc];
+      x.b = s_in[buf][2][sp][lc];
+      x.k = s_in[buf][3][sp][lc];
+      x.r = s_in[buf][4][sp][lc];
+      x.v = vrow[sp * kN];
     };
-    auto step = [&](const In &x, int st) {
+    auto step = [&](const In &x, int sp) {
       float p0 = S.x * x.a.x, p1 = S.z * x.a.z;
       p0 = fmaf(S.y, x.a.y, p0);
       p1 = fmaf(S.w, x.a.w, p1);
@@ -396,10 +366,10 @@ __global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p, in
       float y0 = S.x * x.r.x, y1 = S.z * x.r.z;
       y0 = fmaf(S.y, x.r.y, y0);
       y1 = fmaf(S.w, x.r.w, y1);
-      s_yp[st][t >> 4][lc] = y0 + y1;
+      s_yp[sp][t >> 4][lc] = y0 + y1;
     };
     // the same step plus the transition product's rows: P <- P (diag(w) + a b^T)
-    auto step_tail = [&](const In &x, int st) {
+    auto step_tail = [&](const In &x, int sp) {
       float p0 = S.x * x.a.x, p1 = S.z * x.a.z;
       float q0 = P.x * x.a.x, q1 = P.z * x.a.z;
       p0 = fmaf(S.y, x.a.y, p0);
@@ -426,30 +396,30 @@ __global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p, in
       y1 = fmaf(S.w, x.r.w, y1);
       u0 = fmaf(P.y, x.r.y, u0);
       u1 = fmaf(P.w, x.r.w, u1);
-      s_yp[st][t >> 4][lc] = y0 + y1;
-      if (SEG) s_up[st][t >> 4][lc] = u0 + u1;
+      s_yp[sp][t >> 4][lc] = y0 + y1;
+      if constexpr (SEG) s_up[sp][t >> 4][lc] = u0 + u1;
     };
     // two input register sets in turn: the next step's inputs are read from
     // LDS while the current step computes
     In x0, x1;
     load_in(x0, 0);
-    int st = 0;
+    int sp = 0;
     if (!tail) {
-      for (; st + 1 < steps; st += 2) {
-        load_in(x1, st + 1);
-        step(x0, st);
-        load_in(x0, st + 2 < steps ? st + 2 : st + 1);
-        step(x1, st + 1);
+      for (; sp + 1 < steps; sp += 2) {
+        load_in(x1, sp + 1);
+        step(x0, sp);
+        load_in(x0, sp + 2 < steps ? sp + 2 : sp + 1);
+        step(x1, sp + 1);
       }
-      if (st < steps) step(x0, st);
-    } else if (SEG) {
-      for (; st + 1 < steps; st += 2) {
-        load_in(x1, st + 1);
-        step_tail(x0, st);
-        load_in(x0, st + 2 < steps ? st + 2 : st + 1);
-        step_tail(x1, st + 1);
+      if (sp < steps) step(x0, sp);
+    } else if constexpr (SEG) {
+      for (; sp + 1 < steps; sp += 2) {
+        load_in(x1, sp + 1);
+        step_tail(x0, sp);
+        load_in(x0, sp + 2 < steps ? sp + 2 : sp + 1);
+        step_tail(x1, sp + 1);
       }
-      if (st < steps) step_tail(x0, st);
+      if (sp < steps) step_tail(x0, sp);
     }
     __syncthreads();
     {  // y (and u) of (step t >> 4, row t & 15): sums of the 16 lane partials
@@ -459,19 +429,21 @@ __global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p, in
 #pragma unroll
         for (int l = 0; l < 16; ++l) y += s_yp[ss][rr][l];
         const int64_t o = base + (int64_t)(t0 + c * CH + ss) * C + quarter * 16 + rr;
-        p.y[o] = y;
-        if (SEG && tail) {
-          float u = 0.f;
+        st.put_y(o, y);
+        if constexpr (SEG) {
+          if (tail) {
+            float u = 0.f;
 #pragma unroll
-          for (int l = 0; l < 16; ++l) u += s_up[SEG ? ss : 0][rr][l];
-          p.U[o] = u;
+            for (int l = 0; l < 16; ++l) u += s_up[ss][rr][l];
+            p.U[o] = u;
+          }
         }
       }
     }
-    if (c + 1 < nch) commit((c + 1) * CH, buf ^ 1);
+    if (c + 1 < nch) st.commit(t0 + (c + 1) * CH, s_in[buf ^ 1]);
     __syncthreads();
   }
-  if (!SEG) {
+  if constexpr (!SEG) {
     *Sp = S;
   } else {
     const int64_t slab = (int64_t)p.B * H * kN * kN;
@@ -481,7 +453,22 @@ __global__ __launch_bounds__(256) void wkv7_prefill_kernel(PrefillScanArgs p, in
   }
 }
 
-// Chains the segments of wkv7_prefill_kernel. Grid (4 H, B, (nseg - 1) *
+template <typename TI, typename TW, typename TY>
+int launch_wkv7_scan(const ScanArgs<TI, TW, TY> &p, hipStream_t st) {
+  if (p.T <= 0 || p.B <= 0 || p.H <= 0) return RWKV7_OK;
+  if (p.T == 1)
+    dplr_scan_kernel<false, 1, RawStager<1, TI, TW, TY>><<<dim3(4 * p.H, p.B, 1), 256, 0, st>>>(p, p.T, 1);
+  else
+    dplr_scan_kernel<false, kCh, RawStager<kCh, TI, TW, TY>><<<dim3(4 * p.H, p.B, 1), 256, 0, st>>>(p, p.T, 1);
+  RWKV7_CHECK_LAUNCH();
+  return RWKV7_OK;
+}
+
+template int launch_wkv7_scan<uint16_t, float, uint16_t>(const ScanArgs<uint16_t, float, uint16_t> &, hipStream_t);
+template int launch_wkv7_scan<uint16_t, uint16_t, uint16_t>(const ScanArgs<uint16_t, uint16_t, uint16_t> &, hipStream_t);
+template int launch_wkv7_scan<float, float, float>(const ScanArgs<float, float, float> &, hipStream_t);
+
+// Chains the segments of dplr_scan_kernel (model path). Grid (4 H, B, (nseg - 1) *
 // nblk): the workgroup of segment j >= 1 and 16-token block k of it forms the
 // state entering j, S_in(1) = Send(0), S_in(i + 1) = S_in(i) Pend(i) + Send(i),
 // adds S_in(j) u_t to y_t of its tokens, and (block 0 of the last segment)
@@ -579,9 +566,9 @@ __global__ __launch_bounds__(256) void wkv7_prefill_combine_kernel(PrefillScanAr
 // 0.4B: more, shorter segments lose more to the chain of products than they
 // gain in the scan), and no more than fit the 4 H B workgroups of one segment
 // on the GPU's 256 CUs at once (a segmented workgroup takes a CU's LDS).
-int prefill_segments(int T, int B, int H, int *seg_len) {
+int prefill_segments(int T, int B, int H, int cus, int *seg_len) {
   int P = T < 64 ? 1 : T < 256 ? min(4, T / 32) : min(8, T / 64);
-  P = min(P, 256 / max(1, 4 * H * B));
+  P = min(P, cus / max(1, 4 * H * B));
   if (P < 2) {
     *seg_len = T;
     return 1;
@@ -596,14 +583,14 @@ int launch_wkv7_prefill(const PrefillScanArgs &p, hipStream_t st) {
   if (p.T <= 0 || p.B <= 0 || p.H <= 0) return RWKV7_OK;
   if (p.C != p.H * kN) return RWKV7_ESHAPE;
   int seg_len;
-  const int nseg = prefill_segments(p.T, p.B, p.H, &seg_len);
+  const int nseg = prefill_segments(p.T, p.B, p.H, mk_cus() > 0 ? mk_cus() : 256, &seg_len);
   if (nseg > 1 && (!p.U || !p.Send || !p.Pend)) return RWKV7_EWORKSPACE;
   if (p.T == 1)
-    wkv7_prefill_kernel<false, 1><<<dim3(4 * p.H, p.B, 1), 256, 0, st>>>(p, seg_len, nseg);
+    dplr_scan_kernel<false, 1, GateStager<1>><<<dim3(4 * p.H, p.B, 1), 256, 0, st>>>(p, seg_len, nseg);
   else if (nseg == 1)
-    wkv7_prefill_kernel<false, kCh><<<dim3(4 * p.H, p.B, 1), 256, 0, st>>>(p, seg_len, nseg);
+    dplr_scan_kernel<false, kCh, GateStager<kCh>><<<dim3(4 * p.H, p.B, 1), 256, 0, st>>>(p, seg_len, nseg);
   else
-    wkv7_prefill_kernel<true, kCh><<<dim3(4 * p.H, p.B, nseg), 256, 0, st>>>(p, seg_len, nseg);
+    dplr_scan_kernel<true, kCh, GateStager<kCh>><<<dim3(4 * p.H, p.B, nseg), 256, 0, st>>>(p, seg_len, nseg);
   RWKV7_CHECK_LAUNCH();
   if (nseg > 1) {
     const int nblk = (seg_len + kCh - 1) / kCh;

@@ -15,7 +15,10 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the HIP library)
 
 LIB_NAME = "librwkv7_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
+
+# rwkv7_model.flags
+MODEL_MULTI_LAUNCH_DECODE = 1
 
 # enum indices of the per-layer fp32 vector block (RWKV7_V_*)
 VEC_NAMES = (
@@ -32,6 +35,7 @@ SYMBOLS = (
     "rwkv7_strerror",
     "rwkv7_layer_layout_get",
     "rwkv7_workspace_bytes",
+    "rwkv7_workspace_errors",
     "rwkv7_decode_launches",
     "rwkv7_decode",
     "rwkv7_prefill",
@@ -84,6 +88,7 @@ class Model(ctypes.Structure):
         ("ln_out", ctypes.c_void_p),
         ("layers_frag", ctypes.c_void_p),
         ("head_frag", ctypes.c_void_p),
+        ("flags", ctypes.c_uint32),
     ]
 
 
@@ -143,7 +148,8 @@ def _declare(lib: ctypes.CDLL) -> None:
         "rwkv7_strerror": (ctypes.c_char_p, [ctypes.c_int]),
         "rwkv7_layer_layout_get": (ctypes.c_int, [ctypes.POINTER(Dims), ctypes.POINTER(LayerLayout)]),
         "rwkv7_workspace_bytes": (i64, [ctypes.POINTER(Dims), i32, i32]),
-        "rwkv7_decode_launches": (ctypes.c_int, [ctypes.POINTER(Dims), i32, i32]),
+        "rwkv7_workspace_errors": (ctypes.c_int, [vp, i64, ctypes.POINTER(ctypes.c_uint32), vp]),
+        "rwkv7_decode_launches": (ctypes.c_int, [ctypes.POINTER(Model), i32, i32]),
         "rwkv7_decode": (ctypes.c_int, [ctypes.POINTER(Model), ctypes.POINTER(StateDesc), vp, vp, vp, i64, vp]),
         "rwkv7_prefill": (ctypes.c_int, [ctypes.POINTER(Model), ctypes.POINTER(StateDesc), vp, i32, vp, i64, vp]),
         "rwkv7_wkv7": (ctypes.c_int, [vp, vp, vp, i32, vp, vp, vp, vp, vp, i32, i32, i32, vp]),

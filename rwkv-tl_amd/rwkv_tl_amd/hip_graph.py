@@ -119,15 +119,15 @@ class HIPGraph(RWKV7Model):
         if entry is None:
             tok = torch.zeros(B, dtype=torch.int64, device=self.w.device)
             logits = torch.empty(B, m.V, dtype=torch.float16, device=self.w.device)
-            m.workspace(B, 1)  # allocate outside the capture
+            ws = m.workspace(B, 1)  # allocated outside the capture; the entry keeps it alive
             graph = self._capture(key, S, lambda: m.decode_into(tok, S, logits))
             if graph is None:
                 return m.decode(token, S)
-            entry = (graph, tok, logits)
+            entry = (graph, tok, logits, ws)
             self._remember(key, entry)
         else:
             self._graphs.move_to_end(key)
-        graph, tok, logits = entry
+        graph, tok, logits, _ = entry
         tok.copy_(m._tokens(token, (B,)))
         graph.replay()
         out = logits.clone()
@@ -150,15 +150,15 @@ class HIPGraph(RWKV7Model):
         entry = self._graphs.get(key)
         if entry is None:
             tok = torch.zeros(B, T, dtype=torch.int64, device=self.w.device)
-            m.workspace(B, T)
+            ws = m.workspace(B, T)  # the entry keeps the captured workspace alive
             graph = self._capture(key, S, lambda: m.prefill_into(tok, S))
             if graph is None:
                 return m.prefill(tokens, S)
-            entry = (graph, tok)
+            entry = (graph, tok, ws)
             self._remember(key, entry)
         else:
             self._graphs.move_to_end(key)
-        graph, tok = entry
+        graph, tok, _ = entry
         tok.copy_(m._tokens(tokens, (B, T)))
         graph.replay()
         return S

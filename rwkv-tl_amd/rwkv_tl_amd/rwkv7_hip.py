@@ -49,24 +49,50 @@ class RWKV7HIP(RWKV7Model):
         self.V = int(self.dev.dims.vocab)
         self._ws: Tensor | None = None
         self._ws_bytes = 0
-        self._ws_retired: list[Tensor] = []  # kept alive: captured graphs may point at them
 
     # ------------------------------------------------------------------ #
     # buffers and descriptors
     # ------------------------------------------------------------------ #
 
     def workspace(self, batch: int, seq_len: int) -> Tensor:
-        """A scratch buffer big enough for ``batch x seq_len`` (grown, never shrunk)."""
+        """A scratch buffer big enough for ``batch x seq_len`` (grown, never shrunk).
+
+        A larger request replaces the buffer; a captured HIP graph that still
+        points at the old one holds its own reference to it (``HIPGraph``), so
+        the old buffer is freed once no graph uses it."""
         need = int(self._lib.rwkv7_workspace_bytes(ctypes.byref(self.dev.dims), batch, seq_len))
         if need < 0:
             raise ValueError(f"unsupported batch={batch} seq_len={seq_len}")
         if self._ws is None or self._ws_bytes < need:
-            if self._ws is not None:
-                self._ws_retired.append(self._ws)
             # zeroed: the decode kernel's hand-off words at its start must not match any tag
             self._ws = torch.zeros(need, dtype=torch.uint8, device=self.w.device)
             self._ws_bytes = need
         return self._ws
+
+    @property
+    def decode_path(self) -> str:
+        """``"auto"`` (one persistent kernel per batch-1 step where the device
+        fits its grid) or ``"kernels"`` (the multi-launch GEMV path)."""
+        return "kernels" if self.dev.desc.flags & _lib.MODEL_MULTI_LAUNCH_DECODE else "auto"
+
+    @decode_path.setter
+    def decode_path(self, path: str) -> None:
+        if path not in ("auto", "kernels"):
+            raise ValueError(f"decode_path must be 'auto' or 'kernels', got {path!r}")
+        flags = self.dev.desc.flags & ~_lib.MODEL_MULTI_LAUNCH_DECODE
+        self.dev.desc.flags = flags | (_lib.MODEL_MULTI_LAUNCH_DECODE if path == "kernels" else 0)
+
+    def last_error(self) -> int:
+        """Aborted persistent-decode launches on this model's workspace so far
+        (synchronises the current stream). An aborted step wrote NaN logits and
+        left the State with only the layers completed before the failure."""
+        if self._ws is None:
+            return 0
+        n = ctypes.c_uint32(0)
+        rc = self._lib.rwkv7_workspace_errors(self._ws.data_ptr(), self._ws.numel(), ctypes.byref(n),
+                                              _lib.stream_handle())
+        _lib.check(rc, "rwkv7_workspace_errors")
+        return int(n.value)
 
     def _check_state(self, S: State) -> None:
         t0 = S[0][0]
@@ -111,7 +137,7 @@ class RWKV7HIP(RWKV7Model):
 
     def decode_launches(self, batch: int) -> int:
         """Kernel launches of one decode step with logits (1: a single persistent kernel)."""
-        return int(self._lib.rwkv7_decode_launches(ctypes.byref(self.dev.dims), batch, 1))
+        return int(self._lib.rwkv7_decode_launches(ctypes.byref(self.dev.desc), batch, 1))
 
     def decode_into(self, tok: Tensor, S: State, logits: Tensor | None) -> None:
         """One decode step: ``tok`` int64 [B] on device, ``logits`` f16 [B, V] or None."""

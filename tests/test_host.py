@@ -41,6 +41,26 @@ def _dims(shape="0.4b") -> _lib.Dims:
     return _lib.Dims(s.n_layer, s.n_embd, s.n_head, s.n_ffn, s.vocab, s.rank_w, s.rank_a, s.rank_v, s.rank_g)
 
 
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the decision on a host without a GPU")
+@pytest.mark.parametrize("shape", ["tiny", "0.4b"])
+def test_decode_path_decision_without_a_device(shape):
+    """The persistent decode kernel is chosen only when the device's CU count
+    and occupancy for it are known to fit its grid at once; with no device
+    (this host) the library reports the multi-launch path: embed, six launches
+    per layer and the head for batch 1; embed, ten per layer, LayerNorm and
+    head GEMM for a batch. The model flag gives the same count on any host."""
+    lib = _lib.load()
+    d = _dims(shape)
+    m = _lib.Model(dims=d)
+    L = d.n_layer
+    assert lib.rwkv7_decode_launches(ctypes.byref(m), 1, 1) == 1 + 6 * L + 1
+    assert lib.rwkv7_decode_launches(ctypes.byref(m), 1, 0) == 1 + 6 * L
+    assert lib.rwkv7_decode_launches(ctypes.byref(m), 4, 1) == 1 + 10 * L + 2
+    m.flags = _lib.MODEL_MULTI_LAUNCH_DECODE
+    assert lib.rwkv7_decode_launches(ctypes.byref(m), 1, 1) == 1 + 6 * L + 1
+    assert lib.rwkv7_decode_launches(None, 1, 1) == -1
+
+
 @pytest.mark.parametrize("shape", ["tiny", "0.1b", "0.4b", "1.5b"])
 def test_layer_layout(shape):
     d = _dims(shape)
