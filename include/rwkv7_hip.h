@@ -164,6 +164,21 @@ int rwkv7_decode(const rwkv7_model *model, const rwkv7_state *state,
  * lets the HIP-graph wrapper skip capture where it cannot help. */
 int rwkv7_decode_launches(const rwkv7_model *model, int32_t batch, int32_t with_logits);
 
+/* One batch-1 decode step, as rwkv7_decode, that allocates nothing and takes
+ * no workspace. It has no counterpart in the reference; it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). The persistent decode kernel's
+ * exchange region lives in a static device array of
+ * RWKV7_NOALLOC_SCRATCH_BYTES (1 MiB) that each GPU holds until the process
+ * ends; calls that overlap on one GPU race on it. Returns RWKV7_EWORKSPACE
+ * when the model's exchange region exceeds that size (0.4B needs 0.6 MB), and
+ * RWKV7_ESHAPE when state->batch != 1, model->flags asks for the multi-launch
+ * path, or the persistent kernel does not fit the device. An aborted launch
+ * (see rwkv7_workspace_errors) shows only as NaN logits here. */
+#define RWKV7_NOALLOC_SCRATCH_BYTES (1 << 20)
+int rwkv7_decode_noalloc(const rwkv7_model *model, const rwkv7_state *state,
+                         const int64_t *tokens, void *logits, void *stream);
+
 /* Prefill seq_len tokens per sequence: tokens i64 [B, T] (device). Updates
  * state in place and produces no logits, like RWKV7Base.prefill
  * (demo/_rwkv7_base.py:89-98) / RWKV7Torch.prefill (demo/rwkv7_torch.py:160-171). */

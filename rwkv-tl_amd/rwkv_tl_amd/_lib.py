@@ -38,6 +38,7 @@ SYMBOLS = (
     "rwkv7_workspace_errors",
     "rwkv7_decode_launches",
     "rwkv7_decode",
+    "rwkv7_decode_noalloc",
     "rwkv7_prefill",
     "rwkv7_wkv7",
     "rwkv7_layernorm",
@@ -151,6 +152,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "rwkv7_workspace_errors": (ctypes.c_int, [vp, i64, ctypes.POINTER(ctypes.c_uint32), vp]),
         "rwkv7_decode_launches": (ctypes.c_int, [ctypes.POINTER(Model), i32, i32]),
         "rwkv7_decode": (ctypes.c_int, [ctypes.POINTER(Model), ctypes.POINTER(StateDesc), vp, vp, vp, i64, vp]),
+        "rwkv7_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(Model), ctypes.POINTER(StateDesc), vp, vp, vp]),
         "rwkv7_prefill": (ctypes.c_int, [ctypes.POINTER(Model), ctypes.POINTER(StateDesc), vp, i32, vp, i64, vp]),
         "rwkv7_wkv7": (ctypes.c_int, [vp, vp, vp, i32, vp, vp, vp, vp, vp, i32, i32, i32, vp]),
         "rwkv7_layernorm": (ctypes.c_int, [vp, i32, vp, vp, vp, i32, i32, vp]),
