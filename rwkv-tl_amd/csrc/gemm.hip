@@ -388,6 +388,219 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmGroup g) {
 }
 
 // ---------------------------------------------------------------------------
+// Large-M path (long prefills, see big_fits): the product is MFMA-bound, so
+// the workgroup tile is large enough that each byte staged through LDS feeds
+// many products. BM x BN tile (256 x 256, or 128 x 128 where the larger tiles
+// leave CUs idle), 8 waves as 2 (rows) x 4 (columns), each wave a (BM/2) x
+// (BN/4) block of 16x16 accumulators; K in stages of 32.
+//
+// Operands go global -> LDS directly (global_load_lds_dwordx4: each lane's
+// 16 bytes land at the wave's LDS base + 16 lane), into a ring of kBigNB
+// stage buffers, kBigNB - 1 stages ahead of the products: a CU keeps ~96 KB
+// of loads in flight, which is what hides the L2 / HBM latency at this
+// arithmetic intensity (one stage ahead in registers reached ~0.2 of the MFMA
+// peak). LDS holds both operands in fragment order: a 16-row x 32-k block is
+// the 1 KiB that one v_mfma_f32_16x16x32_f16 operand reads (lane l <-> row
+// l % 16, k 8 (l / 16) .. +8), so a block is one DMA instruction per wave
+// (4 lanes per 64 contiguous bytes of a row, or one contiguous KiB when W
+// comes from the fragment arena) and every fragment read is 64 lanes x 16
+// consecutive bytes, free of bank conflicts.
+//
+// Synchronisation per stage: each wave waits for its own DMAs of the stage
+// (vmcnt), then a bare s_barrier (no memory fence: that would wait for every
+// DMA in flight) makes all of the stage visible and retires the buffer the
+// next DMA overwrites.
+//
+// Workgroups are dealt round-robin over the 8 XCDs; consecutive tiles (same
+// row block, so the same A rows) are given to one XCD so they share its L2.
+// ---------------------------------------------------------------------------
+constexpr int kBigBK = 32;  // k per stage
+constexpr int kBigNB = 4;   // stage buffers (kBigNB - 1 stages in flight)
+
+struct BigGroup {
+  GemmProb p[kMaxProb];
+  int tile_begin[kMaxProb + 1];  // first tile of each problem
+  int tiles_n[kMaxProb];         // column tiles of each problem
+  int nprob, M, m_tiles, tiles;
+};
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// NW waves as a 2 x (NW / 2) grid over the tile.
+template <int BM, int BN, int NW>
+RWKV7_DEV void gemm_big_tile(const BigGroup &g) {
+  constexpr int SA = BM / 16, SB = BN / 16;  // 16-row strips of A and W in a tile = blocks per stage
+  constexpr int PERS = (SA + SB) / NW;       // blocks each wave loads per stage
+  constexpr int GN = NW / 2;                 // waves along the columns
+  constexpr int WM = BM / 32, WN = BN / (16 * GN);  // 16x16 tiles per wave (rows, columns)
+  static_assert((SA + SB) % NW == 0 && SA % PERS == 0, "a wave loads whole blocks of one operand");
+  // s_waitcnt with vmcnt = (kBigNB - 2) stages of this wave's DMAs (6-bit
+  // field: bits 3..0 and 15..14), expcnt and lgkmcnt untouched
+  constexpr int kVm = (kBigNB - 2) * PERS;
+  static_assert(kVm < 64, "vmcnt field");
+  constexpr int kWaitImm = 0x0F70 | (kVm & 15) | ((kVm >> 4) << 14);
+  __shared__ __align__(16) u32x4 lds[kBigNB][SA + SB][64];
+
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  // tile of this workgroup: XCD x = blockIdx % 8 takes tiles [x * per, (x+1) * per)
+  const int per = (g.tiles + 7) / 8;
+  const int tile = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (tile >= g.tiles) return;
+  // the problem of this tile, selected field by field with a uniform index
+  // (indexing the argument array at run time would copy it to scratch)
+  GemmProb P = g.p[0];
+  int tb = g.tile_begin[0], tn = g.tiles_n[0];
+#pragma unroll
+  for (int i = 1; i < kMaxProb; ++i) {
+    if (i < g.nprob && tile >= g.tile_begin[i]) {
+      P = g.p[i];
+      tb = g.tile_begin[i];
+      tn = g.tiles_n[i];
+    }
+  }
+  const int local = tile - tb;
+  const int m0 = local / tn * BM, n0 = local % tn * BN;
+  const int M = g.M, N = P.N, K = P.K;
+
+  // Block b of a stage (A strips 0 .. SA - 1, then W strips): wave wv loads
+  // blocks wv * PERS .. +PERS, all of one operand; lane l the piece of row
+  // 16 strip + l % 16 at k 8 (l / 16) of the stage. Rows past M or N are
+  // clamped (their products are never stored). Offsets in halfs from `base`.
+  const bool isA = wv * PERS < SA;
+  const int sb0 = isA ? wv * PERS : wv * PERS - SA;
+  const bool wfrag = !isA && P.Wf != nullptr;
+  const uint16_t *base = isA ? P.A : wfrag ? P.Wf : P.W;
+  // the operand as a buffer resource: a lane's piece is a 32-bit byte offset,
+  // the stage a scalar one
+  const int64_t rows = isA ? M : wfrag ? (int64_t)(N + 15) / 16 * 16 : N;
+  const int64_t ld = isA ? P.lda : wfrag ? (int64_t)P.nksf * 32 : P.ldw;
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), 0, (int)min<int64_t>(rows * ld * 2, 0x7fffffff),
+                                        0x00020000);
+  const int stage_b = 2 * (wfrag ? 512 : kBigBK);  // bytes per stage (one block in fragment order)
+  unsigned off[PERS];
+#pragma unroll
+  for (int u = 0; u < PERS; ++u) {
+    const int strip = sb0 + u;
+    if (isA) off[u] = 2u * (unsigned)(min(m0 + 16 * strip + (lane & 15), M - 1) * (int)P.lda + 8 * (lane >> 4));
+    else if (wfrag) off[u] = 2u * (unsigned)(min(n0 / 16 + strip, (N + 15) / 16 - 1) * P.nksf * 512 + 8 * lane);
+    else off[u] = 2u * (unsigned)(min(n0 + 16 * strip + (lane & 15), N - 1) * (int)P.ldw + 8 * (lane >> 4));
+  }
+  const int nst = K / kBigBK;
+  // DMA of stage st (clamped: past the last stage the last one is reloaded into
+  // a buffer nobody reads again, which keeps the vmcnt bookkeeping uniform)
+  auto issue = [&](int st, int buf) {
+    const unsigned s2 = (unsigned)(st < nst ? st : nst - 1) * stage_b;
+#pragma unroll
+    for (int u = 0; u < PERS; ++u)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void *)(&lds[buf][wv * PERS + u][0]), 16, off[u], s2, 0, 0);
+  };
+
+  const int wm = wv / GN, wn = wv % GN;  // this wave's block of the tile
+  floatx4 acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int q = 0; q < WN; ++q) acc[i][q] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  auto step = [&](int st, int buf) {
+    __builtin_amdgcn_s_waitcnt(kWaitImm);  // this wave's DMAs of stage st have landed
+    // everyone's have, and every read of buffer (st - 1) % NB is complete (the
+    // lgkmcnt wait); the memory clobber keeps the compiler from moving LDS
+    // reads or DMAs across the barrier
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    issue(st + kBigNB - 1, (buf + kBigNB - 1) % kBigNB);
+    half8 bf[WN];
+#pragma unroll
+    for (int q = 0; q < WN; ++q) bf[q] = __builtin_bit_cast(half8, lds[buf][SA + wn * WN + q][lane]);
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+      const half8 af = __builtin_bit_cast(half8, lds[buf][wm * WM + i][lane]);
+#pragma unroll
+      for (int q = 0; q < WN; ++q) acc[i][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[q], acc[i][q], 0, 0, 0);
+    }
+  };
+#pragma unroll
+  for (int b = 0; b < kBigNB - 1; ++b) issue(b, b);
+  int st = 0;
+  for (; st + kBigNB <= nst; st += kBigNB) {
+#pragma unroll
+    for (int b = 0; b < kBigNB; ++b) step(st + b, b);
+  }
+#pragma unroll
+  for (int b = 0; b < kBigNB; ++b)
+    if (st + b < nst) step(st + b, b);
+  // drain the clamped DMAs before the workgroup's LDS can be reused
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+
+  // lane holds rows 4 (lane >> 4) + {0..3} of column lane & 15 of each 16x16 tile
+#pragma unroll
+  for (int q = 0; q < WN; ++q) {
+    const int col = n0 + 16 * (wn * WN + q) + (lane & 15);
+    if (col >= N) continue;
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + 16 * (wm * WM + i) + 4 * (lane >> 4) + r;
+        if (row < M) store_epi(P, row, col, acc[i][q][r]);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(512) void gemm_big_kernel_256(BigGroup g) { gemm_big_tile<256, 256, 8>(g); }
+__global__ __launch_bounds__(512) void gemm_big_kernel_128(BigGroup g) { gemm_big_tile<128, 128, 8>(g); }
+
+// Problems of the large-M path: K a multiple of 64, at least 256 columns, and
+// enough 128 x 128 tiles for two workgroups per CU (measured: at M = 512 the
+// 32-row tiled kernels with split-K are 2-3x faster; at M = 4096 this path is
+// ~2x faster than them).
+static bool big_fits(const GemmProb &p, int M, int cus) {
+  return p.K % kBigBK == 0 && p.N >= 256 && (int64_t)((M + 127) / 128) * ((p.N + 127) / 128) >= 2 * cus;
+}
+
+#define RWKV7_TRY_GEMM(expr)         \
+  do {                               \
+    const int rc_ = (expr);          \
+    if (rc_ != RWKV7_OK) return rc_; \
+  } while (0)
+
+// Runs a group of problems that all fit the large-M path.
+static int launch_big(const GemmProb *probs, int nprob, int M, int cus, hipStream_t st) {
+  BigGroup g;
+  g.nprob = nprob;
+  g.M = M;
+  // 256 x 256 tiles when they alone give every CU a workgroup, else 128 x 128
+  auto count = [&](int bt) {
+    int t = 0;
+    for (int i = 0; i < nprob; ++i) t += (M + bt - 1) / bt * ((probs[i].N + bt - 1) / bt);
+    return t;
+  };
+  const int BT = count(256) >= cus ? 256 : 128;
+  g.m_tiles = (M + BT - 1) / BT;
+  int t = 0;
+  for (int i = 0; i < kMaxProb; ++i) {
+    g.tile_begin[i] = t;
+    if (i < nprob) {
+      g.p[i] = probs[i];
+      g.tiles_n[i] = (probs[i].N + BT - 1) / BT;
+      t += g.m_tiles * g.tiles_n[i];
+    } else {
+      g.p[i] = probs[0];
+      g.tiles_n[i] = 1;
+    }
+  }
+  g.tile_begin[kMaxProb] = t;
+  g.tiles = t;
+  const int grid = (t + 7) / 8 * 8;
+  if (BT == 256) gemm_big_kernel_256<<<grid, 512, 0, st>>>(g);
+  else gemm_big_kernel_128<<<grid, 512, 0, st>>>(g);
+  RWKV7_CHECK_LAUNCH();
+  return RWKV7_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Skinny path, M <= 32 (batched decode, short prefill). One workgroup of 4
 // waves per 16-column strip of W (and per split of K, see below); the waves
 // split the strip's k-steps, each loading its W fragments and the A fragments
@@ -649,6 +862,21 @@ int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, f
     if (!p.A || !p.W || !p.Y) return RWKV7_EINVAL;
   }
   if (M <= kSkinnyMaxM) return launch_skinny(probs, nprob, M, st, part, ctr, gemm_ws_bytes(M, cus));
+  {
+    // problems the large-M path takes run there; the rest (LoRA widths) below
+    GemmProb big[kMaxProb], rest[kMaxProb];
+    int nb = 0, nr = 0;
+    for (int i = 0; i < nprob; ++i) {
+      if (big_fits(probs[i], M, cus)) big[nb++] = probs[i];
+      else rest[nr++] = probs[i];
+    }
+    if (nb > 0) {
+      RWKV7_TRY_GEMM(launch_big(big, nb, M, cus, st));
+      if (nr == 0) return RWKV7_OK;
+      probs = rest;
+      nprob = nr;
+    }
+  }
   plan_splits(probs, nprob, M, cus, part != nullptr && ctr != nullptr, S, ks);
   int wgs = 0, ctrs = 0;
   int64_t pfl = 0;

@@ -100,7 +100,11 @@ def test_gemv_matches_fp32(N, Kd, cuda):
 
 @pytest.mark.parametrize(
     "M,N,Kd",
-    [(1, 64, 256), (5, 100, 40), (16, 1024, 1024), (33, 72, 16), (128, 4096, 1024), (200, 1024, 4096), (7, 65536, 256)],
+    [(1, 64, 256), (5, 100, 40), (16, 1024, 1024), (33, 72, 16), (128, 4096, 1024), (200, 1024, 4096), (7, 65536, 256),
+     # mid M on the 32/64-row tiled kernels
+     (512, 1024, 1024), (600, 300, 128), (1030, 520, 64),
+     # large-M path: 256 x 256 tiles (also ragged), 128 x 128 tiles (also ragged)
+     (2048, 8192, 1024), (4000, 4000, 64), (4096, 2048, 2048), (2100, 3900, 128)],
 )
 @pytest.mark.parametrize("epi", ["f32", "f16", "relu2", "add"])
 def test_gemm_matches_fp32(M, N, Kd, epi, cuda):
