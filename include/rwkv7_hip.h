@@ -198,6 +198,28 @@ int rwkv7_wkv7(float *S, const void *r, const void *w, int32_t w_is_f32,
                const void *k, const void *v, const void *a, const void *b,
                void *y, int32_t B, int32_t T, int32_t H, void *stream);
 
+/* The same recurrence with every operand f32 (S, r, w, k, v, a, b, y), for
+ * training. When hist != NULL it receives the state entering each step, f32
+ * [B, H, T, 64, 64], which rwkv7_wkv7_backward reads. Forward half of the DPLR
+ * backward the reference plans (TODO.md:46-54: save the per-step states,
+ * register_autograd on the DPLR op). */
+int rwkv7_wkv7_f32(float *S, const float *r, const float *w, const float *k,
+                   const float *v, const float *a, const float *b, float *y,
+                   float *hist, int32_t B, int32_t T, int32_t H, void *stream);
+
+/* Gradients of rwkv7_wkv7_f32 (reverse-time adjoint scan), all f32: given
+ * hist (its recorded states), S_T (the state it left), its inputs, gy = dL/dy
+ * [B, T, H, 64] and gS_T = dL/dS_T [B, H, 64, 64] (NULL: zero), writes
+ * gS0 = dL/dS_0 and gr, gw, gk, gv, ga, gb [B, T, H, 64]. The DPLR backward of
+ * the reference's training plan (TODO.md:46-54); the reference has no kernel
+ * for it. */
+int rwkv7_wkv7_backward(const float *hist, const float *S_T, const float *r,
+                        const float *w, const float *k, const float *v,
+                        const float *a, const float *b, const float *gy,
+                        const float *gS_T, float *gS0, float *gr, float *gw,
+                        float *gk, float *gv, float *ga, float *gb, int32_t B,
+                        int32_t T, int32_t H, void *stream);
+
 /* LayerNorm over the last dimension (eps 1e-5): x f32 or f16 [M, C]
  * (x_is_f32), weight/bias f32 [C], y f32 [M, C]. Stands in for LNWeight
  * (src/rwkv_tl/weight.py:14-15). */

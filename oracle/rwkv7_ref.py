@@ -13,6 +13,8 @@ What it restates (reference citations are ``path:line`` in yuyi2439/rwkv-tl):
   ``tmix {"x": [C] D, "rnn": [H,N,N] fp32}``, ``cmix {"x": [C] D}``), plus an
   optional leading batch dimension the reference does not have.
 * ``wkv7_step``      -- ``demo/rwkv7_torch.py:49-64`` (``_dplr_rwkv``).
+* ``wkv7_scan_grads`` -- gradients of the serial scan by torch autograd (the
+  backward the reference plans in ``TODO.md:46-54`` has no code there).
 * ``time_mix``       -- ``demo/rwkv7_torch.py:67-120``.
 * ``channel_mix``    -- ``demo/rwkv7_torch.py:123-128``.
 * ``decode``         -- ``demo/rwkv7_torch.py:150-158,173-178``.
@@ -229,6 +231,32 @@ def wkv7_scan(S: Tensor, r, w, k, v, a, b) -> tuple[Tensor, Tensor]:
                 S[bi], r[bi, t], w[bi, t], k[bi, t], v[bi, t], a[bi, t], b[bi, t]
             )
     return y, S
+
+
+def wkv7_scan_grads(S: Tensor, r, w, k, v, a, b, gy: Tensor, gS: Tensor | None = None):
+    """Gradients of ``wkv7_scan`` (fp32) by torch autograd: of
+    ``L = <gy, y> + <gS, S_T>`` with respect to ``(S, r, w, k, v, a, b)``.
+
+    The reference has no backward (``TODO.md:46-54`` plans one); the gradient
+    is fixed by the forward restated above, so the checker differentiates that
+    forward with autograd. Pinned in tests/test_oracle.py by finite differences
+    of ``wkv7_brute`` (double precision, no torch)."""
+    xs = [t.detach().float().clone().requires_grad_(True) for t in (S, r, w, k, v, a, b)]
+    with torch.enable_grad():
+        # the per-token loop of wkv7_scan without its in-place stores
+        ys, finals = [], []
+        for bi in range(r.shape[0]):
+            St, yb = xs[0][bi], []
+            for t in range(r.shape[1]):
+                yt, St = wkv7_step(St, *(x[bi, t] for x in xs[1:]))
+                yb.append(yt)
+            ys.append(torch.stack(yb))
+            finals.append(St)
+        y, S_T = torch.stack(ys), torch.stack(finals)
+        L = (y.float() * gy.float()).sum()
+        if gS is not None:
+            L = L + (S_T * gS.float()).sum()
+        return torch.autograd.grad(L, xs)
 
 
 def wkv7_brute(S, r, w, k, v, a, b):

@@ -471,6 +471,25 @@ int rwkv7_wkv7(float *S, const void *r, const void *w, int32_t w_is_f32, const v
   return launch_wkv7_scan(p, st);
 }
 
+int rwkv7_wkv7_f32(float *S, const float *r, const float *w, const float *k, const float *v, const float *a,
+                   const float *b, float *y, float *hist, int32_t B, int32_t T, int32_t H, void *stream) {
+  if (!S || !r || !w || !k || !v || !a || !b || !y) return RWKV7_EINVAL;
+  if (B < 1 || T < 1 || H < 1) return RWKV7_ESHAPE;
+  ScanArgs<float, float, float> p = {S, r, k, v, a, b, w, y, B, T, H, hist};
+  return launch_wkv7_scan(p, static_cast<hipStream_t>(stream));
+}
+
+int rwkv7_wkv7_backward(const float *hist, const float *S_T, const float *r, const float *w, const float *k,
+                        const float *v, const float *a, const float *b, const float *gy, const float *gS_T,
+                        float *gS0, float *gr, float *gw, float *gk, float *gv, float *ga, float *gb, int32_t B,
+                        int32_t T, int32_t H, void *stream) {
+  if (!hist || !S_T || !r || !w || !k || !v || !a || !b || !gy || !gS0 || !gr || !gw || !gk || !gv || !ga || !gb)
+    return RWKV7_EINVAL;
+  if (B < 1 || T < 1 || H < 1) return RWKV7_ESHAPE;
+  Wkv7BwdArgs p = {hist, S_T, r, w, k, v, a, b, gy, gS_T, gS0, gr, gw, gk, gv, ga, gb, B, T, H};
+  return launch_wkv7_bwd(p, static_cast<hipStream_t>(stream));
+}
+
 int rwkv7_layernorm(const void *x, int32_t x_is_f32, const float *weight, const float *bias, float *y, int32_t M,
                     int32_t C, void *stream) {
   if (!x || !weight || !bias || !y) return RWKV7_EINVAL;

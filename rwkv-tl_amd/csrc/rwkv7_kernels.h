@@ -46,9 +46,27 @@ struct ScanArgs {
   const TW *w;
   TY *y;
   int B, T, H;
+  // optional: f32 [B, H, T, 64, 64] receives the state entering each step
+  // (what the backward scan needs)
+  float *hist;
 };
 template <typename TI, typename TW, typename TY>
 int launch_wkv7_scan(const ScanArgs<TI, TW, TY> &p, hipStream_t st);
+
+// Backward of the wkv7 recurrence (reverse-time adjoint scan), all f32:
+// from the gradient of y (and optionally of the final state) to the gradients
+// of r, w, k, v, a, b and of the initial state.
+struct Wkv7BwdArgs {
+  const float *hist;                  // [B, H, T, 64, 64] state entering each step
+  const float *S_T;                   // [B, H, 64, 64] state after the last step
+  const float *r, *w, *k, *v, *a, *b; // [B, T, H, 64]
+  const float *gy;                    // [B, T, H, 64]
+  const float *gS_T;                  // [B, H, 64, 64] or null (zero)
+  float *gS0;                         // [B, H, 64, 64]
+  float *gr, *gw, *gk, *gv, *ga, *gb; // [B, T, H, 64]
+  int B, T, H;
+};
+int launch_wkv7_bwd(const Wkv7BwdArgs &p, hipStream_t st);
 
 struct LnShiftArgs {
   const float *x0;

@@ -261,6 +261,7 @@ struct GateStager {
     }
   }
   RWKV7_DEV void put_y(int64_t o, float y) { p.y[o] = y; }
+  RWKV7_DEV void record(int, int, int, const float4 &) {}
 };
 
 // Operator level: w, a, b, k, r, v as given ([B, T, H, 64]; w f32 or f16).
@@ -274,8 +275,11 @@ struct RawStager {
   bool stager;
   float4 g[6];
 
-  RWKV7_DEV RawStager(const Args &p_, int, int, int64_t base_, int t1_) : p(p_), base(base_), t1(t1_) {
+  int64_t hbase;  // this head's slab of the optional state history
+
+  RWKV7_DEV RawStager(const Args &p_, int h, int, int64_t base_, int t1_) : p(p_), base(base_), t1(t1_) {
     C = p.H * kN;
+    hbase = ((int64_t)blockIdx.y * p.H + h) * p.T * (kN * kN);
     st_tok = threadIdx.x >> 4;
     q = threadIdx.x & 15;
     stager = st_tok < CH;
@@ -297,6 +301,10 @@ struct RawStager {
     for (int i = 0; i < 6; ++i) dst[i][st_tok][q] = g[i];
   }
   RWKV7_DEV void put_y(int64_t o, float y) { p.y[o] = from_f<TY>(y); }
+  // state entering token tt: row `row`, key columns 4 lc .. 4 lc + 3
+  RWKV7_DEV void record(int tt, int row, int lc, const float4 &S) {
+    if (p.hist) *reinterpret_cast<float4 *>(p.hist + hbase + (int64_t)tt * (kN * kN) + row * kN + 4 * lc) = S;
+  }
 };
 
 // SEG: launched with more than one segment (GateStager only). CH: tokens
@@ -350,6 +358,7 @@ __global__ __launch_bounds__(256) void dplr_scan_kernel(typename St::Args p, int
       x.v = vrow[sp * kN];
     };
     auto step = [&](const In &x, int sp) {
+      st.record(t0 + c * CH + sp, row, lc, S);
       float p0 = S.x * x.a.x, p1 = S.z * x.a.z;
       p0 = fmaf(S.y, x.a.y, p0);
       p1 = fmaf(S.w, x.a.w, p1);
@@ -460,6 +469,118 @@ int launch_wkv7_scan(const ScanArgs<TI, TW, TY> &p, hipStream_t st) {
     dplr_scan_kernel<false, 1, RawStager<1, TI, TW, TY>><<<dim3(4 * p.H, p.B, 1), 256, 0, st>>>(p, p.T, 1);
   else
     dplr_scan_kernel<false, kCh, RawStager<kCh, TI, TW, TY>><<<dim3(4 * p.H, p.B, 1), 256, 0, st>>>(p, p.T, 1);
+  RWKV7_CHECK_LAUNCH();
+  return RWKV7_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Backward of the wkv7 recurrence (the training path the reference plans,
+// TODO.md:46-54). Forward, per head (rows i = value, columns j = key):
+//   sa_i = sum_j S[i,j] a_j ;  S'[i,j] = S[i,j] w_j + sa_i b_j + v_i k_j ;
+//   y_i = sum_j S'[i,j] r_j
+// Reverse-time adjoint G = dL/dS', from G = dL/dS_T, for t = T-1 .. 0 with
+// S = the state entering step t (recorded by the forward) and S' the one
+// after it:
+//   G += gy r^T ;  gr = S'^T gy ;  gv = G k ;  gk = G^T v ;  gw = diag(G^T S)
+//   gsa = G b ;  gb = G^T sa ;  ga = S^T gsa ;  G <- G diag(w) + gsa a^T
+// and dL/dS_0 = G at the end. Grid (H, B), 256 threads: thread -> row
+// i = t / 4, key columns 16 (t % 4) .. +16; row sums are 4-lane DPP sums,
+// column sums run over the 16 rows of a wave with lane shuffles and then over
+// the 4 waves in LDS.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void wkv7_bwd_kernel(Wkv7BwdArgs p) {
+  __shared__ float s_in[7][kN];       // r w k v a b gy of the step
+  __shared__ float s_col[5][4][kN];   // per-wave column sums: gr gk gw gb ga
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int h = blockIdx.x, bi = blockIdx.y;
+  const int H = p.H, T = p.T, C = H * kN;
+  const int i = t >> 2, j0 = 16 * (t & 3);
+  const int64_t sbase = ((int64_t)bi * H + h) * kN * kN + (int64_t)i * kN + j0;  // this thread's S piece
+  const int64_t hslab = ((int64_t)bi * H + h) * (int64_t)T * kN * kN;
+  float G[16], Sn[16], Sp[16];
+  auto ld16 = [&](float (&d)[16], const float *src) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float4 q = reinterpret_cast<const float4 *>(src)[e];
+      d[4 * e] = q.x; d[4 * e + 1] = q.y; d[4 * e + 2] = q.z; d[4 * e + 3] = q.w;
+    }
+  };
+  ld16(Sn, p.S_T + sbase);
+  if (p.gS_T) ld16(G, p.gS_T + sbase);
+  else {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) G[e] = 0.f;
+  }
+  const float *ins[7] = {p.r, p.w, p.k, p.v, p.a, p.b, p.gy};
+  for (int tt = T - 1; tt >= 0; --tt) {
+    const int64_t tok = ((int64_t)bi * T + tt) * C + (int64_t)h * kN;
+    for (int e = t; e < 7 * kN; e += 256) s_in[e / kN][e % kN] = ins[e / kN][tok + e % kN];
+    ld16(Sp, p.hist + hslab + (int64_t)tt * kN * kN + (int64_t)i * kN + j0);
+    __syncthreads();
+    const float vi = s_in[3][i], gyi = s_in[6][i];
+    float sa = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sa = fmaf(Sp[e], s_in[4][j0 + e], sa);
+    sa = sum4(sa);
+    float gv = 0.f, gsa = 0.f;
+    float part[5][16];  // gr gk gw gb ga of this thread's columns
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int j = j0 + e;
+      G[e] = fmaf(gyi, s_in[0][j], G[e]);
+      part[0][e] = Sn[e] * gyi;
+      part[1][e] = G[e] * vi;
+      part[2][e] = G[e] * Sp[e];
+      part[3][e] = G[e] * sa;
+      gv = fmaf(G[e], s_in[2][j], gv);
+      gsa = fmaf(G[e], s_in[5][j], gsa);
+    }
+    gv = sum4(gv);
+    gsa = sum4(gsa);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) part[4][e] = gsa * Sp[e];
+    // column sums over the wave's 16 rows: lanes 4 r + c share column group c
+#pragma unroll
+    for (int q = 0; q < 5; ++q)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        float x = part[q][e];
+        x += __shfl_xor(x, 4);
+        x += __shfl_xor(x, 8);
+        x += __shfl_xor(x, 16);
+        x += __shfl_xor(x, 32);
+        part[q][e] = x;
+      }
+    if (lane < 4) {
+#pragma unroll
+      for (int q = 0; q < 5; ++q)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s_col[q][wv][j0 + e] = part[q][e];
+    }
+    if ((t & 3) == 0) p.gv[tok + i] = gv;
+    // adjoint of the state entering the step
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int j = j0 + e;
+      G[e] = fmaf(G[e], s_in[1][j], gsa * s_in[4][j]);
+      Sn[e] = Sp[e];
+    }
+    __syncthreads();
+    for (int e = t; e < 5 * kN; e += 256) {
+      const int q = e / kN, j = e % kN;
+      const float sum = (s_col[q][0][j] + s_col[q][1][j]) + (s_col[q][2][j] + s_col[q][3][j]);
+      float *dst = q == 0 ? p.gr : q == 1 ? p.gk : q == 2 ? p.gw : q == 3 ? p.gb : p.ga;
+      dst[tok + j] = sum;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    reinterpret_cast<float4 *>(p.gS0 + sbase)[e] = make_float4(G[4 * e], G[4 * e + 1], G[4 * e + 2], G[4 * e + 3]);
+}
+
+int launch_wkv7_bwd(const Wkv7BwdArgs &p, hipStream_t st) {
+  if (p.T <= 0 || p.B <= 0 || p.H <= 0) return RWKV7_OK;
+  wkv7_bwd_kernel<<<dim3(p.H, p.B), 256, 0, st>>>(p);
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;
 }

@@ -41,6 +41,8 @@ SYMBOLS = (
     "rwkv7_decode_noalloc",
     "rwkv7_prefill",
     "rwkv7_wkv7",
+    "rwkv7_wkv7_f32",
+    "rwkv7_wkv7_backward",
     "rwkv7_layernorm",
     "rwkv7_lerp",
     "rwkv7_gemv_f16",
@@ -155,6 +157,8 @@ def _declare(lib: ctypes.CDLL) -> None:
         "rwkv7_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(Model), ctypes.POINTER(StateDesc), vp, vp, vp]),
         "rwkv7_prefill": (ctypes.c_int, [ctypes.POINTER(Model), ctypes.POINTER(StateDesc), vp, i32, vp, i64, vp]),
         "rwkv7_wkv7": (ctypes.c_int, [vp, vp, vp, i32, vp, vp, vp, vp, vp, i32, i32, i32, vp]),
+        "rwkv7_wkv7_f32": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, vp]),
+        "rwkv7_wkv7_backward": (ctypes.c_int, [vp] * 17 + [i32, i32, i32, vp]),
         "rwkv7_layernorm": (ctypes.c_int, [vp, i32, vp, vp, vp, i32, i32, vp]),
         "rwkv7_lerp": (ctypes.c_int, [vp, vp, vp, i32, vp, vp, i32, vp]),
         "rwkv7_gemv_f16": (ctypes.c_int, [vp, vp, i64, vp, i32, i32, vp]),

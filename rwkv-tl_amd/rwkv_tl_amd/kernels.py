@@ -69,6 +69,81 @@ def wkv7(S: Tensor, r: Tensor, w: Tensor, k: Tensor, v: Tensor, a: Tensor, b: Te
     return y
 
 
+def _wkv7_f32_shapes(S: Tensor, r: Tensor, *rest: Tensor) -> tuple[int, int, int]:
+    _need(S.dtype == torch.float32 and S.dim() == 4 and S.shape[2:] == (N, N), "S must be f32 [B,H,64,64]")
+    Bsz, H = S.shape[:2]
+    _need(r.dim() == 4 and r.shape[0] == Bsz and r.shape[2] == H and r.shape[3] == N, "r must be [B,T,H,64]")
+    for t in (r, *rest):
+        _need(t.shape == r.shape and t.dtype == torch.float32, f"inputs must be f32 {tuple(r.shape)}")
+    return Bsz, r.shape[1], H
+
+
+def wkv7_f32(S: Tensor, r: Tensor, w: Tensor, k: Tensor, v: Tensor, a: Tensor, b: Tensor,
+             hist: Tensor | None = None) -> Tensor:
+    """``wkv7`` with every operand f32 (the training forward); ``S`` [B,H,64,64]
+    is updated in place and, if given, ``hist`` f32 [B,H,T,64,64] receives the
+    state entering each step (what ``wkv7_backward`` needs). Returns ``y``."""
+    _dev(S, r, w, k, v, a, b)
+    Bsz, T, H = _wkv7_f32_shapes(S, r, w, k, v, a, b)
+    if hist is not None:
+        _dev(hist)
+        _need(hist.dtype == torch.float32 and hist.shape == (Bsz, H, T, N, N), "hist must be f32 [B,H,T,64,64]")
+    y = torch.empty_like(r)
+    lib = _lib.load()
+    rc = lib.rwkv7_wkv7_f32(S.data_ptr(), r.data_ptr(), w.data_ptr(), k.data_ptr(), v.data_ptr(), a.data_ptr(),
+                            b.data_ptr(), y.data_ptr(), _lib.ptr(hist), Bsz, T, H, _lib.stream_handle())
+    _lib.check(rc, "rwkv7_wkv7_f32")
+    return y
+
+
+def wkv7_backward(hist: Tensor, S_T: Tensor, r: Tensor, w: Tensor, k: Tensor, v: Tensor, a: Tensor, b: Tensor,
+                  gy: Tensor, gS_T: Tensor | None = None) -> tuple[Tensor, ...]:
+    """Gradients of ``wkv7_f32``: ``(gS0, gr, gw, gk, gv, ga, gb)`` from
+    ``gy = dL/dy`` and ``gS_T = dL/dS_T`` (None: zero), all f32."""
+    _dev(hist, S_T, r, w, k, v, a, b, gy)
+    Bsz, T, H = _wkv7_f32_shapes(S_T, r, w, k, v, a, b, gy)
+    _need(hist.dtype == torch.float32 and hist.shape == (Bsz, H, T, N, N), "hist must be f32 [B,H,T,64,64]")
+    if gS_T is not None:
+        _dev(gS_T)
+        _need(gS_T.shape == S_T.shape and gS_T.dtype == torch.float32, "gS_T must be like S_T")
+    gS0 = torch.empty_like(S_T)
+    grads = [torch.empty_like(r) for _ in range(6)]
+    lib = _lib.load()
+    rc = lib.rwkv7_wkv7_backward(hist.data_ptr(), S_T.data_ptr(), r.data_ptr(), w.data_ptr(), k.data_ptr(),
+                                 v.data_ptr(), a.data_ptr(), b.data_ptr(), gy.data_ptr(), _lib.ptr(gS_T),
+                                 gS0.data_ptr(), *(g.data_ptr() for g in grads), Bsz, T, H, _lib.stream_handle())
+    _lib.check(rc, "rwkv7_wkv7_backward")
+    return (gS0, *grads)
+
+
+def dplr_seq_forward(S: Tensor, R: Tensor, W: Tensor, K: Tensor, V: Tensor, A: Tensor, B: Tensor):
+    """Functional DPLR sequence for training: ``S`` [H,64,64] or [B,H,64,64]
+    f32 is not modified; inputs [T,H,64] or [B,T,H,64] f32. Returns
+    ``(y, S_T)``."""
+    batched = S.dim() == 4
+    S1 = (S if batched else S.unsqueeze(0)).contiguous().clone()
+    ins = [(x if batched else x.unsqueeze(0)).contiguous() for x in (R, W, K, V, A, B)]
+    y = wkv7_f32(S1, ins[0], ins[1], ins[2], ins[3], ins[4], ins[5])
+    return (y, S1) if batched else (y[0], S1[0])
+
+
+def dplr_seq_backward(S: Tensor, R: Tensor, W: Tensor, K: Tensor, V: Tensor, A: Tensor, B: Tensor,
+                      gy: Tensor, gS: Tensor | None) -> tuple[Tensor, ...]:
+    """Gradients of ``dplr_seq_forward`` w.r.t. ``(S, R, W, K, V, A, B)``:
+    the forward is run again to record the per-step states (the reference's
+    plan, TODO.md:46-54), then the reverse-time scan."""
+    batched = S.dim() == 4
+    u = (lambda x: x) if batched else (lambda x: x.unsqueeze(0))
+    S1 = u(S).contiguous().clone()
+    ins = [u(x).contiguous() for x in (R, W, K, V, A, B)]
+    Bsz, H = S1.shape[:2]
+    T = ins[0].shape[1]
+    hist = torch.empty(Bsz, H, T, N, N, dtype=torch.float32, device=S.device)
+    wkv7_f32(S1, *ins, hist=hist)
+    out = wkv7_backward(hist, S1, *ins, u(gy).contiguous(), None if gS is None else u(gS).contiguous())
+    return out if batched else tuple(g[0] for g in out)
+
+
 def fused_dplr_T(S: Tensor, R: Tensor, W: Tensor, K: Tensor, V: Tensor, A: Tensor, B: Tensor):
     """Sequence DPLR: S [H,64,64] fp32 (in place), inputs [T,H,64]; returns (y [T,H,64], S)."""
     _need(S.dim() == 3, "S must be [H,64,64]")

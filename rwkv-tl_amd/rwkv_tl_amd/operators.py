@@ -115,6 +115,29 @@ OPS: dict[str, tuple[str, Callable, Callable]] = {
     ),
 }
 
+# The training operator (no counterpart in the reference's registry yet; its
+# TODO.md:46-54 plans exactly this: a DPLR custom op with register_autograd).
+# Functional, f32: S [H,64,64] or [B,H,64,64] is not modified; returns (y, S_T).
+TRAIN_OPS: dict[str, tuple[str, Callable, Callable]] = {
+    "fused_dplr_seq": (
+        "(Tensor S, Tensor R, Tensor W, Tensor K, Tensor V, Tensor A, Tensor B) -> (Tensor, Tensor)",
+        K.dplr_seq_forward,
+        lambda S, R, *_: (torch.empty_like(R), torch.empty_like(S)),
+    ),
+}
+
+
+def _dplr_seq_setup(ctx, inputs, output) -> None:
+    ctx.save_for_backward(*inputs)
+
+
+def _dplr_seq_backward(ctx, gy, gS):
+    S, R, W, K_, V, A, B = ctx.saved_tensors
+    if gy is None:
+        gy = torch.zeros_like(R)
+    return K.dplr_seq_backward(S, R, W, K_, V, A, B, gy.contiguous(), None if gS is None else gS.contiguous())
+
+
 _registered = False
 
 
@@ -123,11 +146,14 @@ def register() -> None:
     global _registered
     if _registered:
         return
-    for name, (schema, cuda, meta) in OPS.items():
+    for name, (schema, cuda, meta) in {**OPS, **TRAIN_OPS}.items():
         qual = f"{NAMESPACE}::{name}"
         torch.library.define(qual, schema)
         torch.library.impl(qual, "CUDA")(cuda)
         torch.library.impl(qual, "Meta")(meta)
+    torch.library.register_autograd(
+        f"{NAMESPACE}::fused_dplr_seq", _dplr_seq_backward, setup_context=_dplr_seq_setup
+    )
     _registered = True
 
 

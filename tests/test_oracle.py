@@ -176,6 +176,45 @@ def test_wkv7_brute_plants_detected():
         assert not agrees(bad), bad.__name__
 
 
+def _brute_loss(S, ins, gy, gS):
+    """L = <gy, y> + <gS, S_T> of wkv7_brute (pure-Python doubles); S [H,N,N],
+    ins six [T,H,N] nested lists."""
+    ys, ST = R.wkv7_brute(S, *ins)
+    L = 0.0
+    for t, yt in enumerate(ys):
+        for h, yh in enumerate(yt):
+            L += sum(yv * g for yv, g in zip(yh, gy[t][h]))
+    for h, Sh in enumerate(ST):
+        for i, row in enumerate(Sh):
+            L += sum(x * g for x, g in zip(row, gS[h][i]))
+    return L
+
+
+def test_wkv7_scan_grads_match_finite_differences():
+    """The oracle's DPLR gradients (torch autograd of the fp32 serial scan)
+    against central differences of the pure-Python double-precision loop, in
+    random directions through every input (S0, r, w, k, v, a, b)."""
+    g = torch.Generator().manual_seed(11)
+    H, N, T = 2, 4, 3
+    S = torch.randn(H, N, N, generator=g, dtype=torch.float64) * 0.5
+    ins = [torch.randn(T, H, N, generator=g, dtype=torch.float64) * 0.5 for _ in range(6)]
+    ins[1] = torch.rand(T, H, N, generator=g, dtype=torch.float64) * 0.5 + 0.45  # w in (0.45, 0.95)
+    gy = torch.randn(T, H, N, generator=g, dtype=torch.float64)
+    gS = torch.randn(H, N, N, generator=g, dtype=torch.float64)
+    # argument order of wkv7_brute / wkv7_scan: r, w, k, v, a, b
+    grads = R.wkv7_scan_grads(S.unsqueeze(0), *(x.unsqueeze(0) for x in ins), gy.unsqueeze(0), gS.unsqueeze(0))
+    eps = 1e-6
+    for trial in range(4):
+        dirs = [torch.randn(x.shape, generator=g, dtype=torch.float64) for x in [S] + ins]
+        def at(sign):
+            S2 = (S + sign * eps * dirs[0]).tolist()
+            i2 = [(x + sign * eps * d).tolist() for x, d in zip(ins, dirs[1:])]
+            return _brute_loss(S2, i2, gy.tolist(), gS.tolist())
+        fd = (at(1) - at(-1)) / (2 * eps)
+        an = sum(float((gr.double().reshape(d.shape) * d).sum()) for gr, d in zip(grads, dirs))
+        assert abs(fd - an) <= 1e-4 * max(1.0, abs(fd)), f"trial {trial}: finite difference {fd} vs autograd {an}"
+
+
 def test_wkv7_closed_forms():
     H, N, T = 2, 8, 5
     g = torch.Generator().manual_seed(3)
