@@ -114,6 +114,7 @@ static int64_t decode_ws(const rwkv7_dims &d, char *base, DecodeWs *w) {
 // Workspace of the batched path (M = B * T rows).
 struct BatchWs {
   float *x0, *rkv, *d, *vfirst, *kv, *y, *part;  // kv: gated k, mixed v [2][M][C]
+  float *proj1;  // one-token steps: r, k, v, raw LoRA first steps [M, 3C+SR]
   uint16_t *xmix, *l1, *yg, *hid, *headin;
   float *U, *Send, *Pend;  // segmented scan of long sequences (null with one segment)
 };
@@ -137,6 +138,7 @@ static int64_t batch_ws(const rwkv7_dims &d, int64_t B, int64_t T, char *base, B
   t.yg = reinterpret_cast<uint16_t *>(take(M * C * 2));
   t.hid = reinterpret_cast<uint16_t *>(take(M * F * 2));
   t.headin = reinterpret_cast<uint16_t *>(take(B * C * 2));
+  t.proj1 = T == 1 ? reinterpret_cast<float *>(take(M * (3 * C + SR) * 4)) : nullptr;
   const int cus = mk_cus() > 0 ? mk_cus() : 256;
   t.part = reinterpret_cast<float *>(take(gemm_ws_bytes((int)(M > B ? M : B), cus)));
   int seg_len;
@@ -212,6 +214,7 @@ static int decode_one(const rwkv7_model &m, const rwkv7_state &s, const int64_t 
     t.ra = d.rank_a;
     t.rg = d.rank_g;
     t.layer0 = l == 0;
+    t.yg16 = nullptr;
     RWKV7_TRY(launch_tmix_decode(t, 1, st));
 
     GemvArgs o = {};
@@ -294,6 +297,65 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
     RWKV7_TRY(launch_ln_shift(ls, st));
     const uint16_t *xr = w.xmix, *xw = w.xmix + MC, *xk = w.xmix + 2 * MC, *xv = w.xmix + 3 * MC,
                    *xa = w.xmix + 4 * MC, *xg = w.xmix + 5 * MC;
+    if (T == 1) {
+      // one token per sequence: r, k, v and the raw LoRA first steps into one
+      // [M, 3C+SR] f32 matrix, then the fused per-head kernel (LoRA second
+      // steps, gates, wkv7, GroupNorm, gate) writes the o-projection input
+      const int64_t ldp = 3 * C + SR;
+      float *proj = w.proj1;
+      GemmProb g1[7] = {
+          {xr, wrkv, proj, C, C, ldp, C, C, GEPI_F32},
+          {xk, wrkv + (int64_t)C * C, proj + C, C, C, ldp, C, C, GEPI_F32},
+          {xv, wrkv + 2 * (int64_t)C * C, proj + 2 * C, C, C, ldp, C, C, GEPI_F32},
+          {xv, wl1, proj + 3 * C, C, C, ldp, rv, C, GEPI_F32},
+          {xw, wl1 + (int64_t)rv * C, proj + 3 * C + rv, C, C, ldp, rw, C, GEPI_F32},
+          {xa, wl1 + (int64_t)(rv + rw) * C, proj + 3 * C + rv + rw, C, C, ldp, ra, C, GEPI_F32},
+          {xg, wl1 + (int64_t)(rv + rw + ra) * C, proj + 3 * C + rv + rw + ra, C, C, ldp, rg, C, GEPI_F32},
+      };
+      const char *Fl = m.layers_frag ? static_cast<const char *>(m.layers_frag) + (int64_t)l * lay.frag_bytes : nullptr;
+      auto frag = [&](GemmProb &p, int64_t off, int64_t strip0) {
+        if (!Fl) return;
+        p.nksf = (p.K + 31) / 32;
+        p.Wf = reinterpret_cast<const uint16_t *>(Fl + off) + strip0 * p.nksf * 512;
+      };
+      frag(g1[0], lay.f_rkv, 0);
+      frag(g1[1], lay.f_rkv, C / 16);
+      frag(g1[2], lay.f_rkv, 2 * C / 16);
+      for (int g = 0; g < 4; ++g) frag(g1[3 + g], lay.f_l1[g], 0);
+      RWKV7_TRY(launch_gemm_group(g1, 7, M, st, w.part, ctr));
+      TmixDecodeArgs td;
+      td.proj = proj;
+      td.ldp = ldp;
+      td.w_lora2 = wl2;
+      td.vec = vec;
+      td.vfirst = w.vfirst;
+      td.rnn = rnn;
+      td.xln = nullptr;
+      td.shift = nullptr;  // ln_shift wrote the shift state
+      td.yg = nullptr;
+      td.yg16 = w.yg;
+      td.C = C;
+      td.H = H;
+      td.rv = rv;
+      td.rw = rw;
+      td.ra = ra;
+      td.rg = rg;
+      td.layer0 = l == 0;
+      RWKV7_TRY(launch_tmix_decode(td, B, st));
+      GemmProb go = {w.yg, reinterpret_cast<const uint16_t *>(L + lay.w_o), w.x0, C, C, C, C, C, GEPI_ADD_F32};
+      frag(go, lay.f_o, 0);
+      RWKV7_TRY(launch_gemm_group(&go, 1, M, st, w.part, ctr));
+      LnShiftArgs lc = {w.x0, vec + RWKV7_V_LN2_W * C, vec + RWKV7_V_LN2_B * C, vec + RWKV7_V_FFN_X_K * C,
+                        1, w.xmix, cshift, C, T, M};
+      RWKV7_TRY(launch_ln_shift(lc, st));
+      GemmProb gk = {w.xmix, reinterpret_cast<const uint16_t *>(L + lay.w_fk), w.hid, C, C, F, F, C, GEPI_RELUSQ};
+      frag(gk, lay.f_fk, 0);
+      RWKV7_TRY(launch_gemm_group(&gk, 1, M, st, w.part, ctr));
+      GemmProb gv = {w.hid, reinterpret_cast<const uint16_t *>(L + lay.w_fv), w.x0, F, F, C, C, F, GEPI_ADD_F32};
+      frag(gv, lay.f_fv, 0);
+      RWKV7_TRY(launch_gemm_group(&gv, 1, M, st, w.part, ctr));
+      continue;
+    }
     GemmProb g1[7] = {
         {xr, wrkv, w.rkv, C, C, C, C, C, GEPI_F32},
         {xk, wrkv + (int64_t)C * C, w.rkv + MC, C, C, C, C, C, GEPI_F32},
@@ -409,10 +471,12 @@ int rwkv7_decode_launches(const rwkv7_model *model, int32_t batch, int32_t with_
   if (!model || check_dims(&model->dims) != RWKV7_OK || batch < 1) return -1;
   const rwkv7_dims *dims = &model->dims;
   if (use_persistent_decode(*dims, model->flags, batch, with_logits != 0)) return 1;
-  // decode_one: embed, 6 per layer, head GEMV; run_batched: embed, 10 per
-  // layer, final LayerNorm and head GEMM
+  // decode_one: embed, 6 per layer, head GEMV; run_batched with one token:
+  // embed, 7 per layer (LayerNorm + shift, projections, per-head core,
+  // o-projection, LayerNorm + shift, FFN key, FFN value), final LayerNorm and
+  // head GEMM
   if (batch == 1) return 1 + 6 * dims->n_layer + (with_logits ? 1 : 0);
-  return 1 + 10 * dims->n_layer + (with_logits ? 2 : 0);
+  return 1 + 7 * dims->n_layer + (with_logits ? 2 : 0);
 }
 
 int rwkv7_decode(const rwkv7_model *model, const rwkv7_state *state, const int64_t *tokens, void *logits,

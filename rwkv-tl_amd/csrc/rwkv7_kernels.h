@@ -25,6 +25,12 @@ struct GemvArgs {
 };
 template <int PRO, int EPI> int launch_gemv(const GemvArgs &a, hipStream_t st);
 
+// One token per sequence, grid (H, B): LoRA second step, gates, L2 norm,
+// wkv7, GroupNorm, bonus and output gate. proj f32 [B, ldp] holds r, k, v
+// and the raw LoRA first steps; the gated output goes to yg (f32) or, if
+// yg16 is set, to yg16 (f16, the A operand of the batched o-projection).
+// shift (with xln) receives the time-mix shift state; null when the caller
+// already wrote it.
 struct TmixDecodeArgs {
   const float *proj;
   int64_t ldp;
@@ -36,6 +42,7 @@ struct TmixDecodeArgs {
   uint16_t *shift;
   float *yg;
   int C, H, rv, rw, ra, rg, layer0;
+  uint16_t *yg16;
 };
 int launch_tmix_decode(const TmixDecodeArgs &a, int B, hipStream_t st);
 

@@ -48,6 +48,7 @@ __global__ __launch_bounds__(256) void tmix_decode_kernel(TmixDecodeArgs a) {
     const int R = q == 0 ? a.rv : q == 1 ? a.rw : q == 2 ? a.ra : a.rg;
     const uint4 *wr = reinterpret_cast<const uint4 *>(a.w_lora2 + (int64_t)(h * kN + c) * SR + off);
     float acc = 0.f;
+#pragma unroll 4
     for (int r = 0; r < R; r += 8) {
       float wf[8];
       h8_to_f(wr[r >> 3], wf);
@@ -78,7 +79,7 @@ __global__ __launch_bounds__(256) void tmix_decode_kernel(TmixDecodeArgs a) {
     s_r[t] = r; s_w[t] = w; s_k[t] = kn; s_v[t] = v;
     s_a[t] = kh; s_b[t] = -kh * ag; s_g[t] = s_d[3][t];
     if (t == 0) s_rk = rk;
-    a.shift[(int64_t)b * C + ch] = f2h(a.xln[(int64_t)b * C + ch]);
+    if (a.shift) a.shift[(int64_t)b * C + ch] = f2h(a.xln[(int64_t)b * C + ch]);
   }
   __syncthreads();
 
@@ -117,7 +118,9 @@ __global__ __launch_bounds__(256) void tmix_decode_kernel(TmixDecodeArgs a) {
     const float d = y - mean;
     const float var = wave_sum(d * d) * (1.f / kN);
     const float yn = d * rsqrtf(var + kGnEps) * vec[RWKV7_V_LNX_W * C + ch] + vec[RWKV7_V_LNX_B * C + ch];
-    a.yg[(int64_t)b * C + ch] = (yn + s_rk * s_v[t]) * s_g[t];
+    const float out = (yn + s_rk * s_v[t]) * s_g[t];
+    if (a.yg16) a.yg16[(int64_t)b * C + ch] = f2h(out);
+    else a.yg[(int64_t)b * C + ch] = out;
   }
 }
 

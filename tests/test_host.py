@@ -47,7 +47,7 @@ def test_decode_path_decision_without_a_device(shape):
     """The persistent decode kernel is chosen only when the device's CU count
     and occupancy for it are known to fit its grid at once; with no device
     (this host) the library reports the multi-launch path: embed, six launches
-    per layer and the head for batch 1; embed, ten per layer, LayerNorm and
+    per layer and the head for batch 1; embed, seven per layer, LayerNorm and
     head GEMM for a batch. The model flag gives the same count on any host."""
     lib = _lib.load()
     d = _dims(shape)
@@ -55,7 +55,7 @@ def test_decode_path_decision_without_a_device(shape):
     L = d.n_layer
     assert lib.rwkv7_decode_launches(ctypes.byref(m), 1, 1) == 1 + 6 * L + 1
     assert lib.rwkv7_decode_launches(ctypes.byref(m), 1, 0) == 1 + 6 * L
-    assert lib.rwkv7_decode_launches(ctypes.byref(m), 4, 1) == 1 + 10 * L + 2
+    assert lib.rwkv7_decode_launches(ctypes.byref(m), 4, 1) == 1 + 7 * L + 2
     m.flags = _lib.MODEL_MULTI_LAUNCH_DECODE
     assert lib.rwkv7_decode_launches(ctypes.byref(m), 1, 1) == 1 + 6 * L + 1
     assert lib.rwkv7_decode_launches(None, 1, 1) == -1
