@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define RWKV7_ABI_VERSION 5
+#define RWKV7_ABI_VERSION 6
 #define RWKV7_HEAD_SIZE 64
 
 enum {
@@ -78,11 +78,21 @@ enum {
  *   f_l2[g]  [C, R_g]      second LoRA steps (K = R_g)
  *   f_o [C, C], f_fk [F, C], f_fv [C, F]
  * frag_bytes is the fragment arena size, a multiple of 256. */
+/* Int8 arena, an optional third copy for batch-1 decode with int8 weights
+ * (RWKV7_MODEL_INT8_DECODE): the matrices the decode streams, symmetric per
+ * row, W[n, :] ~ scale[n] * q[n, :] with q int8 in [-127, 127] and scale f32:
+ *   q_rkv [3C+SR, C]   the rows of w_rkv and w_lora1
+ *   q_o [C, C], q_fk [F, C], q_fv [C, F]
+ *   q_scale f32 [3C+SR + C + F + C]: the rows' scales in that order
+ * q_bytes is the int8 arena size, a multiple of 256. The LoRA second steps
+ * and the vectors stay in the f16 arena. */
 typedef struct rwkv7_layer_layout {
   int64_t w_rkv, w_lora1, w_lora2, w_o, w_fk, w_fv, vec;
   int64_t bytes; /* arena size, a multiple of 256 */
   int64_t f_rkv, f_l1[4], f_l2[4], f_o, f_fk, f_fv;
   int64_t frag_bytes;
+  int64_t q_rkv, q_o, q_fk, q_fv, q_scale;
+  int64_t q_bytes;
 } rwkv7_layer_layout;
 
 /* Device-side model. Layer i's arena starts at layers + i * layout.bytes.
@@ -99,11 +109,23 @@ typedef struct rwkv7_model {
   const void *layers_frag; /* optional: L fragment arenas */
   const void *head_frag;   /* optional: head in fragment order */
   uint32_t flags;          /* RWKV7_MODEL_* path choices, 0 for the defaults */
+  const void *layers_q;    /* optional: L int8 arenas (layers_q + i * layout.q_bytes) */
+  const void *head_q;      /* optional: head int8 [V, C], then f32 scales [V] at byte
+                              offset rwkv7_head_q_scale_offset(dims) */
 } rwkv7_model;
 
 /* rwkv7_model.flags: run batch-1 decode as one launch per stage (the
  * multi-launch GEMV path) instead of the single persistent kernel. */
 #define RWKV7_MODEL_MULTI_LAUNCH_DECODE 1u
+/* rwkv7_model.flags: batch-1 decode streams the int8 arenas (layers_q,
+ * head_q; both required) in the persistent kernel, dequantising in the dot
+ * products: half the weight bytes of the f16 decode. The weight-only
+ * quantisation the reference plans inside its hand-written decode GEMV
+ * (TODO.md:58-63). Prefill and batched decode still read the f16 arenas.
+ * A batch-1 decode that cannot run that kernel (no logits requested, the
+ * multi-launch flag, a device without the grid) fails with RWKV7_ESHAPE
+ * rather than running on f16 weights. */
+#define RWKV7_MODEL_INT8_DECODE 2u
 
 /* Recurrent state of `batch` independent sequences, layer-major arenas
  * (src/rwkv_tl/state.py:35-44 plus a leading batch dimension):
@@ -127,6 +149,10 @@ const char *rwkv7_strerror(int code);
  * (n_embd != 64 * n_head, n_embd % 256, n_ffn % 256, ranks % 8, sum of ranks
  * > 512). */
 int rwkv7_layer_layout_get(const rwkv7_dims *dims, rwkv7_layer_layout *out);
+
+/* Byte offset of the f32 row scales inside the int8 head (after V * C bytes,
+ * rounded up to 256), or -1 for unsupported dims. */
+int64_t rwkv7_head_q_scale_offset(const rwkv7_dims *dims);
 
 /* Bytes of scratch that rwkv7_decode / rwkv7_prefill need for `batch`
  * sequences of `seq_len` tokens (seq_len 1 for decode). The workspace must be

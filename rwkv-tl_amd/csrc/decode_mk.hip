@@ -139,6 +139,12 @@ struct MkArgs {
   uint64_t *x_ex, *proj_ex, *core_ex, *hid_ex;
   unsigned *sync;
   unsigned *started;  // [kMaxG] start words
+  // int8 weights (the Q8 instance): per-layer arenas and their sections, the
+  // head and its row scales
+  const char *layers_q;
+  int64_t q_lbytes, q_rkv, q_o, q_fk, q_fv, q_scale;
+  const uint16_t *head_q;  // int8 rows of C bytes, addressed in 16-bit units
+  const float *head_qs;
 };
 
 // Row ranges and roles, computed identically by every wave of a workgroup.
@@ -262,6 +268,51 @@ RWKV7_DEV float row_dot(const uint4 (&w)[NC], const float *x, int nch) {
     acc[c & 1] = a;
   }
   return wave_sum(acc[0] + acc[1]);
+}
+
+// The same for an int8 row: lane l has chunks l + 64c of 16 weights, each
+// dotted with 16 inputs; the row's scale is applied by the caller.
+template <int NC>
+RWKV7_DEV float row_dot_q8(const uint4 (&w)[NC], const float *x, int nch) {
+  const int lane = threadIdx.x & 63;
+  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+  float4 xs[NC][4];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    int j = lane + 64 * c;
+    j = j < nch ? j : nch - 1;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xs[c][q] = x4[4 * j + q];
+  }
+  sched_fence();
+  float acc[2] = {0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const unsigned wd[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float a = acc[q & 1];
+      a = fmaf((float)(int)(signed char)(wd[q] & 0xFF), xs[c][q].x, a);
+      a = fmaf((float)(int)(signed char)((wd[q] >> 8) & 0xFF), xs[c][q].y, a);
+      a = fmaf((float)(int)(signed char)((wd[q] >> 16) & 0xFF), xs[c][q].z, a);
+      a = fmaf((float)(int)(signed char)(wd[q] >> 24), xs[c][q].w, a);
+      acc[q & 1] = a;
+    }
+  }
+  return wave_sum(acc[0] + acc[1]);
+}
+
+// acc + sum_e q[e] * x[e] for 16 int8 weights and 16 f32 inputs in registers.
+RWKV7_DEV float dot16r_q8(const uint4 &w, const float (&x)[16], float acc) {
+  const unsigned wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    acc = fmaf((float)(int)(signed char)(wd[q] & 0xFF), x[4 * q], acc);
+    acc = fmaf((float)(int)(signed char)((wd[q] >> 8) & 0xFF), x[4 * q + 1], acc);
+    acc = fmaf((float)(int)(signed char)((wd[q] >> 16) & 0xFF), x[4 * q + 2], acc);
+    acc = fmaf((float)(int)(signed char)(wd[q] >> 24), x[4 * q + 3], acc);
+  }
+  return acc;
 }
 
 // Loads row r of W (row stride ld halfs, nch 16-byte chunks) as lane chunks.
@@ -778,7 +829,7 @@ RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
 // vectors). They stream while the head workgroups run P2 (the layer's longest
 // wait), and a single vmcnt(0) at the start of P3 covers them all, so the
 // later hand-offs of the layer run with no weight traffic in flight.
-template <int CPL, int RM, int NC5, int VPL, int NHB>
+template <int CPL, int RM, int NC5, int VPL, int NHB, bool Q8>
 RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, const MkCtx &cx, int wv) {
   // Math threads are 0..kMT-1. refresh() passes the thread index through an
   // empty asm at each stage, so per-thread addresses are recomputed there
@@ -790,19 +841,41 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
   };
   const int C = m.C, F = m.F, L = m.L;
   const int nchC = C >> 3, nchF = F >> 3;
+  // Weight rows: f16 (8 per 16-byte chunk) or int8 (16 per chunk, with an
+  // f32 scale per row). CW / N5: chunks per lane of a C-long / F-long row;
+  // wchC / wchF: chunks of a row; wld: row stride of a C-long row in halfs.
+  constexpr int CW = Q8 ? (CPL + 1) / 2 : CPL;
+  constexpr int N5 = Q8 ? (NC5 + 1) / 2 : NC5;
+  const int wchC = Q8 ? C >> 4 : nchC, wchF = Q8 ? F >> 4 : nchF;
+  const int wldC = Q8 ? C >> 1 : C, wldF = Q8 ? F >> 1 : F;
 
-  uint4 w1[RM][CPL];
+  uint4 w1[RM][CW];
   float v1w[VPL], v1b[VPL], mu1[4][VPL];
   uint16_t pv1[VPL];
-  uint4 w3[CPL];
-  uint4 w4[RM][CPL];
+  uint4 w3[CW];
+  uint4 w4[RM][CW];
   float v4w[VPL], v4b[VPL], mu4[VPL];
   uint16_t pv4[VPL];
-  uint4 w5[NC5];
-  uint4 wh[kHRing][kHB][CPL];
+  uint4 w5[N5];
+  uint4 wh[kHRing][kHB][CW];
   float hlw[VPL], hlb[VPL];
+  float q1s[RM], q3s = 1.f, q4s[RM], q5s = 1.f;  // int8 row scales
+  float hqs[kHRing][kHB];
 
   auto layer_ptr = [&](int l) { return a.layers + (int64_t)l * a.lbytes; };
+  auto qlayer = [&](int l) { return a.layers_q + (int64_t)l * a.q_lbytes; };
+  // the matrix rows a stage streams, and their scales (int8) in the order of
+  // the layout's scale section: P1 rows, o rows, FFN key rows, FFN value rows
+  auto wbase = [&](int l, int64_t o16, int64_t o8) {
+    return reinterpret_cast<const uint16_t *>(Q8 ? qlayer(l) + o8 : layer_ptr(l) + o16);
+  };
+  auto qscale = [&](int l, int row) { return reinterpret_cast<const float *>(qlayer(l) + a.q_scale)[row]; };
+  const int N1 = 3 * C + m.SR;
+  // a row's dot product, scale included
+  auto rdot = [&](const auto &w, const float *x, int nch, float sc) {
+    if constexpr (Q8) return row_dot_q8(w, x, nch) * sc;
+    else return row_dot(w, x, nch);
+  };
   auto vec_ptr = [&](int l) { return reinterpret_cast<const float *>(layer_ptr(l) + a.o_vec); };
   // Vector loads are unconditional (index clamped; elements past C are never
   // used): a load under a branch makes the compiler wait for it inside the
@@ -823,11 +896,12 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     }
   };
   auto pre_p1 = [&](int l) {
-    const uint16_t *W = reinterpret_cast<const uint16_t *>(layer_ptr(l) + a.o_rkv);
+    const uint16_t *W = wbase(l, a.o_rkv, a.q_rkv);
 #pragma unroll
     for (int i = 0; i < RM; ++i) {
       const int r = m.p1a + wv + kMW * i;
-      load_row<CPL>(W, C, r, r < m.p1b, nchC, w1[i]);
+      load_row<CW>(W, wldC, r, r < m.p1b, wchC, w1[i]);
+      if constexpr (Q8) q1s[i] = qscale(l, r < N1 ? r : N1 - 1);
     }
     const float *vec = vec_ptr(l);
     ld_vec(v1w, vec + RWKV7_V_LN1_W * C);
@@ -839,16 +913,18 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     sched_fence();
   };
   auto pre_p3 = [&](int l) {
-    const uint16_t *W = reinterpret_cast<const uint16_t *>(layer_ptr(l) + a.o_o);
-    load_row<CPL>(W, C, m.owa + wv, wv < m.nown, nchC, w3);
+    const uint16_t *W = wbase(l, a.o_o, a.q_o);
+    load_row<CW>(W, wldC, m.owa + wv, wv < m.nown, wchC, w3);
+    if constexpr (Q8) q3s = qscale(l, N1 + (m.owa + wv < C ? m.owa + wv : C - 1));
     sched_fence();
   };
   auto pre_p4 = [&](int l) {
-    const uint16_t *W = reinterpret_cast<const uint16_t *>(layer_ptr(l) + a.o_fk);
+    const uint16_t *W = wbase(l, a.o_fk, a.q_fk);
 #pragma unroll
     for (int i = 0; i < RM; ++i) {
       const int r = m.p4a + wv + kMW * i;
-      load_row<CPL>(W, C, r, r < m.p4b, nchC, w4[i]);
+      load_row<CW>(W, wldC, r, r < m.p4b, wchC, w4[i]);
+      if constexpr (Q8) q4s[i] = qscale(l, N1 + C + (r < F ? r : F - 1));
     }
     const float *vec = vec_ptr(l);
     ld_vec(v4w, vec + RWKV7_V_LN2_W * C);
@@ -858,8 +934,9 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     sched_fence();
   };
   auto pre_p5 = [&](int l) {
-    const uint16_t *W = reinterpret_cast<const uint16_t *>(layer_ptr(l) + a.o_fv);
-    load_row<NC5>(W, F, m.owa + wv, wv < m.nown, nchF, w5);
+    const uint16_t *W = wbase(l, a.o_fv, a.q_fv);
+    load_row<N5>(W, wldF, m.owa + wv, wv < m.nown, wchF, w5);
+    if constexpr (Q8) q5s = qscale(l, N1 + C + F + (m.owa + wv < C ? m.owa + wv : C - 1));
     sched_fence();
   };
   // head rows of this wave: a contiguous range, kHB rows per batch
@@ -868,16 +945,17 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
   // Head loads are unconditional (rows and chunks clamped into range, unused
   // lanes later multiply by a zero input) so that the unrolled head loop issues
   // a fixed number of loads and the compiler's load counting stays exact.
-  auto pre_head = [&](int b, uint4 (&dst)[kHB][CPL]) {
+  auto pre_head = [&](int b, uint4 (&dst)[kHB][CW]) {
 #pragma unroll
     for (int k = 0; k < kHB; ++k) {
       int r = hr0 + kHB * b + k;
       r = r < m.hb ? r : m.hb - 1;
-      const uint4 *row = reinterpret_cast<const uint4 *>(a.head + (int64_t)r * C);
+      const uint4 *row = reinterpret_cast<const uint4 *>((Q8 ? a.head_q : a.head) + (int64_t)r * wldC);
+      if constexpr (Q8) hqs[b % kHRing][k] = a.head_qs[r];
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) {
+      for (int c = 0; c < CW; ++c) {
         const int j = lane + 64 * c;
-        dst[k][c] = ld_stream(row + (j < nchC ? j : nchC - 1));
+        dst[k][c] = ld_stream(row + (j < wchC ? j : wchC - 1));
       }
     }
     sched_fence();
@@ -949,7 +1027,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
       for (int i = 0; i < RM; ++i) {
         const int r = m.p1a + wv + kMW * i;
         if (r < m.p1b) {
-          const float d = row_dot<CPL>(w1[i], s.mix + (m.seg_of(r) - m.seg0) * C, nchC);
+          const float d = rdot(w1[i], s.mix + (m.seg_of(r) - m.seg0) * C, wchC, Q8 ? q1s[i] : 1.f);
           if (lane < kRep && ok) publish(a.proj_ex + (int64_t)lane * (3 * C + m.SR) + r, tg, d);
         }
       }
@@ -969,7 +1047,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     // ---------------- P3: o-projection + residual -----------------------------
     refresh();
     if (wv < m.nown && !cx.failed()) {
-      const float d = row_dot<CPL>(w3, s.core_in, nchC);
+      const float d = rdot(w3, s.core_in, wchC, q3s);
       xown += d;
       const int c = m.owa + wv;
       if (lane < kRep) publish(a.x_ex + (int64_t)lane * C + c, cx.tag(ph + 2), xown);
@@ -1008,7 +1086,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
       for (int i = 0; i < RM; ++i) {
         const int r = m.p4a + wv + kMW * i;
         if (r < m.p4b) {
-          const float q = fmaxf(row_dot<CPL>(w4[i], s.mix4, nchC), 0.f);
+          const float q = fmaxf(rdot(w4[i], s.mix4, wchC, Q8 ? q4s[i] : 1.f), 0.f);
           if (lane < kRep && ok) publish(a.hid_ex + (int64_t)lane * F + r, tg, q * q);
         }
       }
@@ -1027,7 +1105,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     // ---------------- P5: FFN value + residual --------------------------------
     refresh();
     if (wv < m.nown && !cx.failed()) {
-      const float d = row_dot<NC5>(w5, s.hid, nchF);
+      const float d = rdot(w5, s.hid, wchF, q5s);
       xown += d;
       const int c = m.owa + wv;
       if (lane < kRep) publish(a.x_ex + (int64_t)lane * C + c, cx.tag(ph + 4), xown);
@@ -1055,23 +1133,28 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
   }
   __syncthreads();  // BH
   const bool bad = cx.failed() || glob_abort;
-  float xr[CPL][8];
+  constexpr int XE = Q8 ? 16 : 8;  // inputs per weight chunk
+  float xr[CW][XE];
 #pragma unroll
-  for (int c = 0; c < CPL; ++c) {
+  for (int c = 0; c < CW; ++c) {
     const int j = lane + 64 * c;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) xr[c][e] = j < nchC ? s.mix[8 * j + e] : 0.f;
+    for (int e = 0; e < XE; ++e) xr[c][e] = j < wchC ? s.mix[XE * j + e] : 0.f;
   }
   float out = 0.f;  // lane k: logit of row hr0 + k
 #pragma unroll
   for (int b = 0; b < NHB; ++b) {
-    uint4 (&cur)[kHB][CPL] = wh[b % kHRing];
+    uint4 (&cur)[kHB][CW] = wh[b % kHRing];
 #pragma unroll
     for (int k = 0; k < kHB; ++k) {
       float acc = 0.f;
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) acc = dot8r(cur[k][c], xr[c], acc);
+      for (int c = 0; c < CW; ++c) {
+        if constexpr (Q8) acc = dot16r_q8(cur[k][c], xr[c], acc);
+        else acc = dot8r(cur[k][c], xr[c], acc);
+      }
       acc = wave_sum(acc);
+      if constexpr (Q8) acc *= hqs[b % kHRing][k];
       if (lane == kHB * b + k) out = acc;
     }
     if (b + kHRing < NHB) pre_head(b + kHRing, cur);
@@ -1083,7 +1166,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
 // One workgroup per CU by construction (2 waves per SIMD): telling the
 // compiler so keeps its scheduler from trading prefetch distance for an
 // occupancy this kernel never runs at.
-template <int CPL, int RM, int NC5, int VPL, int NL2, int NHB>
+template <int CPL, int RM, int NC5, int VPL, int NL2, int NHB, bool Q8>
 __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_mk_kernel(MkArgs a) {
   extern __shared__ __align__(16) float smem[];
   MkGeom m;
@@ -1143,7 +1226,7 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     else math_head<NL2>(a, m, s, cx, wv);
   } else {
     if (wv >= kMW) comm_worker<NC5 / 2>(a, m, s, cx);
-    else math_worker<CPL, RM, NC5, VPL, NHB>(a, m, s, cx, wv);
+    else math_worker<CPL, RM, NC5, VPL, NHB, Q8>(a, m, s, cx, wv);
   }
   // The next launch's epoch. In a launch that completed, this worker ends only
   // after every workgroup has published (its logits need the last layer's x,
@@ -1163,9 +1246,10 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 
 // ---- host side --------------------------------------------------------------
 
-// The one compiled instance: CPL 2, RM 3, NC5 8, VPL 3, NL2 8, NHB 10.
+// The compiled instances: CPL 2, RM 3, NC5 8, VPL 3, NL2 8, NHB 10, with f16
+// or int8 weights.
 constexpr int kCPL = 2, kRM = 3, kNC5 = 8, kVPL = 3, kNL2 = 8, kNHB = 10;
-#define RWKV7_MK_INSTANCE decode_mk_kernel<kCPL, kRM, kNC5, kVPL, kNL2, kNHB>
+#define RWKV7_MK_INSTANCE(Q8) decode_mk_kernel<kCPL, kRM, kNC5, kVPL, kNL2, kNHB, Q8>
 
 static int cdiv(int a, int b) { return (a + b - 1) / b; }
 
@@ -1175,8 +1259,8 @@ static int cdiv(int a, int b) { return (a + b - 1) / b; }
 constexpr int kMaxDevices = 64;
 struct MkDevice {
   std::atomic<int> cus{0};
-  std::atomic<int64_t> lds_allowed{0};
-  std::atomic<int64_t> resident_lds{0};  // largest LDS size found co-resident
+  std::atomic<int64_t> lds_allowed[2] = {{0}, {0}};   // per instance (f16, int8)
+  std::atomic<int64_t> resident_lds[2] = {{0}, {0}};  // largest LDS size found co-resident
 };
 static MkDevice g_mk_dev[kMaxDevices];
 
@@ -1211,19 +1295,19 @@ int64_t mk_exchange_bytes(int C, int F, int SR) {
 // Allows the kernel its dynamic LDS on the current device and checks that a
 // grid of one workgroup per CU can be resident at once (the occupancy of this
 // kernel instance with that LDS is at least one workgroup per CU).
-static bool mk_prepare(int64_t lds) {
+static bool mk_prepare(int64_t lds, bool q8) {
   MkDevice *d = mk_device();
   if (!d) return false;
-  const void *fn = (const void *)RWKV7_MK_INSTANCE;
-  if (lds > d->lds_allowed.load(std::memory_order_relaxed)) {
+  const void *fn = q8 ? (const void *)RWKV7_MK_INSTANCE(true) : (const void *)RWKV7_MK_INSTANCE(false);
+  if (lds > d->lds_allowed[q8].load(std::memory_order_relaxed)) {
     if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) return false;
-    d->lds_allowed.store(lds, std::memory_order_relaxed);
+    d->lds_allowed[q8].store(lds, std::memory_order_relaxed);
   }
-  if (lds <= d->resident_lds.load(std::memory_order_relaxed)) return true;
+  if (lds <= d->resident_lds[q8].load(std::memory_order_relaxed)) return true;
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kT, (size_t)lds) != hipSuccess || per_cu < 1)
     return false;
-  d->resident_lds.store(lds, std::memory_order_relaxed);
+  d->resident_lds[q8].store(lds, std::memory_order_relaxed);
   return true;
 }
 
@@ -1271,11 +1355,15 @@ bool mk_supported(const rwkv7_dims &d, int G) {
   return mk_lds_bytes(C, F, SR) <= 160 * 1024;
 }
 
-bool mk_usable(const rwkv7_dims &d) {
+bool mk_usable(const rwkv7_dims &d, bool q8) {
   const int G = mk_cus();
   if (G < 1 || !mk_supported(d, G)) return false;
   const int SR = d.rank_w + d.rank_a + d.rank_v + d.rank_g;
-  return mk_prepare(mk_lds_bytes(d.n_embd, d.n_ffn, SR));
+  return mk_prepare(mk_lds_bytes(d.n_embd, d.n_ffn, SR), q8);
+}
+
+bool mk_int8(const rwkv7_model &m) {
+  return (m.flags & RWKV7_MODEL_INT8_DECODE) && m.layers_q != nullptr && m.head_q != nullptr;
 }
 
 int launch_decode_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const rwkv7_state &s,
@@ -1284,8 +1372,20 @@ int launch_decode_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const 
   const int SR = d.rank_w + d.rank_a + d.rank_v + d.rank_g;
   const int G = mk_cus();
   const int C = d.n_embd, F = d.n_ffn;
-  if (!mk_usable(d)) return RWKV7_ESHAPE;
+  const bool q8 = mk_int8(m);
+  if (!mk_usable(d, q8)) return RWKV7_ESHAPE;
   MkArgs a;
+  a.layers_q = static_cast<const char *>(m.layers_q);
+  a.q_lbytes = lay.q_bytes;
+  a.q_rkv = lay.q_rkv;
+  a.q_o = lay.q_o;
+  a.q_fk = lay.q_fk;
+  a.q_fv = lay.q_fv;
+  a.q_scale = lay.q_scale;
+  a.head_q = static_cast<const uint16_t *>(m.head_q);
+  a.head_qs = m.head_q ? reinterpret_cast<const float *>(static_cast<const char *>(m.head_q) +
+                                                         ((int64_t)d.vocab * C + 255) / 256 * 256)
+                       : nullptr;
   a.layers = static_cast<const char *>(m.layers);
   a.lbytes = lay.bytes;
   a.o_rkv = lay.w_rkv;
@@ -1319,7 +1419,8 @@ int launch_decode_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const 
   a.core_ex = a.proj_ex + (int64_t)kRep * (3 * C + SR);
   a.hid_ex = a.core_ex + (int64_t)kRep * C;
   const int64_t lds = mk_lds_bytes(C, F, SR);
-  RWKV7_MK_INSTANCE<<<G, kT, lds, st>>>(a);
+  if (q8) RWKV7_MK_INSTANCE(true)<<<G, kT, lds, st>>>(a);
+  else RWKV7_MK_INSTANCE(false)<<<G, kT, lds, st>>>(a);
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;
 }

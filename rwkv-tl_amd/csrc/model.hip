@@ -70,6 +70,19 @@ static void layout_of(const rwkv7_dims &d, rwkv7_layer_layout *o) {
   o->f_fv = off;
   off = align256(off + frag_bytes(C, F));
   o->frag_bytes = off;
+  // int8 arena
+  off = 0;
+  o->q_rkv = off;
+  off = align256(off + (3 * C + SR) * C);
+  o->q_o = off;
+  off = align256(off + C * C);
+  o->q_fk = off;
+  off = align256(off + F * C);
+  o->q_fv = off;
+  off = align256(off + C * F);
+  o->q_scale = off;
+  off = align256(off + (3 * C + SR + C + F + C) * 4);
+  o->q_bytes = off;
 }
 
 // Workspace of the one-sequence decode path (GEMV kernels).
@@ -429,9 +442,9 @@ static int check_model_state(const rwkv7_model *m, const rwkv7_state *s) {
 // for the sizes it was compiled for and when its grid fits on the device at
 // once; the model flag RWKV7_MODEL_MULTI_LAUNCH_DECODE selects the
 // multi-launch path instead.
-static bool use_persistent_decode(const rwkv7_dims &d, uint32_t flags, int batch, bool logits) {
-  if (batch != 1 || !logits || (flags & RWKV7_MODEL_MULTI_LAUNCH_DECODE)) return false;
-  return mk_usable(d);
+static bool use_persistent_decode(const rwkv7_model &m, int batch, bool logits) {
+  if (batch != 1 || !logits || (m.flags & RWKV7_MODEL_MULTI_LAUNCH_DECODE)) return false;
+  return mk_usable(m.dims, mk_int8(m));
 }
 
 }  // namespace rwkv7
@@ -460,6 +473,11 @@ int rwkv7_layer_layout_get(const rwkv7_dims *dims, rwkv7_layer_layout *out) {
   return RWKV7_OK;
 }
 
+int64_t rwkv7_head_q_scale_offset(const rwkv7_dims *dims) {
+  if (check_dims(dims) != RWKV7_OK) return -1;
+  return align256((int64_t)dims->vocab * dims->n_embd);
+}
+
 int64_t rwkv7_workspace_bytes(const rwkv7_dims *dims, int32_t batch, int32_t seq_len) {
   if (check_dims(dims) != RWKV7_OK || batch < 1 || seq_len < 1) return -1;
   const int64_t a = decode_ws(*dims, nullptr, nullptr);
@@ -470,7 +488,7 @@ int64_t rwkv7_workspace_bytes(const rwkv7_dims *dims, int32_t batch, int32_t seq
 int rwkv7_decode_launches(const rwkv7_model *model, int32_t batch, int32_t with_logits) {
   if (!model || check_dims(&model->dims) != RWKV7_OK || batch < 1) return -1;
   const rwkv7_dims *dims = &model->dims;
-  if (use_persistent_decode(*dims, model->flags, batch, with_logits != 0)) return 1;
+  if (use_persistent_decode(*model, batch, with_logits != 0)) return 1;
   // decode_one: embed, 6 per layer, head GEMV; run_batched with one token:
   // embed, 7 per layer (LayerNorm + shift, projections, per-head core,
   // o-projection, LayerNorm + shift, FFN key, FFN value), final LayerNorm and
@@ -485,8 +503,14 @@ int rwkv7_decode(const rwkv7_model *model, const rwkv7_state *state, const int64
   if (!tokens || !workspace) return RWKV7_EINVAL;
   if (workspace_bytes < rwkv7_workspace_bytes(&model->dims, state->batch, 1)) return RWKV7_EWORKSPACE;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // int8 weights exist only for the persistent batch-1 kernel: a batch-1
+  // decode with the flag set that cannot run it is an error, not an f16
+  // fallback (batched decode reads the f16 arenas, as documented)
+  if ((model->flags & RWKV7_MODEL_INT8_DECODE) && state->batch == 1 &&
+      (!mk_int8(*model) || !use_persistent_decode(*model, 1, logits != nullptr)))
+    return RWKV7_ESHAPE;
   if (state->batch == 1) {
-    if (use_persistent_decode(model->dims, model->flags, 1, logits != nullptr)) {
+    if (use_persistent_decode(*model, 1, logits != nullptr)) {
       rwkv7_layer_layout lay;
       layout_of(model->dims, &lay);
       return launch_decode_mk(*model, lay, *state, tokens, logits, static_cast<char *>(workspace), st);

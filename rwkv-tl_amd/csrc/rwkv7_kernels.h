@@ -153,9 +153,11 @@ int launch_gn_rkrk(const uint16_t *y, const uint16_t *r, const uint16_t *k, cons
 // One-token, one-sequence decode as a single persistent kernel (decode_mk.hip).
 int mk_cus();
 bool mk_supported(const rwkv7_dims &d, int G);
-// mk_supported on the current device's CU count, and the kernel's grid fits
-// there all at once (checked once per device)
-bool mk_usable(const rwkv7_dims &d);
+// mk_supported on the current device's CU count, and the kernel's grid (the
+// int8-weight instance if q8) fits there all at once (checked once per device)
+bool mk_usable(const rwkv7_dims &d, bool q8);
+// the model asks for int8 decode and has the int8 arenas
+bool mk_int8(const rwkv7_model &m);
 int64_t mk_exchange_bytes(int C, int F, int SR);
 int launch_decode_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const rwkv7_state &s,
                      const int64_t *tok, void *logits, char *xreg, hipStream_t st);

@@ -15,10 +15,11 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the HIP library)
 
 LIB_NAME = "librwkv7_hip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # rwkv7_model.flags
 MODEL_MULTI_LAUNCH_DECODE = 1
+MODEL_INT8_DECODE = 2
 
 # enum indices of the per-layer fp32 vector block (RWKV7_V_*)
 VEC_NAMES = (
@@ -34,6 +35,7 @@ SYMBOLS = (
     "rwkv7_abi_version",
     "rwkv7_strerror",
     "rwkv7_layer_layout_get",
+    "rwkv7_head_q_scale_offset",
     "rwkv7_workspace_bytes",
     "rwkv7_workspace_errors",
     "rwkv7_decode_launches",
@@ -78,7 +80,8 @@ class LayerLayout(ctypes.Structure):
         (n, ctypes.c_int64)
         for n in ("w_rkv", "w_lora1", "w_lora2", "w_o", "w_fk", "w_fv", "vec", "bytes", "f_rkv")
     ] + [("f_l1", ctypes.c_int64 * 4), ("f_l2", ctypes.c_int64 * 4)] + [
-        (n, ctypes.c_int64) for n in ("f_o", "f_fk", "f_fv", "frag_bytes")
+        (n, ctypes.c_int64) for n in ("f_o", "f_fk", "f_fv", "frag_bytes", "q_rkv", "q_o", "q_fk", "q_fv",
+                                      "q_scale", "q_bytes")
     ]
 
 
@@ -92,6 +95,8 @@ class Model(ctypes.Structure):
         ("layers_frag", ctypes.c_void_p),
         ("head_frag", ctypes.c_void_p),
         ("flags", ctypes.c_uint32),
+        ("layers_q", ctypes.c_void_p),
+        ("head_q", ctypes.c_void_p),
     ]
 
 
@@ -150,6 +155,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "rwkv7_abi_version": (ctypes.c_int, []),
         "rwkv7_strerror": (ctypes.c_char_p, [ctypes.c_int]),
         "rwkv7_layer_layout_get": (ctypes.c_int, [ctypes.POINTER(Dims), ctypes.POINTER(LayerLayout)]),
+        "rwkv7_head_q_scale_offset": (i64, [ctypes.POINTER(Dims)]),
         "rwkv7_workspace_bytes": (i64, [ctypes.POINTER(Dims), i32, i32]),
         "rwkv7_workspace_errors": (ctypes.c_int, [vp, i64, ctypes.POINTER(ctypes.c_uint32), vp]),
         "rwkv7_decode_launches": (ctypes.c_int, [ctypes.POINTER(Model), i32, i32]),

@@ -232,10 +232,9 @@ def quantize_i8(W: Tensor) -> tuple[Tensor, Tensor]:
     [-127, 127], so ``|W - scale * q| <= scale / 2``. A weight-format step
     (torch on W's device), like the checkpoint dtype conversion."""
     _need(W.dim() == 2 and W.is_floating_point(), "W must be a floating [N, K] matrix")
-    w = W.float()
-    scale = w.abs().amax(dim=1) / 127.0
-    q = torch.round(w / torch.where(scale > 0, scale, torch.ones_like(scale))[:, None]).clamp_(-127, 127)
-    return q.to(torch.int8).contiguous(), scale.contiguous()
+    from .weight import quantize_rows_i8
+
+    return quantize_rows_i8(W)
 
 
 def gemv_i8(x: Tensor, q: Tensor, scale: Tensor) -> Tensor:

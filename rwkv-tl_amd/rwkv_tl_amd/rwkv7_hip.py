@@ -35,17 +35,24 @@ class RWKV7HIP(RWKV7Model):
         is_torch_compile: accepted for signature compatibility with the
             reference classes and ignored (launch overhead is removed with HIP
             graphs instead, see ``HIPGraph``).
+        weight_quant: ``None`` (fp16 weights everywhere) or ``"int8"``: batch-1
+            decode streams per-row symmetric int8 copies of the layer matrices
+            and the head (f32 row scales, f32 accumulation), about half the
+            bytes per token; prefill and batched decode keep the fp16 weights.
     """
 
-    def __init__(self, w: RWKV7Weight, *, is_torch_compile: bool = True) -> None:
+    def __init__(self, w: RWKV7Weight, *, is_torch_compile: bool = True, weight_quant: str | None = None) -> None:
         super().__init__(w)
         if w.dtype != torch.float16:
             raise ValueError(f"kernel dtype torch.float16 does not match weight dtype {w.dtype}")
         if w.device.type != "cuda":
             raise ValueError(f"RWKV7HIP needs the weights on a ROCm GPU, got {w.device}")
         self._is_torch_compile = is_torch_compile
+        if weight_quant not in (None, "int8"):
+            raise ValueError(f"weight_quant must be None or 'int8', got {weight_quant!r}")
         self._lib = _lib.load()
-        self.dev = pack_device_weights(w)
+        self.weight_quant = weight_quant
+        self.dev = pack_device_weights(w, int8=weight_quant == "int8")
         self.V = int(self.dev.dims.vocab)
         self._ws: Tensor | None = None
         self._ws_bytes = 0
@@ -207,3 +214,10 @@ def _copy_into(dst, src: State) -> None:
     for ds, ss in zip(dst[0] + dst[1], src[0] + src[1]):
         for k in ds:
             ds[k].copy_(ss[k])
+
+
+class RWKV7HIPInt8(RWKV7HIP):
+    """``RWKV7HIP`` whose batch-1 decode streams int8 weights (``weight_quant="int8"``)."""
+
+    def __init__(self, w: RWKV7Weight, *, is_torch_compile: bool = True) -> None:
+        super().__init__(w, is_torch_compile=is_torch_compile, weight_quant="int8")

@@ -134,11 +134,48 @@ class DeviceWeights:
     desc: _lib.Model
     layers_frag: Tensor | None = None  # uint8 [L, layout.frag_bytes]
     head_frag: Tensor | None = None    # f16, the head in fragment order
+    layers_q: Tensor | None = None     # uint8 [L, layout.q_bytes]: int8 matrices + row scales
+    head_q: Tensor | None = None       # uint8: int8 head [V, C], then f32 row scales [V]
 
     @property
     def nbytes(self) -> int:
-        ts = (self.layers, self.emb, self.head, self.ln_out, self.layers_frag, self.head_frag)
+        ts = (self.layers, self.emb, self.head, self.ln_out, self.layers_frag, self.head_frag, self.layers_q,
+              self.head_q)
         return sum(t.numel() * t.element_size() for t in ts if t is not None)
+
+
+def quantize_rows_i8(W: Tensor) -> tuple[Tensor, Tensor]:
+    """Symmetric per-row int8: ``scale = max|W[n]| * (1/127)`` (fp32; 0 for an
+    all-zero row), ``q = round_half_even(W / scale)`` in [-127, 127], so
+    ``|W - scale * q| <= scale / 2``. A weight-format step done once at load
+    (torch on W's device), like the checkpoint dtype conversion.
+
+    Both steps give the same bits on every device. The scale is one IEEE fp32
+    multiplication by the fp32 constant 1/127 (torch's division by a scalar
+    is not bound to round alike on the CPU and the GPU; ~4 % of the scales
+    differ by one ulp between a true division and a reciprocal
+    multiplication); the quotient is formed in float64, wide enough (fp16
+    ``W`` over fp32 ``scale``) that its rounding never crosses a half-step.
+    With an fp32 quotient, or scales one ulp apart, ~1 element in 10^5 rounds
+    to the neighbouring integer -- enough to move a layer's output by ~1e-4
+    relative."""
+    w = W.float()
+    scale = w.abs().amax(dim=1) * torch.tensor(1.0 / 127.0, dtype=torch.float32, device=w.device)
+    div = torch.where(scale > 0, scale, torch.ones_like(scale)).double()
+    q = torch.round(w.double() / div[:, None]).clamp_(-127, 127)
+    return q.to(torch.int8).contiguous(), scale.contiguous()
+
+
+def int8_matrices(w: "RWKV7Weight") -> list[dict[str, Tensor]]:
+    """Per layer, the f16 matrices the int8 decode streams, as [out, in] rows
+    in the int8 arena's order: ``rkv`` (receptance, key, value rows, then the
+    LoRA first steps v1^T, w1^T, a1^T, g1^T), ``o``, ``fk``, ``fv``."""
+    out = []
+    for blk in w.blocks:
+        att, ffn = blk.att, blk.ffn
+        rkv = torch.cat([att.rkvWt[j].T for j in range(3)] + [att.v1t, att.w1t, att.a1t, att.g1t], 0)
+        out.append({"rkv": rkv, "o": att.oWt.T, "fk": ffn.kWt.T, "fv": ffn.vWt.T})
+    return out
 
 
 def to_fragments(W: Tensor) -> Tensor:
@@ -179,12 +216,14 @@ def _f16_view(buf: Tensor, off: int, rows: int, cols: int) -> Tensor:
     return buf[off : off + rows * cols * 2].view(torch.float16).view(rows, cols)
 
 
-def pack_device_weights(w: RWKV7Weight, fragments: bool = True) -> DeviceWeights:
+def pack_device_weights(w: RWKV7Weight, fragments: bool = True, int8: bool = False) -> DeviceWeights:
     """Build the HIP arenas from reference-layout weights (fp16, on the GPU).
 
     ``fragments`` also builds the fragment-order copy the prefill / batched
     decode GEMMs stream (one contiguous KiB per wave load); it roughly doubles
-    the weight memory."""
+    the weight memory. ``int8`` also builds the int8 arenas of the batch-1
+    decode (``quantize_rows_i8`` per matrix row) and sets the model flag that
+    makes batch-1 decode stream them."""
     if w.dtype != torch.float16:
         raise ValueError(f"the HIP kernels take float16 weights, got {w.dtype}")
     dims = model_dims(w)
@@ -240,6 +279,25 @@ def pack_device_weights(w: RWKV7Weight, fragments: bool = True) -> DeviceWeights
             put(lay.f_fk, _f16_view(src, lay.w_fk, F_, C))
             put(lay.f_fv, _f16_view(src, lay.w_fv, C, F_))
         head_frag = to_fragments(head).contiguous()
+    layers_q = head_q = None
+    if int8:
+        layers_q = torch.zeros(dims.n_layer, lay.q_bytes, dtype=torch.uint8, device=dev)
+        N1 = 3 * C + SR
+        for i, mats in enumerate(int8_matrices(w)):
+            buf = layers_q[i]
+            scales = []
+            for name, off in (("rkv", lay.q_rkv), ("o", lay.q_o), ("fk", lay.q_fk), ("fv", lay.q_fv)):
+                q, sc = quantize_rows_i8(mats[name])
+                buf[off : off + q.numel()].view(torch.int8).view(q.shape).copy_(q)
+                scales.append(sc)
+            sc = torch.cat(scales)
+            assert sc.numel() == N1 + C + F_ + C
+            buf[lay.q_scale : lay.q_scale + sc.numel() * 4].view(torch.float32).copy_(sc)
+        qh, sh = quantize_rows_i8(head)
+        soff = int(_lib.load().rwkv7_head_q_scale_offset(ctypes.byref(dims)))
+        head_q = torch.zeros(soff + sh.numel() * 4, dtype=torch.uint8, device=dev)
+        head_q[: qh.numel()].view(torch.int8).view(qh.shape).copy_(qh)
+        head_q[soff:].view(torch.float32).copy_(sh)
     desc = _lib.Model(
         dims=dims,
         layers=layers.data_ptr(),
@@ -248,5 +306,8 @@ def pack_device_weights(w: RWKV7Weight, fragments: bool = True) -> DeviceWeights
         ln_out=ln_out.data_ptr(),
         layers_frag=layers_frag.data_ptr() if layers_frag is not None else None,
         head_frag=head_frag.data_ptr() if head_frag is not None else None,
+        flags=_lib.MODEL_INT8_DECODE if int8 else 0,
+        layers_q=layers_q.data_ptr() if layers_q is not None else None,
+        head_q=head_q.data_ptr() if head_q is not None else None,
     )
-    return DeviceWeights(dims, lay, layers, emb, head, ln_out, desc, layers_frag, head_frag)
+    return DeviceWeights(dims, lay, layers, emb, head, ln_out, desc, layers_frag, head_frag, layers_q, head_q)

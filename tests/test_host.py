@@ -15,7 +15,7 @@ from oracle import sampling_ref as S
 from rwkv_tl_amd import _lib, make_rwkv7, sample_logits
 from rwkv_tl_amd.checkpoint import SHAPES, make_random_state_dict
 from rwkv_tl_amd.state import State
-from rwkv_tl_amd.weight import RWKV7Weight, layer_layout, model_dims, to_fragments
+from rwkv_tl_amd.weight import RWKV7Weight, layer_layout, model_dims, quantize_rows_i8, to_fragments
 
 REPO = Path(__file__).resolve().parent.parent
 HEADER = REPO / "include" / "rwkv7_hip.h"
@@ -88,6 +88,13 @@ def test_layer_layout(shape):
     for (o0, n0), (o1, _) in zip(regions, regions[1:]):
         assert o0 % 256 == 0 and o1 >= o0 + n0
     assert lay.frag_bytes >= regions[-1][0] + regions[-1][1] and lay.frag_bytes % 256 == 0
+    # int8 arena: q_rkv [3C+SR, C], q_o, q_fk, q_fv, then the f32 row scales
+    q = [(lay.q_rkv, (3 * C + SR) * C), (lay.q_o, C * C), (lay.q_fk, F * C), (lay.q_fv, C * F),
+         (lay.q_scale, 4 * (3 * C + SR + C + F + C))]
+    for (o0, n0), (o1, _) in zip(q, q[1:]):
+        assert o0 % 256 == 0 and o1 >= o0 + n0
+    assert lay.q_bytes >= q[-1][0] + q[-1][1] and lay.q_bytes % 256 == 0
+    assert _lib.load().rwkv7_head_q_scale_offset(ctypes.byref(d)) >= d.vocab * C
 
 
 def test_fragment_order_matches_header_definition():
@@ -298,4 +305,29 @@ def test_make_rwkv7_backends():
         make_rwkv7(torch.device("cpu"))
     cls = make_rwkv7(torch.device("cuda"), backend="fp16")
     assert cls.__name__ == "HIPGraphRWKV7HIP"
+    assert make_rwkv7(torch.device("cuda"), backend="int8", use_graph=False).__name__ == "RWKV7HIPInt8"
     assert make_rwkv7(torch.device("cuda"), use_graph=False).__name__ == "RWKV7HIP"
+
+
+def test_quantize_rows_i8_bounds():
+    """Per-row symmetric int8: every element within half a step of its row's
+    scale, the row's largest |element| maps to +-127, an all-zero row gets
+    scale 0, and a row's scale follows its own largest element only."""
+    g = torch.Generator().manual_seed(5)
+    W = torch.randn(40, 300, generator=g).half()
+    W[3] = 0
+    W[7, 11] = 40.0  # an outlier widens only its own row's step
+    q, s = quantize_rows_i8(W)
+    assert q.dtype == torch.int8 and q.shape == W.shape and s.dtype == torch.float32 and s.shape == (40,)
+    w = W.float()
+    assert float(s[3]) == 0.0 and int(q[3].abs().max()) == 0
+    nz = torch.arange(40) != 3
+    assert torch.equal(q[nz].abs().amax(1).int(), torch.full((39,), 127, dtype=torch.int32))
+    assert torch.allclose(s, w.abs().amax(1) / 127)
+    err = (w - q.float() * s[:, None]).abs()
+    assert bool((err <= s[:, None] * 0.5 + 1e-6 * w.abs().amax(1, keepdim=True)).all())  # + f32 rounding
+    assert float(s[7]) == pytest.approx(40.0 / 127) and float(s[8]) < 0.05
+    # a row that is an exact multiple of its step round-trips exactly
+    e = torch.arange(-127, 128, dtype=torch.float32)[None, :] * 0.5
+    qe, se = quantize_rows_i8(e)
+    assert float(se[0]) == 0.5 and torch.equal(qe[0].float(), torch.arange(-127, 128, dtype=torch.float32))
