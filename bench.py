@@ -23,7 +23,9 @@
 * Extra keys of the same JSON object: decode at batch 16 (ms/step and
   tokens/s), prefill T=128 and T=8 as flat keys ``prefill_T128_ms``,
   ``prefill_T128_hbm_frac``, ``prefill_T128_mfma_frac`` (and the same for
-  T8; prefill through HIP-graph replay for T <= 64), the int8 weight-only GEMV
+  T8; prefill through HIP-graph replay for T <= 64), batch-1 decode on int8
+  weights (``decode_int8``: the same persistent kernel streaming per-row int8
+  matrices, its bytes counted at one byte per int8 weight), the int8 weight-only GEMV
   (``rwkv7_gemv_i8``) against the f16 GEMV on the head matrix (65536 x 1024;
   average launch time over 100 launches and fraction of HBM peak for each),
   the roofline of the whole step as the caller sees it, and the CPU baseline: the oracle's pure-torch fp32
@@ -88,6 +90,18 @@ def algorithmic_bytes(shape, batch: int, tokens_per_seq: int, head: bool) -> flo
     state = batch * L * (8 * H * 64 * 64 + 8 * C)
     io = batch * tokens_per_seq * 2 * C + (batch * 2 * V if head else 0)
     return float(weights + state + io)
+
+
+def int8_decode_bytes(shape, f16_bytes: float) -> float:
+    """Batch-1 decode bytes with int8 weights: every matrix the int8 decode
+    streams (r/k/v, LoRA first steps, o, FFN key/value, head) costs one byte
+    per element instead of two, plus an f32 scale per row; the LoRA second
+    steps and vectors stay as they are."""
+    C, F, V, L = shape.n_embd, shape.n_ffn, shape.vocab, shape.n_layer
+    SR = shape.rank_w + shape.rank_a + shape.rank_v + shape.rank_g
+    elems = L * (4 * C * C + 2 * C * F + C * SR) + V * C
+    rows = L * (3 * C + SR + C + F + C) + V
+    return float(f16_bytes - elems + 4 * rows)
 
 
 def log(msg: str) -> None:
@@ -532,6 +546,22 @@ def main() -> None:
             "hbm_frac": round(b16 / (ms16 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         }
         log(f"decode B=16: {ms16:.4f} ms/step")
+        # ---- decode B=1 on int8 weights (the same persistent kernel streaming
+        # per-row int8 matrices and head, f32 row scales) ----
+        model8 = RWKV7HIP(w, is_torch_compile=False, weight_quant="int8")
+        S8 = State(w.L, w.C, 64, device=dev)
+        for i in range(Wm):
+            model8.decode_into(toks[i], S8, logits1)
+        us_i8 = time_cuda(lambda it=iter(range(K)): model8.decode_into(toks[next(it) % (K + Wm)], S8, logits1),
+                          min(K, 128)) * 1e3
+        i8_bytes = int8_decode_bytes(shape, step_bytes)
+        out["decode_int8"] = {
+            "us_per_token": round(us_i8, 2),
+            "alg_bytes": i8_bytes,
+            "hbm_frac": round(i8_bytes / (us_i8 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        }
+        log(f"decode B=1 int8 weights: {us_i8:.2f} us/token")
+        del model8, S8
         # ---- int8 weight-only GEMV vs the f16 GEMV on the head shape ----
         # (direct C-ABI calls into a preallocated output, so the host wrapper's
         # checks and allocation stay out of the timed launches)

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define RWKV7_ABI_VERSION 6
+#define RWKV7_ABI_VERSION 7
 #define RWKV7_HEAD_SIZE 64
 
 enum {
@@ -126,6 +126,13 @@ typedef struct rwkv7_model {
  * multi-launch flag, a device without the grid) fails with RWKV7_ESHAPE
  * rather than running on f16 weights. */
 #define RWKV7_MODEL_INT8_DECODE 2u
+/* rwkv7_model.flags: every 16-bit value the library reads or writes is
+ * bfloat16 instead of IEEE half -- the matrices of the layer and fragment
+ * arenas, emb, head, the state's tmix_x / cmix_x, logits and the f16 scratch
+ * operands of the MFMA GEMMs (which then run v_mfma_f32_16x16x32_bf16); the
+ * bf16 model of demo/rwkv7_bf16.py:18-27. The vectors section stays fp32,
+ * arithmetic and the wkv state stay fp32. */
+#define RWKV7_MODEL_BF16 4u
 
 /* Recurrent state of `batch` independent sequences, layer-major arenas
  * (src/rwkv_tl/state.py:35-44 plus a leading batch dimension):
@@ -346,8 +353,8 @@ typedef struct rwkv7_sampling {
   uint64_t offset;          /* counter of this draw (one per call; the row is the second counter word) */
 } rwkv7_sampling;
 
-/* Sample one token per row of logits [B, V], f16 or f32 (logits_is_f32;
- * row stride ld elements, V <= 65536), into out i64 [B]. In order: repetition penalty on the tokens
+/* Sample one token per row of logits [B, V] (logits_dtype: 0 f16, 1 f32,
+ * 2 bf16; row stride ld elements, V <= 65536), into out i64 [B]. In order: repetition penalty on the tokens
  * whose bit is set in seen u32 [B, seen_ld] (bit t % 32 of word t / 32;
  * NULL: none), greedy argmax if temperature <= 0, else division by the
  * temperature, top-k (keep x >= the k-th largest), top-p (keep the tokens
@@ -360,7 +367,7 @@ typedef struct rwkv7_sampling {
  * Stands in for sample_logits (demo/sampling.py:13-70) as called by
  * RWKV7Model.generate (demo/_rwkv7_abc.py:41-72), with the draw of
  * torch.multinomial replaced by the counter-based one above. */
-int rwkv7_sample(const void *logits, int32_t logits_is_f32, int64_t ld, int32_t B, int32_t V, const rwkv7_sampling *params,
+int rwkv7_sample(const void *logits, int32_t logits_dtype, int64_t ld, int32_t B, int32_t V, const rwkv7_sampling *params,
                  uint32_t *seen, int64_t seen_ld, int32_t update_seen, int64_t *out, float *probs,
                  int64_t probs_ld, void *stream);
 

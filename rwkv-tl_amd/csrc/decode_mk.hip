@@ -215,22 +215,11 @@ RWKV7_DEV MkLds mk_lds(float *smem, int C, int F, int SR) {
 
 // ---- math-wave helpers --------------------------------------------------------
 
-// acc + sum_e w[e] * x[e] for 8 f16 weights and 8 f32 inputs in LDS.
-RWKV7_DEV float dot8(const uint4 &w, const float *x, float acc) {
-  float wf[8];
-  h8_to_f(w, wf);
-  const float4 u = reinterpret_cast<const float4 *>(x)[0], v = reinterpret_cast<const float4 *>(x)[1];
-  acc = fmaf(wf[0], u.x, acc); acc = fmaf(wf[1], u.y, acc);
-  acc = fmaf(wf[2], u.z, acc); acc = fmaf(wf[3], u.w, acc);
-  acc = fmaf(wf[4], v.x, acc); acc = fmaf(wf[5], v.y, acc);
-  acc = fmaf(wf[6], v.z, acc); acc = fmaf(wf[7], v.w, acc);
-  return acc;
-}
-
-// Same with the 8 inputs in registers.
+// acc + sum_e w[e] * x[e] for 8 16-bit weights (F16T<BF>) and 8 f32 inputs.
+template <bool BF>
 RWKV7_DEV float dot8r(const uint4 &w, const float (&x)[8], float acc) {
   float wf[8];
-  h8_to_f(w, wf);
+  F16T<BF>::to_f8(w, wf);
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc = fmaf(wf[e], x[e], acc);
   return acc;
@@ -242,7 +231,7 @@ RWKV7_DEV float dot8r(const uint4 &w, const float (&x)[8], float acc) {
 // would cost one LDS round trip per chunk); a chunk past the row (zero
 // weights, see load_row) reads a valid x chunk instead. Two accumulators
 // halve the dependent FMA chain.
-template <int NC>
+template <bool BF, int NC>
 RWKV7_DEV float row_dot(const uint4 (&w)[NC], const float *x, int nch) {
   const int lane = threadIdx.x & 63;
   const float4 *x4 = reinterpret_cast<const float4 *>(x);
@@ -259,7 +248,7 @@ RWKV7_DEV float row_dot(const uint4 (&w)[NC], const float *x, int nch) {
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     float wf[8];
-    h8_to_f(w[c], wf);
+    F16T<BF>::to_f8(w[c], wf);
     float a = acc[c & 1];
     a = fmaf(wf[0], xa[c].x, a); a = fmaf(wf[1], xa[c].y, a);
     a = fmaf(wf[2], xa[c].z, a); a = fmaf(wf[3], xa[c].w, a);
@@ -524,7 +513,7 @@ RWKV7_DEV void wait_local(const MkCtx &cx, const unsigned *pubs, unsigned target
 
 // NJF: pairs per lane of one of the kW slices of the FFN hidden vector (every
 // wave of the workgroup reads one slice).
-template <int NJF>
+template <int NJF, bool BF>
 RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, const MkCtx &cx) {
   const int lane = threadIdx.x & 63;
   const int C = m.C, F = m.F, L = m.L;
@@ -535,7 +524,7 @@ RWKV7_DEV void comm_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
   // LayerNorm partial statistics go to xst
   static_assert(kNComm == 1, "the comm wave holds slice kMW");
   const int XS = C / kW;
-  for (int i = lane; i < XS; i += 64) s.x1[kMW * XS + i] = h2f(erow[kMW * XS + i]);
+  for (int i = lane; i < XS; i += 64) s.x1[kMW * XS + i] = F16T<BF>::to_f(erow[kMW * XS + i]);
   slice_stats(s.x1, kMW, XS, s.xst + 2 * kMW);
   auto to = [](float *d) { return [d](int i, float v) { d[i] = v; }; };
   const int rp = m.g % kRep;  // the replica this workgroup reads
@@ -635,7 +624,7 @@ RWKV7_DEV void comm_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
 // Per-head core of head g for every layer: LoRA second step, gates, L2 norm,
 // wkv7, GroupNorm, output gate (demo/rwkv7_torch.py:92-120). NL2: LoRA
 // second-step chunks per thread.
-template <int NL2>
+template <int NL2, bool BF>
 RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const MkCtx &cx, int wv) {
   int mt = threadIdx.x, lane = mt & 63;
   auto refresh = [&]() {
@@ -706,7 +695,7 @@ RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
 #pragma unroll
       for (int i = 0; i < NL2; ++i) {
         float wf[8];
-        h8_to_f(js + i < je ? w2[i] : make_uint4(0, 0, 0, 0), wf);
+        F16T<BF>::to_f8(js + i < je ? w2[i] : make_uint4(0, 0, 0, 0), wf);
         float t = acc[i & 1];
         t = fmaf(wf[0], xa[i].x, t); t = fmaf(wf[1], xa[i].y, t);
         t = fmaf(wf[2], xa[i].z, t); t = fmaf(wf[3], xa[i].w, t);
@@ -829,7 +818,7 @@ RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
 // vectors). They stream while the head workgroups run P2 (the layer's longest
 // wait), and a single vmcnt(0) at the start of P3 covers them all, so the
 // later hand-offs of the layer run with no weight traffic in flight.
-template <int CPL, int RM, int NC5, int VPL, int NHB, bool Q8>
+template <int CPL, int RM, int NC5, int VPL, int NHB, bool Q8, bool BF>
 RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, const MkCtx &cx, int wv) {
   // Math threads are 0..kMT-1. refresh() passes the thread index through an
   // empty asm at each stage, so per-thread addresses are recomputed there
@@ -874,7 +863,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
   // a row's dot product, scale included
   auto rdot = [&](const auto &w, const float *x, int nch, float sc) {
     if constexpr (Q8) return row_dot_q8(w, x, nch) * sc;
-    else return row_dot(w, x, nch);
+    else return row_dot<BF>(w, x, nch);
   };
   auto vec_ptr = [&](int l) { return reinterpret_cast<const float *>(layer_ptr(l) + a.o_vec); };
   // Vector loads are unconditional (index clamped; elements past C are never
@@ -986,7 +975,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     int64_t token = a.tok[0];
     token = token < 0 ? 0 : token >= a.V ? a.V - 1 : token;
     const uint16_t *erow = a.emb + token * C;
-    for (int i = lane; i < XS; i += 64) s.x1[wv * XS + i] = h2f(erow[wv * XS + i]);
+    for (int i = lane; i < XS; i += 64) s.x1[wv * XS + i] = F16T<BF>::to_f(erow[wv * XS + i]);
     slice_stats(s.x1, wv, XS, s.xst + 2 * wv);
   }
   pre_p1(0);
@@ -1010,7 +999,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
         const int c = mt + kMT * i;
         if (c < C) {
           const float ln = (xv[i] - st.x) * st.y * v1w[i] + v1b[i];
-          const float prv = h2f(pv1[i]);
+          const float prv = F16T<BF>::to_f(pv1[i]);
           s.ln1[c] = ln;
 #pragma unroll
           for (int q = 0; q < 4; ++q)
@@ -1052,7 +1041,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
       const int c = m.owa + wv;
       if (lane < kRep) publish(a.x_ex + (int64_t)lane * C + c, cx.tag(ph + 2), xown);
       // every reader of this layer's time-mix shift state is done (all of P2's inputs arrived)
-      if (lane == kRep) a.tmix_x[(int64_t)l * C + c] = f2h(s.ln1[c]);
+      if (lane == kRep) a.tmix_x[(int64_t)l * C + c] = F16T<BF>::from_f(s.ln1[c]);
     }
     count_publish();
     poll_x(cx.tag(ph + 2), s.x4, s.xst + 2 * kW);
@@ -1074,7 +1063,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
         if (c < C) {
           const float ln = (xv[i] - st.x) * st.y * v4w[i] + v4b[i];
           s.ln2[c] = ln;
-          s.mix4[c] = ln + mu4[i] * (h2f(pv4[i]) - ln);
+          s.mix4[c] = ln + mu4[i] * (F16T<BF>::to_f(pv4[i]) - ln);
         }
       }
     }
@@ -1109,7 +1098,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
       xown += d;
       const int c = m.owa + wv;
       if (lane < kRep) publish(a.x_ex + (int64_t)lane * C + c, cx.tag(ph + 4), xown);
-      if (lane == kRep) a.cmix_x[(int64_t)l * C + c] = f2h(s.ln2[c]);
+      if (lane == kRep) a.cmix_x[(int64_t)l * C + c] = F16T<BF>::from_f(s.ln2[c]);
     }
     count_publish();
     poll_x(cx.tag(ph + 4), s.x1, s.xst);
@@ -1151,7 +1140,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
 #pragma unroll
       for (int c = 0; c < CW; ++c) {
         if constexpr (Q8) acc = dot16r_q8(cur[k][c], xr[c], acc);
-        else acc = dot8r(cur[k][c], xr[c], acc);
+        else acc = dot8r<BF>(cur[k][c], xr[c], acc);
       }
       acc = wave_sum(acc);
       if constexpr (Q8) acc *= hqs[b % kHRing][k];
@@ -1160,13 +1149,13 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     if (b + kHRing < NHB) pre_head(b + kHRing, cur);
   }
   // NaN logits if this workgroup's input did not arrive or the launch was aborted
-  if (hr0 + lane < hr1) a.logits[hr0 + lane] = bad ? (uint16_t)0x7E00u : f2h(out);
+  if (hr0 + lane < hr1) a.logits[hr0 + lane] = bad ? F16T<BF>::kNaN : F16T<BF>::from_f(out);
 }
 
 // One workgroup per CU by construction (2 waves per SIMD): telling the
 // compiler so keeps its scheduler from trading prefetch distance for an
 // occupancy this kernel never runs at.
-template <int CPL, int RM, int NC5, int VPL, int NL2, int NHB, bool Q8>
+template <int CPL, int RM, int NC5, int VPL, int NL2, int NHB, bool Q8, bool BF>
 __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_mk_kernel(MkArgs a) {
   extern __shared__ __align__(16) float smem[];
   MkGeom m;
@@ -1223,10 +1212,10 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (m.head) {
     if (wv >= kMW) comm_head(a, m, s, cx);
-    else math_head<NL2>(a, m, s, cx, wv);
+    else math_head<NL2, BF>(a, m, s, cx, wv);
   } else {
-    if (wv >= kMW) comm_worker<NC5 / 2>(a, m, s, cx);
-    else math_worker<CPL, RM, NC5, VPL, NHB, Q8>(a, m, s, cx, wv);
+    if (wv >= kMW) comm_worker<NC5 / 2, BF>(a, m, s, cx);
+    else math_worker<CPL, RM, NC5, VPL, NHB, Q8, BF>(a, m, s, cx, wv);
   }
   // The next launch's epoch. In a launch that completed, this worker ends only
   // after every workgroup has published (its logits need the last layer's x,
@@ -1246,10 +1235,20 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 
 // ---- host side --------------------------------------------------------------
 
-// The compiled instances: CPL 2, RM 3, NC5 8, VPL 3, NL2 8, NHB 10, with f16
-// or int8 weights.
+// The compiled instances: CPL 2, RM 3, NC5 8, VPL 3, NL2 8, NHB 10; variant
+// v = q8 + 2 bf: matrices streamed as 16-bit or int8 (q8), 16-bit data in
+// IEEE half or bfloat16 (bf).
 constexpr int kCPL = 2, kRM = 3, kNC5 = 8, kVPL = 3, kNL2 = 8, kNHB = 10;
-#define RWKV7_MK_INSTANCE(Q8) decode_mk_kernel<kCPL, kRM, kNC5, kVPL, kNL2, kNHB, Q8>
+constexpr int kMkVariants = 4;
+#define RWKV7_MK_INSTANCE(Q8, BF) decode_mk_kernel<kCPL, kRM, kNC5, kVPL, kNL2, kNHB, Q8, BF>
+static const void *mk_instance(int v) {
+  switch (v) {
+    case 0: return (const void *)RWKV7_MK_INSTANCE(false, false);
+    case 1: return (const void *)RWKV7_MK_INSTANCE(true, false);
+    case 2: return (const void *)RWKV7_MK_INSTANCE(false, true);
+    default: return (const void *)RWKV7_MK_INSTANCE(true, true);
+  }
+}
 
 static int cdiv(int a, int b) { return (a + b - 1) / b; }
 
@@ -1259,8 +1258,8 @@ static int cdiv(int a, int b) { return (a + b - 1) / b; }
 constexpr int kMaxDevices = 64;
 struct MkDevice {
   std::atomic<int> cus{0};
-  std::atomic<int64_t> lds_allowed[2] = {{0}, {0}};   // per instance (f16, int8)
-  std::atomic<int64_t> resident_lds[2] = {{0}, {0}};  // largest LDS size found co-resident
+  std::atomic<int64_t> lds_allowed[kMkVariants] = {};   // per instance variant
+  std::atomic<int64_t> resident_lds[kMkVariants] = {};  // largest LDS size found co-resident
 };
 static MkDevice g_mk_dev[kMaxDevices];
 
@@ -1295,19 +1294,19 @@ int64_t mk_exchange_bytes(int C, int F, int SR) {
 // Allows the kernel its dynamic LDS on the current device and checks that a
 // grid of one workgroup per CU can be resident at once (the occupancy of this
 // kernel instance with that LDS is at least one workgroup per CU).
-static bool mk_prepare(int64_t lds, bool q8) {
+static bool mk_prepare(int64_t lds, int v) {
   MkDevice *d = mk_device();
-  if (!d) return false;
-  const void *fn = q8 ? (const void *)RWKV7_MK_INSTANCE(true) : (const void *)RWKV7_MK_INSTANCE(false);
-  if (lds > d->lds_allowed[q8].load(std::memory_order_relaxed)) {
+  if (!d || v < 0 || v >= kMkVariants) return false;
+  const void *fn = mk_instance(v);
+  if (lds > d->lds_allowed[v].load(std::memory_order_relaxed)) {
     if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) return false;
-    d->lds_allowed[q8].store(lds, std::memory_order_relaxed);
+    d->lds_allowed[v].store(lds, std::memory_order_relaxed);
   }
-  if (lds <= d->resident_lds[q8].load(std::memory_order_relaxed)) return true;
+  if (lds <= d->resident_lds[v].load(std::memory_order_relaxed)) return true;
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kT, (size_t)lds) != hipSuccess || per_cu < 1)
     return false;
-  d->resident_lds[q8].store(lds, std::memory_order_relaxed);
+  d->resident_lds[v].store(lds, std::memory_order_relaxed);
   return true;
 }
 
@@ -1355,11 +1354,16 @@ bool mk_supported(const rwkv7_dims &d, int G) {
   return mk_lds_bytes(C, F, SR) <= 160 * 1024;
 }
 
-bool mk_usable(const rwkv7_dims &d, bool q8) {
+static int mk_variant(const rwkv7_model &m) {
+  return (mk_int8(m) ? 1 : 0) + ((m.flags & RWKV7_MODEL_BF16) ? 2 : 0);
+}
+
+bool mk_usable(const rwkv7_model &m) {
+  const rwkv7_dims &d = m.dims;
   const int G = mk_cus();
   if (G < 1 || !mk_supported(d, G)) return false;
   const int SR = d.rank_w + d.rank_a + d.rank_v + d.rank_g;
-  return mk_prepare(mk_lds_bytes(d.n_embd, d.n_ffn, SR), q8);
+  return mk_prepare(mk_lds_bytes(d.n_embd, d.n_ffn, SR), mk_variant(m));
 }
 
 bool mk_int8(const rwkv7_model &m) {
@@ -1372,8 +1376,8 @@ int launch_decode_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const 
   const int SR = d.rank_w + d.rank_a + d.rank_v + d.rank_g;
   const int G = mk_cus();
   const int C = d.n_embd, F = d.n_ffn;
-  const bool q8 = mk_int8(m);
-  if (!mk_usable(d, q8)) return RWKV7_ESHAPE;
+  const int variant = mk_variant(m);
+  if (!mk_usable(m)) return RWKV7_ESHAPE;
   MkArgs a;
   a.layers_q = static_cast<const char *>(m.layers_q);
   a.q_lbytes = lay.q_bytes;
@@ -1419,8 +1423,12 @@ int launch_decode_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const 
   a.core_ex = a.proj_ex + (int64_t)kRep * (3 * C + SR);
   a.hid_ex = a.core_ex + (int64_t)kRep * C;
   const int64_t lds = mk_lds_bytes(C, F, SR);
-  if (q8) RWKV7_MK_INSTANCE(true)<<<G, kT, lds, st>>>(a);
-  else RWKV7_MK_INSTANCE(false)<<<G, kT, lds, st>>>(a);
+  switch (variant) {
+    case 0: RWKV7_MK_INSTANCE(false, false)<<<G, kT, lds, st>>>(a); break;
+    case 1: RWKV7_MK_INSTANCE(true, false)<<<G, kT, lds, st>>>(a); break;
+    case 2: RWKV7_MK_INSTANCE(false, true)<<<G, kT, lds, st>>>(a); break;
+    default: RWKV7_MK_INSTANCE(true, true)<<<G, kT, lds, st>>>(a); break;
+  }
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;
 }

@@ -52,17 +52,19 @@ struct GemmGroup {
 
 RWKV7_DEV void store_epi(const GemmProb &P, int row, int col, float v) {
   const int64_t o = (int64_t)row * P.ldy + col;
+  // 16-bit outputs in the operands' format (half, or bfloat16 if P.bf)
+  auto st16 = [&](float x) { reinterpret_cast<uint16_t *>(P.Y)[o] = P.bf ? f2b(x) : f2h(x); };
   switch (P.epi) {
     case GEPI_F32: reinterpret_cast<float *>(P.Y)[o] = v; break;
-    case GEPI_F16: reinterpret_cast<uint16_t *>(P.Y)[o] = f2h(v); break;
+    case GEPI_F16: st16(v); break;
     case GEPI_RELUSQ: {
       const float q = fmaxf(v, 0.f);
-      reinterpret_cast<uint16_t *>(P.Y)[o] = f2h(q * q);
+      st16(q * q);
       break;
     }
     case GEPI_ADD_F32: reinterpret_cast<float *>(P.Y)[o] += v; break;
-    case GEPI_TANH_F16: reinterpret_cast<uint16_t *>(P.Y)[o] = f2h(tanhf(v)); break;
-    default: reinterpret_cast<uint16_t *>(P.Y)[o] = f2h(sigmoidf_(v)); break;
+    case GEPI_TANH_F16: st16(tanhf(v)); break;
+    default: st16(sigmoidf_(v)); break;
   }
 }
 
@@ -207,7 +209,7 @@ RWKV7_DEV void tile_store(const GemmGroup &g, const TileUnit &w, floatx4 (&acc)[
   }
 }
 
-template <int BM>
+template <int BM, bool BF>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
   constexpr int MB = BM / 16;                // 16-row blocks
   constexpr int kRowH = kKC + kLdsPadH;      // halves per LDS row
@@ -261,12 +263,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
   auto compute = [&](int buf, const uint4 (&w)[4]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const half8 bfrag = __builtin_bit_cast(half8, w[j]);
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
-        const half8 afrag = __builtin_bit_cast(
-            half8, *reinterpret_cast<const uint4 *>(&s_a[buf][mb * 16 + (lane & 15)][32 * j + 8 * (lane >> 4)]));
-        acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag, bfrag, acc[mb], 0, 0, 0);
+        const uint4 afrag = *reinterpret_cast<const uint4 *>(&s_a[buf][mb * 16 + (lane & 15)][32 * j + 8 * (lane >> 4)]);
+        acc[mb] = mfma16<BF>(afrag, w[j], acc[mb]);
       }
     }
   };
@@ -312,7 +312,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
 // memory round trip instead of one per chunk pair (the tiles are latency-bound
 // at these sizes, not bandwidth-bound). Same tiling, unit order, split-K
 // hand-off and epilogue as gemm_kernel.
-template <int BM, int NC>
+template <int BM, int NC, bool BF>
 __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmGroup g) {
   constexpr int MB = BM / 16;
   constexpr int kRowH = kKC + kLdsPadH;
@@ -373,12 +373,10 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmGroup g) {
     if (c < nch) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const half8 bfrag = __builtin_bit_cast(half8, wr[c][j]);
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
-          const half8 afrag = __builtin_bit_cast(
-              half8, *reinterpret_cast<const uint4 *>(&s_a[c][mb * 16 + (lane & 15)][32 * j + 8 * (lane >> 4)]));
-          acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag, bfrag, acc[mb], 0, 0, 0);
+          const uint4 afrag = *reinterpret_cast<const uint4 *>(&s_a[c][mb * 16 + (lane & 15)][32 * j + 8 * (lane >> 4)]);
+          acc[mb] = mfma16<BF>(afrag, wr[c][j], acc[mb]);
         }
       }
     }
@@ -427,7 +425,7 @@ struct BigGroup {
 typedef __attribute__((address_space(3))) void lds_void;
 
 // NW waves as a 2 x (NW / 2) grid over the tile.
-template <int BM, int BN, int NW>
+template <int BM, int BN, int NW, bool BF>
 RWKV7_DEV void gemm_big_tile(const BigGroup &g) {
   constexpr int SA = BM / 16, SB = BN / 16;  // 16-row strips of A and W in a tile = blocks per stage
   constexpr int PERS = (SA + SB) / NW;       // blocks each wave loads per stage
@@ -510,14 +508,14 @@ RWKV7_DEV void gemm_big_tile(const BigGroup &g) {
     // reads or DMAs across the barrier
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     issue(st + kBigNB - 1, (buf + kBigNB - 1) % kBigNB);
-    half8 bf[WN];
+    u32x4 bf[WN];
 #pragma unroll
-    for (int q = 0; q < WN; ++q) bf[q] = __builtin_bit_cast(half8, lds[buf][SA + wn * WN + q][lane]);
+    for (int q = 0; q < WN; ++q) bf[q] = lds[buf][SA + wn * WN + q][lane];
 #pragma unroll
     for (int i = 0; i < WM; ++i) {
-      const half8 af = __builtin_bit_cast(half8, lds[buf][wm * WM + i][lane]);
+      const u32x4 af = lds[buf][wm * WM + i][lane];
 #pragma unroll
-      for (int q = 0; q < WN; ++q) acc[i][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[q], acc[i][q], 0, 0, 0);
+      for (int q = 0; q < WN; ++q) acc[i][q] = mfma16<BF>(af, bf[q], acc[i][q]);
     }
   };
 #pragma unroll
@@ -549,8 +547,10 @@ RWKV7_DEV void gemm_big_tile(const BigGroup &g) {
   }
 }
 
-__global__ __launch_bounds__(512) void gemm_big_kernel_256(BigGroup g) { gemm_big_tile<256, 256, 8>(g); }
-__global__ __launch_bounds__(512) void gemm_big_kernel_128(BigGroup g) { gemm_big_tile<128, 128, 8>(g); }
+__global__ __launch_bounds__(512) void gemm_big_kernel_256(BigGroup g) { gemm_big_tile<256, 256, 8, false>(g); }
+__global__ __launch_bounds__(512) void gemm_big_kernel_128(BigGroup g) { gemm_big_tile<128, 128, 8, false>(g); }
+__global__ __launch_bounds__(512) void gemm_big_kernel_256_bf(BigGroup g) { gemm_big_tile<256, 256, 8, true>(g); }
+__global__ __launch_bounds__(512) void gemm_big_kernel_128_bf(BigGroup g) { gemm_big_tile<128, 128, 8, true>(g); }
 
 // Problems of the large-M path: K a multiple of 64, at least 256 columns, and
 // enough 128 x 128 tiles for two workgroups per CU (measured: at M = 512 the
@@ -594,8 +594,14 @@ static int launch_big(const GemmProb *probs, int nprob, int M, int cus, hipStrea
   g.tile_begin[kMaxProb] = t;
   g.tiles = t;
   const int grid = (t + 7) / 8 * 8;
-  if (BT == 256) gemm_big_kernel_256<<<grid, 512, 0, st>>>(g);
-  else gemm_big_kernel_128<<<grid, 512, 0, st>>>(g);
+  const bool bf = probs[0].bf != 0;
+  if (BT == 256) {
+    if (bf) gemm_big_kernel_256_bf<<<grid, 512, 0, st>>>(g);
+    else gemm_big_kernel_256<<<grid, 512, 0, st>>>(g);
+  } else {
+    if (bf) gemm_big_kernel_128_bf<<<grid, 512, 0, st>>>(g);
+    else gemm_big_kernel_128<<<grid, 512, 0, st>>>(g);
+  }
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;
 }
@@ -628,7 +634,7 @@ struct SkinnyGroup {
   unsigned *ctr;
 };
 
-template <int MB>
+template <int MB, bool BF>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(SkinnyGroup g) {
   constexpr int KB = MB == 1 ? 8 : 5;
   __shared__ __align__(16) float4 red[kSkW][MB][64];
@@ -693,11 +699,8 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(SkinnyGroup g) {
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
       if (j < cnt) {
-        const half8 bfrag = __builtin_bit_cast(half8, wf[j]);
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-          acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, af[j][mb]), bfrag, acc[mb], 0,
-                                                           0, 0);
+        for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma16<BF>(af[j][mb], wf[j], acc[mb]);
       }
     }
   }
@@ -797,8 +800,14 @@ static int launch_skinny(const GemmProb *probs, int nprob, int M, hipStream_t st
   }
   g.wg_begin[kMaxProb] = wgs;
   if (pfl * 4 > part_cap || ctrs > kGemmCounters) return RWKV7_EWORKSPACE;
-  if (MB == 1) gemm_skinny_kernel<1><<<wgs, 256, 0, st>>>(g);
-  else gemm_skinny_kernel<2><<<wgs, 256, 0, st>>>(g);
+  const bool bf = probs[0].bf != 0;
+  if (MB == 1) {
+    if (bf) gemm_skinny_kernel<1, true><<<wgs, 256, 0, st>>>(g);
+    else gemm_skinny_kernel<1, false><<<wgs, 256, 0, st>>>(g);
+  } else {
+    if (bf) gemm_skinny_kernel<2, true><<<wgs, 256, 0, st>>>(g);
+    else gemm_skinny_kernel<2, false><<<wgs, 256, 0, st>>>(g);
+  }
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;
 }
@@ -860,7 +869,9 @@ int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, f
     const GemmProb &p = probs[i];
     if (p.K < 8 || p.N <= 0 || p.K % 8 || p.lda % 8 || p.ldw % 8) return RWKV7_ESHAPE;
     if (!p.A || !p.W || !p.Y) return RWKV7_EINVAL;
+    if (p.bf != probs[0].bf) return RWKV7_EINVAL;  // one operand format per launch
   }
+  const bool bf = probs[0].bf != 0;
   if (M <= kSkinnyMaxM) return launch_skinny(probs, nprob, M, st, part, ctr, gemm_ws_bytes(M, cus));
   {
     // problems the large-M path takes run there; the rest (LoRA widths) below
@@ -909,18 +920,34 @@ int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, f
   int ncmax = 1;
   for (int i = 0; i < nprob; ++i) ncmax = max(ncmax, ks[i] / kKC);
   if (BM == 32 && ncmax <= 8) {
-    if (ncmax == 1) gemm_pf_kernel<32, 1><<<wgs, 256, 0, st>>>(g);
-    else if (ncmax == 2) gemm_pf_kernel<32, 2><<<wgs, 256, 0, st>>>(g);
-    else if (ncmax <= 4) gemm_pf_kernel<32, 4><<<wgs, 256, 0, st>>>(g);
-    else gemm_pf_kernel<32, 8><<<wgs, 256, 0, st>>>(g);
+    if (bf) {
+      if (ncmax == 1) gemm_pf_kernel<32, 1, true><<<wgs, 256, 0, st>>>(g);
+      else if (ncmax == 2) gemm_pf_kernel<32, 2, true><<<wgs, 256, 0, st>>>(g);
+      else if (ncmax <= 4) gemm_pf_kernel<32, 4, true><<<wgs, 256, 0, st>>>(g);
+      else gemm_pf_kernel<32, 8, true><<<wgs, 256, 0, st>>>(g);
+    } else {
+      if (ncmax == 1) gemm_pf_kernel<32, 1, false><<<wgs, 256, 0, st>>>(g);
+      else if (ncmax == 2) gemm_pf_kernel<32, 2, false><<<wgs, 256, 0, st>>>(g);
+      else if (ncmax <= 4) gemm_pf_kernel<32, 4, false><<<wgs, 256, 0, st>>>(g);
+      else gemm_pf_kernel<32, 8, false><<<wgs, 256, 0, st>>>(g);
+    }
     RWKV7_CHECK_LAUNCH();
     return RWKV7_OK;
   }
-  switch (BM) {
-    case 16: gemm_kernel<16><<<wgs, 256, 0, st>>>(g); break;
-    case 32: gemm_kernel<32><<<wgs, 256, 0, st>>>(g); break;
-    case 64: gemm_kernel<64><<<wgs, 256, 0, st>>>(g); break;
-    default: gemm_kernel<128><<<wgs, 256, 0, st>>>(g); break;
+  if (bf) {
+    switch (BM) {
+      case 16: gemm_kernel<16, true><<<wgs, 256, 0, st>>>(g); break;
+      case 32: gemm_kernel<32, true><<<wgs, 256, 0, st>>>(g); break;
+      case 64: gemm_kernel<64, true><<<wgs, 256, 0, st>>>(g); break;
+      default: gemm_kernel<128, true><<<wgs, 256, 0, st>>>(g); break;
+    }
+  } else {
+    switch (BM) {
+      case 16: gemm_kernel<16, false><<<wgs, 256, 0, st>>>(g); break;
+      case 32: gemm_kernel<32, false><<<wgs, 256, 0, st>>>(g); break;
+      case 64: gemm_kernel<64, false><<<wgs, 256, 0, st>>>(g); break;
+      default: gemm_kernel<128, false><<<wgs, 256, 0, st>>>(g); break;
+    }
   }
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;

@@ -1,6 +1,6 @@
-// Decode-time (one token) fp16-weight GEMV kernels: y[n] = sum_k x[k] W[n, k].
+// Decode-time (one token) 16-bit-weight GEMV kernels: y[n] = sum_k x[k] W[n, k].
 //
-// W is [N, K] f16, K-contiguous rows (the checkpoint's [out, in] layout). A
+// W is [N, K] f16 (bfloat16 for a bf16 model), K-contiguous rows (the checkpoint's [out, in] layout). A
 // wavefront owns ROWS consecutive rows at a time; lane l reads the 16-byte
 // chunks l, l+64, ... of each row, so one wave instruction streams 1 KiB of
 // contiguous weights. The input vector is built once per wave in registers by
@@ -16,8 +16,9 @@
 
 namespace rwkv7 {
 
-template <int CPL, int ROWS, int PRO, int EPI>
+template <int CPL, int ROWS, int PRO, int EPI, bool BF>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+  using T16 = F16T<BF>;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int nwave = gridDim.x * 4;
@@ -29,7 +30,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     const int j = lane + kWave * c;
     if (j < nchunk) {
       if (PRO == PRO_F16) {
-        h8_to_f(reinterpret_cast<const uint4 *>(a.x)[j], xb[c]);
+        T16::to_f8(reinterpret_cast<const uint4 *>(a.x)[j], xb[c]);
       } else {
         const float4 *p = reinterpret_cast<const float4 *>(a.x) + 2 * j;
         float4 u = p[0], v = p[1];
@@ -81,7 +82,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
           o[0] = make_float4(xb[c][0], xb[c][1], xb[c][2], xb[c][3]);
           o[1] = make_float4(xb[c][4], xb[c][5], xb[c][6], xb[c][7]);
         }
-        if (PRO == PRO_TMIX || PRO == PRO_CMIX) h8_to_f(reinterpret_cast<const uint4 *>(a.prev)[j], xp[c]);
+        if (PRO == PRO_TMIX || PRO == PRO_CMIX) T16::to_f8(reinterpret_cast<const uint4 *>(a.prev)[j], xp[c]);
       }
     }
   }
@@ -142,7 +143,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (int c = 0; c < CPL; ++c) {
         float wf[8];
-        h8_to_f(w[r][c], wf);
+        T16::to_f8(w[r][c], wf);
 #pragma unroll
         for (int e = 0; e < 8; ++e) t = fmaf(wf[e], xm[c][e], t);
       }
@@ -161,7 +162,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         const float t = fmaxf(v, 0.f);
         reinterpret_cast<float *>(a.y)[n] = t * t;
       } else {
-        reinterpret_cast<uint16_t *>(a.y)[n] = f2h(v);
+        reinterpret_cast<uint16_t *>(a.y)[n] = T16::from_f(v);
       }
     }
   }
@@ -170,20 +171,26 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 // Chooses rows-per-wave and grid size: at most 16 weight chunks in flight per
 // lane, and more rows per wave only when there are enough rows to keep every
 // CU busy. The grid-stride loop covers the rest.
-template <int CPL, int PRO, int EPI>
-static int launch_gemv_cpl(const GemvArgs &a, hipStream_t st) {
+template <int CPL, int PRO, int EPI, bool BF>
+static void launch_gemv_rows(const GemvArgs &a, hipStream_t st) {
   constexpr int kMaxRows = CPL >= 16 ? 1 : 16 / CPL >= 4 ? 4 : 16 / CPL;
   if (kMaxRows >= 4 && a.N % 4 == 0 && a.N / 4 >= 4096) {
     int grid = (a.N / 4 + 3) / 4;
     if (grid > 4096) grid = 4096;
-    gemv_kernel<CPL, (kMaxRows >= 4 ? 4 : 1), PRO, EPI><<<grid, 256, 0, st>>>(a);
+    gemv_kernel<CPL, (kMaxRows >= 4 ? 4 : 1), PRO, EPI, BF><<<grid, 256, 0, st>>>(a);
   } else if (kMaxRows >= 2 && a.N % 2 == 0 && a.N / 2 >= 2048) {
     int grid = (a.N / 2 + 3) / 4;
-    gemv_kernel<CPL, (kMaxRows >= 2 ? 2 : 1), PRO, EPI><<<grid, 256, 0, st>>>(a);
+    gemv_kernel<CPL, (kMaxRows >= 2 ? 2 : 1), PRO, EPI, BF><<<grid, 256, 0, st>>>(a);
   } else {
     int grid = (a.N + 3) / 4;
-    gemv_kernel<CPL, 1, PRO, EPI><<<grid, 256, 0, st>>>(a);
+    gemv_kernel<CPL, 1, PRO, EPI, BF><<<grid, 256, 0, st>>>(a);
   }
+}
+
+template <int CPL, int PRO, int EPI>
+static int launch_gemv_cpl(const GemvArgs &a, hipStream_t st) {
+  if (a.bf) launch_gemv_rows<CPL, PRO, EPI, true>(a, st);
+  else launch_gemv_rows<CPL, PRO, EPI, false>(a, st);
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;
 }

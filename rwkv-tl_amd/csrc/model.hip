@@ -182,7 +182,8 @@ static int decode_one(const rwkv7_model &m, const rwkv7_state &s, const int64_t 
   layout_of(d, &lay);
   DecodeWs w;
   decode_ws(d, ws, &w);
-  RWKV7_TRY(launch_embed(tok, static_cast<const uint16_t *>(m.emb), w.x0, 1, C, d.vocab, st));
+  const int bf = (m.flags & RWKV7_MODEL_BF16) ? 1 : 0;
+  RWKV7_TRY(launch_embed(tok, static_cast<const uint16_t *>(m.emb), w.x0, 1, C, d.vocab, bf, st));
   for (int l = 0; l < d.n_layer; ++l) {
     const char *L = static_cast<const char *>(m.layers) + (int64_t)l * lay.bytes;
     const float *vec = reinterpret_cast<const float *>(L + lay.vec);
@@ -208,6 +209,7 @@ static int decode_one(const rwkv7_model &m, const rwkv7_state &s, const int64_t 
     memcpy(g.seg_mu, mus, sizeof mus);
     g.xln_out = w.xln;
     g.y = w.proj;
+    g.bf = bf;
     RWKV7_TRY((launch_gemv<PRO_TMIX, EPI_F32>(g, st)));
 
     TmixDecodeArgs t;
@@ -228,6 +230,7 @@ static int decode_one(const rwkv7_model &m, const rwkv7_state &s, const int64_t 
     t.rg = d.rank_g;
     t.layer0 = l == 0;
     t.yg16 = nullptr;
+    t.bf = bf;
     RWKV7_TRY(launch_tmix_decode(t, 1, st));
 
     GemvArgs o = {};
@@ -237,6 +240,7 @@ static int decode_one(const rwkv7_model &m, const rwkv7_state &s, const int64_t 
     o.K = C;
     o.x = w.yg;
     o.y = w.x0;
+    o.bf = bf;
     RWKV7_TRY((launch_gemv<PRO_F32, EPI_RESID>(o, st)));
 
     GemvArgs fk = {};
@@ -251,8 +255,9 @@ static int decode_one(const rwkv7_model &m, const rwkv7_state &s, const int64_t 
     fk.mu = vec + RWKV7_V_FFN_X_K * C;
     fk.xln_out = w.xln2;
     fk.y = w.hid;
+    fk.bf = bf;
     RWKV7_TRY((launch_gemv<PRO_CMIX, EPI_RELUSQ>(fk, st)));
-    RWKV7_TRY(launch_store_f16(w.xln2, cshift, C, st));
+    RWKV7_TRY(launch_store_f16(w.xln2, cshift, C, bf, st));
 
     GemvArgs fv = {};
     fv.W = reinterpret_cast<const uint16_t *>(L + lay.w_fv);
@@ -261,6 +266,7 @@ static int decode_one(const rwkv7_model &m, const rwkv7_state &s, const int64_t 
     fv.K = F;
     fv.x = w.hid;
     fv.y = w.x0;
+    fv.bf = bf;
     RWKV7_TRY((launch_gemv<PRO_F32, EPI_RESID>(fv, st)));
   }
   if (logits) {
@@ -274,6 +280,7 @@ static int decode_one(const rwkv7_model &m, const rwkv7_state &s, const int64_t 
     hd.ln_w = lo;
     hd.ln_b = lo + C;
     hd.y = logits;
+    hd.bf = bf;
     RWKV7_TRY((launch_gemv<PRO_LN, EPI_F16>(hd, st)));
   }
   return RWKV7_OK;
@@ -294,7 +301,13 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
   BatchWs w;
   batch_ws(d, B, T, ws, &w);
   unsigned *ctr = gemm_counters(d, ws);
-  RWKV7_TRY(launch_embed(tok, static_cast<const uint16_t *>(m.emb), w.x0, M, C, d.vocab, st));
+  const int bf = (m.flags & RWKV7_MODEL_BF16) ? 1 : 0;
+  // every GEMM of the step runs on the model's 16-bit format
+  auto gemm = [&](GemmProb *p, int n, int rows) {
+    for (int i = 0; i < n; ++i) p[i].bf = bf;
+    return launch_gemm_group(p, n, rows, st, w.part, ctr);
+  };
+  RWKV7_TRY(launch_embed(tok, static_cast<const uint16_t *>(m.emb), w.x0, M, C, d.vocab, bf, st));
   for (int l = 0; l < d.n_layer; ++l) {
     const char *L = static_cast<const char *>(m.layers) + (int64_t)l * lay.bytes;
     const float *vec = reinterpret_cast<const float *>(L + lay.vec);
@@ -307,6 +320,7 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
 
     LnShiftArgs ls = {w.x0, vec + RWKV7_V_LN1_W * C, vec + RWKV7_V_LN1_B * C, vec + RWKV7_V_X_R * C,
                       6, w.xmix, tshift, C, T, M};
+    ls.bf = bf;
     RWKV7_TRY(launch_ln_shift(ls, st));
     const uint16_t *xr = w.xmix, *xw = w.xmix + MC, *xk = w.xmix + 2 * MC, *xv = w.xmix + 3 * MC,
                    *xa = w.xmix + 4 * MC, *xg = w.xmix + 5 * MC;
@@ -335,7 +349,7 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
       frag(g1[1], lay.f_rkv, C / 16);
       frag(g1[2], lay.f_rkv, 2 * C / 16);
       for (int g = 0; g < 4; ++g) frag(g1[3 + g], lay.f_l1[g], 0);
-      RWKV7_TRY(launch_gemm_group(g1, 7, M, st, w.part, ctr));
+      RWKV7_TRY(gemm(g1, 7, M));
       TmixDecodeArgs td;
       td.proj = proj;
       td.ldp = ldp;
@@ -354,19 +368,21 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
       td.ra = ra;
       td.rg = rg;
       td.layer0 = l == 0;
+      td.bf = bf;
       RWKV7_TRY(launch_tmix_decode(td, B, st));
       GemmProb go = {w.yg, reinterpret_cast<const uint16_t *>(L + lay.w_o), w.x0, C, C, C, C, C, GEPI_ADD_F32};
       frag(go, lay.f_o, 0);
-      RWKV7_TRY(launch_gemm_group(&go, 1, M, st, w.part, ctr));
+      RWKV7_TRY(gemm(&go, 1, M));
       LnShiftArgs lc = {w.x0, vec + RWKV7_V_LN2_W * C, vec + RWKV7_V_LN2_B * C, vec + RWKV7_V_FFN_X_K * C,
                         1, w.xmix, cshift, C, T, M};
+      lc.bf = bf;
       RWKV7_TRY(launch_ln_shift(lc, st));
       GemmProb gk = {w.xmix, reinterpret_cast<const uint16_t *>(L + lay.w_fk), w.hid, C, C, F, F, C, GEPI_RELUSQ};
       frag(gk, lay.f_fk, 0);
-      RWKV7_TRY(launch_gemm_group(&gk, 1, M, st, w.part, ctr));
+      RWKV7_TRY(gemm(&gk, 1, M));
       GemmProb gv = {w.hid, reinterpret_cast<const uint16_t *>(L + lay.w_fv), w.x0, F, F, C, C, F, GEPI_ADD_F32};
       frag(gv, lay.f_fv, 0);
-      RWKV7_TRY(launch_gemm_group(&gv, 1, M, st, w.part, ctr));
+      RWKV7_TRY(gemm(&gv, 1, M));
       continue;
     }
     GemmProb g1[7] = {
@@ -389,7 +405,7 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
     frag(g1[1], lay.f_rkv, C / 16);
     frag(g1[2], lay.f_rkv, 2 * C / 16);
     for (int g = 0; g < 4; ++g) frag(g1[3 + g], lay.f_l1[g], 0);
-    RWKV7_TRY(launch_gemm_group(g1, 7, M, st, w.part, ctr));
+    RWKV7_TRY(gemm(g1, 7, M));
     GemmProb g2[4] = {
         {w.l1, wl2, w.d, SR, SR, C, C, rv, GEPI_F32},
         {w.l1 + rv, wl2 + rv, w.d + MC, SR, SR, C, C, rw, GEPI_F32},
@@ -397,35 +413,37 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
         {w.l1 + rv + rw + ra, wl2 + rv + rw + ra, w.d + 3 * MC, SR, SR, C, C, rg, GEPI_F32},
     };
     for (int g = 0; g < 4; ++g) frag(g2[g], lay.f_l2[g], 0);
-    RWKV7_TRY(launch_gemm_group(g2, 4, M, st, w.part, ctr));
+    RWKV7_TRY(gemm(g2, 4, M));
     PrefillScanArgs sc = {rnn, w.rkv, w.d, vec, w.vfirst, w.y, w.kv, w.kv + MC, B, T, H, C, M, l == 0,
                           w.U, w.Send, w.Pend};
     RWKV7_TRY(launch_wkv7_prefill(sc, st));
     GnGateArgs gn = {w.y, w.rkv, w.kv, w.kv + MC, w.d + 3 * MC, vec, w.yg, C, M};
+    gn.bf = bf;
     RWKV7_TRY(launch_gn_gate(gn, st));
     GemmProb go = {w.yg, reinterpret_cast<const uint16_t *>(L + lay.w_o), w.x0, C, C, C, C, C, GEPI_ADD_F32};
     frag(go, lay.f_o, 0);
-    RWKV7_TRY(launch_gemm_group(&go, 1, M, st, w.part, ctr));
+    RWKV7_TRY(gemm(&go, 1, M));
 
     LnShiftArgs lc = {w.x0, vec + RWKV7_V_LN2_W * C, vec + RWKV7_V_LN2_B * C, vec + RWKV7_V_FFN_X_K * C,
                       1, w.xmix, cshift, C, T, M};
+    lc.bf = bf;
     RWKV7_TRY(launch_ln_shift(lc, st));
     GemmProb gk = {w.xmix, reinterpret_cast<const uint16_t *>(L + lay.w_fk), w.hid, C, C, F, F, C, GEPI_RELUSQ};
     frag(gk, lay.f_fk, 0);
-    RWKV7_TRY(launch_gemm_group(&gk, 1, M, st, w.part, ctr));
+    RWKV7_TRY(gemm(&gk, 1, M));
     GemmProb gv = {w.hid, reinterpret_cast<const uint16_t *>(L + lay.w_fv), w.x0, F, F, C, C, F, GEPI_ADD_F32};
     frag(gv, lay.f_fv, 0);
-    RWKV7_TRY(launch_gemm_group(&gv, 1, M, st, w.part, ctr));
+    RWKV7_TRY(gemm(&gv, 1, M));
   }
   if (logits) {
     const float *lo = static_cast<const float *>(m.ln_out);
-    RWKV7_TRY(launch_ln_rows(w.x0, 1, lo, lo + C, w.headin, 0, B, C, T, T - 1, st));
+    RWKV7_TRY(launch_ln_rows(w.x0, 1, lo, lo + C, w.headin, 0, B, C, T, T - 1, bf, st));
     GemmProb gh = {w.headin, static_cast<const uint16_t *>(m.head), logits, C, C, d.vocab, d.vocab, C, GEPI_F16};
     if (m.head_frag) {
       gh.Wf = static_cast<const uint16_t *>(m.head_frag);
       gh.nksf = (C + 31) / 32;
     }
-    RWKV7_TRY(launch_gemm_group(&gh, 1, B, st, w.part, ctr));
+    RWKV7_TRY(gemm(&gh, 1, B));
   }
   return RWKV7_OK;
 }
@@ -444,7 +462,7 @@ static int check_model_state(const rwkv7_model *m, const rwkv7_state *s) {
 // multi-launch path instead.
 static bool use_persistent_decode(const rwkv7_model &m, int batch, bool logits) {
   if (batch != 1 || !logits || (m.flags & RWKV7_MODEL_MULTI_LAUNCH_DECODE)) return false;
-  return mk_usable(m.dims, mk_int8(m));
+  return mk_usable(m);
 }
 
 }  // namespace rwkv7
@@ -582,7 +600,7 @@ int rwkv7_layernorm(const void *x, int32_t x_is_f32, const float *weight, const 
                     int32_t C, void *stream) {
   if (!x || !weight || !bias || !y) return RWKV7_EINVAL;
   if (M < 1) return RWKV7_ESHAPE;
-  return launch_ln_rows(x, x_is_f32, weight, bias, y, 1, M, C, 1, 0, static_cast<hipStream_t>(stream));
+  return launch_ln_rows(x, x_is_f32, weight, bias, y, 1, M, C, 1, 0, 0, static_cast<hipStream_t>(stream));
 }
 
 int rwkv7_lerp(const void *x, const void *prev, const float *mu, int32_t n_mix, void *out, void *x_copy, int32_t C,

@@ -71,7 +71,7 @@ extern "C" int rwkv7_decode_noalloc(const rwkv7_model *model, const rwkv7_state 
   if (state->batch != 1 || (model->flags & RWKV7_MODEL_MULTI_LAUNCH_DECODE)) return RWKV7_ESHAPE;
   const rwkv7_dims &d = model->dims;
   if ((model->flags & RWKV7_MODEL_INT8_DECODE) && !mk_int8(*model)) return RWKV7_EINVAL;
-  if (!mk_usable(d, mk_int8(*model))) return RWKV7_ESHAPE;
+  if (!mk_usable(*model)) return RWKV7_ESHAPE;
   const int64_t need = mk_exchange_bytes(d.n_embd, d.n_ffn, d.rank_w + d.rank_a + d.rank_v + d.rank_g);
   if (need > kNoAllocScratchBytes) return RWKV7_EWORKSPACE;
 

@@ -107,6 +107,49 @@ RWKV7_DEV uint4 f_to_h8(const float f[8]) {
 RWKV7_DEV float h2f(uint16_t u) { return (float)__builtin_bit_cast(_Float16, u); }
 RWKV7_DEV uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
+// bfloat16: the upper half of an fp32 (widening is exact); narrowing rounds
+// to nearest even (v_cvt_pk_bf16_f32).
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+RWKV7_DEV float b2f(uint16_t u) { return __builtin_bit_cast(float, (uint32_t)u << 16); }
+RWKV7_DEV uint16_t f2b(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+
+// The 16-bit storage format of a model's weights, shift states and logits:
+// IEEE half (BF = false) or bfloat16 (BF = true). Arithmetic is fp32 either way.
+template <bool BF>
+struct F16T {
+  static RWKV7_DEV float to_f(uint16_t u) { return BF ? b2f(u) : h2f(u); }
+  static RWKV7_DEV uint16_t from_f(float f) { return BF ? f2b(f) : f2h(f); }
+  static RWKV7_DEV void to_f8(const uint4 &u, float f[8]) {
+    if constexpr (BF) {
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f[2 * i] = __builtin_bit_cast(float, w[i] << 16);
+        f[2 * i + 1] = __builtin_bit_cast(float, w[i] & 0xFFFF0000u);
+      }
+    } else {
+      h8_to_f(u, f);
+    }
+  }
+  static constexpr uint16_t kNaN = BF ? 0x7FC0u : 0x7E00u;
+};
+
+// The same chosen at run time (small elementwise kernels).
+RWKV7_DEV float u16_to_f(uint16_t u, int bf) { return bf ? b2f(u) : h2f(u); }
+RWKV7_DEV uint16_t f_to_u16(float f, int bf) { return bf ? f2b(f) : f2h(f); }
+
+// 16x16x32 MFMA on 16-bit operands of format F16T<BF> (8 per lane, any
+// 16-byte type), fp32 accumulation.
+template <bool BF, class T>
+RWKV7_DEV floatx4 mfma16(const T &a, const T &b, const floatx4 &c) {
+  if constexpr (BF)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0,
+                                                  0, 0);
+}
+
 RWKV7_DEV float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
 
 // Weight streams are read exactly once per step: load them non-temporally so

@@ -22,6 +22,7 @@ struct GemvArgs {
   int seg_mu[7];
   float *xln_out;
   void *y;
+  int bf;  // W, a 16-bit x, prev and a 16-bit y are bfloat16 (else half)
 };
 template <int PRO, int EPI> int launch_gemv(const GemvArgs &a, hipStream_t st);
 
@@ -43,6 +44,7 @@ struct TmixDecodeArgs {
   float *yg;
   int C, H, rv, rw, ra, rg, layer0;
   uint16_t *yg16;
+  int bf;  // w_lora2, shift and yg16 are bfloat16 (else half)
 };
 int launch_tmix_decode(const TmixDecodeArgs &a, int B, hipStream_t st);
 
@@ -83,6 +85,7 @@ struct LnShiftArgs {
   uint16_t *out;
   uint16_t *shift;
   int C, T, M;
+  int bf;  // out and shift are bfloat16 (else half)
 };
 int launch_ln_shift(const LnShiftArgs &a, hipStream_t st);
 
@@ -109,15 +112,17 @@ struct GnGateArgs {
   const float *y, *r, *kn, *v, *g, *vec;
   uint16_t *out;
   int C, M;
+  int bf;  // out is bfloat16 (else half)
 };
 int launch_gn_gate(const GnGateArgs &a, hipStream_t st);
 
-int launch_embed(const int64_t *tok, const uint16_t *emb, float *x0, int M, int C, int V, hipStream_t st);
+// bf: the 16-bit operands are bfloat16 (else half)
+int launch_embed(const int64_t *tok, const uint16_t *emb, float *x0, int M, int C, int V, int bf, hipStream_t st);
 int launch_ln_rows(const void *x, int x_f32, const float *w, const float *b, void *out, int out_f32,
-                   int rows, int C, int stride, int offset, hipStream_t st);
+                   int rows, int C, int stride, int offset, int bf, hipStream_t st);
 int launch_lerp(const uint16_t *x, const uint16_t *prev, const float *mu, int n_mix, uint16_t *out,
                 uint16_t *x_copy, int C, hipStream_t st);
-int launch_store_f16(const float *src, uint16_t *dst, int n, hipStream_t st);
+int launch_store_f16(const float *src, uint16_t *dst, int n, int bf, hipStream_t st);
 
 enum { GEPI_F32 = 0, GEPI_F16 = 1, GEPI_RELUSQ = 2, GEPI_ADD_F32 = 3, GEPI_TANH_F16 = 4, GEPI_SIGM_F16 = 5 };
 struct GemmProb {
@@ -129,6 +134,9 @@ struct GemmProb {
   // nksf blocks per 16-row strip; nullptr reads the row-major W
   const uint16_t *Wf;
   int nksf;
+  // A, W and the 16-bit outputs are bfloat16 (else IEEE half); one value for
+  // every problem of a launch
+  int bf;
 };
 // Split-K workspace: gemm_ws_bytes(M, cus) bytes of partial tiles and
 // kGemmCounters arrival counters that start at zero (every launch leaves them
@@ -153,9 +161,10 @@ int launch_gn_rkrk(const uint16_t *y, const uint16_t *r, const uint16_t *k, cons
 // One-token, one-sequence decode as a single persistent kernel (decode_mk.hip).
 int mk_cus();
 bool mk_supported(const rwkv7_dims &d, int G);
-// mk_supported on the current device's CU count, and the kernel's grid (the
-// int8-weight instance if q8) fits there all at once (checked once per device)
-bool mk_usable(const rwkv7_dims &d, bool q8);
+// mk_supported on the current device's CU count, and the grid of the kernel
+// instance for the model's formats (int8 or 16-bit matrices; half or bfloat16)
+// fits there all at once (checked once per device)
+bool mk_usable(const rwkv7_model &m);
 // the model asks for int8 decode and has the int8 arenas
 bool mk_int8(const rwkv7_model &m);
 int64_t mk_exchange_bytes(int C, int F, int SR);

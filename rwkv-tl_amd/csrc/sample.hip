@@ -277,9 +277,10 @@ RWKV7_DEV void philox4x32_10(uint32_t c[4], uint32_t k0, uint32_t k1) {
 
 // Logits 8..8c+7 of this thread's 64, as f32 (-inf past V). VEC: rows
 // 16-byte aligned and V % 8 == 0, so each 8-logit chunk is whole 16-byte
-// loads or wholly past V.
-template <bool VEC, bool F32>
+// loads or wholly past V. FMT: 0 half, 1 f32, 2 bfloat16.
+template <bool VEC, int FMT>
 RWKV7_DEV void load8(const void *row_ptr, int i0, int V, float *f) {
+  constexpr bool F32 = FMT == 1, BF = FMT == 2;
   if (VEC) {
     if (F32) {
       const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(row_ptr) + i0);
@@ -287,28 +288,30 @@ RWKV7_DEV void load8(const void *row_ptr, int i0, int V, float *f) {
       const float4 v = i0 < V ? p[1] : make_float4(-kInf, -kInf, -kInf, -kInf);
       f[0] = u.x, f[1] = u.y, f[2] = u.z, f[3] = u.w, f[4] = v.x, f[5] = v.y, f[6] = v.z, f[7] = v.w;
     } else {
-      const uint32_t ninf2 = 0xfc00fc00u;  // two f16 -inf
+      const uint32_t ninf2 = BF ? 0xff80ff80u : 0xfc00fc00u;  // two 16-bit -inf
       const uint4 u = i0 < V ? *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(row_ptr) + i0)
                              : make_uint4(ninf2, ninf2, ninf2, ninf2);
-      h8_to_f(u, f);
+      F16T<BF>::to_f8(u, f);
     }
   } else {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int i = i0 + j;
-      f[j] = i >= V ? -kInf : F32 ? static_cast<const float *>(row_ptr)[i] : h2f(static_cast<const uint16_t *>(row_ptr)[i]);
+      f[j] = i >= V  ? -kInf
+             : F32 ? static_cast<const float *>(row_ptr)[i]
+                   : F16T<BF>::to_f(static_cast<const uint16_t *>(row_ptr)[i]);
     }
   }
 }
 
-template <bool VEC, bool F32>
+template <bool VEC, int FMT>
 __global__ __launch_bounds__(kSmpThreads) void sample_kernel(SampleArgs a) {
   __shared__ SampleLds s;
   const int row = blockIdx.x, base = threadIdx.x * kSmpE, V = a.V;
-  const void *src = static_cast<const char *>(a.logits) + (int64_t)row * a.ld * (F32 ? 4 : 2);
+  const void *src = static_cast<const char *>(a.logits) + (int64_t)row * a.ld * (FMT == 1 ? 4 : 2);
   float l[kSmpE];
 #pragma unroll
-  for (int c = 0; c < kSmpE / 8; ++c) load8<VEC, F32>(src, base + 8 * c, V, &l[8 * c]);
+  for (int c = 0; c < kSmpE / 8; ++c) load8<VEC, FMT>(src, base + 8 * c, V, &l[8 * c]);
   // repetition penalty (sampling.py:44-47), applied once per seen token
   if (a.seen && a.pen != 1.f) {
     const uint32_t *sr = a.seen + (int64_t)row * a.seen_ld;
@@ -413,11 +416,12 @@ __global__ __launch_bounds__(kSmpThreads) void sample_kernel(SampleArgs a) {
 }  // namespace
 }  // namespace rwkv7
 
-extern "C" int rwkv7_sample(const void *logits, int32_t logits_is_f32, int64_t ld, int32_t B, int32_t V, const rwkv7_sampling *p,
+extern "C" int rwkv7_sample(const void *logits, int32_t logits_dtype, int64_t ld, int32_t B, int32_t V, const rwkv7_sampling *p,
                             uint32_t *seen, int64_t seen_ld, int32_t update_seen, int64_t *out, float *probs,
                             int64_t probs_ld, void *stream) {
   using namespace rwkv7;
   if (!logits || !p || !out || B < 1 || (update_seen && !seen)) return RWKV7_EINVAL;
+  if (logits_dtype < 0 || logits_dtype > 2) return RWKV7_EINVAL;
   if (V < 1 || V > kSmpMaxV || ld < V || (seen && seen_ld < (V + 31) / 32) || (probs && probs_ld < V))
     return RWKV7_ESHAPE;
   SampleArgs a;
@@ -438,10 +442,11 @@ extern "C" int rwkv7_sample(const void *logits, int32_t logits_is_f32, int64_t l
   a.probs_ld = probs_ld;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const bool vec = reinterpret_cast<uintptr_t>(logits) % 16 == 0 && ld % 8 == 0 && V % 8 == 0;
-  if (logits_is_f32)
-    vec ? sample_kernel<true, true><<<B, kSmpThreads, 0, st>>>(a) : sample_kernel<false, true><<<B, kSmpThreads, 0, st>>>(a);
-  else
-    vec ? sample_kernel<true, false><<<B, kSmpThreads, 0, st>>>(a) : sample_kernel<false, false><<<B, kSmpThreads, 0, st>>>(a);
+  switch (logits_dtype) {
+    case 0: vec ? sample_kernel<true, 0><<<B, kSmpThreads, 0, st>>>(a) : sample_kernel<false, 0><<<B, kSmpThreads, 0, st>>>(a); break;
+    case 1: vec ? sample_kernel<true, 1><<<B, kSmpThreads, 0, st>>>(a) : sample_kernel<false, 1><<<B, kSmpThreads, 0, st>>>(a); break;
+    default: vec ? sample_kernel<true, 2><<<B, kSmpThreads, 0, st>>>(a) : sample_kernel<false, 2><<<B, kSmpThreads, 0, st>>>(a); break;
+  }
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;
 }

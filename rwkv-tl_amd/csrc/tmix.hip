@@ -21,7 +21,9 @@ namespace rwkv7 {
 // ---------------------------------------------------------------------------
 
 
+template <bool BF>
 __global__ __launch_bounds__(256) void tmix_decode_kernel(TmixDecodeArgs a) {
+  using T16 = F16T<BF>;
   __shared__ float s_lora[512];
   __shared__ float s_d[4][kN];
   __shared__ float s_r[kN], s_w[kN], s_k[kN], s_v[kN], s_a[kN], s_b[kN], s_g[kN], s_y[kN];
@@ -51,7 +53,7 @@ __global__ __launch_bounds__(256) void tmix_decode_kernel(TmixDecodeArgs a) {
 #pragma unroll 4
     for (int r = 0; r < R; r += 8) {
       float wf[8];
-      h8_to_f(wr[r >> 3], wf);
+      T16::to_f8(wr[r >> 3], wf);
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc = fmaf(wf[e], s_lora[off + r + e], acc);
     }
@@ -79,7 +81,7 @@ __global__ __launch_bounds__(256) void tmix_decode_kernel(TmixDecodeArgs a) {
     s_r[t] = r; s_w[t] = w; s_k[t] = kn; s_v[t] = v;
     s_a[t] = kh; s_b[t] = -kh * ag; s_g[t] = s_d[3][t];
     if (t == 0) s_rk = rk;
-    if (a.shift) a.shift[(int64_t)b * C + ch] = f2h(a.xln[(int64_t)b * C + ch]);
+    if (a.shift) a.shift[(int64_t)b * C + ch] = T16::from_f(a.xln[(int64_t)b * C + ch]);
   }
   __syncthreads();
 
@@ -119,13 +121,14 @@ __global__ __launch_bounds__(256) void tmix_decode_kernel(TmixDecodeArgs a) {
     const float var = wave_sum(d * d) * (1.f / kN);
     const float yn = d * rsqrtf(var + kGnEps) * vec[RWKV7_V_LNX_W * C + ch] + vec[RWKV7_V_LNX_B * C + ch];
     const float out = (yn + s_rk * s_v[t]) * s_g[t];
-    if (a.yg16) a.yg16[(int64_t)b * C + ch] = f2h(out);
+    if (a.yg16) a.yg16[(int64_t)b * C + ch] = T16::from_f(out);
     else a.yg[(int64_t)b * C + ch] = out;
   }
 }
 
 int launch_tmix_decode(const TmixDecodeArgs &a, int B, hipStream_t st) {
-  tmix_decode_kernel<<<dim3(a.H, B), 256, 0, st>>>(a);
+  if (a.bf) tmix_decode_kernel<true><<<dim3(a.H, B), 256, 0, st>>>(a);
+  else tmix_decode_kernel<false><<<dim3(a.H, B), 256, 0, st>>>(a);
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;
 }
@@ -818,16 +821,17 @@ __global__ __launch_bounds__(256) void ln_shift_kernel(LnShiftArgs a) {
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
     xc[i] = (xc[i] - m0) * r0 * lw[i] + lb[i];
-    xp[i] = has_prev ? (xp[i] - m1) * r1 * lw[i] + lb[i] : h2f(st[i]);
+    xp[i] = has_prev ? (xp[i] - m1) * r1 * lw[i] + lb[i] : u16_to_f(st[i], a.bf);
   }
   for (int j = 0; j < a.n_mix; ++j) {
     uint16_t *o = a.out + ((int64_t)j * a.M + m) * C;
 #pragma unroll
-    for (int i = 0; i < NP; ++i) o[tid + 256 * i] = f2h(xc[i] + mu[j][i] * (xp[i] - xc[i]));
+    for (int i = 0; i < NP; ++i) o[tid + 256 * i] = f_to_u16(xc[i] + mu[j][i] * (xp[i] - xc[i]), a.bf);
   }
   if (t == 0) {
 #pragma unroll
-    for (int i = 0; i < NP; ++i) sh[tid + 256 * i] = f2h(has_last ? (xl[i] - m2) * r2 * lw[i] + lb[i] : xc[i]);
+    for (int i = 0; i < NP; ++i)
+      sh[tid + 256 * i] = f_to_u16(has_last ? (xl[i] - m2) * r2 * lw[i] + lb[i] : xc[i], a.bf);
   }
 }
 
@@ -862,7 +866,7 @@ __global__ __launch_bounds__(256) void gn_gate_kernel(GnGateArgs a) {
   const float var = wave_sum(d * d) * (1.f / kN);
   const float yn = d * rsqrtf(var + kGnEps) * a.vec[RWKV7_V_LNX_W * C + ch] + a.vec[RWKV7_V_LNX_B * C + ch];
   const float rk = wave_sum(a.r[o] * a.kn[o] * a.vec[RWKV7_V_R_K * C + ch]);
-  a.out[o] = f2h((yn + rk * a.v[o]) * a.g[o]);
+  a.out[o] = f_to_u16((yn + rk * a.v[o]) * a.g[o], a.bf);
 }
 
 int launch_gn_gate(const GnGateArgs &a, hipStream_t st) {
@@ -877,16 +881,16 @@ int launch_gn_gate(const GnGateArgs &a, hipStream_t st) {
 // ---------------------------------------------------------------------------
 
 // x0[m] = emb[tok[m]] as f32 (F.embedding, demo/rwkv7_torch.py:173-175).
-__global__ void embed_kernel(const int64_t *tok, const uint16_t *emb, float *x0, int C, int V) {
+__global__ void embed_kernel(const int64_t *tok, const uint16_t *emb, float *x0, int C, int V, int bf) {
   const int m = blockIdx.x;
   int64_t id = tok[m];
   id = id < 0 ? 0 : id >= V ? V - 1 : id;
   const uint16_t *row = emb + id * C;
-  for (int c = threadIdx.x; c < C; c += blockDim.x) x0[(int64_t)m * C + c] = h2f(row[c]);
+  for (int c = threadIdx.x; c < C; c += blockDim.x) x0[(int64_t)m * C + c] = u16_to_f(row[c], bf);
 }
 
-int launch_embed(const int64_t *tok, const uint16_t *emb, float *x0, int M, int C, int V, hipStream_t st) {
-  embed_kernel<<<M, 256, 0, st>>>(tok, emb, x0, C, V);
+int launch_embed(const int64_t *tok, const uint16_t *emb, float *x0, int M, int C, int V, int bf, hipStream_t st) {
+  embed_kernel<<<M, 256, 0, st>>>(tok, emb, x0, C, V, bf);
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;
 }
@@ -895,7 +899,7 @@ int launch_embed(const int64_t *tok, const uint16_t *emb, float *x0, int M, int 
 // last token of each sequence before the LM head).
 __global__ __launch_bounds__(256) void ln_rows_kernel(const void *x, int x_f32, const float *w,
                                                       const float *bvec, void *out, int out_f32,
-                                                      int C, int stride, int offset) {
+                                                      int C, int stride, int offset, int bf) {
   __shared__ float scratch4[4];
   const int i = blockIdx.x;
   const int64_t src = (int64_t)i * stride + offset;
@@ -905,7 +909,7 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const void *x, int x_f32, 
   RWKV7_UNROLL_N(q) {
     const int c = threadIdx.x + 256 * q;
     v[q] = x_f32 ? reinterpret_cast<const float *>(x)[src * C + c]
-                 : h2f(reinterpret_cast<const uint16_t *>(x)[src * C + c]);
+                 : u16_to_f(reinterpret_cast<const uint16_t *>(x)[src * C + c], bf);
     s += v[q];
   }
   const float mean = block_sum256(s, scratch4) / (float)C;
@@ -919,14 +923,14 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const void *x, int x_f32, 
     const int c = threadIdx.x + 256 * q;
     const float y = (v[q] - mean) * rstd * w[c] + bvec[c];
     if (out_f32) reinterpret_cast<float *>(out)[(int64_t)i * C + c] = y;
-    else reinterpret_cast<uint16_t *>(out)[(int64_t)i * C + c] = f2h(y);
+    else reinterpret_cast<uint16_t *>(out)[(int64_t)i * C + c] = f_to_u16(y, bf);
   }
 }
 
 int launch_ln_rows(const void *x, int x_f32, const float *w, const float *b, void *out, int out_f32,
-                   int rows, int C, int stride, int offset, hipStream_t st) {
+                   int rows, int C, int stride, int offset, int bf, hipStream_t st) {
   if (C % 256 || C > 256 * kMaxCPer) return RWKV7_ESHAPE;
-  ln_rows_kernel<<<rows, 256, 0, st>>>(x, x_f32, w, b, out, out_f32, C, stride, offset);
+  ln_rows_kernel<<<rows, 256, 0, st>>>(x, x_f32, w, b, out, out_f32, C, stride, offset, bf);
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;
 }
@@ -948,15 +952,15 @@ int launch_lerp(const uint16_t *x, const uint16_t *prev, const float *mu, int n_
   return RWKV7_OK;
 }
 
-// Copies f32 -> f16 (decode: the channel-mix token-shift state update after
-// the FFN key GEMV has read the old state).
-__global__ void store_f16_kernel(const float *src, uint16_t *dst, int n) {
+// Copies f32 -> 16-bit (decode: the channel-mix token-shift state update
+// after the FFN key GEMV has read the old state).
+__global__ void store_f16_kernel(const float *src, uint16_t *dst, int n, int bf) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) dst[i] = f2h(src[i]);
+  if (i < n) dst[i] = f_to_u16(src[i], bf);
 }
 
-int launch_store_f16(const float *src, uint16_t *dst, int n, hipStream_t st) {
-  store_f16_kernel<<<(n + 255) / 256, 256, 0, st>>>(src, dst, n);
+int launch_store_f16(const float *src, uint16_t *dst, int n, int bf, hipStream_t st) {
+  store_f16_kernel<<<(n + 255) / 256, 256, 0, st>>>(src, dst, n, bf);
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;
 }

@@ -21,7 +21,7 @@ from . import operators  # noqa: F401  (registers torch.ops.rwkv_tl.*, as src/rw
 from .checkpoint import SHAPES, ModelShape, make_random_state_dict
 from .hip_graph import HIPGraph, make_graph_cls, wrap_model
 from .model import RWKV7Model
-from .rwkv7_hip import RWKV7HIP, RWKV7HIPInt8
+from .rwkv7_hip import RWKV7HIP, RWKV7HIPBF16, RWKV7HIPInt8
 from .sampling import sample_logits
 from .state import State
 from .weight import LNWeight, RWKV7Weight
@@ -31,6 +31,7 @@ __all__ = [
     "LNWeight",
     "ModelShape",
     "RWKV7HIP",
+    "RWKV7HIPBF16",
     "RWKV7HIPInt8",
     "RWKV7Model",
     "RWKV7Weight",
@@ -59,19 +60,19 @@ def make_rwkv7(
     """Pick the model class for ``device`` (``demo/__init__.py:43-78``).
 
     Returns ``RWKV7HIP`` wrapped in ``HIPGraph`` when ``use_graph`` (the
-    default) and the device is a GPU; ``backend="int8"`` returns
-    ``RWKV7HIPInt8`` (batch-1 decode on per-row int8 weights). ``backend="bf16"`` and
-    ``backend="torch"`` raise: this library is fp16-only, and the pure-torch
+    default) and the device is a GPU; ``backend="bf16"`` returns
+    ``RWKV7HIPBF16`` (bfloat16 weights, as ``demo/__init__.py:104-105`` picks
+    ``RWKV7BF16``) and ``backend="int8"`` ``RWKV7HIPInt8`` (batch-1 decode on
+    per-row int8 weights). ``backend="torch"`` raises: the pure-torch
     reference model is a test oracle here, not a product backend.
     """
     device = torch.device(device)
-    if backend == "bf16":
-        raise ValueError("backend 'bf16' is not provided: the HIP kernels are float16 only")
     if backend == "torch":
         raise ValueError("backend 'torch' is not provided: the pure-torch model is only a test oracle here")
-    if backend not in _HIP_BACKENDS + ("int8",):
-        raise ValueError(f"unknown backend {backend!r} (expected one of {', '.join(_HIP_BACKENDS + ('int8',))})")
+    names = _HIP_BACKENDS + ("bf16", "int8")
+    if backend not in names:
+        raise ValueError(f"unknown backend {backend!r} (expected one of {', '.join(names)})")
     if device.type != "cuda":
         raise ValueError(f"RWKV7HIP runs on a ROCm GPU; got device {device}")
-    cls = RWKV7HIPInt8 if backend == "int8" else RWKV7HIP
+    cls = {"bf16": RWKV7HIPBF16, "int8": RWKV7HIPInt8}.get(backend, RWKV7HIP)
     return make_graph_cls(cls) if use_graph else cls

@@ -15,11 +15,12 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the HIP library)
 
 LIB_NAME = "librwkv7_hip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # rwkv7_model.flags
 MODEL_MULTI_LAUNCH_DECODE = 1
 MODEL_INT8_DECODE = 2
+MODEL_BF16 = 4
 
 # enum indices of the per-layer fp32 vector block (RWKV7_V_*)
 VEC_NAMES = (

@@ -118,7 +118,7 @@ class HIPGraph(RWKV7Model):
         entry = self._graphs.get(key)
         if entry is None:
             tok = torch.zeros(B, dtype=torch.int64, device=self.w.device)
-            logits = torch.empty(B, m.V, dtype=torch.float16, device=self.w.device)
+            logits = torch.empty(B, m.V, dtype=m.kernel_dtype, device=self.w.device)
             ws = m.workspace(B, 1)  # allocated outside the capture; the entry keeps it alive
             graph = self._capture(key, S, lambda: m.decode_into(tok, S, logits))
             if graph is None:

@@ -31,7 +31,8 @@ class RWKV7HIP(RWKV7Model):
     """RWKV7 decode / prefill on MI355X (fp16 weights, fp32 state and accumulation).
 
     Args:
-        w: weights loaded as float16 on a ROCm device.
+        w: weights loaded as float16 on a ROCm device (``RWKV7HIPBF16``:
+            bfloat16).
         is_torch_compile: accepted for signature compatibility with the
             reference classes and ignored (launch overhead is removed with HIP
             graphs instead, see ``HIPGraph``).
@@ -41,10 +42,13 @@ class RWKV7HIP(RWKV7Model):
             bytes per token; prefill and batched decode keep the fp16 weights.
     """
 
+    # the 16-bit format of the weights, the shift states and the logits
+    kernel_dtype = torch.float16
+
     def __init__(self, w: RWKV7Weight, *, is_torch_compile: bool = True, weight_quant: str | None = None) -> None:
         super().__init__(w)
-        if w.dtype != torch.float16:
-            raise ValueError(f"kernel dtype torch.float16 does not match weight dtype {w.dtype}")
+        if w.dtype != self.kernel_dtype:
+            raise ValueError(f"kernel dtype {self.kernel_dtype} does not match weight dtype {w.dtype}")
         if w.device.type != "cuda":
             raise ValueError(f"RWKV7HIP needs the weights on a ROCm GPU, got {w.device}")
         self._is_torch_compile = is_torch_compile
@@ -105,8 +109,8 @@ class RWKV7HIP(RWKV7Model):
         t0 = S[0][0]
         if len(S[0]) != self.L or t0["x"].shape[-1] != self.C:
             raise ValueError(f"state of {len(S[0])} layers x {t0['x'].shape[-1]} does not fit the model")
-        if t0["x"].dtype != torch.float16:
-            raise ValueError(f"state dtype {t0['x'].dtype} does not match the model dtype torch.float16")
+        if t0["x"].dtype != self.kernel_dtype:
+            raise ValueError(f"state dtype {t0['x'].dtype} does not match the model dtype {self.kernel_dtype}")
         if t0["x"].device != self.w.device:
             raise ValueError(f"state on {t0['x'].device}, model on {self.w.device}")
 
@@ -118,7 +122,7 @@ class RWKV7HIP(RWKV7Model):
         """``S`` itself if its tensors are intact arena views, else a copy."""
         if isinstance(S, State) and S.arena_intact():
             return S, False
-        shadow = State(self.L, self.C, self.N, device=self.w.device, dtype=torch.float16,
+        shadow = State(self.L, self.C, self.N, device=self.w.device, dtype=self.kernel_dtype,
                        batch=None if S[0][0]["rnn"].dim() == 3 else self._batch_of(S))
         shadow.copy_(S)
         return shadow, True
@@ -147,7 +151,7 @@ class RWKV7HIP(RWKV7Model):
         return int(self._lib.rwkv7_decode_launches(ctypes.byref(self.dev.desc), batch, 1))
 
     def decode_into(self, tok: Tensor, S: State, logits: Tensor | None) -> None:
-        """One decode step: ``tok`` int64 [B] on device, ``logits`` f16 [B, V] or None."""
+        """One decode step: ``tok`` int64 [B] on device, ``logits`` [B, V] of the model's dtype, or None."""
         B = S.batch_size
         ws = self.workspace(B, 1)
         sd = self._desc(S)
@@ -179,7 +183,7 @@ class RWKV7HIP(RWKV7Model):
         B = self._batch_of(S)
         tok = self._tokens(token, (B,))
         run, shadow = self._arena_state(S)
-        logits = torch.empty(B, self.V, dtype=torch.float16, device=self.w.device)
+        logits = torch.empty(B, self.V, dtype=self.kernel_dtype, device=self.w.device)
         self.decode_into(tok, run, logits)
         if shadow:
             _copy_into(S, run)
@@ -214,6 +218,15 @@ def _copy_into(dst, src: State) -> None:
     for ds, ss in zip(dst[0] + dst[1], src[0] + src[1]):
         for k in ds:
             ds[k].copy_(ss[k])
+
+
+class RWKV7HIPBF16(RWKV7HIP):
+    """The bfloat16 model (``demo/rwkv7_bf16.py:18-27``): bfloat16 weights as
+    loaded (``RWKV7Weight(path, dtype=torch.bfloat16)``, no conversion),
+    bfloat16 shift states and logits, bf16 MFMA operands in the GEMMs; fp32
+    arithmetic and wkv state as in the float16 model."""
+
+    kernel_dtype = torch.bfloat16
 
 
 class RWKV7HIPInt8(RWKV7HIP):

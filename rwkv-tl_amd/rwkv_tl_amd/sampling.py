@@ -43,6 +43,10 @@ def _params(temperature, top_k, top_p, repetition_penalty, seed: int, offset: in
     )
 
 
+# logits dtypes the kernel reads directly, and their rwkv7_sample code
+_LOGIT_DTYPES = {torch.float16: 0, torch.float32: 1, torch.bfloat16: 2}
+
+
 def _check_logits(logits: Tensor) -> Tensor:
     if not logits.is_cuda:
         raise ValueError("sample_logits runs the HIP sampling kernel: logits must be on the GPU")
@@ -50,7 +54,7 @@ def _check_logits(logits: Tensor) -> Tensor:
         raise ValueError(f"expected [V] or [B, V] logits, got {tuple(logits.shape)}")
     if logits.shape[-1] > MAX_VOCAB or logits.shape[-1] == 0:
         raise ValueError(f"vocabulary of {logits.shape[-1]} is outside 1..{MAX_VOCAB}")
-    if logits.dtype not in (torch.float16, torch.float32):
+    if logits.dtype not in _LOGIT_DTYPES:
         logits = logits.float()
     return logits if logits.stride(-1) == 1 else logits.contiguous()
 
@@ -81,7 +85,7 @@ def sample_into(
     update_seen: bool = False,
     probs: Tensor | None = None,
 ) -> None:
-    """One ``rwkv7_sample`` launch: logits f16/f32 [B, V] (unit column stride)
+    """One ``rwkv7_sample`` launch: logits f16/f32/bf16 [B, V] (unit column stride)
     -> out int64 [B]; ``seen`` int32 [B, ceil(V/32)]; ``probs`` f32 [B, V]."""
     lib = _lib.load()
     B, V = logits.shape
@@ -93,7 +97,7 @@ def sample_into(
         raise ValueError(f"probs must be a contiguous float32 [{B}, {V}] tensor")
     p = _params(temperature, top_k, top_p, repetition_penalty, seed, offset)
     rc = lib.rwkv7_sample(
-        logits.data_ptr(), int(logits.dtype == torch.float32), logits.stride(0), B, V, ctypes.byref(p),
+        logits.data_ptr(), _LOGIT_DTYPES[logits.dtype], logits.stride(0), B, V, ctypes.byref(p),
         _lib.ptr(seen), 0 if seen is None else seen.stride(0), int(update_seen), out.data_ptr(),
         _lib.ptr(probs), 0 if probs is None else probs.stride(0), _lib.stream_handle(),
     )

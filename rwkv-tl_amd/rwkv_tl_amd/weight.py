@@ -212,20 +212,24 @@ def layer_layout(dims: _lib.Dims) -> _lib.LayerLayout:
     return out
 
 
-def _f16_view(buf: Tensor, off: int, rows: int, cols: int) -> Tensor:
-    return buf[off : off + rows * cols * 2].view(torch.float16).view(rows, cols)
+def _f16_view(buf: Tensor, off: int, rows: int, cols: int, dtype: torch.dtype = torch.float16) -> Tensor:
+    """A [rows, cols] view of 16-bit values (float16 or bfloat16) at byte ``off``."""
+    return buf[off : off + rows * cols * 2].view(dtype).view(rows, cols)
 
 
 def pack_device_weights(w: RWKV7Weight, fragments: bool = True, int8: bool = False) -> DeviceWeights:
-    """Build the HIP arenas from reference-layout weights (fp16, on the GPU).
+    """Build the HIP arenas from reference-layout weights (float16 or
+    bfloat16, on the GPU); every 16-bit section keeps the weights' format, and
+    a bfloat16 model gets the ``RWKV7_MODEL_BF16`` flag.
 
     ``fragments`` also builds the fragment-order copy the prefill / batched
     decode GEMMs stream (one contiguous KiB per wave load); it roughly doubles
     the weight memory. ``int8`` also builds the int8 arenas of the batch-1
     decode (``quantize_rows_i8`` per matrix row) and sets the model flag that
     makes batch-1 decode stream them."""
-    if w.dtype != torch.float16:
-        raise ValueError(f"the HIP kernels take float16 weights, got {w.dtype}")
+    if w.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"the HIP kernels take float16 or bfloat16 weights, got {w.dtype}")
+    dt = w.dtype
     dims = model_dims(w)
     lay = layer_layout(dims)
     C, F_ = dims.n_embd, dims.n_ffn
@@ -234,14 +238,14 @@ def pack_device_weights(w: RWKV7Weight, fragments: bool = True, int8: bool = Fal
     layers = torch.zeros(dims.n_layer, lay.bytes, dtype=torch.uint8, device=dev)
     for i, blk in enumerate(w.blocks):
         att, ffn, buf = blk.att, blk.ffn, layers[i]
-        rkv = _f16_view(buf, lay.w_rkv, 3 * C, C)
+        rkv = _f16_view(buf, lay.w_rkv, 3 * C, C, dt)
         for j in range(3):
             rkv[j * C : (j + 1) * C].copy_(att.rkvWt[j].T)
-        _f16_view(buf, lay.w_lora1, SR, C).copy_(torch.cat([att.v1t, att.w1t, att.a1t, att.g1t], 0))
-        _f16_view(buf, lay.w_lora2, C, SR).copy_(torch.cat([att.v2.T, att.w2.T, att.a2.T, att.g2.T], 1))
-        _f16_view(buf, lay.w_o, C, C).copy_(att.oWt.T)
-        _f16_view(buf, lay.w_fk, F_, C).copy_(ffn.kWt.T)
-        _f16_view(buf, lay.w_fv, C, F_).copy_(ffn.vWt.T)
+        _f16_view(buf, lay.w_lora1, SR, C, dt).copy_(torch.cat([att.v1t, att.w1t, att.a1t, att.g1t], 0))
+        _f16_view(buf, lay.w_lora2, C, SR, dt).copy_(torch.cat([att.v2.T, att.w2.T, att.a2.T, att.g2.T], 1))
+        _f16_view(buf, lay.w_o, C, C, dt).copy_(att.oWt.T)
+        _f16_view(buf, lay.w_fk, F_, C, dt).copy_(ffn.kWt.T)
+        _f16_view(buf, lay.w_fv, C, F_, dt).copy_(ffn.vWt.T)
         vec = buf[lay.vec : lay.vec + _lib.NVEC * C * 4].view(torch.float32).view(_lib.NVEC, C)
         src = {
             "ln1_w": att.ln_pre.w, "ln1_b": att.ln_pre.b,
@@ -265,19 +269,19 @@ def pack_device_weights(w: RWKV7Weight, fragments: bool = True, int8: bool = Fal
 
             def put(off: int, Wm: Tensor) -> None:
                 f = to_fragments(Wm)
-                buf[off : off + f.numel() * 2].view(torch.float16).copy_(f)
+                buf[off : off + f.numel() * 2].view(dt).copy_(f)
 
-            put(lay.f_rkv, _f16_view(src, lay.w_rkv, 3 * C, C))
-            l1 = _f16_view(src, lay.w_lora1, SR, C)
-            l2 = _f16_view(src, lay.w_lora2, C, SR)
+            put(lay.f_rkv, _f16_view(src, lay.w_rkv, 3 * C, C, dt))
+            l1 = _f16_view(src, lay.w_lora1, SR, C, dt)
+            l2 = _f16_view(src, lay.w_lora2, C, SR, dt)
             r0 = 0
             for g in range(4):
                 put(lay.f_l1[g], l1[r0 : r0 + R[g]])
                 put(lay.f_l2[g], l2[:, r0 : r0 + R[g]])
                 r0 += R[g]
-            put(lay.f_o, _f16_view(src, lay.w_o, C, C))
-            put(lay.f_fk, _f16_view(src, lay.w_fk, F_, C))
-            put(lay.f_fv, _f16_view(src, lay.w_fv, C, F_))
+            put(lay.f_o, _f16_view(src, lay.w_o, C, C, dt))
+            put(lay.f_fk, _f16_view(src, lay.w_fk, F_, C, dt))
+            put(lay.f_fv, _f16_view(src, lay.w_fv, C, F_, dt))
         head_frag = to_fragments(head).contiguous()
     layers_q = head_q = None
     if int8:
@@ -306,7 +310,7 @@ def pack_device_weights(w: RWKV7Weight, fragments: bool = True, int8: bool = Fal
         ln_out=ln_out.data_ptr(),
         layers_frag=layers_frag.data_ptr() if layers_frag is not None else None,
         head_frag=head_frag.data_ptr() if head_frag is not None else None,
-        flags=_lib.MODEL_INT8_DECODE if int8 else 0,
+        flags=(_lib.MODEL_INT8_DECODE if int8 else 0) | (_lib.MODEL_BF16 if dt == torch.bfloat16 else 0),
         layers_q=layers_q.data_ptr() if layers_q is not None else None,
         head_q=head_q.data_ptr() if head_q is not None else None,
     )

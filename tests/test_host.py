@@ -295,8 +295,7 @@ def test_sample_logits_rejects_cpu_tensors():
 
 
 def test_make_rwkv7_backends():
-    with pytest.raises(ValueError):
-        make_rwkv7(torch.device("cuda"), backend="bf16")
+    assert make_rwkv7(torch.device("cuda"), backend="bf16", use_graph=False).__name__ == "RWKV7HIPBF16"
     with pytest.raises(ValueError):
         make_rwkv7(torch.device("cuda"), backend="torch")
     with pytest.raises(ValueError):
