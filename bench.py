@@ -25,7 +25,8 @@
   ``prefill_T128_hbm_frac``, ``prefill_T128_mfma_frac`` (and the same for
   T8; prefill through HIP-graph replay for T <= 64), batch-1 decode on int8
   weights (``decode_int8``: the same persistent kernel streaming per-row int8
-  matrices, its bytes counted at one byte per int8 weight), the int8 weight-only GEMV
+  matrices, its bytes counted at one byte per int8 weight), batch-1 decode of
+  the bfloat16 model (``decode_bf16``), the int8 weight-only GEMV
   (``rwkv7_gemv_i8``) against the f16 GEMV on the head matrix (65536 x 1024;
   average launch time over 100 launches and fraction of HBM peak for each),
   the roofline of the whole step as the caller sees it, and the CPU baseline: the oracle's pure-torch fp32
@@ -562,6 +563,25 @@ def main() -> None:
         }
         log(f"decode B=1 int8 weights: {us_i8:.2f} us/token")
         del model8, S8
+        # ---- decode B=1 of the bfloat16 model (same seed, bf16 weights) ----
+        from rwkv_tl_amd import RWKV7HIPBF16
+
+        sdb = make_random_state_dict("0.4b", seed=0, dtype=torch.bfloat16)
+        wb = RWKV7Weight.from_state_dict(sdb, device=dev, dtype=torch.bfloat16)
+        del sdb
+        modelb = RWKV7HIPBF16(wb, is_torch_compile=False)
+        Sb = modelb.new_state()
+        logitsb = torch.empty(1, V, dtype=torch.bfloat16, device=dev)
+        for i in range(Wm):
+            modelb.decode_into(toks[i], Sb, logitsb)
+        us_bf = time_cuda(lambda it=iter(range(K)): modelb.decode_into(toks[next(it) % (K + Wm)], Sb, logitsb),
+                          min(K, 128)) * 1e3
+        out["decode_bf16"] = {
+            "us_per_token": round(us_bf, 2),
+            "hbm_frac": round(step_bytes / (us_bf * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        }
+        log(f"decode B=1 bf16 model: {us_bf:.2f} us/token")
+        del modelb, Sb, wb
         # ---- int8 weight-only GEMV vs the f16 GEMV on the head shape ----
         # (direct C-ABI calls into a preallocated output, so the host wrapper's
         # checks and allocation stay out of the timed launches)
