@@ -26,9 +26,10 @@
   T8; prefill through HIP-graph replay for T <= 64), batch-1 decode on int8
   weights (``decode_int8``: the same persistent kernel streaming per-row int8
   matrices, its bytes counted at one byte per int8 weight), batch-1 decode of
-  the bfloat16 model (``decode_bf16``), the int8 weight-only GEMV
-  (``rwkv7_gemv_i8``) against the f16 GEMV on the head matrix (65536 x 1024;
-  average launch time over 100 launches and fraction of HBM peak for each),
+  the bfloat16 model (``decode_bf16``), the int8 and any4 weight-only GEMVs
+  (``rwkv7_gemv_i8``, ``rwkv7_gemv_any4``) against the f16 GEMV on the head
+  matrix (65536 x 1024; average launch time over 100 launches and fraction of
+  HBM peak for each),
   the roofline of the whole step as the caller sees it, and the CPU baseline: the oracle's pure-torch fp32
   model (a port of the reference's ``demo/rwkv7_torch.py``) timed on this
   host's cores on a bounded sample of the same decode workload.
@@ -600,15 +601,23 @@ def main() -> None:
         LB.check(g16(), "rwkv7_gemv_f16")
         us8 = time_cuda(g8, 100) * 1e3
         us16 = time_cuda(g16, 100) * 1e3
+        c4, l4 = KO.quantize_any4(Wh)
+        g4 = lambda: lib.rwkv7_gemv_any4(xh.data_ptr(), c4.data_ptr(), c4.stride(0), l4.data_ptr(), yh.data_ptr(),
+                                         Nh, w.C, sth)
+        LB.check(g4(), "rwkv7_gemv_any4")
+        us4 = time_cuda(g4, 100) * 1e3
         b8, b16h = Nh * w.C + 8 * Nh + 4 * w.C, 2 * Nh * w.C + 4 * Nh + 4 * w.C
+        b4 = Nh * w.C // 2 + 32 * Nh + 4 * Nh + 4 * w.C
         out["gemv_i8_head"] = {
             "shape": [Nh, w.C],
             "i8_us": round(us8, 2),
             "i8_hbm_frac": round(b8 / (us8 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "f16_us": round(us16, 2),
             "f16_hbm_frac": round(b16h / (us16 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "any4_us": round(us4, 2),
+            "any4_hbm_frac": round(b4 / (us4 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         }
-        log(f"gemv head {Nh}x{w.C}: int8 {us8:.2f} us, f16 {us16:.2f} us")
+        log(f"gemv head {Nh}x{w.C}: int8 {us8:.2f} us, any4 {us4:.2f} us, f16 {us16:.2f} us")
         # ---- prefill ----
         pre = {}
         for T in (8, 128):

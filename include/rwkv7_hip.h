@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define RWKV7_ABI_VERSION 7
+#define RWKV7_ABI_VERSION 8
 #define RWKV7_HEAD_SIZE 64
 
 enum {
@@ -280,6 +280,16 @@ int rwkv7_gemv_f16(const float *x, const void *W, int64_t ldw, float *y,
  * hand-written GEMV (TODO.md:58-63), which has no kernel there yet. */
 int rwkv7_gemv_i8(const float *x, const void *Q, int64_t ldq, const float *scale,
                   float *y, int32_t N, int32_t K, void *stream);
+
+/* y[n] = sum_k x[k] lut[n][code(n, k)]: any4 weights -- per row a table lut
+ * f16 [N, 16] and one 4-bit code per weight, codes u8 [N, K/2] (row stride
+ * ldc bytes, ldc % 8 == 0, codes 8-byte and x 16-byte aligned; byte j holds
+ * column 2j in its low nibble and 2j+1 in its high nibble), x and y f32.
+ * 16 <= K <= 8192, K % 16 == 0. The "any4" weight-only format the reference
+ * names beside int8 for its quantised GEMV (TODO.md:58-63); it has no kernel
+ * there. */
+int rwkv7_gemv_any4(const float *x, const void *codes, int64_t ldc, const void *lut,
+                    float *y, int32_t N, int32_t K, void *stream);
 
 /* Y = epi(A W^T): A f16 [M, K] (row stride lda), W f16 [N, K] (ldw), fp32
  * accumulation. epi: 0 store f32, 1 store f16, 2 relu^2 store f16,

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the HIP library)
 
 LIB_NAME = "librwkv7_hip.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # rwkv7_model.flags
 MODEL_MULTI_LAUNCH_DECODE = 1
@@ -50,6 +50,7 @@ SYMBOLS = (
     "rwkv7_lerp",
     "rwkv7_gemv_f16",
     "rwkv7_gemv_i8",
+    "rwkv7_gemv_any4",
     "rwkv7_gemm_f16",
     "rwkv7_w_gate",
     "rwkv7_v_gate",
@@ -170,6 +171,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "rwkv7_lerp": (ctypes.c_int, [vp, vp, vp, i32, vp, vp, i32, vp]),
         "rwkv7_gemv_f16": (ctypes.c_int, [vp, vp, i64, vp, i32, i32, vp]),
         "rwkv7_gemv_i8": (ctypes.c_int, [vp, vp, i64, vp, vp, i32, i32, vp]),
+        "rwkv7_gemv_any4": (ctypes.c_int, [vp, vp, i64, vp, vp, i32, i32, vp]),
         "rwkv7_gemm_f16": (ctypes.c_int, [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp]),
         "rwkv7_w_gate": (ctypes.c_int, [vp, vp, vp, i32, vp]),
         "rwkv7_v_gate": (ctypes.c_int, [vp, vp, vp, vp, vp, i32, vp]),

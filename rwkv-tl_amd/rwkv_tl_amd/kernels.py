@@ -12,6 +12,9 @@ dtype). There is no CPU branch: the reference's in-function torch fallbacks
   (``lerp.py:140-198``), ``fused_lerp6_rkv_copy`` (``lerp.py:200-219``).
 * ``layer_norm`` (``weight.py:14-15``), ``gemv`` and ``gemm`` (the projection
   GEMMs of ``gemm.py:215-305``), ``fused_rkv_gemm`` (``gemm.py:215-262``).
+* Weight-only quantised GEMVs (the reference's plan, ``TODO.md:58-63``):
+  ``quantize_i8`` / ``gemv_i8`` (per-row int8) and ``quantize_any4`` /
+  ``gemv_any4`` (per-row 16-entry tables, 4-bit codes).
 * The time-mix stage operators, f16 in and out: ``fused_w_gate``,
   ``fused_v_gate``, ``fused_a_kk_k`` (``gates.py:287-313``), ``fused_gates``
   (``gates.py:315-357``), ``fused_rank_gemv`` (``gates.py:254-285``),
@@ -250,6 +253,31 @@ def gemv_i8(x: Tensor, q: Tensor, scale: Tensor) -> Tensor:
     rc = lib.rwkv7_gemv_i8(x.data_ptr(), q.data_ptr(), Kd, scale.data_ptr(), y.data_ptr(), N, Kd,
                            _lib.stream_handle())
     _lib.check(rc, "rwkv7_gemv_i8")
+    return y
+
+
+def quantize_any4(W: Tensor) -> tuple[Tensor, Tensor]:
+    """any4 weights for ``gemv_any4``: codes uint8 [N, K/2], lut f16 [N, 16]
+    (``weight.quantize_rows_any4``)."""
+    _need(W.dim() == 2 and W.is_floating_point(), "W must be a floating [N, K] matrix")
+    from .weight import quantize_rows_any4
+
+    return quantize_rows_any4(W)
+
+
+def gemv_any4(x: Tensor, codes: Tensor, lut: Tensor) -> Tensor:
+    """y = W x for any4 weights (``rwkv7_gemv_any4``): x f32 [K], codes uint8
+    [N, K/2] (two 4-bit codes per byte), lut f16 [N, 16]; y f32 [N]."""
+    _dev(x, codes, lut)
+    _need(codes.dtype == torch.uint8 and codes.dim() == 2, "codes must be uint8 [N, K/2]")
+    N, K = codes.shape[0], 2 * codes.shape[1]
+    _need(lut.dtype == torch.float16 and lut.shape == (N, 16), f"lut must be f16 [{N}, 16]")
+    _need(x.dtype == torch.float32 and x.shape == (K,), f"x must be f32 [{K}]")
+    y = torch.empty(N, dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    rc = lib.rwkv7_gemv_any4(x.data_ptr(), codes.data_ptr(), codes.stride(0), lut.data_ptr(), y.data_ptr(), N, K,
+                             _lib.stream_handle())
+    _lib.check(rc, "rwkv7_gemv_any4")
     return y
 
 

@@ -166,6 +166,54 @@ def quantize_rows_i8(W: Tensor) -> tuple[Tensor, Tensor]:
     return q.to(torch.int8).contiguous(), scale.contiguous()
 
 
+def quantize_rows_any4(W: Tensor, iters: int = 12) -> tuple[Tensor, Tensor]:
+    """any4: per row a table of 16 values and one 4-bit code per weight
+    (the learned 4-bit format, "any4", that the reference's quantisation plan
+    names beside int8). The table is a per-row k-means of the row's values:
+    Lloyd iterations (assign every weight to its nearest centroid, move each
+    centroid to the mean of its weights; a cluster that empties keeps its
+    centroid) from the 16 evenly spaced levels of [min, max], so the result is
+    never worse than that uniform 4-bit grid (a Lloyd step cannot increase the
+    squared error). The table is rounded to f16 and every weight then takes
+    the code of its nearest f16 entry. Returns ``codes`` uint8 [N, K/2] (column 2j in the
+    low nibble of byte j, 2j+1 in the high nibble) and ``lut`` f16 [N, 16],
+    ascending. A weight-format step done once at load (torch on W's device;
+    the cluster sums are not bit-reproducible across devices, which only moves
+    centroids by float rounding)."""
+    w = W.float()
+    N, K = w.shape
+    if K % 2 or K < 16:
+        raise ValueError("any4 packs two codes per byte and needs K >= 16 (even)")
+    lo, hi = w.amin(dim=1, keepdim=True), w.amax(dim=1, keepdim=True)
+    cent = (lo + (hi - lo) * (torch.arange(16, device=w.device, dtype=torch.float32) / 15)).contiguous()
+    ones = torch.ones_like(w)
+    for _ in range(iters):
+        mid = ((cent[:, 1:] + cent[:, :-1]) * 0.5).contiguous()
+        code = torch.searchsorted(mid, w)
+        sums = torch.zeros_like(cent).scatter_add_(1, code, w)
+        cnt = torch.zeros_like(cent).scatter_add_(1, code, ones)
+        # an empty cluster moves to one of the row's worst-represented weights
+        # (the e-th empty one to the e-th largest error), which can only lower
+        # the squared error at the next assignment
+        empty = cnt == 0
+        err = (w - cent.gather(1, code)).abs()
+        worst = w.gather(1, err.topk(16, dim=1).indices)
+        rank = (empty.long().cumsum(1) - 1).clamp(min=0)
+        cent = torch.where(empty, worst.gather(1, rank), sums / cnt.clamp(min=1.0)).sort(dim=1).values
+    lut = cent.to(torch.float16).contiguous()
+    lf = lut.float()
+    code = torch.searchsorted(((lf[:, 1:] + lf[:, :-1]) * 0.5).contiguous(), w).to(torch.uint8)
+    codes = (code[:, 0::2] | (code[:, 1::2] << 4)).contiguous()
+    return codes, lut
+
+
+def dequantize_rows_any4(codes: Tensor, lut: Tensor) -> Tensor:
+    """The f32 matrix an any4 (codes, lut) pair stands for."""
+    lo, hi = (codes & 15).long(), (codes >> 4).long()
+    idx = torch.stack([lo, hi], dim=2).reshape(codes.shape[0], -1)
+    return lut.float().gather(1, idx)
+
+
 def int8_matrices(w: "RWKV7Weight") -> list[dict[str, Tensor]]:
     """Per layer, the f16 matrices the int8 decode streams, as [out, in] rows
     in the int8 arena's order: ``rkv`` (receptance, key, value rows, then the
