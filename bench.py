@@ -596,7 +596,7 @@ def main() -> None:
         yh = torch.empty(Nh, dtype=torch.float32, device=dev)
         lib, sth = LB.load(), LB.stream_handle()
         g8 = lambda: lib.rwkv7_gemv_i8(xh.data_ptr(), qh.data_ptr(), w.C, sh.data_ptr(), yh.data_ptr(), Nh, w.C, sth)
-        g16 = lambda: lib.rwkv7_gemv_f16(xh.data_ptr(), Wh.data_ptr(), w.C, yh.data_ptr(), Nh, w.C, sth)
+        g16 = lambda: lib.rwkv7_gemv_f16(xh.data_ptr(), Wh.data_ptr(), w.C, yh.data_ptr(), Nh, w.C, 0, sth)
         LB.check(g8(), "rwkv7_gemv_i8")
         LB.check(g16(), "rwkv7_gemv_f16")
         us8 = time_cuda(g8, 100) * 1e3

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define RWKV7_ABI_VERSION 8
+#define RWKV7_ABI_VERSION 9
 #define RWKV7_HEAD_SIZE 64
 
 enum {
@@ -221,6 +221,13 @@ int rwkv7_prefill(const rwkv7_model *model, const rwkv7_state *state,
 
 /* ---- operator level ---------------------------------------------------- */
 
+/* Every operator below that takes 16-bit operands takes them in one format
+ * per call: IEEE half, or bfloat16 when its bf16 argument is nonzero -- the
+ * reference's two kernel namespaces, rwkv_tl.kernels.fp16 and .bf16
+ * (src/rwkv_tl/kernels/fp16.py:13-30, bf16.py:13-30), which bind the same
+ * kernels to float16 and bfloat16. "f16" in the comments below means that
+ * 16-bit format; arithmetic is fp32 in both. */
+
 /* DPLR (wkv7) recurrence over B sequences of T tokens and H heads:
  *   S[h] <- S[h] diag(w_t) + (S[h] a_t) b_t^T + v_t k_t^T ;  y_t = S[h] r_t
  * S f32 [B, H, 64, 64] (in place); r, k, v, a, b f16 [B, T, H, 64];
@@ -229,7 +236,7 @@ int rwkv7_prefill(const rwkv7_model *model, const rwkv7_state *state,
  * (src/rwkv_tl/kernels/dplr.py:256-285), where A = a, B = b. */
 int rwkv7_wkv7(float *S, const void *r, const void *w, int32_t w_is_f32,
                const void *k, const void *v, const void *a, const void *b,
-               void *y, int32_t B, int32_t T, int32_t H, void *stream);
+               void *y, int32_t B, int32_t T, int32_t H, int32_t bf16, void *stream);
 
 /* The same recurrence with every operand f32 (S, r, w, k, v, a, b, y), for
  * training. When hist != NULL it receives the state entering each step, f32
@@ -257,7 +264,8 @@ int rwkv7_wkv7_backward(const float *hist, const float *S_T, const float *r,
  * (x_is_f32), weight/bias f32 [C], y f32 [M, C]. Stands in for LNWeight
  * (src/rwkv_tl/weight.py:14-15). */
 int rwkv7_layernorm(const void *x, int32_t x_is_f32, const float *weight,
-                    const float *bias, float *y, int32_t M, int32_t C, void *stream);
+                    const float *bias, float *y, int32_t M, int32_t C, int32_t bf16,
+                    void *stream);
 
 /* Token-shift lerps x + mu_i (prev - x), i < n_mix (1 or 6), all f16 [C]
  * except mu f32 [n_mix, C]; out f16 [n_mix, C]. If x_copy != NULL it receives
@@ -265,13 +273,13 @@ int rwkv7_layernorm(const void *x, int32_t x_is_f32, const float *weight,
  * fused_lerp6, fused_lerp6_copy and fused_lerp1_copy
  * (src/rwkv_tl/kernels/lerp.py:140-198). */
 int rwkv7_lerp(const void *x, const void *prev, const float *mu, int32_t n_mix,
-               void *out, void *x_copy, int32_t C, void *stream);
+               void *out, void *x_copy, int32_t C, int32_t bf16, void *stream);
 
 /* y = x W^T for one vector: x f32 [K], W f16 [N, K] (row stride ldw elements),
  * y f32 [N]. K % 256 == 0. Stands in for the decode projections
  * (demo/_rwkv7_base.py:87,206,290; kernels/gemm.py:215-262 at T=1). */
 int rwkv7_gemv_f16(const float *x, const void *W, int64_t ldw, float *y,
-                   int32_t N, int32_t K, void *stream);
+                   int32_t N, int32_t K, int32_t bf16, void *stream);
 
 /* y[n] = scale[n] * sum_k x[k] Q[n, k]: Q int8 [N, K] (row stride ldq bytes,
  * ldq % 16 == 0, Q and x 16-byte aligned), scale f32 [N], x and y f32.
@@ -297,23 +305,23 @@ int rwkv7_gemv_any4(const float *x, const void *codes, int64_t ldc, const void *
  * fused_rkv_gemm / ffn_h / ffn_v / out_mm (src/rwkv_tl/kernels/gemm.py:215-305). */
 int rwkv7_gemm_f16(const void *A, int64_t lda, const void *W, int64_t ldw,
                    void *Y, int64_t ldy, int32_t M, int32_t N, int32_t K,
-                   int32_t epi, void *stream);
+                   int32_t epi, int32_t bf16, void *stream);
 
 /* ---- time-mix stage operators (f16 in and out, fp32 arithmetic) --------- */
 
 /* out[i] = exp(-sigmoid(w0[i] + x[i]) / sqrt(e)), i < C.
  * Replaces fused_w_gate (src/rwkv_tl/kernels/gates.py:287-291). */
-int rwkv7_w_gate(const void *x, const void *w0, void *out, int32_t C, void *stream);
+int rwkv7_w_gate(const void *x, const void *w0, void *out, int32_t C, int32_t bf16, void *stream);
 
 /* out = v + sigmoid(v0 + v12) * (v_first - v), [C].
  * Replaces fused_v_gate (gates.py:293-297). */
 int rwkv7_v_gate(const void *v, const void *v_first, const void *v0, const void *v12, void *out,
-                 int32_t C, void *stream);
+                 int32_t C, int32_t bf16, void *stream);
 
 /* a = sigmoid(a0 + a_x), kk = k * k_k, k' = k + k_a * (k * a - k), [C].
  * Replaces fused_a_kk_k (gates.py:299-313). */
 int rwkv7_a_kk_k(const void *a0, const void *a_x, const void *k, const void *k_k, const void *k_a,
-                 void *a_out, void *kk_out, void *k_out, int32_t C, void *stream);
+                 void *a_out, void *kk_out, void *k_out, int32_t C, int32_t bf16, void *stream);
 
 /* Operands of rwkv7_gates, all f16: rank inputs vr [Rv], wr [Rw], ar [Ra],
  * gr [Rg] (first-step results, before activation); second-step matrices
@@ -331,25 +339,27 @@ typedef struct rwkv7_gates_io {
  * kk = k k_k, k' = k + k_a (k a - k), g = g2t sigmoid(gr).
  * Replaces fused_gates (gates.py:125-213,315-357). */
 int rwkv7_gates(const rwkv7_gates_io *io, int32_t rank_v, int32_t rank_w, int32_t rank_a, int32_t rank_g,
-                int32_t C, void *stream);
+                int32_t C, int32_t bf16, void *stream);
 
 /* Packed LoRA first steps: out = [v1t; w1t; a1t; g1t] @ (xv | xw | xa | xg),
  * W [Rv+Rw+Ra+Rg, C], inputs [C], out [Rv+Rw+Ra+Rg]; C % 8 == 0.
  * Replaces fused_rank_gemv (gates.py:215-285). */
 int rwkv7_rank_gemv(const void *xv, const void *xw, const void *xa, const void *xg, const void *W, void *out,
-                    int32_t rank_v, int32_t rank_w, int32_t rank_a, int32_t rank_g, int32_t C, void *stream);
+                    int32_t rank_v, int32_t rank_w, int32_t rank_a, int32_t rank_g, int32_t C, int32_t bf16,
+                    void *stream);
 
 /* Per head h < H over its 64 channels: kk_norm = kk / max(||kk||, 1e-12),
  * b = -kk_norm * a; all [H, 64].
  * Replaces fused_l2norm_neg_kk_a (src/rwkv_tl/kernels/dplr.py:45-71,229-235). */
-int rwkv7_l2norm_neg_kk_a(const void *kk, const void *a, void *kk_norm, void *b, int32_t H, void *stream);
+int rwkv7_l2norm_neg_kk_a(const void *kk, const void *a, void *kk_norm, void *b, int32_t H, int32_t bf16,
+                          void *stream);
 
 /* Per head: GroupNorm of y (biased variance, eps 64e-5) * ln_w + ln_b, plus
  * (sum over the head of r * k * r_k) * v; y, r, k, v, r_k [H, 64], ln_w,
  * ln_b and out [H * 64].
  * Replaces fused_gn_rkrk (dplr.py:73-124,237-254). */
 int rwkv7_gn_rkrk(const void *y, const void *r, const void *k, const void *v, const void *r_k,
-                  const void *ln_w, const void *ln_b, void *out, int32_t H, void *stream);
+                  const void *ln_w, const void *ln_b, void *out, int32_t H, int32_t bf16, void *stream);
 
 /* ---- sampling ---------------------------------------------------------- */
 

@@ -561,10 +561,22 @@ int rwkv7_prefill(const rwkv7_model *model, const rwkv7_state *state, const int6
 }
 
 int rwkv7_wkv7(float *S, const void *r, const void *w, int32_t w_is_f32, const void *k, const void *v,
-               const void *a, const void *b, void *y, int32_t B, int32_t T, int32_t H, void *stream) {
+               const void *a, const void *b, void *y, int32_t B, int32_t T, int32_t H, int32_t bf16,
+               void *stream) {
   if (!S || !r || !w || !k || !v || !a || !b || !y) return RWKV7_EINVAL;
   if (B < 1 || T < 1 || H < 1) return RWKV7_ESHAPE;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (bf16) {
+    auto bp = [](const void *q) { return static_cast<const bf16_t *>(q); };
+    bf16_t *yb = static_cast<bf16_t *>(y);
+    if (w_is_f32) {
+      ScanArgs<bf16_t, float, bf16_t> p = {S, bp(r), bp(k), bp(v), bp(a), bp(b), static_cast<const float *>(w),
+                                           yb, B, T, H};
+      return launch_wkv7_scan(p, st);
+    }
+    ScanArgs<bf16_t, bf16_t, bf16_t> p = {S, bp(r), bp(k), bp(v), bp(a), bp(b), bp(w), yb, B, T, H};
+    return launch_wkv7_scan(p, st);
+  }
   const uint16_t *r16 = static_cast<const uint16_t *>(r), *k16 = static_cast<const uint16_t *>(k),
                  *v16 = static_cast<const uint16_t *>(v), *a16 = static_cast<const uint16_t *>(a),
                  *b16 = static_cast<const uint16_t *>(b);
@@ -597,22 +609,23 @@ int rwkv7_wkv7_backward(const float *hist, const float *S_T, const float *r, con
 }
 
 int rwkv7_layernorm(const void *x, int32_t x_is_f32, const float *weight, const float *bias, float *y, int32_t M,
-                    int32_t C, void *stream) {
+                    int32_t C, int32_t bf16, void *stream) {
   if (!x || !weight || !bias || !y) return RWKV7_EINVAL;
   if (M < 1) return RWKV7_ESHAPE;
-  return launch_ln_rows(x, x_is_f32, weight, bias, y, 1, M, C, 1, 0, 0, static_cast<hipStream_t>(stream));
+  return launch_ln_rows(x, x_is_f32, weight, bias, y, 1, M, C, 1, 0, bf16 ? 1 : 0, static_cast<hipStream_t>(stream));
 }
 
 int rwkv7_lerp(const void *x, const void *prev, const float *mu, int32_t n_mix, void *out, void *x_copy, int32_t C,
-               void *stream) {
+               int32_t bf16, void *stream) {
   if (!x || !prev || !mu || !out) return RWKV7_EINVAL;
   if ((n_mix != 1 && n_mix != 6) || C < 1) return RWKV7_ESHAPE;
   return launch_lerp(static_cast<const uint16_t *>(x), static_cast<const uint16_t *>(prev), mu, n_mix,
-                     static_cast<uint16_t *>(out), static_cast<uint16_t *>(x_copy), C,
+                     static_cast<uint16_t *>(out), static_cast<uint16_t *>(x_copy), C, bf16 ? 1 : 0,
                      static_cast<hipStream_t>(stream));
 }
 
-int rwkv7_gemv_f16(const float *x, const void *W, int64_t ldw, float *y, int32_t N, int32_t K, void *stream) {
+int rwkv7_gemv_f16(const float *x, const void *W, int64_t ldw, float *y, int32_t N, int32_t K, int32_t bf16,
+                   void *stream) {
   if (!x || !W || !y) return RWKV7_EINVAL;
   if (N < 1 || K < 256 || K % 256 || K > 8192 || ldw < K || ldw % 8) return RWKV7_ESHAPE;
   GemvArgs g = {};
@@ -622,15 +635,17 @@ int rwkv7_gemv_f16(const float *x, const void *W, int64_t ldw, float *y, int32_t
   g.K = K;
   g.x = x;
   g.y = y;
+  g.bf = bf16 ? 1 : 0;
   return launch_gemv<PRO_F32, EPI_F32>(g, static_cast<hipStream_t>(stream));
 }
 
 int rwkv7_gemm_f16(const void *A, int64_t lda, const void *W, int64_t ldw, void *Y, int64_t ldy, int32_t M, int32_t N,
-                   int32_t K, int32_t epi, void *stream) {
+                   int32_t K, int32_t epi, int32_t bf16, void *stream) {
   if (!A || !W || !Y) return RWKV7_EINVAL;
   if (epi < 0 || epi > 3) return RWKV7_EINVAL;
   if (M < 1 || N < 1 || K < 8 || lda < K || ldw < K || ldy < N) return RWKV7_ESHAPE;
   GemmProb p = {static_cast<const uint16_t *>(A), static_cast<const uint16_t *>(W), Y, lda, ldw, ldy, N, K, epi};
+  p.bf = bf16 ? 1 : 0;
   return launch_gemm_group(&p, 1, M, static_cast<hipStream_t>(stream), nullptr, nullptr);
 }
 
@@ -638,29 +653,29 @@ static const uint16_t *h16(const void *p) { return static_cast<const uint16_t *>
 static uint16_t *h16(void *p) { return static_cast<uint16_t *>(p); }
 static hipStream_t hs(void *s) { return static_cast<hipStream_t>(s); }
 
-int rwkv7_w_gate(const void *x, const void *w0, void *out, int32_t C, void *stream) {
+int rwkv7_w_gate(const void *x, const void *w0, void *out, int32_t C, int32_t bf16, void *stream) {
   if (!x || !w0 || !out) return RWKV7_EINVAL;
   if (C < 1) return RWKV7_ESHAPE;
-  return launch_w_gate(h16(x), h16(w0), h16(out), C, hs(stream));
+  return launch_w_gate(h16(x), h16(w0), h16(out), C, bf16 ? 1 : 0, hs(stream));
 }
 
 int rwkv7_v_gate(const void *v, const void *v_first, const void *v0, const void *v12, void *out, int32_t C,
-                 void *stream) {
+                 int32_t bf16, void *stream) {
   if (!v || !v_first || !v0 || !v12 || !out) return RWKV7_EINVAL;
   if (C < 1) return RWKV7_ESHAPE;
-  return launch_v_gate(h16(v), h16(v_first), h16(v0), h16(v12), h16(out), C, hs(stream));
+  return launch_v_gate(h16(v), h16(v_first), h16(v0), h16(v12), h16(out), C, bf16 ? 1 : 0, hs(stream));
 }
 
 int rwkv7_a_kk_k(const void *a0, const void *a_x, const void *k, const void *k_k, const void *k_a, void *a_out,
-                 void *kk_out, void *k_out, int32_t C, void *stream) {
+                 void *kk_out, void *k_out, int32_t C, int32_t bf16, void *stream) {
   if (!a0 || !a_x || !k || !k_k || !k_a || !a_out || !kk_out || !k_out) return RWKV7_EINVAL;
   if (C < 1) return RWKV7_ESHAPE;
   return launch_a_kk_k(h16(a0), h16(a_x), h16(k), h16(k_k), h16(k_a), h16(a_out), h16(kk_out), h16(k_out), C,
-                       hs(stream));
+                       bf16 ? 1 : 0, hs(stream));
 }
 
 int rwkv7_gates(const rwkv7_gates_io *io, int32_t rank_v, int32_t rank_w, int32_t rank_a, int32_t rank_g, int32_t C,
-                void *stream) {
+                int32_t bf16, void *stream) {
   if (!io) return RWKV7_EINVAL;
   const void *ins[16] = {io->vr, io->wr, io->ar, io->gr, io->v2t, io->w2t, io->a2t, io->g2t,
                          io->v,  io->v_first, io->k, io->v0, io->w0, io->a0, io->k_k, io->k_a};
@@ -670,28 +685,31 @@ int rwkv7_gates(const rwkv7_gates_io *io, int32_t rank_v, int32_t rank_w, int32_
   for (const void *p : outs)
     if (!p) return RWKV7_EINVAL;
   if (C < 1 || rank_v < 1 || rank_w < 1 || rank_a < 1 || rank_g < 1) return RWKV7_ESHAPE;
-  return launch_gates(*io, rank_v, rank_w, rank_a, rank_g, C, hs(stream));
+  return launch_gates(*io, rank_v, rank_w, rank_a, rank_g, C, bf16 ? 1 : 0, hs(stream));
 }
 
 int rwkv7_rank_gemv(const void *xv, const void *xw, const void *xa, const void *xg, const void *W, void *out,
-                    int32_t rank_v, int32_t rank_w, int32_t rank_a, int32_t rank_g, int32_t C, void *stream) {
+                    int32_t rank_v, int32_t rank_w, int32_t rank_a, int32_t rank_g, int32_t C, int32_t bf16,
+                    void *stream) {
   if (!xv || !xw || !xa || !xg || !W || !out) return RWKV7_EINVAL;
   if (C < 8 || C % 8 || rank_v < 1 || rank_w < 1 || rank_a < 1 || rank_g < 1) return RWKV7_ESHAPE;
   return launch_rank_gemv(h16(xv), h16(xw), h16(xa), h16(xg), h16(W), h16(out), rank_v, rank_w, rank_a, rank_g, C,
-                          hs(stream));
+                          bf16 ? 1 : 0, hs(stream));
 }
 
-int rwkv7_l2norm_neg_kk_a(const void *kk, const void *a, void *kk_norm, void *b, int32_t H, void *stream) {
+int rwkv7_l2norm_neg_kk_a(const void *kk, const void *a, void *kk_norm, void *b, int32_t H, int32_t bf16,
+                          void *stream) {
   if (!kk || !a || !kk_norm || !b) return RWKV7_EINVAL;
   if (H < 1) return RWKV7_ESHAPE;
-  return launch_l2norm(h16(kk), h16(a), h16(kk_norm), h16(b), H, hs(stream));
+  return launch_l2norm(h16(kk), h16(a), h16(kk_norm), h16(b), H, bf16 ? 1 : 0, hs(stream));
 }
 
 int rwkv7_gn_rkrk(const void *y, const void *r, const void *k, const void *v, const void *r_k, const void *ln_w,
-                  const void *ln_b, void *out, int32_t H, void *stream) {
+                  const void *ln_b, void *out, int32_t H, int32_t bf16, void *stream) {
   if (!y || !r || !k || !v || !r_k || !ln_w || !ln_b || !out) return RWKV7_EINVAL;
   if (H < 1) return RWKV7_ESHAPE;
-  return launch_gn_rkrk(h16(y), h16(r), h16(k), h16(v), h16(r_k), h16(ln_w), h16(ln_b), h16(out), H, hs(stream));
+  return launch_gn_rkrk(h16(y), h16(r), h16(k), h16(v), h16(r_k), h16(ln_w), h16(ln_b), h16(out), H, bf16 ? 1 : 0,
+                        hs(stream));
 }
 
 }  // extern "C"

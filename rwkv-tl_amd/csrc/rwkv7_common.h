@@ -134,9 +134,19 @@ struct F16T {
   static constexpr uint16_t kNaN = BF ? 0x7FC0u : 0x7E00u;
 };
 
+// A bfloat16 element as a distinct type, for templates that take the element
+// type (the operator-level wkv7 scan).
+struct bf16_t {
+  uint16_t bits;
+};
+
 // The same chosen at run time (small elementwise kernels).
 RWKV7_DEV float u16_to_f(uint16_t u, int bf) { return bf ? b2f(u) : h2f(u); }
 RWKV7_DEV uint16_t f_to_u16(float f, int bf) { return bf ? f2b(f) : f2h(f); }
+RWKV7_DEV void u16x8_to_f(const uint4 &u, float f[8], int bf) {
+  if (bf) F16T<true>::to_f8(u, f);
+  else F16T<false>::to_f8(u, f);
+}
 
 // 16x16x32 MFMA on 16-bit operands of format F16T<BF> (8 per lane, any
 // 16-byte type), fp32 accumulation.

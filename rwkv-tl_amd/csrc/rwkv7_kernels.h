@@ -121,7 +121,7 @@ int launch_embed(const int64_t *tok, const uint16_t *emb, float *x0, int M, int 
 int launch_ln_rows(const void *x, int x_f32, const float *w, const float *b, void *out, int out_f32,
                    int rows, int C, int stride, int offset, int bf, hipStream_t st);
 int launch_lerp(const uint16_t *x, const uint16_t *prev, const float *mu, int n_mix, uint16_t *out,
-                uint16_t *x_copy, int C, hipStream_t st);
+                uint16_t *x_copy, int C, int bf, hipStream_t st);
 int launch_store_f16(const float *src, uint16_t *dst, int n, int bf, hipStream_t st);
 
 enum { GEPI_F32 = 0, GEPI_F16 = 1, GEPI_RELUSQ = 2, GEPI_ADD_F32 = 3, GEPI_TANH_F16 = 4, GEPI_SIGM_F16 = 5 };
@@ -145,18 +145,21 @@ constexpr int kGemmCounters = 1024;
 int64_t gemm_ws_bytes(int M, int cus);
 int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, float *part, unsigned *ctr);
 
-// Operator-level time-mix stages (ops.hip).
-int launch_w_gate(const uint16_t *x, const uint16_t *w0, uint16_t *out, int C, hipStream_t st);
+// Operator-level time-mix stages (ops.hip); bf: the 16-bit operands are
+// bfloat16 (else IEEE half).
+int launch_w_gate(const uint16_t *x, const uint16_t *w0, uint16_t *out, int C, int bf, hipStream_t st);
 int launch_v_gate(const uint16_t *v, const uint16_t *vf, const uint16_t *v0, const uint16_t *v12, uint16_t *out,
-                  int C, hipStream_t st);
+                  int C, int bf, hipStream_t st);
 int launch_a_kk_k(const uint16_t *a0, const uint16_t *ax, const uint16_t *k, const uint16_t *k_k,
-                  const uint16_t *k_a, uint16_t *a_out, uint16_t *kk_out, uint16_t *k_out, int C, hipStream_t st);
-int launch_gates(const rwkv7_gates_io &io, int rv, int rw, int ra, int rg, int C, hipStream_t st);
+                  const uint16_t *k_a, uint16_t *a_out, uint16_t *kk_out, uint16_t *k_out, int C, int bf,
+                  hipStream_t st);
+int launch_gates(const rwkv7_gates_io &io, int rv, int rw, int ra, int rg, int C, int bf, hipStream_t st);
 int launch_rank_gemv(const uint16_t *xv, const uint16_t *xw, const uint16_t *xa, const uint16_t *xg,
-                     const uint16_t *W, uint16_t *out, int rv, int rw, int ra, int rg, int C, hipStream_t st);
-int launch_l2norm(const uint16_t *kk, const uint16_t *a, uint16_t *kn, uint16_t *b, int H, hipStream_t st);
+                     const uint16_t *W, uint16_t *out, int rv, int rw, int ra, int rg, int C, int bf,
+                     hipStream_t st);
+int launch_l2norm(const uint16_t *kk, const uint16_t *a, uint16_t *kn, uint16_t *b, int H, int bf, hipStream_t st);
 int launch_gn_rkrk(const uint16_t *y, const uint16_t *r, const uint16_t *k, const uint16_t *v, const uint16_t *r_k,
-                   const uint16_t *lw, const uint16_t *lb, uint16_t *out, int H, hipStream_t st);
+                   const uint16_t *lw, const uint16_t *lb, uint16_t *out, int H, int bf, hipStream_t st);
 
 // One-token, one-sequence decode as a single persistent kernel (decode_mk.hip).
 int mk_cus();

@@ -141,13 +141,20 @@ template <> RWKV7_DEV float to_f<uint16_t>(uint16_t x) { return h2f(x); }
 template <typename T> RWKV7_DEV T from_f(float x);
 template <> RWKV7_DEV float from_f<float>(float x) { return x; }
 template <> RWKV7_DEV uint16_t from_f<uint16_t>(float x) { return f2h(x); }
+template <> RWKV7_DEV float to_f<bf16_t>(bf16_t x) { return b2f(x.bits); }
+template <> RWKV7_DEV bf16_t from_f<bf16_t>(float x) { return bf16_t{f2b(x)}; }
 
 // Four consecutive elements as float4: one 16-byte load for f32, one 8-byte
-// load for f16.
+// load for f16 or bf16.
 RWKV7_DEV float4 ld4_as_f(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 RWKV7_DEV float4 ld4_as_f(const uint16_t *p) {
   const half4 h = __builtin_bit_cast(half4, *reinterpret_cast<const uint2 *>(p));
   return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+}
+RWKV7_DEV float4 ld4_as_f(const bf16_t *p) {
+  const uint2 u = *reinterpret_cast<const uint2 *>(p);
+  return make_float4(__builtin_bit_cast(float, u.x << 16), __builtin_bit_cast(float, u.x & 0xFFFF0000u),
+                     __builtin_bit_cast(float, u.y << 16), __builtin_bit_cast(float, u.y & 0xFFFF0000u));
 }
 
 // ---------------------------------------------------------------------------
@@ -270,7 +277,8 @@ struct GateStager {
   RWKV7_DEV void record(int, int, int, const float4 &) {}
 };
 
-// Operator level: w, a, b, k, r, v as given ([B, T, H, 64]; w f32 or f16).
+// Operator level: w, a, b, k, r, v as given ([B, T, H, 64]; f16 or bf16, w
+// also f32; every operand f32 for the training forward).
 // Thread -> token t >> 4, float4 q = t & 15 of the head's 64 channels.
 template <int CH, typename TI, typename TW, typename TY>
 struct RawStager {
@@ -594,6 +602,8 @@ int launch_wkv7_bwd(const Wkv7BwdArgs &p, hipStream_t st) {
 template int launch_wkv7_scan<uint16_t, float, uint16_t>(const ScanArgs<uint16_t, float, uint16_t> &, hipStream_t);
 template int launch_wkv7_scan<uint16_t, uint16_t, uint16_t>(const ScanArgs<uint16_t, uint16_t, uint16_t> &, hipStream_t);
 template int launch_wkv7_scan<float, float, float>(const ScanArgs<float, float, float> &, hipStream_t);
+template int launch_wkv7_scan<bf16_t, float, bf16_t>(const ScanArgs<bf16_t, float, bf16_t> &, hipStream_t);
+template int launch_wkv7_scan<bf16_t, bf16_t, bf16_t>(const ScanArgs<bf16_t, bf16_t, bf16_t> &, hipStream_t);
 
 // Chains the segments of dplr_scan_kernel (model path). Grid (4 H, B, (nseg - 1) *
 // nblk): the workgroup of segment j >= 1 and 16-token block k of it forms the
@@ -937,17 +947,17 @@ int launch_ln_rows(const void *x, int x_f32, const float *w, const float *b, voi
 
 // Token-shift lerps for one vector (src/rwkv_tl/kernels/lerp.py:140-198).
 __global__ void lerp_kernel(const uint16_t *x, const uint16_t *prev, const float *mu, int n_mix,
-                            uint16_t *out, uint16_t *x_copy, int C) {
+                            uint16_t *out, uint16_t *x_copy, int C, int bf) {
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= C) return;
-  const float xv = h2f(x[c]), pv = h2f(prev[c]);
-  for (int j = 0; j < n_mix; ++j) out[(int64_t)j * C + c] = f2h(xv + mu[(int64_t)j * C + c] * (pv - xv));
+  const float xv = u16_to_f(x[c], bf), pv = u16_to_f(prev[c], bf);
+  for (int j = 0; j < n_mix; ++j) out[(int64_t)j * C + c] = f_to_u16(xv + mu[(int64_t)j * C + c] * (pv - xv), bf);
   if (x_copy) x_copy[c] = x[c];  // after this thread's read of prev[c]
 }
 
 int launch_lerp(const uint16_t *x, const uint16_t *prev, const float *mu, int n_mix, uint16_t *out,
-                uint16_t *x_copy, int C, hipStream_t st) {
-  lerp_kernel<<<(C + 255) / 256, 256, 0, st>>>(x, prev, mu, n_mix, out, x_copy, C);
+                uint16_t *x_copy, int C, int bf, hipStream_t st) {
+  lerp_kernel<<<(C + 255) / 256, 256, 0, st>>>(x, prev, mu, n_mix, out, x_copy, C, bf);
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;
 }

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the HIP library)
 
 LIB_NAME = "librwkv7_hip.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # rwkv7_model.flags
 MODEL_MULTI_LAUNCH_DECODE = 1
@@ -164,22 +164,22 @@ def _declare(lib: ctypes.CDLL) -> None:
         "rwkv7_decode": (ctypes.c_int, [ctypes.POINTER(Model), ctypes.POINTER(StateDesc), vp, vp, vp, i64, vp]),
         "rwkv7_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(Model), ctypes.POINTER(StateDesc), vp, vp, vp]),
         "rwkv7_prefill": (ctypes.c_int, [ctypes.POINTER(Model), ctypes.POINTER(StateDesc), vp, i32, vp, i64, vp]),
-        "rwkv7_wkv7": (ctypes.c_int, [vp, vp, vp, i32, vp, vp, vp, vp, vp, i32, i32, i32, vp]),
+        "rwkv7_wkv7": (ctypes.c_int, [vp, vp, vp, i32, vp, vp, vp, vp, vp, i32, i32, i32, i32, vp]),
         "rwkv7_wkv7_f32": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, vp]),
         "rwkv7_wkv7_backward": (ctypes.c_int, [vp] * 17 + [i32, i32, i32, vp]),
-        "rwkv7_layernorm": (ctypes.c_int, [vp, i32, vp, vp, vp, i32, i32, vp]),
-        "rwkv7_lerp": (ctypes.c_int, [vp, vp, vp, i32, vp, vp, i32, vp]),
-        "rwkv7_gemv_f16": (ctypes.c_int, [vp, vp, i64, vp, i32, i32, vp]),
+        "rwkv7_layernorm": (ctypes.c_int, [vp, i32, vp, vp, vp, i32, i32, i32, vp]),
+        "rwkv7_lerp": (ctypes.c_int, [vp, vp, vp, i32, vp, vp, i32, i32, vp]),
+        "rwkv7_gemv_f16": (ctypes.c_int, [vp, vp, i64, vp, i32, i32, i32, vp]),
         "rwkv7_gemv_i8": (ctypes.c_int, [vp, vp, i64, vp, vp, i32, i32, vp]),
         "rwkv7_gemv_any4": (ctypes.c_int, [vp, vp, i64, vp, vp, i32, i32, vp]),
-        "rwkv7_gemm_f16": (ctypes.c_int, [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp]),
-        "rwkv7_w_gate": (ctypes.c_int, [vp, vp, vp, i32, vp]),
-        "rwkv7_v_gate": (ctypes.c_int, [vp, vp, vp, vp, vp, i32, vp]),
-        "rwkv7_a_kk_k": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, i32, vp]),
-        "rwkv7_gates": (ctypes.c_int, [ctypes.POINTER(GatesIO), i32, i32, i32, i32, i32, vp]),
-        "rwkv7_rank_gemv": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]),
-        "rwkv7_l2norm_neg_kk_a": (ctypes.c_int, [vp, vp, vp, vp, i32, vp]),
-        "rwkv7_gn_rkrk": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, i32, vp]),
+        "rwkv7_gemm_f16": (ctypes.c_int, [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, i32, vp]),
+        "rwkv7_w_gate": (ctypes.c_int, [vp, vp, vp, i32, i32, vp]),
+        "rwkv7_v_gate": (ctypes.c_int, [vp, vp, vp, vp, vp, i32, i32, vp]),
+        "rwkv7_a_kk_k": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, vp]),
+        "rwkv7_gates": (ctypes.c_int, [ctypes.POINTER(GatesIO), i32, i32, i32, i32, i32, i32, vp]),
+        "rwkv7_rank_gemv": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp]),
+        "rwkv7_l2norm_neg_kk_a": (ctypes.c_int, [vp, vp, vp, vp, i32, i32, vp]),
+        "rwkv7_gn_rkrk": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, vp]),
         "rwkv7_sample": (ctypes.c_int, [vp, i32, i64, i32, i32, ctypes.POINTER(Sampling), vp, i64, i32, vp, vp, i64, vp]),
     }
     for name, (res, args) in sig.items():

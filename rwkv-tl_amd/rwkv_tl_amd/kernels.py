@@ -1,10 +1,14 @@
-"""Operator-level API on the HIP library (counterpart of ``rwkv_tl.kernels.fp16``).
+"""Operator-level API on the HIP library (counterpart of ``rwkv_tl.kernels.fp16``
+and ``rwkv_tl.kernels.bf16``).
 
 Same names, argument order and return conventions as the reference
-(``src/rwkv_tl/kernels/fp16.py:13-30``); tensors must be on the ROCm device
-and are validated on the host before any launch (ValueError on a bad shape or
-dtype). There is no CPU branch: the reference's in-function torch fallbacks
-(for example ``dplr.py:258-267``) are not reproduced.
+(``src/rwkv_tl/kernels/fp16.py:13-30``, ``bf16.py:13-30``); tensors must be on
+the ROCm device and are validated on the host before any launch (ValueError on
+a bad shape or dtype). The 16-bit operands of one call are all float16 or all
+bfloat16, and the outputs take the same dtype: this one module serves both of
+the reference's namespaces, which bind the same kernels to the two dtypes.
+There is no CPU branch: the reference's in-function torch fallbacks (for
+example ``dplr.py:258-267``) are not reproduced.
 
 * ``fused_dplr(S, R, W, K, V, A, B)`` / ``fused_dplr_T(...)``: the wkv7 DPLR
   step / sequence (``dplr.py:256-285``); ``wkv7`` is the batched form.
@@ -15,7 +19,7 @@ dtype). There is no CPU branch: the reference's in-function torch fallbacks
 * Weight-only quantised GEMVs (the reference's plan, ``TODO.md:58-63``):
   ``quantize_i8`` / ``gemv_i8`` (per-row int8) and ``quantize_any4`` /
   ``gemv_any4`` (per-row 16-entry tables, 4-bit codes).
-* The time-mix stage operators, f16 in and out: ``fused_w_gate``,
+* The time-mix stage operators, 16-bit in and out: ``fused_w_gate``,
   ``fused_v_gate``, ``fused_a_kk_k`` (``gates.py:287-313``), ``fused_gates``
   (``gates.py:315-357``), ``fused_rank_gemv`` (``gates.py:254-285``),
   ``fused_l2norm_neg_kk_a`` (``dplr.py:229-235``), ``fused_gn_rkrk``
@@ -47,26 +51,39 @@ def _dev(*ts: Tensor) -> None:
         _need(t.is_contiguous(), "tensors must be contiguous")
 
 
+_H16 = (torch.float16, torch.bfloat16)
+
+
+def _h16(*ts: Tensor) -> int:
+    """All float16 or all bfloat16 (on the device); returns the kernels' bf16 flag."""
+    _dev(*ts)
+    dt = ts[0].dtype
+    _need(dt in _H16, f"expected float16 or bfloat16, got {dt}")
+    for t in ts:
+        _need(t.dtype == dt, f"mixed 16-bit dtypes: {dt} and {t.dtype}")
+    return int(dt == torch.bfloat16)
+
+
 def wkv7(S: Tensor, r: Tensor, w: Tensor, k: Tensor, v: Tensor, a: Tensor, b: Tensor) -> Tensor:
     """Batched DPLR recurrence; updates ``S`` [B,H,64,64] fp32 in place.
 
-    ``r, k, v, a, b``: f16 [B, T, H, 64]; ``w``: f16 or f32 of the same shape.
-    Returns ``y`` f16 [B, T, H, 64] with ``y_t = S_t r_t``.
+    ``r, k, v, a, b``: f16 or bf16 [B, T, H, 64]; ``w``: the same 16-bit
+    dtype or f32. Returns ``y`` [B, T, H, 64] of r's dtype with ``y_t = S_t r_t``.
     """
     _dev(S, r, w, k, v, a, b)
     _need(S.dtype == torch.float32 and S.dim() == 4 and S.shape[2:] == (N, N), "S must be f32 [B,H,64,64]")
     Bsz, H = S.shape[:2]
     _need(r.dim() == 4 and r.shape[0] == Bsz and r.shape[2] == H and r.shape[3] == N, "r must be [B,T,H,64]")
     T = r.shape[1]
+    bf = _h16(r, k, v, a, b)
     for name, t in (("k", k), ("v", v), ("a", a), ("b", b)):
-        _need(t.shape == r.shape and t.dtype == torch.float16, f"{name} must be f16 {tuple(r.shape)}")
-    _need(r.dtype == torch.float16, "r must be f16")
-    _need(w.shape == r.shape and w.dtype in (torch.float16, torch.float32), "w must be f16/f32 like r")
+        _need(t.shape == r.shape, f"{name} must be {tuple(r.shape)}")
+    _need(w.shape == r.shape and w.dtype in (r.dtype, torch.float32), "w must be like r, or f32")
     y = torch.empty_like(r)
     lib = _lib.load()
     rc = lib.rwkv7_wkv7(
         S.data_ptr(), r.data_ptr(), w.data_ptr(), int(w.dtype == torch.float32), k.data_ptr(),
-        v.data_ptr(), a.data_ptr(), b.data_ptr(), y.data_ptr(), Bsz, T, H, _lib.stream_handle(),
+        v.data_ptr(), a.data_ptr(), b.data_ptr(), y.data_ptr(), Bsz, T, H, bf, _lib.stream_handle(),
     )
     _lib.check(rc, "rwkv7_wkv7")
     return y
@@ -165,20 +182,19 @@ def fused_dplr(S: Tensor, R: Tensor, W: Tensor, K: Tensor, V: Tensor, A: Tensor,
 
 
 def _lerp(x: Tensor, prev: Tensor, mus: list[Tensor], x_copy: Tensor | None) -> Tensor:
-    _dev(x, prev)
+    bf = _h16(x, prev)
     C = x.shape[-1]
     _need(x.dim() == 1 and prev.shape == x.shape, "x and prev must be [C]")
-    _need(x.dtype == torch.float16 and prev.dtype == torch.float16, "x and prev must be f16")
     mu = torch.stack([m.reshape(-1).float() for m in mus]).contiguous()
     _need(mu.shape[1] == C, "mix vectors must be [C]")
-    out = torch.empty(len(mus), C, dtype=torch.float16, device=x.device)
+    out = torch.empty(len(mus), C, dtype=x.dtype, device=x.device)
     if x_copy is not None:
         _dev(x_copy)
-        _need(x_copy.shape == x.shape and x_copy.dtype == torch.float16, "x_copy must be f16 [C]")
+        _need(x_copy.shape == x.shape and x_copy.dtype == x.dtype, "x_copy must be like x [C]")
     lib = _lib.load()
     rc = lib.rwkv7_lerp(
         x.data_ptr(), prev.data_ptr(), mu.data_ptr(), len(mus), out.data_ptr(),
-        None if x_copy is None else x_copy.data_ptr(), C, _lib.stream_handle(),
+        None if x_copy is None else x_copy.data_ptr(), C, bf, _lib.stream_handle(),
     )
     _lib.check(rc, "rwkv7_lerp")
     return out
@@ -203,27 +219,28 @@ def layer_norm(x: Tensor, weight: Tensor, bias: Tensor) -> Tensor:
     """LayerNorm over the last dim, eps 1e-5; returns f32 (``weight.py:14-15``)."""
     _dev(x)
     C = x.shape[-1]
-    _need(x.dtype in (torch.float16, torch.float32), "x must be f16 or f32")
+    _need(x.dtype in (torch.float16, torch.bfloat16, torch.float32), "x must be f16, bf16 or f32")
     rows = x.reshape(-1, C)
     y = torch.empty(rows.shape, dtype=torch.float32, device=x.device)
     w32, b32 = weight.float().contiguous(), bias.float().contiguous()
     lib = _lib.load()
     rc = lib.rwkv7_layernorm(
         rows.data_ptr(), int(x.dtype == torch.float32), w32.data_ptr(), b32.data_ptr(), y.data_ptr(),
-        rows.shape[0], C, _lib.stream_handle(),
+        rows.shape[0], C, int(x.dtype == torch.bfloat16), _lib.stream_handle(),
     )
     _lib.check(rc, "rwkv7_layernorm")
     return y.reshape(x.shape)
 
 
 def gemv(x: Tensor, W: Tensor) -> Tensor:
-    """``y = W x`` for f16 W [N, K] (``[out, in]``) and f32 x [K]; returns f32 [N]."""
-    _dev(x, W)
-    _need(W.dtype == torch.float16 and W.dim() == 2, "W must be f16 [N, K]")
+    """``y = W x`` for f16 or bf16 W [N, K] (``[out, in]``) and f32 x [K]; returns f32 [N]."""
+    _dev(x)
+    bf = _h16(W)
+    _need(W.dim() == 2, "W must be [N, K]")
     _need(x.dtype == torch.float32 and x.shape == (W.shape[1],), "x must be f32 [K]")
     y = torch.empty(W.shape[0], dtype=torch.float32, device=x.device)
     lib = _lib.load()
-    rc = lib.rwkv7_gemv_f16(x.data_ptr(), W.data_ptr(), W.shape[1], y.data_ptr(), W.shape[0], W.shape[1],
+    rc = lib.rwkv7_gemv_f16(x.data_ptr(), W.data_ptr(), W.shape[1], y.data_ptr(), W.shape[0], W.shape[1], bf,
                             _lib.stream_handle())
     _lib.check(rc, "rwkv7_gemv_f16")
     return y
@@ -282,12 +299,12 @@ def gemv_any4(x: Tensor, codes: Tensor, lut: Tensor) -> Tensor:
 
 
 def gemm(A: Tensor, W: Tensor, epi: str = "f32", out: Tensor | None = None) -> Tensor:
-    """``epi(A W^T)`` for f16 A [M, K], W [N, K]; ``epi`` in f32/f16/relu2/add.
+    """``epi(A W^T)`` for A [M, K], W [N, K], both f16 or both bf16; ``epi`` in
+    f32/f16/relu2/add ("f16" and relu2 store the operands' 16-bit dtype).
 
     ``add`` accumulates into ``out`` (f32 [M, N]) and returns it.
     """
-    _dev(A, W)
-    _need(A.dtype == torch.float16 and W.dtype == torch.float16, "A and W must be f16")
+    bf = _h16(A, W)
     _need(A.dim() == 2 and W.dim() == 2 and A.shape[1] == W.shape[1], "A [M,K] and W [N,K] must share K")
     M, K = A.shape
     Nn = W.shape[0]
@@ -295,11 +312,11 @@ def gemm(A: Tensor, W: Tensor, epi: str = "f32", out: Tensor | None = None) -> T
     if epi == "add":
         _need(out is not None and out.dtype == torch.float32 and out.shape == (M, Nn), "add needs f32 out [M, N]")
     else:
-        dt = torch.float32 if epi == "f32" else torch.float16
+        dt = torch.float32 if epi == "f32" else A.dtype
         out = torch.empty(M, Nn, dtype=dt, device=A.device)
     _dev(out)
     lib = _lib.load()
-    rc = lib.rwkv7_gemm_f16(A.data_ptr(), K, W.data_ptr(), K, out.data_ptr(), Nn, M, Nn, K, code,
+    rc = lib.rwkv7_gemm_f16(A.data_ptr(), K, W.data_ptr(), K, out.data_ptr(), Nn, M, Nn, K, code, bf,
                             _lib.stream_handle())
     _lib.check(rc, "rwkv7_gemm_f16")
     return out
@@ -322,28 +339,23 @@ def fused_lerp6_rkv_copy(x, prev, x_r, x_w, x_k, x_v, x_a, x_g, x_copy, rWt_stac
 
 
 # ---------------------------------------------------------------------------
-# time-mix stage operators (f16 tensors, fp32 arithmetic inside)
+# time-mix stage operators (f16 or bf16 tensors, fp32 arithmetic inside)
 # ---------------------------------------------------------------------------
 
 
-def _f16(*ts: Tensor) -> None:
-    _dev(*ts)
-    for t in ts:
-        _need(t.dtype == torch.float16, f"expected float16, got {t.dtype}")
-
-
-def _vecs(C: int, *ts: Tensor) -> None:
-    _f16(*ts)
+def _vecs(C: int, *ts: Tensor) -> int:
+    bf = _h16(*ts)
     for t in ts:
         _need(t.numel() == C, f"expected {C} elements, got shape {tuple(t.shape)}")
+    return bf
 
 
 def fused_w_gate(x: Tensor, w0: Tensor) -> Tensor:
     """``exp(-sigmoid(w0 + x) / sqrt(e))`` over [C] (``gates.py:287-291``)."""
     C = x.numel()
-    _vecs(C, x, w0)
+    bf = _vecs(C, x, w0)
     out = torch.empty_like(x)
-    _lib.check(_lib.load().rwkv7_w_gate(x.data_ptr(), w0.data_ptr(), out.data_ptr(), C, _lib.stream_handle()),
+    _lib.check(_lib.load().rwkv7_w_gate(x.data_ptr(), w0.data_ptr(), out.data_ptr(), C, bf, _lib.stream_handle()),
                "rwkv7_w_gate")
     return out
 
@@ -351,20 +363,20 @@ def fused_w_gate(x: Tensor, w0: Tensor) -> Tensor:
 def fused_v_gate(v: Tensor, v_first: Tensor, v0: Tensor, v12: Tensor) -> Tensor:
     """``v + sigmoid(v0 + v12) * (v_first - v)`` over [C] (``gates.py:293-297``)."""
     C = v.numel()
-    _vecs(C, v, v_first, v0, v12)
+    bf = _vecs(C, v, v_first, v0, v12)
     out = torch.empty_like(v)
     _lib.check(_lib.load().rwkv7_v_gate(v.data_ptr(), v_first.data_ptr(), v0.data_ptr(), v12.data_ptr(),
-                                        out.data_ptr(), C, _lib.stream_handle()), "rwkv7_v_gate")
+                                        out.data_ptr(), C, bf, _lib.stream_handle()), "rwkv7_v_gate")
     return out
 
 
 def fused_a_kk_k(a0: Tensor, a_x: Tensor, k: Tensor, k_k: Tensor, k_a: Tensor) -> tuple[Tensor, Tensor, Tensor]:
     """``(sigmoid(a0 + a_x), k * k_k, k + k_a * (k * a - k))`` over [C] (``gates.py:299-313``)."""
     C = k.numel()
-    _vecs(C, a0, a_x, k, k_k, k_a)
+    bf = _vecs(C, a0, a_x, k, k_k, k_a)
     a, kk, kn = (torch.empty_like(k) for _ in range(3))
     _lib.check(_lib.load().rwkv7_a_kk_k(a0.data_ptr(), a_x.data_ptr(), k.data_ptr(), k_k.data_ptr(), k_a.data_ptr(),
-                                        a.data_ptr(), kk.data_ptr(), kn.data_ptr(), C, _lib.stream_handle()),
+                                        a.data_ptr(), kk.data_ptr(), kn.data_ptr(), C, bf, _lib.stream_handle()),
                "rwkv7_a_kk_k")
     return a, kk, kn
 
@@ -377,8 +389,8 @@ def fused_gates(vr: Tensor, wr: Tensor, ar: Tensor, gr: Tensor, v: Tensor, v_fir
     ``vr/wr/ar/gr`` are the first-step results [R] before activation,
     ``v2t/w2t/a2t/g2t`` the second-step matrices [C, R]."""
     C = v.numel()
-    _vecs(C, v, v_first, k, v0, w0, a0, k_k, k_a)
-    _f16(vr, wr, ar, gr, v2t, w2t, a2t, g2t)
+    bf = _vecs(C, v, v_first, k, v0, w0, a0, k_k, k_a)
+    _need(_h16(v, vr, wr, ar, gr, v2t, w2t, a2t, g2t) == bf, "one 16-bit dtype for every operand")
     ranks = []
     for r_, m_ in ((vr, v2t), (wr, w2t), (ar, a2t), (gr, g2t)):
         _need(m_.dim() == 2 and m_.shape == (C, r_.numel()), f"rank matrix {tuple(m_.shape)} vs [{C}, {r_.numel()}]")
@@ -386,7 +398,7 @@ def fused_gates(vr: Tensor, wr: Tensor, ar: Tensor, gr: Tensor, v: Tensor, v_fir
     outs = [torch.empty_like(v) for _ in range(6)]
     io = _lib.GatesIO(*(t.data_ptr() for t in (vr, wr, ar, gr, v2t, w2t, a2t, g2t, v, v_first, k, v0, w0, a0,
                                                k_k, k_a, *outs)))
-    _lib.check(_lib.load().rwkv7_gates(ctypes.byref(io), *ranks, C, _lib.stream_handle()), "rwkv7_gates")
+    _lib.check(_lib.load().rwkv7_gates(ctypes.byref(io), *ranks, C, bf, _lib.stream_handle()), "rwkv7_gates")
     return tuple(outs)
 
 
@@ -394,36 +406,36 @@ def fused_rank_gemv(xv: Tensor, xw: Tensor, xa: Tensor, xg: Tensor, packed: Tens
                     rv: int, rw: int, ra: int, rg: int) -> Tensor:
     """``[v1t; w1t; a1t; g1t] @ [xv; xw; xa; xg]`` by row segment; returns [rv+rw+ra+rg] (``gates.py:254-285``)."""
     C = xv.numel()
-    _vecs(C, xv, xw, xa, xg)
-    _f16(packed)
+    bf = _vecs(C, xv, xw, xa, xg)
+    _need(_h16(xv, packed) == bf, "one 16-bit dtype for every operand")
     _need(packed.shape == (rv + rw + ra + rg, C), f"packed {tuple(packed.shape)} vs [{rv + rw + ra + rg}, {C}]")
-    out = torch.empty(rv + rw + ra + rg, dtype=torch.float16, device=xv.device)
+    out = torch.empty(rv + rw + ra + rg, dtype=xv.dtype, device=xv.device)
     _lib.check(_lib.load().rwkv7_rank_gemv(xv.data_ptr(), xw.data_ptr(), xa.data_ptr(), xg.data_ptr(),
-                                           packed.data_ptr(), out.data_ptr(), rv, rw, ra, rg, C,
+                                           packed.data_ptr(), out.data_ptr(), rv, rw, ra, rg, C, bf,
                                            _lib.stream_handle()), "rwkv7_rank_gemv")
     return out
 
 
 def fused_l2norm_neg_kk_a(kk: Tensor, a: Tensor) -> tuple[Tensor, Tensor]:
     """Per head ``kk / max(||kk||, 1e-12)`` and ``-(that) * a``, [H, 64] (``dplr.py:229-235``)."""
-    _f16(kk, a)
+    bf = _h16(kk, a)
     _need(kk.dim() == 2 and kk.shape[1] == N and a.shape == kk.shape, "kk and a must be [H, 64]")
     kn, b = torch.empty_like(kk), torch.empty_like(kk)
     _lib.check(_lib.load().rwkv7_l2norm_neg_kk_a(kk.data_ptr(), a.data_ptr(), kn.data_ptr(), b.data_ptr(),
-                                                 kk.shape[0], _lib.stream_handle()), "rwkv7_l2norm_neg_kk_a")
+                                                 kk.shape[0], bf, _lib.stream_handle()), "rwkv7_l2norm_neg_kk_a")
     return kn, b
 
 
 def fused_gn_rkrk(y: Tensor, r: Tensor, k: Tensor, v: Tensor, r_k: Tensor, ln_xW: Tensor, ln_xB: Tensor) -> Tensor:
     """GroupNorm per head (eps 64e-5) + ``(sum r k r_k) * v``; [H, 64] in, [H*64] out (``dplr.py:237-254``)."""
-    _f16(y, r, k, v, r_k, ln_xW, ln_xB)
+    bf = _h16(y, r, k, v, r_k, ln_xW, ln_xB)
     _need(y.dim() == 2 and y.shape[1] == N, "y must be [H, 64]")
     for t in (r, k, v, r_k):
         _need(t.shape == y.shape, "r, k, v, r_k must match y")
     H = y.shape[0]
     _need(ln_xW.numel() == H * N and ln_xB.numel() == H * N, "ln_x weight and bias must have H*64 elements")
-    out = torch.empty(H * N, dtype=torch.float16, device=y.device)
+    out = torch.empty(H * N, dtype=y.dtype, device=y.device)
     _lib.check(_lib.load().rwkv7_gn_rkrk(y.data_ptr(), r.data_ptr(), k.data_ptr(), v.data_ptr(), r_k.data_ptr(),
-                                         ln_xW.data_ptr(), ln_xB.data_ptr(), out.data_ptr(), H,
+                                         ln_xW.data_ptr(), ln_xB.data_ptr(), out.data_ptr(), H, bf,
                                          _lib.stream_handle()), "rwkv7_gn_rkrk")
     return out

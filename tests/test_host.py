@@ -147,15 +147,15 @@ def test_workspace_and_entry_point_argument_errors():
     model = _lib.Model(dims=d)
     st = _lib.StateDesc(batch=1)
     assert lib.rwkv7_decode(ctypes.byref(model), ctypes.byref(st), None, None, None, 0, None) == 1
-    assert lib.rwkv7_wkv7(None, None, None, 0, None, None, None, None, None, 1, 1, 1, None) == 1
-    assert lib.rwkv7_gemm_f16(1, 8, 1, 8, 1, 8, 1, 8, 8, 9, None) == 1  # bad epilogue code
-    assert lib.rwkv7_gemv_f16(1, 1, 100, 1, 4, 100, None) == 2       # K % 256
+    assert lib.rwkv7_wkv7(None, None, None, 0, None, None, None, None, None, 1, 1, 1, 0, None) == 1
+    assert lib.rwkv7_gemm_f16(1, 8, 1, 8, 1, 8, 1, 8, 8, 9, 0, None) == 1  # bad epilogue code
+    assert lib.rwkv7_gemv_f16(1, 1, 100, 1, 4, 100, 0, None) == 2       # K % 256
     assert lib.rwkv7_gemv_i8(None, 16, 16, 16, 16, 4, 16, None) == 1  # null x
     assert lib.rwkv7_gemv_i8(16, 16, 24, 16, 16, 4, 24, None) == 2    # K % 16
     assert lib.rwkv7_gemv_i8(16, 16, 16, 16, 16, 4, 16384, None) == 2  # K > 8192
     assert lib.rwkv7_gemv_i8(16, 16, 32, 16, 16, 4, 48, None) == 2    # ldq < K
     assert lib.rwkv7_gemv_i8(16, 8, 16, 16, 16, 4, 16, None) == 2     # Q not 16-byte aligned
-    assert lib.rwkv7_lerp(1, 1, 1, 3, 1, None, 8, None) == 2          # n_mix not 1 or 6
+    assert lib.rwkv7_lerp(1, 1, 1, 3, 1, None, 8, 0, None) == 2          # n_mix not 1 or 6
 
 
 def test_state_layout_and_arena():
