@@ -114,8 +114,11 @@ typedef struct rwkv7_model {
                               offset rwkv7_head_q_scale_offset(dims) */
 } rwkv7_model;
 
-/* rwkv7_model.flags: run batch-1 decode as one launch per stage (the
- * multi-launch GEMV path) instead of the single persistent kernel. */
+/* rwkv7_model.flags: run every step on the multi-launch paths (one launch
+ * per stage) instead of the persistent kernels: batch-1 decode on the GEMV
+ * kernels instead of the one-token kernel, and steps of B sequences x T tokens
+ * with B T <= 16 (batched decode, short prefills) on the MFMA GEMMs instead of
+ * the few-row kernel. */
 #define RWKV7_MODEL_MULTI_LAUNCH_DECODE 1u
 /* rwkv7_model.flags: batch-1 decode streams the int8 arenas (layers_q,
  * head_q; both required) in the persistent kernel, dequantising in the dot
@@ -163,12 +166,12 @@ int64_t rwkv7_head_q_scale_offset(const rwkv7_dims *dims);
 
 /* Bytes of scratch that rwkv7_decode / rwkv7_prefill need for `batch`
  * sequences of `seq_len` tokens (seq_len 1 for decode). The workspace must be
- * zero-filled once after allocation: its first region holds the hand-off words
- * of the persistent decode kernel and is kept consistent by every later call.
+ * zero-filled once after allocation: its first regions hold the hand-off words
+ * of the persistent kernels and are kept consistent by every later call.
  * One workspace must not be used by two calls that can run concurrently. */
 int64_t rwkv7_workspace_bytes(const rwkv7_dims *dims, int32_t batch, int32_t seq_len);
 
-/* Number of persistent-decode launches on `workspace` that were aborted
+/* Number of persistent-kernel launches on `workspace` that were aborted
  * (32-bit word at byte 32 of the workspace, cumulative; the caller may zero
  * it). Synchronises `stream` first. A launch aborts when one of its grid-wide
  * hand-offs waits longer than about a second (its workgroups were not all
@@ -184,7 +187,10 @@ int rwkv7_workspace_errors(const void *workspace, int64_t workspace_bytes, uint3
 /* One decode step for every sequence of `state`: tokens i64 [B] (device),
  * logits f16 [B, V] (device). Equivalent of RWKV7Base.decode
  * (demo/_rwkv7_base.py:74-87) / RWKV7Torch.decode (demo/rwkv7_torch.py:150-158),
- * batched. Token ids outside [0, V) are clamped into range. */
+ * batched. Token ids outside [0, V) are clamped into range. One sequence runs
+ * as the one-token persistent kernel, 2..16 sequences as the few-row
+ * persistent kernel, where the device fits their grids (else, and with
+ * RWKV7_MODEL_MULTI_LAUNCH_DECODE, one launch per stage). */
 int rwkv7_decode(const rwkv7_model *model, const rwkv7_state *state,
                  const int64_t *tokens, void *logits, void *workspace,
                  int64_t workspace_bytes, void *stream);
@@ -214,7 +220,9 @@ int rwkv7_decode_noalloc(const rwkv7_model *model, const rwkv7_state *state,
 
 /* Prefill seq_len tokens per sequence: tokens i64 [B, T] (device). Updates
  * state in place and produces no logits, like RWKV7Base.prefill
- * (demo/_rwkv7_base.py:89-98) / RWKV7Torch.prefill (demo/rwkv7_torch.py:160-171). */
+ * (demo/_rwkv7_base.py:89-98) / RWKV7Torch.prefill (demo/rwkv7_torch.py:160-171).
+ * B x T <= 16 rows run as the few-row persistent kernel where the device fits
+ * its grid (not with RWKV7_MODEL_MULTI_LAUNCH_DECODE). */
 int rwkv7_prefill(const rwkv7_model *model, const rwkv7_state *state,
                   const int64_t *tokens, int32_t seq_len, void *workspace,
                   int64_t workspace_bytes, void *stream);

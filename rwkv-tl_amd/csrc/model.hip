@@ -100,8 +100,13 @@ static int64_t exchange_bytes(const rwkv7_dims &d) {
 static unsigned *gemm_counters(const rwkv7_dims &d, char *base) {
   return reinterpret_cast<unsigned *>(base + exchange_bytes(d));
 }
+// Then the exchange region of the persistent few-row kernel (zero before
+// first use, only ever touched by that kernel).
+static char *rows_exchange(const rwkv7_dims &d, char *base) {
+  return base + exchange_bytes(d) + align256((int64_t)kGemmCounters * 4);
+}
 static int64_t fixed_bytes(const rwkv7_dims &d) {
-  return exchange_bytes(d) + align256((int64_t)kGemmCounters * 4);
+  return exchange_bytes(d) + align256((int64_t)kGemmCounters * 4) + align256(rows_exchange_bytes(d));
 }
 
 static int64_t decode_ws(const rwkv7_dims &d, char *base, DecodeWs *w) {
@@ -465,6 +470,21 @@ static bool use_persistent_decode(const rwkv7_model &m, int batch, bool logits) 
   return mk_usable(m);
 }
 
+// Batched decode steps and prefills of B sequences x T tokens with B T <= 16
+// run as the one-launch few-row kernel when it serves the model (half
+// precision, fragment arenas, no multi-launch flag) and its grid fits; batch-1
+// decode has its own kernel above.
+static bool use_rows_kernel(const rwkv7_model &m, int batch, int T) { return rows_usable(m, batch, T); }
+
+static int run_rows(const rwkv7_model &m, const rwkv7_state &s, const int64_t *tok, int T, void *logits, char *ws,
+                    hipStream_t st) {
+  rwkv7_layer_layout lay;
+  layout_of(m.dims, &lay);
+  // the aborted-launch counter shared with the batch-1 kernel (workspace byte 32)
+  return launch_rows_mk(m, lay, s, tok, T, logits, rows_exchange(m.dims, ws), reinterpret_cast<unsigned *>(ws + 32),
+                        st);
+}
+
 }  // namespace rwkv7
 
 using namespace rwkv7;
@@ -506,7 +526,8 @@ int64_t rwkv7_workspace_bytes(const rwkv7_dims *dims, int32_t batch, int32_t seq
 int rwkv7_decode_launches(const rwkv7_model *model, int32_t batch, int32_t with_logits) {
   if (!model || check_dims(&model->dims) != RWKV7_OK || batch < 1) return -1;
   const rwkv7_dims *dims = &model->dims;
-  if (use_persistent_decode(*model, batch, with_logits != 0)) return 1;
+  if (use_persistent_decode(*model, batch, with_logits != 0) || (batch > 1 && use_rows_kernel(*model, batch, 1)))
+    return 1;
   // decode_one: embed, 6 per layer, head GEMV; run_batched with one token:
   // embed, 7 per layer (LayerNorm + shift, projections, per-head core,
   // o-projection, LayerNorm + shift, FFN key, FFN value), final LayerNorm and
@@ -535,6 +556,8 @@ int rwkv7_decode(const rwkv7_model *model, const rwkv7_state *state, const int64
     }
     return decode_one(*model, *state, tokens, logits, static_cast<char *>(workspace), st);
   }
+  if (use_rows_kernel(*model, state->batch, 1))
+    return run_rows(*model, *state, tokens, 1, logits, static_cast<char *>(workspace), st);
   return run_batched(*model, *state, tokens, 1, logits, static_cast<char *>(workspace), st);
 }
 
@@ -556,6 +579,9 @@ int rwkv7_prefill(const rwkv7_model *model, const rwkv7_state *state, const int6
   if (!tokens || !workspace) return RWKV7_EINVAL;
   if (seq_len < 1) return RWKV7_ESHAPE;
   if (workspace_bytes < rwkv7_workspace_bytes(&model->dims, state->batch, seq_len)) return RWKV7_EWORKSPACE;
+  if (use_rows_kernel(*model, state->batch, seq_len))
+    return run_rows(*model, *state, tokens, seq_len, nullptr, static_cast<char *>(workspace),
+                    static_cast<hipStream_t>(stream));
   return run_batched(*model, *state, tokens, seq_len, nullptr, static_cast<char *>(workspace),
                      static_cast<hipStream_t>(stream));
 }

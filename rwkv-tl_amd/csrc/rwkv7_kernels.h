@@ -174,4 +174,16 @@ int64_t mk_exchange_bytes(int C, int F, int SR);
 int launch_decode_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const rwkv7_state &s,
                      const int64_t *tok, void *logits, char *xreg, hipStream_t st);
 
+// A step of B sequences x T tokens with B T <= 16 (batched decode, short
+// prefills) as a single persistent kernel (rows_mk.hip). xreg: its exchange
+// region, rows_exchange_bytes(dims), zero before first use and only ever
+// touched by that kernel; errors: the workspace's aborted-launch counter.
+int64_t rows_exchange_bytes(const rwkv7_dims &d);
+// the model's formats and sizes are ones the kernel serves (half precision,
+// fragment arenas present, no multi-launch flag), B T <= 16, and its grid fits
+// on the current device at once
+bool rows_usable(const rwkv7_model &m, int B, int T);
+int launch_rows_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const rwkv7_state &s, const int64_t *tok,
+                   int T, void *logits, char *xreg, unsigned *errors, hipStream_t st);
+
 }  // namespace rwkv7

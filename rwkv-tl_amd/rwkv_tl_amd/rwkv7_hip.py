@@ -4,12 +4,15 @@ Stands in for ``RWKV7FP16`` / ``RWKV7Base`` (``demo/rwkv7_fp16.py:16-25``,
 ``demo/_rwkv7_base.py:33-310``). Every step is one call into
 ``librwkv7_hip.so``:
 
-* ``decode`` -> ``rwkv7_decode``: one sequence runs fused fp16 GEMV kernels
-  (LayerNorm and token shift folded into the projection prologues, LoRA +
-  gates + wkv7 + GroupNorm + output gate in one per-head kernel); several
-  sequences run the MFMA GEMM path with M = batch.
-* ``prefill`` -> ``rwkv7_prefill``: MFMA GEMMs for every projection and a
-  serial, LDS-staged wkv7 scan per head.
+* ``decode`` -> ``rwkv7_decode``: one sequence runs as a single persistent
+  kernel (GEMV dot products, grid-wide hand-offs between the stages of each
+  layer); 2..16 sequences as the few-row persistent kernel (MFMA on 16-row
+  weight blocks); more as the MFMA GEMM path with M = batch.
+* ``prefill`` -> ``rwkv7_prefill``: B x T <= 16 rows as the few-row kernel;
+  longer prompts as MFMA GEMMs for every projection and a serial, LDS-staged
+  wkv7 scan per head.
+
+``decode_path = "kernels"`` selects the multi-launch paths throughout.
 
 There is no CPU or torch fallback: without the library, construction raises.
 """
@@ -82,8 +85,9 @@ class RWKV7HIP(RWKV7Model):
 
     @property
     def decode_path(self) -> str:
-        """``"auto"`` (one persistent kernel per batch-1 step where the device
-        fits its grid) or ``"kernels"`` (the multi-launch GEMV path)."""
+        """``"auto"`` (one persistent kernel per step where the device fits its
+        grid: batch-1 decode, and batched decode / prefills of at most 16
+        rows) or ``"kernels"`` (the multi-launch GEMV and GEMM paths)."""
         return "kernels" if self.dev.desc.flags & _lib.MODEL_MULTI_LAUNCH_DECODE else "auto"
 
     @decode_path.setter
@@ -94,7 +98,7 @@ class RWKV7HIP(RWKV7Model):
         self.dev.desc.flags = flags | (_lib.MODEL_MULTI_LAUNCH_DECODE if path == "kernels" else 0)
 
     def last_error(self) -> int:
-        """Aborted persistent-decode launches on this model's workspace so far
+        """Aborted persistent-kernel launches on this model's workspace so far
         (synchronises the current stream). An aborted step wrote NaN logits and
         left the State with only the layers completed before the failure."""
         if self._ws is None:
