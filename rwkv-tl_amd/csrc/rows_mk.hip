@@ -167,111 +167,159 @@ struct RkLds {
   unsigned *fail, *ep, *last;
 };
 
-// LN statistics (mean, 1/std) of the M rows of xs, one wave per row; the
-// row's C <= 1024 values stay in registers (four float4 per lane) for the
-// two-pass variance.
+// LN statistics (mean, 1/std) of the M <= 16 rows of xs: 32 threads per row
+// (rows 2w and 2w + 1 on wave w), each holding C / 32 <= 32 of the row's
+// values in registers for the two-pass variance.
 RWKV7_DEV void row_stats(const RkLds &s, int M, int C) {
   const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int m = wv; m < M; m += kRW) {
-    const float *row = s.xs + m * C;
-    float4 v[4];
-    float acc = 0.f;
+  const int m = 2 * wv + (lane >> 5), l32 = lane & 31;
+  const bool live = m < M;
+  float4 v[8];
+  float acc = 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = 4 * lane + 256 * j;
-      v[j] = c < C ? *reinterpret_cast<const float4 *>(row + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-      acc += (v[j].x + v[j].y) + (v[j].z + v[j].w);
-    }
-    const float mean = wave_sum(acc) / (float)C;
-    float q = 0.f;
+  for (int j = 0; j < 8; ++j) {
+    const int c = 4 * l32 + 128 * j;
+    v[j] = live && c < C ? *reinterpret_cast<const float4 *>(s.xs + m * C + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    acc += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  }
+  acc = sum16(acc);
+  const float sum = lane < 32 ? lane_value(acc, 0) + lane_value(acc, 16) : lane_value(acc, 32) + lane_value(acc, 48);
+  const float mean = sum / (float)C;
+  float q = 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (4 * lane + 256 * j < C) {
-        const float d0 = v[j].x - mean, d1 = v[j].y - mean, d2 = v[j].z - mean, d3 = v[j].w - mean;
-        q += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
-      }
+  for (int j = 0; j < 8; ++j) {
+    if (4 * l32 + 128 * j < C) {
+      const float d0 = v[j].x - mean, d1 = v[j].y - mean, d2 = v[j].z - mean, d3 = v[j].w - mean;
+      q += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
     }
-    const float var = wave_sum(q) / (float)C;
-    if (lane == 0) {
-      s.stat[4 * m] = mean;
-      s.stat[4 * m + 1] = rsqrtf(var + kLnEps);
-    }
+  }
+  q = sum16(q);
+  const float sq = lane < 32 ? lane_value(q, 0) + lane_value(q, 16) : lane_value(q, 32) + lane_value(q, 48);
+  if (live && l32 == 0) {
+    s.stat[4 * m] = mean;
+    s.stat[4 * m + 1] = rsqrtf(sq / (float)C + kLnEps);
   }
 }
 
 // The B shift-state rows of a layer ([B][C] f16) into LDS (sst), eight
-// halves per load, up to four loads in flight per thread.
+// halves per load, by waves 1..7 (wave 0 polls; see load_block), up to five
+// loads in flight per thread.
 RWKV7_DEV void load_state(const RkLds &s, const uint16_t *state, int B, int C) {
+  if (threadIdx.x < 64) return;
+  const int tid = threadIdx.x - 64, nt = kRT - 64;
   const uint4 *src = reinterpret_cast<const uint4 *>(state);
   uint4 *dst = reinterpret_cast<uint4 *>(s.sst);
   const int n = B * C / 8;
-  for (int i0 = threadIdx.x; i0 < n; i0 += 4 * kRT) {
-    uint4 v[4];
+  for (int i0 = tid; i0 < n; i0 += 5 * nt) {
+    uint4 v[5];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = i0 + j * kRT < n ? src[i0 + j * kRT] : make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < 5; ++j) v[j] = i0 + j * nt < n ? src[i0 + j * nt] : make_uint4(0, 0, 0, 0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (i0 + j * kRT < n) dst[i0 + j * kRT] = v[j];
+    for (int j = 0; j < 5; ++j)
+      if (i0 + j * nt < n) dst[i0 + j * nt] = v[j];
   }
+}
+
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+// Two floats as packed halves, round to nearest even (v_cvt_pk_f16_f32; the
+// same bits as two single conversions).
+RWKV7_DEV unsigned pack_h2(float lo, float hi) {
+  return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2v{lo, hi}, f16x2v));
 }
 
 // A[m][k] = f16(ln(m) + mu[k] (prev(m) - ln(m))) for rows m < M, with ln(m) =
 // LayerNorm of row m and prev(m) = ln(m - 1) within a sequence, the f16 shift
-// state (sst) for its first token. Thread -> column pair (LN weight, bias and
-// mix loaded once, one packed store per row). Rows M..15 of A are left as they
-// are: they only reach output rows that are never stored.
-RWKV7_DEV void build_mix(const RkLds &s, const RkArgs &a, int C, const float *lw, const float *lb, const float *mu) {
+// state (sst) for its first token. Rows M..15 of A are left as they are: they
+// only reach output rows that are never stored. Thread -> 4 columns (LN
+// weight, bias and mix from load_mix, loaded before the stage's wait) and a
+// contiguous range of rows (the
+// kRT / (C / 4) thread groups split the rows; a range that starts inside a
+// sequence recomputes the LayerNorm of the row before it). Columns [c0, c1)
+// of each sequence's last LayerNorm row -- the new shift state -- also go to
+// shift_dst [B][C / 2] as f16 pairs.
+struct MixVec {
+  float4 w, b, u;  // LN weight, LN bias, mix of this thread's 4 columns
+};
+RWKV7_DEV MixVec load_mix(const float *lw, const float *lb, const float *mu, int C) {
+  const int k = 4 * (threadIdx.x % (C / 4));
+  MixVec v;
+  v.w = *reinterpret_cast<const float4 *>(lw + k);
+  v.b = *reinterpret_cast<const float4 *>(lb + k);
+  v.u = *reinterpret_cast<const float4 *>(mu + k);
+  return v;
+}
+
+RWKV7_DEV void build_mix(const RkLds &s, const RkArgs &a, int C, const MixVec &mv, unsigned *shift_dst, int c0, int c1) {
   const int M = a.M, T = a.T;
-  for (int k = 2 * threadIdx.x; k < C; k += 2 * kRT) {
-    const float2 w = *reinterpret_cast<const float2 *>(lw + k), bias = *reinterpret_cast<const float2 *>(lb + k);
-    const float2 u = *reinterpret_cast<const float2 *>(mu + k);
-    float p0 = 0.f, p1 = 0.f;
-    int t = 0, b = 0;
-    for (int m = 0; m < M; ++m) {
-      const float2 x = *reinterpret_cast<const float2 *>(s.xs + m * C + k);
-      const float mean = s.stat[4 * m], rs = s.stat[4 * m + 1];
-      const float l0 = (x.x - mean) * rs * w.x + bias.x, l1 = (x.y - mean) * rs * w.y + bias.y;
-      if (t == 0) {
-        const unsigned st = *reinterpret_cast<const unsigned *>(s.sst + b * C + k);
-        p0 = h2f((uint16_t)(st & 0xFFFFu));
-        p1 = h2f((uint16_t)(st >> 16));
-      }
-      const float v0 = l0 + u.x * (p0 - l0), v1 = l1 + u.y * (p1 - l1);
-      *reinterpret_cast<unsigned *>(s.A + m * kRLdA + k) = (unsigned)f2h(v0) | ((unsigned)f2h(v1) << 16);
-      p0 = l0;
-      p1 = l1;
-      if (++t == T) t = 0, ++b;
+  const int nq = C / 4, ng = kRT / nq;
+  const int q = threadIdx.x % nq, grp = threadIdx.x / nq;
+  if (grp >= ng) return;
+  const int rpg = (M + ng - 1) / ng;
+  const int m0 = grp * rpg, m1 = min(M, m0 + rpg);
+  if (m0 >= m1) return;
+  const int k = 4 * q;
+  const float4 w = mv.w, bias = mv.b, u = mv.u;
+  const bool shift_cols = k >= c0 && k < c1;
+  auto ln_row = [&](int m) {
+    const float4 x = *reinterpret_cast<const float4 *>(s.xs + m * C + k);
+    const float2 st = *reinterpret_cast<const float2 *>(s.stat + 4 * m);  // mean, 1/std
+    const float nm = -st.x * st.y;
+    return make_float4(fmaf(fmaf(x.x, st.y, nm), w.x, bias.x), fmaf(fmaf(x.y, st.y, nm), w.y, bias.y),
+                       fmaf(fmaf(x.z, st.y, nm), w.z, bias.z), fmaf(fmaf(x.w, st.y, nm), w.w, bias.w));
+  };
+  int t = m0 % T, b = m0 / T;
+  float4 p = t > 0 ? ln_row(m0 - 1) : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int m = m0; m < m1; ++m) {
+    const float4 ln = ln_row(m);
+    if (t == 0) {
+      const uint2 st = *reinterpret_cast<const uint2 *>(s.sst + b * C + k);
+      p = make_float4(h2f((uint16_t)(st.x & 0xFFFFu)), h2f((uint16_t)(st.x >> 16)), h2f((uint16_t)(st.y & 0xFFFFu)),
+                      h2f((uint16_t)(st.y >> 16)));
     }
+    const float v0 = fmaf(u.x, p.x - ln.x, ln.x), v1 = fmaf(u.y, p.y - ln.y, ln.y);
+    const float v2 = fmaf(u.z, p.z - ln.z, ln.z), v3 = fmaf(u.w, p.w - ln.w, ln.w);
+    *reinterpret_cast<uint2 *>(s.A + m * kRLdA + k) = make_uint2(pack_h2(v0, v1), pack_h2(v2, v3));
+    if (t == T - 1 && shift_cols) {
+      rst(shift_dst + (b * C + k) / 2, pack_h2(ln.x, ln.y));
+      rst(shift_dst + (b * C + k) / 2 + 1, pack_h2(ln.z, ln.w));
+    }
+    p = ln;
+    if (++t == T) t = 0, ++b;
   }
 }
 
-// The weights of one 16-row block for this wave: k-steps w, w + kRW, w + 2 kRW,
-// w + 3 kRW of the block's nks <= 4 kRW (fragment k-step k at wf + (k0step +
-// k) 512 halves). Loaded ahead of a stage's wait, used by block_mma after it.
+// The weights of one 16-row block, spread over waves 1..7 (wave 0 polls the
+// hand-off flags and issues no load before a wait: its poll results would
+// queue behind them): wave w >= 1 takes k-steps w - 1, w - 1 + 7, ... of the
+// block's nks <= 35 (fragment k-step k at wf + (k0step + k) 512 halves).
+// Loaded ahead of a stage's wait, used by block_mma after it.
+constexpr int kWW = kRW - 1;  // weight-loading waves
 struct WBlock {
-  uint4 w[4];
+  uint4 w[5];
 };
 RWKV7_DEV WBlock load_block(const uint16_t *wf, int k0step, int nks) {
   const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
   WBlock b;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int kj = wv + kRW * j;
-    b.w[j] = kj < nks ? ld_stream(reinterpret_cast<const uint4 *>(wf + (int64_t)(k0step + kj) * 512) + lane)
-                      : make_uint4(0, 0, 0, 0);
+  for (int j = 0; j < 5; ++j) {
+    const int kj = wv - 1 + kWW * j;
+    b.w[j] = wv > 0 && kj < nks ? ld_stream(reinterpret_cast<const uint4 *>(wf + (int64_t)(k0step + kj) * 512) + lane)
+                                : make_uint4(0, 0, 0, 0);
   }
   return b;
 }
 
 // The block times the A tile (A columns 32 k .. 32 k + 31 for k-step k).
-// Returns the wave's partial 16 x 16 tile, rows = A rows, columns = the
-// block's weight rows.
+// Returns the wave's partial 16 x 16 tile (zero on wave 0), rows = A rows,
+// columns = the block's weight rows.
 RWKV7_DEV floatx4 block_mma(const RkLds &s, const WBlock &wb, int nks) {
   const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
   floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+  if (wv == 0) return acc;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int kj = wv + kRW * j;
+  for (int j = 0; j < 5; ++j) {
+    const int kj = wv - 1 + kWW * j;
     if (kj < nks) {
       const uint4 af = *reinterpret_cast<const uint4 *>(&s.A[(lane & 15) * kRLdA + 32 * kj + 8 * (lane >> 4)]);
       acc = mfma16<false>(af, wb.w[j], acc);
@@ -362,24 +410,6 @@ RWKV7_DEV float residual_in(const RkArgs &a, int l, int m, int c) {
   return h2f(a.emb[clamp_tok(a.tok[m], a.V) * a.C + c]);
 }
 
-// The LayerNorm (lw, lb) of each sequence's last row of xs -- the new token
-// shift state -- as f16 pairs into dst [B][C / 2] (row statistics in stat);
-// thread -> column pair.
-RWKV7_DEV void store_shift(const RkLds &s, const RkArgs &a, const float *lw, const float *lb, unsigned *dst) {
-  const int C = a.C;
-  for (int k2 = threadIdx.x; k2 < C / 2; k2 += kRT) {
-    const int k = 2 * k2;
-    const float w0 = lw[k], w1 = lw[k + 1], b0 = lb[k], b1 = lb[k + 1];
-    for (int b = 0; b < a.B; ++b) {
-      const int m = b * a.T + a.T - 1;
-      const float mean = s.stat[4 * m], rs = s.stat[4 * m + 1];
-      const float l0 = (s.xs[m * C + k] - mean) * rs * w0 + b0;
-      const float l1 = (s.xs[m * C + k + 1] - mean) * rs * w1 + b1;
-      rst(dst + b * (C / 2) + k2, (unsigned)f2h(l0) | ((unsigned)f2h(l1) << 16));
-    }
-  }
-}
-
 // Copies a [B][C / 2] pair buffer into layer l of a state arena [L][B][C]
 // (eight loads in flight per thread).
 RWKV7_DEV void copy_shift(const RkArgs &a, const unsigned *src, uint16_t *arena, int l) {
@@ -426,35 +456,40 @@ RWKV7_DEV void p2_unit(const RkArgs &a, const RkLds &s, const RkCtx &cx, int l, 
   float *s_rk = s_g + 16 * 512;                                    // [T]
   const int ch = h * kN + lane;
   // loads that do not depend on this layer's hand-offs: the wkv state rows,
-  // the wave's LoRA second-step weight fragments and the channel's vectors
+  // the wave's LoRA second-step weight fragments and the channel's vectors --
+  // before the wait on waves 1..7, after it on wave 0 (the polling wave,
+  // whose poll results would queue behind them)
   float S[8];
   float4 *Sp = reinterpret_cast<float4 *>(a.rnn + ((((int64_t)l * a.B + b) * a.H + h) * kN + (t >> 3)) * kN + (t & 7) * 8);
-  {
-    const float4 u0 = Sp[0], u1 = Sp[1];
-    S[0] = u0.x, S[1] = u0.y, S[2] = u0.z, S[3] = u0.w, S[4] = u1.x, S[5] = u1.y, S[6] = u1.z, S[7] = u1.w;
-  }
   // wave w: (gate, channel tile) pairs w and w + 8: gate = pair >> 2, tile = pair & 3
   int goff[2], grank[2];
   uint4 wq[2][4];
+  float v_v0, v_w0, v_a0, v_kk, v_ka, v_rk, v_lw, v_lb;
+  auto prefetch = [&]() {
+    const float4 u0 = Sp[0], u1 = Sp[1];
+    S[0] = u0.x, S[1] = u0.y, S[2] = u0.z, S[3] = u0.w, S[4] = u1.x, S[5] = u1.y, S[6] = u1.z, S[7] = u1.w;
 #pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int q = (wv + kRW * e) >> 2, tile = (wv + kRW * e) & 3;
-    goff[e] = q == 0 ? 0 : q == 1 ? a.rv : q == 2 ? a.rv + a.rw : a.rv + a.rw + a.ra;
-    grank[e] = q == 0 ? a.rv : q == 1 ? a.rw : q == 2 ? a.ra : a.rg;
-    const uint16_t *wrow = l2 + (int64_t)(h * kN + 16 * tile + (lane & 15)) * SR + goff[e];
+    for (int e = 0; e < 2; ++e) {
+      const int q = (wv + kRW * e) >> 2, tile = (wv + kRW * e) & 3;
+      goff[e] = q == 0 ? 0 : q == 1 ? a.rv : q == 2 ? a.rv + a.rw : a.rv + a.rw + a.ra;
+      grank[e] = q == 0 ? a.rv : q == 1 ? a.rw : q == 2 ? a.ra : a.rg;
+      const uint16_t *wrow = l2 + (int64_t)(h * kN + 16 * tile + (lane & 15)) * SR + goff[e];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int k = 32 * ks + 8 * (lane >> 4);
-      wq[e][ks] = k < grank[e] ? *reinterpret_cast<const uint4 *>(wrow + k) : make_uint4(0, 0, 0, 0);
+      for (int ks = 0; ks < 4; ++ks) {
+        const int k = 32 * ks + 8 * (lane >> 4);
+        wq[e][ks] = k < grank[e] ? *reinterpret_cast<const uint4 *>(wrow + k) : make_uint4(0, 0, 0, 0);
+      }
     }
-  }
-  const float v_v0 = vec[RWKV7_V_V0 * C + ch], v_w0 = vec[RWKV7_V_W0 * C + ch], v_a0 = vec[RWKV7_V_A0 * C + ch];
-  const float v_kk = vec[RWKV7_V_K_K * C + ch], v_ka = vec[RWKV7_V_K_A * C + ch], v_rk = vec[RWKV7_V_R_K * C + ch];
-  const float v_lw = vec[RWKV7_V_LNX_W * C + ch], v_lb = vec[RWKV7_V_LNX_B * C + ch];
+    v_v0 = vec[RWKV7_V_V0 * C + ch], v_w0 = vec[RWKV7_V_W0 * C + ch], v_a0 = vec[RWKV7_V_A0 * C + ch];
+    v_kk = vec[RWKV7_V_K_K * C + ch], v_ka = vec[RWKV7_V_K_A * C + ch], v_rk = vec[RWKV7_V_R_K * C + ch];
+    v_lw = vec[RWKV7_V_LNX_W * C + ch], v_lb = vec[RWKV7_V_LNX_B * C + ch];
+  };
+  if (wv != 0) prefetch();
   // the P1 blocks this unit reads: r, k, v rows of head h and every LoRA block
   const int hb = h * (kN / 16), nl = SR / 16;
   auto blk = [&](int i) { return i < 12 ? (i / 4) * (C / 16) + hb + (i & 3) : 3 * C / 16 + (i - 12); };
   const bool ok = wait_flags(cx, a.fl[0], 12 + nl, cx.tag(l, 0), blk);
+  if (wv == 0) prefetch();
   // A1
   if (t < SR) {
     const float *col = a.proj + (int64_t)b * T * N1 + 3 * C + t;
@@ -639,20 +674,25 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
       const int64_t foff = sg < 3 ? a.f_rkv + (int64_t)b1 * nksC * 1024
                          : (sg == 3 ? a.f_l1[0] : sg == 4 ? a.f_l1[1] : sg == 5 ? a.f_l1[2] : a.f_l1[3]) +
                                (int64_t)((row0 - (sg == 3 ? e2 : sg == 4 ? e3 : sg == 5 ? e4 : e5)) / 16) * nksC * 1024;
+      // before the wait: weights and old shift states (waves 1..7), the mix
+      // vectors (wave 0 loads its own after the wait)
       const WBlock wb = load_block(reinterpret_cast<const uint16_t *>(Fp + foff), 0, nksC);
       load_state(s, a.tmix_x + (int64_t)l * a.B * C, a.B, C);
+      const float *lw1 = vec + RWKV7_V_LN1_W * C, *lb1 = vec + RWKV7_V_LN1_B * C, *mu1 = vec + mu * C;
+      MixVec mv{};
+      if (threadIdx.x >= 64) mv = load_mix(lw1, lb1, mu1, C);
       if (l == 0) {
         embed_rows(s, a);
       } else {
         wait_flags(cx, a.fl[4], nP5, cx.tag(l - 1, 4), ident);
         read_x(s, a.x, M, C);
       }
+      if (threadIdx.x < 64) mv = load_mix(lw1, lb1, mu1, C);
       __syncthreads();
       row_stats(s, M, C);
       __syncthreads();
-      build_mix(s, a, C, vec + RWKV7_V_LN1_W * C, vec + RWKV7_V_LN1_B * C, vec + mu * C);
-      if (g == 0 && b1 == 0)  // the new time-mix shift state
-        store_shift(s, a, vec + RWKV7_V_LN1_W * C, vec + RWKV7_V_LN1_B * C, a.sh1);
+      // blocks 0 .. C/16 - 1 also write 16 columns each of the new time-mix shift state
+      build_mix(s, a, C, mv, a.sh1, 16 * b1, b1 < nP3 ? 16 * b1 + 16 : 16 * b1);
       __syncthreads();
       const floatx4 acc = block_mma(s, wb, nksC);
       int m, n;
@@ -677,31 +717,35 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
     // ---------------- P3 ----------------
     for (int b3 = g; b3 < nP3; b3 += G) {
       const WBlock wb = load_block(reinterpret_cast<const uint16_t *>(Fp + a.f_o) + (int64_t)b3 * nksC * 512, 0, nksC);
-      // the residual of this thread's output (final since this workgroup's P1 wait)
+      // the residual of this thread's output (final since this workgroup's P1
+      // wait), loaded and stored by threads 256..511 (not the polling wave)
       const int t = threadIdx.x & 255;
       const int mr = 4 * ((t & 63) >> 4) + (t >> 6), cr = 16 * b3 + (t & 15);
-      const float res = mr < M ? residual_in(a, l, mr, cr) : 0.f;
+      const float res = threadIdx.x >= 256 && mr < M ? residual_in(a, l, mr, cr) : 0.f;
       wait_flags(cx, a.fl[1], nP2, cx.tag(l, 1), ident);
       read_pairs(s, a.core, C, 0, C, M);
       __syncthreads();
       const floatx4 acc = block_mma(s, wb, nksC);
       int m, n;
       const float v = reduce_tile(s, acc, &m, &n);
-      if (threadIdx.x < 256 && m < M && !cx.failed()) rst_f(a.x + (int64_t)m * C + 16 * b3 + n, res + v);
+      if (threadIdx.x >= 256 && m < M && !cx.failed()) rst_f(a.x + (int64_t)m * C + 16 * b3 + n, res + v);
       publish_flag(cx, a.fl[2] + b3, cx.tag(l, 2));
     }
     // ---------------- P4 ----------------
     for (int b4 = g; b4 < nP4; b4 += G) {
       const WBlock wb = load_block(reinterpret_cast<const uint16_t *>(Fp + a.f_fk) + (int64_t)b4 * nksC * 512, 0, nksC);
       load_state(s, a.cmix_x + (int64_t)l * a.B * C, a.B, C);
+      const float *lw2 = vec + RWKV7_V_LN2_W * C, *lb2 = vec + RWKV7_V_LN2_B * C, *mu2 = vec + RWKV7_V_FFN_X_K * C;
+      MixVec mv{};
+      if (threadIdx.x >= 64) mv = load_mix(lw2, lb2, mu2, C);
       wait_flags(cx, a.fl[2], nP3, cx.tag(l, 2), ident);
       read_x(s, a.x, M, C);
+      if (threadIdx.x < 64) mv = load_mix(lw2, lb2, mu2, C);
       __syncthreads();
       row_stats(s, M, C);
       __syncthreads();
-      build_mix(s, a, C, vec + RWKV7_V_LN2_W * C, vec + RWKV7_V_LN2_B * C, vec + RWKV7_V_FFN_X_K * C);
-      if (g == 0 && b4 == 0)  // the new channel-mix shift state
-        store_shift(s, a, vec + RWKV7_V_LN2_W * C, vec + RWKV7_V_LN2_B * C, a.sh2);
+      // blocks 0 .. C/16 - 1 also write 16 columns each of the new channel-mix shift state
+      build_mix(s, a, C, mv, a.sh2, 16 * b4, b4 < nP3 ? 16 * b4 + 16 : 16 * b4);
       __syncthreads();
       const floatx4 acc = block_mma(s, wb, nksC);
       int m, n;
@@ -784,7 +828,7 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
       for (int m = 0; m < B; ++m) {
         const float mean = s.stat[4 * m], rs = s.stat[4 * m + 1];
         const float v0 = (s.xs[m * C + k] - mean) * rs * w0 + b0, v1 = (s.xs[m * C + k + 1] - mean) * rs * w1 + b1;
-        *reinterpret_cast<unsigned *>(s.A + m * kRLdA + k) = (unsigned)f2h(v0) | ((unsigned)f2h(v1) << 16);
+        *reinterpret_cast<unsigned *>(s.A + m * kRLdA + k) = pack_h2(v0, v1);
       }
     }
     __syncthreads();
