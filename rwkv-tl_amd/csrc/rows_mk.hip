@@ -13,7 +13,9 @@
 //   P3  o-projection + residual                            C/16 blocks
 //   P4  LN2 + shift + FFN key + relu^2                     F/16 blocks
 //   P5  FFN value + residual                               C/16 blocks x 4
-//       K-quarters, the last quarter to arrive sums the four in order
+//       K-quarters; quarter 0 adds the other three's partial tiles, handed
+//       over as tagged words ({value, tag} as one 64-bit store / load, polled
+//       directly), in a fixed order
 // then (decode) LN_out and the head, V/16 blocks.
 //
 // Matrix stages run on MFMA (v_mfma_f32_16x16x32_f16): a block is 16 weight
@@ -78,12 +80,11 @@ struct RkArgs {
   int B, T, M, G;
   unsigned *sync, *started, *errors;
   unsigned *fl[5];   // per-stage flags: P1 blocks, P2 units, P3 blocks, P4 blocks, P5 blocks
-  unsigned *ctr5;    // P5 arrival counters, one per block (zero between launches)
   float *proj;       // [M, 3C + SR]
   unsigned *core;    // [M, C/2] f16 pairs
   float *x;          // [M, C]
   unsigned *hid;     // [M, F/2] f16 pairs
-  float *part5;      // [C/16, 4, 256]
+  uint64_t *part;    // [C/16, 4, 256] FFN-value partial tiles of K-quarters 1..3 (tagged words)
   float *vfirst;     // [M, C]
   unsigned *sh1, *sh2;  // [B, C / 2] the new shift states (f16 pairs)
 };
@@ -156,6 +157,52 @@ RWKV7_DEV void publish_flag(const RkCtx &cx, unsigned *flag, unsigned tag) {
   if (threadIdx.x == 0 && !cx.failed()) rst(flag, tag);
 }
 
+// Tagged words: a value and the tag of the (launch, layer, stage) that wrote
+// it, stored and loaded as one 64-bit device-scope access (single-copy
+// atomic), so a reader that sees the tag also sees the value.
+RWKV7_DEV void st64f(uint64_t *p, float v, unsigned tag) {
+  __hip_atomic_store(p, ((uint64_t)tag << 32) | __builtin_bit_cast(unsigned, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+RWKV7_DEV unsigned tag_of(uint64_t w) { return (unsigned)(w >> 32); }
+RWKV7_DEV float val_f(uint64_t w) { return __builtin_bit_cast(float, (unsigned)w); }
+typedef unsigned u32x2r __attribute__((ext_vector_type(2)));
+RWKV7_DEV uint64_t rld8(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  const u32x2r v = __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, /*sc1*/ 16);
+  return ((uint64_t)v[1] << 32) | v[0];
+}
+
+// N tagged words at byte offsets off(i) of r, each read again until its tag
+// equals `tag` (bounded like wait_flags; a thread that gives up raises the
+// abort word or follows another workgroup's).
+template <int N, typename Off>
+RWKV7_DEV void read_words(const RkCtx &cx, __amdgpu_buffer_rsrc_t r, unsigned tag, Off off, uint64_t (&w)[N]) {
+  unsigned pend = (1u << N) - 1u;
+#pragma unroll
+  for (int i = 0; i < N; ++i) w[i] = rld8(r, off(i));
+  int spins = 0;
+  for (;;) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (((pend >> i) & 1u) && tag_of(w[i]) == tag) pend &= ~(1u << i);
+    if (pend == 0 || cx.failed()) break;
+    ++spins;
+    if ((spins & 1023) == 0 && cx.aborted()) {
+      cx.give_up();
+      break;
+    }
+    if (spins > kRSpin) {
+      rst(cx.sync + RS_ABORT, cx.epoch + 1u);
+      cx.give_up();
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if ((pend >> i) & 1u) w[i] = rld8(r, off(i));
+  }
+}
+
 struct RkLds {
   float *xs;        // [M][C] the stage's input rows (f32)
   uint16_t *A;      // [16][kRLdA] the MFMA A operand (f16)
@@ -164,7 +211,7 @@ struct RkLds {
   float *u;         // P2 scratch
   uint16_t *sst;    // [16][C] the layer's old shift states (f16)
   int *tok;         // [16] embedding row offsets of the step's tokens
-  unsigned *fail, *ep, *last;
+  unsigned *fail, *ep;
 };
 
 // LN statistics (mean, 1/std) of the M <= 16 rows of xs: 32 threads per row
@@ -632,7 +679,6 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
   s.stat = s.red + kRW * 256;
   s.fail = reinterpret_cast<unsigned *>(s.stat + 64);
   s.ep = s.fail + 1;
-  s.last = s.fail + 2;
   s.tok = reinterpret_cast<int *>(s.fail + 16);
   s.sst = reinterpret_cast<uint16_t *>(s.fail + 32);
   s.u = s.xs;  // P2 scratch: the input rows and the A tile (contiguous)
@@ -776,27 +822,23 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
       const floatx4 acc = block_mma(s, wb, nksQ);
       int m, n;
       const float v = reduce_tile(s, acc, &m, &n);
-      // split-K hand-off: the partial tile out, then the arrival count
-      float *pb = a.part5 + ((int64_t)b5 * 4 + q) * 256;
-      if (threadIdx.x < 256) rst_f(pb + threadIdx.x, v);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        const unsigned old = __hip_atomic_fetch_add(a.ctr5 + b5, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *s.last = old == 3u;
-        if (old == 3u) rst(a.ctr5 + b5, 0u);
-      }
-      __syncthreads();
-      if (*s.last) {
+      // split-K hand-off: quarters 1..3 store their partial tiles as tagged
+      // words and go on; quarter 0 reads them (each word re-read until it
+      // carries this layer's tag), adds them in the order 0, 1, 2, 3 and the
+      // residual, and publishes the block
+      if (q != 0) {
+        if (threadIdx.x < 256 && !cx.failed()) st64f(a.part + ((int64_t)b5 * 4 + q) * 256 + threadIdx.x, v, cx.tag(l, 4));
+        __syncthreads();
+      } else {
         if (threadIdx.x < 256 && m < M && !cx.failed()) {
-          float p[4];
-#pragma unroll
-          for (int qq = 0; qq < 4; ++qq) p[qq] = rld_f(a.part5 + ((int64_t)b5 * 4 + qq) * 256 + threadIdx.x);
-          rst_f(a.x + (int64_t)m * C + 16 * b5 + n, res + (((p[0] + p[1]) + p[2]) + p[3]));
+          const __amdgpu_buffer_rsrc_t rq = rrsrc(a.part + (int64_t)b5 * 4 * 256, 4 * 256 * 8);
+          uint64_t pw[3];
+          read_words<3>(cx, rq, cx.tag(l, 4), [](int i) { return 8 * ((1 + i) * 256 + (int)threadIdx.x); }, pw);
+          const float sum = ((v + val_f(pw[0])) + val_f(pw[1])) + val_f(pw[2]);
+          if (!cx.failed()) rst_f(a.x + (int64_t)m * C + 16 * b5 + n, res + sum);
         }
         publish_flag(cx, a.fl[4] + b5, cx.tag(l, 4));
       }
-      __syncthreads();
     }
   }
   // ---------------- the channel-mix state of the last layer, the head ----------------
@@ -882,12 +924,11 @@ int64_t rows_exchange_bytes(const rwkv7_dims &d) {
   auto al = [](int64_t x) { return (x + 255) & ~int64_t(255); };
   int64_t o = kRSyncBytes + al(4 * kRMaxG);
   o += al(4 * ((3 * C + SR) / 16)) + al(4 * 16 * H) + al(4 * (C / 16)) + al(4 * (F / 16)) + al(4 * (C / 16));
-  o += al(4 * (C / 16));              // ctr5
   o += al(M * (3 * C + SR) * 4);      // proj
   o += al(M * C * 2);                 // core
   o += al(M * C * 4);                 // x
   o += al(M * F * 2);                 // hid
-  o += al((C / 16) * 4 * 256 * 4);    // part5
+  o += al((C / 16) * 4 * 256 * 8);    // part
   o += al(M * C * 4);                 // vfirst
   o += 2 * al(M * C * 2);             // sh1, sh2
   return o;
@@ -979,8 +1020,6 @@ int launch_rows_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const rw
     a.fl[i] = reinterpret_cast<unsigned *>(p);
     p += al(4 * nfl[i]);
   }
-  a.ctr5 = reinterpret_cast<unsigned *>(p);
-  p += al(4 * (C / 16));
   a.proj = reinterpret_cast<float *>(p);
   p += al(M * (3 * C + SR) * 4);
   a.core = reinterpret_cast<unsigned *>(p);
@@ -989,8 +1028,8 @@ int launch_rows_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const rw
   p += al(M * C * 4);
   a.hid = reinterpret_cast<unsigned *>(p);
   p += al(M * F * 2);
-  a.part5 = reinterpret_cast<float *>(p);
-  p += al((C / 16) * 4 * 256 * 4);
+  a.part = reinterpret_cast<uint64_t *>(p);
+  p += al((C / 16) * 4 * 256 * 8);
   a.vfirst = reinterpret_cast<float *>(p);
   p += al(M * C * 4);
   a.sh1 = reinterpret_cast<unsigned *>(p);
