@@ -80,7 +80,7 @@ struct RkArgs {
   int B, T, M, G;
   unsigned *sync, *started, *errors;
   unsigned *fl[5];   // per-stage flags: P1 blocks, P2 units, P3 blocks, P4 blocks, P5 blocks
-  float *proj;       // [M, 3C + SR]
+  uint64_t *proj;    // [M, 3C + SR] f32 as tagged words
   unsigned *core;    // [M, C/2] f16 pairs
   float *x;          // [M, C]
   unsigned *hid;     // [M, F/2] f16 pairs
@@ -531,45 +531,90 @@ RWKV7_DEV void p2_unit(const RkArgs &a, const RkLds &s, const RkCtx &cx, int l, 
     v_kk = vec[RWKV7_V_K_K * C + ch], v_ka = vec[RWKV7_V_K_A * C + ch], v_rk = vec[RWKV7_V_R_K * C + ch];
     v_lw = vec[RWKV7_V_LNX_W * C + ch], v_lb = vec[RWKV7_V_LNX_B * C + ch];
   };
-  if (wv != 0) prefetch();
-  // the P1 blocks this unit reads: r, k, v rows of head h and every LoRA block
-  const int hb = h * (kN / 16), nl = SR / 16;
-  auto blk = [&](int i) { return i < 12 ? (i / 4) * (C / 16) + hb + (i & 3) : 3 * C / 16 + (i - 12); };
-  const bool ok = wait_flags(cx, a.fl[0], 12 + nl, cx.tag(l, 0), blk);
-  if (wv == 0) prefetch();
-  // A1
-  if (t < SR) {
-    const float *col = a.proj + (int64_t)b * T * N1 + 3 * C + t;
-    float xl[16];
+  prefetch();
+  // A1: the P1 outputs of this unit, tagged words (each read again until it
+  // carries this layer's P1 tag), all in flight at once: the LoRA first steps
+  // as 16-byte chunks (columns j, j + 1 of token m; chunk i = t + kRT c,
+  // c < 5: T SR / 2 <= 5 kRT), then r, k, v of the wave's tokens
+  float pr[2], pk[2], pv[2], pf[2];
+  {
+    const __amdgpu_buffer_rsrc_t rp = rrsrc(a.proj + (int64_t)b * T * N1, (int64_t)T * N1 * 8);
+    const int cpt = SR / 2, nch = T * cpt;
+    const unsigned tg = cx.tag(l, 0);
+    auto coff = [&](int c) {
+      const int i = t + kRT * c, m = i / cpt;
+      return 8 * (m * N1 + 3 * C + 2 * (i - m * cpt));
+    };
+    auto woff = [&](int i) { return 8 * ((wv + kRW * (i / 3)) * N1 + (i % 3) * C + ch); };
+    u32x4r ck[5];
+    uint64_t w[6];
+    unsigned pend = 0;
 #pragma unroll
-    for (int m = 0; m < 16; ++m) xl[m] = m < T ? rld_f(col + (int64_t)m * N1) : 0.f;
-    const bool is_w = t >= a.rv && t < a.rv + a.rw, is_g = t >= a.rv + a.rw + a.ra;
-#pragma unroll
-    for (int m = 0; m < 16; ++m) {
-      if (m < T) {
-        float x = xl[m];
-        if (is_w) x = tanhf(x);
-        else if (is_g) x = sigmoidf_(x);
-        s_l16[m * kLoraLd + t] = f2h(x);
+    for (int c = 0; c < 5; ++c)
+      if (t + kRT * c < nch) {
+        ck[c] = rld16(rp, coff(c));
+        pend |= 1u << c;
       }
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      w[i] = 0;
+      if (wv + kRW * (i / 3) < T) {
+        w[i] = rld8(rp, woff(i));
+        pend |= 32u << i;
+      }
+    }
+    int spins = 0;
+    for (;;) {
+#pragma unroll
+      for (int c = 0; c < 5; ++c) {
+        if (((pend >> c) & 1u) && ck[c][1] == tg && ck[c][3] == tg) {
+          pend &= ~(1u << c);
+          const int i = t + kRT * c, m = i / cpt, j = 2 * (i - m * cpt);
+          // (the elements go through scalars: a bit cast of an ext-vector
+          // element lvalue reads element 0 in this compiler)
+          const unsigned u0 = ck[c][0], u1 = ck[c][2];
+          float x0 = __builtin_bit_cast(float, u0), x1 = __builtin_bit_cast(float, u1);
+          // tanh on the w group, sigmoid on the g group (j and j + 1 share a group: ranks are even)
+          if (j >= a.rv && j < a.rv + a.rw) x0 = tanhf(x0), x1 = tanhf(x1);
+          else if (j >= a.rv + a.rw + a.ra) x0 = sigmoidf_(x0), x1 = sigmoidf_(x1);
+          *reinterpret_cast<unsigned *>(&s_l16[m * kLoraLd + j]) = pack_h2(x0, x1);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 6; ++i)
+        if (((pend >> (5 + i)) & 1u) && tag_of(w[i]) == tg) pend &= ~(32u << i);
+      if (pend == 0 || cx.failed()) break;
+      ++spins;
+      if ((spins & 1023) == 0 && cx.aborted()) {
+        cx.give_up();
+        break;
+      }
+      if (spins > kRSpin) {
+        rst(cx.sync + RS_ABORT, cx.epoch + 1u);
+        cx.give_up();
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int c = 0; c < 5; ++c)
+        if ((pend >> c) & 1u) ck[c] = rld16(rp, coff(c));
+#pragma unroll
+      for (int i = 0; i < 6; ++i)
+        if ((pend >> (5 + i)) & 1u) w[i] = rld8(rp, woff(i));
+    }
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      pr[e] = val_f(w[3 * e]);
+      pk[e] = val_f(w[3 * e + 1]);
+      pv[e] = val_f(w[3 * e + 2]);
+      const int m = wv + kRW * e;
+      pf[e] = l > 0 && m < T ? rld_f(a.vfirst + (int64_t)(b * T + m) * C + ch) : 0.f;
     }
   }
   if (t < 32)  // the zero tail past the last group (a partial k-step of a rank-16 group reads into it)
     for (int m = 0; m < T; ++m) s_l16[m * kLoraLd + SR + t] = 0;
-  float pr[2], pk[2], pv[2], pf[2];
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int m = wv + kRW * e;
-    pr[e] = pk[e] = pv[e] = pf[e] = 0.f;
-    if (m < T) {
-      const float *prow = a.proj + (int64_t)(b * T + m) * N1;
-      pr[e] = rld_f(prow + ch);
-      pk[e] = rld_f(prow + C + ch);
-      pv[e] = rld_f(prow + 2 * C + ch);
-      if (l > 0) pf[e] = rld_f(a.vfirst + (int64_t)(b * T + m) * C + ch);
-    }
-  }
   __syncthreads();
+  const bool ok = !cx.failed();
 #pragma unroll
   for (int e = 0; e < 2; ++e) {  // A2
     const int q = (wv + kRW * e) >> 2, tile = (wv + kRW * e) & 3;
@@ -743,8 +788,8 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
       const floatx4 acc = block_mma(s, wb, nksC);
       int m, n;
       const float v = reduce_tile(s, acc, &m, &n);
-      if (threadIdx.x < 256 && m < M && !cx.failed()) rst_f(a.proj + (int64_t)m * N1 + row0 + n, v);
-      publish_flag(cx, a.fl[0] + b1, cx.tag(l, 0));
+      if (threadIdx.x < 256 && m < M && !cx.failed()) st64f(a.proj + (int64_t)m * N1 + row0 + n, v, cx.tag(l, 0));
+      __syncthreads();
     }
     // ---------------- P2 ----------------
     for (int u = g; u < nP2; u += G) {
@@ -924,7 +969,7 @@ int64_t rows_exchange_bytes(const rwkv7_dims &d) {
   auto al = [](int64_t x) { return (x + 255) & ~int64_t(255); };
   int64_t o = kRSyncBytes + al(4 * kRMaxG);
   o += al(4 * ((3 * C + SR) / 16)) + al(4 * 16 * H) + al(4 * (C / 16)) + al(4 * (F / 16)) + al(4 * (C / 16));
-  o += al(M * (3 * C + SR) * 4);      // proj
+  o += al(M * (3 * C + SR) * 8);      // proj
   o += al(M * C * 2);                 // core
   o += al(M * C * 4);                 // x
   o += al(M * F * 2);                 // hid
@@ -943,7 +988,7 @@ static bool rows_supported(const rwkv7_model &m, int B, int T) {
   const int r[4] = {d.rank_v, d.rank_w, d.rank_a, d.rank_g};
   for (int x : r)
     if (x % 16 || x > 128) return false;  // 16-row P1 blocks; P2 holds at most four k-steps per gate
-  if (d.rank_w + d.rank_a + d.rank_v + d.rank_g > 512) return false;  // P2 LoRA staging
+  if (d.rank_w + d.rank_a + d.rank_v + d.rank_g > 320) return false;  // P2 reads 16 x SR / 2 <= 5 kRT chunks
   const int G = mk_cus();
   return G >= 1 && G <= kRMaxG;
 }
@@ -1020,8 +1065,8 @@ int launch_rows_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const rw
     a.fl[i] = reinterpret_cast<unsigned *>(p);
     p += al(4 * nfl[i]);
   }
-  a.proj = reinterpret_cast<float *>(p);
-  p += al(M * (3 * C + SR) * 4);
+  a.proj = reinterpret_cast<uint64_t *>(p);
+  p += al(M * (3 * C + SR) * 8);
   a.core = reinterpret_cast<unsigned *>(p);
   p += al(M * C * 2);
   a.x = reinterpret_cast<float *>(p);
