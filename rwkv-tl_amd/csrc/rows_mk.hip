@@ -86,7 +86,6 @@ struct RkArgs {
   unsigned *hid;     // [M, F/2] f16 pairs
   uint64_t *part;    // [C/16, 4, 256] FFN-value partial tiles of K-quarters 1..3 (tagged words)
   float *vfirst;     // [M, C]
-  unsigned *sh1, *sh2;  // [B, C / 2] the new shift states (f16 pairs)
 };
 
 RWKV7_DEV unsigned rld(const unsigned *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
@@ -211,6 +210,7 @@ struct RkLds {
   float *u;         // P2 scratch
   uint16_t *sst;    // [16][C] the layer's old shift states (f16)
   int *tok;         // [16] embedding row offsets of the step's tokens
+  uint16_t *shs1, *shs2;  // [16][16] this workgroup's 16 columns of the new time-/channel-mix shift states
   unsigned *fail, *ep;
 };
 
@@ -280,11 +280,10 @@ RWKV7_DEV unsigned pack_h2(float lo, float hi) {
 // state (sst) for its first token. Rows M..15 of A are left as they are: they
 // only reach output rows that are never stored. Thread -> 4 columns (LN
 // weight, bias and mix from load_mix, loaded before the stage's wait) and a
-// contiguous range of rows (the
-// kRT / (C / 4) thread groups split the rows; a range that starts inside a
-// sequence recomputes the LayerNorm of the row before it). Columns [c0, c1)
-// of each sequence's last LayerNorm row -- the new shift state -- also go to
-// shift_dst [B][C / 2] as f16 pairs.
+// contiguous range of rows (the kRT / (C / 4) thread groups split the rows; a
+// range that starts inside a sequence recomputes the LayerNorm of the row
+// before it). With c0 >= 0, columns [c0, c0 + 16) of each sequence's last
+// LayerNorm row -- the new shift state -- also go to slice ([B][16] f16, LDS).
 struct MixVec {
   float4 w, b, u;  // LN weight, LN bias, mix of this thread's 4 columns
 };
@@ -297,7 +296,7 @@ RWKV7_DEV MixVec load_mix(const float *lw, const float *lb, const float *mu, int
   return v;
 }
 
-RWKV7_DEV void build_mix(const RkLds &s, const RkArgs &a, int C, const MixVec &mv, unsigned *shift_dst, int c0, int c1) {
+RWKV7_DEV void build_mix(const RkLds &s, const RkArgs &a, int C, const MixVec &mv, uint16_t *slice, int c0) {
   const int M = a.M, T = a.T;
   const int nq = C / 4, ng = kRT / nq;
   const int q = threadIdx.x % nq, grp = threadIdx.x / nq;
@@ -307,7 +306,7 @@ RWKV7_DEV void build_mix(const RkLds &s, const RkArgs &a, int C, const MixVec &m
   if (m0 >= m1) return;
   const int k = 4 * q;
   const float4 w = mv.w, bias = mv.b, u = mv.u;
-  const bool shift_cols = k >= c0 && k < c1;
+  const bool shift_cols = c0 >= 0 && k >= c0 && k < c0 + 16;
   auto ln_row = [&](int m) {
     const float4 x = *reinterpret_cast<const float4 *>(s.xs + m * C + k);
     const float2 st = *reinterpret_cast<const float2 *>(s.stat + 4 * m);  // mean, 1/std
@@ -327,10 +326,8 @@ RWKV7_DEV void build_mix(const RkLds &s, const RkArgs &a, int C, const MixVec &m
     const float v0 = fmaf(u.x, p.x - ln.x, ln.x), v1 = fmaf(u.y, p.y - ln.y, ln.y);
     const float v2 = fmaf(u.z, p.z - ln.z, ln.z), v3 = fmaf(u.w, p.w - ln.w, ln.w);
     *reinterpret_cast<uint2 *>(s.A + m * kRLdA + k) = make_uint2(pack_h2(v0, v1), pack_h2(v2, v3));
-    if (t == T - 1 && shift_cols) {
-      rst(shift_dst + (b * C + k) / 2, pack_h2(ln.x, ln.y));
-      rst(shift_dst + (b * C + k) / 2 + 1, pack_h2(ln.z, ln.w));
-    }
+    if (t == T - 1 && shift_cols)
+      *reinterpret_cast<uint2 *>(slice + b * 16 + (k - c0)) = make_uint2(pack_h2(ln.x, ln.y), pack_h2(ln.z, ln.w));
     p = ln;
     if (++t == T) t = 0, ++b;
   }
@@ -457,18 +454,13 @@ RWKV7_DEV float residual_in(const RkArgs &a, int l, int m, int c) {
   return h2f(a.emb[clamp_tok(a.tok[m], a.V) * a.C + c]);
 }
 
-// Copies a [B][C / 2] pair buffer into layer l of a state arena [L][B][C]
-// (eight loads in flight per thread).
-RWKV7_DEV void copy_shift(const RkArgs &a, const unsigned *src, uint16_t *arena, int l) {
-  unsigned *dst = reinterpret_cast<unsigned *>(arena) + (int64_t)l * a.B * a.C / 2;
-  const int n = a.B * a.C / 2;
-  for (int i0 = threadIdx.x; i0 < n; i0 += 8 * kRT) {
-    unsigned v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = i0 + j * kRT < n ? rld(src + i0 + j * kRT) : 0u;
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (i0 + j * kRT < n) dst[i0 + j * kRT] = v[j];
+// This workgroup's 16-column slice of a new shift state (LDS [B][16] f16,
+// from build_mix) into columns [c0, c0 + 16) of layer l of a state arena.
+RWKV7_DEV void store_shift_slice(const RkArgs &a, const uint16_t *slice, uint16_t *arena, int l, int c0) {
+  if ((int)threadIdx.x < a.B * 8) {
+    const int b = threadIdx.x >> 3, c = 2 * (threadIdx.x & 7);
+    *reinterpret_cast<unsigned *>(arena + ((int64_t)l * a.B + b) * a.C + c0 + c) =
+        *reinterpret_cast<const unsigned *>(slice + b * 16 + c);
   }
 }
 
@@ -725,7 +717,9 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
   s.fail = reinterpret_cast<unsigned *>(s.stat + 64);
   s.ep = s.fail + 1;
   s.tok = reinterpret_cast<int *>(s.fail + 16);
-  s.sst = reinterpret_cast<uint16_t *>(s.fail + 32);
+  s.shs1 = reinterpret_cast<uint16_t *>(s.fail + 32);
+  s.shs2 = s.shs1 + 256;
+  s.sst = s.shs2 + 256;
   s.u = s.xs;  // P2 scratch: the input rows and the A tile (contiguous)
   if (threadIdx.x == 0) {
     const unsigned e = rld(a.sync + RS_EPOCH);
@@ -745,10 +739,13 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
   const int nksC = C / 32, nksF = F / 32, nksQ = F / 128;  // k-steps: K = C, the fv strip, a quarter
   // P1 row segments r, k, v, then the LoRA first steps v, w, a, g (ends e0..e5, N1)
   const int e0 = C, e1 = 2 * C, e2 = 3 * C, e3 = e2 + a.rv, e4 = e3 + a.rw, e5 = e4 + a.ra;
-  // the workgroup that moves the new shift states into the State arenas once
-  // their old values are no longer read (one with no o-projection block when
-  // the grid has such a workgroup)
-  const int gcopy = G - 1 >= nP3 ? G - 1 : 0;
+  // Workgroup g < C/16 keeps columns [16 g, 16 g + 16) of the new shift states
+  // in LDS and stores them into the State once no workgroup reads the old
+  // values any more: the time-mix state of layer l after its P4 wait (every
+  // o-projection block read every (sequence, head) unit's output, and every
+  // unit read its P1 blocks), the channel-mix state of layer l after the P1
+  // wait of layer l + 1 (or the last wait).
+  const bool slice_owner = g < nP3;
   auto ident = [](int i) { return i; };
 
   for (int l = 0; l < L; ++l) {
@@ -780,10 +777,12 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
       }
       if (threadIdx.x < 64) mv = load_mix(lw1, lb1, mu1, C);
       __syncthreads();
+      // the channel-mix state of the last layer (every FFN-value block of it has published)
+      if (l > 0 && b1 == g && slice_owner && !cx.failed()) store_shift_slice(a, s.shs2, a.cmix_x, l - 1, 16 * g);
       row_stats(s, M, C);
       __syncthreads();
       // blocks 0 .. C/16 - 1 also write 16 columns each of the new time-mix shift state
-      build_mix(s, a, C, mv, a.sh1, 16 * b1, b1 < nP3 ? 16 * b1 + 16 : 16 * b1);
+      build_mix(s, a, C, mv, s.shs1, b1 == g && slice_owner ? 16 * g : -1);
       __syncthreads();
       const floatx4 acc = block_mma(s, wb, nksC);
       int m, n;
@@ -801,10 +800,7 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
     // Once every (sequence, head) unit has published, every P1 block of this
     // layer has been read, so no workgroup reads the old time-mix state of
     // this layer (P1) or the old channel-mix state of the last one (P4) again.
-    if (g == gcopy && wait_flags(cx, a.fl[1], nP2, cx.tag(l, 1), ident)) {
-      copy_shift(a, a.sh1, a.tmix_x, l);
-      if (l > 0) copy_shift(a, a.sh2, a.cmix_x, l - 1);
-    }
+
     // ---------------- P3 ----------------
     for (int b3 = g; b3 < nP3; b3 += G) {
       const WBlock wb = load_block(reinterpret_cast<const uint16_t *>(Fp + a.f_o) + (int64_t)b3 * nksC * 512, 0, nksC);
@@ -833,10 +829,12 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
       read_x(s, a.x, M, C);
       if (threadIdx.x < 64) mv = load_mix(lw2, lb2, mu2, C);
       __syncthreads();
+      // the time-mix state of this layer (every o-projection block has published)
+      if (b4 == g && slice_owner && !cx.failed()) store_shift_slice(a, s.shs1, a.tmix_x, l, 16 * g);
       row_stats(s, M, C);
       __syncthreads();
       // blocks 0 .. C/16 - 1 also write 16 columns each of the new channel-mix shift state
-      build_mix(s, a, C, mv, a.sh2, 16 * b4, b4 < nP3 ? 16 * b4 + 16 : 16 * b4);
+      build_mix(s, a, C, mv, s.shs2, b4 == g && slice_owner ? 16 * g : -1);
       __syncthreads();
       const floatx4 acc = block_mma(s, wb, nksC);
       int m, n;
@@ -890,7 +888,7 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
   const int nb = a.logits ? a.V / 16 : 0;
   WBlock wb = g < nb ? load_block(a.head_frag + (int64_t)g * nksC * 512, 0, nksC) : WBlock{};
   const bool done = wait_flags(cx, a.fl[4], nP5, cx.tag(L - 1, 4), ident);
-  if (g == gcopy && done) copy_shift(a, a.sh2, a.cmix_x, L - 1);
+  if (slice_owner && done) store_shift_slice(a, s.shs2, a.cmix_x, L - 1, 16 * g);
   if (a.logits) {
     const int B = a.B, T = a.T;
     // LN_out of each sequence's last token into A rows 0..B-1
@@ -954,7 +952,9 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
   }
 }
 
-constexpr int64_t rows_lds_bytes() { return 16 * kRMaxC * 4 + 16 * kRLdA * 2 + kRW * 256 * 4 + 64 * 4 + 128 + 16 * kRMaxC * 2; }
+constexpr int64_t rows_lds_bytes() {
+  return 16 * kRMaxC * 4 + 16 * kRLdA * 2 + kRW * 256 * 4 + 64 * 4 + 128 + 2 * 256 * 2 + 16 * kRMaxC * 2;
+}
 
 // Per device, checked once with that device current: 1 when the kernel's
 // dynamic LDS is allowed and a grid of one workgroup per CU fits at once, -1
@@ -975,7 +975,6 @@ int64_t rows_exchange_bytes(const rwkv7_dims &d) {
   o += al(M * F * 2);                 // hid
   o += al((C / 16) * 4 * 256 * 8);    // part
   o += al(M * C * 4);                 // vfirst
-  o += 2 * al(M * C * 2);             // sh1, sh2
   return o;
 }
 
@@ -990,7 +989,7 @@ static bool rows_supported(const rwkv7_model &m, int B, int T) {
     if (x % 16 || x > 128) return false;  // 16-row P1 blocks; P2 holds at most four k-steps per gate
   if (d.rank_w + d.rank_a + d.rank_v + d.rank_g > 320) return false;  // P2 reads 16 x SR / 2 <= 5 kRT chunks
   const int G = mk_cus();
-  return G >= 1 && G <= kRMaxG;
+  return G >= C / 16 && G <= kRMaxG;  // workgroup g < C/16 owns P1 and P4 block g
 }
 
 // The dynamic LDS is allowed and the grid of one workgroup per CU fits at once
@@ -1077,9 +1076,6 @@ int launch_rows_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const rw
   p += al((C / 16) * 4 * 256 * 8);
   a.vfirst = reinterpret_cast<float *>(p);
   p += al(M * C * 4);
-  a.sh1 = reinterpret_cast<unsigned *>(p);
-  p += al(M * C * 2);
-  a.sh2 = reinterpret_cast<unsigned *>(p);
   a.errors = errors;
   rows_mk_kernel<<<a.G, kRT, rows_lds_bytes(), st>>>(a);
   RWKV7_CHECK_LAUNCH();
