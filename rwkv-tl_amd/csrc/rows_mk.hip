@@ -23,17 +23,23 @@
 // operand is the M activation rows (padded to 16) staged in LDS as f16, and
 // the 8 waves of the workgroup split K and sum their 16 x 16 tiles in LDS.
 //
-// Hand-offs: the producer of a block writes its payload (M rows x 16 values)
-// with device-scope (sc1) stores, waits until they are acknowledged
-// (s_waitcnt vmcnt(0)), then a workgroup barrier, then stores the block's flag
-// word = the stage's tag; a consumer polls the flags it needs with
-// device-scope loads and then reads the payload with device-scope loads. This
-// relies on the gfx942/gfx950 behaviour the split-K GEMM relies on: a store
-// issued with sc1 is acknowledged only once it reached the device's coherence
-// point beyond every XCD's L2, and sc1 loads are not served from a stale L2
-// line. Tags are unique per (launch, layer, stage); a buffer is rewritten only
-// after every reader of its previous contents has published a later stage
-// that the writer waited for.
+// Hand-offs. P2 -> P3, P3 -> P4, P4 -> P5 and P5 -> next P1 (the residual
+// rows x, the per-head outputs, the FFN hidden rows): the producer of a block
+// writes its payload with device-scope (sc1) stores, waits until they are
+// acknowledged (s_waitcnt vmcnt(0)), then a workgroup barrier, then stores the
+// block's flag word = the stage's tag; a consumer polls the flags it needs
+// with device-scope loads and then reads the payload with device-scope loads.
+// This relies on the gfx942/gfx950 behaviour the split-K GEMM relies on: a
+// store issued with sc1 is acknowledged only once it reached the device's
+// coherence point beyond every XCD's L2, and sc1 loads are not served from a
+// stale L2 line. P1 -> P2 (the projections, small per reader) and the P5
+// partial tiles: tagged words, {value, tag} stored and loaded as one 64-bit
+// device-scope access (single-copy atomic), which the consumer polls directly
+// -- no acknowledgement wait, flag or separate read; measured, this pays for
+// small payloads but not for the 32-64 KB ones, whose reads it doubles. Tags
+// are unique per (launch, layer, stage); a buffer is rewritten only after
+// every reader of its previous contents has published a later stage that the
+// writer waited for.
 //
 // Every wait is bounded; past the spin limit the waiting workgroup raises the
 // launch's abort word, every other waiter gives up within a few polls, and the
@@ -79,7 +85,7 @@ struct RkArgs {
   uint16_t *logits;  // [B, V] or null
   int B, T, M, G;
   unsigned *sync, *started, *errors;
-  unsigned *fl[5];   // per-stage flags: P1 blocks, P2 units, P3 blocks, P4 blocks, P5 blocks
+  unsigned *fl[5];   // per-stage flags: P2 units, P3 blocks, P4 blocks, P5 blocks (fl[0] unused: P1 hands off tagged words)
   uint64_t *proj;    // [M, 3C + SR] f32 as tagged words
   unsigned *core;    // [M, C/2] f16 pairs
   float *x;          // [M, C]
@@ -968,7 +974,7 @@ int64_t rows_exchange_bytes(const rwkv7_dims &d) {
   const int64_t M = 16;
   auto al = [](int64_t x) { return (x + 255) & ~int64_t(255); };
   int64_t o = kRSyncBytes + al(4 * kRMaxG);
-  o += al(4 * ((3 * C + SR) / 16)) + al(4 * 16 * H) + al(4 * (C / 16)) + al(4 * (F / 16)) + al(4 * (C / 16));
+  o += al(4 * 16 * H) + al(4 * (C / 16)) + al(4 * (F / 16)) + al(4 * (C / 16));
   o += al(M * (3 * C + SR) * 8);      // proj
   o += al(M * C * 2);                 // core
   o += al(M * C * 4);                 // x
@@ -1059,7 +1065,7 @@ int launch_rows_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const rw
   p += kRSyncBytes;
   a.started = reinterpret_cast<unsigned *>(p);
   p += al(4 * kRMaxG);
-  const int64_t nfl[5] = {(3 * C + SR) / 16, 16 * H, C / 16, F / 16, C / 16};
+  const int64_t nfl[5] = {0, 16 * H, C / 16, F / 16, C / 16};
   for (int i = 0; i < 5; ++i) {
     a.fl[i] = reinterpret_cast<unsigned *>(p);
     p += al(4 * nfl[i]);
