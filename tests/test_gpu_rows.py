@@ -141,3 +141,58 @@ def test_rows_kernel_declines_what_it_does_not_serve(cuda):
     model.decode_path = "kernels"
     assert model.decode_launches(16) > 1
     model.decode_path = "auto"
+
+
+def _rows_sync_offset(d) -> int:
+    """Byte offset of the few-row kernel's sync words in the workspace: after
+    the batch-1 kernel's exchange region (sync and start words, then 8
+    replicas of x, proj, core and hid as 8-byte words) and the GEMM split-K
+    counters, each rounded up to 256 bytes. The test checks it against the
+    epoch word before using it."""
+    al = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    C, F = d.n_embd, d.n_ffn
+    SR = d.rank_w + d.rank_a + d.rank_v + d.rank_g
+    mk = 256 + 4 * 1024 + (8 * C + 8 * (3 * C + SR) + 8 * C + 8 * F) * 8
+    return al(mk) + al(1024 * 4)
+
+
+def test_rows_kernel_abort_is_visible(cuda):
+    """The few-row kernel's abort word is set from the host for the next
+    launch, so every bounded wait gives up at once and every workgroup exits
+    normally: NaN logits, the State unchanged, the launch counted in the
+    workspace's error word; the next step runs normally and matches the
+    oracle."""
+    w, model, ref_w = _setup("tiny", cuda)
+    model.decode_path = "auto"
+    B = 4
+    if model.decode_launches(B) != 1:
+        pytest.skip("the few-row kernel does not fit this device")
+    V = w.head.shape[0]
+    g = torch.Generator().manual_seed(44)
+    toks = torch.randint(0, V, (3, B), generator=g)
+    S = State(w.L, w.C, 64, device=cuda, batch=B)
+    ref = R.new_state(w.L, w.C, dtype=torch.float16, batch=B)
+    ws = model.workspace(B, 1)
+    off = _rows_sync_offset(model.dev.dims)
+    words = ws[off:off + 64].view(torch.int32)
+    torch.cuda.synchronize()
+    e0 = int(words[0].item())
+    _, S = model.decode(toks[0].to(cuda), S)
+    _, ref = R.decode(ref_w, toks[0], ref)
+    torch.cuda.synchronize()
+    epoch = int(words[0].item())
+    assert epoch == e0 + 1, "the epoch word did not advance: wrong offset"
+    errs0 = model.last_error()
+    before = [a.clone() for a in S.arenas]
+    words[4] = epoch + 1  # abort word (byte 16) = this launch's epoch + 1
+    lg, S = model.decode(toks[1].to(cuda), S)
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(lg.float()).all()), "aborted launch must write NaN logits"
+    for a, b in zip(S.arenas, before):
+        assert torch.equal(a, b), "aborted launch must leave the State unchanged"
+    assert model.last_error() == errs0 + 1
+    lg, S = model.decode(toks[2].to(cuda), S)
+    l32, ref = R.decode(ref_w, toks[2], ref)
+    for b in range(B):
+        _check_logits(lg[b], l32[b], f"row {b} after an aborted launch")
+    assert model.last_error() == errs0 + 1
