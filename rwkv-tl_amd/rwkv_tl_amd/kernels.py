@@ -47,7 +47,8 @@ def _need(cond: bool, msg: str) -> None:
 
 def _dev(*ts: Tensor) -> None:
     for t in ts:
-        _need(t.device.type == "cuda", f"tensor on {t.device}; the HIP kernels need a ROCm device")
+        if t.device.type != "cuda":
+            raise ValueError(f"tensor on {t.device}; the HIP kernels need a ROCm device")
         _need(t.is_contiguous(), "tensors must be contiguous")
 
 
@@ -58,9 +59,11 @@ def _h16(*ts: Tensor) -> int:
     """All float16 or all bfloat16 (on the device); returns the kernels' bf16 flag."""
     _dev(*ts)
     dt = ts[0].dtype
-    _need(dt in _H16, f"expected float16 or bfloat16, got {dt}")
+    if dt not in _H16:
+        raise ValueError(f"expected float16 or bfloat16, got {dt}")
     for t in ts:
-        _need(t.dtype == dt, f"mixed 16-bit dtypes: {dt} and {t.dtype}")
+        if t.dtype != dt:
+            raise ValueError(f"mixed 16-bit dtypes: {dt} and {t.dtype}")
     return int(dt == torch.bfloat16)
 
 
@@ -77,7 +80,8 @@ def wkv7(S: Tensor, r: Tensor, w: Tensor, k: Tensor, v: Tensor, a: Tensor, b: Te
     T = r.shape[1]
     bf = _h16(r, k, v, a, b)
     for name, t in (("k", k), ("v", v), ("a", a), ("b", b)):
-        _need(t.shape == r.shape, f"{name} must be {tuple(r.shape)}")
+        if t.shape != r.shape:
+            raise ValueError(f"{name} must be {tuple(r.shape)}")
     _need(w.shape == r.shape and w.dtype in (r.dtype, torch.float32), "w must be like r, or f32")
     y = torch.empty_like(r)
     lib = _lib.load()
@@ -94,7 +98,8 @@ def _wkv7_f32_shapes(S: Tensor, r: Tensor, *rest: Tensor) -> tuple[int, int, int
     Bsz, H = S.shape[:2]
     _need(r.dim() == 4 and r.shape[0] == Bsz and r.shape[2] == H and r.shape[3] == N, "r must be [B,T,H,64]")
     for t in (r, *rest):
-        _need(t.shape == r.shape and t.dtype == torch.float32, f"inputs must be f32 {tuple(r.shape)}")
+        if not (t.shape == r.shape and t.dtype == torch.float32):
+            raise ValueError(f"inputs must be f32 {tuple(r.shape)}")
     return Bsz, r.shape[1], H
 
 
@@ -288,8 +293,10 @@ def gemv_any4(x: Tensor, codes: Tensor, lut: Tensor) -> Tensor:
     _dev(x, codes, lut)
     _need(codes.dtype == torch.uint8 and codes.dim() == 2, "codes must be uint8 [N, K/2]")
     N, K = codes.shape[0], 2 * codes.shape[1]
-    _need(lut.dtype == torch.float16 and lut.shape == (N, 16), f"lut must be f16 [{N}, 16]")
-    _need(x.dtype == torch.float32 and x.shape == (K,), f"x must be f32 [{K}]")
+    if not (lut.dtype == torch.float16 and lut.shape == (N, 16)):
+        raise ValueError(f"lut must be f16 [{N}, 16]")
+    if not (x.dtype == torch.float32 and x.shape == (K,)):
+        raise ValueError(f"x must be f32 [{K}]")
     y = torch.empty(N, dtype=torch.float32, device=x.device)
     lib = _lib.load()
     rc = lib.rwkv7_gemv_any4(x.data_ptr(), codes.data_ptr(), codes.stride(0), lut.data_ptr(), y.data_ptr(), N, K,
@@ -346,7 +353,8 @@ def fused_lerp6_rkv_copy(x, prev, x_r, x_w, x_k, x_v, x_a, x_g, x_copy, rWt_stac
 def _vecs(C: int, *ts: Tensor) -> int:
     bf = _h16(*ts)
     for t in ts:
-        _need(t.numel() == C, f"expected {C} elements, got shape {tuple(t.shape)}")
+        if t.numel() != C:
+            raise ValueError(f"expected {C} elements, got shape {tuple(t.shape)}")
     return bf
 
 
@@ -393,7 +401,8 @@ def fused_gates(vr: Tensor, wr: Tensor, ar: Tensor, gr: Tensor, v: Tensor, v_fir
     _need(_h16(v, vr, wr, ar, gr, v2t, w2t, a2t, g2t) == bf, "one 16-bit dtype for every operand")
     ranks = []
     for r_, m_ in ((vr, v2t), (wr, w2t), (ar, a2t), (gr, g2t)):
-        _need(m_.dim() == 2 and m_.shape == (C, r_.numel()), f"rank matrix {tuple(m_.shape)} vs [{C}, {r_.numel()}]")
+        if not (m_.dim() == 2 and m_.shape == (C, r_.numel())):
+            raise ValueError(f"rank matrix {tuple(m_.shape)} vs [{C}, {r_.numel()}]")
         ranks.append(r_.numel())
     outs = [torch.empty_like(v) for _ in range(6)]
     io = _lib.GatesIO(*(t.data_ptr() for t in (vr, wr, ar, gr, v2t, w2t, a2t, g2t, v, v_first, k, v0, w0, a0,
@@ -408,7 +417,8 @@ def fused_rank_gemv(xv: Tensor, xw: Tensor, xa: Tensor, xg: Tensor, packed: Tens
     C = xv.numel()
     bf = _vecs(C, xv, xw, xa, xg)
     _need(_h16(xv, packed) == bf, "one 16-bit dtype for every operand")
-    _need(packed.shape == (rv + rw + ra + rg, C), f"packed {tuple(packed.shape)} vs [{rv + rw + ra + rg}, {C}]")
+    if not (packed.shape == (rv + rw + ra + rg, C)):
+        raise ValueError(f"packed {tuple(packed.shape)} vs [{rv + rw + ra + rg}, {C}]")
     out = torch.empty(rv + rw + ra + rg, dtype=xv.dtype, device=xv.device)
     _lib.check(_lib.load().rwkv7_rank_gemv(xv.data_ptr(), xw.data_ptr(), xa.data_ptr(), xg.data_ptr(),
                                            packed.data_ptr(), out.data_ptr(), rv, rw, ra, rg, C, bf,
