@@ -289,23 +289,36 @@ def bench_configs() -> dict:
     a, b = (-kh).half().to(dev), (kh * alpha).half().to(dev)
     S0 = (torch.randn(B, H, N, N, generator=g) * 0.1).to(dev)
     S = S0.clone()
+    K.wkv7(S, r, w, k, v, a, b)  # first call: device properties, library load
     op_ms = time_cuda(lambda: K.wkv7(S, r, w, k, v, a, b), 20)
-    # the same launch through the C ABI with the arguments prepared once: the
+    # the same launches through the C ABI with the arguments prepared once: the
     # operator's host-side checks and allocation (tens of microseconds of
     # Python per call) no longer leave the GPU idle between launches
     lib = _lib.load()
     y = torch.empty_like(r)
     args = (S.data_ptr(), r.data_ptr(), w.data_ptr(), 1, k.data_ptr(), v.data_ptr(), a.data_ptr(), b.data_ptr(),
-            y.data_ptr(), B, T, H, 0, _lib.stream_handle())
-    _lib.check(lib.rwkv7_wkv7(*args), "rwkv7_wkv7")
-    ms = time_cuda(lambda: lib.rwkv7_wkv7(*args), 50)
+            y.data_ptr(), B, T, H, 0)
+    st = _lib.stream_handle()
+    nb = int(lib.rwkv7_wkv7_chunked_workspace_bytes(B, T, H))
+    ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+    chunked = lambda: lib.rwkv7_wkv7_chunked(*args, ws.data_ptr(), nb, st)  # noqa: E731
+    serial = lambda: lib.rwkv7_wkv7(*args, st)  # noqa: E731
+    _lib.check(chunked(), "rwkv7_wkv7_chunked")
+    _lib.check(serial(), "rwkv7_wkv7")
+    chunked_ms = time_cuda(chunked, 50)
+    serial_ms = time_cuda(serial, 50)
+    # the algorithm kernels.wkv7 picks for this shape
+    ms = chunked_ms if T >= K.CHUNK_MIN_T and 4 * B * H < K._cus(dev) else serial_ms
     c2_bytes = B * T * H * N * (5 * 2 + 4 + 2) + 2 * 4 * B * H * N * N
-    out["C2_wkv7_B8_H16_T128"] = {"ms": round(ms, 4), "op_ms": round(op_ms, 4),
+    out["C2_wkv7_B8_H16_T128"] = {"ms": round(ms, 4), "serial_ms": round(serial_ms, 4),
+                                  "chunked_ms": round(chunked_ms, 4), "op_ms": round(op_ms, 4),
                                   **_fracs(c2_bytes, 9.0 * N * N * B * T * H, ms),
-                                  "note": "ms: back-to-back C-ABI launches; op_ms: through kernels.wkv7 "
-                                          "(host checks included); FLOPs are VALU work (9 N^2 per head "
-                                          "per token), not MFMA"}
-    log(f"C2 wkv7: {ms:.4f} ms per launch, {op_ms:.4f} ms per operator call")
+                                  "note": "ms: back-to-back C-ABI launches of the algorithm the operator "
+                                          "picks for this shape; serial_ms / chunked_ms: rwkv7_wkv7 / "
+                                          "rwkv7_wkv7_chunked; op_ms: through kernels.wkv7 (host checks "
+                                          "included); FLOPs are the serial recurrence's VALU count "
+                                          "(9 N^2 per head per token)"}
+    log(f"C2 wkv7: serial {serial_ms:.4f} ms, chunked {chunked_ms:.4f} ms per launch, {op_ms:.4f} ms per operator call")
 
     def model_for(name: str):
         sd = make_random_state_dict(name, seed=0, dtype=torch.float16)

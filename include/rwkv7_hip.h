@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define RWKV7_ABI_VERSION 9
+#define RWKV7_ABI_VERSION 10
 #define RWKV7_HEAD_SIZE 64
 
 enum {
@@ -245,6 +245,21 @@ int rwkv7_prefill(const rwkv7_model *model, const rwkv7_state *state,
 int rwkv7_wkv7(float *S, const void *r, const void *w, int32_t w_is_f32,
                const void *k, const void *v, const void *a, const void *b,
                void *y, int32_t B, int32_t T, int32_t H, int32_t bf16, void *stream);
+
+/* rwkv7_wkv7 by the chunked algorithm: 16-token chunks whose transfer
+ * matrices are formed on fp32 MFMA, all chunks at once, then one pass per
+ * head that carries the state across the chunks. Same arguments and results
+ * (to fp32 rounding; the state within 1e-5 relative of the serial scan at the
+ * survey's C2 sizes), plus a device workspace of at least
+ * rwkv7_wkv7_chunked_workspace_bytes(B, T, H) bytes (28,928 per 16 tokens of
+ * each sequence and head). The chunked form of fused_dplr_T
+ * (src/rwkv_tl/kernels/dplr.py:272-285), which the reference runs as a
+ * chunked scan (dplr.py:174-227). */
+int64_t rwkv7_wkv7_chunked_workspace_bytes(int32_t B, int32_t T, int32_t H);
+int rwkv7_wkv7_chunked(float *S, const void *r, const void *w, int32_t w_is_f32,
+                       const void *k, const void *v, const void *a, const void *b,
+                       void *y, int32_t B, int32_t T, int32_t H, int32_t bf16,
+                       void *workspace, int64_t workspace_bytes, void *stream);
 
 /* The same recurrence with every operand f32 (S, r, w, k, v, a, b, y), for
  * training. When hist != NULL it receives the state entering each step, f32

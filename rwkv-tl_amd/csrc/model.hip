@@ -135,6 +135,7 @@ struct BatchWs {
   float *proj1;  // one-token steps: r, k, v, raw LoRA first steps [M, 3C+SR]
   uint16_t *xmix, *l1, *yg, *hid, *headin;
   float *U, *Send, *Pend;  // segmented scan of long sequences (null with one segment)
+  float *rec;              // chunk records of the chunked scan (prefill_chunked)
 };
 static int64_t batch_ws(const rwkv7_dims &d, int64_t B, int64_t T, char *base, BatchWs *w) {
   const int64_t C = d.n_embd, F = d.n_ffn, SR = sum_ranks(d), M = B * T;
@@ -161,8 +162,10 @@ static int64_t batch_ws(const rwkv7_dims &d, int64_t B, int64_t T, char *base, B
   t.part = reinterpret_cast<float *>(take(gemm_ws_bytes((int)(M > B ? M : B), cus)));
   int seg_len;
   const int64_t nseg = prefill_segments((int)T, (int)B, d.n_head, cus, &seg_len);
-  t.U = t.Send = t.Pend = nullptr;
-  if (nseg > 1) {
+  t.U = t.Send = t.Pend = t.rec = nullptr;
+  if (prefill_chunked((int)T, (int)B, d.n_head, cus)) {
+    t.rec = reinterpret_cast<float *>(take(wkv7_chunk_rec_bytes((int)B, (int)T, d.n_head)));
+  } else if (nseg > 1) {
     const int64_t slab = nseg * B * d.n_head * (int64_t)RWKV7_HEAD_SIZE * RWKV7_HEAD_SIZE * 4;
     t.U = reinterpret_cast<float *>(take(M * C * 4));
     t.Send = reinterpret_cast<float *>(take(slab));
@@ -420,7 +423,7 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
     for (int g = 0; g < 4; ++g) frag(g2[g], lay.f_l2[g], 0);
     RWKV7_TRY(gemm(g2, 4, M));
     PrefillScanArgs sc = {rnn, w.rkv, w.d, vec, w.vfirst, w.y, w.kv, w.kv + MC, B, T, H, C, M, l == 0,
-                          w.U, w.Send, w.Pend};
+                          w.U, w.Send, w.Pend, w.rec};
     RWKV7_TRY(launch_wkv7_prefill(sc, st));
     GnGateArgs gn = {w.y, w.rkv, w.kv, w.kv + MC, w.d + 3 * MC, vec, w.yg, C, M};
     gn.bf = bf;
@@ -586,33 +589,59 @@ int rwkv7_prefill(const rwkv7_model *model, const rwkv7_state *state, const int6
                      static_cast<hipStream_t>(stream));
 }
 
-int rwkv7_wkv7(float *S, const void *r, const void *w, int32_t w_is_f32, const void *k, const void *v,
-               const void *a, const void *b, void *y, int32_t B, int32_t T, int32_t H, int32_t bf16,
-               void *stream) {
-  if (!S || !r || !w || !k || !v || !a || !b || !y) return RWKV7_EINVAL;
-  if (B < 1 || T < 1 || H < 1) return RWKV7_ESHAPE;
-  hipStream_t st = static_cast<hipStream_t>(stream);
+// The scan instance for the operand formats of an operator-level call: 16-bit
+// r, k, v, a, b (half or bfloat16), w 16-bit or f32, y in r's format.
+extern "C++" template <class Run>
+static int wkv7_dispatch(float *S, const void *r, const void *w, int32_t w_is_f32, const void *k, const void *v,
+                         const void *a, const void *b, void *y, int32_t B, int32_t T, int32_t H, int32_t bf16,
+                         Run run) {
   if (bf16) {
     auto bp = [](const void *q) { return static_cast<const bf16_t *>(q); };
     bf16_t *yb = static_cast<bf16_t *>(y);
     if (w_is_f32) {
       ScanArgs<bf16_t, float, bf16_t> p = {S, bp(r), bp(k), bp(v), bp(a), bp(b), static_cast<const float *>(w),
                                            yb, B, T, H};
-      return launch_wkv7_scan(p, st);
+      return run(p);
     }
     ScanArgs<bf16_t, bf16_t, bf16_t> p = {S, bp(r), bp(k), bp(v), bp(a), bp(b), bp(w), yb, B, T, H};
-    return launch_wkv7_scan(p, st);
+    return run(p);
   }
-  const uint16_t *r16 = static_cast<const uint16_t *>(r), *k16 = static_cast<const uint16_t *>(k),
-                 *v16 = static_cast<const uint16_t *>(v), *a16 = static_cast<const uint16_t *>(a),
-                 *b16 = static_cast<const uint16_t *>(b);
+  auto hp = [](const void *q) { return static_cast<const uint16_t *>(q); };
   uint16_t *y16 = static_cast<uint16_t *>(y);
   if (w_is_f32) {
-    ScanArgs<uint16_t, float, uint16_t> p = {S, r16, k16, v16, a16, b16, static_cast<const float *>(w), y16, B, T, H};
-    return launch_wkv7_scan(p, st);
+    ScanArgs<uint16_t, float, uint16_t> p = {S, hp(r), hp(k), hp(v), hp(a), hp(b), static_cast<const float *>(w),
+                                             y16, B, T, H};
+    return run(p);
   }
-  ScanArgs<uint16_t, uint16_t, uint16_t> p = {S, r16, k16, v16, a16, b16, static_cast<const uint16_t *>(w), y16, B, T, H};
-  return launch_wkv7_scan(p, st);
+  ScanArgs<uint16_t, uint16_t, uint16_t> p = {S, hp(r), hp(k), hp(v), hp(a), hp(b), hp(w), y16, B, T, H};
+  return run(p);
+}
+
+int rwkv7_wkv7(float *S, const void *r, const void *w, int32_t w_is_f32, const void *k, const void *v,
+               const void *a, const void *b, void *y, int32_t B, int32_t T, int32_t H, int32_t bf16,
+               void *stream) {
+  if (!S || !r || !w || !k || !v || !a || !b || !y) return RWKV7_EINVAL;
+  if (B < 1 || T < 1 || H < 1) return RWKV7_ESHAPE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return wkv7_dispatch(S, r, w, w_is_f32, k, v, a, b, y, B, T, H, bf16,
+                       [&](const auto &p) { return launch_wkv7_scan(p, st); });
+}
+
+int64_t rwkv7_wkv7_chunked_workspace_bytes(int32_t B, int32_t T, int32_t H) {
+  if (B < 1 || T < 1 || H < 1) return 0;
+  return wkv7_chunk_rec_bytes(B, T, H);
+}
+
+int rwkv7_wkv7_chunked(float *S, const void *r, const void *w, int32_t w_is_f32, const void *k, const void *v,
+                       const void *a, const void *b, void *y, int32_t B, int32_t T, int32_t H, int32_t bf16,
+                       void *workspace, int64_t workspace_bytes, void *stream) {
+  if (!S || !r || !w || !k || !v || !a || !b || !y || !workspace) return RWKV7_EINVAL;
+  if (B < 1 || T < 1 || H < 1) return RWKV7_ESHAPE;
+  if (workspace_bytes < wkv7_chunk_rec_bytes(B, T, H)) return RWKV7_EWORKSPACE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float *rec = static_cast<float *>(workspace);
+  return wkv7_dispatch(S, r, w, w_is_f32, k, v, a, b, y, B, T, H, bf16,
+                       [&](const auto &p) { return launch_wkv7_chunked(p, rec, st); });
 }
 
 int rwkv7_wkv7_f32(float *S, const float *r, const float *w, const float *k, const float *v, const float *a,

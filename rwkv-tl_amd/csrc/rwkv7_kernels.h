@@ -104,9 +104,25 @@ struct PrefillScanArgs {
   float *vfirst, *y, *kn_out, *v_out;
   int B, T, H, C, M, layer0;
   float *U, *Send, *Pend;
+  // chunk records of the chunked scan (wkv7_chunk_rec_bytes), read when
+  // prefill_chunked(T, B, H, cus)
+  float *rec;
 };
 int prefill_segments(int T, int B, int H, int cus, int *seg_len);
 int launch_wkv7_prefill(const PrefillScanArgs &p, hipStream_t st);
+
+// Chunked wkv7 (16-token chunks on fp32 MFMA, tmix.hip): bytes of the chunk
+// records for B sequences of T tokens and H heads, and the operator-level
+// launch (the same arguments as launch_wkv7_scan, no state history).
+// prefill_chunked: the model's prefill takes the chunked scan -- sequences of
+// at least kChunkMinT tokens whose serial scan (4 H B workgroups) would leave
+// CUs idle (measured on MI355X: 1 x 128 and 1 x 512 at 0.4B faster, 8 x 16
+// heads x 128 tokens and 4 x 32 x 1024 slower than the serial scan).
+constexpr int kChunkMinT = 128;
+bool prefill_chunked(int T, int B, int H, int cus);
+int64_t wkv7_chunk_rec_bytes(int B, int T, int H);
+template <typename TI, typename TW, typename TY>
+int launch_wkv7_chunked(const ScanArgs<TI, TW, TY> &p, float *rec, hipStream_t st);
 
 struct GnGateArgs {
   const float *y, *r, *kn, *v, *g, *vec;

@@ -167,7 +167,8 @@ RWKV7_DEV float4 ld4_as_f(const bf16_t *p) {
 //     each token (demo/rwkv7_torch.py:203-224) from the projections -- every
 //     workgroup computes all 64 channels of its head (the L2 norm of kk needs
 //     them all) and writes the gated k and the mixed v of its 16 channels (and
-//     v itself on layer 0) for the GroupNorm stage;
+//     v itself on layer 0) for the GroupNorm stage (all 64 when constructed
+//     with quarter -1, as the chunked kernels below do);
 //   * RawStager (the operator-level rwkv7_wkv7): the inputs as given.
 //
 // Step loop: sa = S a is a 16-lane DPP sum; S w + v k is formed while it runs,
@@ -266,7 +267,7 @@ struct GateStager {
     dst[4][st_tok][q] = g_r;
     dst[5][st_tok][q] = make_float4(v[0], v[1], v[2], v[3]);
     // this workgroup's 16 channels of the values GroupNorm needs
-    if (tt < t1 && (q >> 2) == quarter) {
+    if (tt < t1 && (quarter < 0 || (q >> 2) == quarter)) {
       const int64_t o = base + (int64_t)tt * C + 4 * q;
       *reinterpret_cast<float4 *>(p.kn_out + o) = make_float4(kn[0], kn[1], kn[2], kn[3]);
       *reinterpret_cast<float4 *>(p.v_out + o) = make_float4(v[0], v[1], v[2], v[3]);
@@ -716,11 +717,356 @@ int prefill_segments(int T, int B, int H, int cus, int *seg_len) {
   return (T + L - 1) / L;
 }
 
+// ---------------------------------------------------------------------------
+// Chunked wkv7 on fp32 MFMA (the model's prefill at T >= kChunkMinT, and
+// rwkv7_wkv7_chunked). Over a chunk of L = 16 tokens entered with state S0,
+// with D(s, t] = prod_{m=s+1..t} diag(w_m) over the key channels (D(t, t] =
+// I) and s = -1 standing for "before the chunk", the recurrence unrolls to
+//   S_t   = S0 D(-1, t] + sum_{s<=t} (sig_s b_s^T + v_s k_s^T) D(s, t]
+//   sig_t = S_{t-1} a_t
+// which is linear in S0. With tokens as rows (Sig, V, U, Y0: 16 x 64 value
+// channels; A~, R~, B^, K^, G1, G2: 16 x 64 key channels):
+//   Sig = G1 S0^T + U,   G1 = T A~,   U = T Aka V,   T = (I - Aba)^-1
+//   Y   = G2 S0^T + Y0,  G2 = R~ + Bbr G1,   Y0 = Bbr U + Bkr V
+//   S16 = S0 diag(gam) + Sig^T B^ + V^T K^
+// where a~_t = a_t D(-1, t-1], r~_t = r_t D(-1, t], b^_s = b_s D(s, 15],
+// k^_s = k_s D(s, 15], gam = D(-1, 15], and the 16 x 16 token matrices are
+//   Aba[t][s] = b_s^T D(s, t-1] a_t,  Aka[t][s] = k_s^T D(s, t-1] a_t  (s < t)
+//   Bbr[t][s] = b_s^T D(s, t] r_t,    Bkr[t][s] = k_s^T D(s, t] r_t    (s <= t).
+// Two kernels:
+// 1. wkv7_chunk_prep_kernel, one workgroup per (chunk, head, sequence), all at
+//    once: stages the chunk through the serial scan's staging policies, forms
+//    the token matrices -- on MFMA as (a~)(b / P_s)^T etc. with the prefix
+//    products P_t = D(-1, t] when every P_t of the chunk lies in [1e-30,
+//    1e30], otherwise straight from products of w -- solves for T by forward
+//    substitution, and writes G1, G2, B^, K^, U, Y0, V and gam as a chunk
+//    record laid out in the chain kernel's MFMA operand order.
+// 2. wkv7_chunk_chain_kernel, grid (4 H, B): each workgroup carries 16 value
+//    rows of a head's state through the chunks in order; per chunk, Sig and Y
+//    from S (16 x 64 by 64 x 16), then S <- S diag(gam) + Sig^T B^ + V^T K^.
+//    Four waves, one 16-column block of the state each; the Sig and Y
+//    partials of the blocks are summed through LDS in block order.
+// A chunk past the end of the sequence is padded with identity steps (w = 1,
+// a = b = k = r = v = 0), whose outputs are not stored.
+// ---------------------------------------------------------------------------
+constexpr int kCk = 16;
+// Chunk record (f32). G1, G2, B^, K^: [wave][lane][kk]; U, V: [quarter][lane][kk];
+// Y0: [quarter][t][i]; gam: [64]. The chain kernel's lane l of wave w (rows
+// 16 q .. of the state) reads element kk of [w or q][l] as its operand of the
+// kk-th MFMA step.
+constexpr int kRecG1 = 0, kRecG2 = 1024, kRecBh = 2048, kRecKh = 3072, kRecU = 4096, kRecY0 = 5120,
+              kRecV = 6144, kRecGam = 7168, kRecFloats = 7232;
+constexpr int kPad = kN + 1;  // a padded 64-channel LDS row
+
+bool prefill_chunked(int T, int B, int H, int cus) { return T >= kChunkMinT && 4 * B * H < cus; }
+
+int64_t wkv7_chunk_rec_bytes(int B, int T, int H) {
+  return (int64_t)((T + kCk - 1) / kCk) * H * B * kRecFloats * 4;
+}
+
+// D (16 x 16) += A (16 x 4) B (4 x 16), f32: lane l gives A[l % 16][l / 16]
+// and B[l / 16][l % 16] and holds D[4 (l / 16) + r][l % 16], r = 0..3.
+RWKV7_DEV floatx4 mfma4(float a, float b, floatx4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+
+template <class St>
+__global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(typename St::Args p, float *rec, int T, int H) {
+  __shared__ StageBuf<kCk> s_stage;  // the stager's output; then AkaV, G1, U, G2, Y0
+  __shared__ float s_x[6][kCk][kPad];  // w, a (a~), b (b / P), k (k / P), r (r~), v
+  __shared__ float s_bh[kCk][kPad], s_kh[kCk][kPad];
+  __shared__ float s_m[4][kCk][kCk + 1];  // Aba, Aka, Bbr, Bkr
+  __shared__ float s_t[kCk][kCk + 1];
+  __shared__ float s_gam[kN];
+  typedef float Row[kPad];
+  Row *s_akav = reinterpret_cast<Row *>(&s_stage[0][0][0]);
+  Row *s_g1 = s_akav + kCk, *s_u = s_akav + 2 * kCk, *s_g2 = s_akav + 3 * kCk, *s_y0 = s_akav + 4 * kCk;
+  static_assert(sizeof(StageBuf<kCk>) >= 5 * kCk * kPad * sizeof(float), "staging buffer reuse");
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int row = lane & 15, kq = lane >> 4, col = 16 * wv + row;
+  const int c = blockIdx.x, h = blockIdx.y, bi = blockIdx.z;
+  const int C = H * kN;
+  const int t0 = c * kCk, t1 = min(T, t0 + kCk), Tl = t1 - t0;
+  St st(p, h, -1, (int64_t)bi * T * C + (int64_t)h * kN, t1);
+  st.fetch(t0);
+  st.commit(t0, s_stage);
+  __syncthreads();
+  {  // to padded f32 rows; tokens past the end become identity steps
+    const int tt = tid >> 4, q4 = 4 * (tid & 15);
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      float4 x = s_stage[i][tt][tid & 15];
+      if (tt >= Tl) x = i == 0 ? make_float4(1.f, 1.f, 1.f, 1.f) : make_float4(0.f, 0.f, 0.f, 0.f);
+      s_x[i][tt][q4] = x.x;
+      s_x[i][tt][q4 + 1] = x.y;
+      s_x[i][tt][q4 + 2] = x.z;
+      s_x[i][tt][q4 + 3] = x.w;
+    }
+  }
+  __syncthreads();
+  bool ok = true;
+  if (tid < kN) {
+    const int j = tid;
+    // suffix products (b^, k^, gam), exact products of w
+    float Q = 1.f;
+#pragma unroll
+    for (int t = kCk - 1; t >= 0; --t) {
+      s_bh[t][j] = s_x[2][t][j] * Q;
+      s_kh[t][j] = s_x[3][t][j] * Q;
+      Q *= s_x[0][t][j];
+    }
+    s_gam[j] = Q;
+    float P = 1.f;
+#pragma unroll
+    for (int t = 0; t < kCk; ++t) {
+      P *= s_x[0][t][j];
+      ok = ok && P >= 1e-30f && P <= 1e30f;  // false for NaN too
+    }
+  }
+  const bool fast = __syncthreads_and(ok);  // block-uniform
+  if (!fast) {  // token matrices straight from products of w: thread (t, s)
+    const int t = tid >> 4, s = tid & 15;
+    float aba = 0.f, aka = 0.f, bbr = 0.f, bkr = 0.f;
+    if (s <= t) {
+      for (int j = 0; j < kN; ++j) {
+        float d = 1.f;  // D(s, t-1]
+        for (int m = s + 1; m < t; ++m) d *= s_x[0][m][j];
+        const float dt = s < t ? d * s_x[0][t][j] : 1.f;  // D(s, t]
+        const float bs = s_x[2][s][j], ks = s_x[3][s][j], at = s_x[1][t][j], rt = s_x[4][t][j];
+        if (s < t) {
+          aba = fmaf(bs * d, at, aba);
+          aka = fmaf(ks * d, at, aka);
+        }
+        bbr = fmaf(bs * dt, rt, bbr);
+        bkr = fmaf(ks * dt, rt, bkr);
+      }
+    }
+    s_m[0][t][s] = aba;
+    s_m[1][t][s] = aka;
+    s_m[2][t][s] = bbr;
+    s_m[3][t][s] = bkr;
+    __syncthreads();
+  }
+  if (tid < kN) {  // a~, r~ (and b / P, k / P for the MFMA form) in place
+    const int j = tid;
+    float P = 1.f;
+#pragma unroll
+    for (int t = 0; t < kCk; ++t) {
+      const float Pp = P;
+      P *= s_x[0][t][j];
+      s_x[1][t][j] *= Pp;
+      s_x[4][t][j] *= P;
+      if (fast) {
+        s_x[2][t][j] = s_x[2][t][j] / P;
+        s_x[3][t][j] = s_x[3][t][j] / P;
+      }
+    }
+  }
+  __syncthreads();
+  if (fast) {  // wave m: token matrix m, (a~ or r~) (b / P or k / P)^T, masked
+    const int m = wv;
+    const Row *X = s_x[m < 2 ? 1 : 4];
+    const Row *Y = s_x[(m & 1) ? 3 : 2];
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < kN / 4; ++kk) acc = mfma4(X[row][4 * kk + kq], Y[row][4 * kk + kq], acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 4 * kq + r, s = row;
+      s_m[m][t][s] = (m < 2 ? s < t : s <= t) ? acc[r] : 0.f;
+    }
+    __syncthreads();
+  }
+  {  // AkaV, value columns 16 wv ..
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) acc = mfma4(s_m[1][row][4 * kk + kq], s_x[5][4 * kk + kq][col], acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s_akav[4 * kq + r][col] = acc[r];
+  }
+  if (tid < kCk) {  // T = (I - Aba)^-1 by forward substitution, lane = column
+    const int cc = tid;
+    float tc[kCk];
+#pragma unroll
+    for (int t = 0; t < kCk; ++t) {
+      float acc = t == cc ? 1.f : 0.f;
+#pragma unroll
+      for (int s = 0; s < t; ++s) acc = fmaf(s_m[0][t][s], tc[s], acc);
+      tc[t] = acc;
+      s_t[t][cc] = acc;
+    }
+  }
+  __syncthreads();
+  {  // G1 = T A~, U = T AkaV (column block wv)
+    floatx4 g = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const float tv = s_t[row][4 * kk + kq];
+      g = mfma4(tv, s_x[1][4 * kk + kq][col], g);
+      u = mfma4(tv, s_akav[4 * kk + kq][col], u);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      s_g1[4 * kq + r][col] = g[r];
+      s_u[4 * kq + r][col] = u[r];
+    }
+  }
+  __syncthreads();
+  {  // G2 = R~ + Bbr G1, Y0 = Bbr U + Bkr V
+    floatx4 g2, y0 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) g2[r] = s_x[4][4 * kq + r][col];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const float bb = s_m[2][row][4 * kk + kq], bk = s_m[3][row][4 * kk + kq];
+      g2 = mfma4(bb, s_g1[4 * kk + kq][col], g2);
+      y0 = mfma4(bb, s_u[4 * kk + kq][col], y0);
+      y0 = mfma4(bk, s_x[5][4 * kk + kq][col], y0);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      s_g2[4 * kq + r][col] = g2[r];
+      s_y0[4 * kq + r][col] = y0[r];
+    }
+  }
+  __syncthreads();
+  // the record, one float4 per thread and array (thread = wave 64 + lane of
+  // the chain kernel's reader)
+  float *R = rec + (((int64_t)bi * H + h) * gridDim.x + c) * kRecFloats;
+  const int w = tid >> 6;
+  auto put = [&](int off, float a0, float a1, float a2, float a3) {
+    *reinterpret_cast<float4 *>(R + off + 4 * tid) = make_float4(a0, a1, a2, a3);
+  };
+  // A operand of the chain's Sig / Y step: G[row][16 w + 4 kk + kq]
+  put(kRecG1, s_g1[row][16 * w + kq], s_g1[row][16 * w + 4 + kq], s_g1[row][16 * w + 8 + kq],
+      s_g1[row][16 * w + 12 + kq]);
+  put(kRecG2, s_g2[row][16 * w + kq], s_g2[row][16 * w + 4 + kq], s_g2[row][16 * w + 8 + kq],
+      s_g2[row][16 * w + 12 + kq]);
+  // B operand of the state update: X[4 kk + kq][16 w + row]
+  put(kRecBh, s_bh[kq][16 * w + row], s_bh[4 + kq][16 * w + row], s_bh[8 + kq][16 * w + row],
+      s_bh[12 + kq][16 * w + row]);
+  put(kRecKh, s_kh[kq][16 * w + row], s_kh[4 + kq][16 * w + row], s_kh[8 + kq][16 * w + row],
+      s_kh[12 + kq][16 * w + row]);
+  // A operand of the state update (value rows 16 q + row, q = w here)
+  put(kRecU, s_u[kq][16 * w + row], s_u[4 + kq][16 * w + row], s_u[8 + kq][16 * w + row],
+      s_u[12 + kq][16 * w + row]);
+  put(kRecV, s_x[5][kq][16 * w + row], s_x[5][4 + kq][16 * w + row], s_x[5][8 + kq][16 * w + row],
+      s_x[5][12 + kq][16 * w + row]);
+  {  // Y0[q][t][i] = Y0[t][16 q + i]
+    const int e = 4 * tid, q = e >> 8, t = (e >> 4) & 15, i = e & 15;
+    put(kRecY0, s_y0[t][16 * q + i], s_y0[t][16 * q + i + 1], s_y0[t][16 * q + i + 2], s_y0[t][16 * q + i + 3]);
+  }
+  if (tid < kN / 4) put(kRecGam, s_gam[4 * tid], s_gam[4 * tid + 1], s_gam[4 * tid + 2], s_gam[4 * tid + 3]);
+}
+
+template <typename TY>
+__global__ __launch_bounds__(256) void wkv7_chunk_chain_kernel(float *S, const float *rec, TY *y, int T, int H) {
+  __shared__ float s_s[kCk][kPad];  // the workgroup's 16 state rows
+  __shared__ float s_xp[4][kCk][kCk + 1], s_yp[4][kCk][kCk + 1];  // per-block Sig^T / Y partials [t][i]
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int row = lane & 15, kq = lane >> 4;
+  const int h = blockIdx.x >> 2, q = blockIdx.x & 3, bi = blockIdx.y;
+  const int NC = (T + kCk - 1) / kCk, C = H * kN;
+  // lane holds S[16 q + 4 kq + r][16 wv + row], r = 0..3 (the MFMA D layout)
+  float *Sp = S + (((int64_t)bi * H + h) * kN + 16 * q) * kN;
+  floatx4 st;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) st[r] = Sp[(4 * kq + r) * kN + 16 * wv + row];
+  const float *R0 = rec + ((int64_t)bi * H + h) * NC * kRecFloats;
+  float4 g1, g2, bh, kh, u, vv;
+  float gam, y0;
+  auto load = [&](int c) {  // the chunk's record, one round of loads
+    const float *R = R0 + (int64_t)c * kRecFloats;
+    g1 = reinterpret_cast<const float4 *>(R + kRecG1)[tid];
+    g2 = reinterpret_cast<const float4 *>(R + kRecG2)[tid];
+    bh = reinterpret_cast<const float4 *>(R + kRecBh)[tid];
+    kh = reinterpret_cast<const float4 *>(R + kRecKh)[tid];
+    u = reinterpret_cast<const float4 *>(R + kRecU)[64 * q + lane];
+    vv = reinterpret_cast<const float4 *>(R + kRecV)[64 * q + lane];
+    gam = R[kRecGam + 16 * wv + row];
+    y0 = R[kRecY0 + 256 * q + tid];
+  };
+  load(0);
+  for (int c = 0; c < NC; ++c) {
+    const float G1[4] = {g1.x, g1.y, g1.z, g1.w}, G2[4] = {g2.x, g2.y, g2.z, g2.w};
+    const float BH[4] = {bh.x, bh.y, bh.z, bh.w}, KH[4] = {kh.x, kh.y, kh.z, kh.w};
+    const float U[4] = {u.x, u.y, u.z, u.w}, V[4] = {vv.x, vv.y, vv.z, vv.w};
+    const float GAM = gam, Y0 = y0;
+    if (c + 1 < NC) load(c + 1);  // the next record streams in meanwhile
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s_s[4 * kq + r][16 * wv + row] = st[r];
+    __syncthreads();
+    // Sig^T and Y over this wave's 16 key columns: D[t][i] = sum_j G[t][j] S[i][j]
+    floatx4 xa = {0.f, 0.f, 0.f, 0.f}, ya = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const float sv = s_s[row][16 * wv + 4 * kk + kq];
+      xa = mfma4(G1[kk], sv, xa);
+      ya = mfma4(G2[kk], sv, ya);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      s_xp[wv][4 * kq + r][row] = xa[r];
+      s_yp[wv][4 * kq + r][row] = ya[r];
+    }
+    __syncthreads();
+    {  // y of token t, value row 16 q + i
+      const int t = tid >> 4, i = tid & 15, tt = c * kCk + t;
+      const float yv = ((s_yp[0][t][i] + s_yp[1][t][i]) + (s_yp[2][t][i] + s_yp[3][t][i])) + Y0;
+      if (tt < T) y[((int64_t)bi * T + tt) * C + h * kN + 16 * q + i] = from_f<TY>(yv);
+    }
+    // S <- S diag(gam) + Sig^T B^ + V^T K^ (this wave's 16 columns)
+    floatx4 acc;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = st[r] * GAM;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int t = 4 * kk + kq;
+      const float xv = ((s_xp[0][t][row] + s_xp[1][t][row]) + (s_xp[2][t][row] + s_xp[3][t][row])) + U[kk];
+      acc = mfma4(xv, BH[kk], acc);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) acc = mfma4(V[kk], KH[kk], acc);
+    st = acc;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) Sp[(4 * kq + r) * kN + 16 * wv + row] = st[r];
+}
+
+template <class St, typename TY>
+static int launch_chunked(const typename St::Args &p, float *S, TY *y, float *rec, int B, int T, int H,
+                          hipStream_t st) {
+  if (!rec) return RWKV7_EWORKSPACE;
+  const int nc = (T + kCk - 1) / kCk;
+  wkv7_chunk_prep_kernel<St><<<dim3(nc, H, B), 256, 0, st>>>(p, rec, T, H);
+  RWKV7_CHECK_LAUNCH();
+  wkv7_chunk_chain_kernel<TY><<<dim3(4 * H, B), 256, 0, st>>>(S, rec, y, T, H);
+  RWKV7_CHECK_LAUNCH();
+  return RWKV7_OK;
+}
+
+template <typename TI, typename TW, typename TY>
+int launch_wkv7_chunked(const ScanArgs<TI, TW, TY> &p, float *rec, hipStream_t st) {
+  if (p.T <= 0 || p.B <= 0 || p.H <= 0) return RWKV7_OK;
+  return launch_chunked<RawStager<kCk, TI, TW, TY>, TY>(p, p.S, p.y, rec, p.B, p.T, p.H, st);
+}
+template int launch_wkv7_chunked<uint16_t, float, uint16_t>(const ScanArgs<uint16_t, float, uint16_t> &, float *,
+                                                            hipStream_t);
+template int launch_wkv7_chunked<uint16_t, uint16_t, uint16_t>(const ScanArgs<uint16_t, uint16_t, uint16_t> &,
+                                                               float *, hipStream_t);
+template int launch_wkv7_chunked<bf16_t, float, bf16_t>(const ScanArgs<bf16_t, float, bf16_t> &, float *,
+                                                        hipStream_t);
+template int launch_wkv7_chunked<bf16_t, bf16_t, bf16_t>(const ScanArgs<bf16_t, bf16_t, bf16_t> &, float *,
+                                                         hipStream_t);
+template int launch_wkv7_chunked<float, float, float>(const ScanArgs<float, float, float> &, float *, hipStream_t);
+
 int launch_wkv7_prefill(const PrefillScanArgs &p, hipStream_t st) {
   if (p.T <= 0 || p.B <= 0 || p.H <= 0) return RWKV7_OK;
   if (p.C != p.H * kN) return RWKV7_ESHAPE;
+  const int cus = mk_cus() > 0 ? mk_cus() : 256;
+  if (prefill_chunked(p.T, p.B, p.H, cus))
+    return launch_chunked<GateStager<kCk>, float>(p, p.S, p.y, p.rec, p.B, p.T, p.H, st);
   int seg_len;
-  const int nseg = prefill_segments(p.T, p.B, p.H, mk_cus() > 0 ? mk_cus() : 256, &seg_len);
+  const int nseg = prefill_segments(p.T, p.B, p.H, cus, &seg_len);
   if (nseg > 1 && (!p.U || !p.Send || !p.Pend)) return RWKV7_EWORKSPACE;
   if (p.T == 1)
     dplr_scan_kernel<false, 1, GateStager<1>><<<dim3(4 * p.H, p.B, 1), 256, 0, st>>>(p, seg_len, nseg);

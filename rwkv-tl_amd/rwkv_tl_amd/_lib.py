@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the HIP library)
 
 LIB_NAME = "librwkv7_hip.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 # rwkv7_model.flags
 MODEL_MULTI_LAUNCH_DECODE = 1
@@ -44,6 +44,8 @@ SYMBOLS = (
     "rwkv7_decode_noalloc",
     "rwkv7_prefill",
     "rwkv7_wkv7",
+    "rwkv7_wkv7_chunked_workspace_bytes",
+    "rwkv7_wkv7_chunked",
     "rwkv7_wkv7_f32",
     "rwkv7_wkv7_backward",
     "rwkv7_layernorm",
@@ -165,6 +167,8 @@ def _declare(lib: ctypes.CDLL) -> None:
         "rwkv7_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(Model), ctypes.POINTER(StateDesc), vp, vp, vp]),
         "rwkv7_prefill": (ctypes.c_int, [ctypes.POINTER(Model), ctypes.POINTER(StateDesc), vp, i32, vp, i64, vp]),
         "rwkv7_wkv7": (ctypes.c_int, [vp, vp, vp, i32, vp, vp, vp, vp, vp, i32, i32, i32, i32, vp]),
+        "rwkv7_wkv7_chunked_workspace_bytes": (ctypes.c_int64, [i32, i32, i32]),
+        "rwkv7_wkv7_chunked": (ctypes.c_int, [vp, vp, vp, i32, vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, i64, vp]),
         "rwkv7_wkv7_f32": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, vp]),
         "rwkv7_wkv7_backward": (ctypes.c_int, [vp] * 17 + [i32, i32, i32, vp]),
         "rwkv7_layernorm": (ctypes.c_int, [vp, i32, vp, vp, vp, i32, i32, i32, vp]),

@@ -67,11 +67,31 @@ def _h16(*ts: Tensor) -> int:
     return int(dt == torch.bfloat16)
 
 
-def wkv7(S: Tensor, r: Tensor, w: Tensor, k: Tensor, v: Tensor, a: Tensor, b: Tensor) -> Tensor:
+# The operator takes the chunked scan for sequences at least this long when
+# the serial scan's 4 workgroups per head and sequence would leave CUs idle
+# (measured on MI355X: B=1, H=16, T=128 faster chunked; the survey's C2,
+# B=8, H=16, T=128, faster serial).
+CHUNK_MIN_T = 32
+_CUS: dict[int, int] = {}
+
+
+def _cus(dev: torch.device) -> int:
+    i = dev.index if dev.index is not None else torch.cuda.current_device()
+    if i not in _CUS:
+        _CUS[i] = torch.cuda.get_device_properties(i).multi_processor_count
+    return _CUS[i]
+
+
+def wkv7(S: Tensor, r: Tensor, w: Tensor, k: Tensor, v: Tensor, a: Tensor, b: Tensor,
+         chunked: bool | None = None) -> Tensor:
     """Batched DPLR recurrence; updates ``S`` [B,H,64,64] fp32 in place.
 
     ``r, k, v, a, b``: f16 or bf16 [B, T, H, 64]; ``w``: the same 16-bit
     dtype or f32. Returns ``y`` [B, T, H, 64] of r's dtype with ``y_t = S_t r_t``.
+    ``chunked``: run the chunked (MFMA) algorithm, ``rwkv7_wkv7_chunked``,
+    with a workspace allocated per call, or the serial scan ``rwkv7_wkv7``;
+    ``None`` chooses the chunked one for ``T >= CHUNK_MIN_T`` when
+    ``4 B H`` is below the device's CU count.
     """
     _dev(S, r, w, k, v, a, b)
     _need(S.dtype == torch.float32 and S.dim() == 4 and S.shape[2:] == (N, N), "S must be f32 [B,H,64,64]")
@@ -85,11 +105,16 @@ def wkv7(S: Tensor, r: Tensor, w: Tensor, k: Tensor, v: Tensor, a: Tensor, b: Te
     _need(w.shape == r.shape and w.dtype in (r.dtype, torch.float32), "w must be like r, or f32")
     y = torch.empty_like(r)
     lib = _lib.load()
-    rc = lib.rwkv7_wkv7(
-        S.data_ptr(), r.data_ptr(), w.data_ptr(), int(w.dtype == torch.float32), k.data_ptr(),
-        v.data_ptr(), a.data_ptr(), b.data_ptr(), y.data_ptr(), Bsz, T, H, bf, _lib.stream_handle(),
-    )
-    _lib.check(rc, "rwkv7_wkv7")
+    args = (S.data_ptr(), r.data_ptr(), w.data_ptr(), int(w.dtype == torch.float32), k.data_ptr(), v.data_ptr(),
+            a.data_ptr(), b.data_ptr(), y.data_ptr(), Bsz, T, H, bf)
+    if chunked is None:
+        chunked = T >= CHUNK_MIN_T and 4 * Bsz * H < _cus(S.device)
+    if chunked:
+        nb = int(lib.rwkv7_wkv7_chunked_workspace_bytes(Bsz, T, H))
+        ws = torch.empty(nb, dtype=torch.uint8, device=S.device)
+        _lib.check(lib.rwkv7_wkv7_chunked(*args, ws.data_ptr(), nb, _lib.stream_handle()), "rwkv7_wkv7_chunked")
+    else:
+        _lib.check(lib.rwkv7_wkv7(*args, _lib.stream_handle()), "rwkv7_wkv7")
     return y
 
 

@@ -51,19 +51,61 @@ def _rel(x, y):
     return float((x.double() - y.double()).norm() / y.double().norm().clamp_min(1e-30))
 
 
+@pytest.mark.parametrize("chunked", [False, True], ids=["serial", "chunked"])
 @pytest.mark.parametrize(
     "B,H,T,w_f32",
     [(8, 16, 128, True), (1, 1, 1, True), (2, 3, 17, False), (1, 4, 33, True), (3, 2, 64, False)],
 )
-def test_wkv7_matches_oracle(B, H, T, w_f32, cuda):
-    print(f"wkv7 B={B} H={H} T={T} w_f32={w_f32}", flush=True)
+def test_wkv7_matches_oracle(B, H, T, w_f32, chunked, cuda):
+    """Both algorithms (rwkv7_wkv7, rwkv7_wkv7_chunked) against the serial
+    fp32 oracle: the state within 1e-5 relative, y (f16) within 2e-3. T = 1,
+    17 and 33 leave the chunked form a partial last chunk."""
+    print(f"wkv7 B={B} H={H} T={T} w_f32={w_f32} chunked={chunked}", flush=True)
     S0, r, w, k, v, a, b = _c2_inputs(B, H, T, seed=B * 100 + T, w_f32=w_f32)
     y_ref, S_ref = R.wkv7_scan(S0, r, w, k, v, a, b)
     S = S0.clone().to(cuda)
-    y = K.wkv7(S, *(t.to(cuda) for t in (r, w, k, v, a, b)))
+    y = K.wkv7(S, *(t.to(cuda) for t in (r, w, k, v, a, b)), chunked=chunked)
     torch.cuda.synchronize()
     assert _rel(S.cpu(), S_ref) < 1e-5
     torch.testing.assert_close(y.cpu().float(), y_ref.float(), rtol=2e-3, atol=2e-3)
+
+
+@pytest.mark.parametrize("w_low", [1e-3, 0.0], ids=["tiny", "zero"])
+def test_wkv7_chunked_strong_decay(w_low, cuda):
+    """Decays whose 16-token products leave [1e-30, 1e30] (tiny or zero w on
+    some channels) take the chunked kernel's direct-product branch for those
+    chunks; results still match the oracle, and no value is lost to an
+    overflow of the reciprocal products."""
+    B, H, T = 2, 3, 48
+    S0, r, w, k, v, a, b = _c2_inputs(B, H, T, seed=5, w_f32=True)
+    w = w.clone()
+    w[0, 16:32, :, :8] = w_low  # chunk 1 of sequence 0: slow branch; the rest fast
+    w[1, :, 1, 60:] = w_low
+    y_ref, S_ref = R.wkv7_scan(S0, r, w, k, v, a, b)
+    S = S0.clone().to(cuda)
+    y = K.wkv7(S, *(t.to(cuda) for t in (r, w, k, v, a, b)), chunked=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(S).all() and torch.isfinite(y.float()).all()
+    assert _rel(S.cpu(), S_ref) < 1e-5
+    torch.testing.assert_close(y.cpu().float(), y_ref.float(), rtol=2e-3, atol=2e-3)
+
+
+def test_wkv7_chunked_long_sequence_agrees_with_serial(cuda):
+    """T = 1024 (the C5 prefill length) in bfloat16: the chunked and serial
+    algorithms agree on the final state to 1e-4 relative and on y to bf16
+    rounding."""
+    B, H, T = 2, 2, 1024
+    S0, r, w, k, v, a, b = _c2_inputs(B, H, T, seed=9, w_f32=True)
+    ins = [t.to(cuda) for t in (r, w, k, v, a, b)]
+    ins = [t.bfloat16() if t.dtype == torch.float16 else t for t in ins]
+    outs = []
+    for chunked in (False, True):
+        S = S0.clone().to(cuda)
+        y = K.wkv7(S, *ins, chunked=chunked)
+        outs.append((S.cpu(), y.float().cpu()))
+    torch.cuda.synchronize()
+    assert _rel(outs[1][0], outs[0][0]) < 1e-4
+    torch.testing.assert_close(outs[1][1], outs[0][1], rtol=2e-2, atol=2e-2)
 
 
 def test_fused_dplr_step_and_sequence_api(cuda):

@@ -151,14 +151,16 @@ def test_prefill_rejects_empty_and_bad_shapes(cuda):
         st.model.decode(torch.tensor([10**6]), S)
 
 
-def test_batched_segmented_prefill_matches_oracle(cuda):
-    """B=3 sequences of 80 tokens (three segments each) prefilled in one call:
-    every row's state and next logits match the oracle's."""
-    print("batched segmented prefill B=3 T=80", flush=True)
+@pytest.mark.parametrize("T", [80, 130], ids=["segmented", "chunked"])
+def test_batched_segmented_prefill_matches_oracle(T, cuda):
+    """B=3 sequences prefilled in one call -- 80 tokens (the segmented serial
+    scan, three segments each) or 130 (the chunked scan, a partial last
+    chunk): every row's state and next logits match the oracle's."""
+    print(f"batched prefill B=3 T={T}", flush=True)
     st = setup_for("tiny", cuda)
     V, B = st.w.head.shape[0], 3
-    g = torch.Generator().manual_seed(80)
-    prompt = torch.randint(0, V, (B, 80), generator=g)
+    g = torch.Generator().manual_seed(T)
+    prompt = torch.randint(0, V, (B, T), generator=g)
     nxt = torch.randint(0, V, (B,), generator=g)
     S = State(st.w.L, st.w.C, 64, device=cuda, batch=B)
     st.model.prefill(prompt.to(cuda), S)
@@ -167,7 +169,7 @@ def test_batched_segmented_prefill_matches_oracle(cuda):
     R.prefill(st.ref32, prompt, ref)
     l32, ref = R.decode(st.ref32, nxt, ref)
     for b in range(B):
-        _check_logits(lg[b], l32[b], f"segmented prefill row {b}")
+        _check_logits(lg[b], l32[b], f"T={T} prefill row {b}")
     for i in range(st.w.L):
         for b in range(B):
             r = _rel(S.tmix[i]["rnn"][b].cpu(), ref[0][i]["rnn"][b])
