@@ -428,6 +428,16 @@ def bench_generate() -> dict:
             us = 1000.0 * sum(a.elapsed_time(b) for a, b in evs) / len(evs)
             out[name][f"sample_kernel_us_B{B}"] = round(us, 2)
             log(f"sample kernel {name} B={B}: {us:.2f} us")
+            if "top_k" in kw:  # the same without the workspace: one workgroup per row
+                smp.workspace = None
+                for a, b in evs:
+                    a.record(stream)
+                    smp(logits, res)
+                    b.record(stream)
+                torch.cuda.synchronize()
+                us1 = 1000.0 * sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+                out[name][f"sample_kernel_us_B{B}_one_workgroup_per_row"] = round(us1, 2)
+                log(f"sample kernel {name} B={B}, one workgroup per row: {us1:.2f} us")
     return out
 
 

@@ -406,13 +406,19 @@ typedef struct rwkv7_sampling {
  * point and drawn by inverse CDF in vocabulary order with Philox4x32-10
  * (key = seed, counter = (offset, row, 0)). update_seen sets the sampled
  * token's bit in seen. probs f32 [B, probs_ld] (optional) receives the kept
- * distribution (one-hot when greedy). One workgroup per row, no host sync.
+ * distribution (one-hot when greedy). No host sync. With a workspace of at
+ * least rwkv7_sample_workspace_bytes(B, V) bytes, a call with temperature >
+ * 0, 1 <= top_k <= 128 and no probs spreads each row over V / 2048
+ * workgroups (each keeps the candidates of its slice of the row, a second
+ * launch draws from them) and draws the same token as without it; otherwise
+ * (workspace NULL) one workgroup per row does all of it.
  * Stands in for sample_logits (demo/sampling.py:13-70) as called by
  * RWKV7Model.generate (demo/_rwkv7_abc.py:41-72), with the draw of
  * torch.multinomial replaced by the counter-based one above. */
+int64_t rwkv7_sample_workspace_bytes(int32_t B, int32_t V);
 int rwkv7_sample(const void *logits, int32_t logits_dtype, int64_t ld, int32_t B, int32_t V, const rwkv7_sampling *params,
                  uint32_t *seen, int64_t seen_ld, int32_t update_seen, int64_t *out, float *probs,
-                 int64_t probs_ld, void *stream);
+                 int64_t probs_ld, void *workspace, int64_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -304,10 +304,85 @@ RWKV7_DEV void load8(const void *row_ptr, int i0, int V, float *f) {
   }
 }
 
+// Temperature-scaled sampling of one row from the E values each thread holds
+// (-inf: none), the threads' values in vocabulary order thread by thread;
+// idx(e) is the vocabulary index of this thread's e-th value. Top-k, top-p,
+// the kept mass and the draw as described at the top; pr (optional) receives
+// the kept distribution at the indices held. Returns the token on the one
+// thread that draws it, -1 on the others.
+template <int E, class Idx>
+RWKV7_DEV int draw_tempered(float (&l)[E], Idx idx, const SampleArgs &a, int row, float *pr, SampleLds &s) {
+  const int V = a.V;
+  float lo = kInf, m = -kInf, tmax = -kInf;
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (l[e] > -kInf) lo = fminf(lo, l[e]), tmax = fmaxf(tmax, l[e]);
+  m = tmax;
+  block_minmax(lo, m, s);
+  float thr = -kInf;  // tokens with x >= thr stay
+  if (a.top_k > 0 && a.top_k < V) {  // sampling.py:56-60
+    // The k-th largest value is at least the k-th largest of the threads'
+    // maxima when k threads hold values: only values from there up take part.
+    float floor_k = lo;
+    if (__syncthreads_count(tmax > -kInf) >= a.top_k) {
+      float tl = tmax > -kInf ? tmax : kInf, th = tmax;
+      block_minmax(tl, th, s);
+      const float tv[1] = {tmax};
+      floor_k = select_gt<false, 1>(tv, tl, th, m, (u64)(a.top_k - 1), s);
+    }
+    thr = select_gt<false, E>(l, floor_k, m, m, (u64)(a.top_k - 1), s);
+    lo = thr;  // the smallest value top-k keeps
+  }
+  if (a.top_p < 1.f) {  // sampling.py:62-68
+    u64 own = 0, z = 0;
+    const float mo = opaque(m);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      if (l[e] < thr) l[e] = -kInf;
+      if (l[e] > -kInf) own += mass(l[e], mo);
+    }
+    block_excl_scan(own, z, s);
+    thr = select_gt<true, E>(l, lo, m, m, (u64)((double)a.top_p * (double)z), s);
+  }
+  u64 own = 0, z = 0;
+  {
+    const float m1 = opaque(m);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      if (l[e] < thr) l[e] = -kInf;
+      if (l[e] > -kInf) own += mass(l[e], m1);
+    }
+  }
+  const u64 excl = block_excl_scan(own, z, s);
+  uint32_t c[4] = {a.off_lo, a.off_hi, (uint32_t)row, 0u};
+  philox4x32_10(c, a.seed_lo, a.seed_hi);
+  const u64 target = __umul64hi(z, (u64)c[0] | ((u64)c[1] << 32));  // in [0, z)
+  int token = -1;  // exactly one thread finds it: z >= 2^40, since the maximum is always kept
+  if (excl <= target && target < excl + own) {
+    u64 acc = excl;
+    const float m2 = opaque(m);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      if (l[e] > -kInf) acc += mass(l[e], m2);
+      if (token < 0 && acc > target) token = idx(e);
+    }
+  }
+  if (pr) {
+    const float inv = 1.f / (float)z, m3 = opaque(m);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int i = idx(e);
+      if (i < V) pr[i] = l[e] > -kInf ? (float)mass(l[e], m3) * inv : 0.f;
+    }
+  }
+  return token;
+}
+
+// The whole row on one workgroup (thread t holds logits 64 t .. 64 t + 63).
+// Returns the token on the thread that holds it (every thread for greedy).
 template <bool VEC, int FMT>
-__global__ __launch_bounds__(kSmpThreads) void sample_kernel(SampleArgs a) {
-  __shared__ SampleLds s;
-  const int row = blockIdx.x, base = threadIdx.x * kSmpE, V = a.V;
+RWKV7_DEV int sample_row(const SampleArgs &a, int row, SampleLds &s) {
+  const int base = threadIdx.x * kSmpE, V = a.V;
   const void *src = static_cast<const char *>(a.logits) + (int64_t)row * a.ld * (FMT == 1 ? 4 : 2);
   float l[kSmpE];
 #pragma unroll
@@ -326,7 +401,7 @@ __global__ __launch_bounds__(kSmpThreads) void sample_kernel(SampleArgs a) {
 #pragma unroll
   for (int e = 0; e < kSmpE; ++e) l[e] = l[e] + 0.f;  // -0 -> +0: one key per value
 
-  int token;
+  float *pr = a.probs ? a.probs + (int64_t)row * a.probs_ld : nullptr;
   if (!(a.temp > 0.f)) {
     // greedy: argmax, first index among ties (sampling.py:49-50)
     float v = -kInf;
@@ -335,90 +410,175 @@ __global__ __launch_bounds__(kSmpThreads) void sample_kernel(SampleArgs a) {
     for (int e = 0; e < kSmpE; ++e)
       if (better(l[e], base + e, v, vi)) v = l[e], vi = base + e;
     block_argmax(v, vi, s);
-    token = vi < V ? vi : 0;  // only a row of NaNs leaves vi past V
-    if (a.probs) {
-      float *pr = a.probs + (int64_t)row * a.probs_ld;
+    const int token = vi < V ? vi : 0;  // only a row of NaNs leaves vi past V
+    if (pr) {
 #pragma unroll
       for (int e = 0; e < kSmpE; ++e)
         if (base + e < V) pr[base + e] = base + e == token ? 1.f : 0.f;
     }
-  } else {
-#pragma unroll
-    for (int e = 0; e < kSmpE; ++e) l[e] = l[e] / a.temp;
-    float lo = kInf, m = -kInf, tmax = -kInf;
-#pragma unroll
-    for (int e = 0; e < kSmpE; ++e)
-      if (l[e] > -kInf) lo = fminf(lo, l[e]), tmax = fmaxf(tmax, l[e]);
-    m = tmax;
-    block_minmax(lo, m, s);
-    float thr = -kInf;  // tokens with x >= thr stay
-    if (a.top_k > 0 && a.top_k < V) {  // sampling.py:56-60
-      // The k-th largest value is at least the k-th largest of the threads'
-      // maxima when k threads hold values: only values from there up take part.
-      float floor_k = lo;
-      if (__syncthreads_count(tmax > -kInf) >= a.top_k) {
-        float tl = tmax > -kInf ? tmax : kInf, th = tmax;
-        block_minmax(tl, th, s);
-        const float tv[1] = {tmax};
-        floor_k = select_gt<false, 1>(tv, tl, th, m, (u64)(a.top_k - 1), s);
-      }
-      thr = select_gt<false, kSmpE>(l, floor_k, m, m, (u64)(a.top_k - 1), s);
-      lo = thr;  // the smallest value top-k keeps
-    }
-    if (a.top_p < 1.f) {  // sampling.py:62-68
-      u64 own = 0, z = 0;
-      const float mo = opaque(m);
-#pragma unroll
-      for (int e = 0; e < kSmpE; ++e) {
-        if (l[e] < thr) l[e] = -kInf;
-        if (l[e] > -kInf) own += mass(l[e], mo);
-      }
-      block_excl_scan(own, z, s);
-      thr = select_gt<true, kSmpE>(l, lo, m, m, (u64)((double)a.top_p * (double)z), s);
-    }
-    u64 own = 0, z = 0;
-    {
-      const float m1 = opaque(m);
-#pragma unroll
-      for (int e = 0; e < kSmpE; ++e) {
-        if (l[e] < thr) l[e] = -kInf;
-        if (l[e] > -kInf) own += mass(l[e], m1);
-      }
-    }
-    const u64 excl = block_excl_scan(own, z, s);
-    uint32_t c[4] = {a.off_lo, a.off_hi, (uint32_t)row, 0u};
-    philox4x32_10(c, a.seed_lo, a.seed_hi);
-    const u64 target = __umul64hi(z, (u64)c[0] | ((u64)c[1] << 32));  // in [0, z)
-    token = -1;  // exactly one thread finds it: z >= 2^40, since the maximum is always kept
-    if (excl <= target && target < excl + own) {
-      u64 acc = excl;
-      const float m2 = opaque(m);
-#pragma unroll
-      for (int e = 0; e < kSmpE; ++e) {
-        if (l[e] > -kInf) acc += mass(l[e], m2);
-        if (token < 0 && acc > target) token = base + e;
-      }
-    }
-    if (a.probs) {
-      float *pr = a.probs + (int64_t)row * a.probs_ld;
-      const float inv = 1.f / (float)z, m3 = opaque(m);
-#pragma unroll
-      for (int e = 0; e < kSmpE; ++e)
-        if (base + e < V) pr[base + e] = l[e] > -kInf ? (float)mass(l[e], m3) * inv : 0.f;
-    }
+    return threadIdx.x == 0 ? token : -1;
   }
-  if (token >= 0 && (a.temp > 0.f || threadIdx.x == 0)) {
+#pragma unroll
+  for (int e = 0; e < kSmpE; ++e) l[e] = l[e] / a.temp;
+  return draw_tempered<kSmpE>(l, [base](int e) { return base + e; }, a, row, pr, s);
+}
+
+RWKV7_DEV void put_token(const SampleArgs &a, int row, int token) {
+  if (token >= 0) {
     a.out[row] = token;
     if (a.update_seen) atomicOr(a.seen + (int64_t)row * a.seen_ld + token / 32, 1u << (token % 32));
   }
 }
 
+template <bool VEC, int FMT>
+__global__ __launch_bounds__(kSmpThreads) void sample_kernel(SampleArgs a) {
+  __shared__ SampleLds s;
+  put_token(a, blockIdx.x, sample_row<VEC, FMT>(a, blockIdx.x, s));
+}
+
+// ---------------------------------------------------------------------------
+// Top-k over many CUs (temperature > 0, 1 <= top_k <= kCandMax, no probs):
+// every token top-k keeps is among the top_k largest of its own slice of the
+// row, so the row is cut into slices of kCandSlice logits, each workgroup of
+// sample_cand_kernel keeps the values of its slice >= the slice's top_k-th
+// largest (ties included; exact, by the same selection as above) in index
+// order, and sample_finish_kernel runs draw_tempered on those candidates,
+// which hold the same values at the same vocabulary positions as the
+// one-workgroup kernel would: the thresholds, the fixed-point masses, the
+// draw and therefore the token are identical. A slice with more than
+// kCandMax candidates (a tie group at its threshold) marks its count -1, and
+// the row is sampled by sample_row instead.
+// ---------------------------------------------------------------------------
+constexpr int kCandSlice = 2 * kSmpThreads;  // 2 logits per thread
+constexpr int kCandMax = 128;                // candidates kept per slice
+constexpr int kCandSlices = kSmpMaxV / kCandSlice;
+constexpr int kCandE = kCandSlices * kCandMax / kSmpThreads;  // candidates per thread in the finish
+
+struct CandBuf {
+  int *cnt;     // [B][G]: candidates of each slice, -1 when more than kCandMax
+  float *val;   // [B][G][kCandMax]
+  int *idx;     // [B][G][kCandMax]
+  int G;
+};
+
+template <int FMT>
+RWKV7_DEV float load1(const void *row_ptr, int i) {
+  if (FMT == 1) return static_cast<const float *>(row_ptr)[i];
+  return F16T<FMT == 2>::to_f(static_cast<const uint16_t *>(row_ptr)[i]);
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kSmpThreads) void sample_cand_kernel(SampleArgs a, CandBuf cb) {
+  __shared__ SampleLds s;
+  const int g = blockIdx.x, row = blockIdx.y, V = a.V;
+  const void *src = static_cast<const char *>(a.logits) + (int64_t)row * a.ld * (FMT == 1 ? 4 : 2);
+  const int i0 = g * kCandSlice + 2 * threadIdx.x;
+  float l[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) l[e] = i0 + e < V ? load1<FMT>(src, i0 + e) : -kInf;
+  if (a.seen && a.pen != 1.f) {  // the same operations, in the same order, as sample_row
+    const uint32_t *sr = a.seen + (int64_t)row * a.seen_ld;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int i = i0 + e;
+      if (i < V && ((sr[i >> 5] >> (i & 31)) & 1u)) l[e] = l[e] > 0.f ? l[e] / a.pen : l[e] * a.pen;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 2; ++e) l[e] = (l[e] + 0.f) / a.temp;
+  float lo = kInf, hi = -kInf;
+#pragma unroll
+  for (int e = 0; e < 2; ++e)
+    if (l[e] > -kInf) lo = fminf(lo, l[e]), hi = fmaxf(hi, l[e]);
+  block_minmax(lo, hi, s);
+  // the slice's top_k-th largest value (lo when it holds fewer values)
+  const float u = select_gt<false, 2>(l, lo, hi, hi, (u64)(a.top_k - 1), s);
+  bool keep[2];
+  int own = 0;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    keep[e] = l[e] > -kInf && l[e] >= u;
+    own += keep[e];
+  }
+  u64 total;
+  int at = (int)block_excl_scan((u64)own, total, s);
+  const int64_t slot = (int64_t)row * cb.G + g;
+  if (threadIdx.x == 0) cb.cnt[slot] = total <= (u64)kCandMax ? (int)total : -1;
+  if (total <= (u64)kCandMax) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      if (keep[e]) {
+        cb.val[slot * kCandMax + at] = l[e];
+        cb.idx[slot * kCandMax + at] = i0 + e;
+        ++at;
+      }
+    }
+  }
+}
+
+template <bool VEC, int FMT>
+__global__ __launch_bounds__(kSmpThreads) void sample_finish_kernel(SampleArgs a, CandBuf cb) {
+  __shared__ SampleLds s;
+  __shared__ int s_off[kCandSlices + 1];
+  __shared__ int s_bad;
+  const int row = blockIdx.x, G = cb.G;
+  if (threadIdx.x < kWave) {  // slice offsets: inclusive prefix of the counts
+    const int L = threadIdx.x;
+    const int c = L < G ? cb.cnt[(int64_t)row * G + L] : 0;
+    int inc = c < 0 ? 0 : c;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int o = __shfl_up(inc, d);
+      if (L >= d) inc += o;
+    }
+    const bool bad = __ballot(c < 0) != 0;
+    if (L <= kCandSlices - 1) s_off[L + 1] = inc;
+    if (L == 0) {
+      s_off[0] = 0;
+      s_bad = bad;
+    }
+  }
+  __syncthreads();
+  if (s_bad) {  // a tie group overflowed a slice: the whole row here
+    put_token(a, row, sample_row<VEC, FMT>(a, row, s));
+    return;
+  }
+  const int n = s_off[G];
+  float l[kCandE];
+  int ix[kCandE];
+#pragma unroll
+  for (int e = 0; e < kCandE; ++e) {
+    const int d = kCandE * threadIdx.x + e;
+    l[e] = -kInf;
+    ix[e] = a.V;
+    if (d < n) {
+      int g = 0;
+      while (g + 1 < G && s_off[g + 1] <= d) ++g;
+      const int64_t at = ((int64_t)row * G + g) * kCandMax + (d - s_off[g]);
+      l[e] = cb.val[at];
+      ix[e] = cb.idx[at];
+    }
+  }
+  put_token(a, row, draw_tempered<kCandE>(l, [&ix](int e) { return ix[e]; }, a, row, nullptr, s));
+}
+
 }  // namespace
 }  // namespace rwkv7
 
+static int64_t cand_bytes(int B, int G) {
+  auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
+  return al((int64_t)B * G * 4) + 2 * al((int64_t)B * G * rwkv7::kCandMax * 4);
+}
+
+extern "C" int64_t rwkv7_sample_workspace_bytes(int32_t B, int32_t V) {
+  using namespace rwkv7;
+  if (B < 1 || V < 1 || V > kSmpMaxV) return 0;
+  return cand_bytes(B, (V + kCandSlice - 1) / kCandSlice);
+}
+
 extern "C" int rwkv7_sample(const void *logits, int32_t logits_dtype, int64_t ld, int32_t B, int32_t V, const rwkv7_sampling *p,
                             uint32_t *seen, int64_t seen_ld, int32_t update_seen, int64_t *out, float *probs,
-                            int64_t probs_ld, void *stream) {
+                            int64_t probs_ld, void *workspace, int64_t workspace_bytes, void *stream) {
   using namespace rwkv7;
   if (!logits || !p || !out || B < 1 || (update_seen && !seen)) return RWKV7_EINVAL;
   if (logits_dtype < 0 || logits_dtype > 2) return RWKV7_EINVAL;
@@ -442,6 +602,31 @@ extern "C" int rwkv7_sample(const void *logits, int32_t logits_dtype, int64_t ld
   a.probs_ld = probs_ld;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const bool vec = reinterpret_cast<uintptr_t>(logits) % 16 == 0 && ld % 8 == 0 && V % 8 == 0;
+  const int G = (V + kCandSlice - 1) / kCandSlice;
+  const bool cand = workspace && workspace_bytes >= cand_bytes(B, G) && a.temp > 0.f && a.top_k >= 1 &&
+                    a.top_k <= kCandMax && a.top_k < V && !probs && G >= 2;
+  if (cand) {
+    char *w = static_cast<char *>(workspace);
+    const int64_t c0 = cand_bytes(B, G) - 2 * (((int64_t)B * G * kCandMax * 4 + 255) / 256 * 256);
+    CandBuf cb;
+    cb.cnt = reinterpret_cast<int *>(w);
+    cb.val = reinterpret_cast<float *>(w + c0);
+    cb.idx = reinterpret_cast<int *>(w + c0 + ((int64_t)B * G * kCandMax * 4 + 255) / 256 * 256);
+    cb.G = G;
+    switch (logits_dtype) {
+      case 0: sample_cand_kernel<0><<<dim3(G, B), kSmpThreads, 0, st>>>(a, cb); break;
+      case 1: sample_cand_kernel<1><<<dim3(G, B), kSmpThreads, 0, st>>>(a, cb); break;
+      default: sample_cand_kernel<2><<<dim3(G, B), kSmpThreads, 0, st>>>(a, cb); break;
+    }
+    RWKV7_CHECK_LAUNCH();
+    switch (logits_dtype) {
+      case 0: vec ? sample_finish_kernel<true, 0><<<B, kSmpThreads, 0, st>>>(a, cb) : sample_finish_kernel<false, 0><<<B, kSmpThreads, 0, st>>>(a, cb); break;
+      case 1: vec ? sample_finish_kernel<true, 1><<<B, kSmpThreads, 0, st>>>(a, cb) : sample_finish_kernel<false, 1><<<B, kSmpThreads, 0, st>>>(a, cb); break;
+      default: vec ? sample_finish_kernel<true, 2><<<B, kSmpThreads, 0, st>>>(a, cb) : sample_finish_kernel<false, 2><<<B, kSmpThreads, 0, st>>>(a, cb); break;
+    }
+    RWKV7_CHECK_LAUNCH();
+    return RWKV7_OK;
+  }
   switch (logits_dtype) {
     case 0: vec ? sample_kernel<true, 0><<<B, kSmpThreads, 0, st>>>(a) : sample_kernel<false, 0><<<B, kSmpThreads, 0, st>>>(a); break;
     case 1: vec ? sample_kernel<true, 1><<<B, kSmpThreads, 0, st>>>(a) : sample_kernel<false, 1><<<B, kSmpThreads, 0, st>>>(a); break;

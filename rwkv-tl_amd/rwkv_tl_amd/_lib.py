@@ -61,6 +61,7 @@ SYMBOLS = (
     "rwkv7_rank_gemv",
     "rwkv7_l2norm_neg_kk_a",
     "rwkv7_gn_rkrk",
+    "rwkv7_sample_workspace_bytes",
     "rwkv7_sample",
 )
 
@@ -184,7 +185,9 @@ def _declare(lib: ctypes.CDLL) -> None:
         "rwkv7_rank_gemv": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp]),
         "rwkv7_l2norm_neg_kk_a": (ctypes.c_int, [vp, vp, vp, vp, i32, i32, vp]),
         "rwkv7_gn_rkrk": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, vp]),
-        "rwkv7_sample": (ctypes.c_int, [vp, i32, i64, i32, i32, ctypes.POINTER(Sampling), vp, i64, i32, vp, vp, i64, vp]),
+        "rwkv7_sample_workspace_bytes": (i64, [i32, i32]),
+        "rwkv7_sample": (ctypes.c_int, [vp, i32, i64, i32, i32, ctypes.POINTER(Sampling), vp, i64, i32, vp, vp, i64,
+                                        vp, i64, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

@@ -3,7 +3,9 @@
 ``sample_logits`` keeps the reference's signature and semantics: repetition
 penalty on ``seen``, greedy argmax when ``temperature`` is None or <= 0, else
 temperature, top-k, top-p and one draw, along the last dimension. All of it is
-one launch of the HIP kernel ``rwkv7_sample`` (one workgroup per row). The
+one call of ``rwkv7_sample``: one workgroup per row, or for top-k sampling
+one workgroup per 2048 logits that keeps its slice's candidates and a second
+launch that draws from them (the same token either way). The
 draw comes from a counter-based generator (Philox4x32-10) keyed by a seed
 taken from torch's CPU generator, so ``torch.manual_seed`` makes it
 reproducible without a device sync; it is a different random stream from
@@ -84,9 +86,12 @@ def sample_into(
     seen: Tensor | None = None,
     update_seen: bool = False,
     probs: Tensor | None = None,
+    workspace: Tensor | None = None,
 ) -> None:
-    """One ``rwkv7_sample`` launch: logits f16/f32/bf16 [B, V] (unit column stride)
-    -> out int64 [B]; ``seen`` int32 [B, ceil(V/32)]; ``probs`` f32 [B, V]."""
+    """One ``rwkv7_sample`` call: logits f16/f32/bf16 [B, V] (unit column stride)
+    -> out int64 [B]; ``seen`` int32 [B, ceil(V/32)]; ``probs`` f32 [B, V].
+    ``workspace`` (``workspace_for(B, V)``) lets top-k sampling spread each
+    row over many workgroups; the token drawn is the same without it."""
     lib = _lib.load()
     B, V = logits.shape
     if out.dtype != torch.int64 or out.numel() != B or not out.is_contiguous():
@@ -99,9 +104,16 @@ def sample_into(
     rc = lib.rwkv7_sample(
         logits.data_ptr(), _LOGIT_DTYPES[logits.dtype], logits.stride(0), B, V, ctypes.byref(p),
         _lib.ptr(seen), 0 if seen is None else seen.stride(0), int(update_seen), out.data_ptr(),
-        _lib.ptr(probs), 0 if probs is None else probs.stride(0), _lib.stream_handle(),
+        _lib.ptr(probs), 0 if probs is None else probs.stride(0),
+        _lib.ptr(workspace), 0 if workspace is None else workspace.numel(), _lib.stream_handle(),
     )
     _lib.check(rc, "rwkv7_sample")
+
+
+def workspace_for(B: int, V: int, device) -> Tensor:
+    """Device workspace of ``rwkv7_sample`` for B rows of V logits."""
+    n = int(_lib.load().rwkv7_sample_workspace_bytes(B, V))
+    return torch.empty(max(n, 1), dtype=torch.uint8, device=device)
 
 
 def sample_logits(
@@ -122,6 +134,7 @@ def sample_logits(
     sample_into(
         x2, out, temperature=temperature, top_k=top_k, top_p=top_p,
         repetition_penalty=repetition_penalty, seed=draw_seed(), offset=0, seen=bits,
+        workspace=workspace_for(B, V, x.device),
     )
     return out[0] if logits.ndim == 1 else out
 
@@ -138,9 +151,11 @@ class Sampler:
         self.seed = draw_seed() if seed is None else seed
         self.step = 0
         self.seen = torch.zeros(batch, (V + 31) // 32, dtype=torch.int32, device=device)
+        self.workspace = workspace_for(batch, V, device)
 
     def __call__(self, logits: Tensor, out: Tensor) -> None:
         x = _check_logits(logits)
         x2 = x.reshape(1, -1) if x.ndim == 1 else x
-        sample_into(x2, out, **self.cfg, seed=self.seed, offset=self.step, seen=self.seen, update_seen=True)
+        sample_into(x2, out, **self.cfg, seed=self.seed, offset=self.step, seen=self.seen, update_seen=True,
+                    workspace=self.workspace)
         self.step += 1

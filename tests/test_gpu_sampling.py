@@ -19,7 +19,7 @@ import torch
 
 from oracle import sampling_ref as S
 from rwkv_tl_amd import sample_logits
-from rwkv_tl_amd.sampling import Sampler, sample_into, seen_bitmap
+from rwkv_tl_amd.sampling import Sampler, sample_into, seen_bitmap, workspace_for
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -246,3 +246,79 @@ def test_rejects_bad_arguments():
     with pytest.raises(ValueError):
         sample_into(torch.randn(2, 10, device=DEV), out, temperature=1.0, top_k=0, top_p=1.0,
                     repetition_penalty=1.0, seed=0, offset=0)
+
+
+# ---- the many-workgroup top-k path: the same tokens ----------------------------------
+
+
+def _both_paths(logits, B, V, seen=None, offset=0, **kw):
+    """The same call with and without a workspace; returns both token
+    vectors and the slice counts the candidate kernel left in the workspace."""
+    kw = {"top_p": 1.0, "repetition_penalty": 1.0, **kw}
+    ws = workspace_for(B, V, DEV)
+    outs = []
+    for w in (ws, None):
+        out = torch.empty(B, dtype=torch.int64, device=DEV)
+        sample_into(logits, out, seed=11, offset=offset, seen=seen, workspace=w, **kw)
+        outs.append(out.cpu())
+    counts = ws[: B * ((V + 2047) // 2048) * 4].view(torch.int32).cpu()
+    return outs[0], outs[1], counts
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("V", [65536, 50277])
+def test_candidate_path_draws_the_same_tokens(dtype, V):
+    """Top-k sampling with a workspace (one workgroup per 2048 logits keeps
+    its slice's top-k candidates, a second launch draws from them) picks
+    exactly the token the one-workgroup kernel picks, for every row, offset,
+    filter setting and repetition penalty; the slice counts show the
+    candidate path ran (each at least top_k and at most 128, or -1 where a
+    tie group at the slice's threshold overflowed and the row went to the
+    one-workgroup code)."""
+    g = torch.Generator().manual_seed(V)
+    B = 16
+    logits = (torch.randn(B, V, generator=g) * 2).to(dtype).to(DEV)
+    seen = seen_bitmap(torch.randint(0, V, (3000,), generator=g), B, V, DEV)
+    for kw in (dict(temperature=1.0, top_k=50, top_p=0.9), dict(temperature=0.7, top_k=1),
+               dict(temperature=1.3, top_k=128, top_p=0.5), dict(temperature=1.0, top_k=7, repetition_penalty=1.5)):
+        for off in range(3):
+            sn = seen if kw.get("repetition_penalty", 1.0) != 1.0 else None
+            a, b, counts = _both_paths(logits, B, V, seen=sn, offset=off, **kw)
+            assert torch.equal(a, b), (kw, off, a.tolist(), b.tolist())
+            ok = (counts == -1) | ((counts >= kw["top_k"]) & (counts <= 128))
+            assert bool(ok.all()), counts.tolist()
+            if kw["top_k"] <= 50:  # (at 128, bf16's coarse values often tie past 128)
+                assert float((counts > 0).float().mean()) > 0.5, counts.tolist()
+
+
+def test_candidate_path_falls_back_on_a_tie_group():
+    """A slice whose top-k threshold falls in a tie group of more than 128
+    values (here: a constant stretch of the row) marks its count -1 and the
+    row is drawn by the one-workgroup code: still the same token."""
+    B, V = 4, 65536
+    g = torch.Generator().manual_seed(1)
+    logits = (torch.randn(B, V, generator=g) * 0.1).half()
+    logits[:, 4096:8192] = 3.0  # two whole slices tied at the top
+    logits = logits.to(DEV)
+    for off in range(4):
+        a, b, counts = _both_paths(logits, B, V, offset=off, temperature=1.0, top_k=50, top_p=0.9)
+        assert torch.equal(a, b)
+        assert int((counts == -1).sum()) >= B
+        assert all(4096 <= int(t) < 8192 for t in a)
+
+
+def test_sampler_with_workspace_updates_seen_like_without():
+    B, V = 3, 65536
+    logits = (torch.randn(B, V, generator=torch.Generator().manual_seed(2)) * 2).half().to(DEV)
+    runs = []
+    for use_ws in (True, False):
+        smp = Sampler(V, DEV, batch=B, temperature=1.0, top_k=20, top_p=0.95, repetition_penalty=1.2, seed=5)
+        if not use_ws:
+            smp.workspace = None
+        out = torch.empty(B, dtype=torch.int64, device=DEV)
+        toks = []
+        for _ in range(6):
+            smp(logits, out)
+            toks.append(out.cpu().clone())
+        runs.append((torch.stack(toks), smp.seen.cpu()))
+    assert torch.equal(runs[0][0], runs[1][0]) and torch.equal(runs[0][1], runs[1][1])
