@@ -310,7 +310,63 @@ RWKV7_DEV void load8(const void *row_ptr, int i0, int V, float *f) {
 // the kept mass and the draw as described at the top; pr (optional) receives
 // the kept distribution at the indices held. Returns the token on the one
 // thread that draws it, -1 on the others.
-template <int E, class Idx>
+// The top-p threshold when at most kWave values are kept: the largest kept
+// value y with sum_{x >= y} mass(x) > W is the value at the first position
+// of the descending order whose running mass exceeds W (a tie group's
+// members share the value, so where in the group that position falls does
+// not matter). The kept values are compacted to LDS, and wave 0 sorts them
+// (bitonic, one per lane), forms the running masses and picks that value.
+// Returns false (and does nothing else) when more values are kept.
+template <int E>
+RWKV7_DEV bool top_p_in_wave(const float (&l)[E], float m, float top_p, float &thr, SampleLds &s) {
+  int own = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) own += l[e] > -kInf;
+  u64 total;
+  int at = (int)block_excl_scan((u64)own, total, s);
+  if (total > (u64)kWave) return false;  // block-uniform
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (l[e] > -kInf) s.cand[at++] = l[e];
+  __syncthreads();
+  if (threadIdx.x < kWave) {
+    const int L = threadIdx.x;
+    float v = L < (int)total ? s.cand[L] : -kInf;
+    const float mo = opaque(m);
+    u64 z = v > -kInf ? mass(v, mo) : 0ull;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) z += shfl_xor64(z, d);
+    const u64 W = (u64)((double)top_p * (double)z);
+#pragma unroll
+    for (int k = 2; k <= kWave; k <<= 1) {  // descending bitonic sort over the lanes
+#pragma unroll
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        const float o = __shfl_xor(v, j);
+        const bool take_max = ((L & j) == 0) == ((L & k) == 0);
+        v = take_max ? fmaxf(v, o) : fminf(v, o);
+      }
+    }
+    u64 c = v > -kInf ? mass(v, mo) : 0ull;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const u64 o = shfl_up64(c, d);
+      if (L >= d) c += o;
+    }
+    const u64 pass = __ballot(c > W);  // nonzero: the last lane holds z > W
+    const int first = __ffsll((unsigned long long)pass) - 1;
+    const float y = __shfl(v, first);
+    if (L == 0) s.wa[0] = y;
+  }
+  __syncthreads();
+  thr = s.wa[0];
+  __syncthreads();
+  return true;
+}
+
+// FLOOR: before the top-k selection, bound the k-th largest value from below
+// by the k-th largest of the threads' maxima (a saving when every thread holds
+// many values, as in the one-workgroup kernel).
+template <int E, bool FLOOR, class Idx>
 RWKV7_DEV int draw_tempered(float (&l)[E], Idx idx, const SampleArgs &a, int row, float *pr, SampleLds &s) {
   const int V = a.V;
   float lo = kInf, m = -kInf, tmax = -kInf;
@@ -320,11 +376,12 @@ RWKV7_DEV int draw_tempered(float (&l)[E], Idx idx, const SampleArgs &a, int row
   m = tmax;
   block_minmax(lo, m, s);
   float thr = -kInf;  // tokens with x >= thr stay
+  bool small = false;  // at most kWave tokens left after top-k
   if (a.top_k > 0 && a.top_k < V) {  // sampling.py:56-60
     // The k-th largest value is at least the k-th largest of the threads'
     // maxima when k threads hold values: only values from there up take part.
     float floor_k = lo;
-    if (__syncthreads_count(tmax > -kInf) >= a.top_k) {
+    if (FLOOR && __syncthreads_count(tmax > -kInf) >= a.top_k) {
       float tl = tmax > -kInf ? tmax : kInf, th = tmax;
       block_minmax(tl, th, s);
       const float tv[1] = {tmax};
@@ -332,17 +389,24 @@ RWKV7_DEV int draw_tempered(float (&l)[E], Idx idx, const SampleArgs &a, int row
     }
     thr = select_gt<false, E>(l, floor_k, m, m, (u64)(a.top_k - 1), s);
     lo = thr;  // the smallest value top-k keeps
+    small = a.top_k <= kWave;
   }
   if (a.top_p < 1.f) {  // sampling.py:62-68
-    u64 own = 0, z = 0;
-    const float mo = opaque(m);
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
+    for (int e = 0; e < E; ++e)
       if (l[e] < thr) l[e] = -kInf;
-      if (l[e] > -kInf) own += mass(l[e], mo);
+    float tp;
+    if (small && top_p_in_wave<E>(l, m, a.top_p, tp, s)) {
+      thr = tp;
+    } else {
+      u64 own = 0, z = 0;
+      const float mo = opaque(m);
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+        if (l[e] > -kInf) own += mass(l[e], mo);
+      block_excl_scan(own, z, s);
+      thr = select_gt<true, E>(l, lo, m, m, (u64)((double)a.top_p * (double)z), s);
     }
-    block_excl_scan(own, z, s);
-    thr = select_gt<true, E>(l, lo, m, m, (u64)((double)a.top_p * (double)z), s);
   }
   u64 own = 0, z = 0;
   {
@@ -420,7 +484,7 @@ RWKV7_DEV int sample_row(const SampleArgs &a, int row, SampleLds &s) {
   }
 #pragma unroll
   for (int e = 0; e < kSmpE; ++e) l[e] = l[e] / a.temp;
-  return draw_tempered<kSmpE>(l, [base](int e) { return base + e; }, a, row, pr, s);
+  return draw_tempered<kSmpE, true>(l, [base](int e) { return base + e; }, a, row, pr, s);
 }
 
 RWKV7_DEV void put_token(const SampleArgs &a, int row, int token) {
@@ -559,7 +623,7 @@ __global__ __launch_bounds__(kSmpThreads) void sample_finish_kernel(SampleArgs a
       ix[e] = cb.idx[at];
     }
   }
-  put_token(a, row, draw_tempered<kCandE>(l, [&ix](int e) { return ix[e]; }, a, row, nullptr, s));
+  put_token(a, row, draw_tempered<kCandE, false>(l, [&ix](int e) { return ix[e]; }, a, row, nullptr, s));
 }
 
 }  // namespace
