@@ -773,6 +773,7 @@ __global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(typename St::Args 
   __shared__ StageBuf<kCk> s_stage;  // the stager's output; then AkaV, G1, U, G2, Y0
   __shared__ float s_x[6][kCk][kPad];  // w, a (a~), b (b / P), k (k / P), r (r~), v
   __shared__ float s_bh[kCk][kPad], s_kh[kCk][kPad];
+  __shared__ float s_p[kCk][kPad];        // prefix products P_t = D(-1, t]
   __shared__ float s_m[4][kCk][kCk + 1];  // Aba, Aka, Bbr, Bkr
   __shared__ float s_t[kCk][kCk + 1];
   __shared__ float s_gam[kN];
@@ -804,9 +805,17 @@ __global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(typename St::Args 
   }
   __syncthreads();
   bool ok = true;
-  if (tid < kN) {
+  if (tid < kN) {  // wave 0: prefix products P_t, and whether they stay in range
     const int j = tid;
-    // suffix products (b^, k^, gam), exact products of w
+    float P = 1.f;
+#pragma unroll
+    for (int t = 0; t < kCk; ++t) {
+      P *= s_x[0][t][j];
+      s_p[t][j] = P;
+      ok = ok && P >= 1e-30f && P <= 1e30f;  // false for NaN too
+    }
+  } else if (tid < 2 * kN) {  // wave 1: suffix products (b^, k^, gam), exact products of w
+    const int j = tid - kN;
     float Q = 1.f;
 #pragma unroll
     for (int t = kCk - 1; t >= 0; --t) {
@@ -815,12 +824,6 @@ __global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(typename St::Args 
       Q *= s_x[0][t][j];
     }
     s_gam[j] = Q;
-    float P = 1.f;
-#pragma unroll
-    for (int t = 0; t < kCk; ++t) {
-      P *= s_x[0][t][j];
-      ok = ok && P >= 1e-30f && P <= 1e30f;  // false for NaN too
-    }
   }
   const bool fast = __syncthreads_and(ok);  // block-uniform
   if (!fast) {  // token matrices straight from products of w: thread (t, s)
@@ -846,13 +849,12 @@ __global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(typename St::Args 
     s_m[3][t][s] = bkr;
     __syncthreads();
   }
-  if (tid < kN) {  // a~, r~ (and b / P, k / P for the MFMA form) in place
-    const int j = tid;
-    float P = 1.f;
+  {  // a~, r~ (and b / P, k / P for the MFMA form) in place: token tid / 16, 4 channels
+    const int t = tid >> 4, j0 = 4 * (tid & 15);
 #pragma unroll
-    for (int t = 0; t < kCk; ++t) {
-      const float Pp = P;
-      P *= s_x[0][t][j];
+    for (int u = 0; u < 4; ++u) {
+      const int j = j0 + u;
+      const float P = s_p[t][j], Pp = t > 0 ? s_p[t - 1][j] : 1.f;
       s_x[1][t][j] *= Pp;
       s_x[4][t][j] *= P;
       if (fast) {
@@ -972,28 +974,35 @@ __global__ __launch_bounds__(256) void wkv7_chunk_chain_kernel(float *S, const f
 #pragma unroll
   for (int r = 0; r < 4; ++r) st[r] = Sp[(4 * kq + r) * kN + 16 * wv + row];
   const float *R0 = rec + ((int64_t)bi * H + h) * NC * kRecFloats;
-  float4 g1, g2, bh, kh, u, vv;
-  float gam, y0;
-  auto load = [&](int c) {  // the chunk's record, one round of loads
-    const float *R = R0 + (int64_t)c * kRecFloats;
-    g1 = reinterpret_cast<const float4 *>(R + kRecG1)[tid];
-    g2 = reinterpret_cast<const float4 *>(R + kRecG2)[tid];
-    bh = reinterpret_cast<const float4 *>(R + kRecBh)[tid];
-    kh = reinterpret_cast<const float4 *>(R + kRecKh)[tid];
-    u = reinterpret_cast<const float4 *>(R + kRecU)[64 * q + lane];
-    vv = reinterpret_cast<const float4 *>(R + kRecV)[64 * q + lane];
-    gam = R[kRecGam + 16 * wv + row];
-    y0 = R[kRecY0 + 256 * q + tid];
+  // this lane's operands of one chunk record
+  struct Ops {
+    float4 g1, g2, bh, kh, u, vv;
+    float gam, y0;
   };
-  load(0);
-  for (int c = 0; c < NC; ++c) {
-    const float G1[4] = {g1.x, g1.y, g1.z, g1.w}, G2[4] = {g2.x, g2.y, g2.z, g2.w};
-    const float BH[4] = {bh.x, bh.y, bh.z, bh.w}, KH[4] = {kh.x, kh.y, kh.z, kh.w};
-    const float U[4] = {u.x, u.y, u.z, u.w}, V[4] = {vv.x, vv.y, vv.z, vv.w};
-    const float GAM = gam, Y0 = y0;
-    if (c + 1 < NC) load(c + 1);  // the next record streams in meanwhile
+  auto load = [&](Ops &o, int c) {  // one round of loads
+    const float *R = R0 + (int64_t)c * kRecFloats;
+    o.g1 = reinterpret_cast<const float4 *>(R + kRecG1)[tid];
+    o.g2 = reinterpret_cast<const float4 *>(R + kRecG2)[tid];
+    o.bh = reinterpret_cast<const float4 *>(R + kRecBh)[tid];
+    o.kh = reinterpret_cast<const float4 *>(R + kRecKh)[tid];
+    o.u = reinterpret_cast<const float4 *>(R + kRecU)[64 * q + lane];
+    o.vv = reinterpret_cast<const float4 *>(R + kRecV)[64 * q + lane];
+    o.gam = R[kRecGam + 16 * wv + row];
+    o.y0 = R[kRecY0 + 256 * q + tid];
+  };
+  auto step = [&](const Ops &o, int c) {
+    const float G1[4] = {o.g1.x, o.g1.y, o.g1.z, o.g1.w}, G2[4] = {o.g2.x, o.g2.y, o.g2.z, o.g2.w};
+    const float BH[4] = {o.bh.x, o.bh.y, o.bh.z, o.bh.w}, KH[4] = {o.kh.x, o.kh.y, o.kh.z, o.kh.w};
+    const float U[4] = {o.u.x, o.u.y, o.u.z, o.u.w}, V[4] = {o.vv.x, o.vv.y, o.vv.z, o.vv.w};
 #pragma unroll
     for (int r = 0; r < 4; ++r) s_s[4 * kq + r][16 * wv + row] = st[r];
+    // S diag(gam) + V^T K^ does not depend on Sig: formed while the barrier
+    // and the Sig products run
+    floatx4 acc;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = st[r] * o.gam;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) acc = mfma4(V[kk], KH[kk], acc);
     __syncthreads();
     // Sig^T and Y over this wave's 16 key columns: D[t][i] = sum_j G[t][j] S[i][j]
     floatx4 xa = {0.f, 0.f, 0.f, 0.f}, ya = {0.f, 0.f, 0.f, 0.f};
@@ -1011,22 +1020,34 @@ __global__ __launch_bounds__(256) void wkv7_chunk_chain_kernel(float *S, const f
     __syncthreads();
     {  // y of token t, value row 16 q + i
       const int t = tid >> 4, i = tid & 15, tt = c * kCk + t;
-      const float yv = ((s_yp[0][t][i] + s_yp[1][t][i]) + (s_yp[2][t][i] + s_yp[3][t][i])) + Y0;
+      const float yv = ((s_yp[0][t][i] + s_yp[1][t][i]) + (s_yp[2][t][i] + s_yp[3][t][i])) + o.y0;
       if (tt < T) y[((int64_t)bi * T + tt) * C + h * kN + 16 * q + i] = from_f<TY>(yv);
     }
-    // S <- S diag(gam) + Sig^T B^ + V^T K^ (this wave's 16 columns)
-    floatx4 acc;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) acc[r] = st[r] * GAM;
+    // S <- S diag(gam) + V^T K^ + Sig^T B^ (this wave's 16 columns)
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int t = 4 * kk + kq;
       const float xv = ((s_xp[0][t][row] + s_xp[1][t][row]) + (s_xp[2][t][row] + s_xp[3][t][row])) + U[kk];
       acc = mfma4(xv, BH[kk], acc);
     }
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) acc = mfma4(V[kk], KH[kk], acc);
     st = acc;
+  };
+  // the next kPf records are in flight while a chunk is carried (one, two
+  // or four measured alike: the step is bound by its barriers and dependent
+  // MFMAs, not by the loads)
+  constexpr int kPf = 2;
+  Ops ops[kPf];
+#pragma unroll
+  for (int i = 0; i < kPf; ++i)
+    if (i < NC) load(ops[i], i);
+  for (int c0 = 0; c0 < NC; c0 += kPf) {
+#pragma unroll
+    for (int i = 0; i < kPf; ++i) {
+      if (c0 + i < NC) {
+        step(ops[i], c0 + i);
+        if (c0 + i + kPf < NC) load(ops[i], c0 + i + kPf);
+      }
+    }
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) Sp[(4 * kq + r) * kN + 16 * wv + row] = st[r];
