@@ -114,10 +114,11 @@ int launch_wkv7_prefill(const PrefillScanArgs &p, hipStream_t st);
 // Chunked wkv7 (16-token chunks on fp32 MFMA, tmix.hip): bytes of the chunk
 // records for B sequences of T tokens and H heads, and the operator-level
 // launch (the same arguments as launch_wkv7_scan, no state history).
-// prefill_chunked: the model's prefill takes the chunked scan -- sequences of
-// at least kChunkMinT tokens whose serial scan (4 H B workgroups) would leave
-// CUs idle (measured on MI355X: 1 x 128 and 1 x 512 at 0.4B faster, 8 x 16
-// heads x 128 tokens and 4 x 32 x 1024 slower than the serial scan).
+// prefill_chunked: the model's prefill takes the chunked scan for sequences
+// of at least kChunkMinT tokens (measured on MI355X against the serial scan,
+// whose four workgroups per head each compute the head's gate math: 0.4B
+// 1 x 128 and 1 x 512 and the 1.5B-shaped 4 x 1024 faster; 0.4B 1 x 32 and
+// 1 x 64 slower).
 constexpr int kChunkMinT = 128;
 bool prefill_chunked(int T, int B, int H, int cus);
 int64_t wkv7_chunk_rec_bytes(int B, int T, int H);

@@ -758,7 +758,7 @@ constexpr int kRecG1 = 0, kRecG2 = 1024, kRecBh = 2048, kRecKh = 3072, kRecU = 4
               kRecV = 6144, kRecGam = 7168, kRecFloats = 7232;
 constexpr int kPad = kN + 1;  // a padded 64-channel LDS row
 
-bool prefill_chunked(int T, int B, int H, int cus) { return T >= kChunkMinT && 4 * B * H < cus; }
+bool prefill_chunked(int T, int, int, int) { return T >= kChunkMinT; }
 
 int64_t wkv7_chunk_rec_bytes(int B, int T, int H) {
   return (int64_t)((T + kCk - 1) / kCk) * H * B * kRecFloats * 4;
