@@ -758,7 +758,14 @@ constexpr int kRecG1 = 0, kRecG2 = 1024, kRecBh = 2048, kRecKh = 3072, kRecU = 4
               kRecV = 6144, kRecGam = 7168, kRecFloats = 7232;
 constexpr int kPad = kN + 1;  // a padded 64-channel LDS row
 
-bool prefill_chunked(int T, int, int, int) { return T >= kChunkMinT; }
+// the chain kernel addresses a (sequence, head)'s records and a sequence's y
+// through 32-bit buffer offsets
+static bool chunk_offsets_fit(int T, int H, int ybytes) {
+  return (int64_t)((T + kCk - 1) / kCk) * kRecFloats * 4 < (int64_t)INT32_MAX &&
+         (int64_t)T * H * kN * ybytes < (int64_t)INT32_MAX;
+}
+
+bool prefill_chunked(int T, int, int H, int) { return T >= kChunkMinT && chunk_offsets_fit(T, H, 4); }
 
 int64_t wkv7_chunk_rec_bytes(int B, int T, int H) {
   return (int64_t)((T + kCk - 1) / kCk) * H * B * kRecFloats * 4;
@@ -960,10 +967,41 @@ __global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(typename St::Args 
   if (tid < kN / 4) put(kRecGam, s_gam[4 * tid], s_gam[4 * tid + 1], s_gam[4 * tid + 2], s_gam[4 * tid + 3]);
 }
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// One chunk record as the chain workgroup of value quarter q uses it, in LDS:
+// G1, G2, B^, K^ of every wave, U and V of the quarter, Y0 of the quarter
+// ([t * 16 + i]) and gam.
+struct ChainSlot {
+  float4 g[4][4][64];  // [G1, G2, B^, K^][wave][lane]
+  // 1 KiB each: U, V ([lane] float4), Y0 ([t * 16 + i]), gam (the first 64;
+  // the rest is what follows gam in the record, unused)
+  float p5[4][256];
+};
+constexpr int kRing = 3;  // chunk records in LDS: the current one and the next two in flight (two workgroups per CU)
+
+// y store of one element: a raw buffer store, dropped by the hardware when the
+// offset is past the sequence (tokens of the padded last chunk), so every
+// step issues the same memory operations (the wait counts below rely on it)
+RWKV7_DEV void store_y(__amdgpu_buffer_rsrc_t r, unsigned off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, off, 0, 0);
+}
+RWKV7_DEV void store_y(__amdgpu_buffer_rsrc_t r, unsigned off, uint16_t v) {
+  __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, 0);
+}
+RWKV7_DEV void store_y(__amdgpu_buffer_rsrc_t r, unsigned off, bf16_t v) {
+  __builtin_amdgcn_raw_buffer_store_b16(v.bits, r, off, 0, 0);
+}
+
 template <typename TY>
 __global__ __launch_bounds__(256) void wkv7_chunk_chain_kernel(float *S, const float *rec, TY *y, int T, int H) {
   __shared__ float s_s[kCk][kPad];  // the workgroup's 16 state rows
   __shared__ float s_xp[4][kCk][kCk + 1], s_yp[4][kCk][kCk + 1];  // per-block Sig^T / Y partials [t][i]
+  // the ring as separate objects, so that the compiler can tell a read of one
+  // slot from a DMA into another (with one array it waits for every DMA)
+  __shared__ ChainSlot s_rec0, s_rec1, s_rec2;
+  static_assert(kRing == 3, "one object per slot");
+  auto slot_ref = [&](int k) -> ChainSlot & { return k == 0 ? s_rec0 : k == 1 ? s_rec1 : s_rec2; };
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int row = lane & 15, kq = lane >> 4;
   const int h = blockIdx.x >> 2, q = blockIdx.x & 3, bi = blockIdx.y;
@@ -973,37 +1011,63 @@ __global__ __launch_bounds__(256) void wkv7_chunk_chain_kernel(float *S, const f
   floatx4 st;
 #pragma unroll
   for (int r = 0; r < 4; ++r) st[r] = Sp[(4 * kq + r) * kN + 16 * wv + row];
-  const float *R0 = rec + ((int64_t)bi * H + h) * NC * kRecFloats;
-  // this lane's operands of one chunk record
-  struct Ops {
-    float4 g1, g2, bh, kh, u, vv;
-    float gam, y0;
+  // this (sequence, head)'s records, and this sequence's y, as buffers
+  const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(rec + ((int64_t)bi * H + h) * NC * kRecFloats), 0, NC * kRecFloats * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t yr =
+      __builtin_amdgcn_make_buffer_rsrc(y + (int64_t)bi * T * C, 0, (int)((int64_t)T * C * sizeof(TY)), 0x00020000);
+  // Record of chunk c into ring slot c % kRing: five DMAs per wave (16 bytes
+  // per lane landing at lane order): its G1, G2, B^, K^ blocks, then one of
+  // U, V, Y0 (quarter q) or gam. Past the last chunk the last one is loaded
+  // again (unused), so the count per step never changes.
+  auto dma = [&](int c, int slot) {
+    const int cc = c < NC ? c : NC - 1;
+    ChainSlot &sl = slot_ref(slot);
+    const int base = cc * kRecFloats * 4;
+    const int offs[4] = {kRecG1, kRecG2, kRecBh, kRecKh};
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_void_t *)&sl.g[a][wv][0], 16, offs[a] * 4 + (64 * wv + lane) * 16,
+                                               base, 0, 0);
+    // the fifth, one per wave and the same for every wave: U, V, Y0 of
+    // quarter q or 1 KiB from gam on (past the record's end the buffer returns
+    // zeros), into p5[wave] -- a destination the compiler can tell apart from
+    // the other slots, so reading them waits for no DMA
+    const int src5 = wv == 0 ? kRecU * 4 + q * 1024 : wv == 1 ? kRecV * 4 + q * 1024
+                   : wv == 2 ? kRecY0 * 4 + q * 1024 : kRecGam * 4;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_void_t *)&sl.p5[wv][0], 16, src5 + lane * 16, base, 0, 0);
   };
-  auto load = [&](Ops &o, int c) {  // one round of loads
-    const float *R = R0 + (int64_t)c * kRecFloats;
-    o.g1 = reinterpret_cast<const float4 *>(R + kRecG1)[tid];
-    o.g2 = reinterpret_cast<const float4 *>(R + kRecG2)[tid];
-    o.bh = reinterpret_cast<const float4 *>(R + kRecBh)[tid];
-    o.kh = reinterpret_cast<const float4 *>(R + kRecKh)[tid];
-    o.u = reinterpret_cast<const float4 *>(R + kRecU)[64 * q + lane];
-    o.vv = reinterpret_cast<const float4 *>(R + kRecV)[64 * q + lane];
-    o.gam = R[kRecGam + 16 * wv + row];
-    o.y0 = R[kRecY0 + 256 * q + tid];
-  };
-  auto step = [&](const Ops &o, int c) {
-    const float G1[4] = {o.g1.x, o.g1.y, o.g1.z, o.g1.w}, G2[4] = {o.g2.x, o.g2.y, o.g2.z, o.g2.w};
-    const float BH[4] = {o.bh.x, o.bh.y, o.bh.z, o.bh.w}, KH[4] = {o.kh.x, o.kh.y, o.kh.z, o.kh.w};
-    const float U[4] = {o.u.x, o.u.y, o.u.z, o.u.w}, V[4] = {o.vv.x, o.vv.y, o.vv.z, o.vv.w};
+  // At the wait of chunk c's step, the memory operations issued after its
+  // DMAs number at least 5 (kRing - 2) (the later records of the prologue),
+  // so waiting for that many outstanding leaves chunk c's own complete.
+  constexpr int kVm = 5 * (kRing - 2);
+  static_assert(kVm < 16, "vmcnt field (low bits only)");
+  constexpr int kWaitRec = 0x0F70 | kVm;
+#pragma unroll
+  for (int c = 0; c < kRing - 1; ++c) dma(c, c);
+  // slot: c % kRing, a constant in the unrolled loop below, so that the
+  // compiler sees the reads of one slot apart from the DMAs into another
+  auto step = [&](int c, int slot) {
+    const ChainSlot &sl = slot_ref(slot);
 #pragma unroll
     for (int r = 0; r < 4; ++r) s_s[4 * kq + r][16 * wv + row] = st[r];
-    // S diag(gam) + V^T K^ does not depend on Sig: formed while the barrier
-    // and the Sig products run
+    __builtin_amdgcn_s_waitcnt(kWaitRec);  // this wave's DMAs of chunk c have landed
+    // everyone's have, and the state tile is in LDS: a bare barrier after the
+    // LDS stores (a memory fence would also wait for the DMAs still in flight)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    dma(c + kRing - 1, (slot + kRing - 1) % kRing);  // the slot of chunk c - 1: its readers passed the barrier
+    const float4 g1 = sl.g[0][wv][lane], g2 = sl.g[1][wv][lane], kh = sl.g[3][wv][lane];
+    const float4 vv = reinterpret_cast<const float4 *>(sl.p5[1])[lane];
+    const float G1[4] = {g1.x, g1.y, g1.z, g1.w}, G2[4] = {g2.x, g2.y, g2.z, g2.w};
+    const float V[4] = {vv.x, vv.y, vv.z, vv.w}, KH[4] = {kh.x, kh.y, kh.z, kh.w};
+    // S diag(gam) + V^T K^ does not depend on Sig: formed while the Sig
+    // products run
+    const float gam = sl.p5[3][16 * wv + row];
     floatx4 acc;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) acc[r] = st[r] * o.gam;
+    for (int r = 0; r < 4; ++r) acc[r] = st[r] * gam;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) acc = mfma4(V[kk], KH[kk], acc);
-    __syncthreads();
     // Sig^T and Y over this wave's 16 key columns: D[t][i] = sum_j G[t][j] S[i][j]
     floatx4 xa = {0.f, 0.f, 0.f, 0.f}, ya = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1017,13 +1081,10 @@ __global__ __launch_bounds__(256) void wkv7_chunk_chain_kernel(float *S, const f
       s_xp[wv][4 * kq + r][row] = xa[r];
       s_yp[wv][4 * kq + r][row] = ya[r];
     }
-    __syncthreads();
-    {  // y of token t, value row 16 q + i
-      const int t = tid >> 4, i = tid & 15, tt = c * kCk + t;
-      const float yv = ((s_yp[0][t][i] + s_yp[1][t][i]) + (s_yp[2][t][i] + s_yp[3][t][i])) + o.y0;
-      if (tt < T) y[((int64_t)bi * T + tt) * C + h * kN + 16 * q + i] = from_f<TY>(yv);
-    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     // S <- S diag(gam) + V^T K^ + Sig^T B^ (this wave's 16 columns)
+    const float4 bh = sl.g[2][wv][lane], u = reinterpret_cast<const float4 *>(sl.p5[0])[lane];
+    const float BH[4] = {bh.x, bh.y, bh.z, bh.w}, U[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int t = 4 * kk + kq;
@@ -1031,24 +1092,19 @@ __global__ __launch_bounds__(256) void wkv7_chunk_chain_kernel(float *S, const f
       acc = mfma4(xv, BH[kk], acc);
     }
     st = acc;
-  };
-  // the next kPf records are in flight while a chunk is carried (one, two
-  // or four measured alike: the step is bound by its barriers and dependent
-  // MFMAs, not by the loads)
-  constexpr int kPf = 2;
-  Ops ops[kPf];
-#pragma unroll
-  for (int i = 0; i < kPf; ++i)
-    if (i < NC) load(ops[i], i);
-  for (int c0 = 0; c0 < NC; c0 += kPf) {
-#pragma unroll
-    for (int i = 0; i < kPf; ++i) {
-      if (c0 + i < NC) {
-        step(ops[i], c0 + i);
-        if (c0 + i + kPf < NC) load(ops[i], c0 + i + kPf);
-      }
+    {  // y of token t, value row 16 q + i (past the sequence: dropped by the buffer)
+      const int t = tid >> 4, i = tid & 15, tt = c * kCk + t;
+      const float yv = ((s_yp[0][t][i] + s_yp[1][t][i]) + (s_yp[2][t][i] + s_yp[3][t][i])) + sl.p5[2][tid];
+      const unsigned off = tt < T ? (unsigned)(((int64_t)tt * C + h * kN + 16 * q + i) * sizeof(TY)) : 0xFFFFFFF0u;
+      store_y(yr, off, from_f<TY>(yv));
     }
+  };
+  for (int c0 = 0; c0 < NC; c0 += kRing) {
+#pragma unroll
+    for (int k = 0; k < kRing; ++k)
+      if (c0 + k < NC) step(c0 + k, k);
   }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // the clamped DMAs land before the workgroup's LDS is reused
 #pragma unroll
   for (int r = 0; r < 4; ++r) Sp[(4 * kq + r) * kN + 16 * wv + row] = st[r];
 }
@@ -1068,6 +1124,7 @@ static int launch_chunked(const typename St::Args &p, float *S, TY *y, float *re
 template <typename TI, typename TW, typename TY>
 int launch_wkv7_chunked(const ScanArgs<TI, TW, TY> &p, float *rec, hipStream_t st) {
   if (p.T <= 0 || p.B <= 0 || p.H <= 0) return RWKV7_OK;
+  if (!chunk_offsets_fit(p.T, p.H, (int)sizeof(TY))) return RWKV7_ESHAPE;
   return launch_chunked<RawStager<kCk, TI, TW, TY>, TY>(p, p.S, p.y, rec, p.B, p.T, p.H, st);
 }
 template int launch_wkv7_chunked<uint16_t, float, uint16_t>(const ScanArgs<uint16_t, float, uint16_t> &, float *,
