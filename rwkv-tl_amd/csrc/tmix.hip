@@ -21,10 +21,12 @@ namespace rwkv7 {
 // ---------------------------------------------------------------------------
 
 
+constexpr int kMaxRanks = 512;  // SR = rv + rw + ra + rg of the batched decode core
+
 template <bool BF>
 __global__ __launch_bounds__(256) void tmix_decode_kernel(TmixDecodeArgs a) {
   using T16 = F16T<BF>;
-  __shared__ float s_lora[512];
+  __shared__ float s_lora[kMaxRanks];
   __shared__ float s_d[4][kN];
   __shared__ float s_r[kN], s_w[kN], s_k[kN], s_v[kN], s_a[kN], s_b[kN], s_g[kN], s_y[kN];
   __shared__ float s_rk;
@@ -127,6 +129,8 @@ __global__ __launch_bounds__(256) void tmix_decode_kernel(TmixDecodeArgs a) {
 }
 
 int launch_tmix_decode(const TmixDecodeArgs &a, int B, hipStream_t st) {
+  // the LoRA rows are read 8 ranks (16 bytes) at a time, all ranks staged in LDS
+  if (a.rv + a.rw + a.ra + a.rg > kMaxRanks || a.rv % 8 || a.rw % 8 || a.ra % 8 || a.rg % 8) return RWKV7_ESHAPE;
   if (a.bf) tmix_decode_kernel<true><<<dim3(a.H, B), 256, 0, st>>>(a);
   else tmix_decode_kernel<false><<<dim3(a.H, B), 256, 0, st>>>(a);
   RWKV7_CHECK_LAUNCH();
