@@ -90,6 +90,36 @@ def test_wkv7_chunked_strong_decay(w_low, cuda):
     torch.testing.assert_close(y.cpu().float(), y_ref.float(), rtol=2e-3, atol=2e-3)
 
 
+@pytest.mark.parametrize("chunked", [False, True], ids=["serial", "chunked"])
+def test_wkv7_closed_forms(chunked, cuda):
+    """Two closed forms of the recurrence (both algorithms, three 16-token
+    chunks): with w = 1 and a = b = 0 the state accumulates sum_t v_t k_t^T
+    and y_t = S_t r_t; with k = v = 0 and a = b = 0 each key column of the
+    state decays by the product of its w."""
+    B, H, T, N = 2, 3, 48, 64
+    g = torch.Generator().manual_seed(12)
+    S0 = torch.randn(B, H, N, N, generator=g, dtype=torch.float64) * 0.1
+    r, k, v = (torch.randn(B, T, H, N, generator=g).half() for _ in range(3))
+    zero = torch.zeros(B, T, H, N).half()
+    # accumulation: S_t = S_0 + sum_{s<=t} v_s k_s^T
+    S = S0.float().to(cuda)
+    y = K.wkv7(S, r.to(cuda), torch.ones(B, T, H, N).to(cuda), k.to(cuda), v.to(cuda), zero.to(cuda),
+               zero.to(cuda), chunked=chunked)
+    vk = torch.einsum("bthi,bthj->bthij", v.double(), k.double()).cumsum(1)  # [B, T, H, N, N]
+    St = S0.unsqueeze(1) + vk
+    y_ref = torch.einsum("bthij,bthj->bthi", St, r.double())
+    torch.cuda.synchronize()
+    assert _rel(S.cpu(), St[:, -1]) < 1e-5
+    torch.testing.assert_close(y.cpu().double(), y_ref, rtol=2e-3, atol=2e-2)
+    # decay: S_T = S_0 diag(prod_t w_t)
+    w = torch.exp(-torch.exp(torch.randn(B, T, H, N, generator=g) * 0.5 - 0.5))
+    S = S0.float().to(cuda)
+    K.wkv7(S, r.to(cuda), w.to(cuda), zero.to(cuda), zero.to(cuda), zero.to(cuda), zero.to(cuda), chunked=chunked)
+    torch.cuda.synchronize()
+    want = S0 * w.double().prod(1).unsqueeze(2)  # column j scaled by prod_t w_t[j]
+    assert _rel(S.cpu(), want) < 1e-5
+
+
 def test_wkv7_chunked_long_sequence_agrees_with_serial(cuda):
     """T = 1024 (the C5 prefill length) in bfloat16: the chunked and serial
     algorithms agree on the final state to 1e-4 relative and on y to bf16
