@@ -427,8 +427,6 @@ struct BigGroup {
   int nprob, M, m_tiles, tiles;
 };
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 // NW waves as a 2 x (NW / 2) grid over the tile.
 template <int BM, int BN, int NW, bool BF>
 RWKV7_DEV void gemm_big_tile(const BigGroup &g) {
@@ -444,7 +442,9 @@ RWKV7_DEV void gemm_big_tile(const BigGroup &g) {
   constexpr int kWaitImm = 0x0F70 | (kVm & 15) | ((kVm >> 4) << 14);
   __shared__ __align__(16) u32x4 lds[kBigNB][SA + SB][64];
 
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  // wv in a scalar register: each wave's DMA operands (buffer, LDS address)
+  // derive from it
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // tile of this workgroup: XCD x = blockIdx % 8 takes tiles [x * per, (x+1) * per)
   const int per = (g.tiles + 7) / 8;
   const int tile = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
@@ -481,9 +481,8 @@ RWKV7_DEV void gemm_big_tile(const BigGroup &g) {
   // the stage a scalar one
   const int64_t rows = isA ? M : wfrag ? (int64_t)(N + 15) / 16 * 16 : N;
   const int64_t ld = isA ? P.lda : wfrag ? (int64_t)P.nksf * 32 : P.ldw;
-  const __amdgpu_buffer_rsrc_t rsrc =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), 0, (int)min<int64_t>(rows * ld * 2, 0x7fffffff),
-                                        0x00020000);
+  const int64_t nbytes = rows * ld * 2;  // integer clamp: the descriptor words stay in scalar registers
+  const i32x4 rsrc = buffer_words(base, nbytes > 0x7fffffff ? 0x7fffffff : (int)nbytes);
   const int stage_b = 2 * (wfrag ? 512 : kBigBK);  // bytes per stage (one block in fragment order)
   unsigned off[PERS];
 #pragma unroll
@@ -500,7 +499,7 @@ RWKV7_DEV void gemm_big_tile(const BigGroup &g) {
     const unsigned s2 = (unsigned)(st < nst ? st : nst - 1) * stage_b;
 #pragma unroll
     for (int u = 0; u < PERS; ++u)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void *)(&lds[buf][wv * PERS + u][0]), 16, off[u], s2, 0, 0);
+      dma16(rsrc, lds_addr(&lds[buf][wv * PERS + u][0]), off[u], s2);
   };
 
   const int wm = wv / GN, wn = wv % GN;  // this wave's block of the tile

@@ -24,6 +24,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 // ---- lane permutes ------------------------------------------------------
 
@@ -169,6 +170,38 @@ RWKV7_DEV uint4 ld_stream(const uint4 *p) {
   const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
+
+// Buffer descriptor of `bytes` bytes at p (both wave-uniform), in scalar
+// registers: base address, stride 0, the byte count (accesses past it are
+// dropped, loads read zeros), 32-bit data format.
+RWKV7_DEV i32x4 buffer_words(const void *p, int bytes) {
+  const uint64_t a = (uint64_t)p;
+  return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)a), __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)),
+               __builtin_amdgcn_readfirstlane(bytes), 0x00020000};
+}
+
+// LDS DMA: each lane's 16 bytes at voff + soff of the buffer land at
+// lds + 16 lane (rsrc, lds and soff wave-uniform). Issued as inline assembly,
+// so that the compiler does not track it: it would otherwise wait for every
+// DMA in flight before any LDS access whose alias information it has lost
+// (most accesses of an unrolled loop, and every access of a multi-buffered
+// array), which serialises a ring of prefetches; and a builtin DMA whose
+// operands it cannot prove uniform becomes a loop over lanes. The caller
+// waits for these loads with counts of its own (s_waitcnt vmcnt) and orders
+// LDS reads after them with a barrier that clobbers memory. M0 carries the
+// LDS address; the gfx9 LDS instructions that the compiler emits do not read
+// M0, and one wait state separates its write from the DMA.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+RWKV7_DEV void dma16(i32x4 rsrc, uint32_t lds, int voff, int soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane((int)lds)), "v"(voff), "s"(rsrc),
+                 "s"(__builtin_amdgcn_readfirstlane(soff))
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+RWKV7_DEV uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)p; }
 
 }  // namespace rwkv7
 

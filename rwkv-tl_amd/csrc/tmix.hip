@@ -971,18 +971,17 @@ __global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(typename St::Args 
   if (tid < kN / 4) put(kRecGam, s_gam[4 * tid], s_gam[4 * tid + 1], s_gam[4 * tid + 2], s_gam[4 * tid + 3]);
 }
 
-typedef __attribute__((address_space(3))) void lds_void_t;
 
-// One chunk record as the chain workgroup of value quarter q uses it, in LDS:
-// G1, G2, B^, K^ of every wave, U and V of the quarter, Y0 of the quarter
-// ([t * 16 + i]) and gam.
+
+// One chunk record in LDS as the chain workgroup of value quarter q uses it:
+// G1, G2, B^, K^ of the four column blocks, then 1 KiB pieces: U, V and Y0
+// ([t * 16 + i]) of quarter q and gam (the first 64 floats of its piece; the
+// rest is what follows gam in the record, unused), one piece per wave.
 struct ChainSlot {
-  float4 g[4][4][64];  // [G1, G2, B^, K^][wave][lane]
-  // 1 KiB each: U, V ([lane] float4), Y0 ([t * 16 + i]), gam (the first 64;
-  // the rest is what follows gam in the record, unused)
-  float p5[4][256];
+  float4 g[4][4][64];  // [G1, G2, B^, K^][column block][lane]
+  float p5[4][256];    // [U, V, Y0, gam]
 };
-constexpr int kRing = 3;  // chunk records in LDS: the current one and the next two in flight (two workgroups per CU)
+constexpr int kRing = 3;  // chunk records in LDS: the current one and the next two in flight
 
 // y store of one element: a raw buffer store, dropped by the hardware when the
 // offset is past the sequence (tokens of the padded last chunk), so every
@@ -997,76 +996,84 @@ RWKV7_DEV void store_y(__amdgpu_buffer_rsrc_t r, unsigned off, bf16_t v) {
   __builtin_amdgcn_raw_buffer_store_b16(v.bits, r, off, 0, 0);
 }
 
+// Grid (4 H, B), 256 threads: one value quarter (16 state rows) of a head per
+// workgroup; wave w takes key column block w.
 template <typename TY>
 __global__ __launch_bounds__(256) void wkv7_chunk_chain_kernel(float *S, const float *rec, TY *y, int T, int H) {
-  __shared__ float s_s[kCk][kPad];  // the workgroup's 16 state rows
+  __shared__ float s_s[16][kPad];  // the workgroup's state rows
   __shared__ float s_xp[4][kCk][kCk + 1], s_yp[4][kCk][kCk + 1];  // per-block Sig^T / Y partials [t][i]
-  // the ring as separate objects, so that the compiler can tell a read of one
-  // slot from a DMA into another (with one array it waits for every DMA)
+  // the ring, one object per slot
   __shared__ ChainSlot s_rec0, s_rec1, s_rec2;
   static_assert(kRing == 3, "one object per slot");
   auto slot_ref = [&](int k) -> ChainSlot & { return k == 0 ? s_rec0 : k == 1 ? s_rec1 : s_rec2; };
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  // wv in a scalar register: the DMA's LDS address derives from it
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int cb = wv;  // this wave's key column block
   const int row = lane & 15, kq = lane >> 4;
-  const int h = blockIdx.x >> 2, q = blockIdx.x & 3, bi = blockIdx.y;
+  const int h = blockIdx.x >> 2, bi = blockIdx.y;
+  const int q = blockIdx.x & 3;  // the quarter's value rows 16 q ..
   const int NC = (T + kCk - 1) / kCk, C = H * kN;
-  // lane holds S[16 q + 4 kq + r][16 wv + row], r = 0..3 (the MFMA D layout)
+  // lane holds S[16 q + 4 kq + r][16 cb + row], r = 0..3 (the MFMA D layout)
   float *Sp = S + (((int64_t)bi * H + h) * kN + 16 * q) * kN;
   floatx4 st;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) st[r] = Sp[(4 * kq + r) * kN + 16 * wv + row];
+  for (int r = 0; r < 4; ++r) st[r] = Sp[(4 * kq + r) * kN + 16 * cb + row];
   // this (sequence, head)'s records, and this sequence's y, as buffers
-  const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float *>(rec + ((int64_t)bi * H + h) * NC * kRecFloats), 0, NC * kRecFloats * 4, 0x00020000);
+  const i32x4 rr = buffer_words(rec + ((int64_t)bi * H + h) * NC * kRecFloats, NC * kRecFloats * 4);
   const __amdgpu_buffer_rsrc_t yr =
       __builtin_amdgcn_make_buffer_rsrc(y + (int64_t)bi * T * C, 0, (int)((int64_t)T * C * sizeof(TY)), 0x00020000);
-  // Record of chunk c into ring slot c % kRing: five DMAs per wave (16 bytes
-  // per lane landing at lane order): its G1, G2, B^, K^ blocks, then one of
-  // U, V, Y0 (quarter q) or gam. Past the last chunk the last one is loaded
-  // again (unused), so the count per step never changes.
+  // the record piece that this wave fetches: U, V, Y0 of quarter q or gam
+  const int psrc = wv == 0 ? kRecU * 4 + q * 1024 : wv == 1 ? kRecV * 4 + q * 1024
+                 : wv == 2 ? kRecY0 * 4 + q * 1024 : kRecGam * 4;
+  // Record of chunk c into a ring slot: block cb of G1, G2, B^, K^ and one
+  // piece per wave (16 bytes per lane landing in lane order). Past the last
+  // chunk the last one is loaded again (unused), so the count per step never
+  // changes.
+  constexpr int kDmaPerWave = 5;
   auto dma = [&](int c, int slot) {
     const int cc = c < NC ? c : NC - 1;
     ChainSlot &sl = slot_ref(slot);
     const int base = cc * kRecFloats * 4;
     const int offs[4] = {kRecG1, kRecG2, kRecBh, kRecKh};
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_void_t *)&sl.g[a][wv][0], 16, offs[a] * 4 + (64 * wv + lane) * 16,
-                                               base, 0, 0);
-    // the fifth, one per wave and the same for every wave: U, V, Y0 of
-    // quarter q or 1 KiB from gam on (past the record's end the buffer returns
-    // zeros), into p5[wave] -- a destination the compiler can tell apart from
-    // the other slots, so reading them waits for no DMA
-    const int src5 = wv == 0 ? kRecU * 4 + q * 1024 : wv == 1 ? kRecV * 4 + q * 1024
-                   : wv == 2 ? kRecY0 * 4 + q * 1024 : kRecGam * 4;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_void_t *)&sl.p5[wv][0], 16, src5 + lane * 16, base, 0, 0);
+    for (int a = 0; a < 4; ++a) dma16(rr, lds_addr(&sl.g[a][cb][0]), offs[a] * 4 + (64 * cb + lane) * 16, base);
+    // one piece per wave into p5[wave] (past the record's end the buffer
+    // returns zeros)
+    dma16(rr, lds_addr(&sl.p5[wv][0]), psrc + lane * 16, base);
   };
-  // At the wait of chunk c's step, the memory operations issued after its
-  // DMAs number at least 5 (kRing - 2) (the later records of the prologue),
-  // so waiting for that many outstanding leaves chunk c's own complete.
-  constexpr int kVm = 5 * (kRing - 2);
+  // Each step issues one record's DMAs and then one y store per wave; the
+  // prologue pairs each record with a y store that the buffer drops. So at
+  // the wait of chunk c's step exactly kVm memory operations were issued
+  // after chunk c's DMAs: the y stores of the kRing - 1 steps (or prologue
+  // entries) since, and the DMAs of the kRing - 2 records in between. The
+  // counter counts loads and stores in issue order, so waiting for at most
+  // kVm outstanding waits for chunk c's record and nothing later.
+  constexpr int kVm = kDmaPerWave * (kRing - 2) + (kRing - 1);
   static_assert(kVm < 16, "vmcnt field (low bits only)");
   constexpr int kWaitRec = 0x0F70 | kVm;
 #pragma unroll
-  for (int c = 0; c < kRing - 1; ++c) dma(c, c);
-  // slot: c % kRing, a constant in the unrolled loop below, so that the
-  // compiler sees the reads of one slot apart from the DMAs into another
+  for (int c = 0; c < kRing - 1; ++c) {
+    dma(c, c);
+    store_y(yr, 0xFFFFFFF0u, from_f<TY>(0.f));  // past the buffer: dropped
+  }
+  // slot: c % kRing, a constant in the unrolled loop below, so that every
+  // slot address is a constant offset
   auto step = [&](int c, int slot) {
     const ChainSlot &sl = slot_ref(slot);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) s_s[4 * kq + r][16 * wv + row] = st[r];
+    for (int r = 0; r < 4; ++r) s_s[4 * kq + r][16 * cb + row] = st[r];
     __builtin_amdgcn_s_waitcnt(kWaitRec);  // this wave's DMAs of chunk c have landed
     // everyone's have, and the state tile is in LDS: a bare barrier after the
     // LDS stores (a memory fence would also wait for the DMAs still in flight)
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     dma(c + kRing - 1, (slot + kRing - 1) % kRing);  // the slot of chunk c - 1: its readers passed the barrier
-    const float4 g1 = sl.g[0][wv][lane], g2 = sl.g[1][wv][lane], kh = sl.g[3][wv][lane];
+    const float4 g1 = sl.g[0][cb][lane], g2 = sl.g[1][cb][lane], kh = sl.g[3][cb][lane];
     const float4 vv = reinterpret_cast<const float4 *>(sl.p5[1])[lane];
     const float G1[4] = {g1.x, g1.y, g1.z, g1.w}, G2[4] = {g2.x, g2.y, g2.z, g2.w};
     const float V[4] = {vv.x, vv.y, vv.z, vv.w}, KH[4] = {kh.x, kh.y, kh.z, kh.w};
     // S diag(gam) + V^T K^ does not depend on Sig: formed while the Sig
     // products run
-    const float gam = sl.p5[3][16 * wv + row];
+    const float gam = sl.p5[3][16 * cb + row];
     floatx4 acc;
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[r] = st[r] * gam;
@@ -1076,18 +1083,19 @@ __global__ __launch_bounds__(256) void wkv7_chunk_chain_kernel(float *S, const f
     floatx4 xa = {0.f, 0.f, 0.f, 0.f}, ya = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      const float sv = s_s[row][16 * wv + 4 * kk + kq];
+      const float sv = s_s[row][16 * cb + 4 * kk + kq];
       xa = mfma4(G1[kk], sv, xa);
       ya = mfma4(G2[kk], sv, ya);
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      s_xp[wv][4 * kq + r][row] = xa[r];
-      s_yp[wv][4 * kq + r][row] = ya[r];
+      s_xp[cb][4 * kq + r][row] = xa[r];
+      s_yp[cb][4 * kq + r][row] = ya[r];
     }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     // S <- S diag(gam) + V^T K^ + Sig^T B^ (this wave's 16 columns)
-    const float4 bh = sl.g[2][wv][lane], u = reinterpret_cast<const float4 *>(sl.p5[0])[lane];
+    const float4 bh = sl.g[2][cb][lane];
+    const float4 u = reinterpret_cast<const float4 *>(sl.p5[0])[lane];
     const float BH[4] = {bh.x, bh.y, bh.z, bh.w}, U[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
@@ -1097,8 +1105,8 @@ __global__ __launch_bounds__(256) void wkv7_chunk_chain_kernel(float *S, const f
     }
     st = acc;
     {  // y of token t, value row 16 q + i (past the sequence: dropped by the buffer)
-      const int t = tid >> 4, i = tid & 15, tt = c * kCk + t;
-      const float yv = ((s_yp[0][t][i] + s_yp[1][t][i]) + (s_yp[2][t][i] + s_yp[3][t][i])) + sl.p5[2][tid];
+      const int lt = tid & 255, t = lt >> 4, i = lt & 15, tt = c * kCk + t;
+      const float yv = ((s_yp[0][t][i] + s_yp[1][t][i]) + (s_yp[2][t][i] + s_yp[3][t][i])) + sl.p5[2][lt];
       const unsigned off = tt < T ? (unsigned)(((int64_t)tt * C + h * kN + 16 * q + i) * sizeof(TY)) : 0xFFFFFFF0u;
       store_y(yr, off, from_f<TY>(yv));
     }
@@ -1110,7 +1118,7 @@ __global__ __launch_bounds__(256) void wkv7_chunk_chain_kernel(float *S, const f
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // the clamped DMAs land before the workgroup's LDS is reused
 #pragma unroll
-  for (int r = 0; r < 4; ++r) Sp[(4 * kq + r) * kN + 16 * wv + row] = st[r];
+  for (int r = 0; r < 4; ++r) Sp[(4 * kq + r) * kN + 16 * cb + row] = st[r];
 }
 
 template <class St, typename TY>

@@ -54,12 +54,14 @@ def _rel(x, y):
 @pytest.mark.parametrize("chunked", [False, True], ids=["serial", "chunked"])
 @pytest.mark.parametrize(
     "B,H,T,w_f32",
-    [(8, 16, 128, True), (1, 1, 1, True), (2, 3, 17, False), (1, 4, 33, True), (3, 2, 64, False)],
+    [(8, 16, 128, True), (1, 1, 1, True), (2, 3, 17, False), (1, 4, 33, True), (3, 2, 64, False),
+     (4, 32, 40, False)],
 )
 def test_wkv7_matches_oracle(B, H, T, w_f32, chunked, cuda):
     """Both algorithms (rwkv7_wkv7, rwkv7_wkv7_chunked) against the serial
     fp32 oracle: the state within 1e-5 relative, y (f16) within 2e-3. T = 1,
-    17 and 33 leave the chunked form a partial last chunk."""
+    17, 33 and 40 leave the chunked form a partial last chunk; 8 x 16 and
+    4 x 32 heads fill every CU with chain workgroups."""
     print(f"wkv7 B={B} H={H} T={T} w_f32={w_f32} chunked={chunked}", flush=True)
     S0, r, w, k, v, a, b = _c2_inputs(B, H, T, seed=B * 100 + T, w_f32=w_f32)
     y_ref, S_ref = R.wkv7_scan(S0, r, w, k, v, a, b)
@@ -90,13 +92,15 @@ def test_wkv7_chunked_strong_decay(w_low, cuda):
     torch.testing.assert_close(y.cpu().float(), y_ref.float(), rtol=2e-3, atol=2e-3)
 
 
+@pytest.mark.parametrize("H", [3, 64])
 @pytest.mark.parametrize("chunked", [False, True], ids=["serial", "chunked"])
-def test_wkv7_closed_forms(chunked, cuda):
+def test_wkv7_closed_forms(chunked, H, cuda):
     """Two closed forms of the recurrence (both algorithms, three 16-token
     chunks): with w = 1 and a = b = 0 the state accumulates sum_t v_t k_t^T
     and y_t = S_t r_t; with k = v = 0 and a = b = 0 each key column of the
-    state decays by the product of its w."""
-    B, H, T, N = 2, 3, 48, 64
+    state decays by the product of its w. H = 64 (B H = 128) fills every CU
+    with chain workgroups."""
+    B, T, N = 2, 48, 64
     g = torch.Generator().manual_seed(12)
     S0 = torch.randn(B, H, N, N, generator=g, dtype=torch.float64) * 0.1
     r, k, v = (torch.randn(B, T, H, N, generator=g).half() for _ in range(3))
@@ -120,11 +124,12 @@ def test_wkv7_closed_forms(chunked, cuda):
     assert _rel(S.cpu(), want) < 1e-5
 
 
-def test_wkv7_chunked_long_sequence_agrees_with_serial(cuda):
+@pytest.mark.parametrize("B,H", [(2, 2), (4, 32)])
+def test_wkv7_chunked_long_sequence_agrees_with_serial(B, H, cuda):
     """T = 1024 (the C5 prefill length) in bfloat16: the chunked and serial
     algorithms agree on the final state to 1e-4 relative and on y to bf16
-    rounding."""
-    B, H, T = 2, 2, 1024
+    rounding; 4 x 32 is the C5 shape."""
+    T = 1024
     S0, r, w, k, v, a, b = _c2_inputs(B, H, T, seed=9, w_f32=True)
     ins = [t.to(cuda) for t in (r, w, k, v, a, b)]
     ins = [t.bfloat16() if t.dtype == torch.float16 else t for t in ins]
