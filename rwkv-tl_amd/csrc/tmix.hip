@@ -1194,13 +1194,22 @@ constexpr int kMaxCPer = 16;  // C <= 4096
 
 // Token shift of prefill (demo/rwkv7_torch.py:189-197, 251-254): prev[t] =
 // LN(x0[t-1]) and prev[0] = state; the state becomes LN(x0[T-1]). The
-// workgroup of t = 0 is the only one that touches the state: it reads it and
-// then writes the new value, so there is no cross-workgroup hazard.
+// workgroup that holds row t = 0 is the only one that touches that
+// sequence's state (or that state's column slice): it reads it and then
+// writes the new value, so there is no cross-workgroup hazard.
 //
-// The kernel is latency-bound (one row per workgroup), so every load (this
-// row, the previous one, the last one for t = 0, the LayerNorm vectors and
-// the mix vectors) is issued up front, and the statistics of all three rows
-// share two block reductions (two-pass mean / variance, as ln_row).
+// Two regimes, by the number of rows M:
+// * few rows (decode, short prefills): latency-bound, so every load is issued
+//   up front and a row's output columns are split over `ncs` workgroups;
+//   each reads the whole row for the statistics but only its slice of the
+//   LayerNorm and mix vectors (the 6 mix vectors are most of a row's bytes),
+//   so more CUs share the row's traffic;
+// * many rows (long prefills): bound by the bytes moved into CUs, so a
+//   workgroup takes R consecutive rows and loads the LayerNorm and mix
+//   vectors once for all of them; a row's normalised predecessor is the
+//   previous row's result, kept in registers.
+// Statistics: two-pass mean / variance per row (as ln_row), the rows needed at
+// once sharing two block reductions.
 RWKV7_DEV void block_sum3(float &a, float &b, float &c, float (*red)[4]) {
   a = wave_sum(a);
   b = wave_sum(b);
@@ -1217,8 +1226,10 @@ RWKV7_DEV void block_sum3(float &a, float &b, float &c, float (*red)[4]) {
   c = (red[2][0] + red[2][1]) + (red[2][2] + red[2][3]);
 }
 
+// One row per workgroup, every load up front (measured faster than the
+// kernel below for C <= 1024 below 1024 rows).
 template <int NP>
-__global__ __launch_bounds__(256) void ln_shift_kernel(LnShiftArgs a) {
+__global__ __launch_bounds__(256) void ln_shift_row_kernel(LnShiftArgs a) {
   __shared__ float red[2][3][4];
   const int m = blockIdx.x;
   const int t = m % a.T, b = m / a.T;
@@ -1281,11 +1292,121 @@ __global__ __launch_bounds__(256) void ln_shift_kernel(LnShiftArgs a) {
   }
 }
 
+template <int NP>
+__global__ __launch_bounds__(256) void ln_shift_kernel(LnShiftArgs a, int R, int ncs) {
+  __shared__ float red[2][3][4];
+  const int C = a.C, tid = threadIdx.x, T = a.T;
+  // this workgroup's output columns: blocks i0 .. i0 + per of the NP
+  // 256-column blocks (column tid + 256 i)
+  const int per = NP / ncs, i0 = blockIdx.y * per;
+  auto mine = [&](int i) { return i >= i0 && i < i0 + per; };
+  const int m0 = blockIdx.x * R, m1 = min(a.M, m0 + R);
+  // Row m's inputs: the row, its predecessor unless already normalised, and
+  // for t = 0 of a multi-token sequence its last token (the new state) and
+  // the old state. Loaded before the vectors below and at the end of the
+  // previous row, so that no wait separates them from other loads.
+  float xc[NP], xp[NP], xl[NP];
+  uint16_t st[NP];
+  auto load_row = [&](int m, bool have_prev) {
+    const int t = m % T, b = m / T;
+    const bool need_p = t > 0 && !have_prev, need_l = t == 0 && T > 1;
+    const float *rc = a.x0 + (int64_t)m * C;
+    const float *rp = a.x0 + (int64_t)(need_p ? m - 1 : m) * C;
+    const float *rl = a.x0 + (int64_t)(need_l ? m + T - 1 : m) * C;
+    const uint16_t *sh = a.shift + (int64_t)b * C;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int c = tid + 256 * i;
+      xc[i] = rc[c];
+      xp[i] = need_p ? rp[c] : 0.f;
+      xl[i] = need_l ? rl[c] : 0.f;
+      st[i] = t == 0 && mine(i) ? sh[c] : (uint16_t)0;
+    }
+  };
+  load_row(m0, false);
+  float lw[NP], lb[NP], mu[6][NP];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    lw[i] = lb[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 6; ++j) mu[j][i] = 0.f;
+    if (mine(i)) {
+      const int c = tid + 256 * i;
+      lw[i] = a.ln_w[c];
+      lb[i] = a.ln_b[c];
+#pragma unroll
+      for (int j = 0; j < 6; ++j)
+        if (j < a.n_mix) mu[j][i] = a.mu[(int64_t)j * C + c];
+    }
+  }
+  const float invC = 1.f / (float)C;
+  float prev[NP];  // LN of the row before m (this slice), once computed
+  bool have_prev = false;
+  for (int m = m0; m < m1; ++m) {
+    const int t = m % T, b = m / T;
+    const bool need_p = t > 0 && !have_prev, need_l = t == 0 && T > 1;
+    uint16_t *sh = a.shift + (int64_t)b * C;
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      s0 += xc[i];
+      s1 += xp[i];
+      s2 += xl[i];
+    }
+    block_sum3(s0, s1, s2, red[0]);
+    const float mc = s0 * invC, mp = s1 * invC, ml = s2 * invC;
+    float q0 = 0.f, q1 = 0.f, q2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      q0 += (xc[i] - mc) * (xc[i] - mc);
+      q1 += (xp[i] - mp) * (xp[i] - mp);
+      q2 += (xl[i] - ml) * (xl[i] - ml);
+    }
+    block_sum3(q0, q1, q2, red[1]);
+    const float rc0 = rsqrtf(q0 * invC + kLnEps), rp0 = rsqrtf(q1 * invC + kLnEps), rl0 = rsqrtf(q2 * invC + kLnEps);
+    float xn[NP], pv[NP], ns[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      xn[i] = (xc[i] - mc) * rc0 * lw[i] + lb[i];
+      pv[i] = t == 0 ? u16_to_f(st[i], a.bf) : need_p ? (xp[i] - mp) * rp0 * lw[i] + lb[i] : prev[i];
+      ns[i] = need_l ? (xl[i] - ml) * rl0 * lw[i] + lb[i] : xn[i];
+    }
+    if (m + 1 < m1) load_row(m + 1, true);
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      if (!mine(i)) continue;
+      const int c = tid + 256 * i;
+#pragma unroll
+      for (int j = 0; j < 6; ++j)
+        if (j < a.n_mix) a.out[((int64_t)j * a.M + m) * C + c] = f_to_u16(xn[i] + mu[j][i] * (pv[i] - xn[i]), a.bf);
+      if (t == 0) sh[c] = f_to_u16(ns[i], a.bf);
+      prev[i] = xn[i];
+    }
+    have_prev = true;
+  }
+}
+
 int launch_ln_shift(const LnShiftArgs &a, hipStream_t st) {
-  if (a.C % 256 || a.C > 256 * kMaxCPer || a.n_mix < 1 || a.n_mix > 6) return RWKV7_ESHAPE;
-  switch (a.C / 256) {
-#define RWKV7_LNS_CASE(n) \
-  case n: ln_shift_kernel<n><<<a.M, 256, 0, st>>>(a); break;
+  if (a.C % 256 || a.C > 256 * kMaxCPer || a.n_mix < 1 || a.n_mix > 6 || a.M <= 0 || a.T <= 0) return RWKV7_ESHAPE;
+  const int np = a.C / 256;
+  // about two workgroups per CU: many rows share a workgroup, few rows are
+  // split over column slices (a power of two dividing np); rows of at most
+  // 1024 columns below that take one workgroup each (measured: 0.4B prefill
+  // 1 x 128 1.88 ms against 1.93 with column slices, 1 x 512 3.39 against
+  // 3.43 with the same grid)
+  const int want = 2 * (mk_cus() > 0 ? mk_cus() : 256);
+  int R = 1, ncs = 1;
+  if (a.M >= 2 * want) R = min(8, a.M / want);
+  else
+    while (ncs * 2 <= np && np % (ncs * 2) == 0 && (int64_t)a.M * ncs < want) ncs *= 2;
+  const bool row_kernel = R == 1 && np <= 4;
+  const dim3 grid((a.M + R - 1) / R, row_kernel ? 1 : ncs);
+  switch (np) {
+#define RWKV7_LNS_CASE(n)                                            \
+  case n:                                                            \
+    if (row_kernel) ln_shift_row_kernel<n><<<grid, 256, 0, st>>>(a); \
+    else ln_shift_kernel<n><<<grid, 256, 0, st>>>(a, R, ncs);        \
+    break;
     RWKV7_LNS_CASE(1) RWKV7_LNS_CASE(2) RWKV7_LNS_CASE(3) RWKV7_LNS_CASE(4)
     RWKV7_LNS_CASE(5) RWKV7_LNS_CASE(6) RWKV7_LNS_CASE(7) RWKV7_LNS_CASE(8)
     RWKV7_LNS_CASE(9) RWKV7_LNS_CASE(10) RWKV7_LNS_CASE(11) RWKV7_LNS_CASE(12)

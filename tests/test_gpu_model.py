@@ -268,6 +268,64 @@ def test_1p5b_shape_long_prefill_and_batch64_properties(cuda):
         _check_logits(lgB[b], lgb, f"1.5b B=64 row {b} vs B=1")
 
 
+def test_0p4b_prefill_1024_rows_matches_split_calls(cuda):
+    """A 2 x 512 prefill (1024 rows: the LayerNorm + shift kernel takes two
+    rows per workgroup) equals two calls of 2 x 256 (512 rows: one row per
+    workgroup): fp32 state within 5e-3, the shift states and the next
+    decode's logits within the logit tolerance."""
+    print("0.4b 2x512 prefill vs 2 x (2x256)", flush=True)
+    _CACHE.clear()
+    sd = make_random_state_dict("0.4b", seed=0, dtype=torch.float16)
+    w = RWKV7Weight.from_state_dict(sd, device=cuda, dtype=torch.float16)
+    del sd
+    model = RWKV7HIP(w, is_torch_compile=False)
+    V = w.head.shape[0]
+    g = torch.Generator().manual_seed(77)
+    toks = torch.randint(0, V, (2, 512), generator=g).to(cuda)
+    nxt = torch.randint(0, V, (2,), generator=g).to(cuda)
+    S1 = State(w.L, w.C, 64, device=cuda, batch=2)
+    model.prefill(toks, S1)
+    S2 = State(w.L, w.C, 64, device=cuda, batch=2)
+    model.prefill(toks[:, :256].contiguous(), S2)
+    model.prefill(toks[:, 256:].contiguous(), S2)
+    for i in range(w.L):
+        r = _rel(S1.tmix[i]["rnn"].cpu(), S2.tmix[i]["rnn"].cpu())
+        assert r < 5e-3, f"layer {i}: one 2x512 prefill vs two of 2x256: {r:.2e}"
+        for key, a, b in (("tmix x", S1.tmix[i]["x"], S2.tmix[i]["x"]), ("cmix x", S1.cmix[i]["x"], S2.cmix[i]["x"])):
+            torch.testing.assert_close(a.float().cpu(), b.float().cpu(), rtol=1e-2, atol=1e-2, msg=f"layer {i} {key}")
+    lg1, _ = model.decode(nxt, S1)
+    lg2, _ = model.decode(nxt, S2)
+    for b in range(2):
+        _check_logits(lg1[b], lg2[b].float(), f"decode row {b} after 2x512 vs 2 x 2x256")
+
+
+@pytest.mark.parametrize("B", [63, 130])
+def test_0p4b_large_batch_decode_rows_match_single_sequences(B, cuda):
+    """Batched one-token steps past the few-row kernel's 16 rows (the
+    multi-launch path with the fused per-head core): two steps; rows 0, a
+    middle one and the last equal the same sequences decoded one at a time by
+    the batch-1 kernel (logits within 1e-2 / 1e-3, fp32 state within 5e-3)."""
+    print(f"0.4b B={B} decode rows vs B=1", flush=True)
+    _CACHE.clear()
+    sd = make_random_state_dict("0.4b", seed=0, dtype=torch.float16)
+    w = RWKV7Weight.from_state_dict(sd, device=cuda, dtype=torch.float16)
+    del sd
+    model = RWKV7HIP(w, is_torch_compile=False)
+    V = w.head.shape[0]
+    g = torch.Generator().manual_seed(B)
+    nxt = torch.randint(0, V, (2, B), generator=g).to(cuda)
+    SB = State(w.L, w.C, 64, device=cuda, batch=B)
+    for step in range(2):
+        lgB, SB = model.decode(nxt[step], SB)
+    for b in (0, B // 2, B - 1):
+        Sb = State(w.L, w.C, 64, device=cuda)
+        for step in range(2):
+            lgb, Sb = model.decode(nxt[step, b : b + 1], Sb)
+        _check_logits(lgB[b], lgb, f"0.4b B={B} row {b} vs B=1")
+        r = _rel(SB.tmix[5]["rnn"][b].cpu(), Sb.tmix[5]["rnn"].cpu())  # batch 1: [H, N, N]
+        assert r < 5e-3, f"B={B} row {b} layer 5 state: {r:.2e}"
+
+
 @pytest.fixture
 def decode_path(request):
     """Sets ``model.decode_path`` for the test and restores "auto" afterwards."""
