@@ -176,6 +176,32 @@ def test_batched_segmented_prefill_matches_oracle(T, cuda):
             assert r < 5e-3, f"layer {i} row {b}: {r:.2e}"
 
 
+def test_many_row_prefill_with_sequence_boundaries_inside_workgroups(cuda):
+    """343 sequences of 3 tokens in one prefill: 1029 rows, so the LayerNorm
+    + shift kernel takes two rows per workgroup and most workgroups straddle
+    a sequence boundary (one row's predecessor is the previous sequence's
+    shift state) and the last one has a single row. Logits of the next token
+    and the states of a spread of rows match the oracle."""
+    print("tiny prefill B=343 T=3", flush=True)
+    st = setup_for("tiny", cuda)
+    V, B, T = st.w.head.shape[0], 343, 3
+    g = torch.Generator().manual_seed(343)
+    prompt = torch.randint(0, V, (B, T), generator=g)
+    nxt = torch.randint(0, V, (B,), generator=g)
+    S = State(st.w.L, st.w.C, 64, device=cuda, batch=B)
+    st.model.prefill(prompt.to(cuda), S)
+    lg, S = st.model.decode(nxt.to(cuda), S)
+    ref = R.new_state(st.w.L, st.w.C, dtype=torch.float16, batch=B)
+    R.prefill(st.ref32, prompt, ref)
+    l32, ref = R.decode(st.ref32, nxt, ref)
+    for b in range(B):
+        _check_logits(lg[b], l32[b], f"B=343 T=3 row {b}")
+    for i in range(st.w.L):
+        for b in (0, 1, 170, 341, 342):
+            r = _rel(S.tmix[i]["rnn"][b].cpu(), ref[0][i]["rnn"][b])
+            assert r < 5e-3, f"layer {i} row {b}: {r:.2e}"
+
+
 @pytest.mark.parametrize("B", [2, 5])
 def test_batched_decode_rows_match_single_sequences(B, cuda):
     print(f"batched decode B={B}", flush=True)
