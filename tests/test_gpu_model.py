@@ -176,16 +176,18 @@ def test_batched_segmented_prefill_matches_oracle(T, cuda):
             assert r < 5e-3, f"layer {i} row {b}: {r:.2e}"
 
 
-def test_many_row_prefill_with_sequence_boundaries_inside_workgroups(cuda):
-    """343 sequences of 3 tokens in one prefill: 1029 rows, so the LayerNorm
-    + shift kernel takes two rows per workgroup and most workgroups straddle
-    a sequence boundary (one row's predecessor is the previous sequence's
-    shift state) and the last one has a single row. Logits of the next token
-    and the states of a spread of rows match the oracle."""
-    print("tiny prefill B=343 T=3", flush=True)
+@pytest.mark.parametrize("B", [343, 2731])
+def test_many_row_prefill_with_sequence_boundaries_inside_workgroups(B, cuda):
+    """B sequences of 3 tokens in one prefill: 1029 or 8193 rows, so the
+    LayerNorm + shift kernel takes 2 or 8 rows per workgroup, most
+    workgroups straddle a sequence boundary (one row's predecessor is the
+    previous sequence's shift state) and the last one has a single row.
+    Logits of the next token and the states of a spread of rows match the
+    oracle."""
+    print(f"tiny prefill B={B} T=3", flush=True)
     st = setup_for("tiny", cuda)
-    V, B, T = st.w.head.shape[0], 343, 3
-    g = torch.Generator().manual_seed(343)
+    V, T = st.w.head.shape[0], 3
+    g = torch.Generator().manual_seed(B)
     prompt = torch.randint(0, V, (B, T), generator=g)
     nxt = torch.randint(0, V, (B,), generator=g)
     S = State(st.w.L, st.w.C, 64, device=cuda, batch=B)
@@ -195,9 +197,9 @@ def test_many_row_prefill_with_sequence_boundaries_inside_workgroups(cuda):
     R.prefill(st.ref32, prompt, ref)
     l32, ref = R.decode(st.ref32, nxt, ref)
     for b in range(B):
-        _check_logits(lg[b], l32[b], f"B=343 T=3 row {b}")
+        _check_logits(lg[b], l32[b], f"B={B} T=3 row {b}")
     for i in range(st.w.L):
-        for b in (0, 1, 170, 341, 342):
+        for b in (0, 1, B // 2, B - 2, B - 1):
             r = _rel(S.tmix[i]["rnn"][b].cpu(), ref[0][i]["rnn"][b])
             assert r < 5e-3, f"layer {i} row {b}: {r:.2e}"
 
