@@ -745,11 +745,12 @@ int prefill_segments(int T, int B, int H, int cus, int *seg_len) {
 //    1e30], otherwise straight from products of w -- solves for T by forward
 //    substitution, and writes G1, G2, B^, K^, U, Y0, V and gam as a chunk
 //    record laid out in the chain kernel's MFMA operand order.
-// 2. wkv7_chunk_chain_kernel, grid (4 H, B): each workgroup carries 16 value
-//    rows of a head's state through the chunks in order; per chunk, Sig and Y
-//    from S (16 x 64 by 64 x 16), then S <- S diag(gam) + Sig^T B^ + V^T K^.
-//    Four waves, one 16-column block of the state each; the Sig and Y
-//    partials of the blocks are summed through LDS in block order.
+// 2. wkv7_chunk_chain_kernel, grid (4 H / NQ, B): each workgroup carries
+//    16 NQ value rows of a head's state through the chunks in order; per
+//    chunk and quarter, Sig and Y from S (16 x 64 by 64 x 16), then
+//    S <- S diag(gam) + Sig^T B^ + V^T K^. Four waves per quarter, one
+//    16-column block of the state each; the Sig and Y partials of the blocks
+//    are summed through LDS in block order.
 // A chunk past the end of the sequence is padded with identity steps (w = 1,
 // a = b = k = r = v = 0), whose outputs are not stored.
 // ---------------------------------------------------------------------------
@@ -973,13 +974,15 @@ __global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(typename St::Args 
 
 
 
-// One chunk record in LDS as the chain workgroup of value quarter q uses it:
+// One chunk record in LDS as a chain workgroup of NQ value quarters uses it:
 // G1, G2, B^, K^ of the four column blocks, then 1 KiB pieces: U, V and Y0
-// ([t * 16 + i]) of quarter q and gam (the first 64 floats of its piece; the
-// rest is what follows gam in the record, unused), one piece per wave.
+// ([t * 16 + i]) of each of its quarters and gam (the first 64 floats of its
+// piece; the rest is what follows gam in the record, unused), one piece per
+// wave (with NQ = 2 the last wave fetches gam again).
+template <int NQ>
 struct ChainSlot {
-  float4 g[4][4][64];  // [G1, G2, B^, K^][column block][lane]
-  float p5[4][256];    // [U, V, Y0, gam]
+  float4 g[4][4][64];   // [G1, G2, B^, K^][column block][lane]
+  float p5[4 * NQ][256];  // U, V, Y0 of each quarter, gam, padding
 };
 constexpr int kRing = 3;  // chunk records in LDS: the current one and the next two in flight
 
@@ -996,22 +999,25 @@ RWKV7_DEV void store_y(__amdgpu_buffer_rsrc_t r, unsigned off, bf16_t v) {
   __builtin_amdgcn_raw_buffer_store_b16(v.bits, r, off, 0, 0);
 }
 
-// Grid (4 H, B), 256 threads: one value quarter (16 state rows) of a head per
-// workgroup; wave w takes key column block w.
-template <typename TY>
-__global__ __launch_bounds__(256) void wkv7_chunk_chain_kernel(float *S, const float *rec, TY *y, int T, int H) {
-  __shared__ float s_s[16][kPad];  // the workgroup's state rows
-  __shared__ float s_xp[4][kCk][kCk + 1], s_yp[4][kCk][kCk + 1];  // per-block Sig^T / Y partials [t][i]
+// Grid (4 H / NQ, B), 256 NQ threads: NQ value quarters (16 state rows each)
+// of a head per workgroup; wave w takes quarter w / 4 of the workgroup and key
+// column block w % 4. With NQ = 2 each record is fetched once for two
+// quarters: at many heads the record stream is what bounds the chain.
+template <typename TY, int NQ>
+__global__ __launch_bounds__(256 * NQ) void wkv7_chunk_chain_kernel(float *S, const float *rec, TY *y, int T, int H) {
+  static_assert(NQ == 1 || NQ == 2, "one or two quarters per workgroup");
+  __shared__ float s_s[16 * NQ][kPad];  // the workgroup's state rows
+  __shared__ float s_xp[NQ][4][kCk][kCk + 1], s_yp[NQ][4][kCk][kCk + 1];  // per-block Sig^T / Y partials [t][i]
   // the ring, one object per slot
-  __shared__ ChainSlot s_rec0, s_rec1, s_rec2;
+  __shared__ ChainSlot<NQ> s_rec0, s_rec1, s_rec2;
   static_assert(kRing == 3, "one object per slot");
-  auto slot_ref = [&](int k) -> ChainSlot & { return k == 0 ? s_rec0 : k == 1 ? s_rec1 : s_rec2; };
+  auto slot_ref = [&](int k) -> ChainSlot<NQ> & { return k == 0 ? s_rec0 : k == 1 ? s_rec1 : s_rec2; };
   // wv in a scalar register: the DMA's LDS address derives from it
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int cb = wv;  // this wave's key column block
+  const int qq = wv >> 2, cb = wv & 3;  // this wave's quarter in the workgroup, key column block
   const int row = lane & 15, kq = lane >> 4;
-  const int h = blockIdx.x >> 2, bi = blockIdx.y;
-  const int q = blockIdx.x & 3;  // the quarter's value rows 16 q ..
+  const int h = blockIdx.x / (4 / NQ), bi = blockIdx.y;
+  const int q = blockIdx.x % (4 / NQ) * NQ + qq;  // the quarter's value rows 16 q ..
   const int NC = (T + kCk - 1) / kCk, C = H * kN;
   // lane holds S[16 q + 4 kq + r][16 cb + row], r = 0..3 (the MFMA D layout)
   float *Sp = S + (((int64_t)bi * H + h) * kN + 16 * q) * kN;
@@ -1022,21 +1028,26 @@ __global__ __launch_bounds__(256) void wkv7_chunk_chain_kernel(float *S, const f
   const i32x4 rr = buffer_words(rec + ((int64_t)bi * H + h) * NC * kRecFloats, NC * kRecFloats * 4);
   const __amdgpu_buffer_rsrc_t yr =
       __builtin_amdgcn_make_buffer_rsrc(y + (int64_t)bi * T * C, 0, (int)((int64_t)T * C * sizeof(TY)), 0x00020000);
-  // the record piece that this wave fetches: U, V, Y0 of quarter q or gam
-  const int psrc = wv == 0 ? kRecU * 4 + q * 1024 : wv == 1 ? kRecV * 4 + q * 1024
-                 : wv == 2 ? kRecY0 * 4 + q * 1024 : kRecGam * 4;
+  // the record piece that this wave fetches: U, V, Y0 of the workgroup's
+  // quarters, then gam (repeated by the waves left over)
+  const int q0 = q - qq;  // the workgroup's first quarter
+  const int psrc = wv < NQ ? kRecU * 4 + (q0 + wv) * 1024 : wv < 2 * NQ ? kRecV * 4 + (q0 + wv - NQ) * 1024
+                 : wv < 3 * NQ ? kRecY0 * 4 + (q0 + wv - 2 * NQ) * 1024 : kRecGam * 4;
   // Record of chunk c into a ring slot: block cb of G1, G2, B^, K^ and one
   // piece per wave (16 bytes per lane landing in lane order). Past the last
   // chunk the last one is loaded again (unused), so the count per step never
   // changes.
-  constexpr int kDmaPerWave = 5;
+  constexpr int kDmaPerWave = 4 / NQ + 1;
   auto dma = [&](int c, int slot) {
     const int cc = c < NC ? c : NC - 1;
-    ChainSlot &sl = slot_ref(slot);
+    ChainSlot<NQ> &sl = slot_ref(slot);
     const int base = cc * kRecFloats * 4;
     const int offs[4] = {kRecG1, kRecG2, kRecBh, kRecKh};
 #pragma unroll
-    for (int a = 0; a < 4; ++a) dma16(rr, lds_addr(&sl.g[a][cb][0]), offs[a] * 4 + (64 * cb + lane) * 16, base);
+    for (int u = 0; u < 4 / NQ; ++u) {
+      const int a = qq * (4 / NQ) + u;  // the waves of column block cb share its four arrays
+      dma16(rr, lds_addr(&sl.g[a][cb][0]), offs[a] * 4 + (64 * cb + lane) * 16, base);
+    }
     // one piece per wave into p5[wave] (past the record's end the buffer
     // returns zeros)
     dma16(rr, lds_addr(&sl.p5[wv][0]), psrc + lane * 16, base);
@@ -1059,21 +1070,21 @@ __global__ __launch_bounds__(256) void wkv7_chunk_chain_kernel(float *S, const f
   // slot: c % kRing, a constant in the unrolled loop below, so that every
   // slot address is a constant offset
   auto step = [&](int c, int slot) {
-    const ChainSlot &sl = slot_ref(slot);
+    const ChainSlot<NQ> &sl = slot_ref(slot);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) s_s[4 * kq + r][16 * cb + row] = st[r];
+    for (int r = 0; r < 4; ++r) s_s[16 * qq + 4 * kq + r][16 * cb + row] = st[r];
     __builtin_amdgcn_s_waitcnt(kWaitRec);  // this wave's DMAs of chunk c have landed
     // everyone's have, and the state tile is in LDS: a bare barrier after the
     // LDS stores (a memory fence would also wait for the DMAs still in flight)
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     dma(c + kRing - 1, (slot + kRing - 1) % kRing);  // the slot of chunk c - 1: its readers passed the barrier
     const float4 g1 = sl.g[0][cb][lane], g2 = sl.g[1][cb][lane], kh = sl.g[3][cb][lane];
-    const float4 vv = reinterpret_cast<const float4 *>(sl.p5[1])[lane];
+    const float4 vv = reinterpret_cast<const float4 *>(sl.p5[NQ + qq])[lane];
     const float G1[4] = {g1.x, g1.y, g1.z, g1.w}, G2[4] = {g2.x, g2.y, g2.z, g2.w};
     const float V[4] = {vv.x, vv.y, vv.z, vv.w}, KH[4] = {kh.x, kh.y, kh.z, kh.w};
     // S diag(gam) + V^T K^ does not depend on Sig: formed while the Sig
     // products run
-    const float gam = sl.p5[3][16 * cb + row];
+    const float gam = sl.p5[3 * NQ][16 * cb + row];
     floatx4 acc;
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[r] = st[r] * gam;
@@ -1083,30 +1094,30 @@ __global__ __launch_bounds__(256) void wkv7_chunk_chain_kernel(float *S, const f
     floatx4 xa = {0.f, 0.f, 0.f, 0.f}, ya = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      const float sv = s_s[row][16 * cb + 4 * kk + kq];
+      const float sv = s_s[16 * qq + row][16 * cb + 4 * kk + kq];
       xa = mfma4(G1[kk], sv, xa);
       ya = mfma4(G2[kk], sv, ya);
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      s_xp[cb][4 * kq + r][row] = xa[r];
-      s_yp[cb][4 * kq + r][row] = ya[r];
+      s_xp[qq][cb][4 * kq + r][row] = xa[r];
+      s_yp[qq][cb][4 * kq + r][row] = ya[r];
     }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     // S <- S diag(gam) + V^T K^ + Sig^T B^ (this wave's 16 columns)
     const float4 bh = sl.g[2][cb][lane];
-    const float4 u = reinterpret_cast<const float4 *>(sl.p5[0])[lane];
+    const float4 u = reinterpret_cast<const float4 *>(sl.p5[qq])[lane];
     const float BH[4] = {bh.x, bh.y, bh.z, bh.w}, U[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int t = 4 * kk + kq;
-      const float xv = ((s_xp[0][t][row] + s_xp[1][t][row]) + (s_xp[2][t][row] + s_xp[3][t][row])) + U[kk];
+      const float xv = ((s_xp[qq][0][t][row] + s_xp[qq][1][t][row]) + (s_xp[qq][2][t][row] + s_xp[qq][3][t][row])) + U[kk];
       acc = mfma4(xv, BH[kk], acc);
     }
     st = acc;
     {  // y of token t, value row 16 q + i (past the sequence: dropped by the buffer)
       const int lt = tid & 255, t = lt >> 4, i = lt & 15, tt = c * kCk + t;
-      const float yv = ((s_yp[0][t][i] + s_yp[1][t][i]) + (s_yp[2][t][i] + s_yp[3][t][i])) + sl.p5[2][lt];
+      const float yv = ((s_yp[qq][0][t][i] + s_yp[qq][1][t][i]) + (s_yp[qq][2][t][i] + s_yp[qq][3][t][i])) + sl.p5[2 * NQ + qq][lt];
       const unsigned off = tt < T ? (unsigned)(((int64_t)tt * C + h * kN + 16 * q + i) * sizeof(TY)) : 0xFFFFFFF0u;
       store_y(yr, off, from_f<TY>(yv));
     }
@@ -1128,7 +1139,12 @@ static int launch_chunked(const typename St::Args &p, float *S, TY *y, float *re
   const int nc = (T + kCk - 1) / kCk;
   wkv7_chunk_prep_kernel<St><<<dim3(nc, H, B), 256, 0, st>>>(p, rec, T, H);
   RWKV7_CHECK_LAUNCH();
-  wkv7_chunk_chain_kernel<TY><<<dim3(4 * H, B), 256, 0, st>>>(S, rec, y, T, H);
+  // two value quarters per workgroup (each record fetched once for both)
+  // where that still leaves a workgroup per CU
+  if (2 * B * H >= (mk_cus() > 0 ? mk_cus() : 256))
+    wkv7_chunk_chain_kernel<TY, 2><<<dim3(2 * H, B), 512, 0, st>>>(S, rec, y, T, H);
+  else
+    wkv7_chunk_chain_kernel<TY, 1><<<dim3(4 * H, B), 256, 0, st>>>(S, rec, y, T, H);
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;
 }
