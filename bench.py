@@ -32,7 +32,14 @@
   HBM peak for each),
   the roofline of the whole step as the caller sees it, and the CPU baseline: the oracle's pure-torch fp32
   model (a port of the reference's ``demo/rwkv7_torch.py``) timed on this
-  host's cores on a bounded sample of the same decode workload.
+  host's cores on a bounded sample of the same decode workload, plus its 1x128
+  prefill, with the host's core counts.
+* Before anything is timed, a correctness gate (as the reference's benchmark
+  has, ``script/benchmark_rwkv7.py:158-182``): the first 8 decode steps of the
+  timed model against the fp32 oracle on the same weights and token ids
+  (logits 1e-2 abs + 1e-3 rel, wkv state 1e-4 relative); on a mismatch the
+  bench prints the gate record and exits non-zero. ``correctness`` in the JSON
+  line holds the record.
 
 ``python bench.py --generate`` prints a different single JSON line instead:
 ``generate`` of 128 tokens after a 16-token prompt on the same model and
@@ -195,18 +202,20 @@ def traffic_from_profile() -> float | None:
     return None
 
 
-def cpu_baseline(shape_name: str, steps: int, warmup: int) -> dict:
-    """The oracle's fp32 pure-torch decode on the host cores (bounded sample)."""
+def host_cores() -> dict:
+    """Cores of this host: all the OS reports, and those this process may run on."""
+    return {"host_logical_cpus": os.cpu_count(), "process_affinity_cpus": len(os.sched_getaffinity(0))}
+
+
+def cpu_baseline(W, steps: int, warmup: int, prefill_t: int) -> dict:
+    """The oracle's fp32 pure-torch decode and prefill on the host cores
+    (bounded sample). ``W`` is the oracle's fp32 model (``R.Weights``)."""
     import torch
 
     from oracle import rwkv7_ref as R
-    from rwkv_tl_amd.checkpoint import make_random_state_dict
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
-    sd = make_random_state_dict(shape_name, seed=0, dtype=torch.float16)
-    W = R.Weights(sd, torch.float32)
-    del sd
     st = R.new_state(W.L, W.C, dtype=torch.float32)
     g = torch.Generator().manual_seed(2)
     toks = torch.randint(0, W.head.shape[0], (steps + warmup,), generator=g)
@@ -217,6 +226,11 @@ def cpu_baseline(shape_name: str, steps: int, warmup: int) -> dict:
         for t in toks[warmup:]:
             R.decode(W, t.reshape(1), st)
         dt = time.perf_counter() - t0
+        tp = torch.randint(0, W.head.shape[0], (prefill_t,), generator=g)
+        sp = R.new_state(W.L, W.C, dtype=torch.float32)
+        t0 = time.perf_counter()
+        R.prefill(W, tp, sp)
+        dp = time.perf_counter() - t0
     cpu_name = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -230,9 +244,45 @@ def cpu_baseline(shape_name: str, steps: int, warmup: int) -> dict:
         "unit": "ms/token",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"0.4B fp32 decode B=1, {steps} timed tokens after {warmup} warm-up, from zero state",
+        "sample": f"0.4B fp32 decode B=1, {steps} timed tokens after {warmup} warm-up, from zero state; "
+                  f"prefill_T{prefill_t}_ms: one 1x{prefill_t} prefill from zero state",
+        f"prefill_T{prefill_t}_ms": round(dp * 1000.0, 1),
         "cpu": cpu_name,
+        **host_cores(),
     }
+
+
+def correctness_gate(graphed, ref_w, toks, steps: int) -> dict:
+    """The reference's benchmark checks each model against the pure-torch one
+    before timing it (script/benchmark_rwkv7.py:158-182,280-284). Here: the
+    first ``steps`` decode steps of the timed model, from a zero state, on the
+    timed token ids, against the fp32 oracle on the same fp16 weights; logits
+    within 1e-2 abs + 1e-3 rel, the fp32 wkv state within 1e-4 relative per
+    layer. Returns the record; the caller exits non-zero when it failed."""
+    import torch
+
+    from oracle import rwkv7_ref as R
+    from rwkv_tl_amd import State
+
+    m = graphed.model
+    S = State(m.L, m.C, 64, device=toks.device)
+    ref = R.new_state(m.L, m.C, dtype=torch.float16)
+    max_d, bad, worst_state = 0.0, 0, 0.0
+    with torch.inference_mode():
+        for i in range(steps):
+            lg, S = graphed.decode(toks[i], S)
+            lr, ref = R.decode(ref_w, toks[i].cpu(), ref)
+            got, want = lg.float().cpu().reshape(-1), lr.float().reshape(-1)
+            d = (got - want).abs()
+            max_d = max(max_d, float(d.max()))
+            bad += int((d > 1e-2 + 1e-3 * want.abs()).sum()) + int((~torch.isfinite(got)).sum())
+    for i in range(m.L):
+        x, y = S.tmix[i]["rnn"].cpu().double(), ref[0][i]["rnn"].double()
+        worst_state = max(worst_state, float((x - y).norm() / y.norm().clamp_min(1e-30)))
+    ok = bad == 0 and worst_state <= 1e-4
+    return {"steps": steps, "oracle": "fp32 pure-torch port (oracle/rwkv7_ref.py) on the same fp16 weights",
+            "logit_bar": "1e-2 abs + 1e-3 rel", "max_abs_logit_diff": round(max_d, 6), "logits_off": bad,
+            "state_bar": 1e-4, "max_state_rel_err": float(f"{worst_state:.3e}"), "pass": ok}
 
 
 def _torch_ops_sample(l, temperature, top_k, top_p):
@@ -449,6 +499,8 @@ def main() -> None:
     ap.add_argument("--cpu-steps", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the headline decode line")
+    ap.add_argument("--no-gate", action="store_true", help="skip the correctness gate against the fp32 oracle")
+    ap.add_argument("--gate-steps", type=int, default=8, help="decode steps the correctness gate checks")
     ap.add_argument("--calib-copy", action="store_true", help="also run a 1 GiB copy kernel (counter calibration)")
     ap.add_argument("--configs", action="store_true",
                     help="time the survey's C2, C4 and C5 configurations instead (one different JSON line)")
@@ -476,6 +528,7 @@ def main() -> None:
 
     import torch
 
+    from oracle import rwkv7_ref as R
     from rwkv_tl_amd import SHAPES, HIPGraph, RWKV7HIP, State
     from rwkv_tl_amd.checkpoint import make_random_state_dict
     from rwkv_tl_amd.weight import RWKV7Weight
@@ -485,6 +538,9 @@ def main() -> None:
     log("building 0.4B weights (seed 0)")
     sd = make_random_state_dict("0.4b", seed=0, dtype=torch.float16)
     w = RWKV7Weight.from_state_dict(sd, device=dev, dtype=torch.float16)
+    # the oracle's fp32 model on the very same weights and embedding rows: the
+    # correctness gate's reference and the CPU baseline
+    ref_w = R.Weights.from_emb(sd, w.emb.cpu(), torch.float32)
     del sd
     model = RWKV7HIP(w, is_torch_compile=False)
     graphed = HIPGraph(model)
@@ -494,6 +550,14 @@ def main() -> None:
     # ---- headline: decode B=1 -------------------------------------------------
     K, Wm = args.steps, args.warmup
     toks = torch.randint(0, V, (K + Wm, 1), generator=g).to(dev)
+    gate = None
+    if not args.no_gate:
+        log(f"correctness gate: {args.gate_steps} decode steps against the fp32 oracle")
+        gate = correctness_gate(graphed, ref_w, toks, args.gate_steps)
+        log(f"correctness gate: {gate}")
+        if not gate["pass"]:
+            print(json.dumps({"metric": METRIC, "value": None, "correctness": gate}), flush=True)
+            raise SystemExit("correctness gate failed: the decode disagrees with the fp32 oracle")
     S = State(w.L, w.C, 64, device=dev)
     log(f"decode B=1: {Wm} warm-up + {K} timed steps")
     for i in range(Wm):
@@ -547,6 +611,7 @@ def main() -> None:
             "batch": 1,
         },
         "tokens_per_s": round(1000.0 / ms_tok, 1),
+        "correctness": gate,
         "roofline_step": {
             "bound": "hbm",
             "achieved": round(step_gbs, 1),
@@ -682,8 +747,8 @@ def main() -> None:
     if args.calib_copy:
         calib_copy()
     if not args.no_cpu:
-        log(f"CPU baseline: {args.cpu_steps} decode steps of the fp32 oracle")
-        out["cpu_baseline"] = cpu_baseline("0.4b", args.cpu_steps, 1)
+        log(f"CPU baseline: {args.cpu_steps} decode steps and a 1x128 prefill of the fp32 oracle")
+        out["cpu_baseline"] = cpu_baseline(ref_w, args.cpu_steps, 1, 128)
     print(json.dumps(out), flush=True)
 
 

@@ -560,12 +560,29 @@ __global__ __launch_bounds__(512) void gemm_big_kernel_128(BigGroup g) { gemm_bi
 __global__ __launch_bounds__(512) void gemm_big_kernel_256_bf(BigGroup g) { gemm_big_tile<256, 256, 8, true>(g); }
 __global__ __launch_bounds__(512) void gemm_big_kernel_128_bf(BigGroup g) { gemm_big_tile<128, 128, 8, true>(g); }
 
+// The large-M kernel reads A and W through buffer resources, whose byte
+// offsets are 32-bit: an operand extent must stay below 2^31 bytes. W (or its
+// fragment copy) is one extent, so a problem whose W spans 2 GiB or more goes
+// to the 64-bit-addressed tiled kernels; A is cut into row blocks of at most
+// big_rows_per_launch(lda) rows, one launch each (A and Y rebased).
+constexpr int64_t kBufMax = 0x7fffffff;
+static bool big_w_addressable(const GemmProb &p) {
+  const int64_t rows = p.Wf ? (int64_t)(p.N + 15) / 16 * 16 : p.N;
+  const int64_t ld = p.Wf ? (int64_t)p.nksf * 32 : p.ldw;
+  return rows * ld * 2 <= kBufMax;
+}
+static int big_rows_per_launch(int64_t lda) {
+  const int64_t rows = kBufMax / (2 * lda) / 256 * 256;  // whole 256-row tiles
+  return (int)(rows < (int64_t)1 << 30 ? rows : (int64_t)1 << 30);
+}
+
 // Problems of the large-M path: K a multiple of 64, at least 256 columns, and
 // enough 128 x 128 tiles for two workgroups per CU (measured: at M = 512 the
 // 32-row tiled kernels with split-K are 2-3x faster; at M = 4096 this path is
 // ~2x faster than them).
 static bool big_fits(const GemmProb &p, int M, int cus) {
-  return p.K % kBigBK == 0 && p.N >= 256 && (int64_t)((M + 127) / 128) * ((p.N + 127) / 128) >= 2 * cus;
+  return p.K % kBigBK == 0 && p.N >= 256 && (int64_t)((M + 127) / 128) * ((p.N + 127) / 128) >= 2 * cus &&
+         big_w_addressable(p) && big_rows_per_launch(p.lda) >= 256;
 }
 
 #define RWKV7_TRY_GEMM(expr)         \
@@ -890,7 +907,19 @@ int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, f
       else rest[nr++] = probs[i];
     }
     if (nb > 0) {
-      RWKV7_TRY_GEMM(launch_big(big, nb, M, cus, st));
+      // row blocks whose A extents stay below 2^31 bytes (big_rows_per_launch)
+      int rows = M;
+      for (int i = 0; i < nb; ++i) rows = min(rows, big_rows_per_launch(big[i].lda));
+      for (int r0 = 0; r0 < M; r0 += rows) {
+        GemmProb blk[kMaxProb];
+        for (int i = 0; i < nb; ++i) {
+          blk[i] = big[i];
+          const int ysz = big[i].epi == GEPI_F32 || big[i].epi == GEPI_ADD_F32 ? 4 : 2;
+          blk[i].A = big[i].A + (int64_t)r0 * big[i].lda;
+          blk[i].Y = static_cast<char *>(big[i].Y) + (int64_t)r0 * big[i].ldy * ysz;
+        }
+        RWKV7_TRY_GEMM(launch_big(blk, nb, min(rows, M - r0), cus, st));
+      }
       if (nr == 0) return RWKV7_OK;
       probs = rest;
       nprob = nr;

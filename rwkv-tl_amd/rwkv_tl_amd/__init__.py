@@ -44,10 +44,12 @@ __all__ = [
     "wrap_model",
 ]
 
-# Backend names of demo/__init__.py:81-120. Every GPU-class name maps to the one
-# HIP model; the NVIDIA-specific variants (mx450, rtx3060) have no meaning on
-# MI355X and are accepted as aliases so existing scripts keep working.
-_HIP_BACKENDS = ("tuned", "auto", "fp16", "hip", "rtx3060", "mx450")
+# Backend names of demo/__init__.py:81-120. The float16 names map to the HIP
+# model; the NVIDIA-specific variants (mx450, rtx3060) have no meaning on
+# MI355X and are accepted as aliases so existing scripts keep working. "auto"
+# picks the bfloat16 model, as demo/__init__.py:98-104 does on every GPU of
+# compute capability 8.0 or newer (the class an MI355X corresponds to).
+_HIP_BACKENDS = ("tuned", "fp16", "hip", "rtx3060", "mx450")
 
 
 def make_rwkv7(
@@ -62,17 +64,19 @@ def make_rwkv7(
     Returns ``RWKV7HIP`` wrapped in ``HIPGraph`` when ``use_graph`` (the
     default) and the device is a GPU; ``backend="bf16"`` returns
     ``RWKV7HIPBF16`` (bfloat16 weights, as ``demo/__init__.py:104-105`` picks
-    ``RWKV7BF16``) and ``backend="int8"`` ``RWKV7HIPInt8`` (batch-1 decode on
-    per-row int8 weights). ``backend="torch"`` raises: the pure-torch
-    reference model is a test oracle here, not a product backend.
+    ``RWKV7BF16``), ``backend="auto"`` the same bfloat16 class (the
+    reference's choice for every GPU of compute capability 8.0 or newer,
+    ``demo/__init__.py:98-104``), and ``backend="int8"`` ``RWKV7HIPInt8``
+    (batch-1 decode on per-row int8 weights). ``backend="torch"`` raises: the
+    pure-torch reference model is a test oracle here, not a product backend.
     """
     device = torch.device(device)
     if backend == "torch":
         raise ValueError("backend 'torch' is not provided: the pure-torch model is only a test oracle here")
-    names = _HIP_BACKENDS + ("bf16", "int8")
+    names = _HIP_BACKENDS + ("auto", "bf16", "int8")
     if backend not in names:
         raise ValueError(f"unknown backend {backend!r} (expected one of {', '.join(names)})")
     if device.type != "cuda":
         raise ValueError(f"RWKV7HIP runs on a ROCm GPU; got device {device}")
-    cls = {"bf16": RWKV7HIPBF16, "int8": RWKV7HIPInt8}.get(backend, RWKV7HIP)
+    cls = {"auto": RWKV7HIPBF16, "bf16": RWKV7HIPBF16, "int8": RWKV7HIPInt8}.get(backend, RWKV7HIP)
     return make_graph_cls(cls) if use_graph else cls

@@ -55,7 +55,9 @@ class RWKV7Model(ABC):
         Each step is decode plus one sampling launch that writes the token into
         a device buffer the next decode reads: no host sync until the final
         ``tolist()``. Repetition penalty applies to the generated tokens only,
-        as in the reference (``seen=out``)."""
+        as in the reference (``seen=out``). A model with ``raise_if_aborted``
+        (the HIP models, also behind ``HIPGraph``) checks after that sync that
+        none of its persistent kernel launches gave up."""
         if isinstance(tokens, Tensor) and tokens.ndim != 1:
             raise ValueError(f"Expected 1D token sequence, got {tokens.shape}")
         if isinstance(tokens, list):
@@ -71,7 +73,11 @@ class RWKV7Model(ABC):
             logits, S = self.decode(token, S)
             sampler(logits, out[i : i + 1])
             token = out[i]
-        return out.tolist(), S
+        ids = out.tolist()
+        check = getattr(self, "raise_if_aborted", None)
+        if check is not None:
+            check()
+        return ids, S
 
     def forward(self, tokens: Tensor, S: State) -> tuple[Tensor, State]:
         """``prefill(tokens[:-1])`` then ``decode(tokens[-1])`` (``_rwkv7_abc.py:74-89``)."""

@@ -9,8 +9,9 @@ Stands in for ``RWKV7FP16`` / ``RWKV7Base`` (``demo/rwkv7_fp16.py:16-25``,
   layer); 2..16 sequences as the few-row persistent kernel (MFMA on 16-row
   weight blocks); more as the MFMA GEMM path with M = batch.
 * ``prefill`` -> ``rwkv7_prefill``: B x T <= 16 rows as the few-row kernel;
-  longer prompts as MFMA GEMMs for every projection and a serial, LDS-staged
-  wkv7 scan per head.
+  longer prompts as MFMA GEMMs for every projection and a wkv7 scan per head:
+  the serial LDS-staged scan (cut into segments from T = 64) below T = 128,
+  the chunked scan (16-token chunks on fp32 MFMA) from T = 128.
 
 ``decode_path = "kernels"`` selects the multi-launch paths throughout.
 
@@ -43,12 +44,18 @@ class RWKV7HIP(RWKV7Model):
             decode streams per-row symmetric int8 copies of the layer matrices
             and the head (f32 row scales, f32 accumulation), about half the
             bytes per token; prefill and batched decode keep the fp16 weights.
+        check_errors: after every ``decode`` / ``prefill``, synchronise and
+            raise ``HipError`` if a persistent kernel of the step gave up a
+            bounded wait (see ``last_error``). Off by default: the check costs
+            a host sync per call. ``generate`` always checks once, after its
+            final sync.
     """
 
     # the 16-bit format of the weights, the shift states and the logits
     kernel_dtype = torch.float16
 
-    def __init__(self, w: RWKV7Weight, *, is_torch_compile: bool = True, weight_quant: str | None = None) -> None:
+    def __init__(self, w: RWKV7Weight, *, is_torch_compile: bool = True, weight_quant: str | None = None,
+                 check_errors: bool = False) -> None:
         super().__init__(w)
         if w.dtype != self.kernel_dtype:
             raise ValueError(f"kernel dtype {self.kernel_dtype} does not match weight dtype {w.dtype}")
@@ -63,6 +70,8 @@ class RWKV7HIP(RWKV7Model):
         self.V = int(self.dev.dims.vocab)
         self._ws: Tensor | None = None
         self._ws_bytes = 0
+        self.check_errors = check_errors
+        self._errors_seen = 0  # aborted launches already reported on the current workspace
 
     # ------------------------------------------------------------------ #
     # buffers and descriptors
@@ -81,6 +90,7 @@ class RWKV7HIP(RWKV7Model):
             # zeroed: the decode kernel's hand-off words at its start must not match any tag
             self._ws = torch.zeros(need, dtype=torch.uint8, device=self.w.device)
             self._ws_bytes = need
+            self._errors_seen = 0  # the error counter lives in the workspace
         return self._ws
 
     @property
@@ -108,6 +118,22 @@ class RWKV7HIP(RWKV7Model):
                                               _lib.stream_handle())
         _lib.check(rc, "rwkv7_workspace_errors")
         return int(n.value)
+
+    def raise_if_aborted(self) -> None:
+        """Raise ``HipError`` if a persistent kernel launch aborted since the
+        last check (synchronises the current stream). An aborted decode wrote
+        NaN logits; an aborted prefill wrote nothing that shows it, and either
+        left the State with only the layers finished before the failure. The
+        persistent kernels abort only when a bounded wait gives up, e.g. when
+        another process or stream held CUs so that the grid was not resident
+        all at once."""
+        n = self.last_error()
+        if n > self._errors_seen:
+            new = n - self._errors_seen
+            self._errors_seen = n
+            raise _lib.HipError(
+                f"{new} persistent kernel launch(es) aborted (a bounded wait gave up); the State holds only the "
+                "layers finished before the failure")
 
     def _check_state(self, S: State) -> None:
         t0 = S[0][0]
@@ -191,6 +217,8 @@ class RWKV7HIP(RWKV7Model):
         self.decode_into(tok, run, logits)
         if shadow:
             _copy_into(S, run)
+        if self.check_errors:
+            self.raise_if_aborted()
         return (logits[0] if S[0][0]["rnn"].dim() == 3 else logits), S
 
     def prefill(self, tokens: Tensor, S: State) -> State:
@@ -214,6 +242,8 @@ class RWKV7HIP(RWKV7Model):
         self.prefill_into(tok, run)
         if shadow:
             _copy_into(S, run)
+        if self.check_errors:
+            self.raise_if_aborted()
         return S
 
 
@@ -236,5 +266,5 @@ class RWKV7HIPBF16(RWKV7HIP):
 class RWKV7HIPInt8(RWKV7HIP):
     """``RWKV7HIP`` whose batch-1 decode streams int8 weights (``weight_quant="int8"``)."""
 
-    def __init__(self, w: RWKV7Weight, *, is_torch_compile: bool = True) -> None:
-        super().__init__(w, is_torch_compile=is_torch_compile, weight_quant="int8")
+    def __init__(self, w: RWKV7Weight, *, is_torch_compile: bool = True, check_errors: bool = False) -> None:
+        super().__init__(w, is_torch_compile=is_torch_compile, weight_quant="int8", check_errors=check_errors)

@@ -214,3 +214,27 @@ def test_bf16_graph_replay_and_factory(cuda):
     lg = la.reshape(1, -1)
     assert lg.dtype == BF
     assert int(sample_logits(lg)[0]) == int(lg.float().argmax())
+
+
+def test_auto_backend_runs_bf16_weights(cuda):
+    """make_rwkv7(dev, backend="auto") on bf16 weights: the reference returns
+    RWKV7BF16 on every GPU of sm >= 80 (demo/__init__.py:98-104), so a caller
+    who loads bfloat16 weights and passes "auto" gets a model that takes them.
+    Its graph-wrapped decode follows the same model's eager decode bit for bit
+    and the fp32 oracle at the batch-1 bar."""
+    st = setup_for("tiny", cuda)
+    cls = make_rwkv7(torch.device("cuda"), backend="auto")
+    model = cls(st.w)
+    assert isinstance(model.model, RWKV7HIPBF16)
+    g = torch.Generator().manual_seed(7)
+    toks = torch.randint(0, st.V, (6,), generator=g)
+    S = model.new_state()
+    Sr = st.model.new_state()
+    sref = R.new_state(st.w.L, st.w.C, dtype=BF)
+    for i, t in enumerate(toks):
+        lg, S = model.decode(t.reshape(1).to(cuda), S)
+        le, Sr = st.model.decode(t.reshape(1).to(cuda), Sr)
+        assert lg.dtype == BF
+        assert torch.equal(lg, le), f"graph vs eager, step {i}"
+        lr, sref = R.decode(st.ref32, t.reshape(1), sref)
+        _check_logits(lg, lr, DEC_ATOL, DEC_RTOL, f"auto step {i}")

@@ -203,6 +203,32 @@ def test_gemm_matches_fp32(M, N, Kd, epi, cuda):
         torch.testing.assert_close(out, ref.half().float(), rtol=2e-3, atol=2e-3)
 
 
+@pytest.mark.slow
+def test_gemm_large_m_beyond_2gib_of_a(cuda):
+    """The large-M GEMM reads its operands through 32-bit buffer offsets, so an
+    A of 2 GiB or more runs as row blocks of whole 256-row tiles below 2^31
+    bytes each (lda 8192: 130816 rows per block). A [131392, 8192] f16 is
+    2.15 GB; rows on both sides of the block boundary, the first rows and the
+    last rows must equal the fp32 product, in both the f32 and add epilogues."""
+    M, N, Kd = 131392, 256, 8192
+    boundary = (2**31 - 1) // (2 * Kd) // 256 * 256
+    assert boundary == 130816
+    print(f"gemm M={M} N={N} K={Kd}: A {M * Kd * 2 / 2**30:.2f} GiB, block boundary row {boundary}", flush=True)
+    g = torch.Generator(device=cuda).manual_seed(3)
+    A = torch.randn(M, Kd, generator=g, device=cuda, dtype=torch.float16)
+    W = (torch.randn(N, Kd, generator=g, device=cuda) * 0.05).half()
+    rows = torch.cat([torch.arange(0, 40), torch.arange(boundary - 300, boundary + 300), torch.arange(M - 40, M)])
+    ref = (A[rows.to(cuda)].float().cpu() @ W.float().cpu().T)
+    out = K.gemm(A, W, "f32")
+    torch.testing.assert_close(out[rows.to(cuda)].cpu(), ref, rtol=1e-4, atol=1e-4)
+    base = torch.randn(M, N, generator=g, device=cuda)
+    want = base[rows.to(cuda)].cpu() + ref
+    K.gemm(A, W, "add", out=base)
+    torch.testing.assert_close(base[rows.to(cuda)].cpu(), want, rtol=1e-4, atol=1e-4)
+    del A, base, out
+    torch.cuda.empty_cache()
+
+
 def test_fused_rkv_gemm_matches_reference_layout(cuda):
     g = torch.Generator().manual_seed(5)
     T, C = 9, 256

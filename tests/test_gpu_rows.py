@@ -196,3 +196,35 @@ def test_rows_kernel_abort_is_visible(cuda):
     for b in range(B):
         _check_logits(lg[b], l32[b], f"row {b} after an aborted launch")
     assert model.last_error() == errs0 + 1
+
+
+def test_rows_prefill_abort_raises_with_check_errors(cuda):
+    """A prefill writes no logits, so an aborted few-row prefill shows only in
+    the workspace's error word. With ``check_errors`` the model reads it after
+    the call and raises; the next prefill runs normally and raises nothing."""
+    from rwkv_tl_amd._lib import HipError
+
+    w, model, ref_w = _setup("tiny", cuda)
+    model.decode_path = "auto"
+    if model.decode_launches(2) != 1:
+        pytest.skip("the few-row kernel does not fit this device")
+    V = w.head.shape[0]
+    g = torch.Generator().manual_seed(45)
+    toks = torch.randint(0, V, (24,), generator=g).to(cuda)
+    S = State(w.L, w.C, 64, device=cuda)
+    ws = model.workspace(1, 8)
+    words = ws[_rows_sync_offset(model.dev.dims):][:64].view(torch.int32)
+    e0 = int(words[0].item())
+    model.prefill(toks[:8], S)
+    torch.cuda.synchronize()
+    epoch = int(words[0].item())
+    assert epoch == e0 + 1, "the epoch word did not advance: wrong offset"
+    model.check_errors = True
+    try:
+        model.raise_if_aborted()  # nothing pending
+        words[4] = epoch + 1  # abort word (byte 16) = the next launch's epoch + 1
+        with pytest.raises(HipError, match="aborted"):
+            model.prefill(toks[8:16], S)
+        model.prefill(toks[16:24], S)
+    finally:
+        model.check_errors = False

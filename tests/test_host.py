@@ -306,6 +306,9 @@ def test_make_rwkv7_backends():
     assert cls.__name__ == "HIPGraphRWKV7HIP"
     assert make_rwkv7(torch.device("cuda"), backend="int8", use_graph=False).__name__ == "RWKV7HIPInt8"
     assert make_rwkv7(torch.device("cuda"), use_graph=False).__name__ == "RWKV7HIP"
+    # "auto" is the bfloat16 model, as demo/__init__.py:98-104 picks RWKV7BF16 on sm >= 80
+    assert make_rwkv7(torch.device("cuda"), backend="auto", use_graph=False).__name__ == "RWKV7HIPBF16"
+    assert make_rwkv7(torch.device("cuda"), backend="auto").__name__ == "HIPGraphRWKV7HIPBF16"
 
 
 def test_quantize_rows_i8_bounds():
