@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define RWKV7_ABI_VERSION 10
+#define RWKV7_ABI_VERSION 11
 #define RWKV7_HEAD_SIZE 64
 
 enum {
@@ -203,6 +203,15 @@ int rwkv7_decode(const rwkv7_model *model, const rwkv7_state *state,
  * lets the HIP-graph wrapper skip capture where it cannot help. */
 int rwkv7_decode_launches(const rwkv7_model *model, int32_t batch, int32_t with_logits);
 
+/* 1 if a step of batch x seq_len tokens (seq_len 1: a decode step with
+ * logits) keeps every activation at fp32-grade precision (the batch-1
+ * kernels compute in fp32; the few-row kernel and the batched GEMMs multiply
+ * f32 activations as 16-bit parts plus 16-bit remainders), 0 if its GEMM
+ * operands are rounded to the model's 16-bit format (the large-M path of
+ * long prefills, where the products are MFMA-bound), -1 for bad arguments.
+ * The reference has no counterpart (its fp16 model rounds every operand). */
+int rwkv7_step_f32_activations(const rwkv7_model *model, int32_t batch, int32_t seq_len);
+
 /* One batch-1 decode step, as rwkv7_decode, that allocates nothing and takes
  * no workspace. It has no counterpart in the reference; it is for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
@@ -324,8 +333,15 @@ int rwkv7_gemv_any4(const float *x, const void *codes, int64_t ldc, const void *
 
 /* Y = epi(A W^T): A f16 [M, K] (row stride lda), W f16 [N, K] (ldw), fp32
  * accumulation. epi: 0 store f32, 1 store f16, 2 relu^2 store f16,
- * 3 add into f32 Y. Y row stride ldy. K % 8 == 0. Stands in for
- * fused_rkv_gemm / ffn_h / ffn_v / out_mm (src/rwkv_tl/kernels/gemm.py:215-305). */
+ * 3 add into f32 Y, 4 tanh store f16, 5 sigmoid store f16, 6 relu^2 store
+ * f32, 7 tanh store f32, 8 sigmoid store f32. Y row stride ldy. K % 8 == 0.
+ * bf16 is a flag word: RWKV7_GEMM_BF16 (A, W and 16-bit outputs are
+ * bfloat16) and RWKV7_GEMM_A_F32 (A is f32, lda in floats, multiplied as its
+ * 16-bit part plus the 16-bit remainder, two MFMAs per weight fragment:
+ * fp32-grade activations). Stands in for fused_rkv_gemm / ffn_h / ffn_v /
+ * out_mm (src/rwkv_tl/kernels/gemm.py:215-305). */
+#define RWKV7_GEMM_BF16 1
+#define RWKV7_GEMM_A_F32 2
 int rwkv7_gemm_f16(const void *A, int64_t lda, const void *W, int64_t ldw,
                    void *Y, int64_t ldy, int32_t M, int32_t N, int32_t K,
                    int32_t epi, int32_t bf16, void *stream);

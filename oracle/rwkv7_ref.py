@@ -17,7 +17,9 @@ What it restates (reference citations are ``path:line`` in yuyi2439/rwkv-tl):
   backward the reference plans in ``TODO.md:46-54`` has no code there).
 * ``time_mix``       -- ``demo/rwkv7_torch.py:67-120``.
 * ``channel_mix``    -- ``demo/rwkv7_torch.py:123-128``.
-* ``decode``         -- ``demo/rwkv7_torch.py:150-158,173-178``.
+* ``decode``         -- ``demo/rwkv7_torch.py:150-158,173-178``;
+  ``decode_rows`` the same for every row of a batched state at once (a speed
+  path for fp32 weights, pinned to ``decode`` row by row).
 * ``tmix_seq`` / ``cmix_seq`` / ``prefill`` -- ``demo/rwkv7_torch.py:160-171,
   180-257`` (serial DPLR over t, ``:227-232``).
 * ``forward``        -- ``demo/_rwkv7_abc.py:74-89``.
@@ -355,6 +357,72 @@ def decode(W: Weights, token: Tensor, state):
         for b in range(state[0][0]["rnn"].shape[0])
     ]
     return torch.stack(rows), state
+
+
+def _time_mix_rows(att: _Att, x0: Tensor, v_first, st: dict[str, Tensor], H: int, N: int):
+    """``time_mix`` for one token of each of B sequences at once (x0 [B, C],
+    state rows [B, ...]): the same formulas with every matrix product taken
+    for all rows together. A speed path of the checker for fp32 weights;
+    pinned to ``time_mix`` row by row in tests/test_oracle.py."""
+    B = x0.shape[0]
+    x = att.ln_pre(x0)
+    prev = st["x"]
+    xr = _lerp(x, prev, att.x_r)
+    xw = _lerp(x, prev, att.x_w)
+    xk = _lerp(x, prev, att.x_k)
+    xv = _lerp(x, prev, att.x_v)
+    xa = _lerp(x, prev, att.x_a)
+    xg = _lerp(x, prev, att.x_g)
+    st["x"].copy_(x)
+    r = xr @ att.rkvWt[0]
+    k = xk @ att.rkvWt[1]
+    v = xv @ att.rkvWt[2]
+    if v_first is None:
+        v_first = v
+    else:
+        v = _lerp(v, v_first, torch.sigmoid(att.v0.reshape(-1) + xv @ att.v1 @ att.v2))
+    w = torch.exp(-torch.sigmoid(att.w0.reshape(-1) + torch.tanh(xw @ att.w1) @ att.w2) / SQRT_E)
+    a = torch.sigmoid(att.a0.reshape(-1) + xa @ att.a1 @ att.a2)
+    kk = k * att.k_k.reshape(-1)
+    k = _lerp(k, k * a, att.k_a.reshape(-1))
+    r, w, k, v, kk, a = [z.reshape(B, H, N) for z in (r, w, k, v, kk, a)]
+    kk = _l2_normalize(kk)
+    S = st["rnn"]
+    b = -kk * a
+    S_new = (
+        torch.einsum("zhvk,zhk->zhvk", S, w.float())
+        + torch.einsum("zhva,zha,zhb->zhvb", S, kk.float(), b.float())
+        + torch.einsum("zhv,zhk->zhvk", v.float(), k.float())
+    )
+    y = torch.einsum("zhvk,zhk->zhv", S_new, r.float()).to(v.dtype)
+    st["rnn"].copy_(S_new)
+    y = F.group_norm(y.reshape(B, H * N), H, att.ln_x.w, att.ln_x.b, GN_EPS)
+    y = y + (torch.sum(r * k * att.r_k, dim=-1, keepdim=True) * v).reshape(B, -1)
+    g = torch.sigmoid(xg @ att.g1) @ att.g2
+    return x0 + (y * g) @ att.oWt, v_first.reshape(B, -1)
+
+
+def _channel_mix_rows(ffn: _Ffn, x0: Tensor, st: dict[str, Tensor]) -> Tensor:
+    """``channel_mix`` for B rows at once (see ``_time_mix_rows``)."""
+    x_ln = ffn.ln_pre(x0)
+    x = _lerp(x_ln, st["x"], ffn.x_k)
+    st["x"].copy_(x_ln)
+    return x0 + F.relu(x @ ffn.kWt) ** 2 @ ffn.vWt
+
+
+def decode_rows(W: Weights, token: Tensor, state):
+    """``decode`` of a batched state (token [B]) with every row computed in
+    the same batched torch operations instead of one row at a time: the same
+    model, ~B times fewer passes over the weights. For fp32 weights (the
+    fp32-math oracle) only; rows agree with ``decode`` to fp32 rounding
+    (tests/test_oracle.py). Returns ``(logits [B, V], state)``."""
+    tmix, cmix = state
+    x = F.embedding(token.reshape(-1), W.emb)
+    v_first = None
+    for i, blk in enumerate(W.blocks):
+        x, v_first = _time_mix_rows(blk.att, x, v_first, tmix[i], W.H, N_HEAD_DIM)
+        x = _channel_mix_rows(blk.ffn, x, cmix[i])
+    return W.ln_out(x) @ W.head.T, state
 
 
 # --------------------------------------------------------------------------

@@ -21,6 +21,12 @@
 //     workgroup) sums the S partials in split order, so the result does not
 //     depend on which workgroup came last, and applies the epilogue.
 //
+// A may also be f32 (GemmProb::a32): each A fragment is then split into its
+// 16-bit hi part and 16-bit remainder (split_hi_lo) and multiplied by the same
+// W fragment twice, which keeps the activations at fp32-grade precision for
+// about the cost of the second MFMA and A's doubled bytes (these kernels are
+// bound by streaming W, not by the MFMAs).
+//
 // One launch runs a group of up to 8 problems that share M and A's rows (the
 // r/k/v projections and the four LoRA first steps of one layer, for instance).
 // Reference counterparts: fused_rkv_gemm, ffn_h, ffn_v, out_mm
@@ -64,7 +70,14 @@ RWKV7_DEV void store_epi(const GemmProb &P, int row, int col, float v) {
     }
     case GEPI_ADD_F32: reinterpret_cast<float *>(P.Y)[o] += v; break;
     case GEPI_TANH_F16: st16(tanhf(v)); break;
-    default: st16(sigmoidf_(v)); break;
+    case GEPI_SIGM_F16: st16(sigmoidf_(v)); break;
+    case GEPI_RELUSQ_F32: {
+      const float q = fmaxf(v, 0.f);
+      reinterpret_cast<float *>(P.Y)[o] = q * q;
+      break;
+    }
+    case GEPI_TANH_F32: reinterpret_cast<float *>(P.Y)[o] = tanhf(v); break;
+    default: reinterpret_cast<float *>(P.Y)[o] = sigmoidf_(v); break;
   }
 }
 
@@ -209,12 +222,44 @@ RWKV7_DEV void tile_store(const GemmGroup &g, const TileUnit &w, floatx4 (&acc)[
   }
 }
 
-template <int BM, bool BF>
+// One 8-element A piece in registers: 16 bytes of 16-bit values, or 32 bytes of
+// f32 (A32) that store_piece splits into the hi and lo planes of LDS.
+template <bool A32>
+struct APiece {
+  uint4 v[A32 ? 2 : 1];
+};
+template <bool A32>
+RWKV7_DEV APiece<A32> load_piece(const GemmProb &P, int rc, int kc) {
+  APiece<A32> a;
+  if constexpr (A32) {
+    const uint4 *q = reinterpret_cast<const uint4 *>(reinterpret_cast<const float *>(P.A) + (int64_t)rc * P.lda + kc);
+    a.v[0] = q[0];
+    a.v[1] = q[1];
+  } else {
+    a.v[0] = *reinterpret_cast<const uint4 *>(P.A + (int64_t)rc * P.lda + kc);
+  }
+  return a;
+}
+// Stores a piece (zeros when !live) at hi[off] and, for A32, its remainder at lo[off].
+template <bool BF, bool A32>
+RWKV7_DEV void store_piece(const APiece<A32> &a, bool live, uint16_t *hi, uint16_t *lo, int off) {
+  if constexpr (A32) {
+    uint4 h = make_uint4(0, 0, 0, 0), l = make_uint4(0, 0, 0, 0);
+    if (live) split_hi_lo<BF>(a.v[0], a.v[1], h, l);
+    *reinterpret_cast<uint4 *>(hi + off) = h;
+    *reinterpret_cast<uint4 *>(lo + off) = l;
+  } else {
+    *reinterpret_cast<uint4 *>(hi + off) = live ? a.v[0] : make_uint4(0, 0, 0, 0);
+  }
+}
+
+template <int BM, bool BF, bool A32>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
   constexpr int MB = BM / 16;                // 16-row blocks
   constexpr int kRowH = kKC + kLdsPadH;      // halves per LDS row
-  constexpr int kAPer = BM * (kKC / 8) / 256;  // 16-byte A pieces per thread per chunk
-  __shared__ __align__(16) uint16_t s_a[2][BM][kRowH];
+  constexpr int kAPer = BM * (kKC / 8) / 256;  // 8-element A pieces per thread per chunk
+  constexpr int NP = A32 ? 2 : 1;            // LDS planes of A: hi (and lo)
+  __shared__ __align__(16) uint16_t s_a[2][NP][BM][kRowH];
   __shared__ int s_last;
 
   const TileUnit U = tile_unit<BM>(g);
@@ -227,7 +272,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
   // A staging: piece idx -> row idx >> 4, 16-byte column idx & 15. Loads are
   // unconditional (row and k clamped into range) and masked after arrival, so
   // the compiler can count outstanding loads exactly.
-  uint4 a_reg[kAPer];
+  APiece<A32> a_reg[kAPer];
   auto load_a = [&](int c) {
     const int k0 = kb + c * kKC;
 #pragma unroll
@@ -235,7 +280,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
       const int idx = t + 256 * u;
       const int r = m0 + (idx >> 4), k = k0 + 8 * (idx & 15);
       const int rc = r < M ? r : M - 1, kc = k < K - 8 ? k : K - 8;
-      a_reg[u] = *reinterpret_cast<const uint4 *>(P.A + (int64_t)rc * P.lda + kc);
+      a_reg[u] = load_piece<A32>(P, rc, kc);
     }
   };
   auto store_a = [&](int c, int buf) {
@@ -244,8 +289,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
     for (int u = 0; u < kAPer; ++u) {
       const int idx = t + 256 * u;
       const int r = m0 + (idx >> 4), k = k0 + 8 * (idx & 15);
-      const uint4 v = (r < M && k < ke) ? a_reg[u] : make_uint4(0, 0, 0, 0);
-      *reinterpret_cast<uint4 *>(&s_a[buf][idx >> 4][8 * (idx & 15)]) = v;
+      const int off = (idx >> 4) * kRowH + 8 * (idx & 15);
+      store_piece<BF, A32>(a_reg[u], r < M && k < ke, &s_a[buf][0][0][0], &s_a[buf][NP - 1][0][0], off);
     }
   };
   // W fragments of chunk c: k-steps kb/32 + 4c + j (see WStrip)
@@ -265,8 +310,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
     for (int j = 0; j < 4; ++j) {
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
-        const uint4 afrag = *reinterpret_cast<const uint4 *>(&s_a[buf][mb * 16 + (lane & 15)][32 * j + 8 * (lane >> 4)]);
-        acc[mb] = mfma16<BF>(afrag, w[j], acc[mb]);
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl) {
+          const uint4 afrag =
+              *reinterpret_cast<const uint4 *>(&s_a[buf][pl][mb * 16 + (lane & 15)][32 * j + 8 * (lane >> 4)]);
+          acc[mb] = mfma16<BF>(afrag, w[j], acc[mb]);
+        }
       }
     }
   };
@@ -312,12 +361,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
 // memory round trip instead of one per chunk pair (the tiles are latency-bound
 // at these sizes, not bandwidth-bound). Same tiling, unit order, split-K
 // hand-off and epilogue as gemm_kernel.
-template <int BM, int NC, bool BF>
+template <int BM, int NC, bool BF, bool A32>
 __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmGroup g) {
   constexpr int MB = BM / 16;
   constexpr int kRowH = kKC + kLdsPadH;
   constexpr int kAPer = BM * (kKC / 8) / 256;
-  __shared__ __align__(16) uint16_t s_a[NC][BM][kRowH];
+  constexpr int NP = A32 ? 2 : 1;
+  __shared__ __align__(16) uint16_t s_a[NC][NP][BM][kRowH];
   __shared__ int s_last;
 
   const TileUnit U = tile_unit<BM>(g);
@@ -330,7 +380,7 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmGroup g) {
   // A pieces (row idx >> 4, 16-byte column idx & 15), loads clamped into range
   // and masked when stored; a chunk past the split re-reads the split's last
   // chunk (an L2 hit) and is never multiplied.
-  uint4 a_reg[NC][kAPer];
+  APiece<A32> a_reg[NC][kAPer];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int k0 = kb + (c < nch ? c : nch - 1) * kKC;
@@ -339,7 +389,7 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmGroup g) {
       const int idx = t + 256 * q;
       const int r = m0 + (idx >> 4), k = k0 + 8 * (idx & 15);
       const int rc = r < M ? r : M - 1, kc = k < K - 8 ? k : K - 8;
-      a_reg[c][q] = *reinterpret_cast<const uint4 *>(P.A + (int64_t)rc * P.lda + kc);
+      a_reg[c][q] = load_piece<A32>(P, rc, kc);
     }
   }
   const WStrip ws = w_strip(P, U.n0, wv, lane);
@@ -359,8 +409,8 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmGroup g) {
     for (int q = 0; q < kAPer; ++q) {
       const int idx = t + 256 * q;
       const int r = m0 + (idx >> 4), k = k0 + 8 * (idx & 15);
-      const uint4 v = (r < M && k < ke) ? a_reg[c][q] : make_uint4(0, 0, 0, 0);
-      *reinterpret_cast<uint4 *>(&s_a[c][idx >> 4][8 * (idx & 15)]) = v;
+      const int off = (idx >> 4) * kRowH + 8 * (idx & 15);
+      store_piece<BF, A32>(a_reg[c][q], r < M && k < ke, &s_a[c][0][0][0], &s_a[c][NP - 1][0][0], off);
     }
   }
   __syncthreads();
@@ -375,8 +425,12 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmGroup g) {
       for (int j = 0; j < 4; ++j) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
-          const uint4 afrag = *reinterpret_cast<const uint4 *>(&s_a[c][mb * 16 + (lane & 15)][32 * j + 8 * (lane >> 4)]);
-          acc[mb] = mfma16<BF>(afrag, wr[c][j], acc[mb]);
+#pragma unroll
+          for (int pl = 0; pl < NP; ++pl) {
+            const uint4 afrag =
+                *reinterpret_cast<const uint4 *>(&s_a[c][pl][mb * 16 + (lane & 15)][32 * j + 8 * (lane >> 4)]);
+            acc[mb] = mfma16<BF>(afrag, wr[c][j], acc[mb]);
+          }
         }
       }
     }
@@ -581,8 +635,16 @@ static int big_rows_per_launch(int64_t lda) {
 // 32-row tiled kernels with split-K are 2-3x faster; at M = 4096 this path is
 // ~2x faster than them).
 static bool big_fits(const GemmProb &p, int M, int cus) {
-  return p.K % kBigBK == 0 && p.N >= 256 && (int64_t)((M + 127) / 128) * ((p.N + 127) / 128) >= 2 * cus &&
-         big_w_addressable(p) && big_rows_per_launch(p.lda) >= 256;
+  return !p.a32 && p.K % kBigBK == 0 && p.N >= 256 &&
+         (int64_t)((M + 127) / 128) * ((p.N + 127) / 128) >= 2 * cus && big_w_addressable(p) &&
+         big_rows_per_launch(p.lda) >= 256;
+}
+
+int gemm_big_min_rows(int N) {
+  if (N < 256) return 0x7fffffff;
+  const int cus = mk_cus() > 0 ? mk_cus() : 256;
+  const int nt = (N + 127) / 128, mt = (2 * cus + nt - 1) / nt;
+  return (mt - 1) * 128 + 1;
 }
 
 #define RWKV7_TRY_GEMM(expr)         \
@@ -659,7 +721,7 @@ struct SkinnyGroup {
   unsigned *ctr;
 };
 
-template <int MB, bool BF>
+template <int MB, bool BF, bool A32>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(SkinnyGroup g) {
   constexpr int KB = MB == 1 ? 8 : 5;
   __shared__ __align__(16) float4 red[kSkW][MB][64];
@@ -691,32 +753,35 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(SkinnyGroup g) {
     const int k = 32 * ks + 8 * (lane >> 4);
     return frag ? (int64_t)ks * 512 : (int64_t)(k < K - 8 ? k : K - 8);
   };
-  const uint16_t *arow[MB];
+  int arow[MB];  // A row of each 16-row block (clamped)
   bool alive[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int r = mb * 16 + (lane & 15);
     alive[mb] = r < M;
-    arow[mb] = P.A + (int64_t)(r < M ? r : M - 1) * P.lda;
+    arow[mb] = r < M ? r : M - 1;
   }
   floatx4 acc[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) acc[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
   for (int kb = ks0; kb < ks1; kb += KB) {
     const int cnt = min(KB, ks1 - kb);  // wave-uniform
-    uint4 wf[KB], af[KB][MB];
+    uint4 wf[KB];
+    APiece<A32> af[KB][MB];
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
       wf[j] = make_uint4(0, 0, 0, 0);
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) af[j][mb] = make_uint4(0, 0, 0, 0);
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int h = 0; h < (A32 ? 2 : 1); ++h) af[j][mb].v[h] = make_uint4(0, 0, 0, 0);
       if (j < cnt) {
         const int k = 32 * (kb + j) + 8 * (lane >> 4);
         const int kc = k < K - 8 ? k : K - 8;
         wf[j] = ld_stream(reinterpret_cast<const uint4 *>(wbase + woff(kb + j)));
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
-          if (alive[mb] && k < K) af[j][mb] = *reinterpret_cast<const uint4 *>(arow[mb] + kc);
+          if (alive[mb] && k < K) af[j][mb] = load_piece<A32>(P, arow[mb], kc);
       }
     }
     // every load of the batch is issued before the first product waits
@@ -725,7 +790,16 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(SkinnyGroup g) {
     for (int j = 0; j < KB; ++j) {
       if (j < cnt) {
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma16<BF>(af[j][mb], wf[j], acc[mb]);
+        for (int mb = 0; mb < MB; ++mb) {
+          if constexpr (A32) {
+            uint4 hi, lo;
+            split_hi_lo<BF>(af[j][mb].v[0], af[j][mb].v[1], hi, lo);
+            acc[mb] = mfma16<BF>(hi, wf[j], acc[mb]);
+            acc[mb] = mfma16<BF>(lo, wf[j], acc[mb]);
+          } else {
+            acc[mb] = mfma16<BF>(af[j][mb].v[0], wf[j], acc[mb]);
+          }
+        }
       }
     }
   }
@@ -765,9 +839,9 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(SkinnyGroup g) {
 // Splits of a skinny strip: enough that one workgroup moves at most ~64 KB
 // of W and A, ~128 KB above 16 rows (measured: with 17..32 rows the larger
 // cap is 4-5% faster, with up to 16 rows 2% slower).
-static int skinny_splits(int M, int K, bool can_split) {
+static int skinny_splits(int M, int K, bool can_split, bool a32) {
   if (!can_split) return 1;
-  const int64_t per_k = 16 * 2 + (int64_t)(M < 16 ? M : 16) * 2 * ((M + 15) / 16);  // bytes per unit of k
+  const int64_t per_k = 16 * 2 + (int64_t)(M < 16 ? M : 16) * (a32 ? 4 : 2) * ((M + 15) / 16);  // bytes per unit of k
   const int64_t cap = M > 16 ? 128 * 1024 : 64 * 1024;
   int S = 1;
   while (S < kMaxSplit && (int64_t)K / S * per_k > cap && K / (2 * S) >= 256) S *= 2;
@@ -785,7 +859,8 @@ static int launch_skinny(const GemmProb *probs, int nprob, int M, hipStream_t st
   // splits per problem, then halved (largest strips x splits first) until the
   // partial tiles and arrival counters fit the workspace
   int split[kMaxProb] = {};
-  for (int i = 0; i < nprob; ++i) split[i] = skinny_splits(M, probs[i].K, part != nullptr && ctr != nullptr);
+  for (int i = 0; i < nprob; ++i)
+    split[i] = skinny_splits(M, probs[i].K, part != nullptr && ctr != nullptr, probs[i].a32 != 0);
   for (;;) {
     int64_t need_fl = 0;
     int need_ctr = 0, worst = -1;
@@ -825,13 +900,17 @@ static int launch_skinny(const GemmProb *probs, int nprob, int M, hipStream_t st
   }
   g.wg_begin[kMaxProb] = wgs;
   if (pfl * 4 > part_cap || ctrs > kGemmCounters) return RWKV7_EWORKSPACE;
-  const bool bf = probs[0].bf != 0;
-  if (MB == 1) {
-    if (bf) gemm_skinny_kernel<1, true><<<wgs, 256, 0, st>>>(g);
-    else gemm_skinny_kernel<1, false><<<wgs, 256, 0, st>>>(g);
-  } else {
-    if (bf) gemm_skinny_kernel<2, true><<<wgs, 256, 0, st>>>(g);
-    else gemm_skinny_kernel<2, false><<<wgs, 256, 0, st>>>(g);
+  const bool bf = probs[0].bf != 0, a32 = probs[0].a32 != 0;
+  const int variant = (MB == 1 ? 0 : 4) | (bf ? 2 : 0) | (a32 ? 1 : 0);
+  switch (variant) {
+    case 0: gemm_skinny_kernel<1, false, false><<<wgs, 256, 0, st>>>(g); break;
+    case 1: gemm_skinny_kernel<1, false, true><<<wgs, 256, 0, st>>>(g); break;
+    case 2: gemm_skinny_kernel<1, true, false><<<wgs, 256, 0, st>>>(g); break;
+    case 3: gemm_skinny_kernel<1, true, true><<<wgs, 256, 0, st>>>(g); break;
+    case 4: gemm_skinny_kernel<2, false, false><<<wgs, 256, 0, st>>>(g); break;
+    case 5: gemm_skinny_kernel<2, false, true><<<wgs, 256, 0, st>>>(g); break;
+    case 6: gemm_skinny_kernel<2, true, false><<<wgs, 256, 0, st>>>(g); break;
+    default: gemm_skinny_kernel<2, true, true><<<wgs, 256, 0, st>>>(g); break;
   }
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;
@@ -847,6 +926,10 @@ static int bm_for(int M) { return M <= 256 ? 32 : 64; }
 // least two 128-wide chunks) until the group has a workgroup per CU and no
 // workgroup streams more than ~256 KB of W and A (measured: a 128 KB cap,
 // i.e. twice the splits, made prefill at T = 128 to 512 2-8% slower).
+//
+// f32 A (a32) at 32-row tiles: also split until a split holds at most 4
+// chunks, the most whose f32 A pieces and W fragments the prefetch-all kernel
+// keeps in registers at once.
 static void plan_splits(const GemmProb *probs, int nprob, int M, int cus, bool can_split, int *S, int *kslice) {
   const int BM = bm_for(M);
   const int m_tiles = (M + BM - 1) / BM;
@@ -854,11 +937,13 @@ static void plan_splits(const GemmProb *probs, int nprob, int M, int cus, bool c
   for (int i = 0; i < nprob; ++i) tiles += m_tiles * ((probs[i].N + kBN - 1) / kBN);
   for (int i = 0; i < nprob; ++i) {
     const int K = probs[i].K;
+    const bool a32 = probs[i].a32 != 0;
     int s = 1;
     if (can_split) {
-      auto bytes = [&](int sp) { return (int64_t)(kBN + BM) * 2 * ((K + sp - 1) / sp); };
-      while (s < kMaxSplit && K / (2 * s) >= 2 * kKC && (tiles * s < cus || bytes(s) > 256 * 1024) &&
-             (int64_t)tiles * 2 * s <= 4 * cus)
+      auto bytes = [&](int sp) { return (int64_t)(2 * kBN + (a32 ? 4 : 2) * BM) * ((K + sp - 1) / sp); };
+      auto too_long = [&](int sp) { return a32 && BM == 32 && (K + sp - 1) / sp > 4 * kKC; };
+      while (s < kMaxSplit && K / (2 * s) >= 2 * kKC &&
+             (tiles * s < cus || bytes(s) > 256 * 1024 || too_long(s)) && (int64_t)tiles * 2 * s <= 4 * cus)
         s *= 2;
     }
     S[i] = s;
@@ -894,9 +979,9 @@ int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, f
     const GemmProb &p = probs[i];
     if (p.K < 8 || p.N <= 0 || p.K % 8 || p.lda % 8 || p.ldw % 8) return RWKV7_ESHAPE;
     if (!p.A || !p.W || !p.Y) return RWKV7_EINVAL;
-    if (p.bf != probs[0].bf) return RWKV7_EINVAL;  // one operand format per launch
+    if (p.bf != probs[0].bf || p.a32 != probs[0].a32) return RWKV7_EINVAL;  // one operand format per launch
   }
-  const bool bf = probs[0].bf != 0;
+  const bool bf = probs[0].bf != 0, a32 = probs[0].a32 != 0;
   if (M <= kSkinnyMaxM) return launch_skinny(probs, nprob, M, st, part, ctr, gemm_ws_bytes(M, cus));
   {
     // problems the large-M path takes run there; the rest (LoRA widths) below
@@ -953,38 +1038,40 @@ int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, f
   }
   g.wg_begin[kMaxProb] = wgs;
   if (pfl * 4 > gemm_ws_bytes(M, cus) || ctrs > kGemmCounters) return RWKV7_EWORKSPACE;
-  // every split of at most 8 chunks: the prefetch-all kernel
+  // every split of at most 8 chunks (4 with f32 A): the prefetch-all kernel
   int ncmax = 1;
   for (int i = 0; i < nprob; ++i) ncmax = max(ncmax, ks[i] / kKC);
-  if (BM == 32 && ncmax <= 8) {
-    if (bf) {
-      if (ncmax == 1) gemm_pf_kernel<32, 1, true><<<wgs, 256, 0, st>>>(g);
-      else if (ncmax == 2) gemm_pf_kernel<32, 2, true><<<wgs, 256, 0, st>>>(g);
-      else if (ncmax <= 4) gemm_pf_kernel<32, 4, true><<<wgs, 256, 0, st>>>(g);
-      else gemm_pf_kernel<32, 8, true><<<wgs, 256, 0, st>>>(g);
-    } else {
-      if (ncmax == 1) gemm_pf_kernel<32, 1, false><<<wgs, 256, 0, st>>>(g);
-      else if (ncmax == 2) gemm_pf_kernel<32, 2, false><<<wgs, 256, 0, st>>>(g);
-      else if (ncmax <= 4) gemm_pf_kernel<32, 4, false><<<wgs, 256, 0, st>>>(g);
-      else gemm_pf_kernel<32, 8, false><<<wgs, 256, 0, st>>>(g);
+  const int nc = ncmax == 1 ? 1 : ncmax == 2 ? 2 : ncmax <= 4 ? 4 : ncmax <= 8 ? 8 : 0;
+  if (BM == 32 && nc > 0 && !(a32 && nc > 4)) {
+#define RWKV7_PF(NC)                                                                     \
+  if (bf) {                                                                              \
+    if (a32) gemm_pf_kernel<32, NC < 4 ? NC : 4, true, true><<<wgs, 256, 0, st>>>(g);   \
+    else gemm_pf_kernel<32, NC, true, false><<<wgs, 256, 0, st>>>(g);                    \
+  } else {                                                                               \
+    if (a32) gemm_pf_kernel<32, NC < 4 ? NC : 4, false, true><<<wgs, 256, 0, st>>>(g);  \
+    else gemm_pf_kernel<32, NC, false, false><<<wgs, 256, 0, st>>>(g);                   \
+  }
+    switch (nc) {
+      case 1: RWKV7_PF(1) break;
+      case 2: RWKV7_PF(2) break;
+      case 4: RWKV7_PF(4) break;
+      default: RWKV7_PF(8) break;
     }
+#undef RWKV7_PF
     RWKV7_CHECK_LAUNCH();
     return RWKV7_OK;
   }
-  if (bf) {
-    switch (BM) {
-      case 16: gemm_kernel<16, true><<<wgs, 256, 0, st>>>(g); break;
-      case 32: gemm_kernel<32, true><<<wgs, 256, 0, st>>>(g); break;
-      case 64: gemm_kernel<64, true><<<wgs, 256, 0, st>>>(g); break;
-      default: gemm_kernel<128, true><<<wgs, 256, 0, st>>>(g); break;
-    }
-  } else {
-    switch (BM) {
-      case 16: gemm_kernel<16, false><<<wgs, 256, 0, st>>>(g); break;
-      case 32: gemm_kernel<32, false><<<wgs, 256, 0, st>>>(g); break;
-      case 64: gemm_kernel<64, false><<<wgs, 256, 0, st>>>(g); break;
-      default: gemm_kernel<128, false><<<wgs, 256, 0, st>>>(g); break;
-    }
+  // the row tiles bm_for picks: 32 or 64 rows
+  const int variant = (BM == 32 ? 0 : 4) | (bf ? 2 : 0) | (a32 ? 1 : 0);
+  switch (variant) {
+    case 0: gemm_kernel<32, false, false><<<wgs, 256, 0, st>>>(g); break;
+    case 1: gemm_kernel<32, false, true><<<wgs, 256, 0, st>>>(g); break;
+    case 2: gemm_kernel<32, true, false><<<wgs, 256, 0, st>>>(g); break;
+    case 3: gemm_kernel<32, true, true><<<wgs, 256, 0, st>>>(g); break;
+    case 4: gemm_kernel<64, false, false><<<wgs, 256, 0, st>>>(g); break;
+    case 5: gemm_kernel<64, false, true><<<wgs, 256, 0, st>>>(g); break;
+    case 6: gemm_kernel<64, true, false><<<wgs, 256, 0, st>>>(g); break;
+    default: gemm_kernel<64, true, true><<<wgs, 256, 0, st>>>(g); break;
   }
   RWKV7_CHECK_LAUNCH();
   return RWKV7_OK;

@@ -129,11 +129,13 @@ static int64_t decode_ws(const rwkv7_dims &d, char *base, DecodeWs *w) {
   return off;
 }
 
-// Workspace of the batched path (M = B * T rows).
+// Workspace of the batched path (M = B * T rows). The GEMM operands xmix, l1,
+// yg, hid and headin are f32 when the step runs with f32 activations
+// (batch_a32), else 16-bit; their buffers are sized for f32 either way.
 struct BatchWs {
   float *x0, *rkv, *d, *vfirst, *kv, *y, *part;  // kv: gated k, mixed v [2][M][C]
   float *proj1;  // one-token steps: r, k, v, raw LoRA first steps [M, 3C+SR]
-  uint16_t *xmix, *l1, *yg, *hid, *headin;
+  void *xmix, *l1, *yg, *hid, *headin;
   float *U, *Send, *Pend;  // segmented scan of long sequences (null with one segment)
   float *rec;              // chunk records of the chunked scan (prefill_chunked)
 };
@@ -147,16 +149,16 @@ static int64_t batch_ws(const rwkv7_dims &d, int64_t B, int64_t T, char *base, B
   };
   BatchWs t;
   t.x0 = reinterpret_cast<float *>(take(M * C * 4));
-  t.xmix = reinterpret_cast<uint16_t *>(take(6 * M * C * 2));
+  t.xmix = take(6 * M * C * 4);
   t.rkv = reinterpret_cast<float *>(take(3 * M * C * 4));
-  t.l1 = reinterpret_cast<uint16_t *>(take(M * SR * 2));
+  t.l1 = take(M * SR * 4);
   t.d = reinterpret_cast<float *>(take(4 * M * C * 4));
   t.vfirst = reinterpret_cast<float *>(take(M * C * 4));
   t.kv = reinterpret_cast<float *>(take(2 * M * C * 4));
   t.y = reinterpret_cast<float *>(take(M * C * 4));
-  t.yg = reinterpret_cast<uint16_t *>(take(M * C * 2));
-  t.hid = reinterpret_cast<uint16_t *>(take(M * F * 2));
-  t.headin = reinterpret_cast<uint16_t *>(take(B * C * 2));
+  t.yg = take(M * C * 4);
+  t.hid = take(M * F * 4);
+  t.headin = take(B * C * 4);
   t.proj1 = T == 1 ? reinterpret_cast<float *>(take(M * (3 * C + SR) * 4)) : nullptr;
   const int cus = mk_cus() > 0 ? mk_cus() : 256;
   t.part = reinterpret_cast<float *>(take(gemm_ws_bytes((int)(M > B ? M : B), cus)));
@@ -294,6 +296,14 @@ static int decode_one(const rwkv7_model &m, const rwkv7_state &s, const int64_t 
   return RWKV7_OK;
 }
 
+// The batched path runs with f32 activations -- every GEMM operand produced
+// in f32 and multiplied as two 16-bit parts (GemmProb::a32) -- when no GEMM of
+// the step would take the large-M path: below gemm_big_min_rows of the
+// widest layer matrix. Above it (long prefills, where the products are
+// MFMA-bound and the large-M kernel streams 16-bit operands by LDS DMA) the
+// activations are rounded to the model's 16-bit format.
+static bool batch_a32(const rwkv7_dims &d, int M) { return M < gemm_big_min_rows(d.n_ffn > d.n_embd ? d.n_ffn : d.n_embd); }
+
 // B sequences x T tokens through the MFMA GEMM path; logits (optional) of the
 // last token of each sequence.
 static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t *tok, int T,
@@ -310,11 +320,26 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
   batch_ws(d, B, T, ws, &w);
   unsigned *ctr = gemm_counters(d, ws);
   const int bf = (m.flags & RWKV7_MODEL_BF16) ? 1 : 0;
-  // every GEMM of the step runs on the model's 16-bit format
+  const int a32 = batch_a32(d, M) ? 1 : 0;
+  const int esz = a32 ? 4 : 2;  // bytes per element of the GEMM operands
+  // every GEMM of the step runs on the model's 16-bit format, with f32 A if a32
   auto gemm = [&](GemmProb *p, int n, int rows) {
-    for (int i = 0; i < n; ++i) p[i].bf = bf;
+    for (int i = 0; i < n; ++i) {
+      p[i].bf = bf;
+      p[i].a32 = a32;
+    }
     return launch_gemm_group(p, n, rows, st, w.part, ctr);
   };
+  // element offset into an operand buffer, as the uint16_t pointer GemmProb
+  // holds for A (at) and as an output pointer (out_at)
+  auto at = [&](void *base, int64_t elems) {
+    return reinterpret_cast<const uint16_t *>(static_cast<char *>(base) + elems * esz);
+  };
+  auto out_at = [&](void *base, int64_t elems) { return static_cast<void *>(static_cast<char *>(base) + elems * esz); };
+  const int epi_relusq = a32 ? GEPI_RELUSQ_F32 : GEPI_RELUSQ;
+  const int epi_plain = a32 ? GEPI_F32 : GEPI_F16;
+  const int epi_tanh = a32 ? GEPI_TANH_F32 : GEPI_TANH_F16;
+  const int epi_sigm = a32 ? GEPI_SIGM_F32 : GEPI_SIGM_F16;
   RWKV7_TRY(launch_embed(tok, static_cast<const uint16_t *>(m.emb), w.x0, M, C, d.vocab, bf, st));
   for (int l = 0; l < d.n_layer; ++l) {
     const char *L = static_cast<const char *>(m.layers) + (int64_t)l * lay.bytes;
@@ -329,9 +354,10 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
     LnShiftArgs ls = {w.x0, vec + RWKV7_V_LN1_W * C, vec + RWKV7_V_LN1_B * C, vec + RWKV7_V_X_R * C,
                       6, w.xmix, tshift, C, T, M};
     ls.bf = bf;
+    ls.out_f32 = a32;
     RWKV7_TRY(launch_ln_shift(ls, st));
-    const uint16_t *xr = w.xmix, *xw = w.xmix + MC, *xk = w.xmix + 2 * MC, *xv = w.xmix + 3 * MC,
-                   *xa = w.xmix + 4 * MC, *xg = w.xmix + 5 * MC;
+    const uint16_t *xr = at(w.xmix, 0), *xw = at(w.xmix, MC), *xk = at(w.xmix, 2 * MC), *xv = at(w.xmix, 3 * MC),
+                   *xa = at(w.xmix, 4 * MC), *xg = at(w.xmix, 5 * MC);
     if (T == 1) {
       // one token per sequence: r, k, v and the raw LoRA first steps into one
       // [M, 3C+SR] f32 matrix, then the fused per-head kernel (LoRA second
@@ -367,8 +393,8 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
       td.rnn = rnn;
       td.xln = nullptr;
       td.shift = nullptr;  // ln_shift wrote the shift state
-      td.yg = nullptr;
-      td.yg16 = w.yg;
+      td.yg = a32 ? static_cast<float *>(w.yg) : nullptr;
+      td.yg16 = a32 ? nullptr : static_cast<uint16_t *>(w.yg);
       td.C = C;
       td.H = H;
       td.rv = rv;
@@ -378,17 +404,18 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
       td.layer0 = l == 0;
       td.bf = bf;
       RWKV7_TRY(launch_tmix_decode(td, B, st));
-      GemmProb go = {w.yg, reinterpret_cast<const uint16_t *>(L + lay.w_o), w.x0, C, C, C, C, C, GEPI_ADD_F32};
+      GemmProb go = {at(w.yg, 0), reinterpret_cast<const uint16_t *>(L + lay.w_o), w.x0, C, C, C, C, C, GEPI_ADD_F32};
       frag(go, lay.f_o, 0);
       RWKV7_TRY(gemm(&go, 1, M));
       LnShiftArgs lc = {w.x0, vec + RWKV7_V_LN2_W * C, vec + RWKV7_V_LN2_B * C, vec + RWKV7_V_FFN_X_K * C,
                         1, w.xmix, cshift, C, T, M};
       lc.bf = bf;
+      lc.out_f32 = a32;
       RWKV7_TRY(launch_ln_shift(lc, st));
-      GemmProb gk = {w.xmix, reinterpret_cast<const uint16_t *>(L + lay.w_fk), w.hid, C, C, F, F, C, GEPI_RELUSQ};
+      GemmProb gk = {at(w.xmix, 0), reinterpret_cast<const uint16_t *>(L + lay.w_fk), w.hid, C, C, F, F, C, epi_relusq};
       frag(gk, lay.f_fk, 0);
       RWKV7_TRY(gemm(&gk, 1, M));
-      GemmProb gv = {w.hid, reinterpret_cast<const uint16_t *>(L + lay.w_fv), w.x0, F, F, C, C, F, GEPI_ADD_F32};
+      GemmProb gv = {at(w.hid, 0), reinterpret_cast<const uint16_t *>(L + lay.w_fv), w.x0, F, F, C, C, F, GEPI_ADD_F32};
       frag(gv, lay.f_fv, 0);
       RWKV7_TRY(gemm(&gv, 1, M));
       continue;
@@ -397,10 +424,10 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
         {xr, wrkv, w.rkv, C, C, C, C, C, GEPI_F32},
         {xk, wrkv + (int64_t)C * C, w.rkv + MC, C, C, C, C, C, GEPI_F32},
         {xv, wrkv + 2 * (int64_t)C * C, w.rkv + 2 * MC, C, C, C, C, C, GEPI_F32},
-        {xv, wl1, w.l1, C, C, SR, rv, C, GEPI_F16},
-        {xw, wl1 + (int64_t)rv * C, w.l1 + rv, C, C, SR, rw, C, GEPI_TANH_F16},
-        {xa, wl1 + (int64_t)(rv + rw) * C, w.l1 + rv + rw, C, C, SR, ra, C, GEPI_F16},
-        {xg, wl1 + (int64_t)(rv + rw + ra) * C, w.l1 + rv + rw + ra, C, C, SR, rg, C, GEPI_SIGM_F16},
+        {xv, wl1, w.l1, C, C, SR, rv, C, epi_plain},
+        {xw, wl1 + (int64_t)rv * C, out_at(w.l1, rv), C, C, SR, rw, C, epi_tanh},
+        {xa, wl1 + (int64_t)(rv + rw) * C, out_at(w.l1, rv + rw), C, C, SR, ra, C, epi_plain},
+        {xg, wl1 + (int64_t)(rv + rw + ra) * C, out_at(w.l1, rv + rw + ra), C, C, SR, rg, C, epi_sigm},
     };
     // fragment-order copies (16 x 32 blocks) when the model has them
     const char *Fl = m.layers_frag ? static_cast<const char *>(m.layers_frag) + (int64_t)l * lay.frag_bytes : nullptr;
@@ -415,10 +442,10 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
     for (int g = 0; g < 4; ++g) frag(g1[3 + g], lay.f_l1[g], 0);
     RWKV7_TRY(gemm(g1, 7, M));
     GemmProb g2[4] = {
-        {w.l1, wl2, w.d, SR, SR, C, C, rv, GEPI_F32},
-        {w.l1 + rv, wl2 + rv, w.d + MC, SR, SR, C, C, rw, GEPI_F32},
-        {w.l1 + rv + rw, wl2 + rv + rw, w.d + 2 * MC, SR, SR, C, C, ra, GEPI_F32},
-        {w.l1 + rv + rw + ra, wl2 + rv + rw + ra, w.d + 3 * MC, SR, SR, C, C, rg, GEPI_F32},
+        {at(w.l1, 0), wl2, w.d, SR, SR, C, C, rv, GEPI_F32},
+        {at(w.l1, rv), wl2 + rv, w.d + MC, SR, SR, C, C, rw, GEPI_F32},
+        {at(w.l1, rv + rw), wl2 + rv + rw, w.d + 2 * MC, SR, SR, C, C, ra, GEPI_F32},
+        {at(w.l1, rv + rw + ra), wl2 + rv + rw + ra, w.d + 3 * MC, SR, SR, C, C, rg, GEPI_F32},
     };
     for (int g = 0; g < 4; ++g) frag(g2[g], lay.f_l2[g], 0);
     RWKV7_TRY(gemm(g2, 4, M));
@@ -427,31 +454,37 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
     RWKV7_TRY(launch_wkv7_prefill(sc, st));
     GnGateArgs gn = {w.y, w.rkv, w.kv, w.kv + MC, w.d + 3 * MC, vec, w.yg, C, M};
     gn.bf = bf;
+    gn.out_f32 = a32;
     RWKV7_TRY(launch_gn_gate(gn, st));
-    GemmProb go = {w.yg, reinterpret_cast<const uint16_t *>(L + lay.w_o), w.x0, C, C, C, C, C, GEPI_ADD_F32};
+    GemmProb go = {at(w.yg, 0), reinterpret_cast<const uint16_t *>(L + lay.w_o), w.x0, C, C, C, C, C, GEPI_ADD_F32};
     frag(go, lay.f_o, 0);
     RWKV7_TRY(gemm(&go, 1, M));
 
     LnShiftArgs lc = {w.x0, vec + RWKV7_V_LN2_W * C, vec + RWKV7_V_LN2_B * C, vec + RWKV7_V_FFN_X_K * C,
                       1, w.xmix, cshift, C, T, M};
     lc.bf = bf;
+    lc.out_f32 = a32;
     RWKV7_TRY(launch_ln_shift(lc, st));
-    GemmProb gk = {w.xmix, reinterpret_cast<const uint16_t *>(L + lay.w_fk), w.hid, C, C, F, F, C, GEPI_RELUSQ};
+    GemmProb gk = {at(w.xmix, 0), reinterpret_cast<const uint16_t *>(L + lay.w_fk), w.hid, C, C, F, F, C, epi_relusq};
     frag(gk, lay.f_fk, 0);
     RWKV7_TRY(gemm(&gk, 1, M));
-    GemmProb gv = {w.hid, reinterpret_cast<const uint16_t *>(L + lay.w_fv), w.x0, F, F, C, C, F, GEPI_ADD_F32};
+    GemmProb gv = {at(w.hid, 0), reinterpret_cast<const uint16_t *>(L + lay.w_fv), w.x0, F, F, C, C, F, GEPI_ADD_F32};
     frag(gv, lay.f_fv, 0);
     RWKV7_TRY(gemm(&gv, 1, M));
   }
   if (logits) {
+    // B rows: the head GEMM always takes f32 A (B is far below the large-M path)
     const float *lo = static_cast<const float *>(m.ln_out);
-    RWKV7_TRY(launch_ln_rows(w.x0, 1, lo, lo + C, w.headin, 0, B, C, T, T - 1, bf, st));
-    GemmProb gh = {w.headin, static_cast<const uint16_t *>(m.head), logits, C, C, d.vocab, d.vocab, C, GEPI_F16};
+    RWKV7_TRY(launch_ln_rows(w.x0, 1, lo, lo + C, w.headin, 1, B, C, T, T - 1, bf, st));
+    GemmProb gh = {static_cast<const uint16_t *>(w.headin), static_cast<const uint16_t *>(m.head), logits, C, C,
+                   d.vocab, d.vocab, C, GEPI_F16};
     if (m.head_frag) {
       gh.Wf = static_cast<const uint16_t *>(m.head_frag);
       gh.nksf = (C + 31) / 32;
     }
-    RWKV7_TRY(gemm(&gh, 1, B));
+    gh.bf = bf;
+    gh.a32 = 1;
+    RWKV7_TRY(launch_gemm_group(&gh, 1, B, st, w.part, ctr));
   }
   return RWKV7_OK;
 }
@@ -537,6 +570,13 @@ int rwkv7_decode_launches(const rwkv7_model *model, int32_t batch, int32_t with_
   // head GEMM
   if (batch == 1) return 1 + 6 * dims->n_layer + (with_logits ? 1 : 0);
   return 1 + 7 * dims->n_layer + (with_logits ? 2 : 0);
+}
+
+int rwkv7_step_f32_activations(const rwkv7_model *model, int32_t batch, int32_t seq_len) {
+  if (!model || check_dims(&model->dims) != RWKV7_OK || batch < 1 || seq_len < 1) return -1;
+  if (seq_len == 1 && use_persistent_decode(*model, batch, true)) return 1;  // fp32 activations throughout
+  if (use_rows_kernel(*model, batch, seq_len)) return 1;                     // f32 rows, hi/lo MFMA
+  return batch_a32(model->dims, batch * seq_len) ? 1 : 0;
 }
 
 int rwkv7_decode(const rwkv7_model *model, const rwkv7_state *state, const int64_t *tokens, void *logits,
@@ -697,10 +737,11 @@ int rwkv7_gemv_f16(const float *x, const void *W, int64_t ldw, float *y, int32_t
 int rwkv7_gemm_f16(const void *A, int64_t lda, const void *W, int64_t ldw, void *Y, int64_t ldy, int32_t M, int32_t N,
                    int32_t K, int32_t epi, int32_t bf16, void *stream) {
   if (!A || !W || !Y) return RWKV7_EINVAL;
-  if (epi < 0 || epi > 3) return RWKV7_EINVAL;
+  if (epi < 0 || epi > GEPI_SIGM_F32 || (bf16 & ~(RWKV7_GEMM_BF16 | RWKV7_GEMM_A_F32))) return RWKV7_EINVAL;
   if (M < 1 || N < 1 || K < 8 || lda < K || ldw < K || ldy < N) return RWKV7_ESHAPE;
   GemmProb p = {static_cast<const uint16_t *>(A), static_cast<const uint16_t *>(W), Y, lda, ldw, ldy, N, K, epi};
-  p.bf = bf16 ? 1 : 0;
+  p.bf = (bf16 & RWKV7_GEMM_BF16) ? 1 : 0;
+  p.a32 = (bf16 & RWKV7_GEMM_A_F32) ? 1 : 0;
   return launch_gemm_group(&p, 1, M, static_cast<hipStream_t>(stream), nullptr, nullptr);
 }
 

@@ -20,8 +20,12 @@
 //
 // Matrix stages run on MFMA (v_mfma_f32_16x16x32_f16): a block is 16 weight
 // rows of the fragment arena (one contiguous KiB per 16 x 32 fragment), the A
-// operand is the M activation rows (padded to 16) staged in LDS as f16, and
+// operand is the M activation rows (padded to 16) staged in LDS as f32, and
 // the 8 waves of the workgroup split K and sum their 16 x 16 tiles in LDS.
+// Each A fragment is split in registers into its 16-bit part and the 16-bit
+// remainder (split_hi_lo) and both are multiplied by the weight fragment, so
+// the activations keep fp32-grade precision; the hand-off payloads (residual
+// rows, per-head outputs, FFN hidden rows) are f32.
 //
 // Hand-offs. P2 -> P3, P3 -> P4, P4 -> P5 and P5 -> next P1 (the residual
 // rows x, the per-head outputs, the FFN hidden rows): the producer of a block
@@ -61,12 +65,13 @@ constexpr int kRT = 512;             // threads per workgroup
 constexpr int kRW = kRT / 64;        // waves
 constexpr int kRSpin = 1 << 21;      // polls before a wait gives up
 constexpr int kRMaxC = 1024;         // A tiles of C columns live in LDS
-constexpr int kRLdA = kRMaxC + 8;    // halves per LDS A row (padding spreads the 16 rows over the banks)
+constexpr int kRLdX = kRMaxC + 4;    // floats per LDS row of xs (padding spreads the 16 rows over the banks)
+constexpr int kRLdA = kRMaxC + 8;    // halves per row of the second LDS region (P2 scratch)
 constexpr int kRMaxG = 1024;
-// P2 keeps the activated LoRA first steps (f16 [16][552]), the second steps
-// and gates of up to 16 tokens (f32 [16][256 + 512] + 16) in the xs and A
-// regions
-static_assert(16 * 552 * 2 + (16 * (256 + 512) + 16) * 4 <= 16 * kRMaxC * 4 + 16 * kRLdA * 2, "P2 scratch");
+// P2 keeps the activated LoRA first steps (f32 [16][552]), the second steps
+// and gates of up to 16 tokens (f32 [16][256 + 512] + 16) in the xs and
+// scratch regions
+static_assert(16 * 552 * 4 + (16 * (256 + 512) + 16) * 4 <= 16 * kRLdX * 4 + 16 * kRLdA * 2, "P2 scratch");
 
 // sync words (byte offsets 0, 16): epoch, abort; then kRMaxG start words
 enum { RS_EPOCH = 0, RS_ABORT = 4 };
@@ -87,9 +92,9 @@ struct RkArgs {
   unsigned *sync, *started, *errors;
   unsigned *fl[5];   // per-stage flags: P2 units, P3 blocks, P4 blocks, P5 blocks (fl[0] unused: P1 hands off tagged words)
   uint64_t *proj;    // [M, 3C + SR] f32 as tagged words
-  unsigned *core;    // [M, C/2] f16 pairs
+  float *core;       // [M, C]
   float *x;          // [M, C]
-  unsigned *hid;     // [M, F/2] f16 pairs
+  float *hid;        // [M, F]
   uint64_t *part;    // [C/16, 4, 256] FFN-value partial tiles of K-quarters 1..3 (tagged words)
   float *vfirst;     // [M, C]
 };
@@ -209,8 +214,8 @@ RWKV7_DEV void read_words(const RkCtx &cx, __amdgpu_buffer_rsrc_t r, unsigned ta
 }
 
 struct RkLds {
-  float *xs;        // [M][C] the stage's input rows (f32)
-  uint16_t *A;      // [16][kRLdA] the MFMA A operand (f16)
+  float *xs;        // [16][kRLdX] the stage's input rows, then its MFMA A operand (f32)
+  uint16_t *A;      // [16][kRLdA] second region, P2 scratch (with xs)
   float *red;       // [kRW][256] per-wave partial tiles
   float *stat;      // [16][4] LN mean, rstd of each row
   float *u;         // P2 scratch
@@ -232,7 +237,7 @@ RWKV7_DEV void row_stats(const RkLds &s, int M, int C) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int c = 4 * l32 + 128 * j;
-    v[j] = live && c < C ? *reinterpret_cast<const float4 *>(s.xs + m * C + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    v[j] = live && c < C ? *reinterpret_cast<const float4 *>(s.xs + m * kRLdX + c) : make_float4(0.f, 0.f, 0.f, 0.f);
     acc += (v[j].x + v[j].y) + (v[j].z + v[j].w);
   }
   acc = sum16(acc);
@@ -281,59 +286,48 @@ RWKV7_DEV unsigned pack_h2(float lo, float hi) {
   return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2v{lo, hi}, f16x2v));
 }
 
-// A[m][k] = f16(ln(m) + mu[k] (prev(m) - ln(m))) for rows m < M, with ln(m) =
-// LayerNorm of row m and prev(m) = ln(m - 1) within a sequence, the f16 shift
-// state (sst) for its first token. Rows M..15 of A are left as they are: they
-// only reach output rows that are never stored. Thread -> 4 columns (LN
-// weight, bias and mix from load_mix, loaded before the stage's wait) and a
-// contiguous range of rows (the kRT / (C / 4) thread groups split the rows; a
-// range that starts inside a sequence recomputes the LayerNorm of the row
-// before it). With c0 >= 0, columns [c0, c0 + 16) of each sequence's last
-// LayerNorm row -- the new shift state -- also go to slice ([B][16] f16, LDS).
+// xs[m][k] <- ln(m) + mu[k] (prev(m) - ln(m)) for rows m < M, in place (f32),
+// with ln(m) = LayerNorm of row m (statistics from row_stats) and prev(m) =
+// ln(m - 1) within a sequence, the f16 shift state (sst) for its first token.
+// Rows M..15 are left as they are: they only reach output rows that are never
+// stored. Thread t < C / 2 owns columns 2t, 2t + 1 of every row (LN weight,
+// bias and mix from load_mix, loaded before the stage's wait) and walks the
+// rows in order, keeping ln(m - 1) in registers, so the in-place update never
+// overwrites a value another thread still reads. With c0 >= 0, columns
+// [c0, c0 + 16) of each sequence's last LayerNorm row -- the new shift state
+// -- also go to slice ([B][16] f16, LDS).
 struct MixVec {
-  float4 w, b, u;  // LN weight, LN bias, mix of this thread's 4 columns
+  float2 w, b, u;  // LN weight, LN bias, mix of this thread's 2 columns
 };
 RWKV7_DEV MixVec load_mix(const float *lw, const float *lb, const float *mu, int C) {
-  const int k = 4 * (threadIdx.x % (C / 4));
+  const int k = 2 * (threadIdx.x % (C / 2));
   MixVec v;
-  v.w = *reinterpret_cast<const float4 *>(lw + k);
-  v.b = *reinterpret_cast<const float4 *>(lb + k);
-  v.u = *reinterpret_cast<const float4 *>(mu + k);
+  v.w = *reinterpret_cast<const float2 *>(lw + k);
+  v.b = *reinterpret_cast<const float2 *>(lb + k);
+  v.u = *reinterpret_cast<const float2 *>(mu + k);
   return v;
 }
 
 RWKV7_DEV void build_mix(const RkLds &s, const RkArgs &a, int C, const MixVec &mv, uint16_t *slice, int c0) {
+  if ((int)threadIdx.x >= C / 2) return;
   const int M = a.M, T = a.T;
-  const int nq = C / 4, ng = kRT / nq;
-  const int q = threadIdx.x % nq, grp = threadIdx.x / nq;
-  if (grp >= ng) return;
-  const int rpg = (M + ng - 1) / ng;
-  const int m0 = grp * rpg, m1 = min(M, m0 + rpg);
-  if (m0 >= m1) return;
-  const int k = 4 * q;
-  const float4 w = mv.w, bias = mv.b, u = mv.u;
+  const int k = 2 * threadIdx.x;
+  const float2 w = mv.w, bias = mv.b, u = mv.u;
   const bool shift_cols = c0 >= 0 && k >= c0 && k < c0 + 16;
-  auto ln_row = [&](int m) {
-    const float4 x = *reinterpret_cast<const float4 *>(s.xs + m * C + k);
+  float2 p = make_float2(0.f, 0.f);
+  int t = 0, b = 0;
+  for (int m = 0; m < M; ++m) {
+    float2 *xp = reinterpret_cast<float2 *>(s.xs + m * kRLdX + k);
+    const float2 x = *xp;
     const float2 st = *reinterpret_cast<const float2 *>(s.stat + 4 * m);  // mean, 1/std
     const float nm = -st.x * st.y;
-    return make_float4(fmaf(fmaf(x.x, st.y, nm), w.x, bias.x), fmaf(fmaf(x.y, st.y, nm), w.y, bias.y),
-                       fmaf(fmaf(x.z, st.y, nm), w.z, bias.z), fmaf(fmaf(x.w, st.y, nm), w.w, bias.w));
-  };
-  int t = m0 % T, b = m0 / T;
-  float4 p = t > 0 ? ln_row(m0 - 1) : make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int m = m0; m < m1; ++m) {
-    const float4 ln = ln_row(m);
+    const float2 ln = make_float2(fmaf(fmaf(x.x, st.y, nm), w.x, bias.x), fmaf(fmaf(x.y, st.y, nm), w.y, bias.y));
     if (t == 0) {
-      const uint2 st = *reinterpret_cast<const uint2 *>(s.sst + b * C + k);
-      p = make_float4(h2f((uint16_t)(st.x & 0xFFFFu)), h2f((uint16_t)(st.x >> 16)), h2f((uint16_t)(st.y & 0xFFFFu)),
-                      h2f((uint16_t)(st.y >> 16)));
+      const unsigned sv = *reinterpret_cast<const unsigned *>(s.sst + b * C + k);
+      p = make_float2(h2f((uint16_t)(sv & 0xFFFFu)), h2f((uint16_t)(sv >> 16)));
     }
-    const float v0 = fmaf(u.x, p.x - ln.x, ln.x), v1 = fmaf(u.y, p.y - ln.y, ln.y);
-    const float v2 = fmaf(u.z, p.z - ln.z, ln.z), v3 = fmaf(u.w, p.w - ln.w, ln.w);
-    *reinterpret_cast<uint2 *>(s.A + m * kRLdA + k) = make_uint2(pack_h2(v0, v1), pack_h2(v2, v3));
-    if (t == T - 1 && shift_cols)
-      *reinterpret_cast<uint2 *>(slice + b * 16 + (k - c0)) = make_uint2(pack_h2(ln.x, ln.y), pack_h2(ln.z, ln.w));
+    *xp = make_float2(fmaf(u.x, p.x - ln.x, ln.x), fmaf(u.y, p.y - ln.y, ln.y));
+    if (t == T - 1 && shift_cols) *reinterpret_cast<unsigned *>(slice + b * 16 + (k - c0)) = pack_h2(ln.x, ln.y);
     p = ln;
     if (++t == T) t = 0, ++b;
   }
@@ -360,7 +354,8 @@ RWKV7_DEV WBlock load_block(const uint16_t *wf, int k0step, int nks) {
   return b;
 }
 
-// The block times the A tile (A columns 32 k .. 32 k + 31 for k-step k).
+// The block times the A tile (xs columns 32 k .. 32 k + 31 for k-step k, f32,
+// each fragment split into its f16 part and f16 remainder: two MFMAs).
 // Returns the wave's partial 16 x 16 tile (zero on wave 0), rows = A rows,
 // columns = the block's weight rows.
 RWKV7_DEV floatx4 block_mma(const RkLds &s, const WBlock &wb, int nks) {
@@ -371,8 +366,11 @@ RWKV7_DEV floatx4 block_mma(const RkLds &s, const WBlock &wb, int nks) {
   for (int j = 0; j < 5; ++j) {
     const int kj = wv - 1 + kWW * j;
     if (kj < nks) {
-      const uint4 af = *reinterpret_cast<const uint4 *>(&s.A[(lane & 15) * kRLdA + 32 * kj + 8 * (lane >> 4)]);
-      acc = mfma16<false>(af, wb.w[j], acc);
+      const float *ap = s.xs + (lane & 15) * kRLdX + 32 * kj + 8 * (lane >> 4);
+      uint4 hi, lo;
+      split_hi_lo<false>(*reinterpret_cast<const uint4 *>(ap), *reinterpret_cast<const uint4 *>(ap + 4), hi, lo);
+      acc = mfma16<false>(hi, wb.w[j], acc);
+      acc = mfma16<false>(lo, wb.w[j], acc);
     }
   }
   return acc;
@@ -394,43 +392,27 @@ RWKV7_DEV float reduce_tile(const RkLds &s, const floatx4 &acc, int *m_out, int 
   return v;
 }
 
-// Reads the [M][C] f32 vector buffer x into xs (device-scope), every load of
-// the thread (at most 8: M C <= 16 kRMaxC floats) in flight before the first
-// LDS store.
-RWKV7_DEV void read_x(const RkLds &s, const float *x, int M, int C) {
-  const __amdgpu_buffer_rsrc_t r = rrsrc(x, (int64_t)M * C * 4);
-  const int n = M * C / 4;
+// Reads columns [c0, c0 + K) of an [M][ld] f32 buffer (device-scope) into xs
+// rows 0..M-1 (K <= kRMaxC), zero rows M..15 when zero_rest; every load of
+// the thread (at most 8) in flight before the first LDS store.
+RWKV7_DEV void read_rows(const RkLds &s, const float *src, int ld, int c0, int K, int M, bool zero_rest) {
+  const __amdgpu_buffer_rsrc_t r = rrsrc(src, (int64_t)M * ld * 4);
+  const int q = K / 4;  // 16-byte pieces per row
+  const int rows = zero_rest ? 16 : M;
   floatx4 v[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const int i = threadIdx.x + j * kRT;
-    v[j] = i < n ? rld16f(r, 16 * i) : floatx4{0.f, 0.f, 0.f, 0.f};
+    const int i = threadIdx.x + j * kRT, m = i / q, p = i - m * q;
+    v[j] = m < M ? rld16f(r, 4 * (m * ld + c0 + 4 * p)) : floatx4{0.f, 0.f, 0.f, 0.f};
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const int i = threadIdx.x + j * kRT;
-    if (i < n) *reinterpret_cast<floatx4 *>(&s.xs[4 * i]) = v[j];
+    const int i = threadIdx.x + j * kRT, m = i / q, p = i - m * q;
+    if (m < rows) *reinterpret_cast<floatx4 *>(&s.xs[m * kRLdX + 4 * p]) = v[j];
   }
 }
-
-// Reads columns [c0, c0 + K) of an [M][ld] f16-pair buffer into A rows 0..M-1,
-// zero rows M..15; every load of the thread (at most 4: K <= kRMaxC) in
-// flight before the first LDS store.
-RWKV7_DEV void read_pairs(const RkLds &s, const unsigned *src, int ld, int c0, int K, int M) {
-  const __amdgpu_buffer_rsrc_t r = rrsrc(src, (int64_t)M * ld * 2);
-  const int q = K / 8;  // 16-byte pieces per row
-  u32x4r v[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int i = threadIdx.x + j * kRT, m = i / q, p = i - m * q;
-    v[j] = m < M ? rld16(r, 2 * (m * ld + c0 + 8 * p)) : u32x4r{0u, 0u, 0u, 0u};
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int i = threadIdx.x + j * kRT, m = i / q, p = i - m * q;
-    if (m < 16) *reinterpret_cast<uint4 *>(&s.A[m * kRLdA + 8 * p]) = make_uint4(v[j][0], v[j][1], v[j][2], v[j][3]);
-  }
-}
+// The [M][C] f32 residual rows x into xs.
+RWKV7_DEV void read_x(const RkLds &s, const float *x, int M, int C) { read_rows(s, x, C, 0, C, M, false); }
 
 RWKV7_DEV int64_t clamp_tok(int64_t id, int V) { return id < 0 ? 0 : id >= V ? V - 1 : id; }
 
@@ -449,7 +431,7 @@ RWKV7_DEV void embed_rows(const RkLds &s, const RkArgs &a) {
     for (int m = 0; m < 16; ++m) v[m] = m < M ? h2f(a.emb[id[m] + k]) : 0.f;
 #pragma unroll
     for (int m = 0; m < 16; ++m)
-      if (m < M) s.xs[m * C + k] = v[m];
+      if (m < M) s.xs[m * kRLdX + k] = v[m];
   }
 }
 
@@ -485,9 +467,9 @@ RWKV7_DEV void store_shift_slice(const RkArgs &a, const uint16_t *slice, uint16_
 //       only on the precomputed gates)
 //   C   GroupNorm over the head, bonus, output gate, one wave per token
 // Per token this is the one-token core's arithmetic (tmix.hip,
-// tmix_decode_kernel) with the LoRA activations rounded to f16 as the
-// multi-token path rounds them (its second-step GEMM operands).
-constexpr int kLoraLd = 512 + 40;  // halves per LDS LoRA row: SR <= 512, a zeroed 32-wide tail, 16-byte rows
+// tmix_decode_kernel), the LoRA activations multiplied as f16 parts and f16
+// remainders.
+constexpr int kLoraLd = 512 + 40;  // floats per LDS LoRA row: SR <= 512, a zeroed 32-wide tail, 16-byte rows
 RWKV7_DEV void p2_unit(const RkArgs &a, const RkLds &s, const RkCtx &cx, int l, int b, int h) {
   const int t = threadIdx.x, wv = t >> 6, lane = t & 63;
   const int C = a.C, SR = a.SR, T = a.T;
@@ -495,8 +477,8 @@ RWKV7_DEV void p2_unit(const RkArgs &a, const RkLds &s, const RkCtx &cx, int l, 
   const char *Lp = a.layers + (int64_t)l * a.lbytes;
   const float *vec = reinterpret_cast<const float *>(Lp + a.o_vec);
   const uint16_t *l2 = reinterpret_cast<const uint16_t *>(Lp + a.o_l2);
-  uint16_t *s_l16 = reinterpret_cast<uint16_t *>(s.u);            // [16][kLoraLd] f16
-  float *s_d = s.u + 16 * kLoraLd / 2;                             // [T][4][64] LoRA second steps v w a g
+  float *s_l32 = s.u;                                              // [16][kLoraLd] f32
+  float *s_d = s.u + 16 * kLoraLd;                                 // [T][4][64] LoRA second steps v w a g
   float *s_g = s_d + 16 * 256;                                     // [T][8][64] r w kn v kh b g y
   float *s_rk = s_g + 16 * 512;                                    // [T]
   const int ch = h * kN + lane;
@@ -575,7 +557,7 @@ RWKV7_DEV void p2_unit(const RkArgs &a, const RkLds &s, const RkCtx &cx, int l, 
           // tanh on the w group, sigmoid on the g group (j and j + 1 share a group: ranks are even)
           if (j >= a.rv && j < a.rv + a.rw) x0 = tanhf(x0), x1 = tanhf(x1);
           else if (j >= a.rv + a.rw + a.ra) x0 = sigmoidf_(x0), x1 = sigmoidf_(x1);
-          *reinterpret_cast<unsigned *>(&s_l16[m * kLoraLd + j]) = pack_h2(x0, x1);
+          *reinterpret_cast<float2 *>(&s_l32[m * kLoraLd + j]) = make_float2(x0, x1);
         }
       }
 #pragma unroll
@@ -610,7 +592,7 @@ RWKV7_DEV void p2_unit(const RkArgs &a, const RkLds &s, const RkCtx &cx, int l, 
     }
   }
   if (t < 32)  // the zero tail past the last group (a partial k-step of a rank-16 group reads into it)
-    for (int m = 0; m < T; ++m) s_l16[m * kLoraLd + SR + t] = 0;
+    for (int m = 0; m < T; ++m) s_l32[m * kLoraLd + SR + t] = 0.f;
   __syncthreads();
   const bool ok = !cx.failed();
 #pragma unroll
@@ -620,9 +602,11 @@ RWKV7_DEV void p2_unit(const RkArgs &a, const RkLds &s, const RkCtx &cx, int l, 
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       if (32 * ks < grank[e]) {
-        const uint4 af =
-            *reinterpret_cast<const uint4 *>(&s_l16[(lane & 15) * kLoraLd + goff[e] + 32 * ks + 8 * (lane >> 4)]);
-        acc = mfma16<false>(af, wq[e][ks], acc);
+        const float *ap = &s_l32[(lane & 15) * kLoraLd + goff[e] + 32 * ks + 8 * (lane >> 4)];
+        uint4 hi, lo;
+        split_hi_lo<false>(*reinterpret_cast<const uint4 *>(ap), *reinterpret_cast<const uint4 *>(ap + 4), hi, lo);
+        acc = mfma16<false>(hi, wq[e][ks], acc);
+        acc = mfma16<false>(lo, wq[e][ks], acc);
       }
     }
 #pragma unroll
@@ -698,11 +682,7 @@ RWKV7_DEV void p2_unit(const RkArgs &a, const RkLds &s, const RkCtx &cx, int l, 
     const float var = wave_sum(dy * dy) * (1.f / kN);
     const float yn = dy * rsqrtf(var + kGnEps) * v_lw + v_lb;
     const float out = (yn + s_rk[m] * gm[192 + lane]) * gm[384 + lane];
-    const float nb = dpp<kDppXor1>(out);
-    if ((lane & 1) == 0 && ok) {
-      const unsigned pair = (unsigned)f2h(out) | ((unsigned)f2h(nb) << 16);
-      rst(a.core + ((int64_t)mg * C + ch) / 2, pair);
-    }
+    if (ok) rst_f(a.core + (int64_t)mg * C + ch, out);
   }
   if (ok && !cx.failed()) {
     Sp[0] = make_float4(S[0], S[1], S[2], S[3]);
@@ -716,9 +696,9 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
   const int C = a.C, F = a.F, M = a.M, L = a.L, G = a.G, SR = a.SR;
   const int g = blockIdx.x;
   RkLds s;
-  s.xs = reinterpret_cast<float *>(rsmem);                       // 16 C floats
-  s.A = reinterpret_cast<uint16_t *>(rsmem + 16 * kRMaxC * 4);   // 16 kRLdA halves
-  s.red = reinterpret_cast<float *>(rsmem + 16 * kRMaxC * 4 + 16 * kRLdA * 2);
+  s.xs = reinterpret_cast<float *>(rsmem);                       // 16 kRLdX floats
+  s.A = reinterpret_cast<uint16_t *>(rsmem + 16 * kRLdX * 4);    // 16 kRLdA halves
+  s.red = reinterpret_cast<float *>(rsmem + 16 * kRLdX * 4 + 16 * kRLdA * 2);
   s.stat = s.red + kRW * 256;
   s.fail = reinterpret_cast<unsigned *>(s.stat + 64);
   s.ep = s.fail + 1;
@@ -726,7 +706,7 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
   s.shs1 = reinterpret_cast<uint16_t *>(s.fail + 32);
   s.shs2 = s.shs1 + 256;
   s.sst = s.shs2 + 256;
-  s.u = s.xs;  // P2 scratch: the input rows and the A tile (contiguous)
+  s.u = s.xs;  // P2 scratch: xs and the second region (contiguous)
   if (threadIdx.x == 0) {
     const unsigned e = rld(a.sync + RS_EPOCH);
     *s.ep = e;
@@ -816,7 +796,7 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
       const int mr = 4 * ((t & 63) >> 4) + (t >> 6), cr = 16 * b3 + (t & 15);
       const float res = threadIdx.x >= 256 && mr < M ? residual_in(a, l, mr, cr) : 0.f;
       wait_flags(cx, a.fl[1], nP2, cx.tag(l, 1), ident);
-      read_pairs(s, a.core, C, 0, C, M);
+      read_rows(s, a.core, C, 0, C, M, true);
       __syncthreads();
       const floatx4 acc = block_mma(s, wb, nksC);
       int m, n;
@@ -847,11 +827,7 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
       float v = reduce_tile(s, acc, &m, &n);
       v = fmaxf(v, 0.f);
       v = v * v;
-      const float nb = dpp<kDppXor1>(v);
-      if (threadIdx.x < 256 && m < M && (n & 1) == 0 && !cx.failed()) {
-        const unsigned pair = (unsigned)f2h(v) | ((unsigned)f2h(nb) << 16);
-        rst(a.hid + ((int64_t)m * F + 16 * b4 + n) / 2, pair);
-      }
+      if (threadIdx.x < 256 && m < M && !cx.failed()) rst_f(a.hid + (int64_t)m * F + 16 * b4 + n, v);
       publish_flag(cx, a.fl[3] + b4, cx.tag(l, 3));
     }
     // ---------------- P5 ----------------
@@ -866,7 +842,7 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
       const int t = threadIdx.x & 255;
       const int mr = 4 * ((t & 63) >> 4) + (t >> 6), cr = 16 * b5 + (t & 15);
       const float res = mr < M ? rld_f(a.x + (int64_t)mr * C + cr) : 0.f;
-      read_pairs(s, a.hid, F, q * Kq, Kq, M);
+      read_rows(s, a.hid, F, q * Kq, Kq, M, true);
       __syncthreads();
       const floatx4 acc = block_mma(s, wb, nksQ);
       int m, n;
@@ -908,18 +884,21 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int i = threadIdx.x + j * kRT;
-      if (i < n) *reinterpret_cast<floatx4 *>(&s.xs[4 * i]) = v[j];
+      const int i = threadIdx.x + j * kRT, bb = (4 * i) / C, k = 4 * i - bb * C;
+      if (i < n) *reinterpret_cast<floatx4 *>(&s.xs[bb * kRLdX + k]) = v[j];
     }
     __syncthreads();
     row_stats(s, B, C);
     __syncthreads();
-    for (int k = 2 * threadIdx.x; k < C; k += 2 * kRT) {
+    // LN_out in place (f32): thread t < C / 2 owns columns 2t, 2t + 1
+    if ((int)threadIdx.x < C / 2) {
+      const int k = 2 * threadIdx.x;
       const float w0 = a.ln_out[k], w1 = a.ln_out[k + 1], b0 = a.ln_out[C + k], b1 = a.ln_out[C + k + 1];
       for (int m = 0; m < B; ++m) {
         const float mean = s.stat[4 * m], rs = s.stat[4 * m + 1];
-        const float v0 = (s.xs[m * C + k] - mean) * rs * w0 + b0, v1 = (s.xs[m * C + k + 1] - mean) * rs * w1 + b1;
-        *reinterpret_cast<unsigned *>(s.A + m * kRLdA + k) = pack_h2(v0, v1);
+        float2 *xp = reinterpret_cast<float2 *>(s.xs + m * kRLdX + k);
+        const float2 x = *xp;
+        *xp = make_float2((x.x - mean) * rs * w0 + b0, (x.y - mean) * rs * w1 + b1);
       }
     }
     __syncthreads();
@@ -959,7 +938,7 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
 }
 
 constexpr int64_t rows_lds_bytes() {
-  return 16 * kRMaxC * 4 + 16 * kRLdA * 2 + kRW * 256 * 4 + 64 * 4 + 128 + 2 * 256 * 2 + 16 * kRMaxC * 2;
+  return 16 * kRLdX * 4 + 16 * kRLdA * 2 + kRW * 256 * 4 + 64 * 4 + 128 + 2 * 256 * 2 + 16 * kRMaxC * 2;
 }
 
 // Per device, checked once with that device current: 1 when the kernel's
@@ -976,9 +955,9 @@ int64_t rows_exchange_bytes(const rwkv7_dims &d) {
   int64_t o = kRSyncBytes + al(4 * kRMaxG);
   o += al(4 * 16 * H) + al(4 * (C / 16)) + al(4 * (F / 16)) + al(4 * (C / 16));
   o += al(M * (3 * C + SR) * 8);      // proj
-  o += al(M * C * 2);                 // core
+  o += al(M * C * 4);                 // core
   o += al(M * C * 4);                 // x
-  o += al(M * F * 2);                 // hid
+  o += al(M * F * 4);                 // hid
   o += al((C / 16) * 4 * 256 * 8);    // part
   o += al(M * C * 4);                 // vfirst
   return o;
@@ -1072,12 +1051,12 @@ int launch_rows_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const rw
   }
   a.proj = reinterpret_cast<uint64_t *>(p);
   p += al(M * (3 * C + SR) * 8);
-  a.core = reinterpret_cast<unsigned *>(p);
-  p += al(M * C * 2);
+  a.core = reinterpret_cast<float *>(p);
+  p += al(M * C * 4);
   a.x = reinterpret_cast<float *>(p);
   p += al(M * C * 4);
-  a.hid = reinterpret_cast<unsigned *>(p);
-  p += al(M * F * 2);
+  a.hid = reinterpret_cast<float *>(p);
+  p += al(M * F * 4);
   a.part = reinterpret_cast<uint64_t *>(p);
   p += al((C / 16) * 4 * 256 * 8);
   a.vfirst = reinterpret_cast<float *>(p);

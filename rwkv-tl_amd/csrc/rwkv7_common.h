@@ -161,6 +161,29 @@ RWKV7_DEV floatx4 mfma16(const T &a, const T &b, const floatx4 &c) {
                                                   0, 0);
 }
 
+// Eight f32 values (two 16-byte words, in order) as two MFMA operands of
+// format F16T<BF>: hi = each value rounded to 16 bits, lo = the remainder
+// x - hi (exact in fp32) rounded to 16 bits. hi + lo carries 22 significant
+// bits for IEEE half (16 for bfloat16), so two MFMAs against the same 16-bit
+// weights multiply f32 activations to about fp32 precision; for half, a
+// remainder below the smallest subnormal (|x| < 2^-13) is lost, an absolute
+// error under 2^-25.
+template <bool BF>
+RWKV7_DEV void split_hi_lo(const uint4 &a, const uint4 &b, uint4 &hi, uint4 &lo) {
+  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float x0 = __builtin_bit_cast(float, w[2 * i]), x1 = __builtin_bit_cast(float, w[2 * i + 1]);
+    const uint16_t h0 = F16T<BF>::from_f(x0), h1 = F16T<BF>::from_f(x1);
+    const uint16_t l0 = F16T<BF>::from_f(x0 - F16T<BF>::to_f(h0)), l1 = F16T<BF>::from_f(x1 - F16T<BF>::to_f(h1));
+    h[i] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+    l[i] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+  }
+  hi = make_uint4(h[0], h[1], h[2], h[3]);
+  lo = make_uint4(l[0], l[1], l[2], l[3]);
+}
+
 RWKV7_DEV float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
 
 // Weight streams are read exactly once per step: load them non-temporally so

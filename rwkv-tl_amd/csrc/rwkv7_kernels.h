@@ -82,10 +82,11 @@ struct LnShiftArgs {
   const float *ln_w, *ln_b;
   const float *mu;
   int n_mix;
-  uint16_t *out;
+  void *out;  // [n_mix][M][C]: f32 if out_f32, else 16-bit
   uint16_t *shift;
   int C, T, M;
-  int bf;  // out and shift are bfloat16 (else half)
+  int bf;       // the 16-bit out and shift are bfloat16 (else half)
+  int out_f32;  // out is f32 (the GEMMs then take it as f32 A)
 };
 int launch_ln_shift(const LnShiftArgs &a, hipStream_t st);
 
@@ -127,9 +128,10 @@ int launch_wkv7_chunked(const ScanArgs<TI, TW, TY> &p, float *rec, hipStream_t s
 
 struct GnGateArgs {
   const float *y, *r, *kn, *v, *g, *vec;
-  uint16_t *out;
+  void *out;  // [M][C]: f32 if out_f32, else 16-bit
   int C, M;
-  int bf;  // out is bfloat16 (else half)
+  int bf;  // a 16-bit out is bfloat16 (else half)
+  int out_f32;
 };
 int launch_gn_gate(const GnGateArgs &a, hipStream_t st);
 
@@ -141,7 +143,18 @@ int launch_lerp(const uint16_t *x, const uint16_t *prev, const float *mu, int n_
                 uint16_t *x_copy, int C, int bf, hipStream_t st);
 int launch_store_f16(const float *src, uint16_t *dst, int n, int bf, hipStream_t st);
 
-enum { GEPI_F32 = 0, GEPI_F16 = 1, GEPI_RELUSQ = 2, GEPI_ADD_F32 = 3, GEPI_TANH_F16 = 4, GEPI_SIGM_F16 = 5 };
+enum {
+  GEPI_F32 = 0,
+  GEPI_F16 = 1,
+  GEPI_RELUSQ = 2,
+  GEPI_ADD_F32 = 3,
+  GEPI_TANH_F16 = 4,
+  GEPI_SIGM_F16 = 5,
+  // the same activations stored as f32
+  GEPI_RELUSQ_F32 = 6,
+  GEPI_TANH_F32 = 7,
+  GEPI_SIGM_F32 = 8,
+};
 struct GemmProb {
   const uint16_t *A, *W;
   void *Y;
@@ -154,7 +167,16 @@ struct GemmProb {
   // A, W and the 16-bit outputs are bfloat16 (else IEEE half); one value for
   // every problem of a launch
   int bf;
+  // A is f32 (lda in floats), multiplied as its 16-bit hi part plus the 16-bit
+  // remainder (split_hi_lo: two MFMAs per weight fragment), so the product
+  // has fp32-grade activations; one value for every problem of a launch, and
+  // such problems never take the large-M path (gemm_big_min_rows)
+  int a32;
 };
+// The fewest rows M at which an N-column problem may take the large-M path
+// (whose operands stream global -> LDS as 16-bit words): callers that want
+// f32 activations (a32) keep M below this for every N of a group.
+int gemm_big_min_rows(int N);
 // Split-K workspace: gemm_ws_bytes(M, cus) bytes of partial tiles and
 // kGemmCounters arrival counters that start at zero (every launch leaves them
 // at zero). With part == nullptr no problem is split.

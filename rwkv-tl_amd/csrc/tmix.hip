@@ -1242,6 +1242,12 @@ RWKV7_DEV void block_sum3(float &a, float &b, float &c, float (*red)[4]) {
   c = (red[2][0] + red[2][1]) + (red[2][2] + red[2][3]);
 }
 
+// A mixed value into the output: f32, or the model's 16-bit format.
+RWKV7_DEV void store_mix(const LnShiftArgs &a, int64_t i, float v) {
+  if (a.out_f32) static_cast<float *>(a.out)[i] = v;
+  else static_cast<uint16_t *>(a.out)[i] = f_to_u16(v, a.bf);
+}
+
 // One row per workgroup, every load up front (measured faster than the
 // kernel below for C <= 1024 below 1024 rows).
 template <int NP>
@@ -1297,9 +1303,9 @@ __global__ __launch_bounds__(256) void ln_shift_row_kernel(LnShiftArgs a) {
     xp[i] = has_prev ? (xp[i] - m1) * r1 * lw[i] + lb[i] : u16_to_f(st[i], a.bf);
   }
   for (int j = 0; j < a.n_mix; ++j) {
-    uint16_t *o = a.out + ((int64_t)j * a.M + m) * C;
+    const int64_t o = ((int64_t)j * a.M + m) * C;
 #pragma unroll
-    for (int i = 0; i < NP; ++i) o[tid + 256 * i] = f_to_u16(xc[i] + mu[j][i] * (xp[i] - xc[i]), a.bf);
+    for (int i = 0; i < NP; ++i) store_mix(a, o + tid + 256 * i, xc[i] + mu[j][i] * (xp[i] - xc[i]));
   }
   if (t == 0) {
 #pragma unroll
@@ -1394,7 +1400,7 @@ __global__ __launch_bounds__(256) void ln_shift_kernel(LnShiftArgs a, int R, int
       const int c = tid + 256 * i;
 #pragma unroll
       for (int j = 0; j < 6; ++j)
-        if (j < a.n_mix) a.out[((int64_t)j * a.M + m) * C + c] = f_to_u16(xn[i] + mu[j][i] * (pv[i] - xn[i]), a.bf);
+        if (j < a.n_mix) store_mix(a, ((int64_t)j * a.M + m) * C + c, xn[i] + mu[j][i] * (pv[i] - xn[i]));
       if (t == 0) sh[c] = f_to_u16(ns[i], a.bf);
       prev[i] = xn[i];
     }
@@ -1449,7 +1455,9 @@ __global__ __launch_bounds__(256) void gn_gate_kernel(GnGateArgs a) {
   const float var = wave_sum(d * d) * (1.f / kN);
   const float yn = d * rsqrtf(var + kGnEps) * a.vec[RWKV7_V_LNX_W * C + ch] + a.vec[RWKV7_V_LNX_B * C + ch];
   const float rk = wave_sum(a.r[o] * a.kn[o] * a.vec[RWKV7_V_R_K * C + ch]);
-  a.out[o] = f_to_u16((yn + rk * a.v[o]) * a.g[o], a.bf);
+  const float out = (yn + rk * a.v[o]) * a.g[o];
+  if (a.out_f32) static_cast<float *>(a.out)[o] = out;
+  else static_cast<uint16_t *>(a.out)[o] = f_to_u16(out, a.bf);
 }
 
 int launch_gn_gate(const GnGateArgs &a, hipStream_t st) {

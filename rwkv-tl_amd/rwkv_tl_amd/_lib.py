@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the HIP library)
 
 LIB_NAME = "librwkv7_hip.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 # rwkv7_model.flags
 MODEL_MULTI_LAUNCH_DECODE = 1
@@ -40,6 +40,7 @@ SYMBOLS = (
     "rwkv7_workspace_bytes",
     "rwkv7_workspace_errors",
     "rwkv7_decode_launches",
+    "rwkv7_step_f32_activations",
     "rwkv7_decode",
     "rwkv7_decode_noalloc",
     "rwkv7_prefill",
@@ -164,6 +165,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "rwkv7_workspace_bytes": (i64, [ctypes.POINTER(Dims), i32, i32]),
         "rwkv7_workspace_errors": (ctypes.c_int, [vp, i64, ctypes.POINTER(ctypes.c_uint32), vp]),
         "rwkv7_decode_launches": (ctypes.c_int, [ctypes.POINTER(Model), i32, i32]),
+        "rwkv7_step_f32_activations": (ctypes.c_int, [ctypes.POINTER(Model), i32, i32]),
         "rwkv7_decode": (ctypes.c_int, [ctypes.POINTER(Model), ctypes.POINTER(StateDesc), vp, vp, vp, i64, vp]),
         "rwkv7_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(Model), ctypes.POINTER(StateDesc), vp, vp, vp]),
         "rwkv7_prefill": (ctypes.c_int, [ctypes.POINTER(Model), ctypes.POINTER(StateDesc), vp, i32, vp, i64, vp]),

@@ -37,7 +37,9 @@ from . import _lib
 
 N = 64
 
-GEMM_EPI = {"f32": 0, "f16": 1, "relu2": 2, "add": 3}
+GEMM_EPI = {"f32": 0, "f16": 1, "relu2": 2, "add": 3, "tanh": 4, "sigmoid": 5, "relu2_f32": 6, "tanh_f32": 7,
+            "sigmoid_f32": 8}
+GEMM_BF16, GEMM_A_F32 = 1, 2  # flag bits of rwkv7_gemm_f16's format word
 
 
 def _need(cond: bool, msg: str) -> None:
@@ -331,24 +333,31 @@ def gemv_any4(x: Tensor, codes: Tensor, lut: Tensor) -> Tensor:
 
 
 def gemm(A: Tensor, W: Tensor, epi: str = "f32", out: Tensor | None = None) -> Tensor:
-    """``epi(A W^T)`` for A [M, K], W [N, K], both f16 or both bf16; ``epi`` in
-    f32/f16/relu2/add ("f16" and relu2 store the operands' 16-bit dtype).
+    """``epi(A W^T)`` for A [M, K], W [N, K] f16 or bf16; A of W's dtype, or
+    float32 (multiplied as its 16-bit part plus the 16-bit remainder: two MFMAs
+    per weight fragment, fp32-grade activations). ``epi`` in f32 / f16 / relu2
+    / add / tanh / sigmoid / relu2_f32 / tanh_f32 / sigmoid_f32 (the plain
+    names store W's 16-bit dtype, ``*_f32`` and ``f32`` float32).
 
     ``add`` accumulates into ``out`` (f32 [M, N]) and returns it.
     """
-    bf = _h16(A, W)
+    a32 = A.dtype == torch.float32
+    bf = _h16(W) if a32 else _h16(A, W)
+    _dev(A)
     _need(A.dim() == 2 and W.dim() == 2 and A.shape[1] == W.shape[1], "A [M,K] and W [N,K] must share K")
+    _need(A.is_contiguous() and W.is_contiguous(), "A and W must be contiguous")
     M, K = A.shape
     Nn = W.shape[0]
     code = GEMM_EPI[epi]
     if epi == "add":
         _need(out is not None and out.dtype == torch.float32 and out.shape == (M, Nn), "add needs f32 out [M, N]")
     else:
-        dt = torch.float32 if epi == "f32" else A.dtype
+        dt = torch.float32 if epi == "f32" or epi.endswith("_f32") else W.dtype
         out = torch.empty(M, Nn, dtype=dt, device=A.device)
     _dev(out)
     lib = _lib.load()
-    rc = lib.rwkv7_gemm_f16(A.data_ptr(), K, W.data_ptr(), K, out.data_ptr(), Nn, M, Nn, K, code, bf,
+    flags = (GEMM_BF16 if bf else 0) | (GEMM_A_F32 if a32 else 0)
+    rc = lib.rwkv7_gemm_f16(A.data_ptr(), K, W.data_ptr(), K, out.data_ptr(), Nn, M, Nn, K, code, flags,
                             _lib.stream_handle())
     _lib.check(rc, "rwkv7_gemm_f16")
     return out

@@ -180,6 +180,15 @@ class RWKV7HIP(RWKV7Model):
         """Kernel launches of one decode step with logits (1: a single persistent kernel)."""
         return int(self._lib.rwkv7_decode_launches(ctypes.byref(self.dev.desc), batch, 1))
 
+    def f32_activations(self, batch: int, seq_len: int) -> bool:
+        """Whether a step of ``batch`` x ``seq_len`` tokens keeps fp32-grade
+        activations (False only for prefills long enough to take the large-M
+        GEMM path, whose operands are rounded to 16 bits)."""
+        r = int(self._lib.rwkv7_step_f32_activations(ctypes.byref(self.dev.desc), batch, seq_len))
+        if r < 0:
+            raise ValueError(f"unsupported batch={batch} seq_len={seq_len}")
+        return r == 1
+
     def decode_into(self, tok: Tensor, S: State, logits: Tensor | None) -> None:
         """One decode step: ``tok`` int64 [B] on device, ``logits`` [B, V] of the model's dtype, or None."""
         B = S.batch_size

@@ -5,20 +5,23 @@
   state, then decode steps from the prefilled state -- the cases of the
   reference benchmark (script/benchmark_rwkv7.py:185-192), which flattens the
   batch into one sequence.
-* C3: 0.4B decode at batch 16 from zero state.
+* C3: 0.4B decode at batch 16 from zero state, 256 steps.
 
 Oracles as in test_gpu_model.py: ``ref32`` (fp32 math on the same fp16
 weights, fp16 shift state) and ``ref16`` (the reference's fp16 semantics).
 Bars, written where they are applied: logits within 1e-2 abs + 1e-3 rel
-against both oracles at every checked step; per-layer wkv state within 5e-3
-relative of ref32 after prefill and after the decode steps (the prefill and
-batched paths feed fp16 operands to the MFMA GEMMs, so the 1e-4 state bar of
-the fp32 batch-1 decode does not apply to them).
+against both oracles at every checked step; per-layer wkv state of every row
+within 1e-4 relative of ref32 after prefill and after the decode steps (the
+every one of these steps keeps fp32-grade activations, the
+batched GEMMs and the few-row kernel multiplying f32 activations as f16 parts
+plus f16 remainders).
 
-Decode steps: 64 after a batch-1 prefill (C4 as stated); 16 after a batched
-prefill and for C3, where the CPU oracle decodes row by row (~1 s per batch
-step). ref32 follows every row at every step. ref16 is compared on rows 0
-and B-1 at the first decode step: for C4 through the committed fixture
+Decode steps: 64 after every prefill (C4 as stated) and 256 for C3. ref32
+follows every row at every step through ``decode_rows`` (all rows in the same
+torch operations, pinned to the row-by-row oracle in test_oracle.py); logits
+are compared at every step of C4 and every 16th step (and the last) of C3.
+ref16 is compared on rows 0 and B-1 at the first decode step: for C4 through
+the committed fixture
 ``tests/golden/c4_ref16.safetensors`` (the oracle's fp16 path takes minutes per
 128-token prefill on a CPU without fast half precision, so
 ``tests/golden/make_c4_ref16.py`` computed those logits -- the 64 largest and
@@ -40,7 +43,7 @@ from rwkv_tl_amd.weight import RWKV7Weight
 pytestmark = [pytest.mark.gpu, pytest.mark.slow]
 
 LOGIT_ATOL, LOGIT_RTOL = 1e-2, 1e-3
-PREFILL_STATE_REL = 5e-3
+STATE_REL = 1e-4
 
 C4_CASES = [(1, 8), (1, 32), (1, 64), (1, 128), (1, 512), (8, 8), (16, 16)]
 
@@ -82,17 +85,18 @@ def m04(cuda):
     return Setup04(cuda)
 
 
-def _run_decode_steps(m, S, s32, toks, label, check16):
-    """Decode ``toks`` [steps, B] on the GPU and in ref32, checking logits
-    against ref32 at every step; ``check16(lg)`` checks the first step against
-    ref16."""
+def _run_decode_steps(m, S, s32, toks, label, check16, every=1):
+    """Decode ``toks`` [steps, B] on the GPU and in ref32 (all rows at once),
+    checking every row's logits against ref32 at every ``every``-th step and
+    the last; ``check16(lg)`` checks the first step against ref16."""
     steps, B = toks.shape
     for i in range(steps):
         lg, S = m.model.decode(toks[i].to(m.w.device), S)
-        l32, s32 = R.decode(m.ref32, toks[i], s32)
+        l32, s32 = R.decode_rows(m.ref32, toks[i], s32)
         assert lg.shape == (B, m.V)
-        for b in range(B):
-            _check_logits(lg[b], l32[b], f"{label} step {i} row {b} vs ref32")
+        if i % every == 0 or i == steps - 1:
+            for b in range(B):
+                _check_logits(lg[b], l32[b], f"{label} step {i} row {b} vs ref32")
         if i == 0:
             check16(lg)
         if i % 16 == 15:
@@ -107,7 +111,7 @@ def c4_ref16(golden_dir):
 
 @pytest.mark.parametrize("B,T", C4_CASES, ids=[f"{b}x{t}" for b, t in C4_CASES])
 def test_c4_prefill_then_decode_0p4b(m04, c4_ref16, B, T):
-    steps = 64 if B == 1 else 16
+    steps = 64
     label = f"C4 0.4b {B}x{T}"
     print(f"{label}: prefill then {steps} decode steps", flush=True)
     g = torch.Generator().manual_seed(1000 * B + T)
@@ -118,7 +122,8 @@ def test_c4_prefill_then_decode_0p4b(m04, c4_ref16, B, T):
     m04.model.prefill(prompt.to(m04.w.device), S)
     s32 = R.new_state(m04.w.L, m04.w.C, dtype=torch.float16, batch=B)
     R.prefill(m04.ref32, prompt, s32)
-    _check_state(S, s32, PREFILL_STATE_REL, f"{label} state after prefill vs ref32")
+    assert m04.model.f32_activations(B, T), "C4 prefills keep f32 activations"
+    _check_state(S, s32, STATE_REL, f"{label} state after prefill vs ref32")
     print(f"  {label}: prefill state checked against ref32", flush=True)
 
     def check16(lg):
@@ -129,11 +134,11 @@ def test_c4_prefill_then_decode_0p4b(m04, c4_ref16, B, T):
             _check_logits(lg[b].float().cpu()[idx], c4_ref16[f"{key}_val"], f"{label} step 0 row {b} vs ref16")
 
     S, s32 = _run_decode_steps(m04, S, s32, toks, label, check16)
-    _check_state(S, s32, PREFILL_STATE_REL, f"{label} state after {steps} decode steps vs ref32")
+    _check_state(S, s32, STATE_REL, f"{label} state after {steps} decode steps vs ref32")
 
 
 def test_c3_decode_batch16_0p4b(m04):
-    B, steps = 16, 16
+    B, steps = 16, 256
     label = "C3 0.4b decode B=16"
     print(f"{label}: {steps} steps from zero state", flush=True)
     g = torch.Generator().manual_seed(316)
@@ -146,5 +151,5 @@ def test_c3_decode_batch16_0p4b(m04):
             l16, _ = R.decode(m04.ref16, toks[0, b : b + 1], R.new_state(m04.w.L, m04.w.C, dtype=torch.float16))
             _check_logits(lg[b], l16, f"{label} step 0 row {b} vs ref16")
 
-    S, s32 = _run_decode_steps(m04, S, s32, toks, label, check16)
-    _check_state(S, s32, PREFILL_STATE_REL, f"{label} state after {steps} steps vs ref32")
+    S, s32 = _run_decode_steps(m04, S, s32, toks, label, check16, every=16)
+    _check_state(S, s32, STATE_REL, f"{label} state after {steps} steps vs ref32")

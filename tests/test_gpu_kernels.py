@@ -203,6 +203,54 @@ def test_gemm_matches_fp32(M, N, Kd, epi, cuda):
         torch.testing.assert_close(out, ref.half().float(), rtol=2e-3, atol=2e-3)
 
 
+@pytest.mark.parametrize(
+    "M,N,Kd",
+    [(1, 64, 256), (5, 100, 40), (16, 1024, 1024), (33, 72, 16), (128, 4096, 1024), (128, 1024, 4096),
+     (200, 1024, 4096), (7, 65536, 256), (512, 1024, 1024), (600, 300, 128), (1030, 520, 64), (2048, 1024, 256)],
+)
+@pytest.mark.parametrize("epi", ["f32", "add", "relu2_f32", "tanh_f32", "sigmoid_f32", "f16"])
+@pytest.mark.parametrize("wdt", [torch.float16, torch.bfloat16])
+def test_gemm_f32_activations_match_fp32(M, N, Kd, epi, wdt, cuda):
+    """f32 A (the model's batched and prefill GEMM operands): the kernels split
+    each activation into its 16-bit part and the 16-bit remainder and multiply
+    both by the weight fragment, so the product must equal the float64 product
+    of the f32 activations and the 16-bit weights to fp32 accuracy: within
+    tol (1 + |x|) of the pre-activation x, carried through the activation by
+    its derivative, with tol = 1e-6 sqrt(K) for half (the fp32 accumulation
+    over K: hi + lo hold 22 significant bits) and 4e-6 sqrt(K) for bfloat16
+    (16 bits). The same bar is shown to fail for A rounded to the 16-bit
+    format (an error near 2^-12 sqrt(K) |w| per output), so it sees the split."""
+    g = torch.Generator().manual_seed(M * 11 + N + Kd)
+    A = torch.randn(M, Kd, generator=g)
+    W = (torch.randn(N, Kd, generator=g) * 0.05).to(wdt)
+    x = A.double() @ W.double().T
+    tol = (1e-6 if wdt == torch.float16 else 4e-6) * Kd**0.5
+    dx = tol * (1.0 + x.abs())  # allowed error of the pre-activation
+    if epi == "add":
+        base = torch.randn(M, N, generator=g)
+        out = K.gemm(A.to(cuda), W.to(cuda), "add", out=base.clone().to(cuda)).cpu().double() - base.double()
+        want, bar = x, dx + 1e-6 * base.double().abs()
+    elif epi == "f16":
+        # the 16-bit store rounds the product; it must be the rounding of x
+        out = K.gemm(A.to(cuda), W.to(cuda), epi).cpu().double()
+        want, bar = x.to(wdt).double(), x.abs() * (2.0**-10 if wdt == torch.float16 else 2.0**-7) + dx
+    else:
+        out = K.gemm(A.to(cuda), W.to(cuda), epi).cpu().double()
+        if epi == "relu2_f32":
+            want, bar = x.clamp_min(0) ** 2, 2.0 * x.abs() * dx + dx**2
+        elif epi == "tanh_f32":
+            want, bar = torch.tanh(x), dx
+        elif epi == "sigmoid_f32":
+            want, bar = torch.sigmoid(x), dx
+        else:
+            want, bar = x, dx
+    d = (out - want).abs()
+    assert bool((d <= bar).all()), f"{int((d > bar).sum())} off, max |d| {float(d.max()):.3e}"
+    if epi == "f32" and M * N * Kd >= 1 << 20:
+        rounded = A.to(wdt).double() @ W.double().T
+        assert bool(((rounded - x).abs() > dx).any()), "the bar does not see 16-bit activations"
+
+
 @pytest.mark.slow
 def test_gemm_large_m_beyond_2gib_of_a(cuda):
     """The large-M GEMM reads its operands through 32-bit buffer offsets, so an

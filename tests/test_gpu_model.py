@@ -135,7 +135,7 @@ def test_prefill_then_decode_matches_oracle(shape, T, cuda):
     l16, s16 = R.forward(st.ref16, toks, s16)
     _check_logits(lg, l32, f"{shape} T={T} vs ref32")
     _check_logits(lg, l16, f"{shape} T={T} vs ref16")
-    _check_state(S, s32, 5e-3, f"{shape} T={T} state vs ref32")
+    _check_state(S, s32, STATE_REL, f"{shape} T={T} state vs ref32")
 
 
 def test_prefill_rejects_empty_and_bad_shapes(cuda):
@@ -155,7 +155,8 @@ def test_prefill_rejects_empty_and_bad_shapes(cuda):
 def test_batched_segmented_prefill_matches_oracle(T, cuda):
     """B=3 sequences prefilled in one call -- 80 tokens (the segmented serial
     scan, three segments each) or 130 (the chunked scan, a partial last
-    chunk): every row's state and next logits match the oracle's."""
+    chunk): every row's state (1e-4: the batched GEMMs
+    take f32 activations) and next logits match the oracle's."""
     print(f"batched prefill B=3 T={T}", flush=True)
     st = setup_for("tiny", cuda)
     V, B = st.w.head.shape[0], 3
@@ -173,7 +174,7 @@ def test_batched_segmented_prefill_matches_oracle(T, cuda):
     for i in range(st.w.L):
         for b in range(B):
             r = _rel(S.tmix[i]["rnn"][b].cpu(), ref[0][i]["rnn"][b])
-            assert r < 5e-3, f"layer {i} row {b}: {r:.2e}"
+            assert r < STATE_REL, f"layer {i} row {b}: {r:.2e}"
 
 
 @pytest.mark.parametrize("B", [343, 2731])
@@ -183,7 +184,9 @@ def test_many_row_prefill_with_sequence_boundaries_inside_workgroups(B, cuda):
     workgroups straddle a sequence boundary (one row's predecessor is the
     previous sequence's shift state) and the last one has a single row.
     Logits of the next token and the states of a spread of rows match the
-    oracle."""
+    oracle: 1e-4 where the step keeps f32 activations (1029 rows), 5e-3 for
+    8193 rows, past the large-M GEMM threshold whose operands are rounded to
+    16 bits."""
     print(f"tiny prefill B={B} T=3", flush=True)
     st = setup_for("tiny", cuda)
     V, T = st.w.head.shape[0], 3
@@ -198,10 +201,12 @@ def test_many_row_prefill_with_sequence_boundaries_inside_workgroups(B, cuda):
     l32, ref = R.decode(st.ref32, nxt, ref)
     for b in range(B):
         _check_logits(lg[b], l32[b], f"B={B} T=3 row {b}")
+    bar = STATE_REL if st.model.f32_activations(B, T) else 5e-3
+    assert (bar == STATE_REL) == (B * T < 8065), "the tiny model's large-M threshold is 8065 rows"
     for i in range(st.w.L):
         for b in (0, 1, B // 2, B - 2, B - 1):
             r = _rel(S.tmix[i]["rnn"][b].cpu(), ref[0][i]["rnn"][b])
-            assert r < 5e-3, f"layer {i} row {b}: {r:.2e}"
+            assert r < bar, f"layer {i} row {b}: {r:.2e}"
 
 
 @pytest.mark.parametrize("B", [2, 5])
@@ -225,7 +230,7 @@ def test_batched_decode_rows_match_single_sequences(B, cuda):
     for i in range(st.w.L):
         for b in range(B):
             r = _rel(S.tmix[i]["rnn"][b].cpu(), ref[0][i]["rnn"][b])
-            assert r < 5e-3, f"layer {i} row {b}: {r:.2e}"
+            assert r < STATE_REL, f"layer {i} row {b}: {r:.2e}"
 
 
 @pytest.mark.slow
@@ -256,7 +261,7 @@ def test_1p5b_shape_batched_prefill_and_decode_match_oracle(cuda):
     for i in range(w.L):
         for b in range(B):
             r = _rel(S.tmix[i]["rnn"][b].cpu(), ref[0][i]["rnn"][b])
-            assert r < 5e-3, f"1.5b layer {i} row {b}: {r:.2e}"
+            assert r < STATE_REL, f"1.5b layer {i} row {b}: {r:.2e}"
     S1 = State(w.L, w.C, 64, device=cuda)
     lg1, S1 = model.decode(nxt[0, :1].to(cuda), S1)
     l1, _ = R.decode(ref32, nxt[0, :1], R.new_state(w.L, w.C, dtype=torch.float16))
@@ -265,42 +270,64 @@ def test_1p5b_shape_batched_prefill_and_decode_match_oracle(cuda):
 
 @pytest.mark.slow
 def test_1p5b_shape_long_prefill_and_batch64_properties(cuda):
-    """Config C5's sizes on the 1.5B shape, where the CPU oracle is too slow:
-    prefill of 4 x 1024 tokens in one call equals two calls of 512 (fp32
-    state within 5e-3, the prefill bar), and rows of a batch-64 decode equal
-    the same sequences decoded one at a time (logits within 1e-2 / 1e-3)."""
+    """Config C5's sizes on the 1.5B shape:
+    * prefill of 4 x 1024 tokens in one call: row 1's state against the fp32
+      oracle's prefill of that sequence, and all rows against two calls of 512
+      (fp32 state within 5e-3: these prefills take the large-M GEMM path,
+      whose operands are rounded to 16 bits);
+    * decode at batch 64 from a zero state for 16 steps: every
+      row's logits at every step and every row's state of every layer at the
+      end equal the same sequence decoded alone (batch-1 path: fp32
+      activations) -- logits within 1e-2 / 1e-3, state within 1e-4 (the
+      batch-64 step keeps f32 activations)."""
     print("1.5b 4x1024 prefill and B=64 decode properties", flush=True)
     _CACHE.clear()
     sd = make_random_state_dict("1.5b", seed=0, dtype=torch.float16)
     w = RWKV7Weight.from_state_dict(sd, device=cuda, dtype=torch.float16)
-    del sd
     model = RWKV7HIP(w, is_torch_compile=False)
     V = w.head.shape[0]
     g = torch.Generator().manual_seed(21)
-    toks = torch.randint(0, V, (4, 1024), generator=g).to(cuda)
+    toks = torch.randint(0, V, (4, 1024), generator=g)
     S1 = State(w.L, w.C, 64, device=cuda, batch=4)
-    model.prefill(toks, S1)
+    assert not model.f32_activations(4, 1024) and not model.f32_activations(4, 512)
+    model.prefill(toks.to(cuda), S1)
     S2 = State(w.L, w.C, 64, device=cuda, batch=4)
-    model.prefill(toks[:, :512].contiguous(), S2)
-    model.prefill(toks[:, 512:].contiguous(), S2)
+    model.prefill(toks[:, :512].contiguous().to(cuda), S2)
+    model.prefill(toks[:, 512:].contiguous().to(cuda), S2)
     for i in range(w.L):
         r = _rel(S1.tmix[i]["rnn"].cpu(), S2.tmix[i]["rnn"].cpu())
         assert r < 5e-3, f"layer {i}: one 1024-token prefill vs two of 512: {r:.2e}"
-    B = 64
-    nxt = torch.randint(0, V, (B,), generator=g).to(cuda)
+    print("  1.5b: 4x1024 vs 2 x 4x512 checked; oracle prefill of row 1 (1024 tokens)", flush=True)
+    ref32 = R.Weights.from_emb(sd, w.emb.cpu(), torch.float32)
+    del sd
+    s32 = R.new_state(w.L, w.C, dtype=torch.float16)
+    R.prefill(ref32, toks[1], s32)
+    for i in range(w.L):
+        r = _rel(S1.tmix[i]["rnn"][1].cpu(), s32[0][i]["rnn"])
+        assert r < 5e-3, f"layer {i}: 4x1024 prefill row 1 vs ref32: {r:.2e}"
+    del ref32, s32
+    B, steps = 64, 16
+    assert model.f32_activations(B, 1)
+    nxt = torch.randint(0, V, (steps, B), generator=g).to(cuda)
     SB = State(w.L, w.C, 64, device=cuda, batch=B)
-    lgB, SB = model.decode(nxt, SB)
-    for b in (0, 17, 63):
-        Sb = State(w.L, w.C, 64, device=cuda)
-        lgb, Sb = model.decode(nxt[b : b + 1], Sb)
-        _check_logits(lgB[b], lgb, f"1.5b B=64 row {b} vs B=1")
+    singles = [State(w.L, w.C, 64, device=cuda) for _ in range(B)]
+    for step in range(steps):
+        lgB, SB = model.decode(nxt[step], SB)
+        for b in range(B):
+            lgb, singles[b] = model.decode(nxt[step, b : b + 1], singles[b])
+            _check_logits(lgB[b], lgb, f"1.5b B=64 step {step} row {b} vs B=1")
+    print(f"  1.5b: B=64 decode, {steps} steps checked against batch-1 decodes", flush=True)
+    for b in range(B):
+        for i in range(w.L):
+            r = _rel(SB.tmix[i]["rnn"][b].cpu(), singles[b].tmix[i]["rnn"].cpu())
+            assert r < STATE_REL, f"1.5b B=64 row {b} layer {i} state vs B=1: {r:.2e}"
 
 
 def test_0p4b_prefill_1024_rows_matches_split_calls(cuda):
     """A 2 x 512 prefill (1024 rows: the LayerNorm + shift kernel takes two
     rows per workgroup) equals two calls of 2 x 256 (512 rows: one row per
-    workgroup): fp32 state within 5e-3, the shift states and the next
-    decode's logits within the logit tolerance."""
+    workgroup): fp32 state within 1e-4 (both keep f32 activations), the
+    shift states and the next decode's logits within the logit tolerance."""
     print("0.4b 2x512 prefill vs 2 x (2x256)", flush=True)
     _CACHE.clear()
     sd = make_random_state_dict("0.4b", seed=0, dtype=torch.float16)
@@ -312,13 +339,14 @@ def test_0p4b_prefill_1024_rows_matches_split_calls(cuda):
     toks = torch.randint(0, V, (2, 512), generator=g).to(cuda)
     nxt = torch.randint(0, V, (2,), generator=g).to(cuda)
     S1 = State(w.L, w.C, 64, device=cuda, batch=2)
+    assert model.f32_activations(2, 512) and model.f32_activations(2, 256)
     model.prefill(toks, S1)
     S2 = State(w.L, w.C, 64, device=cuda, batch=2)
     model.prefill(toks[:, :256].contiguous(), S2)
     model.prefill(toks[:, 256:].contiguous(), S2)
     for i in range(w.L):
         r = _rel(S1.tmix[i]["rnn"].cpu(), S2.tmix[i]["rnn"].cpu())
-        assert r < 5e-3, f"layer {i}: one 2x512 prefill vs two of 2x256: {r:.2e}"
+        assert r < STATE_REL, f"layer {i}: one 2x512 prefill vs two of 2x256: {r:.2e}"
         for key, a, b in (("tmix x", S1.tmix[i]["x"], S2.tmix[i]["x"]), ("cmix x", S1.cmix[i]["x"], S2.cmix[i]["x"])):
             torch.testing.assert_close(a.float().cpu(), b.float().cpu(), rtol=1e-2, atol=1e-2, msg=f"layer {i} {key}")
     lg1, _ = model.decode(nxt, S1)
@@ -332,7 +360,8 @@ def test_0p4b_large_batch_decode_rows_match_single_sequences(B, cuda):
     """Batched one-token steps past the few-row kernel's 16 rows (the
     multi-launch path with the fused per-head core): two steps; rows 0, a
     middle one and the last equal the same sequences decoded one at a time by
-    the batch-1 kernel (logits within 1e-2 / 1e-3, fp32 state within 5e-3)."""
+    the batch-1 kernel (logits within 1e-2 / 1e-3, fp32 state of every layer
+    within 1e-4)."""
     print(f"0.4b B={B} decode rows vs B=1", flush=True)
     _CACHE.clear()
     sd = make_random_state_dict("0.4b", seed=0, dtype=torch.float16)
@@ -350,8 +379,9 @@ def test_0p4b_large_batch_decode_rows_match_single_sequences(B, cuda):
         for step in range(2):
             lgb, Sb = model.decode(nxt[step, b : b + 1], Sb)
         _check_logits(lgB[b], lgb, f"0.4b B={B} row {b} vs B=1")
-        r = _rel(SB.tmix[5]["rnn"][b].cpu(), Sb.tmix[5]["rnn"].cpu())  # batch 1: [H, N, N]
-        assert r < 5e-3, f"B={B} row {b} layer 5 state: {r:.2e}"
+        for i in range(w.L):
+            r = _rel(SB.tmix[i]["rnn"][b].cpu(), Sb.tmix[i]["rnn"].cpu())  # batch 1: [H, N, N]
+            assert r < STATE_REL, f"B={B} row {b} layer {i} state: {r:.2e}"
 
 
 @pytest.fixture

@@ -3,11 +3,11 @@ rows, ``rows_mk.hip``) against the CPU oracle and against the multi-launch
 path on the same inputs.
 
 Bars are those of the batched multi-launch path (``test_gpu_model.py``): the
-matrix stages round their activation operands to fp16 (MFMA inputs), so
+matrix stages multiply f32 activations as f16 parts plus f16 remainders, so
 logits are held to 1e-2 abs + 1e-3 rel of the fp32-math oracle and the fp32
-wkv state to 5e-3 relative per layer and row; the fp16 token-shift states to
-2e-2 abs. The two HIP paths round at the same points but sum in different
-orders, so they agree with each other to the same bars.
+wkv state to 1e-4 relative per layer and row; the fp16
+token-shift states to 2e-2 abs. The two HIP paths sum in different orders,
+so they agree with each other to the same bars.
 """
 
 from __future__ import annotations
@@ -23,7 +23,7 @@ from rwkv_tl_amd.weight import RWKV7Weight
 pytestmark = pytest.mark.gpu
 
 LOGIT_ATOL, LOGIT_RTOL = 1e-2, 1e-3
-STATE_REL = 5e-3
+STATE_REL = 1e-4
 
 _CACHE: dict[str, tuple] = {}
 

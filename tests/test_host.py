@@ -61,6 +61,29 @@ def test_decode_path_decision_without_a_device(shape):
     assert lib.rwkv7_decode_launches(None, 1, 1) == -1
 
 
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the decision on a host without a GPU")
+def test_f32_activation_decision_without_a_device():
+    """Batched steps keep f32 activations (two 16-bit MFMA parts) unless some
+    GEMM of the layer would take the large-M path: with 256 CUs that needs
+    ceil(M / 128) * ceil(N / 128) >= 512 tiles, so the widest matrix (the FFN,
+    N = F) sets the threshold: M >= 1921 rows at F = 4096, M >= 897 at
+    F = 8192. Long prefills beyond it round the operands to 16 bits."""
+    lib = _lib.load()
+    f32 = lambda shape, B, T: lib.rwkv7_step_f32_activations(  # noqa: E731
+        ctypes.byref(_lib.Model(dims=_dims(shape))), B, T)
+    assert f32("0.4b", 1, 128) == 1
+    assert f32("0.4b", 16, 16) == 1
+    assert f32("0.4b", 1, 1920) == 1
+    assert f32("0.4b", 1, 1921) == 0
+    assert f32("0.4b", 130, 1) == 1
+    assert f32("1.5b", 64, 1) == 1
+    assert f32("1.5b", 2, 448) == 1
+    assert f32("1.5b", 1, 897) == 0
+    assert f32("1.5b", 4, 1024) == 0
+    assert f32("0.4b", 0, 1) == -1
+    assert lib.rwkv7_step_f32_activations(None, 1, 1) == -1
+
+
 @pytest.mark.parametrize("shape", ["tiny", "0.1b", "0.4b", "1.5b"])
 def test_layer_layout(shape):
     d = _dims(shape)

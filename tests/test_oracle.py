@@ -378,3 +378,32 @@ def test_c4_ref16_fixture_matches_oracle(golden_dir):
     idx = fx["1x8_row0_idx"]
     assert torch.equal(lg.float()[idx], fx["1x8_row0_val"])
     assert set(torch.topk(lg.float(), 64).indices.tolist()) == set(idx[:64].tolist())
+
+
+@pytest.mark.parametrize("shape", ["tiny", "0.1b"])
+def test_decode_rows_matches_row_by_row_decode(shape):
+    """``decode_rows`` (all rows of a batched state in the same torch ops, the
+    fast checker of the batched GPU tests) equals ``decode`` (each row as its
+    own single-sequence state, golden-pinned) on fp32 weights: logits and wkv
+    states to fp32 rounding over 6 steps of 5 rows from a non-zero state, the
+    f16 shift states to one half-precision step."""
+    from rwkv_tl_amd.checkpoint import make_random_state_dict
+
+    sd = make_random_state_dict(shape, seed=0, dtype=torch.float16)
+    W = R.Weights(sd, torch.float32)
+    B = 5
+    g = torch.Generator().manual_seed(8)
+    toks = torch.randint(0, W.head.shape[0], (7, B), generator=g)
+    sa = R.new_state(W.L, W.C, dtype=torch.float16, batch=B)
+    R.decode(W, toks[0], sa)  # a non-zero starting state
+    sb = ([{k: v.clone() for k, v in d.items()} for d in sa[0]], [{k: v.clone() for k, v in d.items()} for d in sa[1]])
+    for i in range(1, 7):
+        la, sa = R.decode(W, toks[i], sa)
+        lb, sb = R.decode_rows(W, toks[i], sb)
+        torch.testing.assert_close(lb, la, rtol=1e-5, atol=1e-5)
+    for i in range(W.L):
+        for b in range(B):
+            x, y = sb[0][i]["rnn"][b].double(), sa[0][i]["rnn"][b].double()
+            assert float((x - y).norm() / y.norm()) < 1e-5, f"layer {i} row {b}"
+        for part in (0, 1):
+            torch.testing.assert_close(sb[part][i]["x"].float(), sa[part][i]["x"].float(), rtol=0, atol=2e-3)
