@@ -549,7 +549,7 @@ RWKV7_DEV void gemm_big_tile(const BigGroup &g) {
   const int nst = K / kBigBK;
   // DMA of stage st (clamped: past the last stage the last one is reloaded into
   // a buffer nobody reads again, which keeps the vmcnt bookkeeping uniform)
-  auto issue = [&](int st, int buf) {
+  auto issue = [&](int st, int buf) __attribute__((always_inline)) {
     const unsigned s2 = (unsigned)(st < nst ? st : nst - 1) * stage_b;
 #pragma unroll
     for (int u = 0; u < PERS; ++u)
@@ -563,7 +563,7 @@ RWKV7_DEV void gemm_big_tile(const BigGroup &g) {
 #pragma unroll
     for (int q = 0; q < WN; ++q) acc[i][q] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  auto step = [&](int st, int buf) {
+  auto step = [&](int st, int buf) __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(kWaitImm);  // this wave's DMAs of stage st have landed
     // everyone's have, and every read of buffer (st - 1) % NB is complete (the
     // lgkmcnt wait); the memory clobber keeps the compiler from moving LDS
@@ -593,17 +593,43 @@ RWKV7_DEV void gemm_big_tile(const BigGroup &g) {
   // drain the clamped DMAs before the workgroup's LDS can be reused
   __builtin_amdgcn_s_waitcnt(0x0F70);
 
+  // Epilogue: the activation applied in registers under one uniform branch,
+  // then stores. Every accumulator index is a compile-time constant: a
+  // per-element switch made the unrolled loop too large to unroll, and the
+  // dynamic indexing that remained put the whole accumulator array in
+  // scratch memory, written back on every iteration of the stage loop.
+  const int epi = P.epi;
+  auto map = [&](auto fn) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int q = 0; q < WN; ++q)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][q][r] = fn(acc[i][q][r]);
+  };
+  if (epi == GEPI_RELUSQ || epi == GEPI_RELUSQ_F32) map([](float v) { v = fmaxf(v, 0.f); return v * v; });
+  else if (epi == GEPI_TANH_F16 || epi == GEPI_TANH_F32) map([](float v) { return tanhf(v); });
+  else if (epi == GEPI_SIGM_F16 || epi == GEPI_SIGM_F32) map([](float v) { return sigmoidf_(v); });
+  const bool add = epi == GEPI_ADD_F32;
+  const bool f32 = add || epi == GEPI_F32 || epi == GEPI_RELUSQ_F32 || epi == GEPI_TANH_F32 || epi == GEPI_SIGM_F32;
+  float *yf = static_cast<float *>(P.Y);
+  uint16_t *yh = static_cast<uint16_t *>(P.Y);
   // lane holds rows 4 (lane >> 4) + {0..3} of column lane & 15 of each 16x16 tile
 #pragma unroll
   for (int q = 0; q < WN; ++q) {
     const int col = n0 + 16 * (wn * WN + q) + (lane & 15);
-    if (col >= N) continue;
 #pragma unroll
     for (int i = 0; i < WM; ++i) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = m0 + 16 * (wm * WM + i) + 4 * (lane >> 4) + r;
-        if (row < M) store_epi(P, row, col, acc[i][q][r]);
+        if (row < M && col < N) {
+          const int64_t o = (int64_t)row * P.ldy + col;
+          const float v = acc[i][q][r];
+          if (add) yf[o] += v;
+          else if (f32) yf[o] = v;
+          else yh[o] = P.bf ? f2b(v) : f2h(v);
+        }
       }
     }
   }
@@ -920,7 +946,15 @@ static int launch_skinny(const GemmProb *probs, int nprob, int M, hipStream_t st
 // cover the GPU and W, re-read per row tile, comes from L2), 64 beyond
 // (measured at M = 512 to 4096: 128-row tiles leave too few workgroups per CU
 // to hide the chunk loads; 32-row tiles re-read W too often).
-static int bm_for(int M) { return M <= 256 ? 32 : 64; }
+//
+// f32 A (a32) up to kA32Bm16MaxM rows: 16-row tiles, so a workgroup's f32 A
+// chunk takes the bytes (and registers) a 32-row 16-bit chunk takes and the
+// prefetch-all kernel can hold 8 chunks without extra K splits.
+constexpr int kA32Bm16MaxM = 256;
+static int bm_for(int M, bool a32 = false) {
+  if (a32 && M <= kA32Bm16MaxM) return 16;
+  return M <= 256 ? 32 : 64;
+}
 
 // Splits of a tiled problem: K is split (power of two, each split keeping at
 // least two 128-wide chunks) until the group has a workgroup per CU and no
@@ -931,7 +965,7 @@ static int bm_for(int M) { return M <= 256 ? 32 : 64; }
 // chunks, the most whose f32 A pieces and W fragments the prefetch-all kernel
 // keeps in registers at once.
 static void plan_splits(const GemmProb *probs, int nprob, int M, int cus, bool can_split, int *S, int *kslice) {
-  const int BM = bm_for(M);
+  const int BM = bm_for(M, probs[0].a32 != 0);
   const int m_tiles = (M + BM - 1) / BM;
   int tiles = 0;
   for (int i = 0; i < nprob; ++i) tiles += m_tiles * ((probs[i].N + kBN - 1) / kBN);
@@ -968,7 +1002,7 @@ int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, f
   const int cus = mk_cus();
   if (cus <= 0) return RWKV7_ELAUNCH;
   GemmGroup g;
-  const int BM = bm_for(M);
+  const int BM = bm_for(M, probs[0].a32 != 0);
   g.M = M;
   g.m_tiles = (M + BM - 1) / BM;
   g.nprob = nprob;
@@ -1042,14 +1076,17 @@ int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, f
   int ncmax = 1;
   for (int i = 0; i < nprob; ++i) ncmax = max(ncmax, ks[i] / kKC);
   const int nc = ncmax == 1 ? 1 : ncmax == 2 ? 2 : ncmax <= 4 ? 4 : ncmax <= 8 ? 8 : 0;
-  if (BM == 32 && nc > 0 && !(a32 && nc > 4)) {
-#define RWKV7_PF(NC)                                                                     \
-  if (bf) {                                                                              \
-    if (a32) gemm_pf_kernel<32, NC < 4 ? NC : 4, true, true><<<wgs, 256, 0, st>>>(g);   \
-    else gemm_pf_kernel<32, NC, true, false><<<wgs, 256, 0, st>>>(g);                    \
-  } else {                                                                               \
-    if (a32) gemm_pf_kernel<32, NC < 4 ? NC : 4, false, true><<<wgs, 256, 0, st>>>(g);  \
-    else gemm_pf_kernel<32, NC, false, false><<<wgs, 256, 0, st>>>(g);                   \
+  if ((BM == 32 || BM == 16) && nc > 0 && !(a32 && BM == 32 && nc > 4)) {
+#define RWKV7_PF(NC)                                                                          \
+  if (BM == 16) {                                                                             \
+    if (bf) gemm_pf_kernel<16, NC, true, true><<<wgs, 256, 0, st>>>(g);                       \
+    else gemm_pf_kernel<16, NC, false, true><<<wgs, 256, 0, st>>>(g);                         \
+  } else if (bf) {                                                                            \
+    if (a32) gemm_pf_kernel<32, NC < 4 ? NC : 4, true, true><<<wgs, 256, 0, st>>>(g);        \
+    else gemm_pf_kernel<32, NC, true, false><<<wgs, 256, 0, st>>>(g);                         \
+  } else {                                                                                    \
+    if (a32) gemm_pf_kernel<32, NC < 4 ? NC : 4, false, true><<<wgs, 256, 0, st>>>(g);       \
+    else gemm_pf_kernel<32, NC, false, false><<<wgs, 256, 0, st>>>(g);                        \
   }
     switch (nc) {
       case 1: RWKV7_PF(1) break;
@@ -1061,7 +1098,13 @@ int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, f
     RWKV7_CHECK_LAUNCH();
     return RWKV7_OK;
   }
-  // the row tiles bm_for picks: 32 or 64 rows
+  // the row tiles bm_for picks: 16 (f32 A only), 32 or 64 rows
+  if (BM == 16) {
+    if (bf) gemm_kernel<16, true, true><<<wgs, 256, 0, st>>>(g);
+    else gemm_kernel<16, false, true><<<wgs, 256, 0, st>>>(g);
+    RWKV7_CHECK_LAUNCH();
+    return RWKV7_OK;
+  }
   const int variant = (BM == 32 ? 0 : 4) | (bf ? 2 : 0) | (a32 ? 1 : 0);
   switch (variant) {
     case 0: gemm_kernel<32, false, false><<<wgs, 256, 0, st>>>(g); break;
