@@ -202,8 +202,12 @@ RWKV7_DEV WStrip w_strip(const GemmProb &P, int n0, int wv, int lane) {
 
 // Split-K hand-off (when S > 1) and epilogue of a workgroup's tile: lane holds
 // rows 4 (lane >> 4) + {0..3} of column (lane & 15) of each 16-row block.
+// With use_yres (add epilogue only) yres holds the Y values of those
+// elements, loaded before the products, so the epilogue stores without a read
+// round trip.
 template <int MB>
-RWKV7_DEV void tile_store(const GemmGroup &g, const TileUnit &w, floatx4 (&acc)[MB], int *s_last) {
+RWKV7_DEV void tile_store_y(const GemmGroup &g, const TileUnit &w, floatx4 (&acc)[MB], int *s_last, bool use_yres,
+                            const float (&yres)[MB][4]) {
   const GemmProb &P = g.p[w.pi];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int col = w.n0 + wv * 16 + (lane & 15);
@@ -217,9 +221,31 @@ RWKV7_DEV void tile_store(const GemmGroup &g, const TileUnit &w, floatx4 (&acc)[
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = w.m0 + mb * 16 + (lane >> 4) * 4 + r;
-      if (row < g.M) store_epi(P, row, col, acc[mb][r]);
+      if (row >= g.M) continue;
+      if (use_yres) reinterpret_cast<float *>(P.Y)[(int64_t)row * P.ldy + col] = yres[mb][r] + acc[mb][r];
+      else store_epi(P, row, col, acc[mb][r]);
     }
   }
+}
+
+template <int MB>
+RWKV7_DEV void tile_store(const GemmGroup &g, const TileUnit &w, floatx4 (&acc)[MB], int *s_last) {
+  float none[MB][4];
+  tile_store_y<MB>(g, w, acc, s_last, false, none);
+}
+
+// The Y values tile_store's add epilogue accumulates into (addresses clamped
+// into the output; rows and columns past it are never stored).
+template <int MB>
+RWKV7_DEV void load_yres(const GemmGroup &g, const TileUnit &w, float (&y)[MB][4]) {
+  const GemmProb &P = g.p[w.pi];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int col = min(w.n0 + wv * 16 + (lane & 15), P.N - 1);
+  const float *Y = reinterpret_cast<const float *>(P.Y);
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[mb][r] = Y[(int64_t)min(w.m0 + mb * 16 + (lane >> 4) * 4 + r, g.M - 1) * P.ldy + col];
 }
 
 // One 8-element A piece in registers: 16 bytes of 16-bit values, or 32 bytes of
@@ -329,6 +355,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
   load_a(0);
   load_w(0, w0);
   load_w(1, w1);
+  // the residual of an add epilogue, with the first loads
+  const bool add = P.epi == GEPI_ADD_F32;
+  float yres[MB][4];
+  if (add) load_yres<MB>(g, U, yres);
   store_a(0, 0);
   __syncthreads();
   // (scheduling barriers keep each chunk's A loads ahead of the W loads issued
@@ -352,7 +382,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmGroup g) {
     __syncthreads();
   }
 
-  tile_store<MB>(g, U, acc, &s_last);
+  tile_store_y<MB>(g, U, acc, &s_last, add, yres);
 }
 
 // Prefetch-all variant of gemm_kernel for splits of at most NC chunks (every
@@ -401,6 +431,10 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmGroup g) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) wr[c][j] = ws.load(kb32 + 4 * cc + j);
   }
+  // the residual of an add epilogue, after the weights
+  const bool add = P.epi == GEPI_ADD_F32;
+  float yres[MB][4];
+  if (add) load_yres<MB>(g, U, yres);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
@@ -436,7 +470,7 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmGroup g) {
     }
   }
 
-  tile_store<MB>(g, U, acc, &s_last);
+  tile_store_y<MB>(g, U, acc, &s_last, add, yres);
 }
 
 // ---------------------------------------------------------------------------
