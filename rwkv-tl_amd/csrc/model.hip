@@ -322,6 +322,7 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
   const int bf = (m.flags & RWKV7_MODEL_BF16) ? 1 : 0;
   const int a32 = batch_a32(d, M) ? 1 : 0;
   const int esz = a32 ? 4 : 2;  // bytes per element of the GEMM operands
+  const int cus = mk_cus() > 0 ? mk_cus() : 256;  // as launch_wkv7_prefill decides
   // every GEMM of the step runs on the model's 16-bit format, with f32 A if a32
   auto gemm = [&](GemmProb *p, int n, int rows) {
     for (int i = 0; i < n; ++i) {
@@ -448,9 +449,22 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
         {at(w.l1, rv + rw + ra), wl2 + rv + rw + ra, w.d + 3 * MC, SR, SR, C, C, rg, GEPI_F32},
     };
     for (int g = 0; g < 4; ++g) frag(g2[g], lay.f_l2[g], 0);
-    RWKV7_TRY(gemm(g2, 4, M));
     PrefillScanArgs sc = {rnn, w.rkv, w.d, vec, w.vfirst, w.y, w.kv, w.kv + MC, B, T, H, C, M, l == 0,
                           w.U, w.Send, w.Pend, w.rec};
+    if (prefill_chunked(T, B, H, cus) && lora2_fits(rv, rw, ra, rg)) {
+      // the chunked scan's prep kernel forms the LoRA second steps itself
+      sc.l1 = w.l1;
+      sc.w2 = wl2;
+      sc.dg = w.d + 3 * MC;
+      sc.rv = rv;
+      sc.rw = rw;
+      sc.ra = ra;
+      sc.rg = rg;
+      sc.l1_f32 = a32;
+      sc.bf = bf;
+    } else {
+      RWKV7_TRY(gemm(g2, 4, M));
+    }
     RWKV7_TRY(launch_wkv7_prefill(sc, st));
     GnGateArgs gn = {w.y, w.rkv, w.kv, w.kv + MC, w.d + 3 * MC, vec, w.yg, C, M};
     gn.bf = bf;

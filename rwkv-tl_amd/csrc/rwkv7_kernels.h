@@ -108,6 +108,16 @@ struct PrefillScanArgs {
   // chunk records of the chunked scan (wkv7_chunk_rec_bytes), read when
   // prefill_chunked(T, B, H, cus)
   float *rec;
+  // LoRA second steps inside the chunked scan (when l1 is set; d is then
+  // not read): l1 [M, rv+rw+ra+rg] the LoRA first steps after their
+  // activations (f32 if l1_f32, else 16-bit), w2 [C, rv+rw+ra+rg] their
+  // second matrices (16-bit; bfloat16 if bf). The chunk prep kernel forms the
+  // v, w, a steps of its chunk and head on MFMA and writes the g step to dg
+  // [M, C] for the GroupNorm + gate stage.
+  const void *l1 = nullptr;
+  const uint16_t *w2 = nullptr;
+  float *dg = nullptr;
+  int rv = 0, rw = 0, ra = 0, rg = 0, l1_f32 = 0, bf = 0;
 };
 int prefill_segments(int T, int B, int H, int cus, int *seg_len);
 int launch_wkv7_prefill(const PrefillScanArgs &p, hipStream_t st);
@@ -122,6 +132,9 @@ int launch_wkv7_prefill(const PrefillScanArgs &p, hipStream_t st);
 // 1 x 64 slower).
 constexpr int kChunkMinT = 128;
 bool prefill_chunked(int T, int B, int H, int cus);
+// the chunked scan's prep kernel can form the LoRA second steps of these
+// ranks itself (PrefillScanArgs::l1)
+bool lora2_fits(int rv, int rw, int ra, int rg);
 int64_t wkv7_chunk_rec_bytes(int B, int T, int H);
 template <typename TI, typename TW, typename TY>
 int launch_wkv7_chunked(const ScanArgs<TI, TW, TY> &p, float *rec, hipStream_t st);

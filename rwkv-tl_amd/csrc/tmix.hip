@@ -8,6 +8,8 @@
 //   y_i   = sum_j S'_ij r_j
 // Rows are independent given the step's (w, a, b, k, r), so a head's rows can
 // be spread over lanes and workgroups freely; every reduction is along j.
+#include <type_traits>
+
 #include "rwkv7_kernels.h"
 
 namespace rwkv7 {
@@ -207,6 +209,10 @@ struct GateStager {
   bool stager;
   float4 v0v, w0v, a0v, kkv, kav;
   float4 g_r, g_k, g_v, g_dv, g_dw, g_da, g_vf;
+  // when set: the chunk's LoRA second steps v, w, a in LDS ([3][16][lds_ld],
+  // token-major, the head's 64 channels), formed by the caller before commit
+  const float *lds_d = nullptr;
+  int lds_ld = 0;
 
   RWKV7_DEV GateStager(const PrefillScanArgs &p_, int h, int quarter_, int64_t base_, int t1_)
       : p(p_), base(base_), t1(t1_), quarter(quarter_) {
@@ -231,13 +237,21 @@ struct GateStager {
     g_r = ld4_as_f(p.rkv + o);
     g_k = ld4_as_f(p.rkv + MC + o);
     g_v = ld4_as_f(p.rkv + 2 * MC + o);
-    g_dv = ld4_as_f(p.d + o);
-    g_dw = ld4_as_f(p.d + MC + o);
-    g_da = ld4_as_f(p.d + 2 * MC + o);
+    if (!lds_d) {
+      g_dv = ld4_as_f(p.d + o);
+      g_dw = ld4_as_f(p.d + MC + o);
+      g_da = ld4_as_f(p.d + 2 * MC + o);
+    }
     g_vf = p.layer0 ? g_v : ld4_as_f(p.vfirst + o);
   }
   RWKV7_DEV void commit(int c0, StageBuf<CH> &dst) {
     const int tt = c0 + st_tok;
+    if (lds_d) {
+      const int r = st_tok < CH ? st_tok : CH - 1;
+      g_dv = *reinterpret_cast<const float4 *>(lds_d + r * lds_ld + 4 * q);
+      g_dw = *reinterpret_cast<const float4 *>(lds_d + (CH + r) * lds_ld + 4 * q);
+      g_da = *reinterpret_cast<const float4 *>(lds_d + (2 * CH + r) * lds_ld + 4 * q);
+    }
     const float k4[4] = {g_k.x, g_k.y, g_k.z, g_k.w};
     const float vr[4] = {g_v.x, g_v.y, g_v.z, g_v.w}, dv[4] = {g_dv.x, g_dv.y, g_dv.z, g_dv.w};
     const float dw[4] = {g_dw.x, g_dw.y, g_dw.z, g_dw.w}, da[4] = {g_da.x, g_da.y, g_da.z, g_da.w};
@@ -780,6 +794,97 @@ int64_t wkv7_chunk_rec_bytes(int B, int T, int H) {
 // and B[l / 16][l % 16] and holds D[4 (l / 16) + r][l % 16], r = 0..3.
 RWKV7_DEV floatx4 mfma4(float a, float b, floatx4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
 
+// The LoRA second steps of one chunk and head (PrefillScanArgs::l1), for
+// ranks up to kL2Steps 32-wide k-steps each (v, w, a, g: 32, 64, 64, 128 --
+// the 0.1B / 0.4B sizes; lora2_fits). Wave w owns the head's channels
+// 16 w .. 16 w + 15 and multiplies the chunk's 16 rows of the four LoRA first
+// steps by their second matrices on 16x16x32 MFMA -- the products and
+// summation order of the GEMM group it replaces (f32 first steps as 16-bit
+// hi + lo parts, lanes past a rank multiplying zeros). Every operand load is
+// issued before the products (lora2_load, then the stager's own loads), so
+// the step costs one memory round trip. v, w, a go to LDS ([3][16][64],
+// token-major) for the gate stager; g goes to dg for the GroupNorm + gate
+// stage.
+constexpr int kL2Steps[4] = {1, 2, 2, 4};
+constexpr int kL2Total = 9;
+bool lora2_fits(int rv, int rw, int ra, int rg) {
+  return rv <= 32 * kL2Steps[0] && rw <= 32 * kL2Steps[1] && ra <= 32 * kL2Steps[2] && rg <= 32 * kL2Steps[3];
+}
+template <bool F32>
+struct Lora2Regs {
+  uint4 w[kL2Total];
+  uint4 a[kL2Total][F32 ? 2 : 1];
+};
+template <bool F32>
+RWKV7_DEV Lora2Regs<F32> lora2_load(const PrefillScanArgs &p, int h, int bi, int T, int t0, int t1) {
+  Lora2Regs<F32> g;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int SR = p.rv + p.rw + p.ra + p.rg;
+  const int64_t arow = (int64_t)bi * T + min(t0 + (lane & 15), t1 - 1);  // A row: a token (clamped)
+  const uint16_t *wrow = p.w2 + (int64_t)(h * kN + 16 * wv + (lane & 15)) * SR;  // B row: a channel
+  const int rk[4] = {p.rv, p.rw, p.ra, p.rg};
+  int off = 0, st = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int s = 0; s < kL2Steps[j]; ++s, ++st) {
+      const int k = 32 * s + 8 * (lane >> 4);
+      const int kc = off + min(k, rk[j] - 8);  // in range; lanes past the rank are zeroed at use
+      g.w[st] = *reinterpret_cast<const uint4 *>(wrow + kc);
+      if constexpr (F32) {
+        const uint4 *a = reinterpret_cast<const uint4 *>(static_cast<const float *>(p.l1) + arow * SR + kc);
+        g.a[st][0] = a[0];
+        g.a[st][1] = a[1];
+      } else {
+        g.a[st][0] = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p.l1) + arow * SR + kc);
+      }
+    }
+    off += rk[j];
+  }
+  return g;
+}
+template <bool BF, bool F32>
+RWKV7_DEV void lora2_compute(const PrefillScanArgs &p, const Lora2Regs<F32> &g, int h, int bi, int T, int t0, int t1,
+                             float *s_d) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, ch = 16 * wv + (lane & 15);
+  const int rk[4] = {p.rv, p.rw, p.ra, p.rg};
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+  floatx4 acc[4];
+  int st = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < kL2Steps[j]; ++s, ++st) {
+      if (32 * s >= rk[j]) continue;  // uniform
+      const bool live = 32 * s + 8 * (lane >> 4) < rk[j];
+      if constexpr (F32) {
+        uint4 hi, lo;
+        split_hi_lo<BF>(live ? g.a[st][0] : zero, live ? g.a[st][1] : zero, hi, lo);
+        acc[j] = mfma16<BF>(hi, g.w[st], acc[j]);
+        acc[j] = mfma16<BF>(lo, g.w[st], acc[j]);
+      } else {
+        acc[j] = mfma16<BF>(live ? g.a[st][0] : zero, g.w[st], acc[j]);
+      }
+    }
+  }
+  // acc[j][r]: token 4 (lane / 16) + r of the chunk, channel ch of the head
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int t = 4 * (lane >> 4) + r;
+    s_d[t * kN + ch] = acc[0][r];
+    s_d[(kCk + t) * kN + ch] = acc[1][r];
+    s_d[(2 * kCk + t) * kN + ch] = acc[2][r];
+    if (t0 + t < t1) p.dg[((int64_t)bi * T + t0 + t) * p.C + h * kN + ch] = acc[3][r];
+  }
+}
+template <bool BF, bool F32, class St>
+RWKV7_DEV void lora2_chunk(const PrefillScanArgs &p, St &st, int h, int bi, int T, int t0, int t1, float *s_d) {
+  const Lora2Regs<F32> g = lora2_load<F32>(p, h, bi, T, t0, t1);
+  st.fetch(t0);
+  lora2_compute<BF, F32>(p, g, h, bi, T, t0, t1, s_d);
+}
+
 template <class St>
 __global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(typename St::Args p, float *rec, int T, int H) {
   __shared__ StageBuf<kCk> s_stage;  // the stager's output; then AkaV, G1, U, G2, Y0
@@ -793,6 +898,7 @@ __global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(typename St::Args 
   Row *s_akav = reinterpret_cast<Row *>(&s_stage[0][0][0]);
   Row *s_g1 = s_akav + kCk, *s_u = s_akav + 2 * kCk, *s_g2 = s_akav + 3 * kCk, *s_y0 = s_akav + 4 * kCk;
   static_assert(sizeof(StageBuf<kCk>) >= 5 * kCk * kPad * sizeof(float), "staging buffer reuse");
+  static_assert(sizeof(s_x) >= 3 * kCk * kN * sizeof(float), "LoRA steps staged in s_x");
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int row = lane & 15, kq = lane >> 4, col = 16 * wv + row;
@@ -800,7 +906,24 @@ __global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(typename St::Args 
   const int C = H * kN;
   const int t0 = c * kCk, t1 = min(T, t0 + kCk), Tl = t1 - t0;
   St st(p, h, -1, (int64_t)bi * T * C + (int64_t)h * kN, t1);
-  st.fetch(t0);
+  bool fetched = false;
+  if constexpr (std::is_same<St, GateStager<kCk>>::value) {
+    if (p.l1) {
+      float *s_d = &s_x[0][0][0];  // free until the staged chunk is copied there
+      if (p.bf) {
+        if (p.l1_f32) lora2_chunk<true, true>(p, st, h, bi, T, t0, t1, s_d);
+        else lora2_chunk<true, false>(p, st, h, bi, T, t0, t1, s_d);
+      } else {
+        if (p.l1_f32) lora2_chunk<false, true>(p, st, h, bi, T, t0, t1, s_d);
+        else lora2_chunk<false, false>(p, st, h, bi, T, t0, t1, s_d);
+      }
+      st.lds_d = s_d;
+      st.lds_ld = kN;
+      fetched = true;
+      __syncthreads();
+    }
+  }
+  if (!fetched) st.fetch(t0);
   st.commit(t0, s_stage);
   __syncthreads();
   {  // to padded f32 rows; tokens past the end become identity steps
