@@ -983,10 +983,13 @@ static int launch_skinny(const GemmProb *probs, int nprob, int M, hipStream_t st
 //
 // f32 A (a32) up to kA32Bm16MaxM rows: 16-row tiles, so a workgroup's f32 A
 // chunk takes the bytes (and registers) a 32-row 16-bit chunk takes and the
-// prefetch-all kernel can hold 8 chunks without extra K splits.
+// prefetch-all kernel can hold 8 chunks without extra K splits; beyond,
+// 32-row tiles (measured against 64: 0.4B prefill 1 x 512 3.66 vs 4.36 ms,
+// 1 x 1024 6.29 vs 6.62 ms, 1 x 1536 8.67 vs 9.51 ms -- a 64-row f32 tile
+// doubles both the A bytes per workgroup and the MFMAs per W fragment).
 constexpr int kA32Bm16MaxM = 256;
 static int bm_for(int M, bool a32 = false) {
-  if (a32 && M <= kA32Bm16MaxM) return 16;
+  if (a32) return M <= kA32Bm16MaxM ? 16 : 32;
   return M <= 256 ? 32 : 64;
 }
 
