@@ -205,7 +205,8 @@ def test_gemm_matches_fp32(M, N, Kd, epi, cuda):
 
 @pytest.mark.parametrize(
     "M,N,Kd",
-    [(1, 64, 256), (5, 100, 40), (16, 1024, 1024), (33, 72, 16), (128, 4096, 1024), (128, 1024, 4096),
+    [(1, 64, 256), (5, 100, 40), (8, 300, 1024), (12, 1024, 4096), (16, 1024, 1024), (24, 4096, 1024),
+     (33, 72, 16), (128, 4096, 1024), (128, 1024, 4096),
      (200, 1024, 4096), (7, 65536, 256), (512, 1024, 1024), (600, 300, 128), (1030, 520, 64), (2048, 1024, 256)],
 )
 @pytest.mark.parametrize("epi", ["f32", "add", "relu2_f32", "tanh_f32", "sigmoid_f32", "f16"])
