@@ -1005,7 +1005,11 @@ static int bm_for(int M, bool a32 = false) {
 //
 // f32 A (a32) at 32-row tiles: also split until a split holds at most 4
 // chunks, the most whose f32 A pieces and W fragments the prefetch-all kernel
-// keeps in registers at once.
+// keeps in registers at once. f32 A tiles take ~70 KB of LDS in the
+// prefetch-all kernel, so two workgroups share a CU: splitting stops before a
+// second round of workgroups (measured against splitting up to four per CU:
+// the 1.5B shape's B=64 decode 2.65 vs 3.04 ms/step, 0.4B prefill 16 x 16
+// 2.38 vs 2.51 ms; 1 x 128 unchanged).
 static void plan_splits(const GemmProb *probs, int nprob, int M, int cus, bool can_split, int *S, int *kslice) {
   const int BM = bm_for(M, probs[0].a32 != 0);
   const int m_tiles = (M + BM - 1) / BM;
@@ -1019,7 +1023,8 @@ static void plan_splits(const GemmProb *probs, int nprob, int M, int cus, bool c
       auto bytes = [&](int sp) { return (int64_t)(2 * kBN + (a32 ? 4 : 2) * BM) * ((K + sp - 1) / sp); };
       auto too_long = [&](int sp) { return a32 && BM == 32 && (K + sp - 1) / sp > 4 * kKC; };
       while (s < kMaxSplit && K / (2 * s) >= 2 * kKC &&
-             (tiles * s < cus || bytes(s) > 256 * 1024 || too_long(s)) && (int64_t)tiles * 2 * s <= 4 * cus)
+             (tiles * s < cus || bytes(s) > 256 * 1024 || too_long(s)) &&
+             (int64_t)tiles * 2 * s <= (a32 ? 2 : 4) * cus)
         s *= 2;
     }
     S[i] = s;
