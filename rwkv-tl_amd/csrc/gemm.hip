@@ -6,8 +6,11 @@
 // (8 consecutive k of one row). Accumulation is fp32.
 //
 // At the sizes of prefill and batched decode (M = B*T up to a few hundred) the
-// product is bound by streaming W from HBM, so the kernel is built around
-// keeping many weight loads in flight on every CU:
+// product is neither MFMA- nor HBM-bound: a workgroup's time is the latency of
+// its one round of loads, its products and its epilogue (MFMA-busy and fetch
+// counters at the 0.4B prefill: under 0.05 of the MFMA pipes' cycles, ~1 TB/s
+// of fetch). So the kernel is built around issuing every load of a workgroup
+// as early as possible:
 //   * workgroup tile: BM rows x 64 columns; wave w owns columns [16w, 16w+16)
 //     and all BM rows (BM/16 accumulators);
 //   * each wave streams its 16-row strip of W straight into registers, a chunk
@@ -24,8 +27,8 @@
 // A may also be f32 (GemmProb::a32): each A fragment is then split into its
 // 16-bit hi part and 16-bit remainder (split_hi_lo) and multiplied by the same
 // W fragment twice, which keeps the activations at fp32-grade precision for
-// about the cost of the second MFMA and A's doubled bytes (these kernels are
-// bound by streaming W, not by the MFMAs).
+// the cost of the second MFMA (the MFMA pipes are nearly idle at these sizes)
+// and of A's doubled bytes, which lengthen each workgroup's load round.
 //
 // One launch runs a group of up to 8 problems that share M and A's rows (the
 // r/k/v projections and the four LoRA first steps of one layer, for instance).
