@@ -49,6 +49,13 @@ the same loop with the reference's sampling composition in torch operators
 (``demo/sampling.py:13-70``) for comparison; plus the sampling kernel's
 average launch time (HIP events) at B=1 and B=16.
 
+``python bench.py --timeline`` (after ``python rwkv-tl_amd/build_hip.py
+--timeline``) loads the diagnostic library whose persistent kernels stamp the
+GPU's 100 MHz real-time counter at the stage boundaries of every layer, runs
+0.4B decode at B=1 (``decode_mk_kernel``) and B=16 (``rows_mk_kernel``), and
+prints each kernel's per-layer timeline (median over the middle layers of
+the median and latest workgroup at each point) and one JSON line.
+
 ``python bench.py --configs`` prints one more JSON line with the survey's
 other measurement configurations, each timed with HIP events after warm-up:
 C2 (standalone wkv7 scan, B=8, H=16, T=128, fp32 w and state, f16 r/k/v/a/b),
@@ -491,6 +498,100 @@ def bench_generate() -> dict:
     return out
 
 
+TIMELINE_LIB = Path(__file__).resolve().parent / "rwkv-tl_amd" / "rwkv_tl_amd" / "librwkv7_hip_timeline.so"
+# stamp points of the two persistent kernels (csrc/decode_mk.hip, csrc/rows_mk.hip)
+TL_DECODE = ["P1 input ready", "P1 published", "P3 input ready", "P3 published", "P4 input ready",
+             "P4 published", "P5 input ready", "P5 published", "P2 input ready (heads)", "P2 published (heads)"]
+TL_ROWS = ["P1 start", "P1 input ready", "P1 statistics", "P1 products", "P2 start", "P2 done", "P3 start",
+           "P3 input ready", "P3 published", "P4 start", "P4 input ready", "P4 statistics", "P4 products",
+           "P4 published", "P5 start", "P5 input ready", "P5 products", "P5 published"]
+
+
+def _timeline_table(buf, names, groups: int, layers: int, ref_point: int) -> dict:
+    """buf [32][1024][24] uint64 stamps (100 MHz). Per layer l in 1 .. layers-2,
+    times in us from the earliest stamp of ref_point in that layer; for every
+    point the median and the maximum over the workgroups that recorded it,
+    then the median of those over the layers; plus the layer period."""
+    import numpy as np
+
+    rows = {n: {"median_us": [], "last_us": [], "groups": 0} for n in names}
+    period = []
+    for l in range(1, layers - 1):
+        x = buf[l, :groups, : len(names)].astype(np.int64)
+        ref = x[:, ref_point][x[:, ref_point] > 0]
+        nxt = buf[l + 1, :groups, ref_point].astype(np.int64)
+        nxt = nxt[nxt > 0]
+        if ref.size == 0:
+            continue
+        t0 = ref.min()
+        if nxt.size:
+            period.append((nxt.min() - t0) / 100.0)
+        for i, n in enumerate(names):
+            v = x[:, i]
+            v = v[v > 0]
+            if v.size == 0:
+                continue
+            v = (v - t0) / 100.0
+            rows[n]["median_us"].append(float(np.median(v)))
+            rows[n]["last_us"].append(float(v.max()))
+            rows[n]["groups"] = int(v.size)
+    out = {"layer_period_us": round(float(np.median(period)), 2) if period else None, "points": {}}
+    for n in names:
+        r = rows[n]
+        if r["median_us"]:
+            out["points"][n] = {"median_us": round(float(np.median(r["median_us"])), 2),
+                                "last_us": round(float(np.median(r["last_us"])), 2), "workgroups": r["groups"]}
+    return out
+
+
+def bench_timeline() -> dict:
+    """Stage timelines of the two persistent decode kernels (diagnostic build)."""
+    import ctypes
+
+    import numpy as np
+
+    if not TIMELINE_LIB.exists():
+        raise SystemExit(f"{TIMELINE_LIB} not built: python rwkv-tl_amd/build_hip.py --timeline")
+    os.environ["RWKV7_HIP_LIB"] = str(TIMELINE_LIB)
+    import torch
+
+    from rwkv_tl_amd import RWKV7HIP, State, _lib
+    from rwkv_tl_amd.checkpoint import make_random_state_dict
+    from rwkv_tl_amd.weight import RWKV7Weight
+
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    log("building 0.4B weights (seed 0) for the timeline library")
+    sd = make_random_state_dict("0.4b", seed=0, dtype=torch.float16)
+    w = RWKV7Weight.from_state_dict(sd, device=dev, dtype=torch.float16)
+    del sd
+    model = RWKV7HIP(w, is_torch_compile=False)
+    g = torch.Generator(device="cpu").manual_seed(1)
+    shape = (32, 1024, 24)
+    out = {"mode": "timeline", "model": "RWKV7-0.4B fp16", "clock": "GPU real-time counter, 100 MHz",
+           "reading": "per layer (middle layers), us from the earliest workgroup at the reference point: "
+                      "median_us over the workgroups that record the point, last_us the latest of them; "
+                      "medians over the layers"}
+    for name, B, fn, names, ref in (("decode_mk_kernel B=1", 1, "rwkv7_timeline_read_decode", TL_DECODE, 0),
+                                    ("rows_mk_kernel B=16", 16, "rwkv7_timeline_read_rows", TL_ROWS, 1)):
+        S = State(w.L, w.C, 64, device=dev, batch=B)
+        for _ in range(12):
+            tok = torch.randint(0, w.head.shape[0], (B,), generator=g).to(dev)
+            _, S = model.decode(tok, S)
+        torch.cuda.synchronize()
+        model.raise_if_aborted()
+        buf = np.zeros(shape, dtype=np.uint64)
+        read = getattr(lib, fn)
+        read.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+        _lib.check(read(buf.ctypes.data, buf.nbytes), fn)
+        tab = _timeline_table(buf, names, shape[1], w.L, ref)
+        out[name] = tab
+        log(f"{name}: layer period {tab['layer_period_us']} us")
+        for n, r in tab["points"].items():
+            log(f"  {n:24s} median {r['median_us']:7.2f} us  last {r['last_us']:7.2f} us  ({r['workgroups']} workgroups)")
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -506,6 +607,9 @@ def main() -> None:
                     help="time the survey's C2, C4 and C5 configurations instead (one different JSON line)")
     ap.add_argument("--generate", action="store_true",
                     help="time generate() with the on-device sampler instead (one different JSON line)")
+    ap.add_argument("--timeline", action="store_true",
+                    help="stage timelines of the persistent decode kernels from the diagnostic library "
+                         "(python rwkv-tl_amd/build_hip.py --timeline first; one different JSON line)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two rocprofv3 --pmc csv runs and exit (no GPU)")
     args = ap.parse_args()
@@ -521,6 +625,9 @@ def main() -> None:
         sys.exit(2)
     if args.generate:
         print(json.dumps(bench_generate()), flush=True)
+        return
+    if args.timeline:
+        print(json.dumps(bench_timeline()), flush=True)
         return
     if args.configs:
         print(json.dumps(bench_configs()), flush=True)

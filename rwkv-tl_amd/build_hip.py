@@ -22,6 +22,10 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 OUT = HERE / "rwkv_tl_amd" / "librwkv7_hip.so"
+# diagnostic build with the persistent kernels' stage stamps (RWKV7_TIMELINE;
+# bench.py --timeline loads it through RWKV7_HIP_LIB)
+BUILD_TL = HERE / "_build_timeline"
+OUT_TL = HERE / "rwkv_tl_amd" / "librwkv7_hip_timeline.so"
 ARCH = "gfx950"
 
 COMMON_FLAGS = [
@@ -57,30 +61,35 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(err, file=sys.stderr)
 
 
-def build(jobs: int | None = None, verbose: bool = False) -> Path:
-    """Compile every csrc/*.hip and link the shared library; returns its path."""
-    BUILD.mkdir(exist_ok=True)
+def build(jobs: int | None = None, verbose: bool = False, timeline: bool = False) -> Path:
+    """Compile every csrc/*.hip and link the shared library; returns its path.
+    timeline: the diagnostic library with stage stamps, librwkv7_hip_timeline.so."""
+    build_dir, out = (BUILD_TL, OUT_TL) if timeline else (BUILD, OUT)
+    build_dir.mkdir(exist_ok=True)
     cc = hipcc()
     srcs = sorted(CSRC.glob("*.hip"))
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    objs = [BUILD / (s.stem + ".o") for s in srcs]
-    cmds = [[cc, *COMMON_FLAGS, "-c", str(s), "-o", str(o)] for s, o in zip(srcs, objs)]
+    objs = [build_dir / (s.stem + ".o") for s in srcs]
+    flags = [*COMMON_FLAGS, "-DRWKV7_TIMELINE"] if timeline else COMMON_FLAGS
+    cmds = [[cc, *flags, "-c", str(s), "-o", str(o)] for s, o in zip(srcs, objs)]
     jobs = jobs or min(len(cmds), os.cpu_count() or 4, 16)
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
-    tmp = OUT.with_suffix(".so.tmp")
+    tmp = out.with_suffix(".so.tmp")
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)], verbose)
-    os.replace(tmp, OUT)
-    return OUT
+    os.replace(tmp, out)
+    return out
 
 
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--timeline", action="store_true",
+                    help="build the diagnostic library with stage stamps (librwkv7_hip_timeline.so)")
     args = ap.parse_args()
-    print(build(args.jobs, args.verbose))
+    print(build(args.jobs, args.verbose, args.timeline))
 
 
 if __name__ == "__main__":

@@ -65,6 +65,10 @@ constexpr int kMT = kMW * 64;    // math threads
 constexpr int kHB = 4;           // head rows per batch
 constexpr int kHRing = 3;        // head batches in flight
 constexpr int kSpinLimit = 1 << 21;
+// timeline points (diagnostic build): workers 0 P1 input ready, 1 P1 published,
+// 2 P3 input ready, 3 P3 published, 4 P4 input ready, 5 P4 published, 6 P5
+// input ready, 7 P5 published; head workgroups 8 P2 input ready, 9 P2 published
+RWKV7_TL_BUFFER(tl_decode);
 constexpr int kRep = 8;          // replicas of each broadcast hand-off vector
 constexpr int kHidProbe = 4096;  // probe stride of the FFN hidden vector
 constexpr int kXProbe = 1024;    // probe stride of the x vectors
@@ -677,6 +681,7 @@ RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
     wait_flag(cx, s.xflag, cx.tag(5 * l));  // the comm wave's probe saw the P2 input arriving
     head_read(cx, a, s, g, wv, cx.tag(5 * l));
     __syncthreads();  // HA
+    RWKV7_TL(tl_decode, l, 8);
     wait_vm0();       // this layer's operands (issued a layer ago)
     refresh();
     if (wv < 5) {  // LoRA second step, part wv of channel lane
@@ -796,6 +801,7 @@ RWKV7_DEV void math_head(const MkArgs &a, const MkGeom &m, const MkLds &s, const
       const float out = (yn + rk * v) * gate;
 #pragma unroll
       for (int rp = 0; rp < kRep; ++rp) publish(a.core_ex + (int64_t)rp * C + g * kN + lane, cx.tag(5 * l + 1), out);
+      RWKV7_TL(tl_decode, l, 9);
     }
     if (mt < 4 * kN && ok) {
       float4 *Sp = reinterpret_cast<float4 *>(a.rnn + (((int64_t)l * H + g) * kN + row) * kN + j0);
@@ -984,6 +990,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     const int ph = 5 * l;
     // ---------------- P1: LN1 + shift + [r;k;v;LoRA1] ------------------------
     __syncthreads();  // A1
+    RWKV7_TL(tl_decode, l, 0);
     refresh();
     {
       const float2 st = combine_stats(s.xst, C, inv_c);
@@ -1022,6 +1029,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
       }
     }
     count_publish();
+    RWKV7_TL(tl_decode, l, 1);
     // every load of the rest of the layer, issued while the head workgroups wait
     // for their input (that hand-off is slow anyway) and compute
     refresh();
@@ -1032,6 +1040,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
     wait_flag(cx, s.xflag, cx.tag(ph + 1));
     read_all<1, 1>(cx, 0, r_cso, XS, cx.tag(ph + 1), Ident(), [&](int i, float v) { s.core_in[wv * XS + i] = v; });
     __syncthreads();  // A3
+    RWKV7_TL(tl_decode, l, 2);
     wait_vm0();
     // ---------------- P3: o-projection + residual -----------------------------
     refresh();
@@ -1044,8 +1053,10 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
       if (lane == kRep) a.tmix_x[(int64_t)l * C + c] = F16T<BF>::from_f(s.ln1[c]);
     }
     count_publish();
+    RWKV7_TL(tl_decode, l, 3);
     poll_x(cx.tag(ph + 2), s.x4, s.xst + 2 * kW);
     __syncthreads();  // A4
+    RWKV7_TL(tl_decode, l, 4);
     // ---------------- P4: LN2 + shift + FFN key + relu^2 ----------------------
     refresh();
     {
@@ -1081,6 +1092,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
       }
     }
     count_publish();
+    RWKV7_TL(tl_decode, l, 5);
     {
       // every wave reads one slice of the hidden vector (the math waves are
       // idle until it is complete, and 8 readers cut its round trips)
@@ -1091,6 +1103,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
                             [&](int i, float v) { s.hid[wv * FS + i] = v; });
     }
     __syncthreads();  // A5
+    RWKV7_TL(tl_decode, l, 6);
     // ---------------- P5: FFN value + residual --------------------------------
     refresh();
     if (wv < m.nown && !cx.failed()) {
@@ -1101,6 +1114,7 @@ RWKV7_DEV void math_worker(const MkArgs &a, const MkGeom &m, const MkLds &s, con
       if (lane == kRep) a.cmix_x[(int64_t)l * C + c] = F16T<BF>::from_f(s.ln2[c]);
     }
     count_publish();
+    RWKV7_TL(tl_decode, l, 7);
     poll_x(cx.tag(ph + 4), s.x1, s.xst);
   }
 
@@ -1434,3 +1448,5 @@ int launch_decode_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const 
 }
 
 }  // namespace rwkv7
+
+RWKV7_TL_READER(rwkv7_timeline_read_decode, rwkv7::tl_decode);

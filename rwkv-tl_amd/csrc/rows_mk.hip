@@ -68,6 +68,12 @@ constexpr int kRMaxC = 1024;         // A tiles of C columns live in LDS
 constexpr int kRLdX = kRMaxC + 4;    // floats per LDS row of xs (padding spreads the 16 rows over the banks)
 constexpr int kRLdA = kRMaxC + 8;    // halves per row of the second LDS region (P2 scratch)
 constexpr int kRMaxG = 1024;
+// timeline points (diagnostic build), per layer, from the first block of each
+// stage a workgroup runs: P1 0 start, 1 input x ready, 2 statistics, 3 products
+// done; P2 4 start, 5 done; P3 6 start, 7 input ready, 8 published; P4 9 start,
+// 10 input ready, 11 statistics, 12 products done, 13 published; P5 14 start,
+// 15 input ready, 16 products done, 17 published
+RWKV7_TL_BUFFER(tl_rows);
 // P2 keeps the activated LoRA first steps (f32 [16][552]), the second steps
 // and gates of up to 16 tokens (f32 [16][256 + 512] + 16) in the xs and
 // scratch regions
@@ -740,6 +746,7 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
     const float *vec = reinterpret_cast<const float *>(Lp + a.o_vec);
     // ---------------- P1 ----------------
     for (int b1 = g; b1 < nP1; b1 += G) {
+      if (b1 == g) RWKV7_TL(tl_rows, l, 0);
       const int row0 = 16 * b1;
       const int sg = row0 < e0 ? 0 : row0 < e1 ? 1 : row0 < e2 ? 2 : row0 < e3 ? 3 : row0 < e4 ? 4 : row0 < e5 ? 5 : 6;
       const int mu = sg == 0 ? RWKV7_V_X_R : sg == 1 ? RWKV7_V_X_K : sg <= 3 ? RWKV7_V_X_V
@@ -759,6 +766,7 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
         embed_rows(s, a);
       } else {
         wait_flags(cx, a.fl[4], nP5, cx.tag(l - 1, 4), ident);
+        if (b1 == g) RWKV7_TL(tl_rows, l, 1);
         read_x(s, a.x, M, C);
       }
       if (threadIdx.x < 64) mv = load_mix(lw1, lb1, mu1, C);
@@ -766,11 +774,13 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
       // the channel-mix state of the last layer (every FFN-value block of it has published)
       if (l > 0 && b1 == g && slice_owner && !cx.failed()) store_shift_slice(a, s.shs2, a.cmix_x, l - 1, 16 * g);
       row_stats(s, M, C);
+      if (b1 == g) RWKV7_TL(tl_rows, l, 2);
       __syncthreads();
       // blocks 0 .. C/16 - 1 also write 16 columns each of the new time-mix shift state
       build_mix(s, a, C, mv, s.shs1, b1 == g && slice_owner ? 16 * g : -1);
       __syncthreads();
       const floatx4 acc = block_mma(s, wb, nksC);
+      if (b1 == g) RWKV7_TL(tl_rows, l, 3);
       int m, n;
       const float v = reduce_tile(s, acc, &m, &n);
       if (threadIdx.x < 256 && m < M && !cx.failed()) st64f(a.proj + (int64_t)m * N1 + row0 + n, v, cx.tag(l, 0));
@@ -778,8 +788,10 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
     }
     // ---------------- P2 ----------------
     for (int u = g; u < nP2; u += G) {
+      if (u == g) RWKV7_TL(tl_rows, l, 4);
       const int b = u / a.H, h = u % a.H;
       p2_unit(a, s, cx, l, b, h);
+      if (u == g) RWKV7_TL(tl_rows, l, 5);
       publish_flag(cx, a.fl[1] + u, cx.tag(l, 1));
     }
     // ---------------- the shift states ----------------
@@ -789,6 +801,7 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
 
     // ---------------- P3 ----------------
     for (int b3 = g; b3 < nP3; b3 += G) {
+      if (b3 == g) RWKV7_TL(tl_rows, l, 6);
       const WBlock wb = load_block(reinterpret_cast<const uint16_t *>(Fp + a.f_o) + (int64_t)b3 * nksC * 512, 0, nksC);
       // the residual of this thread's output (final since this workgroup's P1
       // wait), loaded and stored by threads 256..511 (not the polling wave)
@@ -796,6 +809,7 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
       const int mr = 4 * ((t & 63) >> 4) + (t >> 6), cr = 16 * b3 + (t & 15);
       const float res = threadIdx.x >= 256 && mr < M ? residual_in(a, l, mr, cr) : 0.f;
       wait_flags(cx, a.fl[1], nP2, cx.tag(l, 1), ident);
+      if (b3 == g) RWKV7_TL(tl_rows, l, 7);
       read_rows(s, a.core, C, 0, C, M, true);
       __syncthreads();
       const floatx4 acc = block_mma(s, wb, nksC);
@@ -803,41 +817,49 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
       const float v = reduce_tile(s, acc, &m, &n);
       if (threadIdx.x >= 256 && m < M && !cx.failed()) rst_f(a.x + (int64_t)m * C + 16 * b3 + n, res + v);
       publish_flag(cx, a.fl[2] + b3, cx.tag(l, 2));
+      if (b3 == g) RWKV7_TL(tl_rows, l, 8);
     }
     // ---------------- P4 ----------------
     for (int b4 = g; b4 < nP4; b4 += G) {
+      if (b4 == g) RWKV7_TL(tl_rows, l, 9);
       const WBlock wb = load_block(reinterpret_cast<const uint16_t *>(Fp + a.f_fk) + (int64_t)b4 * nksC * 512, 0, nksC);
       load_state(s, a.cmix_x + (int64_t)l * a.B * C, a.B, C);
       const float *lw2 = vec + RWKV7_V_LN2_W * C, *lb2 = vec + RWKV7_V_LN2_B * C, *mu2 = vec + RWKV7_V_FFN_X_K * C;
       MixVec mv{};
       if (threadIdx.x >= 64) mv = load_mix(lw2, lb2, mu2, C);
       wait_flags(cx, a.fl[2], nP3, cx.tag(l, 2), ident);
+      if (b4 == g) RWKV7_TL(tl_rows, l, 10);
       read_x(s, a.x, M, C);
       if (threadIdx.x < 64) mv = load_mix(lw2, lb2, mu2, C);
       __syncthreads();
       // the time-mix state of this layer (every o-projection block has published)
       if (b4 == g && slice_owner && !cx.failed()) store_shift_slice(a, s.shs1, a.tmix_x, l, 16 * g);
       row_stats(s, M, C);
+      if (b4 == g) RWKV7_TL(tl_rows, l, 11);
       __syncthreads();
       // blocks 0 .. C/16 - 1 also write 16 columns each of the new channel-mix shift state
       build_mix(s, a, C, mv, s.shs2, b4 == g && slice_owner ? 16 * g : -1);
       __syncthreads();
       const floatx4 acc = block_mma(s, wb, nksC);
+      if (b4 == g) RWKV7_TL(tl_rows, l, 12);
       int m, n;
       float v = reduce_tile(s, acc, &m, &n);
       v = fmaxf(v, 0.f);
       v = v * v;
       if (threadIdx.x < 256 && m < M && !cx.failed()) rst_f(a.hid + (int64_t)m * F + 16 * b4 + n, v);
       publish_flag(cx, a.fl[3] + b4, cx.tag(l, 3));
+      if (b4 == g) RWKV7_TL(tl_rows, l, 13);
     }
     // ---------------- P5 ----------------
     for (int u5 = g; u5 < 4 * nP5; u5 += G) {
+      if (u5 == g) RWKV7_TL(tl_rows, l, 14);
       const int b5 = u5 >> 2, q = u5 & 3;
       const int Kq = F / 4;
       const WBlock wb =
           load_block(reinterpret_cast<const uint16_t *>(Fp + a.f_fv) + (int64_t)b5 * nksF * 512, q * nksQ, nksQ);
       const int f0 = q * (nP4 / 4);
       wait_flags(cx, a.fl[3], nP4 / 4, cx.tag(l, 3), [f0](int i) { return f0 + i; });
+      if (u5 == g) RWKV7_TL(tl_rows, l, 15);
       // the residual (the o-projection output, final: the P4 blocks waited for it)
       const int t = threadIdx.x & 255;
       const int mr = 4 * ((t & 63) >> 4) + (t >> 6), cr = 16 * b5 + (t & 15);
@@ -845,6 +867,7 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
       read_rows(s, a.hid, F, q * Kq, Kq, M, true);
       __syncthreads();
       const floatx4 acc = block_mma(s, wb, nksQ);
+      if (u5 == g) RWKV7_TL(tl_rows, l, 16);
       int m, n;
       const float v = reduce_tile(s, acc, &m, &n);
       // split-K hand-off: quarters 1..3 store their partial tiles as tagged
@@ -863,6 +886,7 @@ __global__ __launch_bounds__(kRT) void rows_mk_kernel(RkArgs a) {
           if (!cx.failed()) rst_f(a.x + (int64_t)m * C + 16 * b5 + n, res + sum);
         }
         publish_flag(cx, a.fl[4] + b5, cx.tag(l, 4));
+        if (u5 == g) RWKV7_TL(tl_rows, l, 17);
       }
     }
   }
@@ -1068,3 +1092,5 @@ int launch_rows_mk(const rwkv7_model &m, const rwkv7_layer_layout &lay, const rw
 }
 
 }  // namespace rwkv7
+
+RWKV7_TL_READER(rwkv7_timeline_read_rows, rwkv7::tl_rows);

@@ -26,6 +26,37 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
+// ---- stage timeline (diagnostic builds) -----------------------------------
+// `build_hip.py --timeline` defines RWKV7_TIMELINE and builds a separate
+// library (librwkv7_hip_timeline.so): thread 0 of a workgroup of a persistent
+// kernel then records the 100 MHz real-time counter at named points of every
+// layer into that kernel's device array, [layer][workgroup][point], which
+// rwkv7_timeline_read_* copies to the host (bench.py --timeline). The product
+// build compiles every stamp away.
+constexpr int kTlLayers = 32, kTlGroups = 1024, kTlPoints = 24;
+#ifdef RWKV7_TIMELINE
+#define RWKV7_TL_BUFFER(name) __device__ unsigned long long name[kTlLayers * kTlGroups * kTlPoints]
+#define RWKV7_TL(buf, layer, pt)                                                                           \
+  do {                                                                                                     \
+    if (threadIdx.x == 0 && (layer) < kTlLayers && blockIdx.x < kTlGroups)                               \
+      buf[((int64_t)(layer) * kTlGroups + blockIdx.x) * kTlPoints + (pt)] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#define RWKV7_TL_READER(fn, buf)                                                                  \
+  extern "C" int fn(void *host, int64_t bytes) {                                                  \
+    if (!host || bytes < (int64_t)sizeof(buf)) return RWKV7_EINVAL;                               \
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(buf), sizeof(buf), 0, hipMemcpyDeviceToHost) ==   \
+                   hipSuccess                                                                      \
+               ? RWKV7_OK                                                                          \
+               : RWKV7_ELAUNCH;                                                                    \
+  }
+#else
+#define RWKV7_TL_BUFFER(name) static_assert(true, "")
+#define RWKV7_TL(buf, layer, pt) \
+  do {                           \
+  } while (0)
+#define RWKV7_TL_READER(fn, buf) static_assert(true, "")
+#endif
+
 // ---- lane permutes ------------------------------------------------------
 
 template <int CTRL>
