@@ -4,8 +4,9 @@ Usage: ``python rwkv-tl_amd/build_hip.py [--jobs N] [--verbose]``.
 
 Every ``csrc/*.hip`` translation unit is compiled to an object in
 ``_build/`` and linked into ``rwkv_tl_amd/librwkv7_hip.so``. The library
-links against ``libamdhip64.so.7``; the Python loader imports torch first, so
-at run time that name binds to the HIP runtime torch has already loaded.
+links against ``libamdhip64.so.7`` and ``libhipblaslt.so.1`` (the large-M
+plain GEMMs); the Python loader imports torch first, so at run time those
+names bind to the HIP runtime and hipBLASLt torch has already loaded.
 """
 
 from __future__ import annotations
@@ -77,7 +78,7 @@ def build(jobs: int | None = None, verbose: bool = False, timeline: bool = False
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
     tmp = out.with_suffix(".so.tmp")
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)], verbose)
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-lhipblaslt", "-o", str(tmp)], verbose)
     os.replace(tmp, out)
     return out
 

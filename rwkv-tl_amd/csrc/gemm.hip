@@ -479,7 +479,9 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmGroup g) {
 // ---------------------------------------------------------------------------
 // Large-M path (long prefills, see big_fits): the product is MFMA-bound, so
 // the workgroup tile is large enough that each byte staged through LDS feeds
-// many products. BM x BN tile (256 x 256, or 128 x 128 where the larger tiles
+// many products. Problems with a plain epilogue run in hipBLASLt instead when
+// it has an algorithm for them (gemm_lt.hip: ~1.7x faster on these shapes);
+// this kernel keeps the relu^2 / tanh / sigmoid epilogues. BM x BN tile (256 x 256, or 128 x 128 where the larger tiles
 // leave CUs idle), 8 waves as 2 (rows) x 4 (columns), each wave a (BM/2) x
 // (BN/4) block of 16x16 accumulators; K in stages of 32.
 //
@@ -1082,13 +1084,17 @@ int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, f
       for (int i = 0; i < nb; ++i) rows = min(rows, big_rows_per_launch(big[i].lda));
       for (int r0 = 0; r0 < M; r0 += rows) {
         GemmProb blk[kMaxProb];
+        int nk = 0;
+        const int mr = min(rows, M - r0);
         for (int i = 0; i < nb; ++i) {
-          blk[i] = big[i];
+          GemmProb b = big[i];
           const int ysz = big[i].epi == GEPI_F32 || big[i].epi == GEPI_ADD_F32 ? 4 : 2;
-          blk[i].A = big[i].A + (int64_t)r0 * big[i].lda;
-          blk[i].Y = static_cast<char *>(big[i].Y) + (int64_t)r0 * big[i].ldy * ysz;
+          b.A = big[i].A + (int64_t)r0 * big[i].lda;
+          b.Y = static_cast<char *>(big[i].Y) + (int64_t)r0 * big[i].ldy * ysz;
+          // plain GEMMs go to hipBLASLt; the others, and any it declines, here
+          if (!lt_gemm(b, mr, st)) blk[nk++] = b;
         }
-        RWKV7_TRY_GEMM(launch_big(blk, nb, min(rows, M - r0), cus, st));
+        if (nk > 0) RWKV7_TRY_GEMM(launch_big(blk, nk, mr, cus, st));
       }
       if (nr == 0) return RWKV7_OK;
       probs = rest;

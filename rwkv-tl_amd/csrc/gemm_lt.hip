@@ -1,0 +1,126 @@
+// Large-M plain GEMMs through hipBLASLt.
+//
+// The long-prefill GEMMs (M = B*T in the thousands: the 1.5B-shaped 4 x 1024
+// prefill) are MFMA-bound, and there the vendor library's kernels run at
+// ~0.4-0.5 of the dense f16 peak where this library's own large-M kernel
+// (gemm.hip, gemm_big_tile) reaches ~0.2-0.3: with 16-bit operands and a plain
+// epilogue -- store f32, store 16-bit, or add into an f32 output -- such a
+// problem is a plain library GEMM, so it goes to hipBLASLt. Everything else
+// (f32 activations, relu^2 / tanh / sigmoid epilogues, the small-M shapes of
+// decode and short prefills) stays on the hand-written kernels, and so does
+// any problem hipBLASLt returns no algorithm for.
+//
+// Mapping: hipBLASLt is column-major, so Y[M, N] = A[M, K] W[N, K]^T (row
+// major) is computed as D = op(W') op(A') with W' = W seen as a K x N
+// column-major matrix (ld = ldw, transposed), A' = A as K x M (ld = lda, not
+// transposed) and D = Y as N x M (ld = ldy). The add epilogue is beta = 1 with
+// C = D = Y. Algorithms are chosen with no workspace, so calls on different
+// streams share nothing but the handle; the chosen algorithm is cached per
+// device and shape.
+#include <hipblaslt/hipblaslt.h>
+
+#include <deque>
+#include <mutex>
+
+#include "rwkv7_kernels.h"
+
+namespace rwkv7 {
+namespace {
+
+struct LtKey {
+  int M, N, K, epi, bf;
+  int64_t lda, ldw, ldy;
+  bool operator==(const LtKey &o) const {
+    return M == o.M && N == o.N && K == o.K && epi == o.epi && bf == o.bf && lda == o.lda && ldw == o.ldw &&
+           ldy == o.ldy;
+  }
+};
+
+struct LtPlan {
+  LtKey key;
+  bool ok = false;
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t lw = nullptr, la = nullptr, ly = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+};
+
+struct LtDevice {
+  std::mutex mu;
+  bool tried = false;
+  hipblasLtHandle_t h = nullptr;
+  std::deque<LtPlan> plans;  // elements stay put as plans are added
+};
+
+constexpr int kLtDevices = 64;
+LtDevice g_lt[kLtDevices];
+
+// The plan of a shape on the current device, built on first use (nullptr if
+// hipBLASLt is unavailable or has no algorithm for it). Nothing is created
+// while the stream is being captured into a graph (the handle may allocate):
+// such a call runs the library's own kernel, and the plan is built by the
+// next call outside a capture.
+const LtPlan *lt_plan(const LtKey &k, hipStream_t st) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kLtDevices) return nullptr;
+  LtDevice &d = g_lt[dev];
+  std::lock_guard<std::mutex> lock(d.mu);
+  for (const LtPlan &p : d.plans)
+    if (p.key == k) return p.ok ? &p : nullptr;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return nullptr;
+  if (!d.tried) {
+    d.tried = true;
+    if (hipblasLtCreate(&d.h) != HIPBLAS_STATUS_SUCCESS) d.h = nullptr;
+  }
+  if (!d.h) return nullptr;
+  LtPlan p;
+  p.key = k;
+  const hipDataType t16 = k.bf ? HIP_R_16BF : HIP_R_16F;
+  const hipDataType ty = k.epi == GEPI_F16 ? t16 : HIP_R_32F;
+  bool ok = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS;
+  const int32_t opT = HIPBLAS_OP_T, opN = HIPBLAS_OP_N;
+  ok = ok && hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT, sizeof(opT)) ==
+                 HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof(opN)) ==
+                 HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatrixLayoutCreate(&p.lw, t16, k.K, k.N, k.ldw) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatrixLayoutCreate(&p.la, t16, k.K, k.M, k.lda) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatrixLayoutCreate(&p.ly, ty, k.N, k.M, k.ldy) == HIPBLAS_STATUS_SUCCESS;
+  if (ok) {
+    hipblasLtMatmulPreference_t pref = nullptr;
+    uint64_t ws = 0;
+    ok = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
+         hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws)) ==
+             HIPBLAS_STATUS_SUCCESS;
+    hipblasLtMatmulHeuristicResult_t res[1];
+    int n = 0;
+    ok = ok && hipblasLtMatmulAlgoGetHeuristic(d.h, p.desc, p.lw, p.la, p.ly, p.ly, pref, 1, res, &n) ==
+                   HIPBLAS_STATUS_SUCCESS &&
+         n > 0 && res[0].state == HIPBLAS_STATUS_SUCCESS && res[0].workspaceSize == 0;
+    if (ok) p.algo = res[0].algo;
+    if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+  }
+  p.ok = ok;
+  d.plans.push_back(p);
+  return p.ok ? &d.plans.back() : nullptr;
+}
+
+}  // namespace
+
+bool lt_eligible(const GemmProb &p) {
+  return !p.a32 && (p.epi == GEPI_F32 || p.epi == GEPI_F16 || p.epi == GEPI_ADD_F32);
+}
+
+bool lt_gemm(const GemmProb &p, int M, hipStream_t st) {
+  if (!lt_eligible(p) || M <= 0) return false;
+  const LtKey k{M, p.N, p.K, p.epi, p.bf ? 1 : 0, p.lda, p.ldw, p.ldy};
+  const LtPlan *pl = lt_plan(k, st);
+  if (!pl) return false;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  const float alpha = 1.f, beta = p.epi == GEPI_ADD_F32 ? 1.f : 0.f;
+  return hipblasLtMatmul(g_lt[dev].h, pl->desc, &alpha, p.W, pl->lw, p.A, pl->la, &beta, p.Y, pl->ly, p.Y, pl->ly,
+                         &pl->algo, nullptr, 0, st) == HIPBLAS_STATUS_SUCCESS;
+}
+
+}  // namespace rwkv7
