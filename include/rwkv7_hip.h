@@ -5,7 +5,12 @@
  * (hipStream_t passed as void*; NULL is the legacy default stream). Nothing in
  * the library allocates or frees device memory, creates streams or events, or
  * synchronises the host (except rwkv7_workspace_errors, a status query): the
- * caller owns every buffer, so the calls can be captured in a HIP graph. Each function returns 0 on success or one of the
+ * caller owns every buffer, so the calls can be captured in a HIP graph. One
+ * exception: a GEMM past the large-M threshold with 16-bit operands and a
+ * plain epilogue (long prefills) runs in hipBLASLt, whose handle -- created
+ * once per device, on the first such call made outside a graph capture (a
+ * call under capture runs the library's own kernel) -- holds memory of its
+ * own until the process ends. Each function returns 0 on success or one of the
  * RWKV7_E* codes below (argument errors are detected on the host before any
  * launch; launch failures return RWKV7_ELAUNCH).
  *
