@@ -55,6 +55,9 @@ GPU's 100 MHz real-time counter at the stage boundaries of every layer, runs
 0.4B decode at B=1 (``decode_mk_kernel``) and B=16 (``rows_mk_kernel``), and
 prints each kernel's per-layer timeline (median over the middle layers of
 the median and latest workgroup at each point) and one JSON line.
+``python bench.py --hops`` (same library) times the hand-off word alone: pairs
+of workgroups on different XCDs or on the same XCD exchange device-scope
+tagged words, and the line gives the one-way latency per hop.
 
 ``python bench.py --configs`` prints one more JSON line with the survey's
 other measurement configurations, each timed with HIP events after warm-up:
@@ -592,6 +595,56 @@ def bench_timeline() -> dict:
     return out
 
 
+def bench_hops(rounds: int = 2008) -> dict:
+    """One-way latency of the persistent kernels' hand-off word (device-scope
+    store, device-scope poll) between two workgroups on different XCDs and on
+    the same XCD, with nothing else running (diagnostic library's probe)."""
+    import ctypes
+
+    import numpy as np
+
+    if not TIMELINE_LIB.exists():
+        raise SystemExit(f"{TIMELINE_LIB} not built: python rwkv-tl_amd/build_hip.py --timeline")
+    os.environ["RWKV7_HIP_LIB"] = str(TIMELINE_LIB)
+    import torch
+
+    from rwkv_tl_amd import _lib
+
+    lib = _lib.load()
+    fn = lib.rwkv7_probe_hops
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_uint32,
+                   ctypes.c_void_p, ctypes.c_void_p]
+    dev = torch.device("cuda:0")
+    G = torch.cuda.get_device_properties(dev).multi_processor_count // 16 * 16
+    out = {"mode": "hops", "workgroups": G, "rounds": rounds,
+           "reading": "per workgroup pair (g, g ^ x): rounds of store own word then poll the partner's; "
+                      "us per round = one-way hand-off latency; median / min / max over the workgroups"}
+    # workgroup g runs on XCD g % 8: partners g ^ 1 and g ^ 4 sit on another XCD, g ^ 8 on the same one
+    for name, x in (("other XCD (partner g ^ 1)", 1), ("other XCD (partner g ^ 4)", 4),
+                    ("same XCD (partner g ^ 8)", 8)):
+        res = []
+        for rep in range(3):
+            words = torch.zeros(16 * G, dtype=torch.int64, device=dev)
+            o = torch.zeros(3 * G, dtype=torch.int64, device=dev)
+            _lib.check(fn(words.data_ptr(), G, x, rounds, 1 + rep * rounds, o.data_ptr(), _lib.stream_handle()),
+                       "rwkv7_probe_hops")
+            torch.cuda.synchronize()
+            res.append(o.cpu().numpy().reshape(G, 3))
+        a = np.stack(res)
+        errs = int(a[:, :, 1].sum())
+        xcc = a[0, :, 2]
+        same = int(sum(xcc[g] == xcc[g ^ x] for g in range(G)))
+        us = a[:, :, 0].astype(np.float64) / (rounds - 8) / 100.0  # 100 MHz ticks
+        out[name] = {"us_median": round(float(np.median(us)), 3), "us_min": round(float(us.min()), 3),
+                     "us_max": round(float(us.max()), 3), "pairs_on_one_xcc": f"{same}/{G}",
+                     "polls_given_up": errs}
+        log(f"{name:28s} {out[name]['us_median']:.3f} us per hop (min {out[name]['us_min']:.3f}, "
+            f"max {out[name]['us_max']:.3f}); pairs on one XCC {same}/{G}; polls given up {errs}")
+    out["xcc_of_workgroups_0_15"] = [int(v) for v in xcc[:16]]
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -610,6 +663,9 @@ def main() -> None:
     ap.add_argument("--timeline", action="store_true",
                     help="stage timelines of the persistent decode kernels from the diagnostic library "
                          "(python rwkv-tl_amd/build_hip.py --timeline first; one different JSON line)")
+    ap.add_argument("--hops", action="store_true",
+                    help="hand-off latency between two workgroups on different / the same XCD, from the "
+                         "diagnostic library (python rwkv-tl_amd/build_hip.py --timeline first; one JSON line)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two rocprofv3 --pmc csv runs and exit (no GPU)")
     args = ap.parse_args()
@@ -628,6 +684,9 @@ def main() -> None:
         return
     if args.timeline:
         print(json.dumps(bench_timeline()), flush=True)
+        return
+    if args.hops:
+        print(json.dumps(bench_hops()), flush=True)
         return
     if args.configs:
         print(json.dumps(bench_configs()), flush=True)
