@@ -203,6 +203,31 @@ def test_gemm_matches_fp32(M, N, Kd, epi, cuda):
         torch.testing.assert_close(out, ref.half().float(), rtol=2e-3, atol=2e-3)
 
 
+@pytest.mark.parametrize("M,N,Kd", [(2048, 8192, 1024), (4096, 2048, 2048), (2100, 3900, 128)])
+@pytest.mark.parametrize("epi", ["f32", "f16", "relu2", "add"])
+def test_gemm_bf16_large_m_matches_fp32(M, N, Kd, epi, cuda):
+    """bfloat16 operands on the large-M path (hipBLASLt for the plain
+    epilogues, the large-M kernel for relu2): the products of bf16 values are
+    exact in fp32, so f32 outputs must match the fp32 product to fp32
+    accumulation accuracy and 16-bit outputs its bfloat16 rounding."""
+    g = torch.Generator().manual_seed(M * 5 + N + Kd)
+    A = torch.randn(M, Kd, generator=g).bfloat16()
+    W = (torch.randn(N, Kd, generator=g) * 0.05).bfloat16()
+    ref = A.float() @ W.float().T
+    if epi == "add":
+        base = torch.randn(M, N, generator=g)
+        out = K.gemm(A.to(cuda), W.to(cuda), "add", out=base.clone().to(cuda)).cpu()
+        torch.testing.assert_close(out, base + ref, rtol=1e-4, atol=1e-4)
+        return
+    out = K.gemm(A.to(cuda), W.to(cuda), epi).cpu().float()
+    if epi == "relu2":
+        ref = ref.clamp_min(0) ** 2
+    if epi == "f32":
+        torch.testing.assert_close(out, ref, rtol=1e-4, atol=1e-4)
+    else:
+        torch.testing.assert_close(out, ref.bfloat16().float(), rtol=8e-3, atol=8e-3)
+
+
 @pytest.mark.parametrize(
     "M,N,Kd",
     [(1, 64, 256), (5, 100, 40), (8, 300, 1024), (12, 1024, 4096), (16, 1024, 1024), (24, 4096, 1024),
