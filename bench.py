@@ -595,6 +595,43 @@ def bench_timeline() -> dict:
     return out
 
 
+def bench_gemm_large(calls: int = 20) -> dict:
+    """The large-M GEMM shapes of the 1.5B-shaped prefill (M = B*T = 4096 or
+    2048), f16 operands, through the C ABI (kernels.gemm): the plain 16-bit
+    epilogue (hipBLASLt) and the relu^2 epilogue (the library's large-M
+    kernel), HIP events over `calls` calls after warm-up."""
+    import torch
+
+    from rwkv_tl_amd import kernels as K
+
+    dev = torch.device("cuda:0")
+    peak = MFMA_F16_PEAK_TFLOPS * 1e12
+    out = {"mode": "gemm_large", "unit": "us per call", "peak_tflops": MFMA_F16_PEAK_TFLOPS, "shapes": {}}
+    for M, N, Kd in ((4096, 8192, 2048), (4096, 2048, 8192), (4096, 6400, 2048), (2048, 8192, 2048)):
+        g = torch.Generator(device="cpu").manual_seed(M + N + Kd)
+        A = (torch.randn(M, Kd, generator=g) * 0.5).half().to(dev)
+        W = (torch.randn(N, Kd, generator=g) * 0.02).half().to(dev)
+        row = {}
+        for epi in ("f16", "relu2"):
+            for _ in range(3):
+                K.gemm(A, W, epi)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(calls):
+                K.gemm(A, W, epi)
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) / calls * 1000
+            frac = 2.0 * M * N * Kd / (us * 1e-6) / peak
+            row[epi] = {"us": round(us, 1), "mfma_frac": round(frac, 3)}
+        out["shapes"][f"{M}x{N}x{Kd}"] = row
+        log(f"{M}x{N}x{Kd}: f16 {row['f16']['us']} us ({row['f16']['mfma_frac']}), "
+            f"relu2 {row['relu2']['us']} us ({row['relu2']['mfma_frac']})")
+        del A, W
+    return out
+
+
 def bench_hops(rounds: int = 2008) -> dict:
     """One-way latency of the persistent kernels' hand-off word (device-scope
     store, device-scope poll) between two workgroups on different XCDs and on
@@ -663,6 +700,8 @@ def main() -> None:
     ap.add_argument("--timeline", action="store_true",
                     help="stage timelines of the persistent decode kernels from the diagnostic library "
                          "(python rwkv-tl_amd/build_hip.py --timeline first; one different JSON line)")
+    ap.add_argument("--gemm-large", action="store_true",
+                    help="time the large-M GEMM shapes of the 1.5B prefill (hipBLASLt vs the relu^2 kernel)")
     ap.add_argument("--hops", action="store_true",
                     help="hand-off latency between two workgroups on different / the same XCD, from the "
                          "diagnostic library (python rwkv-tl_amd/build_hip.py --timeline first; one JSON line)")
@@ -687,6 +726,9 @@ def main() -> None:
         return
     if args.hops:
         print(json.dumps(bench_hops()), flush=True)
+        return
+    if args.gemm_large:
+        print(json.dumps(bench_gemm_large()), flush=True)
         return
     if args.configs:
         print(json.dumps(bench_configs()), flush=True)
