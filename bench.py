@@ -58,6 +58,9 @@ the median and latest workgroup at each point) and one JSON line.
 ``python bench.py --hops`` (same library) times the hand-off word alone: pairs
 of workgroups on different XCDs or on the same XCD exchange device-scope
 tagged words, and the line gives the one-way latency per hop.
+``python bench.py --gemm-large`` times the large-M GEMM shapes of the 1.5B
+prefill through the C ABI: the plain 16-bit epilogue (hipBLASLt) and relu^2
+(the library's large-M kernel), with their fractions of the MFMA peak.
 
 ``python bench.py --configs`` prints one more JSON line with the survey's
 other measurement configurations, each timed with HIP events after warm-up:
