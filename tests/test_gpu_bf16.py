@@ -143,6 +143,35 @@ def test_bf16_multi_launch_decode_matches_persistent(cuda):
     _check_state(Sb, s32, DEC_STATE, "kernels state vs ref32")
 
 
+@pytest.mark.slow
+def test_bf16_large_m_prefill_matches_oracle(cuda):
+    """A bf16 prefill long enough for the large-M GEMM path (0.4B, 2 x 1024 =
+    2048 rows: hipBLASLt for the plain GEMMs, the large-M kernel for relu2,
+    operands rounded to bf16): row 0's wkv state after the prefill against
+    ref32's prefill of that sequence, within 4e-2 relative (the float16
+    large-M bar of 5e-3 scaled by bf16's 2^3 coarser rounding), and the next
+    decode's logits against the reference's own bf16 semantics with its
+    criterion."""
+    print("bf16 large-M prefill 0.4b 2x1024", flush=True)
+    st = setup_for("0.4b", cuda)
+    assert not st.model.f32_activations(2, 1024)
+    g = torch.Generator().manual_seed(1024)
+    prompt = torch.randint(0, st.V, (2, 1024), generator=g)
+    nxt = torch.randint(0, st.V, (1, 2), generator=g)
+    S = st.model.new_state(batch=2)
+    st.model.prefill(prompt.to(cuda), S)
+    s32 = R.new_state(st.w.L, st.w.C, dtype=BF)
+    R.prefill(st.ref32, prompt[0], s32)
+    for i in range(st.w.L):
+        r = _rel(S.tmix[i]["rnn"][0].cpu(), s32[0][i]["rnn"])
+        assert r < 4e-2, f"layer {i}: 2x1024 bf16 prefill row 0 vs ref32: {r:.2e}"
+    lg, _ = st.model.decode(nxt[0].to(cuda), S)
+    sbf = R.new_state(st.w.L, st.w.C, dtype=BF)
+    R.prefill(st.refbf, prompt[0], sbf)
+    lbf, _ = R.decode(st.refbf, nxt[0, :1], sbf)
+    _check_ref_semantics(lg[0], lbf, "0.4b 2x1024 bf16 prefill + decode row 0 vs refbf")
+
+
 @pytest.mark.parametrize("shape,B,T", [("tiny", 1, 40), ("0.1b", 2, 33), ("0.4b", 1, 128)])
 def test_bf16_prefill_then_decode_matches_oracle(shape, B, T, cuda):
     print(f"bf16 prefill parity {shape} {B}x{T}", flush=True)
