@@ -601,8 +601,9 @@ def bench_timeline() -> dict:
 def bench_gemm_large(calls: int = 20) -> dict:
     """The large-M GEMM shapes of the 1.5B-shaped prefill (M = B*T = 4096 or
     2048), f16 operands, through the C ABI (kernels.gemm): the plain 16-bit
-    epilogue (hipBLASLt) and the relu^2 epilogue (the library's large-M
-    kernel), HIP events over `calls` calls after warm-up."""
+    epilogue and the relu^2 epilogue (both hipBLASLt's half product; relu^2
+    adds the in-place squaring pass), HIP events over `calls` calls after
+    warm-up."""
     import torch
 
     from rwkv_tl_amd import kernels as K

@@ -5,10 +5,17 @@
 // ~0.4-0.5 of the dense f16 peak where this library's own large-M kernel
 // (gemm.hip, gemm_big_tile) reaches ~0.2-0.3: with 16-bit operands and a plain
 // epilogue -- store f32, store 16-bit, or add into an f32 output -- such a
-// problem is a plain library GEMM, so it goes to hipBLASLt. Everything else
-// (f32 activations, relu^2 / tanh / sigmoid epilogues, the small-M shapes of
-// decode and short prefills) stays on the hand-written kernels, and so does
-// any problem hipBLASLt returns no algorithm for.
+// problem is a plain library GEMM, so it goes to hipBLASLt. The FFN key's
+// relu^2 into half goes there too, as a half product followed by an in-place
+// pass that stores relu(y)^2 (relusq_half_kernel): the product is rounded to
+// half before it is squared -- the arithmetic of the reference's own fp16 path
+// (relu(x @ W^T) ** 2 on a half product), within 4 units of half roundoff
+// (2^-9 relative) of the singly rounded value. In bfloat16 the same double
+// rounding costs up to 2^-6 relative (1.4 % measured at 2048 x 8192 x 1024),
+// so bf16 relu^2 keeps the large-M kernel's single rounding. Everything else
+// (f32 activations, tanh / sigmoid epilogues, the small-M shapes of decode and
+// short prefills) stays on the hand-written kernels, and so does any problem
+// hipBLASLt returns no algorithm for.
 //
 // Mapping: hipBLASLt is column-major, so Y[M, N] = A[M, K] W[N, K]^T (row
 // major) is computed as D = op(W') op(A') with W' = W seen as a K x N
@@ -105,22 +112,72 @@ const LtPlan *lt_plan(const LtKey &k, hipStream_t st) {
   return p.ok ? &d.plans.back() : nullptr;
 }
 
+// y <- relu(y)^2 in place on M rows of N half values (row stride ldy): one
+// workgroup per row at a time, eight values per 16-byte access when VEC (N and
+// ldy multiples of 8, Y 16-byte aligned), each thread's accesses of a row
+// issued together (up to 4 at a time). The square of a half value is exact in
+// f32, so each value is rounded once, to half, after the square.
+template <bool VEC>
+__global__ __launch_bounds__(256) void relusq_half_kernel(uint16_t *Y, int64_t ldy, int N, int M) {
+  auto sq = [](uint16_t u) -> uint16_t {
+    const float v = fmaxf(h2f(u), 0.f);
+    return f2h(v * v);
+  };
+  auto sq2 = [&](unsigned w) -> unsigned {
+    return (unsigned)sq((uint16_t)(w & 0xffffu)) | ((unsigned)sq((uint16_t)(w >> 16)) << 16);
+  };
+  constexpr int kStep = 8 * 256;  // halves per workgroup access round
+  for (int r = blockIdx.x; r < M; r += gridDim.x) {
+    uint16_t *row = Y + (int64_t)r * ldy;
+    if (VEC) {
+      for (int c0 = 8 * threadIdx.x; c0 < N; c0 += 4 * kStep) {
+        uint4 v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (c0 + j * kStep < N) v[j] = *reinterpret_cast<const uint4 *>(row + c0 + j * kStep);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (c0 + j * kStep < N)
+            *reinterpret_cast<uint4 *>(row + c0 + j * kStep) =
+                make_uint4(sq2(v[j].x), sq2(v[j].y), sq2(v[j].z), sq2(v[j].w));
+      }
+    } else {
+      for (int c = threadIdx.x; c < N; c += 256) row[c] = sq(row[c]);
+    }
+  }
+}
+
+bool launch_relusq_half(const GemmProb &p, int M, hipStream_t st) {
+  const bool vec = p.N % 8 == 0 && p.ldy % 8 == 0 && reinterpret_cast<uintptr_t>(p.Y) % 16 == 0;
+  const int grid = M < 4096 ? M : 4096;
+  uint16_t *y = static_cast<uint16_t *>(p.Y);
+  if (vec) relusq_half_kernel<true><<<grid, 256, 0, st>>>(y, p.ldy, p.N, M);
+  else relusq_half_kernel<false><<<grid, 256, 0, st>>>(y, p.ldy, p.N, M);
+  return hipGetLastError() == hipSuccess;
+}
+
 }  // namespace
 
 bool lt_eligible(const GemmProb &p) {
-  return !p.a32 && (p.epi == GEPI_F32 || p.epi == GEPI_F16 || p.epi == GEPI_ADD_F32);
+  return !p.a32 && (p.epi == GEPI_F32 || p.epi == GEPI_F16 || p.epi == GEPI_ADD_F32 || (p.epi == GEPI_RELUSQ && !p.bf));
 }
 
 bool lt_gemm(const GemmProb &p, int M, hipStream_t st) {
   if (!lt_eligible(p) || M <= 0) return false;
-  const LtKey k{M, p.N, p.K, p.epi, p.bf ? 1 : 0, p.lda, p.ldw, p.ldy};
+  // relu^2 (half) runs as the plain half product (same plan) and the in-place pass
+  const bool relusq = p.epi == GEPI_RELUSQ;
+  const LtKey k{M, p.N, p.K, relusq ? (int)GEPI_F16 : p.epi, p.bf ? 1 : 0, p.lda, p.ldw, p.ldy};
   const LtPlan *pl = lt_plan(k, st);
   if (!pl) return false;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return false;
   const float alpha = 1.f, beta = p.epi == GEPI_ADD_F32 ? 1.f : 0.f;
-  return hipblasLtMatmul(g_lt[dev].h, pl->desc, &alpha, p.W, pl->lw, p.A, pl->la, &beta, p.Y, pl->ly, p.Y, pl->ly,
-                         &pl->algo, nullptr, 0, st) == HIPBLAS_STATUS_SUCCESS;
+  if (hipblasLtMatmul(g_lt[dev].h, pl->desc, &alpha, p.W, pl->lw, p.A, pl->la, &beta, p.Y, pl->ly, p.Y, pl->ly,
+                      &pl->algo, nullptr, 0, st) != HIPBLAS_STATUS_SUCCESS)
+    return false;
+  // a pass that fails to launch leaves the plain product in Y: returning false
+  // has the caller's own kernel recompute the problem into Y
+  return !relusq || launch_relusq_half(p, M, st);
 }
 
 }  // namespace rwkv7

@@ -197,9 +197,10 @@ constexpr int kGemmCounters = 1024;
 int64_t gemm_ws_bytes(int M, int cus);
 int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, float *part, unsigned *ctr);
 // Large-M problems with 16-bit operands and a plain epilogue (f32, 16-bit or
-// add into f32) through hipBLASLt (gemm_lt.hip); lt_gemm returns false when it
-// did not run the problem (no algorithm, library unavailable), and the caller
-// then runs its own kernel.
+// add into f32), or relu^2 into half (a half product, then an in-place pass),
+// through hipBLASLt (gemm_lt.hip); lt_gemm returns false when it did
+// not run the problem (no algorithm, library unavailable), and the caller then
+// runs its own kernel.
 bool lt_eligible(const GemmProb &p);
 bool lt_gemm(const GemmProb &p, int M, hipStream_t st);
 

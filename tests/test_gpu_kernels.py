@@ -228,6 +228,67 @@ def test_gemm_bf16_large_m_matches_fp32(M, N, Kd, epi, cuda):
         torch.testing.assert_close(out, ref.bfloat16().float(), rtol=8e-3, atol=8e-3)
 
 
+@pytest.mark.parametrize("M,N,Kd", [(2048, 8192, 1024), (2100, 3900, 128)])
+def test_gemm_large_m_relu2_squares_the_half_product(M, N, Kd, cuda):
+    """On the large-M path half relu2 runs as hipBLASLt's half product
+    followed by an in-place pass (eight values per access where N allows, one
+    at a time otherwise: N = 3900): its output must equal, bit for bit,
+    relu(p)^2 rounded to half, where p is the same shape's "f16" output (the
+    same algorithm: the plan depends on the shape only) -- the rounding of the
+    reference's fp16 path, relu(x @ W^T) ** 2 on a half product."""
+    g = torch.Generator().manual_seed(M * 3 + N + Kd)
+    A = torch.randn(M, Kd, generator=g).half().to(cuda)
+    W = (torch.randn(N, Kd, generator=g) * 0.05).half().to(cuda)
+    p = K.gemm(A, W, "f16")
+    y = K.gemm(A, W, "relu2")
+    want = (p.float().clamp_min(0) ** 2).half()
+    assert torch.equal(y, want), f"{(y.float() - want.float()).abs().max().item():.3e}"
+
+
+@pytest.mark.parametrize("epi", ["relu2", "f32"])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_gemm_large_m_first_seen_under_capture(epi, dt, cuda):
+    """A large-M shape seen first inside a graph capture runs this library's
+    own large-M kernel (no hipBLASLt plan is built while the stream captures);
+    the same call made eagerly afterwards builds the plan and runs hipBLASLt
+    (bf16 relu2 stays on the own kernel). Every replay (each after eager work
+    that overwrites its output) and the eager call must match the fp32
+    product: f32 to fp32 accumulation accuracy, relu2 to the 16-bit format's
+    rounding. The shape is this test's own (N differs per case), so no
+    earlier call in the process has built its plan."""
+    M, Kd = 2304, 256
+    N = 4352 + (64 if dt == torch.bfloat16 else 0) + (128 if epi == "f32" else 0)
+    g = torch.Generator().manual_seed(N)
+    A = torch.randn(M, Kd, generator=g).to(dt)
+    W = (torch.randn(N, Kd, generator=g) * 0.05).to(dt)
+    ref = A.float() @ W.float().T
+    if epi == "relu2":
+        ref = ref.clamp_min(0) ** 2
+    A, W = A.to(cuda), W.to(cuda)
+    K.gemm(A[:8], W[:64], "f32")  # library loaded, device queried, outside the capture
+    torch.cuda.synchronize()
+
+    def check(out, what):
+        out = out.cpu().float()
+        if epi == "f32":
+            torch.testing.assert_close(out, ref, rtol=1e-4, atol=1e-4, msg=what)
+        elif dt == torch.float16:
+            torch.testing.assert_close(out, ref.half().float(), rtol=2e-3, atol=2e-3, msg=what)
+        else:
+            torch.testing.assert_close(out, ref.bfloat16().float(), rtol=8e-3, atol=8e-3, msg=what)
+
+    s = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        out = K.gemm(A, W, epi)
+    check(K.gemm(A, W, epi), "eager after the capture")
+    for i in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        check(out, f"replay {i}")
+
+
 @pytest.mark.parametrize(
     "M,N,Kd",
     [(1, 64, 256), (5, 100, 40), (8, 300, 1024), (12, 1024, 4096), (16, 1024, 1024), (24, 4096, 1024),
