@@ -479,9 +479,11 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmGroup g) {
 // ---------------------------------------------------------------------------
 // Large-M path (long prefills, see big_fits): the product is MFMA-bound, so
 // the workgroup tile is large enough that each byte staged through LDS feeds
-// many products. Problems with a plain epilogue run in hipBLASLt instead when
-// it has an algorithm for them (gemm_lt.hip: ~1.7x faster on these shapes);
-// this kernel keeps the relu^2 / tanh / sigmoid epilogues. BM x BN tile (256 x 256, or 128 x 128 where the larger tiles
+// many products. Problems with a plain epilogue (and half relu^2) run in
+// hipBLASLt instead when it has an algorithm for them (gemm_lt.hip: ~1.7x
+// faster on these shapes); this kernel keeps the bf16 relu^2 and the tanh /
+// sigmoid epilogues, and the narrow problems (N < 256: the LoRA first steps)
+// of a group whose wide problems take this path. BM x BN tile (256 x 256, or 128 x 128 where the larger tiles
 // leave CUs idle), 8 waves as 2 (rows) x 4 (columns), each wave a (BM/2) x
 // (BN/4) block of 16x16 accumulators; K in stages of 32.
 //
@@ -703,6 +705,14 @@ static bool big_fits(const GemmProb &p, int M, int cus) {
   return !p.a32 && p.K % kBigBK == 0 && p.N >= 256 &&
          (int64_t)((M + 127) / 128) * ((p.N + 127) / 128) >= 2 * cus && big_w_addressable(p) &&
          big_rows_per_launch(p.lda) >= 256;
+}
+
+// Bytes per output element of an epilogue.
+static int epi_out_bytes(int epi) {
+  return epi == GEPI_F32 || epi == GEPI_ADD_F32 || epi == GEPI_RELUSQ_F32 || epi == GEPI_TANH_F32 ||
+                 epi == GEPI_SIGM_F32
+             ? 4
+             : 2;
 }
 
 int gemm_big_min_rows(int N) {
@@ -1045,6 +1055,28 @@ int64_t gemm_ws_bytes(int M, int cus) {
   return tiled > skinny ? tiled : skinny;
 }
 
+// Problems of the large-M path over row blocks whose A extents stay below
+// 2^31 bytes (big_rows_per_launch), A and Y rebased per block. With lt, each
+// problem goes to hipBLASLt first (plain epilogues, half relu^2); the others,
+// and any it declines, run in one launch of the large-M kernel per block.
+static int launch_large_m(const GemmProb *probs, int n, int M, int cus, hipStream_t st, bool lt) {
+  int rows = M;
+  for (int i = 0; i < n; ++i) rows = min(rows, big_rows_per_launch(probs[i].lda));
+  for (int r0 = 0; r0 < M; r0 += rows) {
+    GemmProb blk[kMaxProb];
+    int nk = 0;
+    const int mr = min(rows, M - r0);
+    for (int i = 0; i < n; ++i) {
+      GemmProb b = probs[i];
+      b.A = probs[i].A + (int64_t)r0 * probs[i].lda;
+      b.Y = static_cast<char *>(probs[i].Y) + (int64_t)r0 * probs[i].ldy * epi_out_bytes(probs[i].epi);
+      if (!lt || !lt_gemm(b, mr, st)) blk[nk++] = b;
+    }
+    if (nk > 0) RWKV7_TRY_GEMM(launch_big(blk, nk, mr, cus, st));
+  }
+  return RWKV7_OK;
+}
+
 // Checks shapes and launches one group. Every problem needs K % 8 == 0, K >= 8
 // and 16-byte aligned rows (lda, ldw multiples of 8). part/ctr: split-K
 // workspace (gemm_ws_bytes(M) bytes and kGemmCounters zeroed counters); with
@@ -1079,24 +1111,16 @@ int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, f
       else rest[nr++] = probs[i];
     }
     if (nb > 0) {
-      // row blocks whose A extents stay below 2^31 bytes (big_rows_per_launch)
-      int rows = M;
-      for (int i = 0; i < nb; ++i) rows = min(rows, big_rows_per_launch(big[i].lda));
-      for (int r0 = 0; r0 < M; r0 += rows) {
-        GemmProb blk[kMaxProb];
-        int nk = 0;
-        const int mr = min(rows, M - r0);
-        for (int i = 0; i < nb; ++i) {
-          GemmProb b = big[i];
-          const int ysz = big[i].epi == GEPI_F32 || big[i].epi == GEPI_ADD_F32 ? 4 : 2;
-          b.A = big[i].A + (int64_t)r0 * big[i].lda;
-          b.Y = static_cast<char *>(big[i].Y) + (int64_t)r0 * big[i].ldy * ysz;
-          // plain GEMMs go to hipBLASLt; the others, and any it declines, here
-          if (!lt_gemm(b, mr, st)) blk[nk++] = b;
-        }
-        if (nk > 0) RWKV7_TRY_GEMM(launch_big(blk, nk, mr, cus, st));
-      }
+      RWKV7_TRY_GEMM(launch_large_m(big, nb, M, cus, st, true));
       if (nr == 0) return RWKV7_OK;
+      // The group's narrow problems at the same M (the LoRA first steps beside
+      // r/k/v: N = 64..256, too few tiles for big_fits alone) join the
+      // large-M kernel as well, 128 x 128 tiles in one launch (measured on the
+      // 1.5B 4 x 1024 prefill: 21.4 -> 20.6 ms against the tiled kernels).
+      bool fit = true;
+      for (int i = 0; i < nr; ++i)
+        fit = fit && rest[i].K % kBigBK == 0 && big_w_addressable(rest[i]) && big_rows_per_launch(rest[i].lda) >= 256;
+      if (fit) return launch_large_m(rest, nr, M, cus, st, false);
       probs = rest;
       nprob = nr;
     }
