@@ -245,6 +245,12 @@ struct GateStager {
     g_vf = p.layer0 ? g_v : ld4_as_f(p.vfirst + o);
   }
   RWKV7_DEV void commit(int c0, StageBuf<CH> &dst) {
+    commit_to(c0, [&](int i, int t, int qq, const float4 &x) { dst[i][t][qq] = x; });
+  }
+  // The six staged vectors of this thread's token and float4 go to
+  // sink(vector, token, float4 index, value).
+  template <class Sink>
+  RWKV7_DEV void commit_to(int c0, Sink &&sink) {
     const int tt = c0 + st_tok;
     if (lds_d) {
       const int r = st_tok < CH ? st_tok : CH - 1;
@@ -278,12 +284,12 @@ struct GateStager {
       b[e] = -a[e] * ag[e];
     }
     if (!stager) return;
-    dst[0][st_tok][q] = make_float4(w[0], w[1], w[2], w[3]);
-    dst[1][st_tok][q] = make_float4(a[0], a[1], a[2], a[3]);
-    dst[2][st_tok][q] = make_float4(b[0], b[1], b[2], b[3]);
-    dst[3][st_tok][q] = make_float4(kn[0], kn[1], kn[2], kn[3]);
-    dst[4][st_tok][q] = g_r;
-    dst[5][st_tok][q] = make_float4(v[0], v[1], v[2], v[3]);
+    sink(0, st_tok, q, make_float4(w[0], w[1], w[2], w[3]));
+    sink(1, st_tok, q, make_float4(a[0], a[1], a[2], a[3]));
+    sink(2, st_tok, q, make_float4(b[0], b[1], b[2], b[3]));
+    sink(3, st_tok, q, make_float4(kn[0], kn[1], kn[2], kn[3]));
+    sink(4, st_tok, q, g_r);
+    sink(5, st_tok, q, make_float4(v[0], v[1], v[2], v[3]));
     // this workgroup's 16 channels of the values GroupNorm needs
     if (tt < t1 && (quarter < 0 || (q >> 2) == quarter)) {
       const int64_t o = base + (int64_t)tt * C + 4 * q;
@@ -328,10 +334,14 @@ struct RawStager {
     g[4] = ld4_as_f(p.r + o);
     g[5] = ld4_as_f(p.v + o);
   }
-  RWKV7_DEV void commit(int, StageBuf<CH> &dst) {
+  RWKV7_DEV void commit(int c0, StageBuf<CH> &dst) {
+    commit_to(c0, [&](int i, int t, int qq, const float4 &x) { dst[i][t][qq] = x; });
+  }
+  template <class Sink>
+  RWKV7_DEV void commit_to(int, Sink &&sink) {
     if (!stager) return;
 #pragma unroll
-    for (int i = 0; i < 6; ++i) dst[i][st_tok][q] = g[i];
+    for (int i = 0; i < 6; ++i) sink(i, st_tok, q, g[i]);
   }
   RWKV7_DEV void put_y(int64_t o, float y) { p.y[o] = from_f<TY>(y); }
   // state entering token tt: row `row`, key columns 4 lc .. 4 lc + 3
@@ -885,20 +895,25 @@ RWKV7_DEV void lora2_chunk(const PrefillScanArgs &p, St &st, int h, int bi, int 
   lora2_compute<BF, F32>(p, g, h, bi, T, t0, t1, s_d);
 }
 
-template <class St>
+// L2: the model path with the LoRA second steps formed here (GateStager and
+// p.l1 set); a separate instance, whose registers those products no longer
+// hold, keeps three workgroups per CU for the other cases.
+template <class St, bool L2>
 __global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(typename St::Args p, float *rec, int T, int H) {
-  __shared__ StageBuf<kCk> s_stage;  // the stager's output; then AkaV, G1, U, G2, Y0
-  __shared__ float s_x[6][kCk][kPad];  // w, a (a~), b (b / P), k (k / P), r (r~), v
-  __shared__ float s_bh[kCk][kPad], s_kh[kCk][kPad];
-  __shared__ float s_p[kCk][kPad];        // prefix products P_t = D(-1, t]
+  // 43 KB of LDS, so that three workgroups share a CU (the 1.5B-shaped
+  // 4 x 1024 prefill runs 8192 of them): the stager writes its padded rows
+  // straight into s_x, and the later 16 x 64 results take the rows that are
+  // dead by then -- AkaV and then G2 the prefix products', G1 w's, U b's and
+  // Y0 k's (each phase below ends with a barrier before the next reuses a row)
+  __shared__ float s_x[6][kCk][kPad];     // w, a (a~), b (b / P), k (k / P), r (r~), v
+  __shared__ float s_bkp[3][kCk][kPad];   // b^, k^, prefix products P_t = D(-1, t]
   __shared__ float s_m[4][kCk][kCk + 1];  // Aba, Aka, Bbr, Bkr
   __shared__ float s_t[kCk][kCk + 1];
   __shared__ float s_gam[kN];
   typedef float Row[kPad];
-  Row *s_akav = reinterpret_cast<Row *>(&s_stage[0][0][0]);
-  Row *s_g1 = s_akav + kCk, *s_u = s_akav + 2 * kCk, *s_g2 = s_akav + 3 * kCk, *s_y0 = s_akav + 4 * kCk;
-  static_assert(sizeof(StageBuf<kCk>) >= 5 * kCk * kPad * sizeof(float), "staging buffer reuse");
-  static_assert(sizeof(s_x) >= 3 * kCk * kN * sizeof(float), "LoRA steps staged in s_x");
+  Row *s_bh = s_bkp[0], *s_kh = s_bkp[1], *s_p = s_bkp[2];
+  Row *s_akav = s_bkp[2], *s_g2 = s_bkp[2], *s_g1 = s_x[0], *s_u = s_x[2], *s_y0 = s_x[3];
+  static_assert(sizeof(s_bkp) >= 3 * kCk * kN * sizeof(float), "LoRA steps staged in s_bkp");
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int row = lane & 15, kq = lane >> 4, col = 16 * wv + row;
@@ -907,9 +922,9 @@ __global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(typename St::Args 
   const int t0 = c * kCk, t1 = min(T, t0 + kCk), Tl = t1 - t0;
   St st(p, h, -1, (int64_t)bi * T * C + (int64_t)h * kN, t1);
   bool fetched = false;
-  if constexpr (std::is_same<St, GateStager<kCk>>::value) {
-    if (p.l1) {
-      float *s_d = &s_x[0][0][0];  // free until the staged chunk is copied there
+  if constexpr (L2 && std::is_same<St, GateStager<kCk>>::value) {
+    {
+      float *s_d = &s_bkp[0][0][0];  // free until the products below
       if (p.bf) {
         if (p.l1_f32) lora2_chunk<true, true>(p, st, h, bi, T, t0, t1, s_d);
         else lora2_chunk<true, false>(p, st, h, bi, T, t0, t1, s_d);
@@ -924,20 +939,14 @@ __global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(typename St::Args 
     }
   }
   if (!fetched) st.fetch(t0);
-  st.commit(t0, s_stage);
-  __syncthreads();
-  {  // to padded f32 rows; tokens past the end become identity steps
-    const int tt = tid >> 4, q4 = 4 * (tid & 15);
-#pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      float4 x = s_stage[i][tt][tid & 15];
-      if (tt >= Tl) x = i == 0 ? make_float4(1.f, 1.f, 1.f, 1.f) : make_float4(0.f, 0.f, 0.f, 0.f);
-      s_x[i][tt][q4] = x.x;
-      s_x[i][tt][q4 + 1] = x.y;
-      s_x[i][tt][q4 + 2] = x.z;
-      s_x[i][tt][q4 + 3] = x.w;
-    }
-  }
+  // padded f32 rows; tokens past the end become identity steps
+  st.commit_to(t0, [&](int i, int tt, int qq, float4 x) {
+    if (tt >= Tl) x = i == 0 ? make_float4(1.f, 1.f, 1.f, 1.f) : make_float4(0.f, 0.f, 0.f, 0.f);
+    s_x[i][tt][4 * qq] = x.x;
+    s_x[i][tt][4 * qq + 1] = x.y;
+    s_x[i][tt][4 * qq + 2] = x.z;
+    s_x[i][tt][4 * qq + 3] = x.w;
+  });
   __syncthreads();
   bool ok = true;
   if (tid < kN) {  // wave 0: prefix products P_t, and whether they stay in range
@@ -1260,7 +1269,10 @@ static int launch_chunked(const typename St::Args &p, float *S, TY *y, float *re
                           hipStream_t st) {
   if (!rec) return RWKV7_EWORKSPACE;
   const int nc = (T + kCk - 1) / kCk;
-  wkv7_chunk_prep_kernel<St><<<dim3(nc, H, B), 256, 0, st>>>(p, rec, T, H);
+  bool l2 = false;
+  if constexpr (std::is_same<St, GateStager<kCk>>::value) l2 = p.l1 != nullptr;
+  if (l2) wkv7_chunk_prep_kernel<St, true><<<dim3(nc, H, B), 256, 0, st>>>(p, rec, T, H);
+  else wkv7_chunk_prep_kernel<St, false><<<dim3(nc, H, B), 256, 0, st>>>(p, rec, T, H);
   RWKV7_CHECK_LAUNCH();
   // two value quarters per workgroup (each record fetched once for both)
   // where that still leaves a workgroup per CU
