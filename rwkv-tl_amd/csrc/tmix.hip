@@ -1543,6 +1543,129 @@ __global__ __launch_bounds__(256) void ln_shift_kernel(LnShiftArgs a, int R, int
   }
 }
 
+// The many-rows regime of ln_shift_kernel with each thread on NP consecutive
+// columns (NP a multiple of 4), so that every load and store is a vector
+// access: 16 bytes per lane for f32 rows and vectors, 8 or 16 for the 16-bit
+// mix rows and shift states (ln_shift_kernel's column-strided layout stores
+// the six 16-bit mix rows two bytes per lane, 6 NP stores per thread and row).
+template <int NP>
+__global__ __launch_bounds__(256) void ln_shift_vec_kernel(LnShiftArgs a, int R) {
+  static_assert(NP % 4 == 0, "whole float4 pieces per thread");
+  constexpr int NV = NP / 4;
+  __shared__ float red[2][3][4];
+  const int C = a.C, tid = threadIdx.x, T = a.T, c0 = NP * tid;
+  const int m0 = blockIdx.x * R, m1 = min(a.M, m0 + R);
+  auto ld = [&](const float *row, float (&d)[NP]) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const float4 q = reinterpret_cast<const float4 *>(row + c0)[v];
+      d[4 * v] = q.x;
+      d[4 * v + 1] = q.y;
+      d[4 * v + 2] = q.z;
+      d[4 * v + 3] = q.w;
+    }
+  };
+  float xc[NP], xp[NP], xl[NP];
+  uint32_t st[NP / 2];  // the old shift state, two 16-bit values per word
+  auto load_row = [&](int m, bool have_prev) {
+    const int t = m % T, b = m / T;
+    ld(a.x0 + (int64_t)m * C, xc);
+#pragma unroll
+    for (int i = 0; i < NP; ++i) xp[i] = xl[i] = 0.f;
+    if (t > 0 && !have_prev) ld(a.x0 + (int64_t)(m - 1) * C, xp);
+    if (t == 0 && T > 1) ld(a.x0 + (int64_t)(m + T - 1) * C, xl);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      uint2 u = make_uint2(0u, 0u);
+      if (t == 0) u = reinterpret_cast<const uint2 *>(a.shift + (int64_t)b * C + c0)[v];
+      st[2 * v] = u.x;
+      st[2 * v + 1] = u.y;
+    }
+  };
+  load_row(m0, false);
+  float lw[NP], lb[NP], mu[6][NP];
+  ld(a.ln_w, lw);
+  ld(a.ln_b, lb);
+#pragma unroll
+  for (int j = 0; j < 6; ++j) {
+    if (j < a.n_mix) ld(a.mu + (int64_t)j * C, mu[j]);
+    else
+#pragma unroll
+      for (int i = 0; i < NP; ++i) mu[j][i] = 0.f;
+  }
+  const float invC = 1.f / (float)C;
+  float prev[NP];  // LN of the row before m, once computed
+  bool have_prev = false;
+  for (int m = m0; m < m1; ++m) {
+    const int t = m % T, b = m / T;
+    const bool need_p = t > 0 && !have_prev, need_l = t == 0 && T > 1;
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      s0 += xc[i];
+      s1 += xp[i];
+      s2 += xl[i];
+    }
+    block_sum3(s0, s1, s2, red[0]);
+    const float mc = s0 * invC, mp = s1 * invC, ml = s2 * invC;
+    float q0 = 0.f, q1 = 0.f, q2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      q0 += (xc[i] - mc) * (xc[i] - mc);
+      q1 += (xp[i] - mp) * (xp[i] - mp);
+      q2 += (xl[i] - ml) * (xl[i] - ml);
+    }
+    block_sum3(q0, q1, q2, red[1]);
+    const float rc0 = rsqrtf(q0 * invC + kLnEps), rp0 = rsqrtf(q1 * invC + kLnEps), rl0 = rsqrtf(q2 * invC + kLnEps);
+    float xn[NP], pv[NP], ns[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const uint16_t sv = (uint16_t)(st[i >> 1] >> (16 * (i & 1)));
+      xn[i] = (xc[i] - mc) * rc0 * lw[i] + lb[i];
+      pv[i] = t == 0 ? u16_to_f(sv, a.bf) : need_p ? (xp[i] - mp) * rp0 * lw[i] + lb[i] : prev[i];
+      ns[i] = need_l ? (xl[i] - ml) * rl0 * lw[i] + lb[i] : xn[i];
+    }
+    if (m + 1 < m1) load_row(m + 1, true);
+#pragma unroll
+    for (int j = 0; j < 6; ++j) {
+      if (j >= a.n_mix) continue;
+      float o[NP];
+#pragma unroll
+      for (int i = 0; i < NP; ++i) o[i] = xn[i] + mu[j][i] * (pv[i] - xn[i]);
+      const int64_t base = ((int64_t)j * a.M + m) * C + c0;
+      if (a.out_f32) {
+        float4 *dst = reinterpret_cast<float4 *>(static_cast<float *>(a.out) + base);
+#pragma unroll
+        for (int v = 0; v < NV; ++v) dst[v] = make_float4(o[4 * v], o[4 * v + 1], o[4 * v + 2], o[4 * v + 3]);
+      } else {
+        uint32_t w[NP / 2];
+#pragma unroll
+        for (int i = 0; i < NP / 2; ++i)
+          w[i] = (uint32_t)f_to_u16(o[2 * i], a.bf) | ((uint32_t)f_to_u16(o[2 * i + 1], a.bf) << 16);
+        uint16_t *dst = static_cast<uint16_t *>(a.out) + base;
+        if constexpr (NP % 8 == 0) {
+#pragma unroll
+          for (int v = 0; v < NP / 8; ++v)
+            reinterpret_cast<uint4 *>(dst)[v] = make_uint4(w[4 * v], w[4 * v + 1], w[4 * v + 2], w[4 * v + 3]);
+        } else {
+#pragma unroll
+          for (int v = 0; v < NV; ++v) reinterpret_cast<uint2 *>(dst)[v] = make_uint2(w[2 * v], w[2 * v + 1]);
+        }
+      }
+    }
+    if (t == 0) {
+      uint2 *sh = reinterpret_cast<uint2 *>(a.shift + (int64_t)b * C + c0);
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+        sh[v] = make_uint2((uint32_t)f_to_u16(ns[4 * v], a.bf) | ((uint32_t)f_to_u16(ns[4 * v + 1], a.bf) << 16),
+                           (uint32_t)f_to_u16(ns[4 * v + 2], a.bf) | ((uint32_t)f_to_u16(ns[4 * v + 3], a.bf) << 16));
+    }
+#pragma unroll
+    for (int i = 0; i < NP; ++i) prev[i] = xn[i];
+    have_prev = true;
+  }
+}
+
 int launch_ln_shift(const LnShiftArgs &a, hipStream_t st) {
   if (a.C % 256 || a.C > 256 * kMaxCPer || a.n_mix < 1 || a.n_mix > 6 || a.M <= 0 || a.T <= 0) return RWKV7_ESHAPE;
   const int np = a.C / 256;
@@ -1558,6 +1681,16 @@ int launch_ln_shift(const LnShiftArgs &a, hipStream_t st) {
     while (ncs * 2 <= np && np % (ncs * 2) == 0 && (int64_t)a.M * ncs < want) ncs *= 2;
   const bool row_kernel = R == 1 && np <= 4;
   const dim3 grid((a.M + R - 1) / R, row_kernel ? 1 : ncs);
+  if (R > 1 && np % 4 == 0) {
+    switch (np) {
+      case 4: ln_shift_vec_kernel<4><<<grid, 256, 0, st>>>(a, R); break;
+      case 8: ln_shift_vec_kernel<8><<<grid, 256, 0, st>>>(a, R); break;
+      case 12: ln_shift_vec_kernel<12><<<grid, 256, 0, st>>>(a, R); break;
+      default: ln_shift_vec_kernel<16><<<grid, 256, 0, st>>>(a, R); break;
+    }
+    RWKV7_CHECK_LAUNCH();
+    return RWKV7_OK;
+  }
   switch (np) {
 #define RWKV7_LNS_CASE(n)                                            \
   case n:                                                            \
