@@ -1681,13 +1681,11 @@ int launch_ln_shift(const LnShiftArgs &a, hipStream_t st) {
     while (ncs * 2 <= np && np % (ncs * 2) == 0 && (int64_t)a.M * ncs < want) ncs *= 2;
   const bool row_kernel = R == 1 && np <= 4;
   const dim3 grid((a.M + R - 1) / R, row_kernel ? 1 : ncs);
-  if (R > 1 && np % 4 == 0) {
-    switch (np) {
-      case 4: ln_shift_vec_kernel<4><<<grid, 256, 0, st>>>(a, R); break;
-      case 8: ln_shift_vec_kernel<8><<<grid, 256, 0, st>>>(a, R); break;
-      case 12: ln_shift_vec_kernel<12><<<grid, 256, 0, st>>>(a, R); break;
-      default: ln_shift_vec_kernel<16><<<grid, 256, 0, st>>>(a, R); break;
-    }
+  // the vector form at C = 1024 and 2048 (the 0.4B and 1.5B widths; at 4096
+  // its registers would leave one wave per SIMD)
+  if (R > 1 && (np == 4 || np == 8)) {
+    if (np == 4) ln_shift_vec_kernel<4><<<grid, 256, 0, st>>>(a, R);
+    else ln_shift_vec_kernel<8><<<grid, 256, 0, st>>>(a, R);
     RWKV7_CHECK_LAUNCH();
     return RWKV7_OK;
   }
