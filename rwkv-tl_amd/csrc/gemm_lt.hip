@@ -37,9 +37,11 @@ namespace {
 struct LtKey {
   int M, N, K, epi, bf;
   int64_t lda, ldw, ldy;
+  int batch;              // problems of one strided-batched call
+  int64_t sa, sw, sy;     // their strides, in elements of A, W and Y
   bool operator==(const LtKey &o) const {
     return M == o.M && N == o.N && K == o.K && epi == o.epi && bf == o.bf && lda == o.lda && ldw == o.ldw &&
-           ldy == o.ldy;
+           ldy == o.ldy && batch == o.batch && sa == o.sa && sw == o.sw && sy == o.sy;
   }
 };
 
@@ -93,6 +95,16 @@ const LtPlan *lt_plan(const LtKey &k, hipStream_t st) {
   ok = ok && hipblasLtMatrixLayoutCreate(&p.lw, t16, k.K, k.N, k.ldw) == HIPBLAS_STATUS_SUCCESS;
   ok = ok && hipblasLtMatrixLayoutCreate(&p.la, t16, k.K, k.M, k.lda) == HIPBLAS_STATUS_SUCCESS;
   ok = ok && hipblasLtMatrixLayoutCreate(&p.ly, ty, k.N, k.M, k.ldy) == HIPBLAS_STATUS_SUCCESS;
+  if (ok && k.batch > 1) {
+    const int32_t bc = k.batch;
+    const hipblasLtMatrixLayout_t lays[3] = {p.lw, p.la, p.ly};
+    const int64_t strides[3] = {k.sw, k.sa, k.sy};
+    for (int i = 0; i < 3 && ok; ++i)
+      ok = hipblasLtMatrixLayoutSetAttribute(lays[i], HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc)) ==
+               HIPBLAS_STATUS_SUCCESS &&
+           hipblasLtMatrixLayoutSetAttribute(lays[i], HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &strides[i],
+                                             sizeof(strides[i])) == HIPBLAS_STATUS_SUCCESS;
+  }
   if (ok) {
     hipblasLtMatmulPreference_t pref = nullptr;
     uint64_t ws = 0;
@@ -162,11 +174,14 @@ bool lt_eligible(const GemmProb &p) {
   return !p.a32 && (p.epi == GEPI_F32 || p.epi == GEPI_F16 || p.epi == GEPI_ADD_F32 || (p.epi == GEPI_RELUSQ && !p.bf));
 }
 
-bool lt_gemm(const GemmProb &p, int M, hipStream_t st) {
-  if (!lt_eligible(p) || M <= 0) return false;
+bool lt_gemm(const GemmProb &p, int M, hipStream_t st) { return lt_gemm_batched(p, 1, 0, 0, 0, M, st); }
+
+bool lt_gemm_batched(const GemmProb &p, int batch, int64_t sa, int64_t sw, int64_t sy, int M, hipStream_t st) {
+  if (!lt_eligible(p) || M <= 0 || batch < 1) return false;
   // relu^2 (half) runs as the plain half product (same plan) and the in-place pass
   const bool relusq = p.epi == GEPI_RELUSQ;
-  const LtKey k{M, p.N, p.K, relusq ? (int)GEPI_F16 : p.epi, p.bf ? 1 : 0, p.lda, p.ldw, p.ldy};
+  const LtKey k{M, p.N, p.K, relusq ? (int)GEPI_F16 : p.epi, p.bf ? 1 : 0, p.lda, p.ldw, p.ldy,
+                batch, batch > 1 ? sa : 0, batch > 1 ? sw : 0, batch > 1 ? sy : 0};
   const LtPlan *pl = lt_plan(k, st);
   if (!pl) return false;
   int dev = 0;
@@ -176,8 +191,13 @@ bool lt_gemm(const GemmProb &p, int M, hipStream_t st) {
                       &pl->algo, nullptr, 0, st) != HIPBLAS_STATUS_SUCCESS)
     return false;
   // a pass that fails to launch leaves the plain product in Y: returning false
-  // has the caller's own kernel recompute the problem into Y
-  return !relusq || launch_relusq_half(p, M, st);
+  // has the caller's own kernels recompute the problems into Y
+  for (int b = 0; relusq && b < batch; ++b) {
+    GemmProb q = p;
+    q.Y = static_cast<uint16_t *>(p.Y) + b * sy;
+    if (!launch_relusq_half(q, M, st)) return false;
+  }
+  return true;
 }
 
 }  // namespace rwkv7

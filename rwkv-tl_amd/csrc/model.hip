@@ -356,9 +356,14 @@ static int run_batched(const rwkv7_model &m, const rwkv7_state &s, const int64_t
                       6, w.xmix, tshift, C, T, M};
     ls.bf = bf;
     ls.out_f32 = a32;
+    // 16-bit operands (the large-M path): r, k, v at one stride, for one
+    // strided-batched GEMM call (with f32 activations the stored order
+    // measured ~1 % faster at 0.4B 1 x 512)
+    ls.mix_order = a32 ? 0 : 1;
     RWKV7_TRY(launch_ln_shift(ls, st));
-    const uint16_t *xr = at(w.xmix, 0), *xw = at(w.xmix, MC), *xk = at(w.xmix, 2 * MC), *xv = at(w.xmix, 3 * MC),
-                   *xa = at(w.xmix, 4 * MC), *xg = at(w.xmix, 5 * MC);
+    const int64_t sk = a32 ? 2 : 1, sv = a32 ? 3 : 2, sw = a32 ? 1 : 3;  // slots of k, v, w
+    const uint16_t *xr = at(w.xmix, 0), *xk = at(w.xmix, sk * MC), *xv = at(w.xmix, sv * MC),
+                   *xw = at(w.xmix, sw * MC), *xa = at(w.xmix, 4 * MC), *xg = at(w.xmix, 5 * MC);
     if (T == 1) {
       // one token per sequence: r, k, v and the raw LoRA first steps into one
       // [M, 3C+SR] f32 matrix, then the fused per-head kernel (LoRA second

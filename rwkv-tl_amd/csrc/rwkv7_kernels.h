@@ -87,6 +87,9 @@ struct LnShiftArgs {
   int C, T, M;
   int bf;       // the 16-bit out and shift are bfloat16 (else half)
   int out_f32;  // out is f32 (the GEMMs then take it as f32 A)
+  // output slot order of six mixes: 0 as the mix vectors are stored (r, w,
+  // k, v, a, g), 1 r, k, v, w, a, g (r, k, v at one stride: one batched GEMM)
+  int mix_order = 0;
 };
 int launch_ln_shift(const LnShiftArgs &a, hipStream_t st);
 
@@ -203,6 +206,9 @@ int launch_gemm_group(const GemmProb *probs, int nprob, int M, hipStream_t st, f
 // runs its own kernel.
 bool lt_eligible(const GemmProb &p);
 bool lt_gemm(const GemmProb &p, int M, hipStream_t st);
+// `batch` problems like p whose A, W and Y follow at strides sa, sw (16-bit
+// elements) and sy (elements of Y), as one strided-batched call.
+bool lt_gemm_batched(const GemmProb &p, int batch, int64_t sa, int64_t sw, int64_t sy, int M, hipStream_t st);
 
 // Operator-level time-mix stages (ops.hip); bf: the 16-bit operands are
 // bfloat16 (else IEEE half).

@@ -1377,6 +1377,15 @@ RWKV7_DEV void block_sum3(float &a, float &b, float &c, float (*red)[4]) {
   c = (red[2][0] + red[2][1]) + (red[2][2] + red[2][3]);
 }
 
+// The mix vector (row of a.mu) of output slot j: stored order, or with RKV
+// (LnShiftArgs::mix_order 1) r, k, v, w, a, g. A compile-time choice: a
+// run-time select of the row made the row kernel wait for its vector loads
+// one at a time.
+template <bool RKV>
+constexpr int mix_row(int j) {
+  return !RKV ? j : j == 1 ? 2 : j == 2 ? 3 : j == 3 ? 1 : j;
+}
+
 // A mixed value into the output: f32, or the model's 16-bit format.
 RWKV7_DEV void store_mix(const LnShiftArgs &a, int64_t i, float v) {
   if (a.out_f32) static_cast<float *>(a.out)[i] = v;
@@ -1449,7 +1458,7 @@ __global__ __launch_bounds__(256) void ln_shift_row_kernel(LnShiftArgs a) {
   }
 }
 
-template <int NP>
+template <int NP, bool RKV>
 __global__ __launch_bounds__(256) void ln_shift_kernel(LnShiftArgs a, int R, int ncs) {
   __shared__ float red[2][3][4];
   const int C = a.C, tid = threadIdx.x, T = a.T;
@@ -1493,7 +1502,7 @@ __global__ __launch_bounds__(256) void ln_shift_kernel(LnShiftArgs a, int R, int
       lb[i] = a.ln_b[c];
 #pragma unroll
       for (int j = 0; j < 6; ++j)
-        if (j < a.n_mix) mu[j][i] = a.mu[(int64_t)j * C + c];
+        if (j < a.n_mix) mu[j][i] = a.mu[(int64_t)mix_row<RKV>(j) * C + c];
     }
   }
   const float invC = 1.f / (float)C;
@@ -1548,7 +1557,7 @@ __global__ __launch_bounds__(256) void ln_shift_kernel(LnShiftArgs a, int R, int
 // access: 16 bytes per lane for f32 rows and vectors, 8 or 16 for the 16-bit
 // mix rows and shift states (ln_shift_kernel's column-strided layout stores
 // the six 16-bit mix rows two bytes per lane, 6 NP stores per thread and row).
-template <int NP>
+template <int NP, bool RKV>
 __global__ __launch_bounds__(256) void ln_shift_vec_kernel(LnShiftArgs a, int R) {
   static_assert(NP % 4 == 0, "whole float4 pieces per thread");
   constexpr int NV = NP / 4;
@@ -1588,7 +1597,7 @@ __global__ __launch_bounds__(256) void ln_shift_vec_kernel(LnShiftArgs a, int R)
   ld(a.ln_b, lb);
 #pragma unroll
   for (int j = 0; j < 6; ++j) {
-    if (j < a.n_mix) ld(a.mu + (int64_t)j * C, mu[j]);
+    if (j < a.n_mix) ld(a.mu + (int64_t)mix_row<RKV>(j) * C, mu[j]);
     else
 #pragma unroll
       for (int i = 0; i < NP; ++i) mu[j][i] = 0.f;
@@ -1679,21 +1688,28 @@ int launch_ln_shift(const LnShiftArgs &a, hipStream_t st) {
   if (a.M >= 2 * want) R = min(8, a.M / want);
   else
     while (ncs * 2 <= np && np % (ncs * 2) == 0 && (int64_t)a.M * ncs < want) ncs *= 2;
-  const bool row_kernel = R == 1 && np <= 4;
+  const bool rkv = a.mix_order != 0;  // only the two other kernels take this order
+  const bool row_kernel = R == 1 && np <= 4 && !rkv;
   const dim3 grid((a.M + R - 1) / R, row_kernel ? 1 : ncs);
   // the vector form at C = 1024 and 2048 (the 0.4B and 1.5B widths; at 4096
   // its registers would leave one wave per SIMD)
   if (R > 1 && (np == 4 || np == 8)) {
-    if (np == 4) ln_shift_vec_kernel<4><<<grid, 256, 0, st>>>(a, R);
-    else ln_shift_vec_kernel<8><<<grid, 256, 0, st>>>(a, R);
+    if (np == 4) {
+      if (rkv) ln_shift_vec_kernel<4, true><<<grid, 256, 0, st>>>(a, R);
+      else ln_shift_vec_kernel<4, false><<<grid, 256, 0, st>>>(a, R);
+    } else {
+      if (rkv) ln_shift_vec_kernel<8, true><<<grid, 256, 0, st>>>(a, R);
+      else ln_shift_vec_kernel<8, false><<<grid, 256, 0, st>>>(a, R);
+    }
     RWKV7_CHECK_LAUNCH();
     return RWKV7_OK;
   }
   switch (np) {
-#define RWKV7_LNS_CASE(n)                                            \
-  case n:                                                            \
-    if (row_kernel) ln_shift_row_kernel<n><<<grid, 256, 0, st>>>(a); \
-    else ln_shift_kernel<n><<<grid, 256, 0, st>>>(a, R, ncs);        \
+#define RWKV7_LNS_CASE(n)                                                   \
+  case n:                                                                   \
+    if (row_kernel) ln_shift_row_kernel<n><<<grid, 256, 0, st>>>(a);        \
+    else if (rkv) ln_shift_kernel<n, true><<<grid, 256, 0, st>>>(a, R, ncs); \
+    else ln_shift_kernel<n, false><<<grid, 256, 0, st>>>(a, R, ncs);        \
     break;
     RWKV7_LNS_CASE(1) RWKV7_LNS_CASE(2) RWKV7_LNS_CASE(3) RWKV7_LNS_CASE(4)
     RWKV7_LNS_CASE(5) RWKV7_LNS_CASE(6) RWKV7_LNS_CASE(7) RWKV7_LNS_CASE(8)
