@@ -900,26 +900,31 @@ RWKV7_DEV void lora2_chunk(const PrefillScanArgs &p, St &st, int h, int bi, int 
 // hold, keeps three workgroups per CU for the other cases.
 template <class St, bool L2>
 __global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(typename St::Args p, float *rec, int T, int H) {
-  // 43 KB of LDS, so that three workgroups share a CU (the 1.5B-shaped
-  // 4 x 1024 prefill runs 8192 of them): the stager writes its padded rows
-  // straight into s_x, and the later 16 x 64 results take the rows that are
-  // dead by then -- AkaV and then G2 the prefix products', G1 w's, U b's and
-  // Y0 k's (each phase below ends with a barrier before the next reuses a row)
+  // 35 KB of LDS without the LoRA steps (43 KB with them, which stage there),
+  // so that four workgroups share a CU (the 1.5B-shaped 4 x 1024 prefill
+  // runs 8192 of them): the stager writes its padded rows straight into s_x,
+  // b^ and k^ go from registers straight into the record, and the later
+  // 16 x 64 results take the rows that are dead by then -- AkaV and then G2
+  // the prefix products', G1 w's, U b's and Y0 k's (each phase below ends
+  // with a barrier before the next reuses a row)
+  constexpr int NB = L2 ? 3 : 1;
   __shared__ float s_x[6][kCk][kPad];     // w, a (a~), b (b / P), k (k / P), r (r~), v
-  __shared__ float s_bkp[3][kCk][kPad];   // b^, k^, prefix products P_t = D(-1, t]
+  __shared__ float s_bkp[NB][kCk][kPad];  // prefix products P_t = D(-1, t] (and the LoRA steps before them)
   __shared__ float s_m[4][kCk][kCk + 1];  // Aba, Aka, Bbr, Bkr
   __shared__ float s_t[kCk][kCk + 1];
   __shared__ float s_gam[kN];
   typedef float Row[kPad];
-  Row *s_bh = s_bkp[0], *s_kh = s_bkp[1], *s_p = s_bkp[2];
-  Row *s_akav = s_bkp[2], *s_g2 = s_bkp[2], *s_g1 = s_x[0], *s_u = s_x[2], *s_y0 = s_x[3];
-  static_assert(sizeof(s_bkp) >= 3 * kCk * kN * sizeof(float), "LoRA steps staged in s_bkp");
+  Row *s_p = s_bkp[NB - 1];
+  Row *s_akav = s_bkp[NB - 1], *s_g2 = s_bkp[NB - 1], *s_g1 = s_x[0], *s_u = s_x[2], *s_y0 = s_x[3];
+  static_assert(!L2 || sizeof(s_bkp) >= 3 * kCk * kN * sizeof(float), "LoRA steps staged in s_bkp");
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int row = lane & 15, kq = lane >> 4, col = 16 * wv + row;
   const int c = blockIdx.x, h = blockIdx.y, bi = blockIdx.z;
   const int C = H * kN;
   const int t0 = c * kCk, t1 = min(T, t0 + kCk), Tl = t1 - t0;
+  // this chunk's record
+  float *R = rec + (((int64_t)bi * H + h) * gridDim.x + c) * kRecFloats;
   St st(p, h, -1, (int64_t)bi * T * C + (int64_t)h * kN, t1);
   bool fetched = false;
   if constexpr (L2 && std::is_same<St, GateStager<kCk>>::value) {
@@ -960,14 +965,22 @@ __global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(typename St::Args 
     }
   } else if (tid < 2 * kN) {  // wave 1: suffix products (b^, k^, gam), exact products of w
     const int j = tid - kN;
-    float Q = 1.f;
+    float Q = 1.f, bh[kCk], kh[kCk];
 #pragma unroll
     for (int t = kCk - 1; t >= 0; --t) {
-      s_bh[t][j] = s_x[2][t][j] * Q;
-      s_kh[t][j] = s_x[3][t][j] * Q;
+      bh[t] = s_x[2][t][j] * Q;
+      kh[t] = s_x[3][t][j] * Q;
       Q *= s_x[0][t][j];
     }
     s_gam[j] = Q;
+    // B operand of the state update, X[4 kk + kq][16 w + row], as the chain
+    // kernel's thread 64 w + 16 kq + row reads it (kk = 0..3 in one float4)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int off = 4 * (64 * (j >> 4) + 16 * q + (j & 15));
+      *reinterpret_cast<float4 *>(R + kRecBh + off) = make_float4(bh[q], bh[4 + q], bh[8 + q], bh[12 + q]);
+      *reinterpret_cast<float4 *>(R + kRecKh + off) = make_float4(kh[q], kh[4 + q], kh[8 + q], kh[12 + q]);
+    }
   }
   const bool fast = __syncthreads_and(ok);  // block-uniform
   if (!fast) {  // token matrices straight from products of w: thread (t, s)
@@ -1075,9 +1088,8 @@ __global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(typename St::Args 
     }
   }
   __syncthreads();
-  // the record, one float4 per thread and array (thread = wave 64 + lane of
-  // the chain kernel's reader)
-  float *R = rec + (((int64_t)bi * H + h) * gridDim.x + c) * kRecFloats;
+  // the rest of the record, one float4 per thread and array (thread = wave
+  // 64 + lane of the chain kernel's reader)
   const int w = tid >> 6;
   auto put = [&](int off, float a0, float a1, float a2, float a3) {
     *reinterpret_cast<float4 *>(R + off + 4 * tid) = make_float4(a0, a1, a2, a3);
@@ -1087,11 +1099,6 @@ __global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(typename St::Args 
       s_g1[row][16 * w + 12 + kq]);
   put(kRecG2, s_g2[row][16 * w + kq], s_g2[row][16 * w + 4 + kq], s_g2[row][16 * w + 8 + kq],
       s_g2[row][16 * w + 12 + kq]);
-  // B operand of the state update: X[4 kk + kq][16 w + row]
-  put(kRecBh, s_bh[kq][16 * w + row], s_bh[4 + kq][16 * w + row], s_bh[8 + kq][16 * w + row],
-      s_bh[12 + kq][16 * w + row]);
-  put(kRecKh, s_kh[kq][16 * w + row], s_kh[4 + kq][16 * w + row], s_kh[8 + kq][16 * w + row],
-      s_kh[12 + kq][16 * w + row]);
   // A operand of the state update (value rows 16 q + row, q = w here)
   put(kRecU, s_u[kq][16 * w + row], s_u[4 + kq][16 * w + row], s_u[8 + kq][16 * w + row],
       s_u[12 + kq][16 * w + row]);
@@ -1269,10 +1276,12 @@ static int launch_chunked(const typename St::Args &p, float *S, TY *y, float *re
                           hipStream_t st) {
   if (!rec) return RWKV7_EWORKSPACE;
   const int nc = (T + kCk - 1) / kCk;
-  bool l2 = false;
-  if constexpr (std::is_same<St, GateStager<kCk>>::value) l2 = p.l1 != nullptr;
-  if (l2) wkv7_chunk_prep_kernel<St, true><<<dim3(nc, H, B), 256, 0, st>>>(p, rec, T, H);
-  else wkv7_chunk_prep_kernel<St, false><<<dim3(nc, H, B), 256, 0, st>>>(p, rec, T, H);
+  if constexpr (std::is_same<St, GateStager<kCk>>::value) {
+    if (p.l1) wkv7_chunk_prep_kernel<St, true><<<dim3(nc, H, B), 256, 0, st>>>(p, rec, T, H);
+    else wkv7_chunk_prep_kernel<St, false><<<dim3(nc, H, B), 256, 0, st>>>(p, rec, T, H);
+  } else {
+    wkv7_chunk_prep_kernel<St, false><<<dim3(nc, H, B), 256, 0, st>>>(p, rec, T, H);
+  }
   RWKV7_CHECK_LAUNCH();
   // two value quarters per workgroup (each record fetched once for both)
   // where that still leaves a workgroup per CU
